@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode-attention hot path on one MI355X.
+
+One step = one call of the HIP kernel over the headline workload (BASELINE.json
+B=30720, Hq=Hkv=16, seqlen_q=1, seqlen_kv=16, D=128, bf16 Q/K/V
+drawn N(0,1) from a fixed seed, fp32 accumulation, fp16 output), with every
+input resident in HBM before the timed region.
+
+Prints one JSON line:
+  value         algorithmic TB/s of the whole timed region (bytes per call as
+                the reference counts them, fmha_host.cpp:428-430, times calls,
+                over the wall time between the first and last event);
+  roofline      the kernel alone: algorithmic bytes per launch over the mean
+                of per-launch HIP-event durations on the launch stream, against
+                the 8 TB/s HBM peak; traffic = measured HBM bytes per launch
+                from the committed rocprofv3 counter summary, when present;
+  cpu_baseline  the reference's own CPU loop (fmha_host.cpp:158-284, built from
+                /root/reference into oracle/_ref) -- or the restated oracle
+                when that build is absent -- timed single-threaded on this
+                host over a bounded sample of the same workload.
+"""
+import argparse
+import contextlib
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "µs/call + achieved HBM TB/s (% of peak) at B=30720,H=16,Skv=16,d=128"
+WORKLOAD = dict(batch=30720, num_heads_q=16, num_heads_kv=16, seqlen_kv=16, head_dim=128, std=1.0)
+SEED = 0xF3A00000 + 16 * 2
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fmha_decode_c2_traffic.json")
+
+
+def algorithmic_bytes(B, Hq, Hkv, S, D):
+    # Q (bf16) + K and V (bf16) + O (fp16), fmha_host.cpp:428-430 with Hkv heads for K/V.
+    return 2 * B * Hq * D + 2 * (2 * B * S * Hkv * D) + 2 * B * Hq * D
+
+
+@contextlib.contextmanager
+def _quiet_stdout():
+    """Silence fd 1 (the reference loop prints while it validates)."""
+    sys.stdout.flush()
+    saved = os.dup(1)
+    with open(os.devnull, "w") as dn:
+        os.dup2(dn.fileno(), 1)
+        try:
+            yield
+        finally:
+            sys.stdout.flush()
+            os.dup2(saved, 1)
+            os.close(saved)
+
+
+def cpu_baseline(q, k, v, o, B, Hq, Hkv, S, D, scale, max_batches):
+    """Time the reference CPU loop on the first `max_batches` batches."""
+    import numpy as np
+    import torch
+    import oracle
+
+    nb = min(B, max_batches)
+    qh = q.view(B, Hq, D)[:nb].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    kh = k.view(B * S, Hkv, D)[: nb * S].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    vh = v.view(B * S, Hkv, D)[: nb * S].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    oh = o.view(B, Hq, D)[:nb].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    cu = np.arange(0, (nb + 1) * S, S, dtype=np.int32)
+    nbytes = algorithmic_bytes(nb, Hq, Hkv, S, D)
+    if oracle.ref_available() and Hq == Hkv:
+        kind = "reference"
+        with _quiet_stdout():
+            t0 = time.perf_counter()
+            _, passed = oracle.ref_do_validation(qh, kh, vh, cu, Hq, Hkv, D, gpu_o=oh)
+            dt = time.perf_counter() - t0
+        extra = {"reference_check_of_gpu_output": "passed" if passed else "failed"}
+    else:
+        kind = "port"
+        t0 = time.perf_counter()
+        oracle.decode(qh, kh, vh, cu, Hq, Hkv, D, scale, nthreads=1)
+        dt = time.perf_counter() - t0
+        extra = {}
+    out = {
+        "value": nbytes / dt / 1e12,
+        "unit": "TB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"first {nb} of {B} batches of the timed workload (all heads, S={S}), one pass, "
+                  f"single thread: {dt:.2f} s; us_per_call scaled to the full batch = "
+                  f"{dt * 1e6 * B / nb:.0f}",
+        "us_per_call_full_batch": dt * 1e6 * B / nb,
+    }
+    out.update(extra)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-batches", type=int, default=30720,
+                    help="batches of the workload the CPU baseline runs (bounded sample)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode path shards by batch or KV head without communication, so the "
+              "one-GPU figure is the per-GPU figure", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import fmha_amd
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    W = WORKLOAD
+    B, Hq, Hkv, S, D = W["batch"], W["num_heads_q"], W["num_heads_kv"], W["seqlen_kv"], W["head_dim"]
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    q = torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(B, S, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(B, S, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+    o = torch.empty(B, Hq, 1, D, device=dev, dtype=torch.float16)
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+    qp, kp, vp, op = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+
+    def step():
+        fmha_amd.launch_fmha_decode_uniform(sptr, qp, kp, vp, op, S, B, Hq, Hkv, 1, D, D, scale)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for i in range(K):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    per = [a.elapsed_time(b) for a, b in ev]           # ms, each launch alone
+    total_ms = ev[0][0].elapsed_time(ev[-1][1])        # ms, first start to last end
+    ms_per_step = total_ms / K
+    kern_ms = sum(per) / K
+    nbytes = algorithmic_bytes(B, Hq, Hkv, S, D)
+    value_tbs = nbytes / (ms_per_step * 1e-3) / 1e12
+    achieved_gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    per_sorted = sorted(per)
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(q, k, v, o, B, Hq, Hkv, S, D, scale, args.cpu_batches)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value_tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_call": round(ms_per_step * 1e3, 2),
+        "us_per_call_kernel_mean": round(kern_ms * 1e3, 2),
+        "us_per_call_kernel_median": round(per_sorted[K // 2] * 1e3, 2),
+        "pct_of_peak": round(100.0 * value_tbs * 1e3 / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "accumulate": "f32",
+        "data": "synthetic: seeded N(0,1) bf16 generated on the GPU",
+        "config": {
+            "workload": "BASELINE configs[1]: decode attention B=30720 Hq=Hkv=16 seqlen_q=1 "
+                        "seqlen_kv=16 D=128, bf16 in, fp16 out",
+            "batch": B, "num_heads_q": Hq, "num_heads_kv": Hkv, "seqlen_q": 1, "seqlen_kv": S,
+            "head_dim": D, "bytes_per_call": nbytes, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "wall_s_timed_region": round(wall, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,18 @@
+"""fmha_amd -- MI355X (gfx950) decode attention: seqlen_q = 1, KV length
+0..16 per sequence, bf16 Q/K/V, fp32 accumulation, fp16 output, with
+grouped-query attention.  The kernels are hand-written HIP in fmha_amd/csrc;
+the C ABI is include/fmha_decode.h; this package is its host-side interface.
+"""
+from .decode import (MAX_SEQLEN_KV, FmhaDecodeError, fmha_decode, launch_fmha_decode,
+                     launch_fmha_decode_uniform)
+from ._lib import LIB_PATH, EXPORTED
+
+__all__ = [
+    "MAX_SEQLEN_KV",
+    "FmhaDecodeError",
+    "fmha_decode",
+    "launch_fmha_decode",
+    "launch_fmha_decode_uniform",
+    "LIB_PATH",
+    "EXPORTED",
+]

@@ -1,0 +1,45 @@
+"""ctypes binding of libfmha_decode.so (declarations in include/fmha_decode.h).
+
+The library must have been built (fmha_amd/_build.py); there is no fallback
+implementation: a missing library is an error.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfmha_decode.so")
+
+# Every symbol include/fmha_decode.h declares.
+EXPORTED = (
+    "fmha_decode_fwd",
+    "fmha_decode_fwd_uniform",
+    "fmha_decode_error_string",
+    "fmha_decode_last_error_detail",
+    "fmha_decode_version",
+)
+
+_lib = None
+
+
+def load():
+    """Load the library once and declare its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i32, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
+    lib.fmha_decode_fwd.restype = ctypes.c_int
+    lib.fmha_decode_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_fwd_uniform.restype = ctypes.c_int
+    lib.fmha_decode_fwd_uniform.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_error_string.restype = ctypes.c_char_p
+    lib.fmha_decode_error_string.argtypes = [ctypes.c_int]
+    lib.fmha_decode_last_error_detail.restype = ctypes.c_char_p
+    lib.fmha_decode_last_error_detail.argtypes = []
+    lib.fmha_decode_version.restype = ctypes.c_int
+    lib.fmha_decode_version.argtypes = []
+    _lib = lib
+    return lib

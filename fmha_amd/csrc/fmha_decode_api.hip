@@ -1,0 +1,182 @@
+// fmha_decode_api.hip -- C ABI of libfmha_decode.so: argument checks, launch
+// shape and kernel selection for the gfx950 decode-attention kernel.
+//
+// Replaces the reference's launch helper launch_fmha_mfma_4x4x4
+// (fmha_mfma_4x4x4_kernel.hpp:370-389), which takes a caller-computed grid,
+// runs the D=256 kernel for any head_dim other than 128 and reports nothing;
+// here every argument is checked before the GPU is touched and the library
+// computes its own grid.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "fmha_decode.h"
+#include "fmha_decode_kernel.hpp"
+
+namespace {
+
+using fmha_decode::DecodeArgs;
+using fmha_decode::kBlockThreads;
+using fmha_decode::kWaveSize;
+using fmha_decode::kWavesPerBlock;
+
+thread_local char g_detail[256] = "";
+
+int reject(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_detail, sizeof(g_detail), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int D, int G, int SB>
+hipError_t launch_one(const DecodeArgs& a, hipStream_t stream) {
+  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL((fmha_decode::fmha_decode_fwd_kernel<D, G, SB>), dim3(blocks), dim3(kBlockThreads), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <int D, int G>
+hipError_t launch_bucket(const DecodeArgs& a, int sb, hipStream_t stream) {
+  switch (sb) {
+    case 0: return launch_one<D, G, 0>(a, stream);
+    case 1: return launch_one<D, G, 1>(a, stream);
+    case 2: return launch_one<D, G, 2>(a, stream);
+    case 4: return launch_one<D, G, 4>(a, stream);
+    case 8: return launch_one<D, G, 8>(a, stream);
+    default: return launch_one<D, G, 16>(a, stream);
+  }
+}
+
+template <int D>
+hipError_t launch_group(const DecodeArgs& a, int g, int sb, hipStream_t stream) {
+  switch (g) {
+    case 1: return launch_bucket<D, 1>(a, sb, stream);
+    case 2: return launch_bucket<D, 2>(a, sb, stream);
+    case 4: return launch_bucket<D, 4>(a, sb, stream);
+    default: return launch_bucket<D, 8>(a, sb, stream);
+  }
+}
+
+// Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
+int bucket_for(int s) {
+  int b = 1;
+  while (b < s) b <<= 1;
+  return b;
+}
+
+int check_common(const void* Q, const void* K, const void* V, void* O, int32_t batch, int32_t hq,
+                 int32_t hkv, int32_t seqlen_q, int32_t dq, int32_t dkv, float scale, bool kv_may_be_null) {
+  if (batch < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch must be >= 0 (got %d)", batch);
+  if (hq <= 0 || hkv <= 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head counts must be > 0 (num_heads_q=%d, num_heads_kv=%d)", hq,
+                  hkv);
+  if (hq % hkv != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "num_heads_q (%d) must be a multiple of num_heads_kv (%d)", hq,
+                  hkv);
+  const int g = hq / hkv;
+  if (g != 1 && g != 2 && g != 4 && g != 8)
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be 1, 2, 4 or 8 (got %d)", g);
+  if (seqlen_q != 1) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_q must be 1 (got %d)", seqlen_q);
+  if (dq != dkv)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head_dim_q (%d) must equal head_dim_kv (%d)", dq, dkv);
+  if (dq != 64 && dq != 128 && dq != 256)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head_dim must be 64, 128 or 256 (got %d)", dq);
+  if (!std::isfinite(scale)) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "softmax_scale must be finite");
+  // Byte sizes of one batch's Q/O rows and of one batch's K/V span must fit
+  // the 31-bit buffer ranges the kernel builds.
+  if ((int64_t)hq * dq * 2 >= (int64_t(1) << 31) ||
+      (int64_t)hkv * dq * 2 * FMHA_DECODE_MAX_SEQLEN_KV >= (int64_t(1) << 31))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head count too large (num_heads_q=%d, num_heads_kv=%d)", hq, hkv);
+  if (batch == 0) return FMHA_DECODE_SUCCESS;
+  if (!Q || !O) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "Q and O must be non-null");
+  // K and V may be null only when no row can be read (uniform seqlen_kv == 0).
+  if ((!K || !V) && !kv_may_be_null)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K and V must be non-null");
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "Q, K, V and O must be 16-byte aligned");
+  return FMHA_DECODE_SUCCESS;
+}
+
+int launch(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu, int32_t seqlen_kv,
+           int32_t batch, int32_t hq, int32_t hkv, int32_t dq, float scale) {
+  const int heads_per_wave = kWaveSize / (dq / 8);
+  const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
+  const int64_t units = upb * batch;
+  if (units > (int64_t)UINT32_MAX - kWavesPerBlock)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
+  DecodeArgs a;
+  a.q = static_cast<const uint16_t*>(Q);
+  a.k = static_cast<const uint16_t*>(K);
+  a.v = static_cast<const uint16_t*>(V);
+  a.o = static_cast<uint16_t*>(O);
+  a.cu = cu;
+  a.seqlen_uniform = seqlen_kv;
+  a.num_heads_q = hq;
+  a.num_heads_kv = hkv;
+  a.units_per_batch = (int32_t)upb;
+  a.total_units = (uint32_t)units;
+  a.scale = scale;
+  const int sb = cu ? 0 : bucket_for(seqlen_kv);
+  const int g = hq / hkv;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  switch (dq) {
+    case 64: err = launch_group<64>(a, g, sb, s); break;
+    case 128: err = launch_group<128>(a, g, sb, s); break;
+    default: err = launch_group<256>(a, g, sb, s); break;
+  }
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return FMHA_DECODE_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
+                               const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                               int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                               float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
+  return launch(stream, Q, K, V, O, cu_seqlens_kv, 0, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
+}
+
+extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       int32_t seqlen_kv, int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                       int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                       float softmax_scale) {
+  g_detail[0] = '\0';
+  if (seqlen_kv < 0 || seqlen_kv > FMHA_DECODE_MAX_SEQLEN_KV)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_kv must lie in [0, %d] (got %d)",
+                  FMHA_DECODE_MAX_SEQLEN_KV, seqlen_kv);
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, seqlen_kv == 0);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  return launch(stream, Q, K, V, O, nullptr, seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q,
+                softmax_scale);
+}
+
+extern "C" const char* fmha_decode_error_string(int code) {
+  switch (code) {
+    case FMHA_DECODE_SUCCESS: return "success";
+    case FMHA_DECODE_ERROR_INVALID_VALUE: return "invalid argument";
+    case FMHA_DECODE_ERROR_NOT_SUPPORTED: return "configuration not supported";
+    default: return hipGetErrorString(static_cast<hipError_t>(code));
+  }
+}
+
+extern "C" const char* fmha_decode_last_error_detail(void) { return g_detail; }
+
+extern "C" int fmha_decode_version(void) { return 100; }

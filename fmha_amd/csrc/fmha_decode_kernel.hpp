@@ -1,0 +1,390 @@
+// fmha_decode_kernel.hpp -- gfx950 decode-attention kernel (seqlen_q = 1,
+// KV length 0..16 per sequence, bf16 Q/K/V, fp32 accumulation, fp16 output).
+//
+// Semantics restated from the reference CPU loop (fmha_host.cpp:169-245) and
+// the wired-in kernel (fmha_mfma_4x4x4_kernel.hpp:243-268, :326-334): fp32 dot
+// products, scale, max-subtracted softmax with a sum>0 guard, softmax weights
+// rounded to bf16 before P.V, fp32 accumulation, one RNE rounding to fp16.
+// Query head h reads KV head h / G with G = Hq / Hkv.
+//
+// Work decomposition (one wavefront = one independent unit, no block barrier):
+//   * a KV head is served by LPH = D/8 consecutive lanes; lane r of the group
+//     owns dims [8r, 8r+8): one 16-byte bf16x8 chunk per KV row;
+//   * a wave serves HPW = 64/LPH consecutive KV heads of one batch and all G
+//     query heads of each, so every K/V byte is read from HBM exactly once;
+//   * each lane issues all of its Q, K and V loads (1 + 2*SMAX b128 buffer
+//     loads) before any arithmetic, so a wave keeps 2*SMAX KiB of K/V per
+//     64 lanes in flight;
+//   * K/V rows are fetched through a buffer resource whose num_records ends at
+//     this batch's last row: rows j >= S_b (padding up to the power-of-two
+//     bucket SMAX) and lanes of absent heads read 0 without touching memory.
+//
+// QK^T: v_dot2_f32_bf16 on the packed pairs (4 per row), then a transposing
+// butterfly across the LPH lanes of the head: at each step a lane keeps one
+// half of its partial sums and swaps the other half with its partner, so the
+// G*SMAX scores of the head end up fully reduced and spread over the lanes
+// (15 exchanges for 16 scores instead of 64 for independent butterflies).
+// Softmax runs on that distribution; the bf16 weights go through 128 bytes of
+// LDS per head so every lane of the head sees all of them; P.V packs row pairs
+// with v_perm_b32 and accumulates with v_dot2_f32_bf16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmha_decode {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Type produced/consumed by the raw-buffer b128 builtins.
+typedef uint32_t u32x4_gcc __attribute__((vector_size(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaveSize = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlockThreads = kWaveSize * kWavesPerBlock;
+constexpr int kMaxSeq = 16;
+// Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format,
+// no swizzle, no index stride).
+constexpr int kBufferWord3 = 0x00020000;
+// A byte offset beyond every num_records this kernel builds (all < 2^31):
+// loads there return 0 and stores are dropped, with no memory access.
+constexpr uint32_t kOffsetOutOfRange = 0x80000000u;
+
+struct DecodeArgs {
+  const uint16_t* q;        // [batch, Hq, D] bf16 bits
+  const uint16_t* k;        // [rows, Hkv, D] bf16 bits
+  const uint16_t* v;        // [rows, Hkv, D] bf16 bits
+  uint16_t* o;              // [batch, Hq, D] fp16 bits
+  const int32_t* cu;        // [batch+1] row offsets, or null (uniform)
+  int32_t seqlen_uniform;   // rows per batch when cu == null
+  int32_t num_heads_q;
+  int32_t num_heads_kv;
+  int32_t units_per_batch;  // waves per batch: ceil(Hkv / HPW)
+  uint32_t total_units;     // batch * units_per_batch
+  float scale;
+};
+
+__device__ __forceinline__ constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
+
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t x) { return __builtin_bit_cast(bf16x2, x); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, kBufferWord3);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+  u32x4_gcc x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, 0);
+  return __builtin_bit_cast(u32x4, x);
+}
+
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, u32x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x), r, (int)voffset, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Lane exchanges inside the group of LPH lanes that serves one KV head.
+//
+// The butterfly uses partner masks, in order, from {16, 8, 7, 2, 1} (the last
+// log2(LPH) of them).  Mask m pairs lane i with lane i ^ m; its split bit is
+// the top bit of m.  Every mask is zero on the split bits of earlier steps, so
+// partners always hold the same subset of partial sums, and the masks are
+// linearly independent, so the exchanges cover all LPH lanes.
+//   16: lane i^16 (crosses the two 16-lane rows of a 32-lane group)
+//    8: DPP row_ror:8        (i ^ 8 inside a 16-lane row)
+//    7: DPP row_half_mirror  (i ^ 7 inside an 8-lane half row)
+//    2: DPP quad_perm[2,3,0,1]
+//    1: DPP quad_perm[1,0,3,2]
+// ---------------------------------------------------------------------------
+template <int LPH>
+__device__ __forceinline__ constexpr int step_mask(int s) {
+  constexpr int kMasks[5] = {16, 8, 7, 2, 1};
+  return kMasks[5 - ilog2(LPH) + s];
+}
+
+template <int MASK>
+__device__ __forceinline__ float lane_xchg(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  int y;
+  if constexpr (MASK == 16) {
+    y = __shfl_xor(xi, 16, kWaveSize);
+  } else if constexpr (MASK == 8) {
+    y = __builtin_amdgcn_mov_dpp(xi, 0x128, 0xf, 0xf, false);
+  } else if constexpr (MASK == 7) {
+    y = __builtin_amdgcn_mov_dpp(xi, 0x141, 0xf, 0xf, false);
+  } else if constexpr (MASK == 2) {
+    y = __builtin_amdgcn_mov_dpp(xi, 0x4e, 0xf, 0xf, false);
+  } else {
+    static_assert(MASK == 1, "unsupported lane mask");
+    y = __builtin_amdgcn_mov_dpp(xi, 0xb1, 0xf, 0xf, false);
+  }
+  return __builtin_bit_cast(float, y);
+}
+
+template <int MASK>
+__device__ __forceinline__ constexpr int split_bit() { return ilog2(MASK); }
+
+// One butterfly step over N live partial sums: lanes whose split bit is 0
+// keep x[0, N/2), the others keep x[N/2, N); both halves end compacted into
+// x[0, N/2).  With N == 1 the step is a plain all-reduce of x[0].
+template <int MASK, int N>
+__device__ __forceinline__ void butterfly_step(float* x, int lane) {
+  if constexpr (N == 1) {
+    x[0] += lane_xchg<MASK>(x[0]);
+  } else {
+    const bool upper = (lane >> split_bit<MASK>()) & 1;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const float a = x[i];
+      const float b = x[i + N / 2];
+      const float keep = upper ? b : a;
+      const float send = upper ? a : b;
+      x[i] = keep + lane_xchg<MASK>(send);
+    }
+  }
+}
+
+template <int LPH, int V, int S>
+struct TransposeReduce {
+  static __device__ __forceinline__ void run(float* x, int lane) {
+    if constexpr (S < ilog2(LPH)) {
+      constexpr int live = (V >> S) > 1 ? (V >> S) : 1;
+      butterfly_step<step_mask<LPH>(S), live>(x, lane);
+      TransposeReduce<LPH, V, S + 1>::run(x, lane);
+    }
+  }
+};
+
+// All-reduce (max or sum) over the lanes that differ only in the split bits
+// of butterfly steps [FIRST, LAST).
+template <int LPH, int FIRST, int LAST, bool IS_MAX>
+struct GroupReduce {
+  static __device__ __forceinline__ float run(float x) {
+    if constexpr (FIRST < LAST) {
+      const float y = lane_xchg<step_mask<LPH>(FIRST)>(x);
+      x = IS_MAX ? fmaxf(x, y) : x + y;
+      return GroupReduce<LPH, FIRST + 1, LAST, IS_MAX>::run(x);
+    } else {
+      return x;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
+// ---------------------------------------------------------------------------
+template <int D, int G, int SMAX>
+__device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, int64_t row0, int S,
+                                            int hk, bool head_ok, int lane, uint16_t* lds_p) {
+  constexpr int LPH = D / 8;                 // lanes per KV head
+  constexpr int NS = ilog2(LPH);             // butterfly steps
+  constexpr int V = G * SMAX;                // scores per KV head
+  constexpr int L = NS < ilog2(V) ? NS : ilog2(V);  // splitting steps
+  constexpr int W = (V >> NS) > 1 ? (V >> NS) : 1;  // scores per lane after the butterfly
+  constexpr int GS = W < SMAX ? W : SMAX;    // scores of one query head inside a lane
+  constexpr int C = ilog2(SMAX / GS);        // steps spanning one query head's lanes
+  constexpr int VP = G * kMaxSeq;            // LDS bf16 slots per KV head
+
+  const int r = lane % LPH;
+  const int hkl = lane / LPH;
+  const int hq_count = a.num_heads_q;
+  const int hkv_count = a.num_heads_kv;
+
+  // ---- buffer resources and per-lane byte offsets ----
+  const uint32_t q_bytes = (uint32_t)hq_count * D * 2;
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq_count * D, q_bytes);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq_count * D, q_bytes);
+  const uint32_t row_bytes = (uint32_t)hkv_count * D * 2;
+  const uint32_t kv_bytes = (uint32_t)S * row_bytes;
+  const uint64_t kv_elem0 = (uint64_t)row0 * hkv_count * D;
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + kv_elem0, kv_bytes);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + kv_elem0, kv_bytes);
+
+  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kOffsetOutOfRange;
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kOffsetOutOfRange;
+
+  // ---- issue every load of this unit ----
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16(q_rsrc, qo_off + g * D * 2);
+  u32x4 kr[SMAX];
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16(k_rsrc, kv_off + j * row_bytes);
+  u32x4 vr[SMAX];
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16(v_rsrc, kv_off + j * row_bytes);
+
+  // ---- partial scores over this lane's 8 dims ----
+  float x[V];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t qw = qv[g][i];
+        const uint32_t kw = kr[j][i];
+        acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw), as_bf16x2(kw), acc, false);
+      }
+      x[g * SMAX + j] = acc;
+    }
+  }
+
+  // ---- reduce over the head's lanes; lane keeps scores [blk*W, blk*W + W) ----
+  TransposeReduce<LPH, V, 0>::run(x, lane);
+  const int blk = r >> (NS - L);
+
+  // ---- masked softmax (per query head) ----
+  float p[W];
+#pragma unroll
+  for (int h0 = 0; h0 < W; h0 += GS) {
+    float t[GS];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < GS; ++w) {
+      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
+      const bool ok = j < S;
+      t[w] = x[h0 + w] * a.scale;
+      m = ok ? fmaxf(m, t[w]) : m;
+    }
+    m = GroupReduce<LPH, L - C, L, true>::run(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < GS; ++w) {
+      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
+      const bool ok = j < S;
+      t[w] = ok ? expf(t[w] - m) : 0.0f;
+      sum += t[w];
+    }
+    sum = GroupReduce<LPH, L - C, L, false>::run(sum);
+#pragma unroll
+    for (int w = 0; w < GS; ++w) p[h0 + w] = (sum > 0.0f) ? (t[w] / sum) : 0.0f;
+  }
+
+  // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
+  uint16_t* lds_head = lds_p + hkl * VP;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int vi = blk * W + w;
+    const int g = vi / SMAX;
+    const int j = vi % SMAX;
+    lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- P.V over row pairs ----
+  constexpr int NP = (SMAX + 1) / 2;
+  const uint32_t* lds_pairs = reinterpret_cast<const uint32_t*>(lds_head);
+  uint32_t pp[G][NP];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int jp = 0; jp < NP; ++jp) {
+      uint32_t w2 = lds_pairs[g * (kMaxSeq / 2) + jp];
+      if constexpr (SMAX == 1) w2 &= 0xffffu;  // slot 1 is not part of this bucket
+      pp[g][jp] = w2;
+    }
+  }
+
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+
+#pragma unroll
+  for (int jp = 0; jp < NP; ++jp) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v0 = vr[2 * jp][i];
+      const uint32_t v1 = (2 * jp + 1 < SMAX) ? (uint32_t)vr[(2 * jp + 1 < SMAX) ? 2 * jp + 1 : 0][i] : 0u;
+      lo[i] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // (V_j[2i],   V_j+1[2i])
+      hi[i] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);  // (V_j[2i+1], V_j+1[2i+1])
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const bf16x2 pw = as_bf16x2(pp[g][jp]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[g][2 * i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(lo[i]), pw, acc[g][2 * i], false);
+        acc[g][2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(hi[i]), pw, acc[g][2 * i + 1], false);
+      }
+    }
+  }
+
+  // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    u32x4 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)acc[g][2 * i]);
+      const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)acc[g][2 * i + 1]);
+      out[i] = h0 | (h1 << 16);
+    }
+    buffer_store16(o_rsrc, qo_off + g * D * 2, out);
+  }
+}
+
+// Batches whose cu_seqlens span is outside [0, 16] get NaN outputs so that a
+// broken length table is visible in the result.
+template <int D, int G>
+__device__ __forceinline__ void decode_bad_length(const DecodeArgs& a, uint32_t b, int hk, bool head_ok, int lane) {
+  constexpr int LPH = D / 8;
+  const int r = lane % LPH;
+  const uint32_t q_bytes = (uint32_t)a.num_heads_q * D * 2;
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * a.num_heads_q * D, q_bytes);
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kOffsetOutOfRange;
+  const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+#pragma unroll
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, nan4);
+}
+
+// SB = 1, 2, 4, 8, 16: every batch has exactly seqlen_uniform <= SB rows
+// (uniform layout, no cu array).  SB = 0: lengths come from cu and each wave
+// picks the smallest bucket that holds its batch.
+template <int D, int G, int SB>
+__global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeArgs a) {
+  constexpr int LPH = D / 8;
+  constexpr int HPW = kWaveSize / LPH;
+  constexpr int VP = G * kMaxSeq;
+  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP];
+
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+  const uint32_t unit = blockIdx.x * kWavesPerBlock + wave;
+  if (unit >= a.total_units) return;
+  const uint32_t upb = (uint32_t)a.units_per_batch;
+  const uint32_t b = unit / upb;
+  const uint32_t hg = unit - b * upb;
+  const int hk = (int)hg * HPW + lane / LPH;
+  const bool head_ok = hk < a.num_heads_kv;
+  uint16_t* lds_wave = lds_p + wave * HPW * VP;
+
+  if constexpr (SB != 0) {
+    const int S = a.seqlen_uniform;
+    decode_unit<D, G, SB>(a, b, (int64_t)b * S, S, hk, head_ok, lane, lds_wave);
+  } else {
+    const int c0 = a.cu[b];
+    const int c1 = a.cu[b + 1];
+    const int S = c1 - c0;
+    if (S < 0 || S > kMaxSeq) {
+      decode_bad_length<D, G>(a, b, hk, head_ok, lane);
+    } else if (S <= 1) {
+      decode_unit<D, G, 1>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    } else if (S <= 2) {
+      decode_unit<D, G, 2>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    } else if (S <= 4) {
+      decode_unit<D, G, 4>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    } else if (S <= 8) {
+      decode_unit<D, G, 8>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    } else {
+      decode_unit<D, G, 16>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    }
+  }
+}
+
+}  // namespace fmha_decode

@@ -1,0 +1,116 @@
+"""Host-side interface of the decode-attention path.
+
+Two levels, both thin wrappers over the C ABI in include/fmha_decode.h:
+
+* launch_fmha_decode / launch_fmha_decode_uniform -- pointer level, the same
+  parameters, order and meaning as the reference's launch helper
+  launch_fmha_mfma_4x4x4 (fmha_mfma_4x4x4_kernel.hpp:370-376) without the
+  caller-chosen grid/block; a rejected call raises FmhaDecodeError instead of
+  failing silently.
+* fmha_decode -- tensor level, for torch device tensors: checks shapes,
+  dtypes and devices, allocates O if not given, launches on torch's current
+  stream.
+"""
+import math
+
+from . import _lib
+
+MAX_SEQLEN_KV = 16
+
+
+class FmhaDecodeError(RuntimeError):
+    """A call the library rejected (code is the hipError_t value returned)."""
+
+    def __init__(self, code, message, detail):
+        super().__init__(f"fmha_decode error {code} ({message}): {detail}")
+        self.code = code
+        self.detail = detail
+
+
+def _raise_if(rc):
+    if rc != 0:
+        lib = _lib.load()
+        raise FmhaDecodeError(rc, lib.fmha_decode_error_string(rc).decode(),
+                              lib.fmha_decode_last_error_detail().decode())
+
+
+def launch_fmha_decode(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv,
+                       seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
+    """Variable-length decode attention on raw device pointers (ints).
+
+    stream is a hipStream_t as an int (0 = null stream).  Mirrors
+    launch_fmha_mfma_4x4x4 (fmha_mfma_4x4x4_kernel.hpp:370-376).
+    """
+    rc = _lib.load().fmha_decode_fwd(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q,
+                                     num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                     float(softmax_scale))
+    _raise_if(rc)
+
+
+def launch_fmha_decode_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv,
+                               seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
+    """Uniform-length decode attention (K/V as [batch, seqlen_kv, Hkv, D])."""
+    rc = _lib.load().fmha_decode_fwd_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q,
+                                             num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                             float(softmax_scale))
+    _raise_if(rc)
+
+
+def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None, out=None):
+    """Decode attention on torch tensors; returns O (fp16, shaped like q).
+
+    q: [B, Hq, 1, D] or [B, Hq, D], bfloat16, contiguous, on a GPU.
+    k, v: [rows, Hkv, D] packed (with cu_seqlens_kv) or [B, S, Hkv, D]
+      (uniform, with seqlen_kv or inferred from the shape); bfloat16.
+    cu_seqlens_kv: int32 [B+1] on the same device, or None.
+    softmax_scale: defaults to 1/sqrt(D), as the reference passes
+      (fmha_host.cpp:371).
+    """
+    import torch
+
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise ValueError("q must have seqlen_q == 1")
+        B, Hq, _, D = q.shape
+    elif q.dim() == 3:
+        B, Hq, D = q.shape
+    else:
+        raise ValueError("q must be [B, Hq, 1, D] or [B, Hq, D]")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16 (got {t.dtype})")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if k.shape != v.shape:
+        raise ValueError("k and v must have the same shape")
+    Hkv = k.shape[-2]
+    if k.shape[-1] != D:
+        raise ValueError("k/v head_dim must equal q head_dim")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    elif out.dtype != torch.float16 or out.shape != q.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float16 tensor shaped like q")
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    if cu_seqlens_kv is not None:
+        if cu_seqlens_kv.dtype != torch.int32 or cu_seqlens_kv.numel() != B + 1:
+            raise ValueError("cu_seqlens_kv must be int32 with batch+1 entries")
+        if cu_seqlens_kv.device != q.device or not cu_seqlens_kv.is_contiguous():
+            raise ValueError("cu_seqlens_kv must be a contiguous tensor on q's device")
+        if k.dim() != 3:
+            raise ValueError("packed k/v must be [rows, Hkv, D]")
+        launch_fmha_decode(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                           cu_seqlens_kv.data_ptr(), B, Hq, Hkv, 1, D, D, softmax_scale)
+    else:
+        if seqlen_kv is None:
+            if k.dim() != 4 or k.shape[0] != B:
+                raise ValueError("uniform k/v must be [B, S, Hkv, D] when seqlen_kv is not given")
+            seqlen_kv = k.shape[1]
+        if k.numel() != B * seqlen_kv * Hkv * D:
+            raise ValueError("k/v size does not match batch * seqlen_kv * Hkv * D")
+        launch_fmha_decode_uniform(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                   seqlen_kv, B, Hq, Hkv, 1, D, D, softmax_scale)
+    return out

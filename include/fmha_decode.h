@@ -1,0 +1,112 @@
+/*
+ * fmha_decode.h -- C ABI of the MI355X (gfx950) decode-attention library
+ * (libfmha_decode.so).
+ *
+ * The path: one query token per sequence (seqlen_q == 1) attending to a short
+ * KV cache of 0..16 tokens, bf16 Q/K/V, fp32 accumulation, fp16 output:
+ *
+ *   for every batch b and query head h (kv head hk = h / (Hq / Hkv)):
+ *     s_j = sum_d Q[b,h,d] * K[cu[b]+j, hk, d]                  j < S_b
+ *     P_j = bf16( exp(s_j*scale - max) / sum_i exp(s_i*scale - max) )
+ *     O[b,h,d] = fp16( sum_j P_j * V[cu[b]+j, hk, d] )
+ *
+ * Layouts (element counts, row-major, no padding):
+ *   Q  [batch, num_heads_q, 1, head_dim]    bf16   (BHSD with S = 1)
+ *   O  [batch, num_heads_q, 1, head_dim]    fp16
+ *   K  [total_kv, num_heads_kv, head_dim]   bf16   packed over batches
+ *   V  [total_kv, num_heads_kv, head_dim]   bf16   packed over batches
+ *   cu_seqlens_kv [batch + 1]               int32  batch b owns rows
+ *                                                  [cu[b], cu[b+1]) of K/V
+ *
+ * All pointers are device pointers owned by the caller.  Calls are
+ * asynchronous on the given stream (a hipStream_t passed as void*, NULL for
+ * the null stream), allocate nothing, keep no mutable global state and may be
+ * issued from any number of host threads.
+ *
+ * Return value: 0 (hipSuccess) or a hipError_t value.  Arguments are checked
+ * before anything touches the GPU; a rejected call launches nothing.
+ */
+#ifndef FMHA_DECODE_H_
+#define FMHA_DECODE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest KV length per sequence the kernels accept (the reference hard-codes
+ * the same bound: fmha_mfma_4x4x4_kernel.hpp:179, fmha_host.cpp:164). */
+#define FMHA_DECODE_MAX_SEQLEN_KV 16
+
+/* hipError_t values returned by this library. */
+#define FMHA_DECODE_SUCCESS 0
+#define FMHA_DECODE_ERROR_INVALID_VALUE 1    /* hipErrorInvalidValue */
+#define FMHA_DECODE_ERROR_NOT_SUPPORTED 801  /* hipErrorNotSupported */
+
+/*
+ * Variable-length decode attention.
+ *
+ * Replaces launch_fmha_mfma_4x4x4 (reference fmha_mfma_4x4x4_kernel.hpp:370-376):
+ * the same parameters in the same order and meaning, without the caller-chosen
+ * grid/block (the library picks its own launch shape), with the stream passed
+ * as void* and with an error code instead of void.
+ *
+ *   stream          hipStream_t to launch on (NULL = null stream)
+ *   Q, K, V, O      device pointers, 16-byte aligned, layouts above
+ *   cu_seqlens_kv   device int32 [batch+1], non-decreasing, cu[0] = 0 is not
+ *                   required (any base offset works); each S_b = cu[b+1]-cu[b]
+ *                   must lie in [0, 16].  A batch with S_b == 0 gets O = 0 (as
+ *                   the reference CPU loop does).  A batch with S_b outside
+ *                   [0, 16] gets O = NaN: the kernel cannot return an error.
+ *   batch           >= 0 (0 launches nothing)
+ *   num_heads_q     > 0, a multiple of num_heads_kv
+ *   num_heads_kv    > 0; num_heads_q / num_heads_kv must be 1, 2, 4 or 8
+ *   seqlen_q        must be 1 (decode)
+ *   head_dim_q      64, 128 or 256
+ *   head_dim_kv     must equal head_dim_q
+ *   softmax_scale   finite; the reference passes 1/sqrt(head_dim)
+ *                   (fmha_host.cpp:371)
+ *
+ * Unlike the reference kernel, which indexes K/V with the query head
+ * (fmha_mfma_4x4x4_kernel.hpp:195-196), query head h reads KV head
+ * h / (num_heads_q / num_heads_kv) (grouped-query attention).
+ */
+int fmha_decode_fwd(void* stream,
+                    const void* Q, const void* K, const void* V, void* O,
+                    const int32_t* cu_seqlens_kv,
+                    int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                    int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                    float softmax_scale);
+
+/*
+ * Uniform-length decode attention: every batch has seqlen_kv KV rows, K and V
+ * are [batch, seqlen_kv, num_heads_kv, head_dim] (the packed layout above with
+ * cu[b] = b * seqlen_kv), and no cu_seqlens array is read.  This is the
+ * launch contract's seqlen_kv parameter; the reference derives every length
+ * from cu_seqlens_kv instead (fmha_mfma_4x4x4_kernel.hpp:94-96).
+ * seqlen_kv must lie in [0, 16]; with seqlen_kv == 0 no row is read, every
+ * output is 0 and K and V may be NULL.  Other arguments as fmha_decode_fwd.
+ */
+int fmha_decode_fwd_uniform(void* stream,
+                            const void* Q, const void* K, const void* V, void* O,
+                            int32_t seqlen_kv,
+                            int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                            int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                            float softmax_scale);
+
+/* Human-readable text for a code returned above (never NULL). */
+const char* fmha_decode_error_string(int code);
+
+/* Text describing why the most recent call on this host thread was rejected
+ * ("" after a successful call). */
+const char* fmha_decode_last_error_detail(void);
+
+/* Library version, encoded as major*10000 + minor*100 + patch. */
+int fmha_decode_version(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FMHA_DECODE_H_ */

@@ -1,0 +1,97 @@
+"""Shared helpers for the tests: seeded inputs, launching through the C ABI,
+checking against the oracle with the documented gate.
+
+Gate (written here, used by every parity test): an output element o passes
+against the oracle value r when
+
+    |o - r| <= ATOL + RTOL * |r| + slack
+
+with ATOL = 2e-3, RTOL = 1e-2 (read allclose-style)
+and slack = sum_j |bf16(p_j(1+eps)) - bf16(p_j(1-eps))| * |V_jd|, eps = 2^-19:
+non-zero only where a softmax weight sits next to a bf16 rounding midpoint,
+where an fp32 rounding difference legitimately flips the reference's bf16
+rounding of that weight (fmha_host.cpp:225).  The reference's own rule
+|o - r| <= 1e-2 + 1e-2|r| (fmha_host.cpp:260) is checked too, with no slack.
+"""
+import math
+
+import numpy as np
+
+import oracle
+
+ATOL = 2e-3
+RTOL = 1e-2
+
+# (B, Hq, Hkv, S, D, std)
+CONFIGS = {
+    1: (30720, 16, 16, 1, 128, 1.0),
+    2: (30720, 16, 16, 16, 128, 1.0),
+    3: (30720, 16, 16, 5, 256, 1.0),
+    4: (30720, 32, 16, 16, 128, 1.0),
+    5: (30720, 32, 32, 16, 256, 2.0),
+}
+
+
+def default_scale(d):
+    # fmha_host.cpp:371 passes 1.0f / sqrt(head_dim); in float32 this equals
+    # 1.0f / sqrtf(head_dim) (fmha_host.cpp:211) for every supported D.
+    return float(np.float32(1.0) / np.sqrt(np.float32(d)))
+
+
+def cu_from_seqlens(seqlens):
+    return np.concatenate([[0], np.cumsum(np.asarray(seqlens, dtype=np.int64))]).astype(np.int32)
+
+
+def bf16_normal(shape, gen, std=1.0):
+    """Seeded N(0, std) rounded to bf16 (torch RNE), as uint16 bits."""
+    import torch
+    x = torch.randn(*shape, generator=gen, dtype=torch.float32) * std
+    return x.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def make_inputs(B, Hq, Hkv, D, seqlens, seed, std=1.0):
+    import torch
+    gen = torch.Generator().manual_seed(seed)
+    cu = cu_from_seqlens(seqlens)
+    rows = int(cu[-1])
+    q = bf16_normal((B, Hq, D), gen, std)
+    k = bf16_normal((rows, Hkv, D), gen, std)
+    v = bf16_normal((rows, Hkv, D), gen, std)
+    return q, k, v, cu
+
+
+def to_dev(bits, device="cuda"):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device)
+    return t.view(torch.bfloat16)
+
+
+def run_gpu(q, k, v, cu, Hq, Hkv, D, scale=None, uniform_s=None, device="cuda"):
+    """Launch the HIP kernel through the C ABI; returns O as fp16 bits."""
+    import torch
+    import fmha_amd
+    scale = default_scale(D) if scale is None else scale
+    B = q.shape[0]
+    qd, kd, vd = to_dev(q, device), to_dev(k, device), to_dev(v, device)
+    if uniform_s is None:
+        cud = torch.from_numpy(np.ascontiguousarray(cu)).to(device)
+        o = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, softmax_scale=scale)
+    else:
+        o = fmha_amd.fmha_decode(qd, kd.view(B, uniform_s, Hkv, D), vd.view(B, uniform_s, Hkv, D),
+                                 seqlen_kv=uniform_s, softmax_scale=scale)
+    torch.cuda.synchronize()
+    return o.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def check(o, q, k, v, cu, Hq, Hkv, D, scale=None):
+    """Compare GPU output bits with the oracle; returns the stats dict."""
+    scale = default_scale(D) if scale is None else scale
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, scale, p_mode=0, with_slack=True)
+    st = oracle.compare(o.reshape(r.shape), r, slack, ATOL, RTOL)
+    return st
+
+
+def assert_pass(st, ctx=""):
+    assert st["nonfinite"] == 0, f"{ctx}: non-finite outputs {st}"
+    assert st["fails"] == 0, f"{ctx}: gate failures {st}"
+    assert st["ref_rule_fails"] == 0, f"{ctx}: reference-rule failures {st}"

@@ -1,0 +1,134 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/fmha_decode.h declares, and rejects bad arguments before touching the
+GPU (no call here reaches a kernel launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "fmha_decode.h")
+BAD = 1      # hipErrorInvalidValue
+NOTSUP = 801  # hipErrorNotSupported
+
+# Fake but 16-byte aligned device addresses: every call below is rejected (or
+# is a batch-0 no-op) before anything dereferences them.
+P = 0x10000
+Q, K, V, O, CU = P, P * 2, P * 3, P * 4, P * 5
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fmha_decode_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from fmha_amd import _lib
+    return _lib.load()
+
+
+def test_exports_every_declared_function(lib):
+    names = header_functions()
+    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_uniform", "fmha_decode_error_string",
+                          "fmha_decode_last_error_detail", "fmha_decode_version"}
+    from fmha_amd import _lib
+    assert set(names) == set(_lib.EXPORTED)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_version_and_strings(lib):
+    assert lib.fmha_decode_version() >= 100
+    assert lib.fmha_decode_error_string(0) == b"success"
+    assert lib.fmha_decode_error_string(BAD) == b"invalid argument"
+    assert lib.fmha_decode_error_string(NOTSUP) == b"configuration not supported"
+
+
+def fwd(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"], a["hq"],
+                               a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
+def uni(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, s=16, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_uniform(a["stream"], a["q"], a["k"], a["v"], a["o"], a["s"], a["batch"],
+                                       a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(batch=-1), BAD, "batch"),
+    (dict(hq=0), BAD, "head counts"),
+    (dict(hkv=0), BAD, "head counts"),
+    (dict(hq=16, hkv=5), BAD, "multiple"),
+    (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
+    (dict(hq=32, hkv=2), NOTSUP, "1, 2, 4 or 8"),
+    (dict(sq=2), BAD, "seqlen_q"),
+    (dict(sq=0), BAD, "seqlen_q"),
+    (dict(dq=128, dkv=256), BAD, "head_dim_q"),
+    (dict(dq=96, dkv=96), BAD, "64, 128 or 256"),
+    (dict(dq=512, dkv=512), BAD, "64, 128 or 256"),
+    (dict(scale=float("nan")), BAD, "finite"),
+    (dict(scale=float("inf")), BAD, "finite"),
+    (dict(q=None), BAD, "non-null"),
+    (dict(o=None), BAD, "non-null"),
+    (dict(k=K + 8), BAD, "aligned"),
+    (dict(o=O + 2), BAD, "aligned"),
+    (dict(cu=None), BAD, "cu_seqlens_kv"),
+    (dict(cu=CU + 2), BAD, "cu_seqlens_kv"),
+    (dict(hq=1 << 20, hkv=1 << 20), BAD, "too large"),
+])
+def test_varlen_rejects(lib, kw, code, needle):
+    assert fwd(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(s=-1), BAD, "seqlen_kv"),
+    (dict(s=17), BAD, "seqlen_kv"),
+    (dict(s=1000), BAD, "seqlen_kv"),
+    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    (dict(v=None), BAD, "non-null"),
+])
+def test_uniform_rejects(lib, kw, code, needle):
+    assert uni(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+def test_batch_zero_is_a_noop(lib):
+    # Nothing is launched and no pointer is needed for an empty batch.
+    assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
+    assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
+    assert lib.fmha_decode_last_error_detail() == b""
+
+
+def test_python_wrapper_raises(lib):
+    import fmha_amd
+    with pytest.raises(fmha_amd.FmhaDecodeError) as ei:
+        fmha_amd.launch_fmha_decode(0, Q, K, V, O, CU, 4, 16, 16, 2, 128, 128, 0.1)
+    assert ei.value.code == BAD and "seqlen_q" in ei.value.detail
+
+
+def test_compat_header_compiles():
+    """include/fmha_decode_compat.hpp (the drop-in for the reference's
+    launch_fmha_mfma_4x4x4) compiles as host code against the C ABI."""
+    import subprocess
+    import tempfile
+    src = ('#include "fmha_decode_compat.hpp"\n'
+           'void f(const bhalf_t* q, const bhalf_t* k, const bhalf_t* v, half_t* o, const int* cu) {\n'
+           '  launch_fmha_mfma_4x4x4(dim3(1, 1, 10), dim3(256, 1, 1), 0, q, k, v, o, cu,\n'
+           '                         10, 16, 16, 1, 128, 128, 0.0883883f);\n}\n')
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "t.cpp")
+        open(p, "w").write(src)
+        r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-fsyntax-only", "-x", "hip",
+                            "--offload-arch=gfx950", "-I", os.path.join(ROOT, "include"), p],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
