@@ -35,34 +35,77 @@ int reject(int code, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Concurrency cap.  Each wave issues all of its loads at once; MI355X
+// streams best with about 128 KiB of requests in flight per CU (measured:
+// 3-5 waves of the S=16, D=128 unit per CU beat the 5-6 that registers
+// allow by 4%).  The library reserves unused LDS per workgroup so that
+// only that many waves fit on a CU.
+constexpr int kInflightBytesPerCU = 128 * 1024;
+constexpr int kMaxWavesPerCU = 32;
+
+// Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
+// on a CU with `lds_per_cu` bytes (0 when no cap is needed).
+size_t lds_reserve_for(int waves, int lds_per_cu, size_t static_lds) {
+  if (waves >= kMaxWavesPerCU || lds_per_cu <= 0) return 0;
+  // Midway between the per-group share that fits `waves` groups and the one
+  // that would fit `waves + 1`, so allocation granularity cannot tip it.
+  const size_t hi = (size_t)lds_per_cu / waves;
+  const size_t lo = (size_t)lds_per_cu / (waves + 1);
+  const size_t per_group = (hi + lo) / 2;
+  return per_group > static_lds ? per_group - static_lds : 0;
+}
+
+int lds_per_cu() {
+  int dev = 0, bytes = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess) return 0;
+  return bytes;
+}
+
 template <int D, int G, int SB>
-hipError_t launch_one(const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
+  const auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, SB>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL((fmha_decode::fmha_decode_fwd_kernel<D, G, SB>), dim3(blocks), dim3(kBlockThreads), 0,
-                     stream, a);
+  hipFuncAttributes attr;
+  size_t static_lds = 0;
+  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess)
+    static_lds = attr.sharedSizeBytes;
+  const size_t dyn = lds_reserve_for(waves_per_cu, lds_per_cu(), static_lds);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), dyn, stream, a);
   return hipGetLastError();
 }
 
 template <int D, int G>
-hipError_t launch_bucket(const DecodeArgs& a, int sb, hipStream_t stream) {
+hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
   switch (sb) {
-    case 0: return launch_one<D, G, 0>(a, stream);
-    case 1: return launch_one<D, G, 1>(a, stream);
-    case 2: return launch_one<D, G, 2>(a, stream);
-    case 4: return launch_one<D, G, 4>(a, stream);
-    case 8: return launch_one<D, G, 8>(a, stream);
-    default: return launch_one<D, G, 16>(a, stream);
+    case 0: return launch_one<D, G, 0>(a, w, stream);
+    case 1: return launch_one<D, G, 1>(a, w, stream);
+    case 2: return launch_one<D, G, 2>(a, w, stream);
+    case 4: return launch_one<D, G, 4>(a, w, stream);
+    case 8: return launch_one<D, G, 8>(a, w, stream);
+    default: return launch_one<D, G, 16>(a, w, stream);
   }
 }
 
 template <int D>
-hipError_t launch_group(const DecodeArgs& a, int g, int sb, hipStream_t stream) {
+hipError_t launch_group(const DecodeArgs& a, int g, int sb, int w, hipStream_t stream) {
   switch (g) {
-    case 1: return launch_bucket<D, 1>(a, sb, stream);
-    case 2: return launch_bucket<D, 2>(a, sb, stream);
-    case 4: return launch_bucket<D, 4>(a, sb, stream);
-    default: return launch_bucket<D, 8>(a, sb, stream);
+    case 1: return launch_bucket<D, 1>(a, sb, w, stream);
+    case 2: return launch_bucket<D, 2>(a, sb, w, stream);
+    case 4: return launch_bucket<D, 4>(a, sb, w, stream);
+    default: return launch_bucket<D, 8>(a, sb, w, stream);
   }
+}
+
+// Waves per CU for a unit that moves `rows` K/V rows and G query heads:
+// each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
+// of Q in and 1 KiB of O out.
+int waves_per_cu_for(int rows, int g) {
+  const int unit_bytes = 1024 * (2 * rows + 2 * g);
+  int w = kInflightBytesPerCU / unit_bytes;
+  if (w < 3) w = 3;
+  if (w > kMaxWavesPerCU) w = kMaxWavesPerCU;
+  return w;
 }
 
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
@@ -126,12 +169,14 @@ int launch(void* stream, const void* Q, const void* K, const void* V, void* O, c
   a.scale = scale;
   const int sb = cu ? 0 : bucket_for(seqlen_kv);
   const int g = hq / hkv;
+  // Varlen batches: lengths are on the device; size the cap for 8 rows.
+  const int w = waves_per_cu_for(cu ? 8 : seqlen_kv, g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   switch (dq) {
-    case 64: err = launch_group<64>(a, g, sb, s); break;
-    case 128: err = launch_group<128>(a, g, sb, s); break;
-    default: err = launch_group<256>(a, g, sb, s); break;
+    case 64: err = launch_group<64>(a, g, sb, w, s); break;
+    case 128: err = launch_group<128>(a, g, sb, w, s); break;
+    default: err = launch_group<256>(a, g, sb, w, s); break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;

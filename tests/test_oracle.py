@@ -1,0 +1,244 @@
+"""Pins the CPU oracle (oracle/fmha_oracle.cpp) before anything is compared
+with it.  Each check is chosen so that a plausible mistake in the oracle (a
+dropped term, a wrong head mapping, a transposed index, a wrong rounding)
+fails at least one of them:
+
+  * bit-exact against the reference's own CPU loop: committed fixtures
+    (tests/golden/mha_*.npz, written by the reference's do_validation) and,
+    where the reference build exists, live random cases;
+  * the reference's length generator (tests/golden/seqlens_ref.json);
+  * float64 mode against torch's float64 scaled_dot_product_attention
+    (committed GQA fixtures and live cases);
+  * closed forms: S=1 gives fp16(V); Q=0 gives uniform bf16(1/S) weights; one
+    dominant key gives fp16(V_j); S=0 gives 0;
+  * invariants: GQA equals MHA on head-repeated K/V bit for bit; batch
+    independence; permutation of the KV rows changes the result only within
+    the gate;
+  * rounding helpers against torch (bf16) and numpy (fp16) over every bf16
+    bit pattern and random fp32 patterns.
+"""
+import glob
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.common import ATOL, RTOL, cu_from_seqlens, default_scale, make_inputs
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+needs_ref = pytest.mark.skipif(not oracle.ref_available(),
+                               reason="oracle/_ref not built (the reference is not mounted here)")
+
+
+def _f32(bits):
+    return oracle.bf16_to_f32(bits)
+
+
+# ---------------------------------------------------------------- rounding
+def test_f32_to_bf16_matches_torch():
+    import torch
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32),
+                           # exact ties and near-ties around every rounding step
+                           (np.arange(0, 2 ** 16, dtype=np.uint32) << 16) | 0x8000,
+                           (np.arange(0, 2 ** 16, dtype=np.uint32) << 16) | 0x7fff,
+                           (np.arange(0, 2 ** 16, dtype=np.uint32) << 16) | 0x8001]).astype(np.uint32)
+    x = bits.view(np.float32)
+    finite = np.isfinite(x)
+    got = oracle.f32_to_bf16(x[finite])
+    want = torch.from_numpy(x[finite].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f32_to_f16_matches_numpy():
+    rng = np.random.default_rng(1)
+    # every bf16 value (the shape of the kernel's S=1 output path) plus random
+    # fp32 patterns concentrated on the fp16 range, ties included
+    allbf = (np.arange(0, 2 ** 16, dtype=np.uint32) << 16).view(np.float32)
+    rnd = rng.integers(0, 2 ** 32, 300000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    small = (rng.standard_normal(300000) * np.exp(rng.uniform(-20, 12, 300000))).astype(np.float32)
+    f16 = np.arange(0, 2 ** 16, dtype=np.uint16).view(np.float16).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        ties = ((f16[:-1].astype(np.float64) + f16[1:].astype(np.float64)) / 2).astype(np.float32)
+    x = np.concatenate([allbf, rnd, small, ties])
+    x = x[~np.isnan(x)]
+    got = oracle.f32_to_f16(x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- reference
+def test_seqlens_match_reference_fixture():
+    fx = json.load(open(os.path.join(GOLDEN, "seqlens_ref.json")))
+    got = oracle.generate_seqlens(len(fx["seqlens"]), 16)
+    assert got.tolist() == fx["seqlens"]
+    assert all(2 <= s <= 16 for s in got)
+
+
+@needs_ref
+def test_seqlens_match_reference_live():
+    for b, m in [(1000, 16), (10, 16), (257, 8), (64, 4)]:
+        assert np.array_equal(oracle.generate_seqlens(b, m), oracle.ref_generate_seqlens(b, m))
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "mha_*.npz"))))
+def test_bitexact_reference_fixtures(path):
+    z = np.load(path, allow_pickle=False)
+    B, Hq, Hkv, D = z["meta"].tolist()
+    o, _ = oracle.decode(z["q"], z["k"], z["v"], z["cu"], Hq, Hkv, D, default_scale(D))
+    assert np.array_equal(o, z["o"])
+
+
+@needs_ref
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("H", [1, 4, 16])
+def test_bitexact_reference_live(D, H, capfd):
+    seqlens = oracle.generate_seqlens(48, 16)
+    seqlens[:3] = [1, 16, 5]
+    q, k, v, cu = make_inputs(48, H, H, D, seqlens, seed=D + H, std=2.0 if D == 256 else 1.0)
+    o, _ = oracle.decode(q, k, v, cu, H, H, D, default_scale(D))
+    r, ok = oracle.ref_do_validation(q, k, v, cu, H, H, D, gpu_o=o)
+    capfd.readouterr()  # the reference prints while it validates
+    assert ok and np.array_equal(o, r)
+
+
+# ---------------------------------------------------------------- float64
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "gqa_sdpa_*.npz"))))
+def test_f64_against_sdpa_fixtures(path):
+    z = np.load(path, allow_pickle=False)
+    B, Hq, Hkv, D = z["meta"].tolist()
+    o = oracle.decode_f64(z["q"], z["k"], z["v"], z["cu"], Hq, Hkv, D, 1.0 / np.sqrt(D))
+    assert np.max(np.abs(o - z["o"])) < 1e-12
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 64), (8, 2, 128), (4, 1, 256)])
+def test_f64_against_sdpa_live(Hq, Hkv, D):
+    import torch
+    seqlens = [1, 2, 9, 16]
+    q, k, v, cu = make_inputs(len(seqlens), Hq, Hkv, D, seqlens, seed=Hq * D)
+    o = oracle.decode_f64(q, k, v, cu, Hq, Hkv, D, 1.0 / np.sqrt(D))
+    t = lambda a: torch.from_numpy(_f32(a)).double()
+    for b in range(len(seqlens)):
+        kb = t(k[cu[b]:cu[b + 1]]).repeat_interleave(Hq // Hkv, 1).transpose(0, 1)
+        vb = t(v[cu[b]:cu[b + 1]]).repeat_interleave(Hq // Hkv, 1).transpose(0, 1)
+        ref = torch.nn.functional.scaled_dot_product_attention(t(q[b]).unsqueeze(1), kb, vb,
+                                                               scale=1.0 / np.sqrt(D))[:, 0]
+        assert np.max(np.abs(o[b] - ref.numpy())) < 1e-12
+
+
+def test_bf16_weights_within_rounding_bound_of_f64():
+    """The bf16-P output differs from the float64 truth by at most the weight
+    rounding (unit roundoff 2^-8 per weight, so sum_j 2^-8 p_j |V_jd| <=
+    2^-8 max_j |V_jd|), fp32 sums and one fp16 rounding (2^-11, doubled)."""
+    seqlens = oracle.generate_seqlens(64, 16)
+    q, k, v, cu = make_inputs(64, 8, 4, 128, seqlens, seed=5)
+    o, _ = oracle.decode(q, k, v, cu, 8, 4, 128, default_scale(128))
+    t = oracle.decode_f64(q, k, v, cu, 8, 4, 128, default_scale(128))
+    vabs = np.abs(_f32(v)).astype(np.float64)
+    of = oracle.f16_to_f32(o).astype(np.float64)
+    for b in range(64):
+        bound = 2.0 ** -8 * vabs[cu[b]:cu[b + 1]].max(axis=0).repeat(2, axis=0) + 1e-4
+        bound = bound + np.abs(t[b]) * 2.0 ** -10
+        assert np.all(np.abs(of[b] - t[b]) <= bound)
+
+
+# ---------------------------------------------------------------- closed forms
+def test_s1_is_fp16_of_v():
+    q, k, v, cu = make_inputs(9, 4, 2, 128, [1] * 9, seed=7)
+    o, _ = oracle.decode(q, k, v, cu, 4, 2, 128, default_scale(128))
+    want = oracle.f32_to_f16(np.repeat(_f32(v), 2, axis=1))
+    assert np.array_equal(o, want)
+
+
+def test_s0_is_zero():
+    q, k, v, cu = make_inputs(3, 4, 4, 64, [0, 3, 0], seed=8)
+    o, _ = oracle.decode(q, k, v, cu, 4, 4, 64, default_scale(64))
+    assert not o[0].any() and not o[2].any() and o[1].any()
+
+
+@pytest.mark.parametrize("S", [2, 3, 5, 16])
+def test_zero_query_gives_uniform_bf16_weights(S):
+    q, k, v, cu = make_inputs(2, 4, 4, 128, [S, S], seed=S)
+    q[:] = 0
+    o, _ = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128))
+    w = _f32(oracle.f32_to_bf16(np.float32(1.0) / np.float32(S)))  # bf16(1/S)
+    for b in range(2):
+        acc = np.zeros((4, 128), np.float32)
+        for j in range(S):                       # fp32, in row order
+            acc = acc + w * _f32(v[cu[b] + j])
+        assert np.array_equal(o[b], oracle.f32_to_f16(acc))
+
+
+def test_dominant_key_is_one_hot():
+    D, S = 128, 16
+    q, k, v, cu = make_inputs(1, 2, 2, D, [S], seed=11)
+    q[:] = oracle.f32_to_bf16(np.ones((1, 2, D), np.float32))
+    k[:] = oracle.f32_to_bf16(np.full((S, 2, D), -1.0, np.float32))
+    k[6] = oracle.f32_to_bf16(np.full((2, D), 16.0, np.float32))  # logit gap 17*128*scale > 200
+    o, _ = oracle.decode(q, k, v, cu, 2, 2, D, default_scale(D))
+    assert np.array_equal(o[0], oracle.f32_to_f16(_f32(v[6])))
+
+
+# ---------------------------------------------------------------- invariants
+def test_gqa_equals_mha_on_repeated_kv():
+    seqlens = oracle.generate_seqlens(20, 16)
+    for g in (2, 4, 8):
+        q, k, v, cu = make_inputs(20, 2 * g, 2, 128, seqlens, seed=g)
+        o_g, _ = oracle.decode(q, k, v, cu, 2 * g, 2, 128, default_scale(128))
+        o_m, _ = oracle.decode(q, np.repeat(k, g, 1), np.repeat(v, g, 1), cu, 2 * g, 2 * g, 128,
+                               default_scale(128))
+        assert np.array_equal(o_g, o_m)
+        # an interleaved mapping (KV head = h % Hkv) reads other rows; the
+        # check above tells it apart from the grouped one
+        o_wrong, _ = oracle.decode(q, np.tile(k, (1, g, 1)), np.tile(v, (1, g, 1)), cu, 2 * g, 2 * g,
+                                   128, default_scale(128))
+        assert not np.array_equal(o_g, o_wrong)
+
+
+def test_batch_independence():
+    seqlens = [4, 16, 9]
+    q, k, v, cu = make_inputs(3, 4, 4, 128, seqlens, seed=12)
+    o, _ = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128))
+    o1, _ = oracle.decode(q[1:2], k[cu[1]:cu[2]], v[cu[1]:cu[2]], cu_from_seqlens([16]), 4, 4, 128,
+                          default_scale(128))
+    assert np.array_equal(o[1], o1[0])
+
+
+def test_row_permutation_within_gate():
+    seqlens = [16] * 8
+    q, k, v, cu = make_inputs(8, 4, 4, 128, seqlens, seed=13)
+    perm = np.random.default_rng(0).permutation(16)
+    kp = k.reshape(8, 16, 4, 128)[:, perm].reshape(k.shape)
+    vp = v.reshape(8, 16, 4, 128)[:, perm].reshape(v.shape)
+    o, slack = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128), with_slack=True)
+    op, _ = oracle.decode(q, kp, vp, cu, 4, 4, 128, default_scale(128))
+    st = oracle.compare(op, o, slack, ATOL, RTOL)
+    assert st["fails"] == 0 and st["ref_rule_fails"] == 0
+
+
+def test_gate_rejects_planted_error():
+    """The comparison flags a one-element error of 4 fp16 ulps at |r| ~ 1 and
+    a NaN, and accepts identical outputs."""
+    q, k, v, cu = make_inputs(4, 4, 4, 128, [16] * 4, seed=14)
+    o, slack = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128), with_slack=True)
+    assert oracle.compare(o, o, slack)["fails"] == 0
+    bad = o.copy().ravel()
+    i = int(np.argmax(np.abs(oracle.f16_to_f32(bad)) > 0.5))
+    val = oracle.f16_to_f32(bad[i:i + 1])[0]
+    bad[i] = oracle.f32_to_f16(np.array([val * 1.03], np.float32))[0]
+    st = oracle.compare(bad, o.ravel(), None)
+    assert st["fails"] == 1 and st["first_fail"] == i
+    bad[i] = 0x7e00
+    st = oracle.compare(bad, o.ravel(), slack)
+    assert st["fails"] == 1 and st["nonfinite"] == 1
+
+
+def test_rejects_bad_lengths():
+    q, k, v, cu = make_inputs(2, 1, 1, 64, [3, 3], seed=15)
+    with pytest.raises(ValueError):
+        oracle.decode(q, k, v, np.array([0, 17, 6], np.int32), 1, 1, 64, 0.125)
+    with pytest.raises(ValueError):
+        oracle.decode(q, k, v, np.array([0, 4, 3], np.int32), 1, 1, 64, 0.125)
