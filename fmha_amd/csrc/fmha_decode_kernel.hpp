@@ -76,12 +76,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, kBufferWord3);
 }
 
-// Cache-policy operand of the buffer instructions: bit 1 is the non-temporal
-// (streaming) hint on gfx950.  K and V are read exactly once, so they are
-// fetched non-temporally; measured on MI355X this lifts the streaming rate by
-// about 12% over default-policy loads.
+// Cache-policy operand of the buffer instructions (gfx950: bit 0 sc0, bit 1
+// nt, bit 4 sc1).
+//   * K and V are read exactly once: non-temporal (streaming) loads, +12% on
+//     MI355X over default-policy loads.
+//   * O is stored at device scope (sc1): the write goes through the XCD's L2
+//     instead of leaving dirty lines there to be written back later in the
+//     middle of the read stream; +3% on every configuration measured.  The
+//     data is visible to later kernels either way.
+//   * Q keeps the default policy (a non-temporal Q load measured 4% slower).
 constexpr int kPolicyDefault = 0;
 constexpr int kPolicyStream = 2;
+constexpr int kPolicyStoreThrough = 16;
 
 template <int POLICY>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
@@ -90,7 +96,7 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 }
 
 __device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, u32x4 x) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x), r, (int)voffset, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x), r, (int)voffset, 0, kPolicyStoreThrough);
 }
 
 // ---------------------------------------------------------------------------
