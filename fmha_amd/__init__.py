@@ -3,7 +3,8 @@
 grouped-query attention.  The kernels are hand-written HIP in fmha_amd/csrc;
 the C ABI is include/fmha_decode.h; this package is its host-side interface.
 """
-from .decode import (MAX_SEQLEN_KV, FmhaDecodeError, fmha_decode, launch_fmha_decode,
+from .decode import (MAX_SEQLEN_KV, FmhaDecodeError, fmha_decode, fmha_decode_paged, fmha_decode_strided,
+                     launch_fmha_decode, launch_fmha_decode_paged, launch_fmha_decode_strided,
                      launch_fmha_decode_uniform)
 from ._lib import LIB_PATH, EXPORTED
 
@@ -11,6 +12,10 @@ __all__ = [
     "MAX_SEQLEN_KV",
     "FmhaDecodeError",
     "fmha_decode",
+    "fmha_decode_strided",
+    "fmha_decode_paged",
+    "launch_fmha_decode_strided",
+    "launch_fmha_decode_paged",
     "launch_fmha_decode",
     "launch_fmha_decode_uniform",
     "LIB_PATH",

@@ -13,6 +13,8 @@ LIB_PATH = os.path.join(_HERE, "libfmha_decode.so")
 EXPORTED = (
     "fmha_decode_fwd",
     "fmha_decode_fwd_uniform",
+    "fmha_decode_fwd_strided",
+    "fmha_decode_fwd_paged",
     "fmha_decode_error_string",
     "fmha_decode_last_error_detail",
     "fmha_decode_version",
@@ -35,6 +37,12 @@ def load():
     lib.fmha_decode_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_uniform.restype = ctypes.c_int
     lib.fmha_decode_fwd_uniform.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
+    i64 = ctypes.c_int64
+    lib.fmha_decode_fwd_strided.restype = ctypes.c_int
+    lib.fmha_decode_fwd_strided.argtypes = [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, i32, i32,
+                                            i32, f32]
+    lib.fmha_decode_fwd_paged.restype = ctypes.c_int
+    lib.fmha_decode_fwd_paged.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_error_string.restype = ctypes.c_char_p
     lib.fmha_decode_error_string.argtypes = [ctypes.c_int]
     lib.fmha_decode_last_error_detail.restype = ctypes.c_char_p

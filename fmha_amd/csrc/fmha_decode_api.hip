@@ -62,9 +62,9 @@ int lds_per_cu() {
   return bytes;
 }
 
-template <int D, int G, int SB>
+template <int D, int G, int LAYOUT, int SB>
 hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  const auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, SB>;
+  const auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipFuncAttributes attr;
   size_t static_lds = 0;
@@ -75,25 +75,40 @@ hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream)
   return hipGetLastError();
 }
 
-template <int D, int G>
+// sb: 0 = lengths from a.lens (bucket picked per wave), else the uniform
+// length's power-of-two bucket.  The paged layout always reads lengths.
+template <int D, int G, int LAYOUT>
 hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
-  switch (sb) {
-    case 0: return launch_one<D, G, 0>(a, w, stream);
-    case 1: return launch_one<D, G, 1>(a, w, stream);
-    case 2: return launch_one<D, G, 2>(a, w, stream);
-    case 4: return launch_one<D, G, 4>(a, w, stream);
-    case 8: return launch_one<D, G, 8>(a, w, stream);
-    default: return launch_one<D, G, 16>(a, w, stream);
+  if constexpr (LAYOUT == fmha_decode::kLayoutPaged) {
+    return launch_one<D, G, LAYOUT, 0>(a, w, stream);
+  } else {
+    switch (sb) {
+      case 0: return launch_one<D, G, LAYOUT, 0>(a, w, stream);
+      case 1: return launch_one<D, G, LAYOUT, 1>(a, w, stream);
+      case 2: return launch_one<D, G, LAYOUT, 2>(a, w, stream);
+      case 4: return launch_one<D, G, LAYOUT, 4>(a, w, stream);
+      case 8: return launch_one<D, G, LAYOUT, 8>(a, w, stream);
+      default: return launch_one<D, G, LAYOUT, 16>(a, w, stream);
+    }
   }
 }
 
-template <int D>
+template <int D, int LAYOUT>
 hipError_t launch_group(const DecodeArgs& a, int g, int sb, int w, hipStream_t stream) {
   switch (g) {
-    case 1: return launch_bucket<D, 1>(a, sb, w, stream);
-    case 2: return launch_bucket<D, 2>(a, sb, w, stream);
-    case 4: return launch_bucket<D, 4>(a, sb, w, stream);
-    default: return launch_bucket<D, 8>(a, sb, w, stream);
+    case 1: return launch_bucket<D, 1, LAYOUT>(a, sb, w, stream);
+    case 2: return launch_bucket<D, 2, LAYOUT>(a, sb, w, stream);
+    case 4: return launch_bucket<D, 4, LAYOUT>(a, sb, w, stream);
+    default: return launch_bucket<D, 8, LAYOUT>(a, sb, w, stream);
+  }
+}
+
+template <int LAYOUT>
+hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_group<64, LAYOUT>(a, g, sb, w, stream);
+    case 128: return launch_group<128, LAYOUT>(a, g, sb, w, stream);
+    default: return launch_group<256, LAYOUT>(a, g, sb, w, stream);
   }
 }
 
@@ -148,39 +163,45 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
   return FMHA_DECODE_SUCCESS;
 }
 
-int launch(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu, int32_t seqlen_kv,
-           int32_t batch, int32_t hq, int32_t hkv, int32_t dq, float scale) {
+// Fills the layout-independent fields, picks the wave cap and launches.
+// rows_hint: KV rows per batch used to size the per-CU wave cap.
+int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows_hint) {
   const int heads_per_wave = kWaveSize / (dq / 8);
-  const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
+  const int64_t upb = (a.num_heads_kv + heads_per_wave - 1) / heads_per_wave;
   const int64_t units = upb * batch;
   if (units > (int64_t)UINT32_MAX - kWavesPerBlock)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
-  DecodeArgs a;
-  a.q = static_cast<const uint16_t*>(Q);
-  a.k = static_cast<const uint16_t*>(K);
-  a.v = static_cast<const uint16_t*>(V);
-  a.o = static_cast<uint16_t*>(O);
-  a.cu = cu;
-  a.seqlen_uniform = seqlen_kv;
-  a.num_heads_q = hq;
-  a.num_heads_kv = hkv;
   a.units_per_batch = (int32_t)upb;
   a.total_units = (uint32_t)units;
-  a.scale = scale;
-  const int sb = cu ? 0 : bucket_for(seqlen_kv);
-  const int g = hq / hkv;
-  // Varlen batches: lengths are on the device; size the cap for 8 rows.
-  const int w = waves_per_cu_for(cu ? 8 : seqlen_kv, g);
+  const int g = a.num_heads_q / a.num_heads_kv;
+  const int w = waves_per_cu_for(rows_hint, g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
-  switch (dq) {
-    case 64: err = launch_group<64>(a, g, sb, w, s); break;
-    case 128: err = launch_group<128>(a, g, sb, w, s); break;
-    default: err = launch_group<256>(a, g, sb, w, s); break;
+  switch (layout) {
+    case fmha_decode::kLayoutPacked: err = launch_dim<fmha_decode::kLayoutPacked>(a, dq, g, sb, w, s); break;
+    case fmha_decode::kLayoutStrided: err = launch_dim<fmha_decode::kLayoutStrided>(a, dq, g, sb, w, s); break;
+    default: err = launch_dim<fmha_decode::kLayoutPaged>(a, dq, g, sb, w, s); break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
 }
+
+DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32_t hq, int32_t hkv, float scale) {
+  DecodeArgs a = {};
+  a.q = static_cast<const uint16_t*>(Q);
+  a.k = static_cast<const uint16_t*>(K);
+  a.v = static_cast<const uint16_t*>(V);
+  a.o = static_cast<uint16_t*>(O);
+  a.num_heads_q = hq;
+  a.num_heads_kv = hkv;
+  a.scale = scale;
+  a.max_rows = FMHA_DECODE_MAX_SEQLEN_KV;
+  return a;
+}
+
+// Rows a lengths array may announce, for sizing the wave cap: the
+// reference's own varlen workload averages 4.3 rows; 8 covers it.
+constexpr int kVarlenRowsHint = 8;
 
 }  // namespace
 
@@ -195,7 +216,11 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
-  return launch(stream, Q, K, V, O, cu_seqlens_kv, 0, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
+  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.lens = cu_seqlens_kv;
+  a.row_stride = num_heads_kv * head_dim_q;
+  a.head_stride = head_dim_q;
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
 }
 
 extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -209,8 +234,80 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, seqlen_kv == 0);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
-  return launch(stream, Q, K, V, O, nullptr, seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q,
-                softmax_scale);
+  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.seqlen_uniform = seqlen_kv;
+  a.row_stride = num_heads_kv * head_dim_q;
+  a.head_stride = head_dim_q;
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), seqlen_kv);
+}
+
+extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       const int32_t* seqlens_kv, int32_t seqlen_kv, int64_t kv_batch_stride,
+                                       int64_t kv_row_stride, int64_t kv_head_stride, int32_t batch,
+                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
+  g_detail[0] = '\0';
+  if (seqlen_kv < 0 || (!seqlens_kv && seqlen_kv > FMHA_DECODE_MAX_SEQLEN_KV))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE,
+                  "seqlen_kv must be >= 0, and <= %d when seqlens_kv is null (got %d)", FMHA_DECODE_MAX_SEQLEN_KV,
+                  seqlen_kv);
+  const int cap = seqlen_kv < FMHA_DECODE_MAX_SEQLEN_KV ? seqlen_kv : FMHA_DECODE_MAX_SEQLEN_KV;
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, cap == 0);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
+  if ((kv_batch_stride | kv_row_stride | kv_head_stride) & 7)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be multiples of 8 elements (16 bytes)");
+  // Bytes one batch's descriptor may span must stay below 2^30.
+  const int64_t extent = cap == 0 ? 0
+                                  : (int64_t)(cap - 1) * kv_row_stride +
+                                        (int64_t)(num_heads_kv - 1) * kv_head_stride + head_dim_q;
+  if (extent * 2 >= (int64_t(1) << 30))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "one batch's K/V span exceeds 1 GiB");
+  if (seqlens_kv && (reinterpret_cast<uintptr_t>(seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlens_kv must be 4-byte aligned");
+  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.lens = seqlens_kv;
+  a.seqlen_uniform = seqlens_kv ? 0 : seqlen_kv;
+  a.max_rows = cap;
+  a.batch_stride = kv_batch_stride;
+  a.row_stride = (int32_t)kv_row_stride;
+  a.head_stride = (int32_t)kv_head_stride;
+  const int sb = seqlens_kv ? 0 : bucket_for(seqlen_kv);
+  return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb,
+                seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv);
+}
+
+extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_cache, const void* V_cache, void* O,
+                                     const int32_t* block_table, int32_t block_table_stride,
+                                     const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
+                                     int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                     int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K_cache, V_cache, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (page_size < 1 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "page_size must be a power of two in [1, 2^20] (got %d)",
+                  page_size);
+  if (!block_table || !seqlens_kv)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "block_table and seqlens_kv must be non-null");
+  if (((reinterpret_cast<uintptr_t>(block_table) | reinterpret_cast<uintptr_t>(seqlens_kv)) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "block_table and seqlens_kv must be 4-byte aligned");
+  if (block_table_stride < 1)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "block_table_stride must be >= 1 (got %d)", block_table_stride);
+  DecodeArgs a = base_args(Q, K_cache, V_cache, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.lens = seqlens_kv;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  a.seqlen_uniform = shift;
+  a.row_stride = num_heads_kv * head_dim_q;
+  a.head_stride = head_dim_q;
+  a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
+  return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0, kVarlenRowsHint);
 }
 
 extern "C" const char* fmha_decode_error_string(int code) {

@@ -50,22 +50,63 @@ constexpr int kMaxSeq = 16;
 // Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format,
 // no swizzle, no index stride).
 constexpr int kBufferWord3 = 0x00020000;
-// A byte offset beyond every num_records this kernel builds (all < 2^31):
-// loads there return 0 and stores are dropped, with no memory access.
-constexpr uint32_t kOffsetOutOfRange = 0x80000000u;
+// Byte offsets beyond every num_records this kernel builds (all < 2^30):
+// loads there return 0 and stores are dropped, with no memory access.  A lane
+// of an absent head adds kLaneOutOfRange, a row past the batch's length adds
+// kRowOutOfRange; the sum of both still fits 32 bits.
+constexpr uint32_t kLaneOutOfRange = 0x40000000u;
+constexpr uint32_t kRowOutOfRange = 0x80000000u;
+
+// Where a batch's K/V rows live.
+//   kLayoutPacked:  rows [cu[b], cu[b+1]) of a [rows, Hkv, D] tensor, or
+//                   rows [b*S, b*S+S) with uniform lengths (lens == null);
+//   kLayoutStrided: element (b, j, h, d) at b*batch_stride + j*row_stride +
+//                   h*head_stride + d (BSHD, BHSD, padded caches), lengths
+//                   from lens[b] or uniform;
+//   kLayoutPaged:   a [pages, page_size, Hkv, D] cache (page_size a power of
+//                   two); row j of batch b is slot j % page_size of page
+//                   block_table[b*bt_stride + j / page_size]; lengths from
+//                   lens[b].  seqlen_uniform holds log2(page_size) and
+//                   batch_stride the page stride.
+constexpr int kLayoutPacked = 0;
+constexpr int kLayoutStrided = 1;
+constexpr int kLayoutPaged = 2;
 
 struct DecodeArgs {
   const uint16_t* q;        // [batch, Hq, D] bf16 bits
-  const uint16_t* k;        // [rows, Hkv, D] bf16 bits
-  const uint16_t* v;        // [rows, Hkv, D] bf16 bits
+  const uint16_t* k;        // bf16 bits, layout above
+  const uint16_t* v;        // bf16 bits, same layout and strides as k
   uint16_t* o;              // [batch, Hq, D] fp16 bits
-  const int32_t* cu;        // [batch+1] row offsets, or null (uniform)
-  int32_t seqlen_uniform;   // rows per batch when cu == null
+  const int32_t* lens;      // packed: cu offsets [batch+1]; strided/paged: lengths [batch]; or null
+  const int32_t* block_table;  // paged only
+  int64_t batch_stride;     // elements (strided); page stride (paged)
+  int32_t row_stride;       // elements between rows
+  int32_t head_stride;      // elements between KV heads
+  int32_t bt_stride;        // paged: block_table entries per batch
+  int32_t max_rows;         // largest valid length (16, or page_size when smaller)
+  int32_t seqlen_uniform;   // rows per batch when lens == null; paged: log2(page_size)
   int32_t num_heads_q;
   int32_t num_heads_kv;
   int32_t units_per_batch;  // waves per batch: ceil(Hkv / HPW)
   uint32_t total_units;     // batch * units_per_batch
   float scale;
+};
+
+// One batch's K/V as the kernel reads it: byte strides relative to k/v, the
+// descriptor range, the length.
+struct KVSpan {
+  const uint16_t* k;
+  const uint16_t* v;
+  uint32_t records;
+  uint32_t row_bytes;
+  uint32_t head_bytes;
+  int S;
+  // kLayoutPaged: this batch's block-table row, log2(page_size), page stride
+  // in elements, bytes of one row (all heads).
+  const int32_t* pages;
+  uint32_t page_shift;
+  uint64_t page_stride;
+  uint32_t row_extent;
 };
 
 __device__ __forceinline__ constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
@@ -190,9 +231,9 @@ struct GroupReduce {
 // ---------------------------------------------------------------------------
 // One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX>
-__device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, int64_t row0, int S,
-                                            int hk, bool head_ok, int lane, uint16_t* lds_p) {
+template <int D, int G, int SMAX, int LAYOUT>
+__device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, const KVSpan& kv, int hk,
+                                            bool head_ok, int lane, uint16_t* lds_p) {
   constexpr int LPH = D / 8;                 // lanes per KV head
   constexpr int NS = ilog2(LPH);             // butterfly steps
   constexpr int V = G * SMAX;                // scores per KV head
@@ -205,31 +246,61 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, int
   const int r = lane % LPH;
   const int hkl = lane / LPH;
   const int hq_count = a.num_heads_q;
-  const int hkv_count = a.num_heads_kv;
 
+  const int S = kv.S;
   // ---- buffer resources and per-lane byte offsets ----
   const uint32_t q_bytes = (uint32_t)hq_count * D * 2;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq_count * D, q_bytes);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq_count * D, q_bytes);
-  const uint32_t row_bytes = (uint32_t)hkv_count * D * 2;
-  const uint32_t kv_bytes = (uint32_t)S * row_bytes;
-  const uint64_t kv_elem0 = (uint64_t)row0 * hkv_count * D;
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + kv_elem0, kv_bytes);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + kv_elem0, kv_bytes);
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kv.k, kv.records);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(kv.v, kv.records);
 
-  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kOffsetOutOfRange;
-  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kOffsetOutOfRange;
+  const uint32_t kv_off = head_ok ? (uint32_t)hk * kv.head_bytes + (uint32_t)r * 16u : kLaneOutOfRange;
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+  // Row j's byte offset.  Packed rows past S already fall outside the
+  // descriptor's range; a strided batch's range can include padding rows of
+  // other heads, so there rows at or past S are moved out of range.
+  uint32_t row_off[SMAX];
+  row_off[0] = 0;
+#pragma unroll
+  for (int j = 1; j < SMAX; ++j) row_off[j] = row_off[j - 1] + kv.row_bytes;
+  if constexpr (LAYOUT == kLayoutStrided) {
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) row_off[j] = j < S ? row_off[j] : kRowOutOfRange;
+  }
 
   // ---- issue every load of this unit ----
   u32x4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, qo_off + g * D * 2);
   u32x4 kr[SMAX];
-#pragma unroll
-  for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + j * row_bytes);
   u32x4 vr[SMAX];
+  if constexpr (LAYOUT != kLayoutPaged) {
 #pragma unroll
-  for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + j * row_bytes);
+    for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + row_off[j]);
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
+  } else {
+    // Row j sits in page pages[j >> page_shift] at slot j & (page_size-1):
+    // one descriptor per row, spanning that row's heads, empty past S (the
+    // block-table entry read for such a row is entry 0, which always exists).
+    uint64_t row_elem[SMAX];
+    uint32_t row_rec[SMAX];
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+      const int jj = j < S ? j : 0;
+      const uint32_t page = (uint32_t)kv.pages[jj >> kv.page_shift];
+      const uint32_t slot = (uint32_t)jj & ((1u << kv.page_shift) - 1u);
+      row_elem[j] = (uint64_t)page * kv.page_stride + (uint64_t)slot * (kv.row_bytes >> 1);
+      row_rec[j] = j < S ? kv.row_extent : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j)
+      kr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.k + row_elem[j], row_rec[j]), kv_off);
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j)
+      vr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.v + row_elem[j], row_rec[j]), kv_off);
+  }
   // Keep the scheduler from sinking loads into the arithmetic below: all
   // 1 + 2*SMAX requests of the unit are in flight before the first wait.
   __builtin_amdgcn_sched_barrier(0);
@@ -350,7 +421,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, int
   }
 }
 
-// Batches whose cu_seqlens span is outside [0, 16] get NaN outputs so that a
+// Batches whose length is outside [0, max_rows] get NaN outputs so that a
 // broken length table is visible in the result.
 template <int D, int G>
 __device__ __forceinline__ void decode_bad_length(const DecodeArgs& a, uint32_t b, int hk, bool head_ok, int lane) {
@@ -358,16 +429,60 @@ __device__ __forceinline__ void decode_bad_length(const DecodeArgs& a, uint32_t 
   const int r = lane % LPH;
   const uint32_t q_bytes = (uint32_t)a.num_heads_q * D * 2;
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * a.num_heads_q * D, q_bytes);
-  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kOffsetOutOfRange;
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
   for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, nan4);
 }
 
-// SB = 1, 2, 4, 8, 16: every batch has exactly seqlen_uniform <= SB rows
-// (uniform layout, no cu array).  SB = 0: lengths come from cu and each wave
-// picks the smallest bucket that holds its batch.
-template <int D, int G, int SB>
+// This batch's K/V span for the layout.  Returns false when the batch's
+// length is outside [0, max_rows] (the caller then writes NaN).
+template <int D, int LAYOUT, bool UNIFORM>
+__device__ __forceinline__ bool batch_span(const DecodeArgs& a, uint32_t b, KVSpan& kv) {
+  int S;
+  uint64_t elem0;
+  if constexpr (LAYOUT == kLayoutPacked) {
+    int64_t row0;
+    if constexpr (UNIFORM) {
+      S = a.seqlen_uniform;
+      row0 = (int64_t)b * S;
+    } else {
+      row0 = a.lens[b];
+      S = a.lens[b + 1] - (int)row0;
+    }
+    elem0 = (uint64_t)row0 * (uint64_t)a.row_stride;
+  } else if constexpr (LAYOUT == kLayoutStrided) {
+    S = UNIFORM ? a.seqlen_uniform : a.lens[b];
+    elem0 = (uint64_t)b * (uint64_t)a.batch_stride;
+  } else {
+    S = a.lens[b];
+    elem0 = 0;
+    kv.pages = a.block_table + (uint64_t)b * a.bt_stride;
+    kv.page_shift = (uint32_t)a.seqlen_uniform;  // log2(page_size) for this layout
+    kv.page_stride = (uint64_t)a.batch_stride;
+    kv.row_extent = ((uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+  }
+  if (S < 0 || S > a.max_rows) return false;
+  kv.k = a.k + elem0;
+  kv.v = a.v + elem0;
+  kv.S = S;
+  kv.row_bytes = (uint32_t)a.row_stride * 2u;
+  kv.head_bytes = (uint32_t)a.head_stride * 2u;
+  // Range of the descriptor: up to the last valid row's last head.
+  if constexpr (LAYOUT == kLayoutStrided) {
+    kv.records = S == 0 ? 0u
+                        : ((uint32_t)(S - 1) * (uint32_t)a.row_stride +
+                           (uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+  } else {
+    kv.records = (uint32_t)S * kv.row_bytes;  // rows are [Hkv, D] and contiguous
+  }
+  return true;
+}
+
+// SB = 1, 2, 4, 8, 16: every batch has exactly seqlen_uniform <= SB rows.
+// SB = 0: lengths come from a.lens and each wave picks the smallest bucket
+// that holds its batch.
+template <int D, int G, int LAYOUT, int SB>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
@@ -385,25 +500,27 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
   const bool head_ok = hk < a.num_heads_kv;
   uint16_t* lds_wave = lds_p + wave * HPW * VP;
 
+  KVSpan kv;
+  const bool length_ok = batch_span<D, LAYOUT, SB != 0>(a, b, kv);
+  // A uniform length was validated on the host; only table lengths can be bad.
+  if (SB == 0 && !length_ok) {
+    decode_bad_length<D, G>(a, b, hk, head_ok, lane);
+    return;
+  }
   if constexpr (SB != 0) {
-    const int S = a.seqlen_uniform;
-    decode_unit<D, G, SB>(a, b, (int64_t)b * S, S, hk, head_ok, lane, lds_wave);
+    decode_unit<D, G, SB, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
   } else {
-    const int c0 = a.cu[b];
-    const int c1 = a.cu[b + 1];
-    const int S = c1 - c0;
-    if (S < 0 || S > kMaxSeq) {
-      decode_bad_length<D, G>(a, b, hk, head_ok, lane);
-    } else if (S <= 1) {
-      decode_unit<D, G, 1>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+    const int S = kv.S;
+    if (S <= 1) {
+      decode_unit<D, G, 1, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 2) {
-      decode_unit<D, G, 2>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 2, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 4) {
-      decode_unit<D, G, 4>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 4, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 8) {
-      decode_unit<D, G, 8>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 8, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else {
-      decode_unit<D, G, 16>(a, b, c0, S, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 16, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
     }
   }
 }

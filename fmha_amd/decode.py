@@ -9,7 +9,8 @@ Two levels, both thin wrappers over the C ABI in include/fmha_decode.h:
   failing silently.
 * fmha_decode -- tensor level, for torch device tensors: checks shapes,
   dtypes and devices, allocates O if not given, launches on torch's current
-  stream.
+  stream.  fmha_decode_strided and fmha_decode_paged do the same for strided
+  (BSHD / BHSD / padded) and paged KV caches.
 """
 import math
 
@@ -54,6 +55,108 @@ def launch_fmha_decode_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q
                                              num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                                              float(softmax_scale))
     _raise_if(rc)
+
+
+def launch_fmha_decode_strided(stream, Q, K, V, O, seqlens_kv, seqlen_kv, kv_batch_stride, kv_row_stride,
+                               kv_head_stride, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                               head_dim_kv, softmax_scale):
+    """Decode attention over strided K/V (strides in elements); seqlens_kv is
+    a device pointer to int32 lengths or 0 for a uniform length."""
+    rc = _lib.load().fmha_decode_fwd_strided(stream, Q, K, V, O, seqlens_kv, seqlen_kv, kv_batch_stride,
+                                             kv_row_stride, kv_head_stride, batch, num_heads_q, num_heads_kv,
+                                             seqlen_q, head_dim_q, head_dim_kv, float(softmax_scale))
+    _raise_if(rc)
+
+
+def launch_fmha_decode_paged(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv,
+                             page_size, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                             softmax_scale):
+    """Decode attention over a paged [pages, page_size, Hkv, D] cache."""
+    rc = _lib.load().fmha_decode_fwd_paged(stream, Q, K_cache, V_cache, O, block_table, block_table_stride,
+                                           seqlens_kv, page_size, batch, num_heads_q, num_heads_kv, seqlen_q,
+                                           head_dim_q, head_dim_kv, float(softmax_scale))
+    _raise_if(rc)
+
+
+def _q_shape(q):
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise ValueError("q must have seqlen_q == 1")
+        return q.shape[0], q.shape[1], q.shape[3]
+    if q.dim() == 3:
+        return tuple(q.shape)
+    raise ValueError("q must be [B, Hq, 1, D] or [B, Hq, D]")
+
+
+def _check_q_out(q, out):
+    import torch
+    if q.dtype != torch.bfloat16 or not q.is_cuda or not q.is_contiguous():
+        raise ValueError("q must be a contiguous bfloat16 GPU tensor")
+    if out is None:
+        return torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    if out.dtype != torch.float16 or out.shape != q.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float16 tensor shaped like q")
+    return out
+
+
+def _check_lengths(t, B, device):
+    import torch
+    if t is None:
+        return 0
+    if t.dtype != torch.int32 or t.numel() != B or t.device != device or not t.is_contiguous():
+        raise ValueError("seqlens_kv must be a contiguous int32 tensor [batch] on q's device")
+    return t.data_ptr()
+
+
+def fmha_decode_strided(q, k, v, seqlens_kv=None, softmax_scale=None, out=None):
+    """Decode attention for K/V given as any [B, S, Hkv, D] view with unit
+    innermost stride: a contiguous padded BSHD cache, or a BHSD cache passed
+    as k.transpose(1, 2).  seqlens_kv (int32 [B]) gives each batch's length
+    (rows past it are never read); without it every batch uses all S rows."""
+    import torch
+    B, Hq, D = _q_shape(q)
+    out = _check_q_out(q, out)
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or t.shape[0] != B or t.shape[3] != D:
+            raise ValueError(f"{name} must be a bfloat16 GPU tensor [B, S, Hkv, D]")
+        if t.stride(3) != 1:
+            raise ValueError(f"{name} must have unit stride in the head dimension")
+    if k.shape != v.shape or k.stride() != v.stride():
+        raise ValueError("k and v must have the same shape and strides")
+    S, Hkv = k.shape[1], k.shape[2]
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    lens = _check_lengths(seqlens_kv, B, q.device)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    launch_fmha_decode_strided(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lens, S,
+                               k.stride(0), k.stride(1), k.stride(2), B, Hq, Hkv, 1, D, D, softmax_scale)
+    return out
+
+
+def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scale=None, out=None):
+    """Decode attention over a paged cache: k_cache/v_cache [pages, page_size,
+    Hkv, D] bfloat16, block_table int32 [B, max_pages], seqlens_kv int32 [B]."""
+    import torch
+    B, Hq, D = _q_shape(q)
+    out = _check_q_out(q, out)
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or not t.is_contiguous() or t.shape[3] != D:
+            raise ValueError(f"{name} must be a contiguous bfloat16 GPU tensor [pages, page_size, Hkv, D]")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must have the same shape")
+    if (block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B
+            or block_table.stride(1) != 1 or block_table.device != q.device):
+        raise ValueError("block_table must be int32 [B, max_pages] with unit column stride on q's device")
+    lens = _check_lengths(seqlens_kv, B, q.device)
+    if lens == 0:
+        raise ValueError("seqlens_kv is required for a paged cache")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    launch_fmha_decode_paged(stream, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                             block_table.data_ptr(), block_table.stride(0), lens, k_cache.shape[1], B, Hq,
+                             k_cache.shape[2], 1, D, D, softmax_scale)
+    return out
 
 
 def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None, out=None):

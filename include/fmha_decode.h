@@ -95,6 +95,52 @@ int fmha_decode_fwd_uniform(void* stream,
                             int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                             float softmax_scale);
 
+/*
+ * Decode attention over K/V addressed by strides, for caches that are not
+ * packed: element d of head h, row j of batch b is at
+ *     K + b*kv_batch_stride + j*kv_row_stride + h*kv_head_stride + d
+ * (strides in elements, >= 0, multiples of 8; V uses the same strides).
+ * [B, Hkv, S, D] (BHSD, the layout the reference README documents,
+ * README.md:166-168) is (Hkv*S*D, D, S*D); a padded [B, S, Hkv, D] cache is
+ * (S*Hkv*D, Hkv*D, D).
+ *
+ *   seqlens_kv   device int32 [batch] lengths, or NULL for a uniform length
+ *   seqlen_kv    uniform length (in [0, 16]) when seqlens_kv is NULL; else
+ *                the rows each batch has room for: a length above
+ *                min(seqlen_kv, 16) gets NaN outputs, rows past a batch's
+ *                length are never read (padding may hold anything)
+ * One batch's span (rows and heads) must stay below 1 GiB.  Other arguments
+ * as fmha_decode_fwd.
+ */
+int fmha_decode_fwd_strided(void* stream,
+                            const void* Q, const void* K, const void* V, void* O,
+                            const int32_t* seqlens_kv, int32_t seqlen_kv,
+                            int64_t kv_batch_stride, int64_t kv_row_stride, int64_t kv_head_stride,
+                            int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                            int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                            float softmax_scale);
+
+/*
+ * Decode attention over a paged KV cache [num_pages, page_size, Hkv, D]
+ * (K_cache and V_cache alike).  Row j of batch b is slot j % page_size of page
+ * block_table[b * block_table_stride + j / page_size].
+ *
+ *   block_table         device int32, ceil(len/page_size) valid entries per
+ *                       batch row (the row itself is block_table_stride long)
+ *   seqlens_kv          device int32 [batch] lengths in [0, 16]; a length
+ *                       outside that range gets NaN outputs
+ *   page_size           a power of two in [1, 2^20]
+ * Other arguments as fmha_decode_fwd.  The reference has no paged layout;
+ * this entry point is the KV-cache format of serving engines.
+ */
+int fmha_decode_fwd_paged(void* stream,
+                          const void* Q, const void* K_cache, const void* V_cache, void* O,
+                          const int32_t* block_table, int32_t block_table_stride,
+                          const int32_t* seqlens_kv, int32_t page_size,
+                          int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                          int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                          float softmax_scale);
+
 /* Human-readable text for a code returned above (never NULL). */
 const char* fmha_decode_error_string(int code);
 

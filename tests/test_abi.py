@@ -32,7 +32,8 @@ def lib():
 
 def test_exports_every_declared_function(lib):
     names = header_functions()
-    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_uniform", "fmha_decode_error_string",
+    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_uniform", "fmha_decode_fwd_strided",
+                          "fmha_decode_fwd_paged", "fmha_decode_error_string",
                           "fmha_decode_last_error_detail", "fmha_decode_version"}
     from fmha_amd import _lib
     assert set(names) == set(_lib.EXPORTED)
@@ -102,10 +103,63 @@ def test_uniform_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
+def strided(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, lens=CU, s=16, bs=16 * 16 * 128, rs=16 * 128, hs=128, batch=4,
+             hq=16, hkv=16, sq=1, dq=128, dkv=128, scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_strided(a["stream"], a["q"], a["k"], a["v"], a["o"], a["lens"], a["s"], a["bs"],
+                                       a["rs"], a["hs"], a["batch"], a["hq"], a["hkv"], a["sq"], a["dq"],
+                                       a["dkv"], a["scale"])
+
+
+def paged(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, bt=CU, bts=4, lens=CU + 64, ps=16, batch=4, hq=16, hkv=16, sq=1,
+             dq=128, dkv=128, scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_paged(a["stream"], a["q"], a["k"], a["v"], a["o"], a["bt"], a["bts"], a["lens"],
+                                     a["ps"], a["batch"], a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"],
+                                     a["scale"])
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(s=-1), BAD, "seqlen_kv"),
+    (dict(lens=None, s=17), BAD, "seqlen_kv"),
+    (dict(bs=-8), BAD, "strides"),
+    (dict(rs=12), BAD, "multiples of 8"),
+    (dict(hs=4), BAD, "multiples of 8"),
+    (dict(rs=1 << 26), BAD, "1 GiB"),
+    (dict(lens=CU + 2), BAD, "seqlens_kv"),
+    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    (dict(k=None), BAD, "non-null"),
+    (dict(dq=128, dkv=64), BAD, "head_dim_q"),
+])
+def test_strided_rejects(lib, kw, code, needle):
+    assert strided(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(ps=0), BAD, "page_size"),
+    (dict(ps=24), BAD, "page_size"),
+    (dict(ps=1 << 21), BAD, "page_size"),
+    (dict(bt=None), BAD, "block_table"),
+    (dict(lens=None), BAD, "seqlens_kv"),
+    (dict(bt=CU + 2), BAD, "aligned"),
+    (dict(bts=0), BAD, "block_table_stride"),
+    (dict(sq=2), BAD, "seqlen_q"),
+    (dict(v=None), BAD, "non-null"),
+])
+def test_paged_rejects(lib, kw, code, needle):
+    assert paged(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
 def test_batch_zero_is_a_noop(lib):
     # Nothing is launched and no pointer is needed for an empty batch.
     assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
+    assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
+    assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0
     assert lib.fmha_decode_last_error_detail() == b""
 
 

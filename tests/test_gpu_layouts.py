@@ -1,0 +1,147 @@
+"""GPU parity for the strided (BSHD, BHSD, padded) and paged KV layouts
+(fmha_decode_fwd_strided / fmha_decode_fwd_paged): each case gathers the
+rows a batch owns into the packed layout and checks the kernel against the
+oracle there, with every row the kernel must not read poisoned with NaN."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.common import assert_pass, cu_from_seqlens, default_scale
+
+pytestmark = pytest.mark.gpu
+
+NAN = np.uint16(0x7FC0)
+
+
+def _bf16(gen, shape, device):
+    import torch
+    return torch.randn(*shape, generator=gen, device=device, dtype=torch.bfloat16)
+
+
+def _bits(t):
+    import torch
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _check(o, q, packed_k, packed_v, seqlens, Hq, Hkv, D, ctx):
+    r, slack = oracle.decode(_bits(q).reshape(len(seqlens), Hq, D), packed_k, packed_v,
+                             cu_from_seqlens(seqlens), Hq, Hkv, D, default_scale(D), with_slack=True)
+    assert_pass(oracle.compare(_bits(o).reshape(r.shape), r, slack), ctx)
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("cap", [5, 16, 24])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 16), (256, 8, 4), (64, 16, 2)])
+def test_strided_varlen(layout, cap, D, Hq, Hkv):
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(cap * 1000 + D + Hq)
+    B = 37
+    rng = np.random.default_rng(cap + D)
+    seqlens = rng.integers(0, min(cap, 16) + 1, size=B).astype(np.int32)
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    if layout == "bhsd":
+        kc = _bf16(gen, (B, Hkv, cap, D), dev)
+        vc = _bf16(gen, (B, Hkv, cap, D), dev)
+        for b in range(B):                      # poison the padding rows
+            kc[b, :, seqlens[b]:] = float("nan")
+            vc[b, :, seqlens[b]:] = float("nan")
+        k, v = kc.transpose(1, 2), vc.transpose(1, 2)
+    else:
+        k = _bf16(gen, (B, cap, Hkv, D), dev)
+        v = _bf16(gen, (B, cap, Hkv, D), dev)
+        for b in range(B):
+            k[b, seqlens[b]:] = float("nan")
+            v[b, seqlens[b]:] = float("nan")
+    lens = torch.from_numpy(seqlens).to(dev)
+    o = fmha_amd.fmha_decode_strided(q, k, v, seqlens_kv=lens)
+    torch.cuda.synchronize()
+    pk = np.concatenate([_bits(k[b, :seqlens[b]]) for b in range(B)])
+    pv = np.concatenate([_bits(v[b, :seqlens[b]]) for b in range(B)])
+    _check(o, q, pk, pv, seqlens, Hq, Hkv, D, f"{layout} cap={cap} D={D}")
+
+
+@pytest.mark.parametrize("S", [1, 6, 16])
+def test_strided_uniform_bhsd(S):
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(S)
+    B, Hq, Hkv, D = 29, 32, 16, 128
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    kc = _bf16(gen, (B, Hkv, S, D), dev)
+    vc = _bf16(gen, (B, Hkv, S, D), dev)
+    o = fmha_amd.fmha_decode_strided(q, kc.transpose(1, 2), vc.transpose(1, 2))
+    torch.cuda.synchronize()
+    seqlens = np.full(B, S, np.int32)
+    _check(o, q, _bits(kc.transpose(1, 2)).reshape(-1, Hkv, D), _bits(vc.transpose(1, 2)).reshape(-1, Hkv, D),
+           seqlens, Hq, Hkv, D, f"bhsd uniform S={S}")
+
+
+def test_strided_length_beyond_capacity_is_nan():
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    B, H, D, cap = 3, 4, 128, 6
+    q = _bf16(gen, (B, H, 1, D), dev)
+    k = _bf16(gen, (B, cap, H, D), dev)
+    v = _bf16(gen, (B, cap, H, D), dev)
+    lens = torch.tensor([6, 7, 2], dtype=torch.int32, device=dev)
+    o = fmha_amd.fmha_decode_strided(q, k, v, seqlens_kv=lens).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o[1]).all() and torch.isfinite(o[0]).all() and torch.isfinite(o[2]).all()
+
+
+@pytest.mark.parametrize("page_size", [1, 2, 4, 8, 16, 32])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 16), (256, 16, 8), (64, 8, 1)])
+def test_paged(page_size, D, Hq, Hkv):
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(page_size * 100 + D)
+    B = 41
+    rng = np.random.default_rng(page_size + D)
+    seqlens = rng.integers(0, 17, size=B).astype(np.int32)
+    need = [(int(s) + page_size - 1) // page_size for s in seqlens]
+    max_pages = max(max(need), 1) + 1
+    num_pages = sum(need) + 7
+    perm = rng.permutation(num_pages)
+    bt = np.full((B, max_pages), -1, np.int32)   # unused entries hold garbage
+    used, i = [], 0
+    for b in range(B):
+        for p in range(need[b]):
+            bt[b, p] = perm[i]
+            used.append(perm[i])
+            i += 1
+    kc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    rows_k, rows_v = [], []
+    for b in range(B):
+        for j in range(seqlens[b]):
+            page, slot = bt[b, j // page_size], j % page_size
+            kr, vr = _bf16(gen, (Hkv, D), dev), _bf16(gen, (Hkv, D), dev)
+            kc[page, slot], vc[page, slot] = kr, vr
+            rows_k.append(_bits(kr))
+            rows_v.append(_bits(vr))
+    o = fmha_amd.fmha_decode_paged(q, kc, vc, torch.from_numpy(bt).to(dev), torch.from_numpy(seqlens).to(dev))
+    torch.cuda.synchronize()
+    pk = np.stack(rows_k) if rows_k else np.zeros((0, Hkv, D), np.uint16)
+    pv = np.stack(rows_v) if rows_v else np.zeros((0, Hkv, D), np.uint16)
+    _check(o, q, pk, pv, seqlens, Hq, Hkv, D, f"paged ps={page_size} D={D}")
+
+
+def test_paged_bad_length_is_nan():
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    q = _bf16(gen, (2, 4, 1, 64), dev)
+    kc = _bf16(gen, (4, 16, 4, 64), dev)
+    bt = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32, device=dev)
+    lens = torch.tensor([17, 3], dtype=torch.int32, device=dev)
+    o = fmha_amd.fmha_decode_paged(q, kc, kc, bt, lens).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o[0]).all() and torch.isfinite(o[1]).all()
