@@ -15,6 +15,8 @@ EXPORTED = (
     "fmha_decode_fwd_uniform",
     "fmha_decode_fwd_strided",
     "fmha_decode_fwd_paged",
+    "fmha_decode_splitkv_workspace_size",
+    "fmha_decode_fwd_splitkv",
     "fmha_decode_error_string",
     "fmha_decode_last_error_detail",
     "fmha_decode_version",
@@ -43,6 +45,11 @@ def load():
                                             i32, f32]
     lib.fmha_decode_fwd_paged.restype = ctypes.c_int
     lib.fmha_decode_fwd_paged.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, i32, f32]
+    sz = ctypes.c_size_t
+    lib.fmha_decode_splitkv_workspace_size.restype = sz
+    lib.fmha_decode_splitkv_workspace_size.argtypes = [i32, i32, i32, i32, i32]
+    lib.fmha_decode_fwd_splitkv.restype = ctypes.c_int
+    lib.fmha_decode_fwd_splitkv.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32, vp, sz]
     lib.fmha_decode_error_string.restype = ctypes.c_char_p
     lib.fmha_decode_error_string.argtypes = [ctypes.c_int]
     lib.fmha_decode_last_error_detail.restype = ctypes.c_char_p

@@ -15,10 +15,12 @@
 
 #include "fmha_decode.h"
 #include "fmha_decode_kernel.hpp"
+#include "fmha_decode_splitkv.hpp"
 
 namespace {
 
 using fmha_decode::DecodeArgs;
+using fmha_decode::SplitArgs;
 using fmha_decode::kBlockThreads;
 using fmha_decode::kWaveSize;
 using fmha_decode::kWavesPerBlock;
@@ -203,6 +205,106 @@ DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32
 // reference's own varlen workload averages 4.3 rows; 8 covers it.
 constexpr int kVarlenRowsHint = 8;
 
+// ---------------------------------------------------------------------------
+// Split-KV (lengths beyond 16)
+// ---------------------------------------------------------------------------
+constexpr size_t kWorkspaceAlign = 256;
+
+size_t align_up(size_t x) { return (x + kWorkspaceAlign - 1) / kWorkspaceAlign * kWorkspaceAlign; }
+
+struct SplitPlan {
+  int chunk_rows = 16;
+  int nchunks = 1;
+  int64_t units = 0;
+  size_t off_t = 0, off_m = 0, off_l = 0, off_ml = 0, off_opart = 0, total = 0;
+};
+
+// Chunks of C rows (C in {64, 128, 256}, or the rows' own multiple of 16
+// when shorter): small enough that batch * head groups * chunks fills the
+// GPU with 4096 waves where the work allows, large enough that the partial
+// outputs (4*D bytes per chunk and query head) stay a few percent of K/V.
+SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
+  SplitPlan p;
+  const int heads_per_wave = kWaveSize / (d / 8);
+  const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
+  p.units = upb * batch;
+  int c = 256;
+  while (c > 64 && p.units * ((max_rows + c - 1) / c) < 4096) c /= 2;
+  const int fit = max_rows <= 16 ? 16 : (max_rows + 15) / 16 * 16;  // no longer than the rows need
+  if (c > fit) c = fit;
+  p.chunk_rows = c;
+  p.nchunks = max_rows <= 0 ? 1 : (max_rows + c - 1) / c;
+  const size_t heads = (size_t)batch * hq;
+  size_t off = 0;
+  p.off_t = off;
+  off += align_up(heads * (size_t)p.nchunks * c * 4);
+  p.off_m = off;
+  off += align_up(heads * (size_t)p.nchunks * 4);
+  p.off_l = off;
+  off += align_up(heads * (size_t)p.nchunks * 4);
+  p.off_ml = off;
+  off += align_up(heads * 2 * 4);
+  p.off_opart = off;
+  if (p.nchunks > 1) off += align_up(heads * (size_t)p.nchunks * d * 4);
+  p.total = off;
+  return p;
+}
+
+template <int D, int G>
+hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
+  const uint32_t waves = a.total_units * (uint32_t)a.nchunks;
+  // 16 rows of K (or V) per wave in flight: 8 waves reach ~128 KiB per CU.
+  const int w = kInflightBytesPerCU / (16 * 1024);
+  {
+    const auto kernel = fmha_decode::splitkv_scores_kernel<D, G>;
+    hipFuncAttributes attr;
+    size_t st = 0;
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess) st = attr.sharedSizeBytes;
+    hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_for(w, lds_per_cu(), st), stream, a);
+  }
+  const uint64_t heads = (uint64_t)a.batch * a.num_heads_q;
+  // Many chunks per row: a wave (stats) or a block (combine) per head.
+  const bool wide = a.nchunks > 16;
+  if (wide)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_wave_kernel, dim3((unsigned)heads), dim3(64), 0, stream, a);
+  else
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel, dim3((unsigned)((heads + 255) / 256)), dim3(256), 0,
+                       stream, a);
+  const bool direct = a.nchunks == 1;
+  {
+    const void* kp = direct ? reinterpret_cast<const void*>(fmha_decode::splitkv_pv_kernel<D, G, true>)
+                            : reinterpret_cast<const void*>(fmha_decode::splitkv_pv_kernel<D, G, false>);
+    hipFuncAttributes attr;
+    size_t st = 0;
+    if (hipFuncGetAttributes(&attr, kp) == hipSuccess) st = attr.sharedSizeBytes;
+    const size_t dyn = lds_reserve_for(w, lds_per_cu(), st);
+    if (direct)
+      hipLaunchKernelGGL((fmha_decode::splitkv_pv_kernel<D, G, true>), dim3(waves), dim3(kBlockThreads), dyn, stream,
+                         a);
+    else
+      hipLaunchKernelGGL((fmha_decode::splitkv_pv_kernel<D, G, false>), dim3(waves), dim3(kBlockThreads), dyn,
+                         stream, a);
+  }
+  if (!direct && wide) {
+    hipLaunchKernelGGL(fmha_decode::splitkv_combine_block_kernel<D>, dim3((unsigned)heads), dim3(256), 0, stream, a);
+  } else if (!direct) {
+    const uint64_t lanes = heads * (D / 8);
+    hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                       stream, a);
+  }
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream) {
+  switch (g) {
+    case 1: return launch_split_dg<D, 1>(a, stream);
+    case 2: return launch_split_dg<D, 2>(a, stream);
+    case 4: return launch_split_dg<D, 4>(a, stream);
+    default: return launch_split_dg<D, 8>(a, stream);
+  }
+}
+
 }  // namespace
 
 extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -308,6 +410,74 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
   a.head_stride = head_dim_q;
   a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
   return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0, kVarlenRowsHint);
+}
+
+extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                                     int32_t max_seqlen_kv, int32_t head_dim) {
+  if (batch <= 0 || num_heads_q <= 0 || num_heads_kv <= 0 || max_seqlen_kv < 0 ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return 0;
+  return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
+}
+
+extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
+                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
+                                       void* workspace, size_t workspace_bytes) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
+  if (max_seqlen_kv < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv must be >= 0");
+  const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim_q);
+  // Row offsets of one batch (rows up to nchunks * C) must stay below 2^30 bytes.
+  const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
+  if ((int64_t)plan.nchunks * plan.chunk_rows * row_bytes >= (int64_t(1) << 30))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv too large for this head count (%d)", max_seqlen_kv);
+  if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
+  if ((reinterpret_cast<uintptr_t>(workspace) & (kWorkspaceAlign - 1)) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be 256-byte aligned");
+  if (workspace_bytes < plan.total)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
+                  plan.total);
+  if (plan.units * plan.nchunks > (int64_t)INT32_MAX || (int64_t)batch * num_heads_q > (int64_t)INT32_MAX)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch * heads * chunks too large");
+  char* ws = static_cast<char*>(workspace);
+  SplitArgs a = {};
+  a.q = static_cast<const uint16_t*>(Q);
+  a.k = static_cast<const uint16_t*>(K);
+  a.v = static_cast<const uint16_t*>(V);
+  a.o = static_cast<uint16_t*>(O);
+  a.cu = cu_seqlens_kv;
+  a.t = reinterpret_cast<float*>(ws + plan.off_t);
+  a.m = reinterpret_cast<float*>(ws + plan.off_m);
+  a.l = reinterpret_cast<float*>(ws + plan.off_l);
+  a.ml = reinterpret_cast<float*>(ws + plan.off_ml);
+  a.opart = reinterpret_cast<float*>(ws + plan.off_opart);
+  a.num_heads_q = num_heads_q;
+  a.num_heads_kv = num_heads_kv;
+  a.units_per_batch = (int32_t)(plan.units / batch);
+  a.nchunks = plan.nchunks;
+  a.chunk_rows = plan.chunk_rows;
+  a.max_rows = max_seqlen_kv;
+  a.t_stride = plan.nchunks * plan.chunk_rows;
+  a.batch = batch;
+  a.total_units = (uint32_t)plan.units;
+  a.scale = softmax_scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int g = num_heads_q / num_heads_kv;
+  hipError_t err;
+  switch (head_dim_q) {
+    case 64: err = launch_split_d<64>(a, g, s); break;
+    case 128: err = launch_split_d<128>(a, g, s); break;
+    default: err = launch_split_d<256>(a, g, s); break;
+  }
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return FMHA_DECODE_SUCCESS;
 }
 
 extern "C" const char* fmha_decode_error_string(int code) {

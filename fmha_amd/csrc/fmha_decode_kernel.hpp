@@ -228,6 +228,65 @@ struct GroupReduce {
   }
 };
 
+// Partial dot products of this lane's 8 dims: x[g*NR + j] = q_g . k_j.
+template <int G, int NR>
+__device__ __forceinline__ void partial_scores(const u32x4 (&qv)[G], const u32x4 (&kr)[NR], float* x) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t qw = qv[g][i];
+        const uint32_t kw = kr[j][i];
+        acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw), as_bf16x2(kw), acc, false);
+      }
+      x[g * NR + j] = acc;
+    }
+  }
+}
+
+// acc[g][d] += sum_j P_g,j * V_j[d] over NR rows, rows taken in pairs:
+// pp[g][jp] holds the bf16 weights of rows 2jp (low half) and 2jp+1.
+template <int G, int NR>
+__device__ __forceinline__ void accumulate_pv(const u32x4 (&vr)[NR], const uint32_t (&pp)[G][(NR + 1) / 2],
+                                              float (&acc)[G][8]) {
+  constexpr int NP = (NR + 1) / 2;
+#pragma unroll
+  for (int jp = 0; jp < NP; ++jp) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v0 = vr[2 * jp][i];
+      const uint32_t v1 = (2 * jp + 1 < NR) ? (uint32_t)vr[(2 * jp + 1 < NR) ? 2 * jp + 1 : 0][i] : 0u;
+      lo[i] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // (V_j[2i],   V_j+1[2i])
+      hi[i] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);  // (V_j[2i+1], V_j+1[2i+1])
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const bf16x2 pw = as_bf16x2(pp[g][jp]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[g][2 * i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(lo[i]), pw, acc[g][2 * i], false);
+        acc[g][2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(hi[i]), pw, acc[g][2 * i + 1], false);
+      }
+    }
+  }
+}
+
+// Eight fp32 values -> eight fp16 (round to nearest even), packed.
+__device__ __forceinline__ u32x4 pack_f16x8(const float (&a)[8]) {
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)a[2 * i]);
+    const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)a[2 * i + 1]);
+    out[i] = h0 | (h1 << 16);
+  }
+  return out;
+}
+
 // ---------------------------------------------------------------------------
 // One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
 // ---------------------------------------------------------------------------
@@ -307,20 +366,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
 
   // ---- partial scores over this lane's 8 dims ----
   float x[V];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int j = 0; j < SMAX; ++j) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t qw = qv[g][i];
-        const uint32_t kw = kr[j][i];
-        acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw), as_bf16x2(kw), acc, false);
-      }
-      x[g * SMAX + j] = acc;
-    }
-  }
+  partial_scores<G, SMAX>(qv, kr, x);
 
   // ---- reduce over the head's lanes; lane keeps scores [blk*W, blk*W + W) ----
   TransposeReduce<LPH, V, 0>::run(x, lane);
@@ -385,40 +431,11 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-
-#pragma unroll
-  for (int jp = 0; jp < NP; ++jp) {
-    uint32_t lo[4], hi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v0 = vr[2 * jp][i];
-      const uint32_t v1 = (2 * jp + 1 < SMAX) ? (uint32_t)vr[(2 * jp + 1 < SMAX) ? 2 * jp + 1 : 0][i] : 0u;
-      lo[i] = __builtin_amdgcn_perm(v1, v0, 0x05040100u);  // (V_j[2i],   V_j+1[2i])
-      hi[i] = __builtin_amdgcn_perm(v1, v0, 0x07060302u);  // (V_j[2i+1], V_j+1[2i+1])
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const bf16x2 pw = as_bf16x2(pp[g][jp]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[g][2 * i] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(lo[i]), pw, acc[g][2 * i], false);
-        acc[g][2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(hi[i]), pw, acc[g][2 * i + 1], false);
-      }
-    }
-  }
+  accumulate_pv<G, SMAX>(vr, pp, acc);
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    u32x4 out;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)acc[g][2 * i]);
-      const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)acc[g][2 * i + 1]);
-      out[i] = h0 | (h1 << 16);
-    }
-    buffer_store16(o_rsrc, qo_off + g * D * 2, out);
-  }
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, pack_f16x8(acc[g]));
 }
 
 // Batches whose length is outside [0, max_rows] get NaN outputs so that a

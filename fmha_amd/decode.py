@@ -78,6 +78,55 @@ def launch_fmha_decode_paged(stream, Q, K_cache, V_cache, O, block_table, block_
     _raise_if(rc)
 
 
+def splitkv_workspace_size(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim):
+    """Bytes of device workspace fmha_decode_fwd_splitkv needs (0 if the
+    arguments are invalid)."""
+    return int(_lib.load().fmha_decode_splitkv_workspace_size(batch, num_heads_q, num_heads_kv, max_seqlen_kv,
+                                                              head_dim))
+
+
+def launch_fmha_decode_splitkv(stream, Q, K, V, O, cu_seqlens_kv, max_seqlen_kv, batch, num_heads_q,
+                               num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale, workspace,
+                               workspace_bytes):
+    """Decode attention for lengths up to max_seqlen_kv (any size) over the
+    packed layout, using a caller-provided device workspace."""
+    rc = _lib.load().fmha_decode_fwd_splitkv(stream, Q, K, V, O, cu_seqlens_kv, max_seqlen_kv, batch,
+                                             num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                             float(softmax_scale), workspace, workspace_bytes)
+    _raise_if(rc)
+
+
+def fmha_decode_splitkv(q, k, v, cu_seqlens_kv, max_seqlen_kv, softmax_scale=None, out=None, workspace=None):
+    """Decode attention with lengths beyond 16: q [B, Hq, 1, D] or [B, Hq, D],
+    k/v packed [rows, Hkv, D] bfloat16, cu_seqlens_kv int32 [B+1], every
+    length <= max_seqlen_kv.  workspace: a uint8 device tensor of at least
+    splitkv_workspace_size(...) bytes (allocated here when None)."""
+    import torch
+    B, Hq, D = _q_shape(q)
+    out = _check_q_out(q, out)
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 3 or not t.is_contiguous() or t.shape[2] != D:
+            raise ValueError(f"{name} must be a contiguous bfloat16 GPU tensor [rows, Hkv, D]")
+    if k.shape != v.shape:
+        raise ValueError("k and v must have the same shape")
+    if (cu_seqlens_kv.dtype != torch.int32 or cu_seqlens_kv.numel() != B + 1
+            or cu_seqlens_kv.device != q.device or not cu_seqlens_kv.is_contiguous()):
+        raise ValueError("cu_seqlens_kv must be a contiguous int32 tensor [batch+1] on q's device")
+    Hkv = k.shape[1]
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    need = splitkv_workspace_size(B, Hq, Hkv, int(max_seqlen_kv), D)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if workspace.dtype != torch.uint8 or workspace.device != q.device or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor on q's device")
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    launch_fmha_decode_splitkv(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                               cu_seqlens_kv.data_ptr(), int(max_seqlen_kv), B, Hq, Hkv, 1, D, D, softmax_scale,
+                               workspace.data_ptr(), workspace.numel())
+    return out
+
+
 def _q_shape(q):
     if q.dim() == 4:
         if q.shape[2] != 1:

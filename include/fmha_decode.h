@@ -29,6 +29,7 @@
 #ifndef FMHA_DECODE_H_
 #define FMHA_DECODE_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -140,6 +141,29 @@ int fmha_decode_fwd_paged(void* stream,
                           int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                           int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                           float softmax_scale);
+
+/*
+ * Decode attention for KV lengths beyond 16 (split-KV): the packed layout and
+ * cu_seqlens_kv of fmha_decode_fwd, lengths in [0, max_seqlen_kv] (a length
+ * outside that range gets NaN outputs).  The weights are still rounded to
+ * bf16 after normalisation by the global max and sum, as in the reference's
+ * CPU loop (fmha_host.cpp:209-226) extended past its 16-row arrays; the
+ * reference itself stops at 16 (fmha_mfma_4x4x4_kernel.hpp:179, README.md:233).
+ *
+ * The caller provides a device workspace of at least
+ * fmha_decode_splitkv_workspace_size(batch, Hq, Hkv, max_seqlen_kv, head_dim)
+ * bytes, 256-byte aligned; its contents on entry do not matter.  Calls that
+ * share a workspace must be ordered (same stream or synchronised).
+ */
+size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                          int32_t max_seqlen_kv, int32_t head_dim);
+
+int fmha_decode_fwd_splitkv(void* stream,
+                            const void* Q, const void* K, const void* V, void* O,
+                            const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv,
+                            int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                            int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                            float softmax_scale, void* workspace, size_t workspace_bytes);
 
 /* Human-readable text for a code returned above (never NULL). */
 const char* fmha_decode_error_string(int code);

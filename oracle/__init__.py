@@ -44,9 +44,9 @@ def lib():
         vp, i64, i32, f32, f64 = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float,
                                   ctypes.c_double)
         L.oracle_decode.restype = ctypes.c_int
-        L.oracle_decode.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f32, i32, vp, vp, f64, i32]
+        L.oracle_decode.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f32, i32, vp, vp, f64, i32, i32]
         L.oracle_decode_f64.restype = ctypes.c_int
-        L.oracle_decode_f64.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f64, vp, i32]
+        L.oracle_decode_f64.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f64, vp, i32, i32]
         L.oracle_compare.restype = None
         L.oracle_compare.argtypes = [vp, vp, vp, i64, f64, f64, vp]
         L.oracle_generate_seqlens.restype = None
@@ -66,31 +66,44 @@ def _u16(a):
     return a
 
 
-def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps=SLACK_EPS,
-           nthreads=0):
+def slack_eps_for(max_len):
+    """Relative perturbation of a softmax weight the gate tolerates: 2^-19,
+    or, for long rows, 4*sqrt(max_len) float32 unit roundoffs -- the typical
+    error of the loop's sequential float32 sum of max_len exponentials, which
+    a kernel summing in another order does not share.  Up to 256 rows the
+    first term rules."""
+    return max(SLACK_EPS, 4.0 * float(max_len) ** 0.5 * 2.0 ** -24)
+
+
+def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps=None,
+           nthreads=0, max_seqlen=16):
     """Restated reference loop.  q [B,Hq,D], k/v [rows,Hkv,D] as uint16 bf16
-    bits; cu int32 [B+1].  Returns (o fp16 bits [B,Hq,D], slack or None)."""
+    bits; cu int32 [B+1]; lengths up to max_seqlen (the reference's 16 by
+    default).  Returns (o fp16 bits [B,Hq,D], slack or None)."""
     q, k, v = _u16(q), _u16(k), _u16(v)
     cu = np.ascontiguousarray(cu, dtype=np.int32)
     B = cu.shape[0] - 1
     o = np.empty((B, hq, d), dtype=np.uint16)
     slack = np.empty((B, hq, d), dtype=np.float32) if with_slack else None
     nt = nthreads if nthreads > 0 else (os.cpu_count() or 1)
+    if slack_eps is None:
+        slack_eps = slack_eps_for(int(np.max(np.diff(cu))) if B > 0 else 0)
     rc = lib().oracle_decode(_p(q), _p(k), _p(v), _p(cu), B, hq, hkv, d, float(scale), p_mode,
-                             _p(o), _p(slack), float(slack_eps), nt)
+                             _p(o), _p(slack), float(slack_eps), nt, max_seqlen)
     if rc != 0:
         raise ValueError("oracle_decode rejected its arguments")
     return o, slack
 
 
-def decode_f64(q, k, v, cu, hq, hkv, d, scale, nthreads=0):
+def decode_f64(q, k, v, cu, hq, hkv, d, scale, nthreads=0, max_seqlen=16):
     """Float64 decode attention; returns float64 [B,Hq,D]."""
     q, k, v = _u16(q), _u16(k), _u16(v)
     cu = np.ascontiguousarray(cu, dtype=np.int32)
     B = cu.shape[0] - 1
     o = np.empty((B, hq, d), dtype=np.float64)
     nt = nthreads if nthreads > 0 else (os.cpu_count() or 1)
-    rc = lib().oracle_decode_f64(_p(q), _p(k), _p(v), _p(cu), B, hq, hkv, d, float(scale), _p(o), nt)
+    rc = lib().oracle_decode_f64(_p(q), _p(k), _p(v), _p(cu), B, hq, hkv, d, float(scale), _p(o), nt,
+                                 max_seqlen)
     if rc != 0:
         raise ValueError("oracle_decode_f64 rejected its arguments")
     return o

@@ -14,10 +14,10 @@
 //   * 64-bit sizes everywhere (the reference sizes tensors in int,
 //     fmha_host.cpp:85-93).
 // For Hq == Hkv and scale == 1.0f/sqrtf(D) the bf16-P mode is bit-identical to
-// the reference loop; tests/test_oracle_ref.py checks that against the
+// the reference loop; tests/test_oracle.py checks that against the
 // reference's own do_validation compiled from /root/reference (oracle/_ref).
 //
-// Pinning (see tests/test_oracle.py, tests/test_oracle_ref.py): bit-exact
+// Pinning (see tests/test_oracle.py): bit-exact
 // against the reference do_validation (MHA); S=1 known answer O = fp16(V);
 // Q=0 closed form P = bf16(1/S); one dominant key -> O = fp16(V_j); GQA equal
 // to MHA on head-repeated K/V; fp64 mode against torch's float64
@@ -90,7 +90,13 @@ inline uint16_t f32_to_f16(float f) {
 // fmha_vectorized_fma_kernel.hpp:256).
 void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t kv_stride, int S, int D, float scale,
               int p_mode, uint16_t* o, float* slack, double slack_eps) {
-  float scores[16];
+  // The reference sizes these arrays for 16 rows (fmha_host.cpp:164, :215);
+  // longer rows extend the same loop.
+  thread_local std::vector<float> scores_buf, p_buf, jump_buf;
+  scores_buf.resize(S > 16 ? S : 16);
+  p_buf.resize(S > 16 ? S : 16);
+  jump_buf.resize(S > 16 ? S : 16);
+  float* scores = scores_buf.data();
   for (int s = 0; s < S; s++) {
     float sum = 0;
     const uint16_t* kr = k + (int64_t)s * kv_stride;
@@ -102,8 +108,8 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   for (int s = 0; s < S; s++) maxv = fmaxf(maxv, scores[s]);
   float sum_exp = 0.0f;
   for (int s = 0; s < S; s++) sum_exp += expf(scores[s] - maxv);
-  float p[16];
-  float jump[16];
+  float* p = p_buf.data();
+  float* jump = jump_buf.data();
   for (int s = 0; s < S; s++) {
     const float pf = expf(scores[s] - maxv) / sum_exp;
     p[s] = p_mode == 0 ? bf16_to_f32(f32_to_bf16(pf)) : pf;
@@ -132,7 +138,9 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
 // "truth" comparisons.
 void head_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t kv_stride, int S, int D, double scale,
               double* o) {
-  double t[16];
+  thread_local std::vector<double> t_buf;
+  t_buf.resize(S > 16 ? S : 16);
+  double* t = t_buf.data();
   double m = -INFINITY;
   for (int s = 0; s < S; s++) {
     double sum = 0;
@@ -158,14 +166,15 @@ extern "C" {
 // cu: [batch+1] row offsets.  p_mode 0 = bf16 weights (reference CPU loop),
 // 1 = fp32 weights.  o: fp16 bits [batch, hq, d].  slack: optional float
 // [batch, hq, d] (see head_f32).  Returns 0, or -1 for a length outside
-// [0, 16] or bad arguments (nothing is written then).
+// [0, max_seqlen] or bad arguments (nothing is written then).  The
+// reference's bound is 16; longer rows run the same loop.
 int oracle_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* cu, int64_t batch, int hq,
                   int hkv, int d, float scale, int p_mode, uint16_t* o, float* slack, double slack_eps,
-                  int nthreads) {
-  if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0) return -1;
+                  int nthreads, int max_seqlen) {
+  if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0 || max_seqlen < 0) return -1;
   for (int64_t b = 0; b < batch; b++) {
     const int S = cu[b + 1] - cu[b];
-    if (S < 0 || S > 16) return -1;
+    if (S < 0 || S > max_seqlen) return -1;
   }
   const int g = hq / hkv;
   const int64_t kv_stride = (int64_t)hkv * d;
@@ -185,11 +194,11 @@ int oracle_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
 
 // Float64 decode attention (no rounding anywhere but the bf16 inputs).
 int oracle_decode_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* cu, int64_t batch,
-                      int hq, int hkv, int d, double scale, double* o, int nthreads) {
-  if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0) return -1;
+                      int hq, int hkv, int d, double scale, double* o, int nthreads, int max_seqlen) {
+  if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0 || max_seqlen < 0) return -1;
   for (int64_t b = 0; b < batch; b++) {
     const int S = cu[b + 1] - cu[b];
-    if (S < 0 || S > 16) return -1;
+    if (S < 0 || S > max_seqlen) return -1;
   }
   const int g = hq / hkv;
   const int64_t kv_stride = (int64_t)hkv * d;

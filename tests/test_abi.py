@@ -33,7 +33,8 @@ def lib():
 def test_exports_every_declared_function(lib):
     names = header_functions()
     assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_uniform", "fmha_decode_fwd_strided",
-                          "fmha_decode_fwd_paged", "fmha_decode_error_string",
+                          "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
+                          "fmha_decode_fwd_splitkv", "fmha_decode_error_string",
                           "fmha_decode_last_error_detail", "fmha_decode_version"}
     from fmha_amd import _lib
     assert set(names) == set(_lib.EXPORTED)
@@ -154,12 +155,45 @@ def test_paged_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
+def splitkv(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, maxs=1000, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088, ws=P * 64, wsb=1 << 30)
+    a.update(kw)
+    return lib.fmha_decode_fwd_splitkv(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["maxs"], a["batch"],
+                                       a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"], a["ws"], a["wsb"])
+
+
+def test_splitkv_workspace_size(lib):
+    f = lib.fmha_decode_splitkv_workspace_size
+    assert f(0, 16, 16, 100, 128) == 0 and f(4, 16, 16, -1, 128) == 0 and f(4, 16, 16, 100, 96) == 0
+    small, big = f(4, 16, 16, 100, 128), f(4, 16, 16, 10000, 128)
+    assert 0 < small < big and small % 256 == 0 and big % 256 == 0
+    # scores (4 B per row and query head) dominate a long row
+    assert big >= 4 * 16 * 10000 * 4
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(maxs=-1), BAD, "max_seqlen_kv"),
+    (dict(maxs=1 << 20), BAD, "too large"),
+    (dict(ws=None), BAD, "workspace"),
+    (dict(ws=P * 64 + 16), BAD, "256-byte"),
+    (dict(wsb=1024), BAD, "too small"),
+    (dict(cu=None), BAD, "cu_seqlens_kv"),
+    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    (dict(sq=3), BAD, "seqlen_q"),
+])
+def test_splitkv_rejects(lib, kw, code, needle):
+    assert splitkv(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
 def test_batch_zero_is_a_noop(lib):
     # Nothing is launched and no pointer is needed for an empty batch.
     assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
     assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
     assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0
+    assert splitkv(lib, batch=0, q=None, k=None, v=None, o=None, cu=None, ws=None) == 0
     assert lib.fmha_decode_last_error_detail() == b""
 
 
