@@ -142,7 +142,7 @@ def run_config(suite, idx, args):
         st = oracle.compare(os_, r, slack, ATOL, RTOL)
         ok = st["fails"] == 0 and st["ref_rule_fails"] == 0 and st["nonfinite"] == 0
         res["validation"] = {"batches_checked": int(len(sel)), "passed": ok,
-                             **{k_: st[k_] for k_ in ("n", "fails", "ref_rule_fails", "nonfinite",
+                             **{k_: st[k_] for k_ in ("n", "fails", "ref_rule_fails", "ref_rule_fails_raw", "nonfinite",
                                                       "slack_elems", "max_abs", "max_rel")}}
     return res
 
