@@ -37,12 +37,14 @@ int reject(int code, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Concurrency cap.  Each wave issues all of its loads at once; MI355X
-// streams best with about 128 KiB of requests in flight per CU (measured:
-// 3-5 waves of the S=16, D=128 unit per CU beat the 5-6 that registers
-// allow by 4%).  The library reserves unused LDS per workgroup so that
-// only that many waves fit on a CU.
-constexpr int kInflightBytesPerCU = 128 * 1024;
+// Concurrency cap.  Each wave issues all of its loads at once, and MI355X
+// streams fastest with a bounded amount of them in flight per CU: measured
+// sweeps put the best at about 80 KiB for units of 10-36 KiB (3 waves of the
+// S=16, D=128 unit: 7.13 TB/s, against 6.63 TB/s uncapped; 6 waves of the
+// S=5, D=256 unit; 8 waves of the reference's Poisson(4) varlen unit).  Tiny
+// units (S=1) want every wave the registers allow.  The library reserves
+// unused LDS per workgroup so that only that many waves fit on a CU.
+constexpr int kInflightBytesPerCU = 80 * 1024;
 constexpr int kMaxWavesPerCU = 32;
 
 // Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
@@ -116,13 +118,12 @@ hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStrea
 
 // Waves per CU for a unit that moves `rows` K/V rows and G query heads:
 // each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
-// of Q in and 1 KiB of O out.
+// of Q in and 1 KiB of O out.  Caps of 16 or more are dropped (no cap).
 int waves_per_cu_for(int rows, int g) {
   const int unit_bytes = 1024 * (2 * rows + 2 * g);
   int w = kInflightBytesPerCU / unit_bytes;
-  if (w < 3) w = 3;
-  if (w > kMaxWavesPerCU) w = kMaxWavesPerCU;
-  return w;
+  if (w >= 16) return kMaxWavesPerCU;
+  return w < 3 ? 3 : w;
 }
 
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
@@ -201,9 +202,10 @@ DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32
   return a;
 }
 
-// Rows a lengths array may announce, for sizing the wave cap: the
-// reference's own varlen workload averages 4.3 rows; 8 covers it.
-constexpr int kVarlenRowsHint = 8;
+// Rows per batch assumed when lengths come from a device array (the host
+// cannot see them): the reference's own varlen workload, Poisson(4) lengths
+// in [2, 16], averages 4.3 rows, and its best cap is the 4-row one.
+constexpr int kVarlenRowsHint = 4;
 
 // ---------------------------------------------------------------------------
 // Split-KV (lengths beyond 16)
@@ -253,8 +255,9 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   const uint32_t waves = a.total_units * (uint32_t)a.nchunks;
-  // 16 rows of K (or V) per wave in flight: 8 waves reach ~128 KiB per CU.
-  const int w = kInflightBytesPerCU / (16 * 1024);
+  // 16 rows of K (or V) per wave in flight; these two-phase kernels measured
+  // best at 8 waves per CU (4.4 vs 3.9 TB/s at 5 on long-context shapes).
+  const int w = 8;
   {
     const auto kernel = fmha_decode::splitkv_scores_kernel<D, G>;
     hipFuncAttributes attr;
