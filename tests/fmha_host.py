@@ -10,8 +10,10 @@ selected configuration it:
     own generator (Poisson(4) rejected outside [2, max], mt19937(42),
     fmha_host.cpp:58-72) for the reference-suite configurations;
   * times `--iters` calls (HIP events per call on the launch stream, after
-    `--warmup` calls) and reports µs/call, algorithmic TB/s and % of the
-    8 TB/s HBM peak, counting bytes as fmha_host.cpp:428-430 does;
+    `--warmup` calls; with --rotate N, N input sets used in turn so that a
+    small configuration is not served from the 256 MB MALL) and reports
+    µs/call, algorithmic TB/s and % of the 8 TB/s HBM peak, counting bytes
+    as fmha_host.cpp:428-430 does;
   * zeroes O, runs once more and checks the whole output against the oracle
     with the gate in tests/common.py (or a seeded sample of batches);
   * prints one JSON line per configuration and exits non-zero if any check
@@ -75,34 +77,41 @@ def run_config(suite, idx, args):
     rows = int(cu_h[-1])
     seed = 0xF3A00000 + 16 * idx + (0 if suite == "baseline" else 8)
     gen = torch.Generator(device=dev).manual_seed(seed)
-    q = torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.bfloat16)
-    k = torch.randn(rows, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
-    v = torch.randn(rows, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
-    if std != 1.0:
-        q.mul_(std), k.mul_(std), v.mul_(std)
+    # --rotate N: N independent input/output sets used in turn, so that a
+    # small configuration cannot be served from the 256 MB MALL between calls.
+    sets = []
+    for _ in range(max(1, args.rotate)):
+        q = torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(rows, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(rows, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+        if std != 1.0:
+            q.mul_(std), k.mul_(std), v.mul_(std)
+        o = torch.empty(B, Hq, 1, D, device=dev, dtype=torch.float16)
+        sets.append((q, k, v, o))
+    q, k, v, o = sets[0]
     cu = torch.from_numpy(cu_h).to(dev)
-    o = torch.empty(B, Hq, 1, D, device=dev, dtype=torch.float16)
     scale = 1.0 / math.sqrt(D)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
     uniform = S is not None and not args.varlen
 
-    def call():
+    def call(i=0):
+        qq, kk, vv, oo = sets[i % len(sets)]
         if uniform:
-            fmha_amd.launch_fmha_decode_uniform(sp, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            fmha_amd.launch_fmha_decode_uniform(sp, qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), oo.data_ptr(),
                                                 S, B, Hq, Hkv, 1, D, D, scale)
         else:
-            fmha_amd.launch_fmha_decode(sp, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            fmha_amd.launch_fmha_decode(sp, qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), oo.data_ptr(),
                                         cu.data_ptr(), B, Hq, Hkv, 1, D, D, scale)
 
-    for _ in range(args.warmup):
-        call()
+    for i in range(args.warmup):
+        call(i)
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.iters)]
-    for a, b in ev:
+    for i, (a, b) in enumerate(ev):
         a.record(stream)
-        call()
+        call(i)
         b.record(stream)
     torch.cuda.synchronize()
     per = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)  # µs
@@ -113,6 +122,7 @@ def run_config(suite, idx, args):
         "suite": suite, "config": idx, "batch": B, "num_heads_q": Hq, "num_heads_kv": Hkv,
         "seqlen_kv": S if S is not None else "poisson(4) in [2,16]", "head_dim": D, "std": std,
         "path": "uniform" if uniform else "cu_seqlens", "rows": rows, "bytes_per_call": nbytes,
+        "input_sets": len(sets),
         "us_per_call_median": round(med_us, 2), "us_per_call_mean": round(mean_us, 2),
         "tb_s_median": round(nbytes / (med_us * 1e-6) / 1e12, 4),
         "pct_of_peak_median": round(100 * nbytes / (med_us * 1e-6) / 1e12 / HBM_PEAK_TBS, 2),
@@ -154,6 +164,8 @@ def main():
     ap.add_argument("--iters", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--validate", choices=["full", "sample", "none"], default="sample")
+    ap.add_argument("--rotate", type=int, default=1,
+                    help="independent input sets used in turn (defeats MALL residency for small configs)")
     ap.add_argument("--varlen", action="store_true",
                     help="launch uniform configurations through the cu_seqlens entry point")
     args = ap.parse_args()
