@@ -14,6 +14,10 @@ Prints one JSON line:
                 of per-launch HIP-event durations on the launch stream, against
                 the 8 TB/s HBM peak; traffic = measured HBM bytes per launch
                 from the committed rocprofv3 counter summary, when present;
+  rotated_inputs  the same calls over --rotate input/output sets used in
+                turn (no call finds Q or O of the previous call in the MALL);
+                the timed loop above reuses one set, as the reference's
+                harness does (fmha_host.cpp:377-389);
   cpu_baseline  the reference's own CPU loop (fmha_host.cpp:158-284, built from
                 /root/reference into oracle/_ref) -- or the restated oracle
                 when that build is absent -- timed single-threaded on this
@@ -105,6 +109,8 @@ def main():
     ap.add_argument("--cpu-batches", type=int, default=30720,
                     help="batches of the workload the CPU baseline runs (bounded sample)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--rotate", type=int, default=2,
+                    help="input/output sets of the second timed leg (1 = skip that leg)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -129,8 +135,8 @@ def main():
     sptr = stream.cuda_stream
     qp, kp, vp, op = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
 
-    def step():
-        fmha_amd.launch_fmha_decode_uniform(sptr, qp, kp, vp, op, S, B, Hq, Hkv, 1, D, D, scale)
+    def step(ptrs=(qp, kp, vp, op)):
+        fmha_amd.launch_fmha_decode_uniform(sptr, *ptrs, S, B, Hq, Hkv, 1, D, D, scale)
 
     for _ in range(args.warmup):
         step()
@@ -154,6 +160,40 @@ def main():
     value_tbs = nbytes / (ms_per_step * 1e-3) / 1e12
     achieved_gbs = nbytes / (kern_ms * 1e-3) / 1e9
     per_sorted = sorted(per)
+
+    # Second leg: the same calls over --rotate input/output sets used in
+    # turn.  In the leg above the next call finds part of Q (read with the
+    # default policy) and the rewritten O in the 256 MB MALL; here every call
+    # reads and writes buffers the previous call did not touch.
+    rotated = None
+    if args.rotate > 1:
+        sets = [(qp, kp, vp, op)]
+        keep = []
+        for _ in range(args.rotate - 1):
+            t = (torch.randn(B, Hq, 1, D, generator=gen, device=dev, dtype=torch.bfloat16),
+                 torch.randn(B, S, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16),
+                 torch.randn(B, S, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16),
+                 torch.empty(B, Hq, 1, D, device=dev, dtype=torch.float16))
+            keep.append(t)
+            sets.append(tuple(x.data_ptr() for x in t))
+        for i in range(args.warmup):
+            step(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        for i in range(K):
+            ev[i][0].record(stream)
+            step(sets[i % len(sets)])
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        rot_ms = ev[0][0].elapsed_time(ev[-1][1]) / K
+        rot_kern_ms = sum(a.elapsed_time(b) for a, b in ev) / K
+        rotated = {
+            "input_sets": len(sets),
+            "us_per_call": round(rot_ms * 1e3, 2),
+            "us_per_call_kernel_mean": round(rot_kern_ms * 1e3, 2),
+            "tb_s": round(nbytes / (rot_ms * 1e-3) / 1e12, 4),
+            "pct_of_peak": round(100.0 * nbytes / (rot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        }
+        del keep
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -196,6 +236,7 @@ def main():
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },
+        "rotated_inputs": rotated,
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }

@@ -15,7 +15,7 @@
 //   * each lane issues all of its Q, K and V loads (G + 2*SMAX b128 buffer
 //     loads, K/V with the streaming hint) before any arithmetic, so a wave
 //     keeps 2*SMAX KiB of K/V in flight; the host caps the waves per CU (by
-//     reserving LDS) so that a CU holds about 128 KiB of requests, the level
+//     reserving LDS) so that a CU holds about 80 KiB of requests, the level
 //     at which MI355X streams fastest;
 //   * K/V rows are fetched through a buffer resource whose num_records ends at
 //     this batch's last row: rows j >= S_b (padding up to the power-of-two
@@ -120,15 +120,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // Cache-policy operand of the buffer instructions (gfx950: bit 0 sc0, bit 1
 // nt, bit 4 sc1).
 //   * K and V are read exactly once: non-temporal (streaming) loads, +12% on
-//     MI355X over default-policy loads.
-//   * O is stored at device scope (sc1): the write goes through the XCD's L2
-//     instead of leaving dirty lines there to be written back later in the
-//     middle of the read stream; +3% on every configuration measured.  The
+//     MI355X over default-policy loads.  Adding sc0 or sc1 to them changes
+//     nothing measurable.
+//   * O is written exactly once: stored non-temporally at device scope
+//     (nt | sc1), written through the XCD's L2 without being kept there.
+//     Interleaved A/B on MI355X, µs per call, device scope alone vs nt|sc1:
+//     B=30720 S=16 D=128 with Hq=Hkv=32: 1270 vs 1214; Hq=32 Hkv=16: 706
+//     vs 640; Hq=64 Hkv=16: 812 vs 775; S=5 D=256 Hq=Hkv=16: 452 vs 416;
+//     Hq=Hkv=32 D=256: 2508 vs 2469; Hq=Hkv=16 D=128 with four input sets
+//     in rotation: 647 vs 628.  Device scope alone wins (by 1.5-3%) only
+//     where all of O (126 MB) fits in the 256 MB MALL and the next call
+//     rewrites the same buffer: the MALL then absorbs the rewrite.  The
 //     data is visible to later kernels either way.
 //   * Q keeps the default policy (a non-temporal Q load measured 4% slower).
 constexpr int kPolicyDefault = 0;
 constexpr int kPolicyStream = 2;
-constexpr int kPolicyStoreThrough = 16;
+constexpr int kPolicyStreamStore = 2 | 16;
 
 template <int POLICY>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
@@ -137,7 +144,7 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 }
 
 __device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, u32x4 x) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x), r, (int)voffset, 0, kPolicyStoreThrough);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x), r, (int)voffset, 0, kPolicyStreamStore);
 }
 
 // ---------------------------------------------------------------------------

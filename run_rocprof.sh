@@ -20,7 +20,7 @@ mkdir -p "$OUT"
 cd /tmp && export TMPDIR=/tmp
 
 case "$WL" in
-  bench) CMD=(python3 "$ROOT/bench.py" --no-cpu); TRACE_ARGS=(--steps 50 --warmup 5); PMC_ARGS=(--steps 3 --warmup 1) ;;
+  bench) CMD=(python3 "$ROOT/bench.py" --no-cpu --rotate 1); TRACE_ARGS=(--steps 50 --warmup 5); PMC_ARGS=(--steps 3 --warmup 1) ;;
   b[1-5]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#b}" --suite baseline --validate none)
           TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
   r[0-4]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#r}" --suite reference --validate none)
