@@ -217,33 +217,40 @@ size_t align_up(size_t x) { return (x + kWorkspaceAlign - 1) / kWorkspaceAlign *
 struct SplitPlan {
   int chunk_rows = 16;
   int nchunks = 1;
+  int nblk = 1;
   int64_t units = 0;
   size_t off_t = 0, off_m = 0, off_l = 0, off_ml = 0, off_opart = 0, total = 0;
 };
 
-// Chunks of C rows (C in {64, 128, 256}, or the rows' own multiple of 16
-// when shorter): small enough that batch * head groups * chunks fills the
-// GPU with 4096 waves where the work allows, large enough that the partial
-// outputs (4*D bytes per chunk and query head) stay a few percent of K/V.
+// Waves the P.V pass aims for: 8 per CU.  Each holds two sub-blocks of V
+// (up to 32 KiB) in flight.
+constexpr int64_t kSplitTargetWaves = 2048;
+
+// Scores: one wave per 16-row block.  P.V: chunks of C rows (C in
+// {64, ..., 512}, or the rows' own multiple of 16 when shorter), the largest
+// that still gives kSplitTargetWaves waves where the work allows, so the
+// partial outputs (4*D bytes per chunk and query head) stay a few percent
+// of V.
 SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
   SplitPlan p;
   const int heads_per_wave = kWaveSize / (d / 8);
   const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
   p.units = upb * batch;
-  int c = 256;
-  while (c > 64 && p.units * ((max_rows + c - 1) / c) < 4096) c /= 2;
+  int c = 512;
+  while (c > 64 && p.units * ((max_rows + c - 1) / c) < kSplitTargetWaves) c /= 2;
   const int fit = max_rows <= 16 ? 16 : (max_rows + 15) / 16 * 16;  // no longer than the rows need
   if (c > fit) c = fit;
   p.chunk_rows = c;
   p.nchunks = max_rows <= 0 ? 1 : (max_rows + c - 1) / c;
+  p.nblk = max_rows <= 0 ? 1 : (max_rows + fmha_decode::kSplitBlockRows - 1) / fmha_decode::kSplitBlockRows;
   const size_t heads = (size_t)batch * hq;
   size_t off = 0;
   p.off_t = off;
-  off += align_up(heads * (size_t)p.nchunks * c * 4);
+  off += align_up(heads * (size_t)p.nblk * fmha_decode::kSplitBlockRows * 4);
   p.off_m = off;
-  off += align_up(heads * (size_t)p.nchunks * 4);
+  off += align_up(heads * (size_t)p.nblk * 4);
   p.off_l = off;
-  off += align_up(heads * (size_t)p.nchunks * 4);
+  off += align_up(heads * (size_t)p.nblk * 4);
   p.off_ml = off;
   off += align_up(heads * 2 * 4);
   p.off_opart = off;
@@ -252,48 +259,66 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
   return p;
 }
 
+// Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
+// Scores waves request 32 KiB of K (16 KiB for G = 8) plus G KiB of Q at
+// once; P.V waves keep two 16-row (8-row for G = 8) sub-blocks of V in
+// flight.  Sweeps over long-context shapes (B=64 S=4096, B=8 S=32768, B=256
+// S=1024 G=8, B=1 S=131072) put both optima at 8; 3 or 4 scores waves cost
+// 5-20%.
+constexpr int kSplitScoresWavesPerCU = 8;
+constexpr int kSplitPvWavesPerCU = 8;
+
+template <typename K>
+size_t lds_reserve_kernel(K kernel, int waves) {
+  hipFuncAttributes attr;
+  size_t st = 0;
+  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess) st = attr.sharedSizeBytes;
+  return lds_reserve_for(waves, lds_per_cu(), st);
+}
+
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
-  const uint32_t waves = a.total_units * (uint32_t)a.nchunks;
-  // 16 rows of K (or V) per wave in flight; these two-phase kernels measured
-  // best at 8 waves per CU (4.4 vs 3.9 TB/s at 5 on long-context shapes).
-  const int w = 8;
+  constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
+  constexpr int NB = G >= 8 ? 1 : 2;   // 16-row blocks per scores wave (register budget)
+  const uint32_t upb = (uint32_t)a.units_per_batch;
+  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
+  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;
   {
-    const auto kernel = fmha_decode::splitkv_scores_kernel<D, G>;
-    hipFuncAttributes attr;
-    size_t st = 0;
-    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess) st = attr.sharedSizeBytes;
-    hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_for(w, lds_per_cu(), st), stream, a);
+    const auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB>;
+    hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel(kernel, kSplitScoresWavesPerCU), stream, a);
   }
-  const uint64_t heads = (uint64_t)a.batch * a.num_heads_q;
-  // Many chunks per row: a wave (stats) or a block (combine) per head.
-  const bool wide = a.nchunks > 16;
-  if (wide)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_wave_kernel, dim3((unsigned)heads), dim3(64), 0, stream, a);
+  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
+  // One lane per (batch, query head) for rows of at most 16 blocks, else one
+  // workgroup per head sized to the row's block count (8 blocks per thread
+  // and round).
+  if (a.nblk <= 16)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_lane_kernel, dim3((heads + 255) / 256), dim3(256), 0, stream, a);
+  else if (a.nblk <= 8 * 64)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<64>, dim3(heads), dim3(64), 0, stream, a);
+  else if (a.nblk <= 8 * 256)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<256>, dim3(heads), dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel, dim3((unsigned)((heads + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
+  if (a.nchunks == 1) {
+    const auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true>;
+    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel(kernel, kSplitPvWavesPerCU),
                        stream, a);
-  const bool direct = a.nchunks == 1;
-  {
-    const void* kp = direct ? reinterpret_cast<const void*>(fmha_decode::splitkv_pv_kernel<D, G, true>)
-                            : reinterpret_cast<const void*>(fmha_decode::splitkv_pv_kernel<D, G, false>);
-    hipFuncAttributes attr;
-    size_t st = 0;
-    if (hipFuncGetAttributes(&attr, kp) == hipSuccess) st = attr.sharedSizeBytes;
-    const size_t dyn = lds_reserve_for(w, lds_per_cu(), st);
-    if (direct)
-      hipLaunchKernelGGL((fmha_decode::splitkv_pv_kernel<D, G, true>), dim3(waves), dim3(kBlockThreads), dyn, stream,
-                         a);
-    else
-      hipLaunchKernelGGL((fmha_decode::splitkv_pv_kernel<D, G, false>), dim3(waves), dim3(kBlockThreads), dyn,
-                         stream, a);
+    return hipGetLastError();
   }
-  if (!direct && wide) {
-    hipLaunchKernelGGL(fmha_decode::splitkv_combine_block_kernel<D>, dim3((unsigned)heads), dim3(256), 0, stream, a);
-  } else if (!direct) {
-    const uint64_t lanes = heads * (D / 8);
+  {
+    const auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false>;
+    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel(kernel, kSplitPvWavesPerCU),
+                       stream, a);
+  }
+  if (a.nchunks <= 16) {
+    const uint64_t lanes = (uint64_t)heads * (D / 8);
     hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
                        stream, a);
+  } else if (a.nchunks <= 256) {
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads), dim3(1024), 0, stream, a);
   }
   return hipGetLastError();
 }
@@ -437,9 +462,12 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
   if (max_seqlen_kv < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv must be >= 0");
   const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim_q);
-  // Row offsets of one batch (rows up to nchunks * C) must stay below 2^30 bytes.
+  // One batch's K/V rows (up to nblk * 16) and one batch's scores
+  // (Hq * nblk * 16 floats) are each addressed through a buffer range that
+  // must stay below 2^30 bytes.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
-  if ((int64_t)plan.nchunks * plan.chunk_rows * row_bytes >= (int64_t(1) << 30))
+  const int64_t padded_rows = (int64_t)plan.nblk * fmha_decode::kSplitBlockRows;
+  if (padded_rows * row_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv too large for this head count (%d)", max_seqlen_kv);
   if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
   if ((reinterpret_cast<uintptr_t>(workspace) & (kWorkspaceAlign - 1)) != 0)
@@ -447,8 +475,8 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
   if (workspace_bytes < plan.total)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
                   plan.total);
-  if (plan.units * plan.nchunks > (int64_t)INT32_MAX || (int64_t)batch * num_heads_q > (int64_t)INT32_MAX)
-    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch * heads * chunks too large");
+  if (plan.units * plan.nblk > (int64_t)INT32_MAX || (int64_t)batch * num_heads_q > (int64_t)INT32_MAX)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch * heads * blocks too large");
   char* ws = static_cast<char*>(workspace);
   SplitArgs a = {};
   a.q = static_cast<const uint16_t*>(Q);
@@ -464,12 +492,11 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
   a.num_heads_q = num_heads_q;
   a.num_heads_kv = num_heads_kv;
   a.units_per_batch = (int32_t)(plan.units / batch);
+  a.nblk = plan.nblk;
   a.nchunks = plan.nchunks;
   a.chunk_rows = plan.chunk_rows;
   a.max_rows = max_seqlen_kv;
-  a.t_stride = plan.nchunks * plan.chunk_rows;
   a.batch = batch;
-  a.total_units = (uint32_t)plan.units;
   a.scale = softmax_scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = num_heads_q / num_heads_kv;

@@ -8,21 +8,27 @@
 // max and sum before any weight is formed, the work runs in four launches
 // over a caller-provided workspace:
 //
-//   1. scores:  wave = (batch, KV-head group, chunk of C rows).  16-row
-//               sub-blocks: K loads, dot products, transposing butterfly
-//               (shared with the short kernel), scaled scores t_j -> T, and
-//               the chunk's running (max m_c, sum l_c of exp(t - m_c)).
-//   2. stats:   lane = (batch, query head): m = max_c m_c,
-//               L = sum_c l_c * exp(m_c - m).
-//   3. pv:      wave = (batch, KV-head group, chunk): per sub-block the 64
-//               lanes form P_j = bf16(exp(t_j - m) / L) for the wave's heads
-//               into LDS, then V loads and packed dot2 accumulation; the
-//               chunk's fp32 partial output -> Opart (or fp16 O directly when
-//               every batch fits one chunk).
-//   4. combine: lane = (batch, query head, 8 dims): O = fp16(sum_c Opart).
+//   1. scores:  one wave per (batch, block of 16 rows, KV-head group): the
+//               block's Q and K rows are requested at once (as in the short
+//               kernel), dot products, transposing butterfly (shared with
+//               the short kernel); scaled scores t_j -> T, and per query head
+//               the block's max m_b and sum l_b of exp(t_j - m_b).
+//   2. stats:   one workgroup per (batch, query head): m = max_b m_b,
+//               L = sum_b l_b * exp(m_b - m), loads batched, reduction order
+//               fixed (deterministic).
+//   3. pv:      one wave per (batch, chunk of C rows, KV-head group), walking
+//               the chunk in sub-blocks of NR rows with two register sets:
+//               the next sub-block's V rows and scores are in flight while
+//               the current one is processed.  The 64 lanes form
+//               P_j = bf16(exp(t_j - m) / L) for the wave's heads into LDS,
+//               then packed dot2 accumulation; the chunk's fp32 partial
+//               output -> Opart, or fp16 O directly when every batch fits one
+//               chunk.
+//   4. combine: O = fp16(sum_c Opart), chunks added in order.
 //
-// K and V are each read once; T, the stats and Opart add 4 bytes per row per
-// query head and 4*D bytes per chunk per query head.
+// K and V are each read once; T adds 4 bytes per row and query head (written
+// by 1, read by 3), the block statistics 8 bytes per 16 rows and query head,
+// Opart 4*D bytes per chunk and query head.
 #pragma once
 
 #include "fmha_decode_kernel.hpp"
@@ -35,69 +41,77 @@ struct SplitArgs {
   const uint16_t* v;
   uint16_t* o;            // [batch, Hq, D] fp16
   const int32_t* cu;      // [batch+1]
-  float* t;               // [batch, Hq, t_stride] scaled scores
-  float* m;               // [batch, Hq, nchunks] chunk max
-  float* l;               // [batch, Hq, nchunks] chunk sum of exp(t - m_c)
+  float* t;               // [batch, nblk, Hq, 16] scaled scores
+  float* m;               // [batch, Hq, nblk] block max
+  float* l;               // [batch, Hq, nblk] block sum of exp(t - m_b)
   float* ml;              // [batch, Hq, 2] global max, global sum
   float* opart;           // [batch, Hq, nchunks, D] partial outputs
   int32_t num_heads_q;
   int32_t num_heads_kv;
-  int32_t units_per_batch;
-  int32_t nchunks;        // chunks per batch row (max_rows / chunk_rows, rounded up)
+  int32_t units_per_batch;  // KV-head groups per batch: ceil(Hkv / HPW)
+  int32_t nblk;           // 16-row blocks per batch row: ceil(max_rows / 16)
+  int32_t nchunks;        // P.V chunks per batch row: ceil(max_rows / chunk_rows)
   int32_t chunk_rows;     // C, a multiple of 16
   int32_t max_rows;       // lengths above this are invalid (NaN output)
-  int32_t t_stride;       // nchunks * chunk_rows
   int32_t batch;
-  uint32_t total_units;   // batch * units_per_batch
   float scale;
 };
 
-// Decodes a split wave id into (batch, head group, chunk) and the batch's
-// K/V range.  Returns false for an empty chunk or an invalid length.
-template <int D>
-__device__ __forceinline__ bool split_wave(const SplitArgs& a, uint32_t& b, int& hk, bool& head_ok, int& row0,
-                                           int& S, int64_t& base, int lane) {
-  constexpr int LPH = D / 8;
-  constexpr int HPW = kWaveSize / LPH;
-  const uint32_t id = blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-  const uint32_t nch = (uint32_t)a.nchunks;
-  const uint32_t unit = id / nch;
-  const uint32_t c = id - unit * nch;
-  if (unit >= a.total_units) return false;
-  const uint32_t upb = (uint32_t)a.units_per_batch;
-  b = unit / upb;
-  const uint32_t hg = unit - b * upb;
-  hk = (int)hg * HPW + lane / LPH;
-  head_ok = hk < a.num_heads_kv;
-  base = a.cu[b];
-  S = a.cu[b + 1] - (int)base;
-  row0 = (int)c * a.chunk_rows;
-  return S >= 0 && S <= a.max_rows && row0 < S;
+constexpr int kSplitBlockRows = kMaxSeq;  // rows per scores wave
+
+__device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+  return buffer_load16<kPolicyStream>(r, voffset);
+}
+
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voffset, 0, kPolicyDefault));
 }
 
 // ---------------------------------------------------------------------------
 // 1. scores
 // ---------------------------------------------------------------------------
-template <int D, int G>
+// Scores of 16-row block blk of batch b live at
+// T[((b * nblk + blk) * Hq + query head) * 16 + row % 16]: each wave writes
+// one contiguous span (its heads' 16 rows), whole cache lines.
+__device__ __forceinline__ uint64_t t_block_base(const SplitArgs& a, uint64_t b, int blk) {
+  return ((b * (uint64_t)a.nblk + (uint64_t)blk) * (uint64_t)a.num_heads_q) * kSplitBlockRows;
+}
+
+// NB blocks of 16 rows per wave, all of their K rows requested at once.
+template <int D, int G, int NB>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs a) {
   constexpr int LPH = D / 8;
+  constexpr int HPW = kWaveSize / LPH;
   constexpr int NS = ilog2(LPH);
-  constexpr int NR = 16;
+  constexpr int NR = kSplitBlockRows;
   constexpr int V = G * NR;
   constexpr int L = NS < ilog2(V) ? NS : ilog2(V);
   constexpr int W = (V >> NS) > 1 ? (V >> NS) : 1;
   constexpr int GS = W < NR ? W : NR;
   constexpr int C = ilog2(NR / GS);
   const int lane = threadIdx.x & (kWaveSize - 1);
-  uint32_t b;
-  int hk, row0, S;
-  bool head_ok;
-  int64_t base;
-  if (!split_wave<D>(a, b, hk, head_ok, row0, S, base, lane)) return;
+  // Wave order (batch, block group, head group): consecutive waves read
+  // neighbouring heads of the same rows.
+  const uint32_t id = blockIdx.x;
+  const uint32_t upb = (uint32_t)a.units_per_batch;
+  const uint32_t nwb = ((uint32_t)a.nblk + NB - 1) / NB;
+  const uint32_t per_b = nwb * upb;
+  const uint32_t b = id / per_b;
+  if (b >= (uint32_t)a.batch) return;
+  const uint32_t rem = id - b * per_b;
+  const uint32_t wb = rem / upb;
+  const uint32_t hg = rem - wb * upb;
+  const int64_t base = a.cu[b];
+  const int S = a.cu[b + 1] - (int)base;
+  const int j0 = (int)wb * NB * NR;
+  if (S < 0 || S > a.max_rows || j0 >= S) return;
+  const int hk = (int)hg * HPW + lane / LPH;
+  const bool head_ok = hk < a.num_heads_kv;
   const int r = lane % LPH;
   const int hq = a.num_heads_q;
   const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
+  // Range ends at the batch's last row: rows past S read 0 without access.
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + (uint64_t)base * a.num_heads_kv * D, (uint32_t)S * row_bytes);
   const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
   const uint32_t q_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
@@ -105,58 +119,64 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   u32x4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, q_off + g * D * 2);
+  u32x4 kr[NB * NR];
+#pragma unroll
+  for (int j = 0; j < NB * NR; ++j) kr[j] = buffer_load16_nt(k_rsrc, kv_off + (uint32_t)(j0 + j) * row_bytes);
+  __builtin_amdgcn_sched_barrier(0);
 
-  const int blk = r >> (NS - L);
-  // Heads whose scores this lane holds after the butterfly: W/GS groups.
-  float run_m[W / GS];
-  float run_l[W / GS];
+  // After the butterfly, lane r holds scores [blkl*W, blkl*W + W) of the
+  // G*NR (query head, row) pairs; lanes equal in r >> (NS - L) hold copies.
+  const int blkl = r >> (NS - L);
+  const bool writer = head_ok && (r & ((1 << (NS - L)) - 1)) == 0;
 #pragma unroll
-  for (int h = 0; h < W / GS; ++h) {
-    run_m[h] = -__builtin_inff();
-    run_l[h] = 0.0f;
-  }
-  const int row_end = min(S, row0 + a.chunk_rows);
-  for (int j0 = row0; j0 < row_end; j0 += NR) {
-    u32x4 kr[NR];
+  for (int q = 0; q < NB; ++q) {
+    const int blk = (int)wb * NB + q;
+    const int jb = j0 + q * NR;
+    if (jb >= S) break;
+    u32x4 ks[NR];
 #pragma unroll
-    for (int j = 0; j < NR; ++j)
-      kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + (uint32_t)(j0 + j) * row_bytes);
+    for (int j = 0; j < NR; ++j) ks[j] = kr[q * NR + j];
     float x[V];
-    partial_scores<G, NR>(qv, kr, x);
+    partial_scores<G, NR>(qv, ks, x);
     TransposeReduce<LPH, V, 0>::run(x, lane);
+    float* tb = a.t + t_block_base(a, b, blk) + (uint64_t)hk * G * NR;
 #pragma unroll
     for (int h = 0; h < W / GS; ++h) {
       float t[GS];
       float bm = -__builtin_inff();
+      const int vi0 = blkl * W + h * GS;
+      const int g = vi0 / NR;
+      const int jr0 = vi0 % NR;
 #pragma unroll
       for (int w = 0; w < GS; ++w) {
-        const int vi = blk * W + h * GS + w;
-        const int row = j0 + vi % NR;
         t[w] = x[h * GS + w] * a.scale;
-        bm = row < S ? fmaxf(bm, t[w]) : bm;
-        if (head_ok && row < S) a.t[((uint64_t)b * hq + hk * G + vi / NR) * a.t_stride + row] = t[w];
+        bm = jb + jr0 + w < S ? fmaxf(bm, t[w]) : bm;
       }
+      // Scores of rows past S (their K rows read as 0) land in the block's
+      // padding, which nothing reads as a weight.
+      if (writer) {
+        if constexpr (GS % 4 == 0) {
+#pragma unroll
+          for (int w = 0; w < GS; w += 4)
+            *reinterpret_cast<float4*>(tb + g * NR + jr0 + w) = float4{t[w], t[w + 1], t[w + 2], t[w + 3]};
+        } else {
+#pragma unroll
+          for (int w = 0; w < GS; ++w) tb[g * NR + jr0 + w] = t[w];
+        }
+      }
+      // Every block has a valid row, so the group's max is finite for finite
+      // scores.
       bm = GroupReduce<LPH, L - C, L, true>::run(bm);
-      const float nm = fmaxf(run_m[h], bm);  // finite: every sub-block has a valid row
       float bs = 0.0f;
 #pragma unroll
-      for (int w = 0; w < GS; ++w) {
-        const int row = j0 + (blk * W + h * GS + w) % NR;
-        bs += row < S ? expf(t[w] - nm) : 0.0f;
-      }
+      for (int w = 0; w < GS; ++w) bs += jb + jr0 + w < S ? expf(t[w] - bm) : 0.0f;
       bs = GroupReduce<LPH, L - C, L, false>::run(bs);
-      run_l[h] = run_l[h] * expf(run_m[h] - nm) + bs;
-      run_m[h] = nm;
+      if (writer && (blkl & ((1 << C) - 1)) == 0) {
+        const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk;
+        a.m[idx] = bm;
+        a.l[idx] = bs;
+      }
     }
-  }
-  if (!head_ok) return;
-  const int c = row0 / a.chunk_rows;
-#pragma unroll
-  for (int h = 0; h < W / GS; ++h) {
-    const int g = (blk * W + h * GS) / NR;
-    const uint64_t idx = ((uint64_t)b * hq + hk * G + g) * a.nchunks + c;
-    a.m[idx] = run_m[h];
-    a.l[idx] = run_l[h];
   }
 }
 
@@ -172,78 +192,180 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// ---------------------------------------------------------------------------
-// 2. stats: per (batch, query head), the global max and sum of exponentials.
-// Few chunks: one lane per head.  Many chunks: one wave per head, lanes
-// striding the chunks (lane order is fixed, so results are deterministic).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void splitkv_stats_wave_kernel(SplitArgs a) {
-  const uint64_t i = blockIdx.x;  // b * Hq + h
-  const int lane = threadIdx.x;
-  const uint64_t b = i / (uint64_t)a.num_heads_q;
-  const int S = a.cu[b + 1] - a.cu[b];
-  if (S <= 0 || S > a.max_rows) return;
-  const int n = (S + a.chunk_rows - 1) / a.chunk_rows;
-  const float* m = a.m + i * a.nchunks;
-  const float* l = a.l + i * a.nchunks;
-  float gm = -__builtin_inff();
-  for (int c = lane; c < n; c += kWaveSize) gm = fmaxf(gm, m[c]);
-  gm = wave_max(gm);
-  float gl = 0.0f;
-  for (int c = lane; c < n; c += kWaveSize) gl += l[c] * expf(m[c] - gm);
-  gl = wave_sum(gl);
-  if (lane == 0) {
-    a.ml[2 * i] = gm;
-    a.ml[2 * i + 1] = gl;
+// Max or sum over a workgroup of THREADS threads, in a fixed order (wave
+// trees, then waves in index order); every thread gets the result.
+template <int THREADS, bool IS_MAX>
+__device__ __forceinline__ float block_reduce(float x, float* red) {
+  x = IS_MAX ? wave_max(x) : wave_sum(x);
+  if constexpr (THREADS == kWaveSize) {
+    return x;
+  } else {
+    constexpr int NW = THREADS / kWaveSize;
+    if ((threadIdx.x & (kWaveSize - 1)) == 0) red[threadIdx.x / kWaveSize] = x;
+    __syncthreads();
+    float y = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) y = IS_MAX ? fmaxf(y, red[w]) : y + red[w];
+    __syncthreads();  // red is reused by the next call
+    return y;
   }
 }
 
-__global__ __launch_bounds__(256) void splitkv_stats_kernel(SplitArgs a) {
-  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// ---------------------------------------------------------------------------
+// 2. stats: per (batch, query head), the global max and sum of exponentials
+// over the row's 16-row blocks.
+// ---------------------------------------------------------------------------
+// Rows of at most 16 blocks: one lane per head, all loads in flight.
+__global__ __launch_bounds__(256) void splitkv_stats_lane_kernel(SplitArgs a) {
+  constexpr int NB = 16;
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // b * Hq + h
   if (i >= (uint64_t)a.batch * a.num_heads_q) return;
   const uint64_t b = i / (uint64_t)a.num_heads_q;
   const int S = a.cu[b + 1] - a.cu[b];
   if (S <= 0 || S > a.max_rows) return;
-  const int n = (S + a.chunk_rows - 1) / a.chunk_rows;
-  const float* m = a.m + i * a.nchunks;
-  const float* l = a.l + i * a.nchunks;
-  float gm = -__builtin_inff();
-  for (int c = 0; c < n; ++c) gm = fmaxf(gm, m[c]);
+  const int n = (S + kSplitBlockRows - 1) / kSplitBlockRows;
+  const float* m = a.m + i * a.nblk;
+  const float* l = a.l + i * a.nblk;
+  float xm[NB], xl[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) {
+    xm[c] = c < n ? m[c] : -__builtin_inff();
+    xl[c] = c < n ? l[c] : 0.0f;
+  }
+  float gm = xm[0];
+#pragma unroll
+  for (int c = 1; c < NB; ++c) gm = fmaxf(gm, xm[c]);
   float gl = 0.0f;
-  for (int c = 0; c < n; ++c) gl += l[c] * expf(m[c] - gm);
+#pragma unroll
+  for (int c = 0; c < NB; ++c) gl += c < n ? xl[c] * expf(xm[c] - gm) : 0.0f;
   a.ml[2 * i] = gm;
   a.ml[2 * i + 1] = gl;
+}
+
+// Longer rows: one THREADS-thread group per head, U loads in flight per
+// thread, reduction order fixed.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void splitkv_stats_kernel(SplitArgs a) {
+  constexpr int U = 8;
+  __shared__ float red[THREADS / kWaveSize];
+  const uint64_t i = blockIdx.x;  // b * Hq + h
+  const int t = threadIdx.x;
+  const uint64_t b = i / (uint64_t)a.num_heads_q;
+  const int S = a.cu[b + 1] - a.cu[b];
+  if (S <= 0 || S > a.max_rows) return;  // the same for every thread of the group
+  const int n = (S + kSplitBlockRows - 1) / kSplitBlockRows;
+  const float* m = a.m + i * a.nblk;
+  const float* l = a.l + i * a.nblk;
+  float vm = -__builtin_inff();
+  for (int c0 = t; c0 < n; c0 += THREADS * U) {
+    float xm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * THREADS;
+      xm[u] = c < n ? m[c] : -__builtin_inff();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) vm = fmaxf(vm, xm[u]);
+  }
+  const float gm = block_reduce<THREADS, true>(vm, red);
+  float vs = 0.0f;
+  for (int c0 = t; c0 < n; c0 += THREADS * U) {
+    float xm[U], xl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * THREADS;
+      xm[u] = c < n ? m[c] : 0.0f;
+      xl[u] = c < n ? l[c] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) vs += c0 + u * THREADS < n ? xl[u] * expf(xm[u] - gm) : 0.0f;
+  }
+  const float gl = block_reduce<THREADS, false>(vs, red);
+  if (t == 0) {
+    a.ml[2 * i] = gm;
+    a.ml[2 * i + 1] = gl;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // 3. P.V per chunk.  DIRECT: every batch fits one chunk, so the wave writes
 // fp16 O itself (and the zero / NaN rows of empty or invalid batches).
 // ---------------------------------------------------------------------------
-template <int D, int G, bool DIRECT>
-__global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) {
-  constexpr int LPH = D / 8;
-  constexpr int HPW = kWaveSize / LPH;
-  constexpr int NR = 16;
+template <int D, int G, int NR>
+struct PvSlots {
+  static constexpr int LPH = D / 8;
+  static constexpr int HPW = kWaveSize / LPH;
+  static constexpr int SLOTS = HPW * G * NR;  // weights per sub-block
+  static constexpr int PER_LANE = (SLOTS + kWaveSize - 1) / kWaveSize;
+};
+
+// One sub-block: weights -> LDS -> row pairs -> accumulate.  Slot
+// f = lane + 64*i is (KV head f / (G*NR), query g = (f / NR) % G, row f % NR)
+// of the wave's heads; valid[i] marks slots inside the chunk.
+template <int D, int G, int NR>
+__device__ __forceinline__ void pv_sub_block(const u32x4 (&vr)[NR], const float (&tv)[PvSlots<D, G, NR>::PER_LANE],
+                                             const float (&gm)[PvSlots<D, G, NR>::PER_LANE],
+                                             const float (&gsum)[PvSlots<D, G, NR>::PER_LANE], int rows_left,
+                                             bool (&slot_ok)[PvSlots<D, G, NR>::PER_LANE], uint16_t* lds_p, int hkl,
+                                             int lane, float (&acc)[G][8]) {
+  using P = PvSlots<D, G, NR>;
   constexpr int VP = G * kMaxSeq;
-  constexpr int SLOTS = HPW * G * NR;                        // weights per sub-block
-  constexpr int PER_LANE = (SLOTS + kWaveSize - 1) / kWaveSize;
+#pragma unroll
+  for (int i = 0; i < P::PER_LANE; ++i) {
+    const int f = lane + kWaveSize * i;
+    const int jf = f % NR;
+    const bool valid = slot_ok[i] && jf < rows_left;
+    const float p = valid ? expf(tv[i] - gm[i]) / gsum[i] : 0.0f;
+    if (f < P::SLOTS)
+      lds_p[(f / (G * NR)) * VP + ((f / NR) % G) * kMaxSeq + jf] = __builtin_bit_cast(uint16_t, (__bf16)p);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t* pairs = reinterpret_cast<const uint32_t*>(lds_p + hkl * VP);
+  uint32_t pp[G][(NR + 1) / 2];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int jp = 0; jp < NR / 2; ++jp) pp[g][jp] = pairs[g * (kMaxSeq / 2) + jp];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  accumulate_pv<G, NR>(vr, pp, acc);
+}
+
+template <int D, int G, int NR, bool DIRECT>
+__global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) {
+  using P = PvSlots<D, G, NR>;
+  constexpr int LPH = P::LPH;
+  constexpr int HPW = P::HPW;
+  constexpr int PL = P::PER_LANE;
+  constexpr int VP = G * kMaxSeq;
+  static_assert(NR % 2 == 0 && NR <= kMaxSeq, "sub-block rows");
   __shared__ __attribute__((aligned(16))) uint16_t lds_p[HPW * VP];
   const int lane = threadIdx.x & (kWaveSize - 1);
-  uint32_t b = 0;
-  int hk = 0, row0 = -1, S = 0;
-  bool head_ok = false;
-  int64_t base = 0;
-  const bool live = split_wave<D>(a, b, hk, head_ok, row0, S, base, lane);
-  const int r = lane % LPH;
+  const uint32_t id = blockIdx.x;
+  const uint32_t upb = (uint32_t)a.units_per_batch;
+  const uint32_t per_b = (uint32_t)a.nchunks * upb;
+  const uint32_t b = id / per_b;
+  if (b >= (uint32_t)a.batch) return;
+  const uint32_t rem = id - b * per_b;
+  const uint32_t c = rem / upb;
+  const uint32_t hg = rem - c * upb;
+  const int64_t base = a.cu[b];
+  const int S = a.cu[b + 1] - (int)base;
+  const bool bad = S < 0 || S > a.max_rows;
+  const int row0 = (int)c * a.chunk_rows;
   const int hkl = lane / LPH;
+  const int hk = (int)hg * HPW + hkl;
+  const bool head_ok = hk < a.num_heads_kv;
+  const int r = lane % LPH;
   const int hq = a.num_heads_q;
-  if (!live) {
+  if (bad || row0 >= S) {
     // Only chunk 0 of a DIRECT launch owns the output of an empty or invalid
-    // batch; everything else has nothing to do.
+    // batch; the combine kernel covers them otherwise.
     if constexpr (DIRECT) {
-      const uint32_t id = blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-      if (id >= a.total_units * (uint32_t)a.nchunks || row0 != 0) return;
-      const bool bad = S < 0 || S > a.max_rows;
+      if (c != 0) return;
       const u32x4 fill = bad ? u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u} : u32x4{0u, 0u, 0u, 0u};
       const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
       const uint32_t o_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
@@ -252,23 +374,31 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     }
     return;
   }
+  const int rows = min(S - row0, a.chunk_rows);
   const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + (uint64_t)base * a.num_heads_kv * D, (uint32_t)S * row_bytes);
+  // The chunk's rows only: sub-blocks past its end read 0 without access.
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      make_rsrc(a.v + ((uint64_t)base + row0) * a.num_heads_kv * D, (uint32_t)rows * row_bytes);
   const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+  // This batch's scores, [nblk, Hq, 16].
+  const __amdgpu_buffer_rsrc_t t_rsrc =
+      make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * kSplitBlockRows * 4u);
   const int hk0 = hk - hkl;  // first KV head of this wave
 
-  // The weight slots this lane forms: slot f = lane + 64*i covers
-  // (head hkl_f, query g_f, row j_f) of the wave's heads.
-  float gm[PER_LANE], gsum[PER_LANE];
+  float gm[PL], gsum[PL];
+  uint32_t t_off[PL];
+  bool slot_ok[PL];
 #pragma unroll
-  for (int i = 0; i < PER_LANE; ++i) {
+  for (int i = 0; i < PL; ++i) {
     const int f = lane + kWaveSize * i;
     const int hkf = hk0 + f / (G * NR);
     const int gf = (f / NR) % G;
-    const bool ok = f < SLOTS && hkf < a.num_heads_kv;
+    const int jf = f % NR;
+    slot_ok[i] = f < P::SLOTS && hkf < a.num_heads_kv;
     const uint64_t hqi = (uint64_t)b * hq + hkf * G + gf;
-    gm[i] = ok ? a.ml[2 * hqi] : 0.0f;
-    gsum[i] = ok ? a.ml[2 * hqi + 1] : 1.0f;
+    gm[i] = slot_ok[i] ? a.ml[2 * hqi] : 0.0f;
+    gsum[i] = slot_ok[i] ? a.ml[2 * hqi + 1] : 1.0f;
+    t_off[i] = slot_ok[i] ? (uint32_t)((hkf * G + gf) * kSplitBlockRows + jf) * 4u : kLaneOutOfRange;
   }
 
   float acc[G][8];
@@ -277,41 +407,27 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
 
-  const int row_end = min(S, row0 + a.chunk_rows);
-  for (int j0 = row0; j0 < row_end; j0 += NR) {
-    u32x4 vr[NR];
+  // Two register sets: sub-block s+1 is requested before s is processed.
+  // Requests past the chunk's last row return 0 without memory access (V)
+  // or read scores of other rows that the row check masks (T).
+  const int nsub = (rows + NR - 1) / NR;
+  u32x4 va[NR], vb[NR];
+  float ta[PL], tb[PL];
+  auto load = [&](u32x4 (&vr)[NR], float (&tv)[PL], int s) {
 #pragma unroll
-    for (int j = 0; j < NR; ++j)
-      vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + (uint32_t)(j0 + j) * row_bytes);
-    // Weights of this sub-block: exp(t - m) / L rounded to bf16, 0 past S.
+    for (int j = 0; j < NR; ++j) vr[j] = buffer_load16_nt(v_rsrc, kv_off + (uint32_t)(s * NR + j) * row_bytes);
+    // Sub-blocks never straddle a 16-row block (row0 is a multiple of 16).
+    const uint32_t sub = (uint32_t)(((row0 + s * NR) / kSplitBlockRows) * hq * kSplitBlockRows +
+                                    (s * NR) % kSplitBlockRows) * 4u;
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) {
-      const int f = lane + kWaveSize * i;
-      const int hlf = f / (G * NR);
-      const int gf = (f / NR) % G;
-      const int jf = f % NR;
-      const int hkf = hk0 + hlf;
-      const int row = j0 + jf;
-      float p = 0.0f;
-      if (f < SLOTS && hkf < a.num_heads_kv && row < S) {
-        const float t = a.t[((uint64_t)b * hq + hkf * G + gf) * a.t_stride + row];
-        p = expf(t - gm[i]) / gsum[i];
-      }
-      if (f < SLOTS) lds_p[hlf * VP + gf * kMaxSeq + jf] = __builtin_bit_cast(uint16_t, (__bf16)p);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t* pairs = reinterpret_cast<const uint32_t*>(lds_p + hkl * VP);
-    uint32_t pp[G][NR / 2];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int jp = 0; jp < NR / 2; ++jp) pp[g][jp] = pairs[g * (kMaxSeq / 2) + jp];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    accumulate_pv<G, NR>(vr, pp, acc);
+    for (int i = 0; i < PL; ++i) tv[i] = buffer_load_f32(t_rsrc, t_off[i] + sub);
+  };
+  load(va, ta, 0);
+  for (int s = 0; s < nsub; s += 2) {
+    load(vb, tb, s + 1);
+    pv_sub_block<D, G, NR>(va, ta, gm, gsum, rows - s * NR, slot_ok, lds_p, hkl, lane, acc);
+    load(va, ta, s + 2);
+    if (s + 1 < nsub) pv_sub_block<D, G, NR>(vb, tb, gm, gsum, rows - (s + 1) * NR, slot_ok, lds_p, hkl, lane, acc);
   }
 
   if constexpr (DIRECT) {
@@ -321,7 +437,6 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, o_off + g * D * 2, pack_f16x8(acc[g]));
   } else {
     if (!head_ok) return;
-    const int c = row0 / a.chunk_rows;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float* dst = a.opart + (((uint64_t)b * hq + hk * G + g) * a.nchunks + c) * D + r * 8;
@@ -340,8 +455,18 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
 // ---------------------------------------------------------------------------
 // 4. combine: O = fp16(sum over the batch's chunks of Opart), chunk order.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void add8(float (&acc)[8], const u32x4& lo, const u32x4& hi) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc[k] += __builtin_bit_cast(float, (uint32_t)lo[k]);
+    acc[4 + k] += __builtin_bit_cast(float, (uint32_t)hi[k]);
+  }
+}
+
+// Few chunks: one lane per (batch, query head, 8 dims), U chunks in flight.
 template <int D>
 __global__ __launch_bounds__(256) void splitkv_combine_kernel(SplitArgs a) {
+  constexpr int U = 4;
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const uint64_t per_head = D / 8;
   if (i >= (uint64_t)a.batch * a.num_heads_q * per_head) return;
@@ -356,27 +481,32 @@ __global__ __launch_bounds__(256) void splitkv_combine_kernel(SplitArgs a) {
   } else {
     const int n = (S + a.chunk_rows - 1) / a.chunk_rows;
     const float* src = a.opart + head * a.nchunks * D + d0;
-    for (int c = 0; c < n; ++c) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D + 4);
+    for (int c0 = 0; c0 < n; c0 += U) {
+      u32x4 lo[U], hi[U];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        acc[k] += __builtin_bit_cast(float, (uint32_t)lo[k]);
-        acc[4 + k] += __builtin_bit_cast(float, (uint32_t)hi[k]);
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u < n ? c0 + u : c0;
+        lo[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
+        hi[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D + 4);
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (c0 + u < n) add8(acc, lo[u], hi[u]);
     }
     out = pack_f16x8(acc);
   }
   *reinterpret_cast<u32x4*>(a.o + head * D + d0) = out;
 }
 
-// Many chunks: one 256-thread block per (batch, query head); thread t sums
-// dims [8*(t % (D/8)), +8) over chunks c = t / (D/8) + k * CG, then the CG
-// partial sums of each dim group are added in order through LDS.
-template <int D>
-__global__ __launch_bounds__(256) void splitkv_combine_block_kernel(SplitArgs a) {
+// Many chunks: one THREADS-thread block per (batch, query head); thread t
+// sums dims [8*(t % (D/8)), +8) over chunks c = t / (D/8) + k * CG (U chunks
+// in flight), then the CG partial sums of each dim group are added in order
+// through LDS.
+template <int D, int THREADS>
+__global__ __launch_bounds__(THREADS) void splitkv_combine_block_kernel(SplitArgs a) {
   constexpr int DG = D / 8;
-  constexpr int CG = 256 / DG;
+  constexpr int CG = THREADS / DG;
+  constexpr int U = 4;
   __shared__ float part[CG][D];
   const uint64_t head = blockIdx.x;  // b * Hq + h
   const int t = threadIdx.x;
@@ -388,14 +518,17 @@ __global__ __launch_bounds__(256) void splitkv_combine_block_kernel(SplitArgs a)
   const int n = bad ? 0 : (S + a.chunk_rows - 1) / a.chunk_rows;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const float* src = a.opart + head * a.nchunks * D + dg * 8;
-  for (int c = cg; c < n; c += CG) {
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D + 4);
+  for (int c0 = cg; c0 < n; c0 += CG * U) {
+    u32x4 lo[U], hi[U];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      acc[k] += __builtin_bit_cast(float, (uint32_t)lo[k]);
-      acc[4 + k] += __builtin_bit_cast(float, (uint32_t)hi[k]);
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * CG < n ? c0 + u * CG : c0;
+      lo[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
+      hi[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D + 4);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + u * CG < n) add8(acc, lo[u], hi[u]);
   }
 #pragma unroll
   for (int k = 0; k < 8; ++k) part[cg][dg * 8 + k] = acc[k];

@@ -1,0 +1,72 @@
+#!/usr/bin/env python3
+"""Timing of the split-KV entry point (fmha_decode_fwd_splitkv) on
+long-context shapes, for the profile under profiles/.
+
+For each shape (uniform lengths, bf16 N(0,1) inputs on the GPU), calls the
+library --warmup times, then times --iters calls with a HIP event pair per
+call on the launch stream and prints one JSON line: median µs per call and
+algorithmic TB/s (Q + K + V + O as the reference counts them,
+fmha_host.cpp:428-430, with Hkv heads for K/V; workspace traffic not
+counted).  Run it under `rocprofv3 --kernel-trace --stats` for the per-kernel
+split.
+
+    python3 tests/profiling/splitkv_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+SHAPES = [(64, 32, 8, 4096, 128), (8, 32, 8, 32768, 128), (256, 64, 8, 1024, 128), (1, 32, 8, 131072, 128),
+          (30720, 16, 16, 16, 128)]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--shapes", default="")
+    a = ap.parse_args()
+    import torch
+    import fmha_amd
+
+    shapes = [tuple(int(x) for x in s.split(":")) for s in a.shapes.split(",")] if a.shapes else SHAPES
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    for B, hq, hkv, S, D in shapes:
+        g = torch.Generator(device=dev).manual_seed(B * 7 + S)
+        q = torch.randn(B, hq, 1, D, generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(B * S, hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(B * S, hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+        cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32, device=dev)
+        o = torch.empty(B, hq, 1, D, device=dev, dtype=torch.float16)
+        ws = torch.empty(fmha_amd.splitkv_workspace_size(B, hq, hkv, S, D), dtype=torch.uint8, device=dev)
+        scale = 1.0 / math.sqrt(D)
+
+        def call():
+            fmha_amd.fmha_decode_splitkv(q, k, v, cu, S, softmax_scale=scale, out=o, workspace=ws)
+
+        for _ in range(a.warmup):
+            call()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.iters)]
+        for e0, e1 in ev:
+            e0.record(stream)
+            call()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        per = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
+        med = per[len(per) // 2]
+        nbytes = 2 * B * hq * D * 2 + 4 * B * S * hkv * D
+        print(json.dumps({"B": B, "Hq": hq, "Hkv": hkv, "S": S, "D": D, "us_per_call_median": round(med, 1),
+                          "tb_s": round(nbytes / med / 1e6, 3), "workspace_bytes": ws.numel()}), flush=True)
+        del q, k, v, o, ws
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()
