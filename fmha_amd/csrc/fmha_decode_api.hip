@@ -8,6 +8,7 @@
 // computes its own grid.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -59,23 +60,45 @@ size_t lds_reserve_for(int waves, int lds_per_cu, size_t static_lds) {
   return per_group > static_lds ? per_group - static_lds : 0;
 }
 
+// LDS bytes per CU of the current device, queried once per device.
 int lds_per_cu() {
-  int dev = 0, bytes = 0;
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cacheable = dev >= 0 && dev < kMaxDevices;
+  if (cacheable) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int bytes = 0;
   if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess) return 0;
+  if (cacheable) cache[dev].store(bytes, std::memory_order_relaxed);
   return bytes;
+}
+
+// Static LDS of a kernel, queried once (a property of the code object).
+template <auto KERNEL>
+size_t static_lds() {
+  static const size_t bytes = [] {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(KERNEL)) == hipSuccess ? attr.sharedSizeBytes
+                                                                                           : size_t(0);
+  }();
+  return bytes;
+}
+
+// Dynamic LDS that caps KERNEL at `waves` one-wave workgroups per CU.
+template <auto KERNEL>
+size_t lds_reserve_kernel(int waves) {
+  return lds_reserve_for(waves, lds_per_cu(), static_lds<KERNEL>());
 }
 
 template <int D, int G, int LAYOUT, int SB>
 hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  const auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB>;
+  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipFuncAttributes attr;
-  size_t static_lds = 0;
-  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess)
-    static_lds = attr.sharedSizeBytes;
-  const size_t dyn = lds_reserve_for(waves_per_cu, lds_per_cu(), static_lds);
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), dyn, stream, a);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
 }
 
@@ -268,14 +291,6 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
 constexpr int kSplitScoresWavesPerCU = 8;
 constexpr int kSplitPvWavesPerCU = 8;
 
-template <typename K>
-size_t lds_reserve_kernel(K kernel, int waves) {
-  hipFuncAttributes attr;
-  size_t st = 0;
-  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess) st = attr.sharedSizeBytes;
-  return lds_reserve_for(waves, lds_per_cu(), st);
-}
-
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
@@ -284,9 +299,9 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
   const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;
   {
-    const auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB>;
+    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB>;
     hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel(kernel, kSplitScoresWavesPerCU), stream, a);
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
   }
   const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
   // One lane per (batch, query head) for rows of at most 16 blocks, else one
@@ -301,14 +316,14 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   else
     hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
   if (a.nchunks == 1) {
-    const auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true>;
-    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel(kernel, kSplitPvWavesPerCU),
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true>;
+    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, a);
     return hipGetLastError();
   }
   {
-    const auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false>;
-    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel(kernel, kSplitPvWavesPerCU),
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false>;
+    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, a);
   }
   if (a.nchunks <= 16) {

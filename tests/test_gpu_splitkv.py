@@ -28,7 +28,8 @@ def _case(B, Hq, Hkv, D, seqlens, max_len, seed, std=1.0):
     assert_pass(st, f"splitkv B={B} D={D} max={max_len}")
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 16), (64, 32, 4), (256, 16, 8), (128, 8, 1)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 16), (64, 32, 4), (256, 16, 8), (128, 8, 1), (128, 32, 8),
+                                     (256, 16, 4)])
 @pytest.mark.parametrize("max_len", [17, 100, 700, 2048])
 def test_varlen_long(D, Hq, Hkv, max_len):
     rng = np.random.default_rng(max_len + D)
@@ -36,6 +37,27 @@ def test_varlen_long(D, Hq, Hkv, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=max_len * 3 + D)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2), (256, 8, 8)])
+def test_block_boundaries(D, Hq, Hkv):
+    """Lengths on and next to the 16-row block edges: a scores wave whose
+    second block is partly or wholly past the row's end."""
+    seqlens = np.array([16, 32, 48, 31, 33, 47, 15, 17, 1, 64], np.int32)
+    _case(len(seqlens), Hq, Hkv, D, seqlens, 64, seed=11 + D)
+
+
+def test_mid_chunk_count():
+    """16 < chunks <= 256 (the 256-thread combine) with two heads per KV head."""
+    rng = np.random.default_rng(12)
+    seqlens = rng.integers(6000, 8193, size=16).astype(np.int32)
+    seqlens[0] = 8192
+    _case(16, 32, 8, 128, seqlens, 8192, seed=12, std=0.5)
+
+
+def test_mid_block_count():
+    """512 < blocks <= 2048 (the 256-thread statistics) on one long row."""
+    _case(1, 32, 8, 128, np.array([20000], np.int32), 20000, seed=13, std=0.5)
 
 
 def test_short_lengths_match_short_path():
