@@ -283,18 +283,17 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
 }
 
 // Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
-// Scores waves request 32 KiB of K (16 KiB for G = 8) plus G KiB of Q at
-// once; P.V waves keep two 16-row (8-row for G = 8) sub-blocks of V in
-// flight.  Sweeps over long-context shapes (B=64 S=4096, B=8 S=32768, B=256
-// S=1024 G=8, B=1 S=131072) put both optima at 8; 3 or 4 scores waves cost
-// 5-20%.
+// Scores waves request 32 KiB of K plus G KiB of Q at once; P.V waves keep
+// two 16-row (8-row for G = 8) sub-blocks of V in flight.  Sweeps over
+// long-context shapes (B=64 S=4096, B=8 S=32768, B=256 S=1024 G=8, B=1
+// S=131072) put both optima at 8; 3 or 4 scores waves cost 5-20%.
 constexpr int kSplitScoresWavesPerCU = 8;
 constexpr int kSplitPvWavesPerCU = 8;
 
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
-  constexpr int NB = G >= 8 ? 1 : 2;   // 16-row blocks per scores wave (register budget)
+  constexpr int NB = 2;                // 16-row blocks per scores wave
   const uint32_t upb = (uint32_t)a.units_per_batch;
   const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
   const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;

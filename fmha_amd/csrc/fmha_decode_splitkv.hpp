@@ -78,13 +78,16 @@ __device__ __forceinline__ uint64_t t_block_base(const SplitArgs& a, uint64_t b,
 }
 
 // NB blocks of 16 rows per wave, all of their K rows requested at once.
+// The G query heads of a KV head are scored GH at a time against the same K
+// registers (GH = 4 bounds the partial sums a lane holds to 64).
 template <int D, int G, int NB>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
   constexpr int NS = ilog2(LPH);
   constexpr int NR = kSplitBlockRows;
-  constexpr int V = G * NR;
+  constexpr int GH = G > 4 ? 4 : G;
+  constexpr int V = GH * NR;
   constexpr int L = NS < ilog2(V) ? NS : ilog2(V);
   constexpr int W = (V >> NS) > 1 ? (V >> NS) : 1;
   constexpr int GS = W < NR ? W : NR;
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   __builtin_amdgcn_sched_barrier(0);
 
   // After the butterfly, lane r holds scores [blkl*W, blkl*W + W) of the
-  // G*NR (query head, row) pairs; lanes equal in r >> (NS - L) hold copies.
+  // GH*NR (query head, row) pairs; lanes equal in r >> (NS - L) hold copies.
   const int blkl = r >> (NS - L);
   const bool writer = head_ok && (r & ((1 << (NS - L)) - 1)) == 0;
 #pragma unroll
@@ -136,45 +139,51 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
     u32x4 ks[NR];
 #pragma unroll
     for (int j = 0; j < NR; ++j) ks[j] = kr[q * NR + j];
-    float x[V];
-    partial_scores<G, NR>(qv, ks, x);
-    TransposeReduce<LPH, V, 0>::run(x, lane);
     float* tb = a.t + t_block_base(a, b, blk) + (uint64_t)hk * G * NR;
 #pragma unroll
-    for (int h = 0; h < W / GS; ++h) {
-      float t[GS];
-      float bm = -__builtin_inff();
-      const int vi0 = blkl * W + h * GS;
-      const int g = vi0 / NR;
-      const int jr0 = vi0 % NR;
+    for (int g0 = 0; g0 < G; g0 += GH) {
+      u32x4 qh[GH];
 #pragma unroll
-      for (int w = 0; w < GS; ++w) {
-        t[w] = x[h * GS + w] * a.scale;
-        bm = jb + jr0 + w < S ? fmaxf(bm, t[w]) : bm;
-      }
-      // Scores of rows past S (their K rows read as 0) land in the block's
-      // padding, which nothing reads as a weight.
-      if (writer) {
-        if constexpr (GS % 4 == 0) {
+      for (int g = 0; g < GH; ++g) qh[g] = qv[g0 + g];
+      float x[V];
+      partial_scores<GH, NR>(qh, ks, x);
+      TransposeReduce<LPH, V, 0>::run(x, lane);
 #pragma unroll
-          for (int w = 0; w < GS; w += 4)
-            *reinterpret_cast<float4*>(tb + g * NR + jr0 + w) = float4{t[w], t[w + 1], t[w + 2], t[w + 3]};
-        } else {
+      for (int h = 0; h < W / GS; ++h) {
+        float t[GS];
+        float bm = -__builtin_inff();
+        const int vi0 = blkl * W + h * GS;
+        const int g = g0 + vi0 / NR;
+        const int jr0 = vi0 % NR;
 #pragma unroll
-          for (int w = 0; w < GS; ++w) tb[g * NR + jr0 + w] = t[w];
+        for (int w = 0; w < GS; ++w) {
+          t[w] = x[h * GS + w] * a.scale;
+          bm = jb + jr0 + w < S ? fmaxf(bm, t[w]) : bm;
         }
-      }
-      // Every block has a valid row, so the group's max is finite for finite
-      // scores.
-      bm = GroupReduce<LPH, L - C, L, true>::run(bm);
-      float bs = 0.0f;
+        // Scores of rows past S (their K rows read as 0) land in the
+        // block's padding, which nothing reads as a weight.
+        if (writer) {
+          if constexpr (GS % 4 == 0) {
 #pragma unroll
-      for (int w = 0; w < GS; ++w) bs += jb + jr0 + w < S ? expf(t[w] - bm) : 0.0f;
-      bs = GroupReduce<LPH, L - C, L, false>::run(bs);
-      if (writer && (blkl & ((1 << C) - 1)) == 0) {
-        const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk;
-        a.m[idx] = bm;
-        a.l[idx] = bs;
+            for (int w = 0; w < GS; w += 4)
+              *reinterpret_cast<float4*>(tb + g * NR + jr0 + w) = float4{t[w], t[w + 1], t[w + 2], t[w + 3]};
+          } else {
+#pragma unroll
+            for (int w = 0; w < GS; ++w) tb[g * NR + jr0 + w] = t[w];
+          }
+        }
+        // Every block has a valid row, so the group's max is finite for
+        // finite scores.
+        bm = GroupReduce<LPH, L - C, L, true>::run(bm);
+        float bs = 0.0f;
+#pragma unroll
+        for (int w = 0; w < GS; ++w) bs += jb + jr0 + w < S ? expf(t[w] - bm) : 0.0f;
+        bs = GroupReduce<LPH, L - C, L, false>::run(bs);
+        if (writer && (blkl & ((1 << C) - 1)) == 0) {
+          const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk;
+          a.m[idx] = bm;
+          a.l[idx] = bs;
+        }
       }
     }
   }

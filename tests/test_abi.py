@@ -220,3 +220,38 @@ def test_compat_header_compiles():
                             "--offload-arch=gfx950", "-I", os.path.join(ROOT, "include"), p],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_error_detail_is_per_thread(lib):
+    """The detail text of a rejected call belongs to the calling thread: a
+    thread making valid (empty) calls never sees another thread's text, and
+    a rejecting thread always reads its own.  ctypes releases the GIL for
+    the call, so the two threads' calls overlap."""
+    import threading
+    errors = []
+    start = threading.Barrier(2)
+
+    def rejecting():
+        start.wait()
+        for i in range(2000):
+            rc = fwd(lib, sq=2 + i % 3)
+            detail = lib.fmha_decode_last_error_detail().decode()
+            if rc != BAD or f"seqlen_q must be 1 (got {2 + i % 3})" not in detail:
+                errors.append(("rejecting", i, rc, detail))
+                return
+
+    def succeeding():
+        start.wait()
+        for i in range(2000):
+            rc = fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None)
+            detail = lib.fmha_decode_last_error_detail()
+            if rc != 0 or detail != b"":
+                errors.append(("succeeding", i, rc, detail))
+                return
+
+    threads = [threading.Thread(target=rejecting), threading.Thread(target=succeeding)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
