@@ -476,12 +476,14 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
   if (max_seqlen_kv < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv must be >= 0");
   const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim_q);
-  // One batch's K/V rows (up to nblk * 16) and one batch's scores
-  // (Hq * nblk * 16 floats) are each addressed through a buffer range that
-  // must stay below 2^30 bytes.
+  // One batch's K/V rows (up to nblk * 16), one batch's scores
+  // (Hq * nblk * 16 floats) and one batch's partial outputs are each
+  // addressed through a buffer range that must stay below 2^30 bytes.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
   const int64_t padded_rows = (int64_t)plan.nblk * fmha_decode::kSplitBlockRows;
-  if (padded_rows * row_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30))
+  const int64_t part_bytes = (int64_t)num_heads_q * plan.nchunks * head_dim_q * 4;  // one batch's partials
+  if (padded_rows * row_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30) ||
+      part_bytes >= (int64_t(1) << 30))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv too large for this head count (%d)", max_seqlen_kv);
   if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
   if ((reinterpret_cast<uintptr_t>(workspace) & (kWorkspaceAlign - 1)) != 0)

@@ -139,7 +139,11 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
     u32x4 ks[NR];
 #pragma unroll
     for (int j = 0; j < NR; ++j) ks[j] = kr[q * NR + j];
-    float* tb = a.t + t_block_base(a, b, blk) + (uint64_t)hk * G * NR;
+    // This block's scores [Hq][16], written non-temporally (read once, by
+    // the P.V pass): 4-6% faster on long-context shapes than default-policy
+    // stores.
+    const __amdgpu_buffer_rsrc_t t_rsrc = make_rsrc(a.t + t_block_base(a, b, blk), (uint32_t)hq * NR * 4u);
+    const uint32_t t_lane = head_ok ? (uint32_t)hk * G * NR * 4u : kLaneOutOfRange;
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GH) {
       u32x4 qh[GH];
@@ -163,13 +167,20 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
         // Scores of rows past S (their K rows read as 0) land in the
         // block's padding, which nothing reads as a weight.
         if (writer) {
+          const uint32_t off = t_lane + (uint32_t)(g * NR + jr0) * 4u;
           if constexpr (GS % 4 == 0) {
 #pragma unroll
-            for (int w = 0; w < GS; w += 4)
-              *reinterpret_cast<float4*>(tb + g * NR + jr0 + w) = float4{t[w], t[w + 1], t[w + 2], t[w + 3]};
+            for (int w = 0; w < GS; w += 4) {
+              const u32x4 v4 = {__builtin_bit_cast(uint32_t, t[w]), __builtin_bit_cast(uint32_t, t[w + 1]),
+                                __builtin_bit_cast(uint32_t, t[w + 2]), __builtin_bit_cast(uint32_t, t[w + 3])};
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, v4), t_rsrc, (int)(off + w * 4),
+                                                     0, kPolicyStreamStore);
+            }
           } else {
 #pragma unroll
-            for (int w = 0; w < GS; ++w) tb[g * NR + jr0 + w] = t[w];
+            for (int w = 0; w < GS; ++w)
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, t[w]), t_rsrc, (int)(off + w * 4), 0,
+                                                    kPolicyStreamStore);
           }
         }
         // Every block has a valid row, so the group's max is finite for
@@ -445,18 +456,25 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
 #pragma unroll
     for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, o_off + g * D * 2, pack_f16x8(acc[g]));
   } else {
-    if (!head_ok) return;
+    // Partial outputs [Hq][nchunks][D] of this batch, read by the combine
+    // pass right after: default-policy stores keep them in the caches
+    // (non-temporal ones measured 4-9% slower overall).
+    const uint32_t part_bytes = (uint32_t)a.nchunks * D * 4u;
+    const __amdgpu_buffer_rsrc_t p_rsrc =
+        make_rsrc(a.opart + (uint64_t)b * hq * a.nchunks * D, (uint32_t)hq * part_bytes);
+    const uint32_t p_off = head_ok ? (uint32_t)hk * G * part_bytes + (c * D + r * 8) * 4u : kLaneOutOfRange;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float* dst = a.opart + (((uint64_t)b * hq + hk * G + g) * a.nchunks + c) * D + r * 8;
       u32x4 lo, hi;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         lo[i] = __builtin_bit_cast(uint32_t, acc[g][i]);
         hi[i] = __builtin_bit_cast(uint32_t, acc[g][4 + i]);
       }
-      *reinterpret_cast<u32x4*>(dst) = lo;
-      *reinterpret_cast<u32x4*>(dst + 4) = hi;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, lo), p_rsrc, (int)(p_off + g * part_bytes),
+                                             0, kPolicyDefault);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, hi), p_rsrc,
+                                             (int)(p_off + g * part_bytes + 16), 0, kPolicyDefault);
     }
   }
 }
