@@ -526,14 +526,14 @@ __global__ __launch_bounds__(256) void splitkv_combine_kernel(SplitArgs a) {
 }
 
 // Many chunks: one THREADS-thread block per (batch, query head); thread t
-// sums dims [8*(t % (D/8)), +8) over chunks c = t / (D/8) + k * CG (U chunks
-// in flight), then the CG partial sums of each dim group are added in order
-// through LDS.
+// sums dims [8*(t % (D/8)), +8) over chunks c = t / (D/8) + k * CG (U = 8
+// chunks in flight), then the CG partial sums of each dim group are added in
+// order through LDS.
 template <int D, int THREADS>
 __global__ __launch_bounds__(THREADS) void splitkv_combine_block_kernel(SplitArgs a) {
   constexpr int DG = D / 8;
   constexpr int CG = THREADS / DG;
-  constexpr int U = 4;
+  constexpr int U = 8;
   __shared__ float part[CG][D];
   const uint64_t head = blockIdx.x;  // b * Hq + h
   const int t = threadIdx.x;
