@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(_HERE, "libfmha_decode.so")
 # Every symbol include/fmha_decode.h declares.
 EXPORTED = (
     "fmha_decode_fwd",
+    "fmha_decode_fwd_fp32_weights",
     "fmha_decode_fwd_uniform",
     "fmha_decode_fwd_strided",
     "fmha_decode_fwd_paged",
@@ -37,6 +38,8 @@ def load():
     vp, i32, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
     lib.fmha_decode_fwd.restype = ctypes.c_int
     lib.fmha_decode_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_fwd_fp32_weights.restype = ctypes.c_int
+    lib.fmha_decode_fwd_fp32_weights.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_uniform.restype = ctypes.c_int
     lib.fmha_decode_fwd_uniform.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
     i64 = ctypes.c_int64

@@ -94,9 +94,9 @@ size_t lds_reserve_kernel(int waves) {
   return lds_reserve_for(waves, lds_per_cu(), static_lds<KERNEL>());
 }
 
-template <int D, int G, int LAYOUT, int SB>
+template <int D, int G, int LAYOUT, int SB, bool PF32>
 hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB>;
+  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
@@ -104,38 +104,39 @@ hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream)
 
 // sb: 0 = lengths from a.lens (bucket picked per wave), else the uniform
 // length's power-of-two bucket.  The paged layout always reads lengths.
-template <int D, int G, int LAYOUT>
+// PF32: fp32 softmax weights (instantiated for the packed layout only).
+template <int D, int G, int LAYOUT, bool PF32>
 hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
   if constexpr (LAYOUT == fmha_decode::kLayoutPaged) {
-    return launch_one<D, G, LAYOUT, 0>(a, w, stream);
+    return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
   } else {
     switch (sb) {
-      case 0: return launch_one<D, G, LAYOUT, 0>(a, w, stream);
-      case 1: return launch_one<D, G, LAYOUT, 1>(a, w, stream);
-      case 2: return launch_one<D, G, LAYOUT, 2>(a, w, stream);
-      case 4: return launch_one<D, G, LAYOUT, 4>(a, w, stream);
-      case 8: return launch_one<D, G, LAYOUT, 8>(a, w, stream);
-      default: return launch_one<D, G, LAYOUT, 16>(a, w, stream);
+      case 0: return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
+      case 1: return launch_one<D, G, LAYOUT, 1, PF32>(a, w, stream);
+      case 2: return launch_one<D, G, LAYOUT, 2, PF32>(a, w, stream);
+      case 4: return launch_one<D, G, LAYOUT, 4, PF32>(a, w, stream);
+      case 8: return launch_one<D, G, LAYOUT, 8, PF32>(a, w, stream);
+      default: return launch_one<D, G, LAYOUT, 16, PF32>(a, w, stream);
     }
   }
 }
 
-template <int D, int LAYOUT>
+template <int D, int LAYOUT, bool PF32>
 hipError_t launch_group(const DecodeArgs& a, int g, int sb, int w, hipStream_t stream) {
   switch (g) {
-    case 1: return launch_bucket<D, 1, LAYOUT>(a, sb, w, stream);
-    case 2: return launch_bucket<D, 2, LAYOUT>(a, sb, w, stream);
-    case 4: return launch_bucket<D, 4, LAYOUT>(a, sb, w, stream);
-    default: return launch_bucket<D, 8, LAYOUT>(a, sb, w, stream);
+    case 1: return launch_bucket<D, 1, LAYOUT, PF32>(a, sb, w, stream);
+    case 2: return launch_bucket<D, 2, LAYOUT, PF32>(a, sb, w, stream);
+    case 4: return launch_bucket<D, 4, LAYOUT, PF32>(a, sb, w, stream);
+    default: return launch_bucket<D, 8, LAYOUT, PF32>(a, sb, w, stream);
   }
 }
 
-template <int LAYOUT>
+template <int LAYOUT, bool PF32 = false>
 hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStream_t stream) {
   switch (d) {
-    case 64: return launch_group<64, LAYOUT>(a, g, sb, w, stream);
-    case 128: return launch_group<128, LAYOUT>(a, g, sb, w, stream);
-    default: return launch_group<256, LAYOUT>(a, g, sb, w, stream);
+    case 64: return launch_group<64, LAYOUT, PF32>(a, g, sb, w, stream);
+    case 128: return launch_group<128, LAYOUT, PF32>(a, g, sb, w, stream);
+    default: return launch_group<256, LAYOUT, PF32>(a, g, sb, w, stream);
   }
 }
 
@@ -190,8 +191,10 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
 }
 
 // Fills the layout-independent fields, picks the wave cap and launches.
-// rows_hint: KV rows per batch used to size the per-CU wave cap.
-int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows_hint) {
+// rows_hint: KV rows per batch used to size the per-CU wave cap; fp32_weights
+// selects the fp32-weight kernels (packed layout only).
+int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows_hint,
+           bool fp32_weights = false) {
   const int heads_per_wave = kWaveSize / (dq / 8);
   const int64_t upb = (a.num_heads_kv + heads_per_wave - 1) / heads_per_wave;
   const int64_t units = upb * batch;
@@ -204,7 +207,10 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   switch (layout) {
-    case fmha_decode::kLayoutPacked: err = launch_dim<fmha_decode::kLayoutPacked>(a, dq, g, sb, w, s); break;
+    case fmha_decode::kLayoutPacked:
+      err = fp32_weights ? launch_dim<fmha_decode::kLayoutPacked, true>(a, dq, g, sb, w, s)
+                         : launch_dim<fmha_decode::kLayoutPacked>(a, dq, g, sb, w, s);
+      break;
     case fmha_decode::kLayoutStrided: err = launch_dim<fmha_decode::kLayoutStrided>(a, dq, g, sb, w, s); break;
     default: err = launch_dim<fmha_decode::kLayoutPaged>(a, dq, g, sb, w, s); break;
   }
@@ -365,6 +371,24 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
+}
+
+extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                            const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                                            int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                                            int32_t head_dim_kv, float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
+  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.lens = cu_seqlens_kv;
+  a.row_stride = num_heads_kv * head_dim_q;
+  a.head_stride = head_dim_q;
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint, true);
 }
 
 extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,

@@ -28,7 +28,10 @@
 // (15 exchanges for 16 scores instead of 64 for independent butterflies).
 // Softmax runs on that distribution; the bf16 weights go through 128 bytes of
 // LDS per head so every lane of the head sees all of them; P.V packs row pairs
-// with v_perm_b32 and accumulates with v_dot2_f32_bf16.
+// with v_perm_b32 and accumulates with v_dot2_f32_bf16.  With fp32 weights
+// (PF32, the semantics of the reference's fmha_vectorized_fma) they take 64
+// bytes of LDS per query head and P.V is one fused multiply-add per element
+// and row, rows in order.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -297,7 +300,7 @@ __device__ __forceinline__ u32x4 pack_f16x8(const float (&a)[8]) {
 // ---------------------------------------------------------------------------
 // One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX, int LAYOUT>
+template <int D, int G, int SMAX, int LAYOUT, bool PF32>
 __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, const KVSpan& kv, int hk,
                                             bool head_ok, int lane, uint16_t* lds_p) {
   constexpr int LPH = D / 8;                 // lanes per KV head
@@ -406,39 +409,66 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
     for (int w = 0; w < GS; ++w) p[h0 + w] = (sum > 0.0f) ? (t[w] / sum) : 0.0f;
   }
 
-  // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
-  uint16_t* lds_head = lds_p + hkl * VP;
-#pragma unroll
-  for (int w = 0; w < W; ++w) {
-    const int vi = blk * W + w;
-    const int g = vi / SMAX;
-    const int j = vi % SMAX;
-    lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- P.V over row pairs ----
-  constexpr int NP = (SMAX + 1) / 2;
-  const uint32_t* lds_pairs = reinterpret_cast<const uint32_t*>(lds_head);
-  uint32_t pp[G][NP];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int jp = 0; jp < NP; ++jp) {
-      uint32_t w2 = lds_pairs[g * (kMaxSeq / 2) + jp];
-      if constexpr (SMAX == 1) w2 &= 0xffffu;  // slot 1 is not part of this bucket
-      pp[g][jp] = w2;
-    }
-  }
-
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-  accumulate_pv<G, SMAX>(vr, pp, acc);
+
+  if constexpr (!PF32) {
+    // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
+    uint16_t* lds_head = lds_p + hkl * VP;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int vi = blk * W + w;
+      const int g = vi / SMAX;
+      const int j = vi % SMAX;
+      lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- P.V over row pairs ----
+    constexpr int NP = (SMAX + 1) / 2;
+    const uint32_t* lds_pairs = reinterpret_cast<const uint32_t*>(lds_head);
+    uint32_t pp[G][NP];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int jp = 0; jp < NP; ++jp) {
+        uint32_t w2 = lds_pairs[g * (kMaxSeq / 2) + jp];
+        if constexpr (SMAX == 1) w2 &= 0xffffu;  // slot 1 is not part of this bucket
+        pp[g][jp] = w2;
+      }
+    }
+    accumulate_pv<G, SMAX>(vr, pp, acc);
+  } else {
+    // ---- fp32 weights -> LDS slot [hkl][g*16 + j] (4 bytes each) ----
+    float* lds_head = reinterpret_cast<float*>(lds_p) + hkl * VP;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int vi = blk * W + w;
+      lds_head[(vi / SMAX) * kMaxSeq + vi % SMAX] = p[w];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- P.V row by row in row order, one fused multiply-add per element ----
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < SMAX; ++j) {
+        const float w = lds_head[g * kMaxSeq + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t x = vr[j][i];
+          acc[g][2 * i] = __builtin_fmaf(w, __builtin_bit_cast(float, x << 16), acc[g][2 * i]);
+          acc[g][2 * i + 1] = __builtin_fmaf(w, __builtin_bit_cast(float, x & 0xffff0000u), acc[g][2 * i + 1]);
+        }
+      }
+    }
+  }
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
@@ -506,12 +536,17 @@ __device__ __forceinline__ bool batch_span(const DecodeArgs& a, uint32_t b, KVSp
 // SB = 1, 2, 4, 8, 16: every batch has exactly seqlen_uniform <= SB rows.
 // SB = 0: lengths come from a.lens and each wave picks the smallest bucket
 // that holds its batch.
-template <int D, int G, int LAYOUT, int SB>
+// PF32: softmax weights kept in fp32 and P.V as one fused multiply-add per
+// row in row order (the semantics of the reference's fmha_vectorized_fma,
+// fmha_vectorized_fma_kernel.hpp:243-296); otherwise weights rounded to bf16
+// (the reference CPU loop and fmha_mfma_4x4x4).
+template <int D, int G, int LAYOUT, int SB, bool PF32 = false>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
   constexpr int VP = G * kMaxSeq;
-  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP];
+  constexpr int WB = PF32 ? 2 : 1;  // 16-bit LDS words per weight
+  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP * WB];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -522,7 +557,7 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
   const uint32_t hg = unit - b * upb;
   const int hk = (int)hg * HPW + lane / LPH;
   const bool head_ok = hk < a.num_heads_kv;
-  uint16_t* lds_wave = lds_p + wave * HPW * VP;
+  uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
 
   KVSpan kv;
   const bool length_ok = batch_span<D, LAYOUT, SB != 0>(a, b, kv);
@@ -532,19 +567,19 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
     return;
   }
   if constexpr (SB != 0) {
-    decode_unit<D, G, SB, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+    decode_unit<D, G, SB, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
   } else {
     const int S = kv.S;
     if (S <= 1) {
-      decode_unit<D, G, 1, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 1, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 2) {
-      decode_unit<D, G, 2, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 2, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 4) {
-      decode_unit<D, G, 4, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 4, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 8) {
-      decode_unit<D, G, 8, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 8, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else {
-      decode_unit<D, G, 16, LAYOUT>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 16, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     }
   }
 }

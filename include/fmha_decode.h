@@ -81,6 +81,24 @@ int fmha_decode_fwd(void* stream,
                     float softmax_scale);
 
 /*
+ * fmha_decode_fwd with the softmax weights kept in fp32: P_j is the fp32
+ * quotient exp(s_j*scale - max) / sum, not rounded to bf16, and
+ * O[b,h,d] = fp16(acc) with acc = fma(P_j, V_j[d], acc) for j = 0, 1, ...
+ * in row order.  These are the semantics of the reference's other VALU
+ * kernel, fmha_vectorized_fma (fmha_vectorized_fma_kernel.hpp:69-83 for its
+ * parameter list, :243-296 for the weights and the accumulation), which has
+ * no launch helper in the reference; the wired-in fmha_mfma_4x4x4 and the
+ * reference CPU check round the weights to bf16 (fmha_decode_fwd).  Same
+ * arguments, layouts, checks and errors as fmha_decode_fwd.
+ */
+int fmha_decode_fwd_fp32_weights(void* stream,
+                                 const void* Q, const void* K, const void* V, void* O,
+                                 const int32_t* cu_seqlens_kv,
+                                 int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                 int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                 float softmax_scale);
+
+/*
  * Uniform-length decode attention: every batch has seqlen_kv KV rows, K and V
  * are [batch, seqlen_kv, num_heads_kv, head_dim] (the packed layout above with
  * cu[b] = b * seqlen_kv), and no cu_seqlens array is read.  This is the

@@ -32,7 +32,8 @@ def lib():
 
 def test_exports_every_declared_function(lib):
     names = header_functions()
-    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_uniform", "fmha_decode_fwd_strided",
+    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_uniform",
+                          "fmha_decode_fwd_strided",
                           "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
                           "fmha_decode_fwd_splitkv", "fmha_decode_error_string",
                           "fmha_decode_last_error_detail", "fmha_decode_version"}
@@ -55,6 +56,14 @@ def fwd(lib, **kw):
     a.update(kw)
     return lib.fmha_decode_fwd(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"], a["hq"],
                                a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
+def fwd32(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_fp32_weights(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"],
+                                            a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
 
 
 def uni(lib, **kw):
@@ -187,9 +196,26 @@ def test_splitkv_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(batch=-1), BAD, "batch"),
+    (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
+    (dict(sq=2), BAD, "seqlen_q"),
+    (dict(dq=96, dkv=96), BAD, "64, 128 or 256"),
+    (dict(scale=float("nan")), BAD, "finite"),
+    (dict(v=None), BAD, "non-null"),
+    (dict(q=Q + 4), BAD, "aligned"),
+    (dict(cu=None), BAD, "cu_seqlens_kv"),
+    (dict(cu=CU + 1), BAD, "cu_seqlens_kv"),
+])
+def test_fp32_weights_rejects(lib, kw, code, needle):
+    assert fwd32(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
 def test_batch_zero_is_a_noop(lib):
     # Nothing is launched and no pointer is needed for an empty batch.
     assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
+    assert fwd32(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
     assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
     assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0

@@ -4,9 +4,11 @@ oracle/_ref, on the same inputs as this library's kernel.
 North-star parity: the new kernel must agree with the CPU reference and with
 the existing GPU kernel.  These tests run the wired-in fmha_mfma_4x4x4
 (fmha_mfma_4x4x4_kernel.hpp:370-389) and fmha_vectorized_fma
-(fmha_vectorized_fma_kernel.hpp:69-331) and check all three against the
-oracle gate, and time all three on the same stream (the timings are printed;
-profiles/ keeps the summary).
+(fmha_vectorized_fma_kernel.hpp:69-331) beside this library's bf16-weight
+and fp32-weight paths, check each against the oracle gate (the fp32-weight
+path against the oracle's fp32-weight loop and against fmha_vectorized_fma,
+whose semantics it has), and time all four on the same stream (the timings
+are printed; profiles/ keeps the summary).
 
 The reference kernels are only launched inside the shapes where their
 indexing stays in bounds: Hq == Hkv (they index K/V with the query head,
@@ -54,11 +56,12 @@ def _launch_ref(name, q, k, v, o, cu, cu_h, B, H, D):
     assert rc == 0, f"{name} launch failed: {rc}"
 
 
-def _launch_ours(q, k, v, o, cu, B, H, D):
+def _launch_ours(q, k, v, o, cu, B, H, D, fp32_weights=False):
     import torch
     import fmha_amd
-    fmha_amd.launch_fmha_decode(torch.cuda.current_stream().cuda_stream, q.data_ptr(), k.data_ptr(),
-                                v.data_ptr(), o.data_ptr(), cu.data_ptr(), B, H, H, 1, D, D, default_scale(D))
+    launch = fmha_amd.launch_fmha_decode_fp32_weights if fp32_weights else fmha_amd.launch_fmha_decode
+    launch(torch.cuda.current_stream().cuda_stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+           cu.data_ptr(), B, H, H, 1, D, D, default_scale(D))
 
 
 def _bits(t):
@@ -101,10 +104,10 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
     q, k, v, cu, cu_h = _inputs(B, H, D, seqlens, seed=B + H + D)
     outs = {}
     times = {}
-    for name in ("ours",) + REF_KERNELS:
+    for name in ("ours", "ours_fp32_weights") + REF_KERNELS:
         o = torch.zeros(B, H, 1, D, device=q.device, dtype=torch.float16)
-        if name == "ours":
-            run = lambda: _launch_ours(q, k, v, o, cu, B, H, D)
+        if name.startswith("ours"):
+            run = lambda o=o, f=(name != "ours"): _launch_ours(q, k, v, o, cu, B, H, D, fp32_weights=f)
         else:
             run = lambda name=name: _launch_ref(name, q, k, v, o, cu, cu_h, B, H, D)
         run()
@@ -123,11 +126,18 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
     cus = np.concatenate([[0], np.cumsum(seqlens[sel])]).astype(np.int32)
     r, slack = oracle.decode(_bits(q.view(B, H, D)[idx]), _bits(ks), _bits(vs), cus, H, H, D,
                              default_scale(D), with_slack=True)
+    r32, _ = oracle.decode(_bits(q.view(B, H, D)[idx]), _bits(ks), _bits(vs), cus, H, H, D, default_scale(D),
+                           p_mode=1)
     for name, o in outs.items():
         st = oracle.compare(_bits(o.view(B, H, D)[idx]), r, slack)
         print(f"{label}: {name} vs oracle: {st}", flush=True)
         if name == "ours":
             assert_pass(st, f"{label} ours")
+        elif name == "ours_fp32_weights":
+            # fp32 weights: checked against the oracle's fp32-weight loop, no slack
+            st32 = oracle.compare(_bits(o.view(B, H, D)[idx]), r32)
+            print(f"{label}: {name} vs fp32-weight oracle: {st32}", flush=True)
+            assert_pass(st32, f"{label} ours, fp32 weights")
         else:
             # the reference's own rule (fmha_host.cpp:260) is what its kernels promise
             assert st["ref_rule_fails"] == 0 and st["nonfinite"] == 0, f"{label} {name}: {st}"
@@ -136,3 +146,8 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
                         _bits(outs["ref_launch_mfma_4x4x4"].view(B, H, D)[idx]), slack)
     print(f"{label}: ours vs fmha_mfma_4x4x4: {st}", flush=True)
     assert st["ref_rule_fails"] == 0
+    # the fp32-weight path against fmha_vectorized_fma, whose semantics it has
+    st = oracle.compare(_bits(outs["ours_fp32_weights"].view(B, H, D)[idx]),
+                        _bits(outs["ref_launch_vectorized_fma"].view(B, H, D)[idx]))
+    print(f"{label}: ours (fp32 weights) vs fmha_vectorized_fma: {st}", flush=True)
+    assert_pass(st, f"{label} ours (fp32 weights) vs fmha_vectorized_fma")
