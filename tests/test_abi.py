@@ -281,3 +281,30 @@ def test_error_detail_is_per_thread(lib):
     for t in threads:
         t.join()
     assert not errors, errors[:3]
+
+
+def test_header_is_plain_c():
+    """include/fmha_decode.h is a C header: a C99 translation unit that calls
+    every entry point compiles with gcc (declarations only, nothing runs)."""
+    import subprocess
+    import tempfile
+    src = ('#include "fmha_decode.h"\n'
+           'int f(void* s, const void* q, const void* k, const void* v, void* o, const int32_t* cu,\n'
+           '      void* ws) {\n'
+           '  int rc = fmha_decode_fwd(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_fp32_weights(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_uniform(s, q, k, v, o, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_strided(s, q, k, v, o, cu, 16, 32768, 2048, 128, 1, 16, 16, 1, 128, 128,\n'
+           '                                0.088f);\n'
+           '  rc |= fmha_decode_fwd_paged(s, q, k, v, o, cu, 4, cu, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  size_t n = fmha_decode_splitkv_workspace_size(1, 16, 16, 100, 128);\n'
+           '  rc |= fmha_decode_fwd_splitkv(s, q, k, v, o, cu, 100, 1, 16, 16, 1, 128, 128, 0.088f, ws, n);\n'
+           '  const char* t = fmha_decode_error_string(rc);\n'
+           '  const char* d = fmha_decode_last_error_detail();\n'
+           '  return rc + fmha_decode_version() + (t == d);\n}\n')
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "t.c")
+        open(p, "w").write(src)
+        r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I",
+                            os.path.join(ROOT, "include"), p], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr

@@ -67,3 +67,28 @@ def test_closer_to_float64_than_bf16_weights():
     e32, e16 = np.abs(o32 - t).mean(), np.abs(o16 - t).mean()
     print(f"mean |error| vs float64: fp32 weights {e32:.3g}, bf16 weights {e16:.3g}", flush=True)
     assert e32 < 0.8 * e16
+
+
+def test_poisoned_neighbours():
+    """A batch's output does not depend on its neighbours' rows (NaN there)."""
+    H, D = 16, 128
+    seqlens = np.array([16, 7, 16], np.int32)
+    q, k, v, cu = make_inputs(3, H, H, D, seqlens, seed=713)
+    alone = _run(q[1:2], k[cu[1]:cu[2]], v[cu[1]:cu[2]], np.array([0, 7], np.int32), H, H, D)
+    nan = np.uint16(0x7FC0)
+    kp, vp = k.copy(), v.copy()
+    for t in (kp, vp):
+        t[: cu[1]] = nan
+        t[cu[2]:] = nan
+    o = _run(q, kp, vp, cu, H, H, D).reshape(3, H, D)
+    assert np.array_equal(o[1], alone.reshape(H, D))
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(3, 3), (12, 3), (40, 5), (56, 7)])
+@pytest.mark.parametrize("D", [64, 256])
+def test_ragged_head_counts(Hq, Hkv, D):
+    seqlens = np.random.default_rng(Hq + Hkv + D).integers(0, 17, size=19).astype(np.int32)
+    q, k, v, cu = make_inputs(19, Hq, Hkv, D, seqlens, seed=714 + Hq + D)
+    o = _run(q, k, v, cu, Hq, Hkv, D)
+    r, _ = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), p_mode=1)
+    assert_pass(oracle.compare(o.reshape(r.shape), r), f"fp32 weights Hq={Hq} Hkv={Hkv} D={D}")
