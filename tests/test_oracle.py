@@ -182,6 +182,51 @@ def test_dominant_key_is_one_hot():
     assert np.array_equal(o[0], oracle.f32_to_f16(_f32(v[6])))
 
 
+# ------------------------------------------- fp32 weights (p_mode=1): pins
+# The fp32-weight loop (the numerics of fmha_vectorized_fma_kernel.hpp:243-296)
+# keeps the weights unrounded; these checks would catch a stray bf16 rounding,
+# a dropped normalisation or a wrong accumulation order.
+@pytest.mark.parametrize("S", [2, 3, 5, 7, 16])
+def test_fp32_weights_zero_query_is_exact_uniform(S):
+    q, k, v, cu = make_inputs(2, 4, 4, 128, [S, S], seed=40 + S)
+    q[:] = 0
+    o, _ = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128), p_mode=1)
+    w = np.float32(1.0) / np.float32(S)          # exp(0) / S, not rounded to bf16
+    for b in range(2):
+        acc = np.zeros((4, 128), np.float32)
+        for j in range(S):                       # fp32, in row order
+            acc = acc + w * _f32(v[cu[b] + j])
+        assert np.array_equal(o[b], oracle.f32_to_f16(acc))
+
+
+def test_fp32_weights_one_row_and_dominant_key():
+    q, k, v, cu = make_inputs(5, 4, 2, 128, [1] * 5, seed=44)
+    o, _ = oracle.decode(q, k, v, cu, 4, 2, 128, default_scale(128), p_mode=1)
+    assert np.array_equal(o, oracle.f32_to_f16(np.repeat(_f32(v), 2, axis=1)))
+    D, S = 128, 16
+    q, k, v, cu = make_inputs(1, 2, 2, D, [S], seed=45)
+    q[:] = oracle.f32_to_bf16(np.ones((1, 2, D), np.float32))
+    k[:] = oracle.f32_to_bf16(np.full((S, 2, D), -1.0, np.float32))
+    k[9] = oracle.f32_to_bf16(np.full((2, D), 16.0, np.float32))
+    o, _ = oracle.decode(q, k, v, cu, 2, 2, D, default_scale(D), p_mode=1)
+    assert np.array_equal(o[0], oracle.f32_to_f16(_f32(v[9])))
+
+
+def test_fp32_weights_within_fp16_rounding_of_f64():
+    """Without the bf16 rounding of the weights the only sizeable error left
+    is the final fp16 rounding (2^-11 relative) plus fp32 noise."""
+    seqlens = oracle.generate_seqlens(64, 16)
+    q, k, v, cu = make_inputs(64, 8, 4, 128, seqlens, seed=46)
+    o, _ = oracle.decode(q, k, v, cu, 8, 4, 128, default_scale(128), p_mode=1)
+    t = oracle.decode_f64(q, k, v, cu, 8, 4, 128, default_scale(128))
+    of = oracle.f16_to_f32(o).astype(np.float64)
+    assert np.all(np.abs(of - t) <= 2.0 ** -11 * np.abs(t) + 1e-5)
+    ob, _ = oracle.decode(q, k, v, cu, 8, 4, 128, default_scale(128), p_mode=0)
+    e32 = np.abs(of - t).mean()
+    e16 = np.abs(oracle.f16_to_f32(ob).astype(np.float64) - t).mean()
+    assert e32 < 0.5 * e16
+
+
 # ---------------------------------------------------------------- invariants
 def test_gqa_equals_mha_on_repeated_kv():
     seqlens = oracle.generate_seqlens(20, 16)
