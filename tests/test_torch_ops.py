@@ -41,6 +41,13 @@ def test_op_matches_direct_call_and_oracle():
     r, slack = oracle.decode(q, k, v, cu, 8, 4, 128, default_scale(128), with_slack=True)
     bits = o_op.view(torch.int16).cpu().numpy().view(np.uint16)
     assert_pass(oracle.compare(bits, r, slack), "torch op")
+    # fp32 weights through the op
+    o32_op = torch.ops.fmha_amd.decode(qd, kd, vd, cud, -1, 0.0, True)
+    o32_dir = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, fp32_weights=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o32_op.view(torch.int16), o32_dir.view(torch.int16))
+    r32, _ = oracle.decode(q, k, v, cu, 8, 4, 128, default_scale(128), p_mode=1)
+    assert_pass(oracle.compare(o32_op.view(torch.int16).cpu().numpy().view(np.uint16), r32), "torch op fp32")
 
 
 @pytest.mark.gpu
