@@ -21,7 +21,8 @@ Prints one JSON line:
   cpu_baseline  the reference's own CPU loop (fmha_host.cpp:158-284, built from
                 /root/reference into oracle/_ref) -- or the restated oracle
                 when that build is absent -- timed single-threaded on this
-                host over a bounded sample of the same workload.
+                host over a bounded sample of the same workload, plus the
+                restated loop on up to 16 host cores (port_all_cores).
 """
 import argparse
 import contextlib
@@ -98,6 +99,14 @@ def cpu_baseline(q, k, v, o, B, Hq, Hkv, S, D, scale, max_batches):
         "us_per_call_full_batch": dt * 1e6 * B / nb,
     }
     out.update(extra)
+    # The same sample through the restated loop (oracle/), OpenMP over batches
+    # on the host's cores (at most 16, the GPU box's share).
+    threads = max(1, min(16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    oracle.decode(qh, kh, vh, cu, Hq, Hkv, D, scale, nthreads=threads)
+    dt_mt = time.perf_counter() - t0
+    out["port_all_cores"] = {"value": nbytes / dt_mt / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+                             "seconds": round(dt_mt, 3), "us_per_call_full_batch": dt_mt * 1e6 * B / nb}
     return out
 
 
