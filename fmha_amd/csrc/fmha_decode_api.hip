@@ -16,6 +16,7 @@
 
 #include "fmha_decode.h"
 #include "fmha_decode_kernel.hpp"
+#include "fmha_decode_onepass.hpp"
 #include "fmha_decode_splitkv.hpp"
 
 namespace {
@@ -296,8 +297,37 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
 constexpr int kSplitScoresWavesPerCU = 8;
 constexpr int kSplitPvWavesPerCU = 8;
 
+// Rows longer than 16 go through one pass (onepass_decode_kernel: one wave
+// per batch and head group, no workspace traffic, one launch) when there are
+// at least 512 such units and the row's scores and weights fit the wave's
+// LDS budget; otherwise through the four split-KV launches.  Measured
+// (µs, split -> one pass, 8 waves per CU): B=2048 Hq=32 Hkv=8 S=128 201 ->
+// 171; B=4096 S=64 206 -> 178; B=16384 S=24 327 -> 296; B=256 S=256 (512
+// units) 69 -> 58; B=128 S=256 (256 units) 43 -> 49 and B=16 S=256 23 -> 49,
+// where a wave's walk over its row outlasts split-KV's shorter waves.
+constexpr int64_t kOnepassMinUnits = 512;
+constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
+constexpr int kOnepassWavesPerCU = 8;
+
+template <int D, int G>
+bool onepass_fits(const SplitArgs& a) {
+  return (int64_t)a.batch * a.units_per_batch >= kOnepassMinUnits &&
+         fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
+}
+
+template <int D, int G>
+hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G>;
+  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
+  const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
+  const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
+  hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), need > cap ? need : cap, stream, a);
+  return hipGetLastError();
+}
+
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
+  if (onepass_fits<D, G>(a)) return launch_onepass_dg<D, G>(a, stream);
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
   constexpr int NB = 2;                // 16-row blocks per scores wave
   const uint32_t upb = (uint32_t)a.units_per_batch;
@@ -517,6 +547,17 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
                   plan.total);
   if (plan.units * plan.nblk > (int64_t)INT32_MAX || (int64_t)batch * num_heads_q > (int64_t)INT32_MAX)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch * heads * blocks too large");
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
+    // Rows that fit the short kernel take it (same numerics, lengths above
+    // max_seqlen_kv give NaN there too); the workspace goes unused.
+    DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+    d.lens = cu_seqlens_kv;
+    d.row_stride = num_heads_kv * head_dim_q;
+    d.head_stride = head_dim_q;
+    d.max_rows = max_seqlen_kv;
+    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
+                  max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint);
+  }
   char* ws = static_cast<char*>(workspace);
   SplitArgs a = {};
   a.q = static_cast<const uint16_t*>(Q);

@@ -1,0 +1,226 @@
+// fmha_decode_onepass.hpp -- single-pass decode attention for KV lengths
+// beyond 16 when there are enough (batch, KV-head group) units to fill the
+// GPU without splitting rows, gfx950.
+//
+// Same semantics as the split-KV path: fp32 scores, global max and sum,
+// weights rounded to bf16 after normalisation (fmha_host.cpp:209-226), fp32
+// P.V, one fp16 rounding.  One wave per (batch, group of HPW KV heads), as in
+// the short kernel, in three phases:
+//
+//   1. K: 16-row sub-blocks with two register sets (two sub-blocks in flight,
+//      a set refilled as soon as it is scored); dot products and the
+//      transposing butterfly of the short kernel; scaled scores -> LDS.  The
+//      first two V sub-blocks are requested at the end of this phase.
+//   2. softmax in the wave: per (KV head, query head) the max and the sum of
+//      exponentials over the row, read back from LDS by the head's lanes;
+//      bf16 weights -> LDS.
+//   3. V: sub-blocks of NRV rows with two register sets, refilled as they
+//      are consumed; packed bf16 weight pairs from LDS, dot2 accumulation;
+//      fp16 O.
+//
+// K and V are each read once and nothing else touches memory (no workspace),
+// in one launch.  LDS per wave: HPW * G * SP * 6 bytes (fp32 scores and bf16
+// weights for SP = the row bound rounded up to 32).  Both loops run an even
+// number of sub-blocks with no branch inside, so every wait is a fixed count:
+// an odd row's last sub-block pairs with one past its end, whose requests
+// read 0 without memory access, whose scores land in LDS padding the softmax
+// never reads and whose weights are 0.
+#pragma once
+
+#include "fmha_decode_splitkv.hpp"
+
+namespace fmha_decode {
+
+template <int D, int G>
+struct OnepassShape {
+  static constexpr int LPH = D / 8;
+  static constexpr int HPW = kWaveSize / LPH;
+  static constexpr int NRV = G >= 8 ? 8 : 16;  // V rows per sub-block (register budget)
+};
+
+// LDS row stride for a row bound of nblk 16-row blocks: an even number of
+// blocks, so the loops' paired sub-blocks always have room.
+constexpr int onepass_lds_rows(int nblk) { return (nblk + 1) / 2 * 2 * kSplitBlockRows; }
+
+// LDS bytes one wave needs for a row stride of sp.
+template <int D, int G>
+constexpr size_t onepass_lds_bytes(int sp) {
+  return (size_t)OnepassShape<D, G>::HPW * G * sp * 6;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs a) {
+  using P = OnepassShape<D, G>;
+  constexpr int LPH = P::LPH;
+  constexpr int HPW = P::HPW;
+  constexpr int NRV = P::NRV;
+  constexpr int NS = ilog2(LPH);
+  constexpr int NR = kSplitBlockRows;
+  constexpr int GH = G > 4 ? 4 : G;  // query heads scored per pass (partial sums per lane <= 64)
+  constexpr int VS = GH * NR;
+  constexpr int L = NS < ilog2(VS) ? NS : ilog2(VS);
+  constexpr int W = (VS >> NS) > 1 ? (VS >> NS) : 1;
+  constexpr int LPG = LPH / G;  // lanes per query head in the softmax phase
+  static_assert(LPG >= 1, "at most LPH query heads per KV head");
+  extern __shared__ __attribute__((aligned(16))) float onepass_lds[];
+
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t unit = blockIdx.x;
+  const uint32_t upb = (uint32_t)a.units_per_batch;
+  const uint32_t b = unit / upb;
+  if (b >= (uint32_t)a.batch) return;
+  const uint32_t hg = unit - b * upb;
+  const int hkl = lane / LPH;
+  const int r = lane % LPH;
+  const int hk = (int)hg * HPW + hkl;
+  const bool head_ok = hk < a.num_heads_kv;
+  const int hq = a.num_heads_q;
+  const int64_t base = a.cu[b];
+  const int S = a.cu[b + 1] - (int)base;
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+  if (S <= 0 || S > a.max_rows) {
+    // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+    const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+#pragma unroll
+    for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, fill);
+    return;
+  }
+  const int sp = onepass_lds_rows(a.nblk);  // LDS row stride
+  float* sc = onepass_lds + (size_t)hkl * G * sp;                                         // [G][sp] fp32
+  uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sp) + (size_t)hkl * G * sp;  // [G][sp]
+
+  const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
+  const uint64_t kv0 = (uint64_t)base * a.num_heads_kv * D;
+  // Ranges end at the batch's last row: later rows read 0 without access.
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + kv0, (uint32_t)S * row_bytes);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + kv0, (uint32_t)S * row_bytes);
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
+  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, qo_off + g * D * 2);
+
+  // ---- 1. scores of every row -> LDS ----
+  const int blkl = r >> (NS - L);
+  const bool writer = (r & ((1 << (NS - L)) - 1)) == 0;
+  const int nsub = ((S + NR - 1) / NR + 1) / 2 * 2;  // even
+  auto load_k = [&](u32x4 (&kr)[NR], int s) {
+#pragma unroll
+    for (int j = 0; j < NR; ++j) kr[j] = buffer_load16_nt(k_rsrc, kv_off + (uint32_t)(s * NR + j) * row_bytes);
+  };
+  auto score = [&](const u32x4 (&kr)[NR], int s) {
+#pragma unroll
+    for (int g0 = 0; g0 < G; g0 += GH) {
+      u32x4 qh[GH];
+#pragma unroll
+      for (int g = 0; g < GH; ++g) qh[g] = qv[g0 + g];
+      float x[VS];
+      partial_scores<GH, NR>(qh, kr, x);
+      TransposeReduce<LPH, VS, 0>::run(x, lane);
+      if (writer) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const int vi = blkl * W + w;
+          sc[(g0 + vi / NR) * sp + s * NR + vi % NR] = x[w] * a.scale;
+        }
+      }
+    }
+  };
+  {
+    // Two sub-blocks in flight: a register set is refilled as soon as it has
+    // been scored (past the row's end the refills read 0 without access).
+    // The scheduling barriers keep the compiler from interleaving a refill
+    // with the scoring of the other set, which would make it wait for both.
+    u32x4 ka[NR], kb[NR];
+    load_k(ka, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(kb, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int s = 0; s < nsub; s += 2) {
+      score(ka, s);
+      __builtin_amdgcn_sched_barrier(0);
+      load_k(ka, s + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      score(kb, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_k(kb, s + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // The first two V sub-blocks are requested before the softmax, which they
+  // do not depend on, so they arrive while it runs.
+  using VBuf = u32x4[NRV];
+  VBuf va, vb;
+  auto load_v = [&](u32x4 (&vr)[NRV], int s) {
+#pragma unroll
+    for (int j = 0; j < NRV; ++j) vr[j] = buffer_load16_nt(v_rsrc, kv_off + (uint32_t)(s * NRV + j) * row_bytes);
+  };
+  load_v(va, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_v(vb, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- 2. softmax per (KV head, query head): lane r takes query head
+  // r % G and rows r / G, r / G + LPG, ... ----
+  {
+    const int g = r % G;
+    const int j0 = r / G;
+    float* t = sc + g * sp;
+    float m = -__builtin_inff();
+    for (int j = j0; j < S; j += LPG) m = fmaxf(m, t[j]);
+#pragma unroll
+    for (int msk = G; msk < LPH; msk <<= 1) m = fmaxf(m, __shfl_xor(m, msk, kWaveSize));
+    float l = 0.0f;
+    for (int j = j0; j < S; j += LPG) {
+      const float e = expf(t[j] - m);
+      t[j] = e;
+      l += e;
+    }
+#pragma unroll
+    for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
+    uint16_t* p = pw + g * sp;
+    const int pad = (S + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
+    for (int j = j0; j < pad; j += LPG)
+      p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? t[j] / l : 0.0f)) : (uint16_t)0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- 3. P.V ----
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+  const int nsv = ((S + NRV - 1) / NRV + 1) / 2 * 2;  // even
+  auto pv = [&](const u32x4 (&vr)[NRV], int s) {
+    uint32_t pp[G][NRV / 2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint32_t* pairs = reinterpret_cast<const uint32_t*>(pw + g * sp + s * NRV);
+#pragma unroll
+      for (int jp = 0; jp < NRV / 2; ++jp) pp[g][jp] = pairs[jp];
+    }
+    accumulate_pv<G, NRV>(vr, pp, acc);
+  };
+  for (int s = 0; s < nsv; s += 2) {
+    pv(va, s);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(va, s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    pv(vb, s + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(vb, s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, pack_f16x8(acc[g]));
+}
+
+}  // namespace fmha_decode

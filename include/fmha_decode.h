@@ -168,6 +168,11 @@ int fmha_decode_fwd_paged(void* stream,
  * CPU loop (fmha_host.cpp:209-226) extended past its 16-row arrays; the
  * reference itself stops at 16 (fmha_mfma_4x4x4_kernel.hpp:179, README.md:233).
  *
+ * The library picks the kernels: the kernel of fmha_decode_fwd when
+ * max_seqlen_kv <= 16; one single-pass launch when there are at least 512
+ * (batch, KV-head group) waves and a row's scores fit the wave's LDS; else
+ * four split-KV launches (scores, statistics, P.V per chunk, combine).
+ *
  * The caller provides a device workspace of at least
  * fmha_decode_splitkv_workspace_size(batch, Hq, Hkv, max_seqlen_kv, head_dim)
  * bytes, 256-byte aligned; its contents on entry do not matter.  Calls that

@@ -60,16 +60,24 @@ def test_mid_block_count():
     _case(1, 32, 8, 128, np.array([20000], np.int32), 20000, seed=13, std=0.5)
 
 
-def test_short_lengths_match_short_path():
-    """Lengths <= 16 through split-KV agree with the oracle as the short path does."""
-    seqlens = oracle.generate_seqlens(300, 16)
-    _case(300, 16, 16, 128, seqlens, 16, seed=5)
+@pytest.mark.parametrize("max_len", [16, 5])
+def test_short_lengths_match_short_path(max_len):
+    """max_seqlen_kv <= 16 through the split-KV entry (the short kernel runs
+    it): oracle parity, and NaN for a batch longer than max_seqlen_kv."""
+    seqlens = np.minimum(oracle.generate_seqlens(300, 16), max_len).astype(np.int32)
+    _case(300, 16, 16, 128, seqlens, max_len, seed=5)
+    if max_len < 16:
+        bad = seqlens.copy()
+        bad[7] = max_len + 1
+        q, k, v, cu = make_inputs(300, 16, 16, 128, bad, seed=6)
+        o = oracle.f16_to_f32(_run(q, k, v, cu, 16, 16, 128, max_len).reshape(300, 16, 128))
+        assert np.all(np.isnan(o[7])) and np.all(np.isfinite(np.delete(o, 7, axis=0)))
 
 
 def test_many_batches_direct_path():
     """max length fits one chunk: the PV kernel writes O directly."""
-    seqlens = np.random.default_rng(3).integers(0, 41, size=2000).astype(np.int32)
-    _case(2000, 8, 8, 128, seqlens, 40, seed=6)
+    seqlens = np.random.default_rng(3).integers(0, 41, size=200).astype(np.int32)
+    _case(200, 8, 8, 128, seqlens, 40, seed=6)
 
 
 def test_one_long_sequence():
@@ -92,3 +100,50 @@ def test_bad_and_empty_lengths():
     r, slack = oracle.decode(q[:1], k[:20], v[:20], cu_from_seqlens([20]), H, H, D, default_scale(D),
                              with_slack=True, max_seqlen=25)
     assert_pass(oracle.compare(o[:1], r, slack), "batch 0")
+
+
+# Single-pass path (onepass_decode_kernel): taken by fmha_decode_fwd_splitkv
+# when batch * ceil(Hkv / (64 / (D/8))) >= 512 and the wave's scores and
+# weights (HPW * G * rows * 6 bytes, rows rounded up to 32) fit 40 KiB of LDS.
+def _onepass_taken(B, Hq, Hkv, D, max_len):
+    hpw = 64 // (D // 8)
+    units = B * ((Hkv + hpw - 1) // hpw)
+    sp = (max_len + 31) // 32 * 32
+    return units >= 512 and hpw * (Hq // Hkv) * sp * 6 <= 40 * 1024
+
+
+def test_split_path_still_covered():
+    """The split-KV cases above keep below the single-pass threshold."""
+    assert not _onepass_taken(6, 16, 16, 128, 2048) and not _onepass_taken(16, 32, 8, 128, 8192)
+    assert not _onepass_taken(1, 32, 8, 128, 40000) and not _onepass_taken(4, 16, 16, 256, 600)
+    assert not _onepass_taken(10, 16, 2, 64, 64) and not _onepass_taken(10, 32, 8, 128, 64)
+    assert not _onepass_taken(200, 8, 8, 128, 40)
+
+
+@pytest.mark.parametrize("D,B", [(64, 1024), (128, 512), (256, 256)])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_onepass_all_shapes(D, B, G):
+    Hkv, max_len = 16, 96
+    assert _onepass_taken(B, Hkv * G, Hkv, D, max_len)
+    seqlens = np.random.default_rng(D + G).integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hkv * G, Hkv, D, seqlens, max_len, seed=900 + D + G)
+
+
+def test_onepass_edge_lengths():
+    """Rows shorter than a head's lanes, on and next to the 16-row edges, the
+    row bound itself and an empty row, in one batch that takes the single
+    pass; an invalid length gives NaN for its batch only."""
+    import torch
+    B, Hq, Hkv, D, max_len = 2048, 32, 8, 128, 256
+    assert _onepass_taken(B, Hq, Hkv, D, max_len)
+    edge = np.array([0, 1, 2, 3, 15, 16, 17, 31, 32, 33, 47, 48, 49, 255, 256], np.int32)
+    seqlens = np.random.default_rng(31).integers(1, 64, size=B).astype(np.int32)
+    seqlens[: len(edge)] = edge
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=931)
+    bad = seqlens.copy()
+    bad[5] = max_len + 1
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, bad, seed=932)
+    o = oracle.f16_to_f32(_run(q, k, v, cu, Hq, Hkv, D, max_len).reshape(B, Hq, D))
+    assert np.all(np.isnan(o[5])) and np.all(np.isfinite(np.delete(o, 5, axis=0)))
+    assert np.all(o[0] == 0)
