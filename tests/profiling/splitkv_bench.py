@@ -21,8 +21,12 @@ import sys
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
 
+# Long rows over few sequences (split path), many sequences of 24-256 rows
+# (single pass; the last one below its threshold), and the 16-row headline
+# batch through this entry point (short kernel).
 SHAPES = [(64, 32, 8, 4096, 128), (8, 32, 8, 32768, 128), (256, 64, 8, 1024, 128), (1, 32, 8, 131072, 128),
-          (30720, 16, 16, 16, 128)]
+          (2048, 32, 8, 128, 128), (4096, 32, 8, 64, 128), (16384, 32, 8, 24, 128), (8192, 16, 16, 64, 128),
+          (512, 32, 8, 128, 128), (256, 32, 8, 256, 128), (128, 32, 8, 256, 128), (30720, 16, 16, 16, 128)]
 
 
 def main():
