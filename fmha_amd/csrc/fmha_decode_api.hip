@@ -328,6 +328,8 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
 template <int D, int G>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   if (onepass_fits<D, G>(a)) return launch_onepass_dg<D, G>(a, stream);
+  // The combine grid has one workgroup per (batch, query head, 32 dims).
+  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
   constexpr int NB = 2;                // 16-row blocks per scores wave
   const uint32_t upb = (uint32_t)a.units_per_batch;
@@ -366,9 +368,11 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
                        stream, a);
   } else if (a.nchunks <= 256) {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads * (D / 32)), dim3(256), 0,
+                       stream, a);
   } else {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads * (D / 32)), dim3(1024), 0,
+                       stream, a);
   }
   return hipGetLastError();
 }

@@ -525,49 +525,55 @@ __global__ __launch_bounds__(256) void splitkv_combine_kernel(SplitArgs a) {
   *reinterpret_cast<u32x4*>(a.o + head * D + d0) = out;
 }
 
-// Many chunks: one THREADS-thread block per (batch, query head); thread t
-// sums dims [8*(t % (D/8)), +8) over chunks c = t / (D/8) + k * CG (U = 8
-// chunks in flight), then the CG partial sums of each dim group are added in
-// order through LDS.
+// Many chunks: one THREADS-thread block per (batch, query head, slice of
+// 32 dims), so that a head's partials are read by D/32 CUs and every chunk's
+// slice is one 128-byte line.  Thread t sums dims [4*(t % 8), +4) of the
+// slice over chunks c = t / 8 + k * CG (U = 8 chunks in flight); then the CG
+// partial sums of each dim are added in order through LDS.
 template <int D, int THREADS>
 __global__ __launch_bounds__(THREADS) void splitkv_combine_block_kernel(SplitArgs a) {
-  constexpr int DG = D / 8;
-  constexpr int CG = THREADS / DG;
+  constexpr int SLICE = 32;
+  constexpr int NSL = D / SLICE;
+  constexpr int LPS = SLICE / 4;  // lanes per slice
+  constexpr int CG = THREADS / LPS;
   constexpr int U = 8;
-  __shared__ float part[CG][D];
-  const uint64_t head = blockIdx.x;  // b * Hq + h
+  __shared__ float part[CG][SLICE];
+  const uint64_t head = blockIdx.x / NSL;  // b * Hq + h
+  const int d0 = (int)(blockIdx.x - head * NSL) * SLICE;
   const int t = threadIdx.x;
-  const int dg = t % DG;
-  const int cg = t / DG;
+  const int dl = t % LPS;
+  const int cg = t / LPS;
   const uint64_t b = head / (uint64_t)a.num_heads_q;
   const int S = a.cu[b + 1] - a.cu[b];
   const bool bad = S < 0 || S > a.max_rows;
   const int n = bad ? 0 : (S + a.chunk_rows - 1) / a.chunk_rows;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const float* src = a.opart + head * a.nchunks * D + dg * 8;
+  float acc[4] = {0, 0, 0, 0};
+  const float* src = a.opart + head * a.nchunks * D + d0 + dl * 4;
   for (int c0 = cg; c0 < n; c0 += CG * U) {
-    u32x4 lo[U], hi[U];
+    u32x4 x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * CG < n ? c0 + u * CG : c0;
-      lo[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
-      hi[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D + 4);
+      x[u] = *reinterpret_cast<const u32x4*>(src + (uint64_t)c * D);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (c0 + u * CG < n) add8(acc, lo[u], hi[u]);
+      if (c0 + u * CG < n)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] += __builtin_bit_cast(float, (uint32_t)x[u][k]);
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) part[cg][dg * 8 + k] = acc[k];
+  for (int k = 0; k < 4; ++k) part[cg][dl * 4 + k] = acc[k];
   __syncthreads();
-  if (cg != 0) return;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
+  if (t >= SLICE / 8) return;
+  // Threads 0..3 each finish 8 dims of the slice: sum over the chunk groups
+  // in order, then one 16-byte fp16 store.
+  float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int g = 0; g < CG; ++g)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] += part[g][dg * 8 + k];
-  const u32x4 out = bad ? u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u} : pack_f16x8(acc);
-  *reinterpret_cast<u32x4*>(a.o + head * D + dg * 8) = out;
+    for (int k = 0; k < 8; ++k) o[k] += part[g][t * 8 + k];
+  const u32x4 out = bad ? u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u} : pack_f16x8(o);
+  *reinterpret_cast<u32x4*>(a.o + head * D + d0 + t * 8) = out;
 }
 
 }  // namespace fmha_decode
