@@ -7,13 +7,17 @@ drawn N(0,1) from a fixed seed, fp32 accumulation, fp16 output), with every
 input resident in HBM before the timed region.
 
 Prints one JSON line:
-  value         algorithmic TB/s of the whole timed region (bytes per call as
-                the reference counts them, fmha_host.cpp:428-430, times calls,
-                over the wall time between the first and last event);
+  value         algorithmic TB/s of the timed region: K back-to-back calls
+                between one HIP-event pair on the launch stream, as the
+                reference's harness times them (fmha_host.cpp:377-397); bytes
+                per call as the reference counts them (fmha_host.cpp:428-430);
   roofline      the kernel alone: algorithmic bytes per launch over the mean
-                of per-launch HIP-event durations on the launch stream, against
-                the 8 TB/s HBM peak; traffic = measured HBM bytes per launch
-                from the committed rocprofv3 counter summary, when present;
+                of per-launch HIP-event durations, from a second loop of K
+                calls, each between its own event pair on the launch stream
+                (those events add a few µs between launches, so they stay out
+                of the value loop), against the 8 TB/s HBM peak; traffic =
+                measured HBM bytes per launch from the committed rocprofv3
+                counter summary, when present;
   rotated_inputs  the same calls over --rotate input/output sets used in
                 turn (no call finds Q or O of the previous call in the MALL);
                 the timed loop above reuses one set, as the reference's
@@ -153,17 +157,33 @@ def main():
 
     K = args.steps
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    torch.cuda.synchronize()
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed_loop(ptr_sets):
+        """K back-to-back calls between one event pair: ms per call."""
+        torch.cuda.synchronize()
+        e_start.record(stream)
+        for i in range(K):
+            step(ptr_sets[i % len(ptr_sets)])
+        e_end.record(stream)
+        torch.cuda.synchronize()
+        return e_start.elapsed_time(e_end) / K
+
+    def per_launch_loop(ptr_sets):
+        """K calls, each between its own event pair: per-launch ms."""
+        torch.cuda.synchronize()
+        for i in range(K):
+            ev[i][0].record(stream)
+            step(ptr_sets[i % len(ptr_sets)])
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in ev]
+
+    one_set = [(qp, kp, vp, op)]
     wall0 = time.perf_counter()
-    for i in range(K):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
+    ms_per_step = timed_loop(one_set)
     wall = time.perf_counter() - wall0
-    per = [a.elapsed_time(b) for a, b in ev]           # ms, each launch alone
-    total_ms = ev[0][0].elapsed_time(ev[-1][1])        # ms, first start to last end
-    ms_per_step = total_ms / K
+    per = per_launch_loop(one_set)                      # ms, each launch alone
     kern_ms = sum(per) / K
     nbytes = algorithmic_bytes(B, Hq, Hkv, S, D)
     value_tbs = nbytes / (ms_per_step * 1e-3) / 1e12
@@ -187,14 +207,8 @@ def main():
             sets.append(tuple(x.data_ptr() for x in t))
         for i in range(args.warmup):
             step(sets[i % len(sets)])
-        torch.cuda.synchronize()
-        for i in range(K):
-            ev[i][0].record(stream)
-            step(sets[i % len(sets)])
-            ev[i][1].record(stream)
-        torch.cuda.synchronize()
-        rot_ms = ev[0][0].elapsed_time(ev[-1][1]) / K
-        rot_kern_ms = sum(a.elapsed_time(b) for a, b in ev) / K
+        rot_ms = timed_loop(sets)
+        rot_kern_ms = sum(per_launch_loop(sets)) / K
         rotated = {
             "input_sets": len(sets),
             "us_per_call": round(rot_ms * 1e3, 2),
