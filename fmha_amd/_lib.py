@@ -18,6 +18,8 @@ EXPORTED = (
     "fmha_decode_fwd_paged",
     "fmha_decode_splitkv_workspace_size",
     "fmha_decode_fwd_splitkv",
+    "fmha_decode_fwd_splitkv_strided",
+    "fmha_decode_fwd_splitkv_paged",
     "fmha_decode_error_string",
     "fmha_decode_last_error_detail",
     "fmha_decode_version",
@@ -53,6 +55,12 @@ def load():
     lib.fmha_decode_splitkv_workspace_size.argtypes = [i32, i32, i32, i32, i32]
     lib.fmha_decode_fwd_splitkv.restype = ctypes.c_int
     lib.fmha_decode_fwd_splitkv.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32, vp, sz]
+    lib.fmha_decode_fwd_splitkv_strided.restype = ctypes.c_int
+    lib.fmha_decode_fwd_splitkv_strided.argtypes = [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, i32,
+                                                    i32, i32, f32, vp, sz]
+    lib.fmha_decode_fwd_splitkv_paged.restype = ctypes.c_int
+    lib.fmha_decode_fwd_splitkv_paged.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, i32,
+                                                  i32, f32, vp, sz]
     lib.fmha_decode_error_string.restype = ctypes.c_char_p
     lib.fmha_decode_error_string.argtypes = [ctypes.c_int]
     lib.fmha_decode_last_error_detail.restype = ctypes.c_char_p

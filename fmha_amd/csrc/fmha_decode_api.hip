@@ -315,9 +315,9 @@ bool onepass_fits(const SplitArgs& a) {
          fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
 }
 
-template <int D, int G>
+template <int D, int G, int LAYOUT>
 hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G>;
+  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT>;
   const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
   const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
   const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
@@ -325,9 +325,10 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int D, int G>
+// LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
+template <int D, int G, int LAYOUT>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
-  if (onepass_fits<D, G>(a)) return launch_onepass_dg<D, G>(a, stream);
+  if (onepass_fits<D, G>(a)) return launch_onepass_dg<D, G, LAYOUT>(a, stream);
   // The combine grid has one workgroup per (batch, query head, 32 dims).
   if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
@@ -336,7 +337,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
   const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;
   {
-    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB>;
+    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
                        lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
   }
@@ -353,13 +354,13 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   else
     hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
   if (a.nchunks == 1) {
-    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true>;
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, a);
     return hipGetLastError();
   }
   {
-    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false>;
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, a);
   }
@@ -377,13 +378,22 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int D>
+template <int D, int LAYOUT>
 hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream) {
   switch (g) {
-    case 1: return launch_split_dg<D, 1>(a, stream);
-    case 2: return launch_split_dg<D, 2>(a, stream);
-    case 4: return launch_split_dg<D, 4>(a, stream);
-    default: return launch_split_dg<D, 8>(a, stream);
+    case 1: return launch_split_dg<D, 1, LAYOUT>(a, stream);
+    case 2: return launch_split_dg<D, 2, LAYOUT>(a, stream);
+    case 4: return launch_split_dg<D, 4, LAYOUT>(a, stream);
+    default: return launch_split_dg<D, 8, LAYOUT>(a, stream);
+  }
+}
+
+template <int LAYOUT>
+hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_split_d<64, LAYOUT>(a, g, stream);
+    case 128: return launch_split_d<128, LAYOUT>(a, g, stream);
+    default: return launch_split_d<256, LAYOUT>(a, g, stream);
   }
 }
 
@@ -481,12 +491,18 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
                 seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv);
 }
 
-extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_cache, const void* V_cache, void* O,
-                                     const int32_t* block_table, int32_t block_table_stride,
-                                     const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
-                                     int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
-                                     int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
-  g_detail[0] = '\0';
+namespace {
+
+int log2_pow2(int x) {
+  int shift = 0;
+  while ((1 << shift) < x) ++shift;
+  return shift;
+}
+
+int paged_checks(const void* Q, const void* K_cache, const void* V_cache, void* O, const int32_t* block_table,
+                 int32_t block_table_stride, const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
+                 int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                 int32_t head_dim_kv, float softmax_scale) {
   int rc = check_common(Q, K_cache, V_cache, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
@@ -499,17 +515,48 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "block_table and seqlens_kv must be 4-byte aligned");
   if (block_table_stride < 1)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "block_table_stride must be >= 1 (got %d)", block_table_stride);
+  return FMHA_DECODE_SUCCESS;
+}
+
+// Rows a block-table row can map: lengths above this get NaN, so no batch
+// reads past its own row of the table.
+int32_t paged_capacity(int32_t block_table_stride, int32_t page_size, int32_t max_rows) {
+  const int64_t cap = (int64_t)block_table_stride * page_size;
+  return cap < max_rows ? (int32_t)cap : max_rows;
+}
+
+// The short kernel over a paged cache; lengths above max_rows (<= 16) give NaN.
+int paged_short(void* stream, const void* Q, const void* K_cache, const void* V_cache, void* O,
+                const int32_t* block_table, int32_t block_table_stride, const int32_t* seqlens_kv, int32_t page_size,
+                int32_t max_rows, int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t head_dim_q,
+                float softmax_scale) {
+  max_rows = paged_capacity(block_table_stride, page_size, max_rows);
   DecodeArgs a = base_args(Q, K_cache, V_cache, O, num_heads_q, num_heads_kv, softmax_scale);
   a.lens = seqlens_kv;
   a.block_table = block_table;
   a.bt_stride = block_table_stride;
-  int shift = 0;
-  while ((1 << shift) < page_size) ++shift;
-  a.seqlen_uniform = shift;
+  a.seqlen_uniform = log2_pow2(page_size);
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
   a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
-  return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0, kVarlenRowsHint);
+  a.max_rows = max_rows;
+  return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0,
+                max_rows < kVarlenRowsHint ? max_rows : kVarlenRowsHint);
+}
+
+}  // namespace
+
+extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_cache, const void* V_cache, void* O,
+                                     const int32_t* block_table, int32_t block_table_stride,
+                                     const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
+                                     int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                     int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
+                        num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
+                     FMHA_DECODE_MAX_SEQLEN_KV, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
 }
 
 extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
@@ -520,27 +567,19 @@ extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_
   return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
 }
 
-extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
-                                       const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
-                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
-                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
-                                       void* workspace, size_t workspace_bytes) {
-  g_detail[0] = '\0';
-  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
-  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
-  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
-  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
-    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
-  if (max_seqlen_kv < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv must be >= 0");
-  const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim_q);
-  // One batch's K/V rows (up to nblk * 16), one batch's scores
-  // (Hq * nblk * 16 floats) and one batch's partial outputs are each
-  // addressed through a buffer range that must stay below 2^30 bytes.
-  const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
+namespace {
+
+// Checks shared by the split-KV entry points, then the plan and the
+// layout-independent fields of the launch.  kv_span_bytes: the largest byte
+// range one wave's K/V descriptor covers in the caller's layout (must stay
+// below 2^30, as must one batch's scores and partial outputs).
+int split_prepare(const void* Q, const void* K, const void* V, void* O, int32_t max_seqlen_kv, int32_t batch,
+                  int32_t num_heads_q, int32_t num_heads_kv, int32_t head_dim, float softmax_scale, void* workspace,
+                  size_t workspace_bytes, int64_t kv_span_bytes, SplitArgs& a) {
+  const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim);
   const int64_t padded_rows = (int64_t)plan.nblk * fmha_decode::kSplitBlockRows;
-  const int64_t part_bytes = (int64_t)num_heads_q * plan.nchunks * head_dim_q * 4;  // one batch's partials
-  if (padded_rows * row_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30) ||
+  const int64_t part_bytes = (int64_t)num_heads_q * plan.nchunks * head_dim * 4;  // one batch's partials
+  if (kv_span_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30) ||
       part_bytes >= (int64_t(1) << 30))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv too large for this head count (%d)", max_seqlen_kv);
   if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
@@ -551,24 +590,12 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
                   plan.total);
   if (plan.units * plan.nblk > (int64_t)INT32_MAX || (int64_t)batch * num_heads_q > (int64_t)INT32_MAX)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch * heads * blocks too large");
-  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
-    // Rows that fit the short kernel take it (same numerics, lengths above
-    // max_seqlen_kv give NaN there too); the workspace goes unused.
-    DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
-    d.lens = cu_seqlens_kv;
-    d.row_stride = num_heads_kv * head_dim_q;
-    d.head_stride = head_dim_q;
-    d.max_rows = max_seqlen_kv;
-    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
-                  max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint);
-  }
   char* ws = static_cast<char*>(workspace);
-  SplitArgs a = {};
+  a = SplitArgs{};
   a.q = static_cast<const uint16_t*>(Q);
   a.k = static_cast<const uint16_t*>(K);
   a.v = static_cast<const uint16_t*>(V);
   a.o = static_cast<uint16_t*>(O);
-  a.cu = cu_seqlens_kv;
   a.t = reinterpret_cast<float*>(ws + plan.off_t);
   a.m = reinterpret_cast<float*>(ws + plan.off_m);
   a.l = reinterpret_cast<float*>(ws + plan.off_l);
@@ -583,16 +610,136 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
   a.max_rows = max_seqlen_kv;
   a.batch = batch;
   a.scale = softmax_scale;
+  return FMHA_DECODE_SUCCESS;
+}
+
+int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int g = num_heads_q / num_heads_kv;
+  const int g = a.num_heads_q / a.num_heads_kv;
   hipError_t err;
-  switch (head_dim_q) {
-    case 64: err = launch_split_d<64>(a, g, s); break;
-    case 128: err = launch_split_d<128>(a, g, s); break;
-    default: err = launch_split_d<256>(a, g, s); break;
+  switch (layout) {
+    case fmha_decode::kLayoutPacked: err = launch_split_layout<fmha_decode::kLayoutPacked>(a, head_dim, g, s); break;
+    case fmha_decode::kLayoutStrided: err = launch_split_layout<fmha_decode::kLayoutStrided>(a, head_dim, g, s); break;
+    case fmha_decode::kLayoutPaged: err = launch_split_layout<fmha_decode::kLayoutPaged>(a, head_dim, g, s); break;
+    default: err = launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s); break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
+}
+
+int split_check_workspace_args(int32_t max_seqlen_kv) {
+  if (max_seqlen_kv < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "max_seqlen_kv must be >= 0");
+  return FMHA_DECODE_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
+                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
+                                       void* workspace, size_t workspace_bytes) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
+  if ((rc = split_check_workspace_args(max_seqlen_kv)) != FMHA_DECODE_SUCCESS) return rc;
+  // One batch's K/V rows (up to nblk * 16) are addressed through one range.
+  const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
+  const int64_t padded_rows = ((int64_t)max_seqlen_kv + 15) / 16 * 16;
+  SplitArgs a;
+  rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale, workspace,
+                     workspace_bytes, (padded_rows > 16 ? padded_rows : 16) * row_bytes, a);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
+    // Rows that fit the short kernel take it (same numerics, lengths above
+    // max_seqlen_kv give NaN there too); the workspace goes unused.
+    DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+    d.lens = cu_seqlens_kv;
+    d.row_stride = num_heads_kv * head_dim_q;
+    d.head_stride = head_dim_q;
+    d.max_rows = max_seqlen_kv;
+    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
+                  max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint);
+  }
+  a.cu = cu_seqlens_kv;
+  a.len_mode = fmha_decode::kLenCu;
+  return split_launch(stream, fmha_decode::kLayoutPacked, a, head_dim_q);
+}
+
+extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                               const int32_t* seqlens_kv, int32_t max_seqlen_kv,
+                                               int64_t kv_batch_stride, int64_t kv_row_stride,
+                                               int64_t kv_head_stride, int32_t batch, int32_t num_heads_q,
+                                               int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                                               int32_t head_dim_kv, float softmax_scale, void* workspace,
+                                               size_t workspace_bytes) {
+  g_detail[0] = '\0';
+  int rc = split_check_workspace_args(max_seqlen_kv);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
+    return fmha_decode_fwd_strided(stream, Q, K, V, O, seqlens_kv, max_seqlen_kv, kv_batch_stride, kv_row_stride,
+                                   kv_head_stride, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                                   head_dim_kv, softmax_scale);
+  rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale,
+                    false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
+  if ((kv_batch_stride | kv_row_stride | kv_head_stride) & 7)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be multiples of 8 elements (16 bytes)");
+  if (seqlens_kv && (reinterpret_cast<uintptr_t>(seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlens_kv must be 4-byte aligned");
+  // One batch's rows and heads are addressed through one range.
+  const int64_t extent =
+      ((int64_t)(max_seqlen_kv - 1) * kv_row_stride + (int64_t)(num_heads_kv - 1) * kv_head_stride + head_dim_q) * 2;
+  if (extent >= (int64_t(1) << 30))
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "one batch's K/V span exceeds 1 GiB");
+  SplitArgs a;
+  rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale, workspace,
+                     workspace_bytes, extent, a);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  a.cu = seqlens_kv;
+  a.len_mode = seqlens_kv ? fmha_decode::kLenArray : fmha_decode::kLenUniform;
+  a.batch_stride = kv_batch_stride;
+  a.row_stride = (int32_t)kv_row_stride;
+  a.head_stride = (int32_t)kv_head_stride;
+  return split_launch(stream, fmha_decode::kLayoutStrided, a, head_dim_q);
+}
+
+extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const void* K_cache, const void* V_cache,
+                                             void* O, const int32_t* block_table, int32_t block_table_stride,
+                                             const int32_t* seqlens_kv, int32_t page_size, int32_t max_seqlen_kv,
+                                             int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                             int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                             float softmax_scale, void* workspace, size_t workspace_bytes) {
+  g_detail[0] = '\0';
+  int rc = split_check_workspace_args(max_seqlen_kv);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
+                    num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  max_seqlen_kv = paged_capacity(block_table_stride, page_size, max_seqlen_kv);
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
+    return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
+                       max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
+  // A sub-block's range covers at most 16 rows of one page.
+  const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
+  SplitArgs a;
+  rc = split_prepare(Q, K_cache, V_cache, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q,
+                     softmax_scale, workspace, workspace_bytes, 16 * row_bytes, a);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  a.cu = seqlens_kv;
+  a.len_mode = fmha_decode::kLenArray;
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.page_shift = log2_pow2(page_size);
+  a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
+  return split_launch(stream, page_size >= 16 ? fmha_decode::kLayoutPagedBlock : fmha_decode::kLayoutPaged, a,
+                      head_dim_q);
 }
 
 extern "C" const char* fmha_decode_error_string(int code) {

@@ -116,6 +116,16 @@ __device__ __forceinline__ constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + 
 
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t x) { return __builtin_bit_cast(bf16x2, x); }
 
+// A value every lane reads at the same index, from memory no kernel writes
+// while this one runs (the block table): read through the constant address
+// space, it becomes a scalar load that the compiler issues ahead and batches,
+// where a plain load of it is a vector load whose full wait also waits for
+// every K/V request issued before it.
+__device__ __forceinline__ int32_t load_uniform_i32(const int32_t* p, uint64_t idx) {
+  typedef const __attribute__((address_space(4))) int32_t constant_i32;
+  return ((constant_i32*)p)[idx];
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, kBufferWord3);
 }
@@ -358,7 +368,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) {
       const int jj = j < S ? j : 0;
-      const uint32_t page = (uint32_t)kv.pages[jj >> kv.page_shift];
+      const uint32_t page = (uint32_t)load_uniform_i32(kv.pages, (uint32_t)jj >> kv.page_shift);
       const uint32_t slot = (uint32_t)jj & ((1u << kv.page_shift) - 1u);
       row_elem[j] = (uint64_t)page * kv.page_stride + (uint64_t)slot * (kv.row_bytes >> 1);
       row_rec[j] = j < S ? kv.row_extent : 0u;

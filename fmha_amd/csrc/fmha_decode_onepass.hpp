@@ -48,7 +48,7 @@ constexpr size_t onepass_lds_bytes(int sp) {
   return (size_t)OnepassShape<D, G>::HPW * G * sp * 6;
 }
 
-template <int D, int G>
+template <int D, int G, int LAYOUT = kLayoutPacked>
 __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs a) {
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
@@ -75,8 +75,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   const int hk = (int)hg * HPW + hkl;
   const bool head_ok = hk < a.num_heads_kv;
   const int hq = a.num_heads_q;
-  const int64_t base = a.cu[b];
-  const int S = a.cu[b + 1] - (int)base;
+  const int S = split_len_l<LAYOUT>(a, b);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
   const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
   if (S <= 0 || S > a.max_rows) {
@@ -90,13 +89,12 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   float* sc = onepass_lds + (size_t)hkl * G * sp;                                         // [G][sp] fp32
   uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sp) + (size_t)hkl * G * sp;  // [G][sp]
 
-  const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
-  const uint64_t kv0 = (uint64_t)base * a.num_heads_kv * D;
-  // Ranges end at the batch's last row: later rows read 0 without access.
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + kv0, (uint32_t)S * row_bytes);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + kv0, (uint32_t)S * row_bytes);
+  // Rows [0, S) of the batch: later rows read 0 without access.
+  const int64_t row_base = split_row_base<LAYOUT>(a, b);
+  LongRows<D, LAYOUT> krows, vrows;
+  krows.init(a, a.k, b, row_base, 0, S, hk, head_ok, r);
+  vrows.init(a, a.v, b, row_base, 0, S, hk, head_ok, r);
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
-  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
 
   u32x4 qv[G];
 #pragma unroll
@@ -106,10 +104,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   const int blkl = r >> (NS - L);
   const bool writer = (r & ((1 << (NS - L)) - 1)) == 0;
   const int nsub = ((S + NR - 1) / NR + 1) / 2 * 2;  // even
-  auto load_k = [&](u32x4 (&kr)[NR], int s) {
-#pragma unroll
-    for (int j = 0; j < NR; ++j) kr[j] = buffer_load16_nt(k_rsrc, kv_off + (uint32_t)(s * NR + j) * row_bytes);
-  };
+  auto load_k = [&](u32x4 (&kr)[NR], int s) { krows.template load<NR>(kr, s * NR); };
   auto score = [&](const u32x4 (&kr)[NR], int s) {
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GH) {
@@ -153,10 +148,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   // do not depend on, so they arrive while it runs.
   using VBuf = u32x4[NRV];
   VBuf va, vb;
-  auto load_v = [&](u32x4 (&vr)[NRV], int s) {
-#pragma unroll
-    for (int j = 0; j < NRV; ++j) vr[j] = buffer_load16_nt(v_rsrc, kv_off + (uint32_t)(s * NRV + j) * row_bytes);
-  };
+  auto load_v = [&](u32x4 (&vr)[NRV], int s) { vrows.template load<NRV>(vr, s * NRV); };
   load_v(va, 0);
   __builtin_amdgcn_sched_barrier(0);
   load_v(vb, 1);

@@ -35,12 +35,17 @@
 
 namespace fmha_decode {
 
+// How a batch's length is found (SplitArgs::len_mode).
+constexpr int kLenCu = 0;       // cu[b + 1] - cu[b] (packed layout)
+constexpr int kLenArray = 1;    // cu[b] holds the length itself
+constexpr int kLenUniform = 2;  // every batch has max_rows rows
+
 struct SplitArgs {
   const uint16_t* q;      // [batch, Hq, D] bf16
-  const uint16_t* k;      // [rows, Hkv, D] bf16, packed by cu
+  const uint16_t* k;      // bf16 K rows in the launch's layout (LongRows)
   const uint16_t* v;
   uint16_t* o;            // [batch, Hq, D] fp16
-  const int32_t* cu;      // [batch+1]
+  const int32_t* cu;      // packed: [batch+1] row offsets; else [batch] lengths (or null, uniform)
   float* t;               // [batch, nblk, Hq, 16] scaled scores
   float* m;               // [batch, Hq, nblk] block max
   float* l;               // [batch, Hq, nblk] block sum of exp(t - m_b)
@@ -55,7 +60,29 @@ struct SplitArgs {
   int32_t max_rows;       // lengths above this are invalid (NaN output)
   int32_t batch;
   float scale;
+  int32_t len_mode;       // kLenCu, kLenArray or kLenUniform
+  // kLayoutStrided: element strides of K/V; kLayoutPaged: page stride in
+  // batch_stride, row (slot) stride in row_stride, block table and
+  // log2(page_size).
+  int64_t batch_stride;
+  int32_t row_stride;
+  int32_t head_stride;
+  const int32_t* block_table;
+  int32_t bt_stride;
+  int32_t page_shift;
 };
+
+// Length of batch b (may be out of [0, max_rows]: the kernels check).
+__device__ __forceinline__ int split_len(const SplitArgs& a, uint64_t b) {
+  if (a.len_mode == kLenCu) return a.cu[b + 1] - a.cu[b];
+  if (a.len_mode == kLenArray) return a.cu[b];
+  return a.max_rows;
+}
+template <int LAYOUT>
+__device__ __forceinline__ int split_len_l(const SplitArgs& a, uint64_t b) {
+  if constexpr (LAYOUT == kLayoutPacked) return a.cu[b + 1] - a.cu[b];
+  return split_len(a, b);
+}
 
 constexpr int kSplitBlockRows = kMaxSeq;  // rows per scores wave
 
@@ -65,6 +92,116 @@ __device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint
 
 __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voffset, 0, kPolicyDefault));
+}
+
+// Pages of at least 16 rows, for the long-row kernels: a sub-block of up to
+// 16 rows (aligned to its size) lies in one page, so it needs one block-table
+// lookup and one descriptor.  kLayoutPaged then means pages of 1-8 rows (one
+// lookup per row).  The host picks between the two, so that no pipelined loop
+// carries a branch (the compiler would wait for every request at its head).
+constexpr int kLayoutPagedBlock = 3;
+
+// A pointer the whole wave holds, moved to scalar registers: a buffer
+// descriptor built from a value the compiler keeps in vector registers
+// becomes a loop over the lanes.
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<const uint16_t*>(((uint64_t)hi << 32) | lo);
+}
+
+// One wave's view of the K (or V) rows [lo, hi) of batch b, in one of the
+// layouts of the short kernel:
+//   kLayoutPacked:  rows cu[b] + j of [rows, Hkv, D];
+//   kLayoutStrided: element b*batch_stride + j*row_stride + h*head_stride + d;
+//   kLayoutPaged, kLayoutPagedBlock: slot j % page_size of page
+//                   block_table[b][j / page_size] in a [pages, page_size,
+//                   Hkv, D] cache.
+// load<NR>(out, rel0) fetches rows lo + rel0 .. lo + rel0 + NR - 1 (rel0 a
+// multiple of NR, lo a multiple of 16, NR <= 16): 16 bytes per lane, this
+// lane's head and dims; rows at or past hi read 0 without memory access, so
+// padding, neighbouring batches and unused pages are never read.
+template <int D, int LAYOUT>
+struct LongRows {
+  static constexpr bool PAGED = LAYOUT == kLayoutPaged || LAYOUT == kLayoutPagedBlock;
+  __amdgpu_buffer_rsrc_t rsrc;  // packed, strided: rows [lo, hi)
+  const uint16_t* base;         // paged: the cache
+  const int32_t* pages;         // paged: this batch's block-table row
+  uint32_t row_bytes;           // bytes between consecutive rows (slots)
+  uint32_t lane_off;            // this lane's head and dims within a row
+  uint32_t page_shift;
+  uint64_t page_stride;         // elements
+  int lo, n;                    // first row, rows in range
+
+  __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t row_base, int lo_,
+                                       int hi, int hk, bool head_ok, int r) {
+    lo = lo_;
+    n = hi > lo_ ? hi - lo_ : 0;
+    if constexpr (LAYOUT == kLayoutPacked) {
+      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+      rsrc = make_rsrc(t + ((uint64_t)row_base + lo) * a.num_heads_kv * D, (uint32_t)n * row_bytes);
+    } else if constexpr (LAYOUT == kLayoutStrided) {
+      row_bytes = (uint32_t)a.row_stride * 2u;
+      lane_off = head_ok ? (uint32_t)(hk * a.head_stride + r * 8) * 2u : kLaneOutOfRange;
+      const uint32_t span = n == 0 ? 0u
+                                   : ((uint32_t)(n - 1) * (uint32_t)a.row_stride +
+                                      (uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+      rsrc = make_rsrc(t + (uint64_t)b * (uint64_t)a.batch_stride + (uint64_t)lo * (uint64_t)a.row_stride, span);
+    } else {
+      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+      base = t;
+      pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+      page_shift = (uint32_t)a.page_shift;
+      page_stride = (uint64_t)a.batch_stride;
+    }
+  }
+
+  // Descriptor of `rows` rows from row `row` on, inside one page.  A row past
+  // the end looks up block-table entry 0 of the batch (present whenever the
+  // batch has a row) and gets an empty range.
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows) const {
+    const uint32_t page = (uint32_t)load_uniform_i32(pages, (uint32_t)row >> page_shift);
+    const uint32_t slot = (uint32_t)row & ((1u << page_shift) - 1u);
+    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(rows * (int)row_bytes);
+    return make_rsrc(uniform_ptr(base + (uint64_t)page * page_stride + (uint64_t)slot * (row_bytes >> 1)), range);
+  }
+
+  template <int NR>
+  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
+    static_assert(NR <= 16, "a sub-block fits a 16-row page");
+    if constexpr (LAYOUT == kLayoutPacked) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) out[j] = buffer_load16_nt(rsrc, lane_off + (uint32_t)(rel0 + j) * row_bytes);
+    } else if constexpr (LAYOUT == kLayoutStrided) {
+      // The range can cover other heads' padding rows: rows past the end
+      // are moved out of range.
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+        out[j] = buffer_load16_nt(rsrc, lane_off + (rel0 + j < n ? (uint32_t)(rel0 + j) * row_bytes : kRowOutOfRange));
+    } else if constexpr (LAYOUT == kLayoutPagedBlock) {
+      const int valid = n - rel0 < 0 ? 0 : (n - rel0 > NR ? NR : n - rel0);
+      const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid);
+#pragma unroll
+      for (int j = 0; j < NR; ++j) out[j] = buffer_load16_nt(pr, lane_off + (uint32_t)j * row_bytes);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const bool ok = rel0 + j < n;
+        out[j] = buffer_load16_nt(page_rsrc(lo + (ok ? rel0 + j : 0), ok ? 1 : 0), lane_off);
+      }
+    }
+  }
+};
+
+// First packed row of batch b (0 for the other layouts, which address rows
+// per batch).
+template <int LAYOUT>
+__device__ __forceinline__ int64_t split_row_base(const SplitArgs& a, uint64_t b) {
+  if constexpr (LAYOUT == kLayoutPacked) return a.cu[b];
+  return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -80,7 +217,7 @@ __device__ __forceinline__ uint64_t t_block_base(const SplitArgs& a, uint64_t b,
 // NB blocks of 16 rows per wave, all of their K rows requested at once.
 // The G query heads of a KV head are scored GH at a time against the same K
 // registers (GH = 4 bounds the partial sums a lane holds to 64).
-template <int D, int G, int NB>
+template <int D, int G, int NB, int LAYOUT = kLayoutPacked>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
@@ -104,19 +241,17 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   const uint32_t rem = id - b * per_b;
   const uint32_t wb = rem / upb;
   const uint32_t hg = rem - wb * upb;
-  const int64_t base = a.cu[b];
-  const int S = a.cu[b + 1] - (int)base;
+  const int S = split_len_l<LAYOUT>(a, b);
   const int j0 = (int)wb * NB * NR;
   if (S < 0 || S > a.max_rows || j0 >= S) return;
   const int hk = (int)hg * HPW + lane / LPH;
   const bool head_ok = hk < a.num_heads_kv;
   const int r = lane % LPH;
   const int hq = a.num_heads_q;
-  const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
-  // Range ends at the batch's last row: rows past S read 0 without access.
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + (uint64_t)base * a.num_heads_kv * D, (uint32_t)S * row_bytes);
-  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+  // Rows [0, S) of the batch: rows past S read 0 without access.
+  LongRows<D, LAYOUT> kv;
+  kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, hk, head_ok, r);
   const uint32_t q_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
 
   u32x4 qv[G];
@@ -124,7 +259,12 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, q_off + g * D * 2);
   u32x4 kr[NB * NR];
 #pragma unroll
-  for (int j = 0; j < NB * NR; ++j) kr[j] = buffer_load16_nt(k_rsrc, kv_off + (uint32_t)(j0 + j) * row_bytes);
+  for (int q = 0; q < NB; ++q) {
+    u32x4 kq[NR];
+    kv.template load<NR>(kq, j0 + q * NR);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) kr[q * NR + j] = kq[j];
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // After the butterfly, lane r holds scores [blkl*W, blkl*W + W) of the
@@ -241,7 +381,7 @@ __global__ __launch_bounds__(256) void splitkv_stats_lane_kernel(SplitArgs a) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // b * Hq + h
   if (i >= (uint64_t)a.batch * a.num_heads_q) return;
   const uint64_t b = i / (uint64_t)a.num_heads_q;
-  const int S = a.cu[b + 1] - a.cu[b];
+  const int S = split_len(a, b);
   if (S <= 0 || S > a.max_rows) return;
   const int n = (S + kSplitBlockRows - 1) / kSplitBlockRows;
   const float* m = a.m + i * a.nblk;
@@ -271,7 +411,7 @@ __global__ __launch_bounds__(THREADS) void splitkv_stats_kernel(SplitArgs a) {
   const uint64_t i = blockIdx.x;  // b * Hq + h
   const int t = threadIdx.x;
   const uint64_t b = i / (uint64_t)a.num_heads_q;
-  const int S = a.cu[b + 1] - a.cu[b];
+  const int S = split_len(a, b);
   if (S <= 0 || S > a.max_rows) return;  // the same for every thread of the group
   const int n = (S + kSplitBlockRows - 1) / kSplitBlockRows;
   const float* m = a.m + i * a.nblk;
@@ -354,7 +494,7 @@ __device__ __forceinline__ void pv_sub_block(const u32x4 (&vr)[NR], const float 
   accumulate_pv<G, NR>(vr, pp, acc);
 }
 
-template <int D, int G, int NR, bool DIRECT>
+template <int D, int G, int NR, bool DIRECT, int LAYOUT = kLayoutPacked>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) {
   using P = PvSlots<D, G, NR>;
   constexpr int LPH = P::LPH;
@@ -372,8 +512,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   const uint32_t rem = id - b * per_b;
   const uint32_t c = rem / upb;
   const uint32_t hg = rem - c * upb;
-  const int64_t base = a.cu[b];
-  const int S = a.cu[b + 1] - (int)base;
+  const int S = split_len_l<LAYOUT>(a, b);
   const bool bad = S < 0 || S > a.max_rows;
   const int row0 = (int)c * a.chunk_rows;
   const int hkl = lane / LPH;
@@ -395,11 +534,9 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     return;
   }
   const int rows = min(S - row0, a.chunk_rows);
-  const uint32_t row_bytes = (uint32_t)a.num_heads_kv * D * 2;
   // The chunk's rows only: sub-blocks past its end read 0 without access.
-  const __amdgpu_buffer_rsrc_t v_rsrc =
-      make_rsrc(a.v + ((uint64_t)base + row0) * a.num_heads_kv * D, (uint32_t)rows * row_bytes);
-  const uint32_t kv_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+  LongRows<D, LAYOUT> vrows;
+  vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), row0, row0 + rows, hk, head_ok, r);
   // This batch's scores, [nblk, Hq, 16].
   const __amdgpu_buffer_rsrc_t t_rsrc =
       make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * kSplitBlockRows * 4u);
@@ -434,8 +571,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   u32x4 va[NR], vb[NR];
   float ta[PL], tb[PL];
   auto load = [&](u32x4 (&vr)[NR], float (&tv)[PL], int s) {
-#pragma unroll
-    for (int j = 0; j < NR; ++j) vr[j] = buffer_load16_nt(v_rsrc, kv_off + (uint32_t)(s * NR + j) * row_bytes);
+    vrows.template load<NR>(vr, s * NR);
     // Sub-blocks never straddle a 16-row block (row0 is a multiple of 16).
     const uint32_t sub = (uint32_t)(((row0 + s * NR) / kSplitBlockRows) * hq * kSplitBlockRows +
                                     (s * NR) % kSplitBlockRows) * 4u;
@@ -500,7 +636,7 @@ __global__ __launch_bounds__(256) void splitkv_combine_kernel(SplitArgs a) {
   const uint64_t head = i / per_head;  // b * Hq + h
   const int d0 = (int)(i - head * per_head) * 8;
   const uint64_t b = head / (uint64_t)a.num_heads_q;
-  const int S = a.cu[b + 1] - a.cu[b];
+  const int S = split_len(a, b);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   u32x4 out;
   if (S < 0 || S > a.max_rows) {
@@ -544,7 +680,7 @@ __global__ __launch_bounds__(THREADS) void splitkv_combine_block_kernel(SplitArg
   const int dl = t % LPS;
   const int cg = t / LPS;
   const uint64_t b = head / (uint64_t)a.num_heads_q;
-  const int S = a.cu[b + 1] - a.cu[b];
+  const int S = split_len(a, b);
   const bool bad = S < 0 || S > a.max_rows;
   const int n = bad ? 0 : (S + a.chunk_rows - 1) / a.chunk_rows;
   float acc[4] = {0, 0, 0, 0};

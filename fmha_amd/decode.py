@@ -88,6 +88,30 @@ def launch_fmha_decode_paged(stream, Q, K_cache, V_cache, O, block_table, block_
     _raise_if(rc)
 
 
+def launch_fmha_decode_splitkv_strided(stream, Q, K, V, O, seqlens_kv, max_seqlen_kv, kv_batch_stride,
+                                       kv_row_stride, kv_head_stride, batch, num_heads_q, num_heads_kv, seqlen_q,
+                                       head_dim_q, head_dim_kv, softmax_scale, workspace, workspace_bytes):
+    """Strided K/V with lengths up to max_seqlen_kv (any size), using a
+    caller-provided device workspace; seqlens_kv is a device pointer or 0."""
+    rc = _lib.load().fmha_decode_fwd_splitkv_strided(stream, Q, K, V, O, seqlens_kv, max_seqlen_kv, kv_batch_stride,
+                                                     kv_row_stride, kv_head_stride, batch, num_heads_q, num_heads_kv,
+                                                     seqlen_q, head_dim_q, head_dim_kv, float(softmax_scale),
+                                                     workspace, workspace_bytes)
+    _raise_if(rc)
+
+
+def launch_fmha_decode_splitkv_paged(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv,
+                                     page_size, max_seqlen_kv, batch, num_heads_q, num_heads_kv, seqlen_q,
+                                     head_dim_q, head_dim_kv, softmax_scale, workspace, workspace_bytes):
+    """Paged [pages, page_size, Hkv, D] cache with lengths up to
+    max_seqlen_kv (any size), using a caller-provided device workspace."""
+    rc = _lib.load().fmha_decode_fwd_splitkv_paged(stream, Q, K_cache, V_cache, O, block_table, block_table_stride,
+                                                   seqlens_kv, page_size, max_seqlen_kv, batch, num_heads_q,
+                                                   num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                                   float(softmax_scale), workspace, workspace_bytes)
+    _raise_if(rc)
+
+
 def splitkv_workspace_size(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim):
     """Bytes of device workspace fmha_decode_fwd_splitkv needs (0 if the
     arguments are invalid)."""
@@ -167,11 +191,24 @@ def _check_lengths(t, B, device):
     return t.data_ptr()
 
 
-def fmha_decode_strided(q, k, v, seqlens_kv=None, softmax_scale=None, out=None):
+def _workspace(workspace, need, device):
+    import torch
+    if workspace is None:
+        return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if workspace.dtype != torch.uint8 or workspace.device != device or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor on q's device")
+    return workspace
+
+
+def fmha_decode_strided(q, k, v, seqlens_kv=None, softmax_scale=None, out=None, workspace=None):
     """Decode attention for K/V given as any [B, S, Hkv, D] view with unit
     innermost stride: a contiguous padded BSHD cache, or a BHSD cache passed
     as k.transpose(1, 2).  seqlens_kv (int32 [B]) gives each batch's length
-    (rows past it are never read); without it every batch uses all S rows."""
+    (rows past it are never read; a length above S gives NaN); without it
+    every batch uses all S rows.  S may exceed 16: the call then goes through
+    fmha_decode_fwd_splitkv_strided with workspace (a uint8 device tensor of
+    splitkv_workspace_size(B, Hq, Hkv, S, D) bytes, allocated here when
+    None)."""
     import torch
     B, Hq, D = _q_shape(q)
     out = _check_q_out(q, out)
@@ -187,14 +224,26 @@ def fmha_decode_strided(q, k, v, seqlens_kv=None, softmax_scale=None, out=None):
         softmax_scale = 1.0 / math.sqrt(D)
     lens = _check_lengths(seqlens_kv, B, q.device)
     stream = torch.cuda.current_stream(q.device).cuda_stream
+    if S > MAX_SEQLEN_KV:
+        ws = _workspace(workspace, splitkv_workspace_size(B, Hq, Hkv, S, D), q.device)
+        launch_fmha_decode_splitkv_strided(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lens, S,
+                                           k.stride(0), k.stride(1), k.stride(2), B, Hq, Hkv, 1, D, D, softmax_scale,
+                                           ws.data_ptr(), ws.numel())
+        return out
     launch_fmha_decode_strided(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lens, S,
                                k.stride(0), k.stride(1), k.stride(2), B, Hq, Hkv, 1, D, D, softmax_scale)
     return out
 
 
-def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scale=None, out=None):
+def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scale=None, out=None,
+                      max_seqlen_kv=None, workspace=None):
     """Decode attention over a paged cache: k_cache/v_cache [pages, page_size,
-    Hkv, D] bfloat16, block_table int32 [B, max_pages], seqlens_kv int32 [B]."""
+    Hkv, D] bfloat16, block_table int32 [B, max_pages], seqlens_kv int32 [B].
+    Lengths above max_seqlen_kv (default 16, the reference's bound) or above
+    max_pages * page_size give NaN.  With max_seqlen_kv given the call goes
+    through fmha_decode_fwd_splitkv_paged with workspace (a uint8 device
+    tensor of splitkv_workspace_size(B, Hq, Hkv, max_seqlen_kv, D) bytes,
+    allocated here when None; unused for max_seqlen_kv <= 16)."""
     import torch
     B, Hq, D = _q_shape(q)
     out = _check_q_out(q, out)
@@ -212,6 +261,14 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
     stream = torch.cuda.current_stream(q.device).cuda_stream
+    if max_seqlen_kv is not None:
+        Hkv = k_cache.shape[2]
+        ws = _workspace(workspace, splitkv_workspace_size(B, Hq, Hkv, int(max_seqlen_kv), D), q.device)
+        launch_fmha_decode_splitkv_paged(stream, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                         block_table.data_ptr(), block_table.stride(0), lens, k_cache.shape[1],
+                                         int(max_seqlen_kv), B, Hq, Hkv, 1, D, D, softmax_scale, ws.data_ptr(),
+                                         ws.numel())
+        return out
     launch_fmha_decode_paged(stream, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
                              block_table.data_ptr(), block_table.stride(0), lens, k_cache.shape[1], B, Hq,
                              k_cache.shape[2], 1, D, D, softmax_scale)

@@ -146,8 +146,9 @@ int fmha_decode_fwd_strided(void* stream,
  *
  *   block_table         device int32, ceil(len/page_size) valid entries per
  *                       batch row (the row itself is block_table_stride long)
- *   seqlens_kv          device int32 [batch] lengths in [0, 16]; a length
- *                       outside that range gets NaN outputs
+ *   seqlens_kv          device int32 [batch] lengths in [0, min(16,
+ *                       block_table_stride * page_size)]; a length outside
+ *                       that range gets NaN outputs
  *   page_size           a power of two in [1, 2^20]
  * Other arguments as fmha_decode_fwd.  The reference has no paged layout;
  * this entry point is the KV-cache format of serving engines.
@@ -187,6 +188,48 @@ int fmha_decode_fwd_splitkv(void* stream,
                             int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                             int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                             float softmax_scale, void* workspace, size_t workspace_bytes);
+
+/*
+ * fmha_decode_fwd_splitkv over the strided K/V of fmha_decode_fwd_strided
+ * (BHSD, padded BSHD, any batch/row/head strides in elements, multiples of
+ * 8): lengths beyond 16 for those caches.
+ *
+ *   seqlens_kv     device int32 [batch] lengths, or NULL: every batch has
+ *                  max_seqlen_kv rows
+ *   max_seqlen_kv  rows each batch has room for; a length above it gets NaN
+ *                  outputs, rows past a batch's length are never read
+ * One batch's span (max_seqlen_kv rows, all heads) must stay below 1 GiB.
+ * The workspace is sized by fmha_decode_splitkv_workspace_size(batch, Hq,
+ * Hkv, max_seqlen_kv, head_dim) and unused when max_seqlen_kv <= 16 (the
+ * call then runs fmha_decode_fwd_strided).  No counterpart in the reference,
+ * which has neither layout nor lengths beyond 16 (README.md:166-168,
+ * README.md:233).
+ */
+int fmha_decode_fwd_splitkv_strided(void* stream,
+                                    const void* Q, const void* K, const void* V, void* O,
+                                    const int32_t* seqlens_kv, int32_t max_seqlen_kv,
+                                    int64_t kv_batch_stride, int64_t kv_row_stride, int64_t kv_head_stride,
+                                    int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                    int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                    float softmax_scale, void* workspace, size_t workspace_bytes);
+
+/*
+ * fmha_decode_fwd_splitkv over the paged cache of fmha_decode_fwd_paged:
+ * lengths beyond 16 for a [pages, page_size, Hkv, D] cache.  A length above
+ * min(max_seqlen_kv, block_table_stride * page_size) gets NaN outputs (so no
+ * batch reads past its row of the block table); rows past a batch's length
+ * and pages it does not map are never read.  Workspace as for
+ * fmha_decode_fwd_splitkv_strided (unused when that bound is <= 16: the call
+ * then runs fmha_decode_fwd_paged's kernel).  No counterpart in the
+ * reference.
+ */
+int fmha_decode_fwd_splitkv_paged(void* stream,
+                                  const void* Q, const void* K_cache, const void* V_cache, void* O,
+                                  const int32_t* block_table, int32_t block_table_stride,
+                                  const int32_t* seqlens_kv, int32_t page_size, int32_t max_seqlen_kv,
+                                  int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                  int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                  float softmax_scale, void* workspace, size_t workspace_bytes);
 
 /* Human-readable text for a code returned above (never NULL). */
 const char* fmha_decode_error_string(int code);

@@ -35,7 +35,8 @@ def test_exports_every_declared_function(lib):
     assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_uniform",
                           "fmha_decode_fwd_strided",
                           "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
-                          "fmha_decode_fwd_splitkv", "fmha_decode_error_string",
+                          "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_strided",
+                          "fmha_decode_fwd_splitkv_paged", "fmha_decode_error_string",
                           "fmha_decode_last_error_detail", "fmha_decode_version"}
     from fmha_amd import _lib
     assert set(names) == set(_lib.EXPORTED)
@@ -196,6 +197,67 @@ def test_splitkv_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
+def splitkv_strided(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, lens=CU, maxs=1000, bs=1000 * 16 * 128, rs=16 * 128, hs=128,
+             batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128, scale=0.088, ws=P * 64, wsb=1 << 30)
+    a.update(kw)
+    return lib.fmha_decode_fwd_splitkv_strided(a["stream"], a["q"], a["k"], a["v"], a["o"], a["lens"], a["maxs"],
+                                               a["bs"], a["rs"], a["hs"], a["batch"], a["hq"], a["hkv"], a["sq"],
+                                               a["dq"], a["dkv"], a["scale"], a["ws"], a["wsb"])
+
+
+def splitkv_paged(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, bt=CU, bts=64, lens=CU + 64, ps=16, maxs=1000, batch=4, hq=16,
+             hkv=16, sq=1, dq=128, dkv=128, scale=0.088, ws=P * 64, wsb=1 << 30)
+    a.update(kw)
+    return lib.fmha_decode_fwd_splitkv_paged(a["stream"], a["q"], a["k"], a["v"], a["o"], a["bt"], a["bts"],
+                                             a["lens"], a["ps"], a["maxs"], a["batch"], a["hq"], a["hkv"], a["sq"],
+                                             a["dq"], a["dkv"], a["scale"], a["ws"], a["wsb"])
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(maxs=-1), BAD, "max_seqlen_kv"),
+    (dict(bs=-8), BAD, "strides"),
+    (dict(rs=12), BAD, "multiples of 8"),
+    (dict(rs=1 << 20), BAD, "1 GiB"),
+    (dict(lens=CU + 2), BAD, "seqlens_kv"),
+    (dict(ws=None), BAD, "workspace"),
+    (dict(wsb=1024), BAD, "too small"),
+    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    (dict(k=None), BAD, "non-null"),
+    (dict(maxs=16, lens=None, rs=12), BAD, "multiples of 8"),   # <= 16 rows: fmha_decode_fwd_strided's checks
+])
+def test_splitkv_strided_rejects(lib, kw, code, needle):
+    assert splitkv_strided(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(maxs=-1), BAD, "max_seqlen_kv"),
+    (dict(ps=24), BAD, "page_size"),
+    (dict(bt=None), BAD, "block_table"),
+    (dict(lens=None), BAD, "seqlens_kv"),
+    (dict(bts=0), BAD, "block_table_stride"),
+    (dict(ws=None), BAD, "workspace"),
+    (dict(wsb=1024), BAD, "too small"),
+    (dict(sq=2), BAD, "seqlen_q"),
+    (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
+])
+def test_splitkv_paged_rejects(lib, kw, code, needle):
+    assert splitkv_paged(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+def test_splitkv_paged_bound_is_the_block_table_row(lib):
+    """Lengths beyond block_table_stride * page_size count as invalid: a call
+    with a larger max_seqlen_kv needs only the workspace of that bound (64
+    entries of 16-row pages here).  The call is rejected for a workspace one
+    byte short of it, before any launch."""
+    need = lib.fmha_decode_splitkv_workspace_size(4, 16, 16, 64 * 16, 128)
+    assert splitkv_paged(lib, maxs=1 << 18, wsb=need - 1) == BAD
+    assert f"need {need})" in lib.fmha_decode_last_error_detail().decode()
+
+
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(batch=-1), BAD, "batch"),
     (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
@@ -220,6 +282,8 @@ def test_batch_zero_is_a_noop(lib):
     assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
     assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0
     assert splitkv(lib, batch=0, q=None, k=None, v=None, o=None, cu=None, ws=None) == 0
+    assert splitkv_strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None, ws=None) == 0
+    assert splitkv_paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None, ws=None) == 0
     assert lib.fmha_decode_last_error_detail() == b""
 
 
@@ -299,6 +363,10 @@ def test_header_is_plain_c():
            '  rc |= fmha_decode_fwd_paged(s, q, k, v, o, cu, 4, cu, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'
            '  size_t n = fmha_decode_splitkv_workspace_size(1, 16, 16, 100, 128);\n'
            '  rc |= fmha_decode_fwd_splitkv(s, q, k, v, o, cu, 100, 1, 16, 16, 1, 128, 128, 0.088f, ws, n);\n'
+           '  rc |= fmha_decode_fwd_splitkv_strided(s, q, k, v, o, cu, 100, 204800, 2048, 128, 1, 16, 16, 1, 128,\n'
+           '                                        128, 0.088f, ws, n);\n'
+           '  rc |= fmha_decode_fwd_splitkv_paged(s, q, k, v, o, cu, 7, cu, 16, 100, 1, 16, 16, 1, 128, 128,\n'
+           '                                      0.088f, ws, n);\n'
            '  const char* t = fmha_decode_error_string(rc);\n'
            '  const char* d = fmha_decode_last_error_detail();\n'
            '  return rc + fmha_decode_version() + (t == d);\n}\n')

@@ -1,0 +1,193 @@
+"""GPU parity of lengths beyond 16 over strided and paged caches
+(fmha_decode_fwd_splitkv_strided / fmha_decode_fwd_splitkv_paged, reached
+through fmha_amd.fmha_decode_strided and fmha_amd.fmha_decode_paged).
+
+Each case builds the cache on the host from packed rows (tests.common
+make_inputs), with every row, slot and page the kernels must not read set to
+NaN, and checks the output against the oracle run over the packed rows past
+16 (oracle.decode(max_seqlen=...)), gate as in tests/common.py.  Small
+batches take the split-KV launches, large ones the single pass (batch * KV
+head groups >= 512); page sizes below 16 look pages up per row, 16 and above
+per 16-row sub-block."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.common import assert_pass, cu_from_seqlens, default_scale, make_inputs, to_dev
+
+pytestmark = pytest.mark.gpu
+
+NAN_BITS = np.uint16(0x7FC0)
+
+
+def _units(B, Hkv, D):
+    hpw = 64 // (D // 8)
+    return B * ((Hkv + hpw - 1) // hpw)
+
+
+def _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, ctx):
+    import torch
+    bits = o.view(torch.int16).cpu().numpy().view(np.uint16)
+    r, slack = oracle.decode(q, kp, vp, cu_from_seqlens(seqlens), Hq, Hkv, D, default_scale(D), with_slack=True,
+                             max_seqlen=max_len)
+    st = oracle.compare(bits.reshape(r.shape), r, slack)
+    print(f"{ctx}: {st}", flush=True)
+    assert_pass(st, ctx)
+
+
+def _strided_cache(kp, seqlens, cap, Hkv, D, layout):
+    """Host cache [B, cap, Hkv, D] (bshd) or [B, Hkv, cap, D] (bhsd) with NaN padding."""
+    B = len(seqlens)
+    cu = cu_from_seqlens(seqlens)
+    c = np.full((B, cap, Hkv, D), NAN_BITS, np.uint16)
+    for b in range(B):
+        c[b, :seqlens[b]] = kp[cu[b]:cu[b + 1]]
+    if layout == "bhsd":
+        c = np.ascontiguousarray(c.transpose(0, 2, 1, 3))
+    return c
+
+
+def _strided_view(c, layout):
+    t = to_dev(c)
+    return t.transpose(1, 2) if layout == "bhsd" else t
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("B,cap", [(5, 700), (600, 72)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2), (256, 16, 4)])
+def test_strided_long(layout, B, cap, D, Hq, Hkv):
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(B + cap + D)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[0] = cap
+    seqlens[1] = 0
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=B * 7 + D)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, layout), layout)
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, layout), layout)
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    path = "single pass" if _units(B, Hkv, D) >= 512 else "split"
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} B={B} cap={cap} D={D} Hq={Hq} Hkv={Hkv} ({path})")
+
+
+def test_strided_uniform_long_bhsd():
+    """No lengths array: every batch has all cap rows."""
+    import fmha_amd
+    import torch
+    B, Hq, Hkv, D, cap = 3, 16, 16, 128, 300
+    seqlens = np.full(B, cap, np.int32)
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=77)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, "bhsd uniform S=300")
+
+
+def test_strided_long_length_beyond_capacity_is_nan():
+    import fmha_amd
+    import torch
+    B, H, D, cap = 3, 4, 128, 40
+    seqlens = np.array([40, 30, 2], np.int32)
+    q, kp, vp, cu = make_inputs(B, H, H, D, seqlens, seed=78)
+    kc = to_dev(_strided_cache(kp, seqlens, cap, H, D, "bshd"))
+    vc = to_dev(_strided_cache(vp, seqlens, cap, H, D, "bshd"))
+    lens = torch.tensor([40, 41, 2], dtype=torch.int32, device="cuda")
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=lens).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o[1]).all() and torch.isfinite(o[0]).all() and torch.isfinite(o[2]).all()
+
+
+def _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng, extra_pages=5, spare_entries=1):
+    """Host page caches with pages handed out in random order, NaN in every
+    slot no batch owns, -1 in every block-table entry past a batch's pages."""
+    B = len(seqlens)
+    cu = cu_from_seqlens(seqlens)
+    need = [(int(s) + page_size - 1) // page_size for s in seqlens]
+    max_pages = max(max(need), 1) + spare_entries
+    num_pages = sum(need) + extra_pages
+    perm = rng.permutation(num_pages).astype(np.int32)
+    bt = np.full((B, max_pages), -1, np.int32)
+    kc = np.full((num_pages, page_size, Hkv, D), NAN_BITS, np.uint16)
+    vc = np.full((num_pages, page_size, Hkv, D), NAN_BITS, np.uint16)
+    i = 0
+    for b in range(B):
+        for p in range(need[b]):
+            page = perm[i]
+            i += 1
+            bt[b, p] = page
+            r0, r1 = cu[b] + p * page_size, min(cu[b] + (p + 1) * page_size, cu[b + 1])
+            kc[page, :r1 - r0] = kp[r0:r1]
+            vc[page, :r1 - r0] = vp[r0:r1]
+    return kc, vc, bt
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 16, 64])
+@pytest.mark.parametrize("B,max_len", [(4, 600), (700, 40)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 8, 1), (256, 16, 8)])
+def test_paged_long(page_size, B, max_len, D, Hq, Hkv):
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(page_size * 1000 + B + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    seqlens[-1] = 0
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + B + D)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    path = "single pass" if _units(B, Hkv, D) >= 512 else "split"
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len,
+           f"paged ps={page_size} B={B} max={max_len} D={D} Hq={Hq} Hkv={Hkv} ({path})")
+
+
+@pytest.mark.parametrize("page_size", [2, 32])
+def test_paged_long_bounds_are_nan(page_size):
+    """A length above max_seqlen_kv, and one above what the block-table row
+    maps (block_table_stride * page_size), give NaN for that batch only."""
+    import fmha_amd
+    import torch
+    B, H, D, max_len = 4, 8, 128, 100
+    rng = np.random.default_rng(page_size)
+    seqlens = np.array([100, 60, 7, 33], np.int32)
+    q, kp, vp, cu = make_inputs(B, H, H, D, seqlens, seed=79)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, H, D, rng, spare_entries=0)
+    lens = torch.from_numpy(seqlens).cuda()
+    lens[2] = max_len + 1
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(), lens,
+                                   max_seqlen_kv=max_len).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o[2]).all()
+    assert torch.isfinite(o[[0, 1, 3]]).all()
+    # The table rows end at the longest batch's pages: a bound above them is
+    # cut to the row's capacity, so a length past it is NaN as well.
+    cap = bt.shape[1] * page_size
+    lens2 = torch.from_numpy(seqlens).cuda()
+    lens2[3] = cap + 1
+    o2 = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(), lens2,
+                                    max_seqlen_kv=10 * cap).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o2[3]).all() and torch.isfinite(o2[[0, 1, 2]]).all()
+
+
+def test_paged_short_bound_through_long_entry():
+    """max_seqlen_kv <= 16 runs the short kernel with that bound."""
+    import fmha_amd
+    import torch
+    B, Hq, Hkv, D, page_size = 40, 16, 4, 128, 4
+    rng = np.random.default_rng(5)
+    seqlens = rng.integers(0, 11, size=B).astype(np.int32)
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=80)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=10)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, 16, "paged short bound 10")
+    lens = torch.from_numpy(seqlens).cuda()
+    lens[3] = 11
+    o2 = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(), lens,
+                                    max_seqlen_kv=10).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(o2[3]).all()
