@@ -11,6 +11,12 @@ counted).  Run it under `rocprofv3 --kernel-trace --stats` for the per-kernel
 split.
 
     python3 tests/profiling/splitkv_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...]
+        [--layout packed|bhsd|pagedN]
+
+--layout bhsd stores K/V as [B, Hkv, S, D] (fmha_decode_strided on the
+transposed view); pagedN as pages of N rows handed out in a random order
+with an [B, S/N] block table (fmha_decode_paged with max_seqlen_kv = S).
+S <= 16 then runs the short kernels of those layouts.
 """
 import argparse
 import json
@@ -34,6 +40,7 @@ def main():
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--shapes", default="")
+    ap.add_argument("--layout", default="packed")
     a = ap.parse_args()
     import torch
     import fmha_amd
@@ -48,11 +55,39 @@ def main():
         v = torch.randn(B * S, hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
         cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32, device=dev)
         o = torch.empty(B, hq, 1, D, device=dev, dtype=torch.float16)
-        ws = torch.empty(fmha_amd.splitkv_workspace_size(B, hq, hkv, S, D), dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(fmha_amd.splitkv_workspace_size(B, hq, hkv, S, D), 1), dtype=torch.uint8, device=dev)
         scale = 1.0 / math.sqrt(D)
 
-        def call():
-            fmha_amd.fmha_decode_splitkv(q, k, v, cu, S, softmax_scale=scale, out=o, workspace=ws)
+        if a.layout == "packed":
+            def call():
+                fmha_amd.fmha_decode_splitkv(q, k, v, cu, S, softmax_scale=scale, out=o, workspace=ws)
+        elif a.layout == "bhsd":
+            kt = k.view(B, S, hkv, D).transpose(1, 2).contiguous().transpose(1, 2)
+            vt = v.view(B, S, hkv, D).transpose(1, 2).contiguous().transpose(1, 2)
+            del k, v
+
+            def call():
+                fmha_amd.fmha_decode_strided(q, kt, vt, softmax_scale=scale, out=o, workspace=ws)
+        elif a.layout.startswith("paged"):
+            ps = int(a.layout[5:])
+            npg = B * ((S + ps - 1) // ps)
+            perm = torch.randperm(npg, generator=torch.Generator().manual_seed(S)).to(torch.int32)
+            bt = perm.view(B, -1).to(dev)
+            kc = torch.zeros(npg, ps, hkv, D, device=dev, dtype=torch.bfloat16)
+            vc = torch.zeros(npg, ps, hkv, D, device=dev, dtype=torch.bfloat16)
+            rows = torch.arange(B * S, device=dev)
+            b_of, j_of = rows // S, rows % S
+            page = bt[b_of, j_of // ps].long()
+            kc[page, j_of % ps] = k
+            vc[page, j_of % ps] = v
+            del k, v, rows, b_of, j_of, page
+            lens = torch.full((B,), S, dtype=torch.int32, device=dev)
+
+            def call():
+                fmha_amd.fmha_decode_paged(q, kc, vc, bt, lens, softmax_scale=scale, out=o,
+                                           max_seqlen_kv=S, workspace=ws)
+        else:
+            raise SystemExit(f"unknown layout {a.layout}")
 
         for _ in range(a.warmup):
             call()
@@ -66,9 +101,10 @@ def main():
         per = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
         med = per[len(per) // 2]
         nbytes = 2 * B * hq * D * 2 + 4 * B * S * hkv * D
-        print(json.dumps({"B": B, "Hq": hq, "Hkv": hkv, "S": S, "D": D, "us_per_call_median": round(med, 1),
+        print(json.dumps({"layout": a.layout, "B": B, "Hq": hq, "Hkv": hkv, "S": S, "D": D,
+                          "us_per_call_median": round(med, 1),
                           "tb_s": round(nbytes / med / 1e6, 3), "workspace_bytes": ws.numel()}), flush=True)
-        del q, k, v, o, ws
+        del q, o, ws, call
         torch.cuda.empty_cache()
 
 
