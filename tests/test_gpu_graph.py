@@ -55,3 +55,77 @@ def test_graph_replays_match_eager():
         # eager work between replays
         fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud)
         torch.cuda.synchronize()
+
+
+def test_graph_long_rows_replay_match_eager():
+    """Lengths beyond 16 in a graph: the four split-KV launches (few
+    batches), the single pass (many), and the strided and paged variants,
+    each replay checked bit for bit against the eager result."""
+    import torch
+    import fmha_amd
+    rng = np.random.default_rng(90)
+    outs = []
+    calls = []
+    # split-KV launches: 3 batches, rows up to 700
+    s1 = np.array([700, 1, 333], np.int32)
+    q1, k1, v1, cu1 = make_inputs(3, 16, 4, 128, s1, seed=91)
+    q1d, k1d, v1d, cu1d = to_dev(q1), to_dev(k1), to_dev(v1), torch.from_numpy(cu1).cuda()
+    ws1 = torch.empty(fmha_amd.splitkv_workspace_size(3, 16, 4, 700, 128), dtype=torch.uint8, device="cuda")
+    # single pass: 600 batches, rows up to 64
+    s2 = rng.integers(0, 65, size=600).astype(np.int32)
+    q2, k2, v2, cu2 = make_inputs(600, 32, 8, 128, s2, seed=92)
+    q2d, k2d, v2d, cu2d = to_dev(q2), to_dev(k2), to_dev(v2), torch.from_numpy(cu2).cuda()
+    ws2 = torch.empty(fmha_amd.splitkv_workspace_size(600, 32, 8, 64, 128), dtype=torch.uint8, device="cuda")
+    # strided (BHSD view) and paged copies of the first case
+    kb = torch.zeros(3, 4, 700, 128, dtype=torch.bfloat16, device="cuda")
+    vb = torch.zeros_like(kb)
+    kc = torch.zeros(3 * 44, 16, 4, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(3 * 44, dtype=torch.int32, device="cuda").view(3, 44)
+    for b in range(3):
+        n, r0 = int(s1[b]), int(cu1[b])
+        kb[b, :, :n] = k1d[r0:r0 + n].transpose(0, 1)
+        vb[b, :, :n] = v1d[r0:r0 + n].transpose(0, 1)
+        for j in range(0, n, 16):
+            m = min(16, n - j)
+            kc[bt[b, j // 16], :m] = k1d[r0 + j:r0 + j + m]
+            vc[bt[b, j // 16], :m] = v1d[r0 + j:r0 + j + m]
+    lens1 = torch.from_numpy(s1).cuda()
+    ws3 = torch.empty_like(ws1)
+    ws4 = torch.empty_like(ws1)
+    outs = [torch.empty(3, 16, 128, dtype=torch.float16, device="cuda"),
+            torch.empty(600, 32, 128, dtype=torch.float16, device="cuda"),
+            torch.empty(3, 16, 128, dtype=torch.float16, device="cuda"),
+            torch.empty(3, 16, 128, dtype=torch.float16, device="cuda")]
+
+    def calls():
+        fmha_amd.fmha_decode_splitkv(q1d, k1d, v1d, cu1d, 700, out=outs[0], workspace=ws1)
+        fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 64, out=outs[1], workspace=ws2)
+        fmha_amd.fmha_decode_strided(q1d, kb.transpose(1, 2), vb.transpose(1, 2), seqlens_kv=lens1, out=outs[2],
+                                     workspace=ws3)
+        fmha_amd.fmha_decode_paged(q1d, kc, vc, bt, lens1, out=outs[3], max_seqlen_kv=700, workspace=ws4)
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    assert torch.equal(eager[0].view(torch.int16), eager[2].view(torch.int16))
+    assert torch.equal(eager[0].view(torch.int16), eager[3].view(torch.int16))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        calls()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        ws1.fill_(255)
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
+        fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 64)
+        torch.cuda.synchronize()

@@ -19,6 +19,14 @@ def test_fake_impl_shapes_without_gpu():
         q3 = torch.empty(4, 8, 64, dtype=torch.bfloat16, device="cuda")
         ku = torch.empty(4, 3, 8, 64, dtype=torch.bfloat16, device="cuda")
         assert torch.ops.fmha_amd.decode(q3, ku, ku, None, 3, 0.125).shape == q3.shape
+        ks = torch.empty(400, 2, 128, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.fmha_amd.decode_splitkv(q, ks, ks, cu, 100, 0.0).shape == q.shape
+        kb = torch.empty(4, 2, 300, 128, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+        lens = torch.empty(4, dtype=torch.int32, device="cuda")
+        assert torch.ops.fmha_amd.decode_strided(q, kb, kb, lens, 0.0).dtype == torch.float16
+        kc = torch.empty(40, 16, 2, 128, dtype=torch.bfloat16, device="cuda")
+        bt = torch.empty(4, 10, dtype=torch.int32, device="cuda")
+        assert torch.ops.fmha_amd.decode_paged(q, kc, kc, bt, lens, 0.0, 160).shape == q.shape
 
 
 @pytest.mark.gpu
@@ -68,3 +76,58 @@ def test_opcheck_and_compile():
     o2 = f(*args[:4])
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+@pytest.mark.gpu
+def test_layout_ops_match_direct_calls():
+    """decode_splitkv / decode_strided / decode_paged give the bits of the
+    direct calls, pass opcheck, and run under torch.compile."""
+    import torch
+    import fmha_amd
+    import fmha_amd.torch_ops  # noqa: F401
+    B, Hq, Hkv, D, S = 6, 16, 4, 128, 200
+    seqlens = np.array([200, 17, 0, 150, 3, 99], np.int32)
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=1002)
+    qd, kd, vd, cud = to_dev(q), to_dev(k), to_dev(v), torch.from_numpy(cu).cuda()
+    lens = torch.from_numpy(seqlens).cuda()
+    o_sk = torch.ops.fmha_amd.decode_splitkv(qd, kd, vd, cud, S, 0.0)
+    # the same rows as a BHSD cache and as a paged cache of 16-row pages
+    kb = torch.zeros(B, Hkv, S, D, dtype=torch.bfloat16, device="cuda")
+    vb = torch.zeros_like(kb)
+    pages_per = (S + 15) // 16
+    kc = torch.zeros(B * pages_per, 16, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(B * pages_per, dtype=torch.int32, device="cuda").flip(0).view(B, pages_per).contiguous()
+    for b in range(B):
+        rows = slice(int(cu[b]), int(cu[b + 1]))
+        n = int(seqlens[b])
+        kb[b, :, :n] = kd[rows].transpose(0, 1)
+        vb[b, :, :n] = vd[rows].transpose(0, 1)
+        for j in range(0, n, 16):
+            m = min(16, n - j)
+            kc[bt[b, j // 16], :m] = kd[int(cu[b]) + j:int(cu[b]) + j + m]
+            vc[bt[b, j // 16], :m] = vd[int(cu[b]) + j:int(cu[b]) + j + m]
+    o_st = torch.ops.fmha_amd.decode_strided(qd, kb.transpose(1, 2), vb.transpose(1, 2), lens, 0.0)
+    o_pg = torch.ops.fmha_amd.decode_paged(qd, kc, vc, bt, lens, 0.0, S)
+    torch.cuda.synchronize()
+    assert torch.equal(o_sk.view(torch.int16),
+                       fmha_amd.fmha_decode_splitkv(qd, kd, vd, cud, S).view(torch.int16))
+    assert torch.equal(o_st.view(torch.int16),
+                       fmha_amd.fmha_decode_strided(qd, kb.transpose(1, 2), vb.transpose(1, 2),
+                                                    seqlens_kv=lens).view(torch.int16))
+    assert torch.equal(o_pg.view(torch.int16),
+                       fmha_amd.fmha_decode_paged(qd, kc, vc, bt, lens, max_seqlen_kv=S).view(torch.int16))
+    from tests.common import assert_pass
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True, max_seqlen=S)
+    for name, o in (("splitkv", o_sk), ("strided", o_st), ("paged", o_pg)):
+        assert_pass(oracle.compare(o.view(torch.int16).cpu().numpy().view(np.uint16), r, slack), f"op {name}")
+    tests = ("test_schema", "test_faketensor", "test_aot_dispatch_static")
+    torch.library.opcheck(torch.ops.fmha_amd.decode_splitkv.default, (qd, kd, vd, cud, S, 0.0), test_utils=tests)
+    torch.library.opcheck(torch.ops.fmha_amd.decode_paged.default, (qd, kc, vc, bt, lens, 0.0, S),
+                          test_utils=tests)
+
+    def f(q_, kc_, vc_, bt_, lens_):
+        return torch.ops.fmha_amd.decode_paged(q_, kc_, vc_, bt_, lens_, 0.0, S).float().sum(dim=-1)
+
+    g = torch.compile(f, backend="aot_eager", fullgraph=True)
+    assert torch.equal(g(qd, kc, vc, bt, lens), f(qd, kc, vc, bt, lens))
