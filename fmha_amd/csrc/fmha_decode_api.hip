@@ -252,22 +252,36 @@ struct SplitPlan {
   size_t off_t = 0, off_m = 0, off_l = 0, off_ml = 0, off_opart = 0, total = 0;
 };
 
-// Waves the P.V pass aims for: 8 per CU.  Each holds two sub-blocks of V
-// (up to 32 KiB) in flight.
-constexpr int64_t kSplitTargetWaves = 2048;
+// P.V waves the split pass aims for.  A wave keeps two sub-blocks of V in
+// flight: 2 * 16 rows of 1 KiB (the wave's heads' share of a row) for G <= 4,
+// half that for G = 8 (8-row sub-blocks), and less again when the batch has
+// fewer KV heads than a wave holds (idle lanes).  The target is 512 waves of
+// the full kind, scaled up by those two factors, so that the V requests in
+// flight per CU stay about the same and the pass runs in one round of long
+// waves: fewer, longer chunks also mean fewer partial outputs to combine.
+// Measured against a fixed 2048 (µs): B=1 S=131072 Hq=32 Hkv=8 D=128
+// 118.4 -> 105.5; B=64 S=4096 200.5 -> 188.7; B=16 Hq=16 Hkv=8 S=8192 D=256
+// 186.7 -> 175.5; B=32 Hq=64 Hkv=8 S=8192 234.0 -> 216.5; B=4 Hq=32 Hkv=4
+// S=32768 D=64 (half the lanes idle) 72.0 -> 72.1; B=256 Hq=64 Hkv=8 S=1024
+// 230.1 -> 240.1, the one shape measured slower.
+int64_t split_target_waves(int hq, int hkv, int d) {
+  const int heads_per_wave = kWaveSize / (d / 8);
+  const int g = hq / hkv;
+  const int active = hkv < heads_per_wave ? hkv : heads_per_wave;
+  return (int64_t)512 * (g >= 8 ? 2 : 1) * heads_per_wave / active;
+}
 
 // Scores: one wave per 16-row block.  P.V: chunks of C rows (C in
 // {64, ..., 512}, or the rows' own multiple of 16 when shorter), the largest
-// that still gives kSplitTargetWaves waves where the work allows, so the
-// partial outputs (4*D bytes per chunk and query head) stay a few percent
-// of V.
+// that still gives split_target_waves waves where the work allows.
 SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
   SplitPlan p;
   const int heads_per_wave = kWaveSize / (d / 8);
   const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
   p.units = upb * batch;
+  const int64_t target = split_target_waves(hq, hkv, d);
   int c = 512;
-  while (c > 64 && p.units * ((max_rows + c - 1) / c) < kSplitTargetWaves) c /= 2;
+  while (c > 64 && p.units * ((max_rows + c - 1) / c) < target) c /= 2;
   const int fit = max_rows <= 16 ? 16 : (max_rows + 15) / 16 * 16;  // no longer than the rows need
   if (c > fit) c = fit;
   p.chunk_rows = c;
@@ -290,10 +304,10 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
 }
 
 // Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
-// Scores waves request 32 KiB of K plus G KiB of Q at once; P.V waves keep
+// Scores waves request 16 KiB of K plus G KiB of Q at once; P.V waves keep
 // two 16-row (8-row for G = 8) sub-blocks of V in flight.  Sweeps over
 // long-context shapes (B=64 S=4096, B=8 S=32768, B=256 S=1024 G=8, B=1
-// S=131072) put both optima at 8; 3 or 4 scores waves cost 5-20%.
+// S=131072) put both optima at 8 (4-6 cost 2-5%, 12-16 within 1%).
 constexpr int kSplitScoresWavesPerCU = 8;
 constexpr int kSplitPvWavesPerCU = 8;
 
@@ -332,7 +346,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   // The combine grid has one workgroup per (batch, query head, 32 dims).
   if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
-  constexpr int NB = 2;                // 16-row blocks per scores wave
+  constexpr int NB = 1;                // 16-row blocks per scores wave (2 measured 1-3% slower)
   const uint32_t upb = (uint32_t)a.units_per_batch;
   const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
   const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;

@@ -19,6 +19,20 @@ def _run(q, k, v, cu, Hq, Hkv, D, max_len):
     return o.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def _plan(B, Hq, Hkv, max_len, D):
+    """(chunks, blocks) of the split-KV plan (plan_split in
+    fmha_decode_api.hip): P.V chunks of C rows, C the largest of 512, 256,
+    ..., 64 that still gives the target number of waves, 16-row blocks."""
+    hpw = 64 // (D // 8)
+    units = B * ((Hkv + hpw - 1) // hpw)
+    target = 512 * (2 if Hq // Hkv >= 8 else 1) * hpw // min(Hkv, hpw)
+    c = 512
+    while c > 64 and units * ((max_len + c - 1) // c) < target:
+        c //= 2
+    c = min(c, max(16, (max_len + 15) // 16 * 16))
+    return (max_len + c - 1) // c, (max_len + 15) // 16
+
+
 def _case(B, Hq, Hkv, D, seqlens, max_len, seed, std=1.0):
     q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed, std)
     o = _run(q, k, v, cu, Hq, Hkv, D, max_len)
@@ -41,22 +55,24 @@ def test_varlen_long(D, Hq, Hkv, max_len):
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 16, 2), (256, 8, 8)])
 def test_block_boundaries(D, Hq, Hkv):
-    """Lengths on and next to the 16-row block edges: a scores wave whose
-    second block is partly or wholly past the row's end."""
+    """Lengths on and next to the 16-row block edges: scores waves whose
+    block is partly past the row's end, P.V sub-blocks likewise."""
     seqlens = np.array([16, 32, 48, 31, 33, 47, 15, 17, 1, 64], np.int32)
     _case(len(seqlens), Hq, Hkv, D, seqlens, 64, seed=11 + D)
 
 
 def test_mid_chunk_count():
-    """16 < chunks <= 256 (the 256-thread combine) with two heads per KV head."""
+    """16 < chunks <= 256 (the 256-thread combine) with four query heads per KV head."""
+    assert 16 < _plan(4, 32, 8, 8192, 128)[0] <= 256
     rng = np.random.default_rng(12)
-    seqlens = rng.integers(6000, 8193, size=16).astype(np.int32)
+    seqlens = rng.integers(6000, 8193, size=4).astype(np.int32)
     seqlens[0] = 8192
-    _case(16, 32, 8, 128, seqlens, 8192, seed=12, std=0.5)
+    _case(4, 32, 8, 128, seqlens, 8192, seed=12, std=0.5)
 
 
 def test_mid_block_count():
     """512 < blocks <= 2048 (the 256-thread statistics) on one long row."""
+    assert 512 < _plan(1, 32, 8, 20000, 128)[1] <= 2048
     _case(1, 32, 8, 128, np.array([20000], np.int32), 20000, seed=13, std=0.5)
 
 
@@ -76,11 +92,16 @@ def test_short_lengths_match_short_path(max_len):
 
 def test_many_batches_direct_path():
     """max length fits one chunk: the PV kernel writes O directly."""
+    assert _plan(200, 8, 8, 40, 128)[0] == 1
     seqlens = np.random.default_rng(3).integers(0, 41, size=200).astype(np.int32)
     _case(200, 8, 8, 128, seqlens, 40, seed=6)
 
 
 def test_one_long_sequence():
+    """More than 256 chunks (the 1024-thread combine), more than 2048 blocks
+    (the 1024-thread statistics)."""
+    chunks, blocks = _plan(1, 32, 8, 40000, 128)
+    assert chunks > 256 and blocks > 2048
     _case(1, 32, 8, 128, np.array([40000], np.int32), 40000, seed=7, std=0.5)
 
 
