@@ -346,14 +346,25 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   // The combine grid has one workgroup per (batch, query head, 32 dims).
   if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
-  constexpr int NB = 1;                // 16-row blocks per scores wave (2 measured 1-3% slower)
-  const uint32_t upb = (uint32_t)a.units_per_batch;
-  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + NB - 1) / NB) * upb;
-  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)a.nchunks * upb;
+  // With fewer KV heads than a wave holds, its lane groups serve 2^shift
+  // blocks (scores) or chunks (P.V) of the same heads instead of idling:
+  // packed and strided layouts, whose descriptor spans the batch's rows
+  // (the paged ones address one page at a time).  One block per scores
+  // wave otherwise (two measured 1-3% slower).
+  constexpr int HPW = kWaveSize / (D / 8);
+  int shift = 0;
+  if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+    while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
+  SplitArgs as = a;
+  as.sub_shift = shift;
+  as.units_per_batch = (a.num_heads_kv + (HPW >> shift) - 1) / (HPW >> shift);
+  const uint32_t upb = (uint32_t)as.units_per_batch;
+  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + (1 << shift) - 1) >> shift) * upb;
+  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)((a.nchunks + (1 << shift) - 1) >> shift) * upb;
   {
-    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, NB, LAYOUT>;
+    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, as);
   }
   const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
   // One lane per (batch, query head) for rows of at most 16 blocks, else one
@@ -368,15 +379,17 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   else
     hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
   if (a.nchunks == 1) {
+    // One chunk per batch: the P.V wave writes O itself, one chunk per wave.
     constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
+    const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
+    hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, a);
     return hipGetLastError();
   }
   {
     constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
-                       stream, a);
+                       stream, as);
   }
   if (a.nchunks <= 16) {
     const uint64_t lanes = (uint64_t)heads * (D / 8);

@@ -70,6 +70,22 @@ struct SplitArgs {
   const int32_t* block_table;
   int32_t bt_stride;
   int32_t page_shift;
+  // log2 of the sub-units per wave (scores, P.V): with fewer KV heads than a
+  // wave holds, its lane groups take 2^sub_shift blocks (scores) or chunks
+  // (P.V) of the same heads instead of idling (packed and strided layouts).
+  int32_t sub_shift;
+};
+
+// Lane groups of a wave under SplitArgs::sub_shift: group hkl (of HPW)
+// serves KV head hg * (HPW >> sub_shift) + hkl % (HPW >> sub_shift) for
+// sub-unit hkl / (HPW >> sub_shift).
+template <int HPW>
+struct SubUnits {
+  int shift;  // log2(heads per sub-unit)
+  __device__ __forceinline__ explicit SubUnits(int sub_shift) : shift(ilog2(HPW) - sub_shift) {}
+  __device__ __forceinline__ int heads() const { return 1 << shift; }
+  __device__ __forceinline__ int unit(int hkl) const { return hkl >> shift; }
+  __device__ __forceinline__ int head(uint32_t hg, int hkl) const { return (int)(hg << shift) + (hkl & (heads() - 1)); }
 };
 
 // Length of batch b (may be out of [0, max_rows]: the kernels check).
@@ -130,14 +146,22 @@ struct LongRows {
   const int32_t* pages;         // paged: this batch's block-table row
   uint32_t row_bytes;           // bytes between consecutive rows (slots)
   uint32_t lane_off;            // this lane's head and dims within a row
+  int lane_rows;                // rows from lo to this lane's first row (packed, strided)
+  int lane_n;                   // rows from lo at which this lane's rows end (packed, strided)
   uint32_t page_shift;
   uint64_t page_stride;         // elements
   int lo, n;                    // first row, rows in range
 
+  // lane_rows_: this lane's rows start that many rows after lo, and end at
+  // lane_end (relative to lo, at most hi - lo): lane groups serving
+  // different blocks or chunks.  Both 0 / hi - lo for the paged layouts.
   __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t row_base, int lo_,
-                                       int hi, int hk, bool head_ok, int r) {
+                                       int hi, int hk, bool head_ok, int r, int lane_rows_ = 0,
+                                       int lane_end = 1 << 30) {
     lo = lo_;
     n = hi > lo_ ? hi - lo_ : 0;
+    lane_rows = lane_rows_;
+    lane_n = lane_end < n ? lane_end : n;
     if constexpr (LAYOUT == kLayoutPacked) {
       row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
       lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
@@ -172,15 +196,14 @@ struct LongRows {
   template <int NR>
   __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
     static_assert(NR <= 16, "a sub-block fits a 16-row page");
-    if constexpr (LAYOUT == kLayoutPacked) {
+    if constexpr (LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided) {
+      // Rows past this lane's end are moved out of range (a strided range
+      // can also cover other heads' padding rows).
 #pragma unroll
-      for (int j = 0; j < NR; ++j) out[j] = buffer_load16_nt(rsrc, lane_off + (uint32_t)(rel0 + j) * row_bytes);
-    } else if constexpr (LAYOUT == kLayoutStrided) {
-      // The range can cover other heads' padding rows: rows past the end
-      // are moved out of range.
-#pragma unroll
-      for (int j = 0; j < NR; ++j)
-        out[j] = buffer_load16_nt(rsrc, lane_off + (rel0 + j < n ? (uint32_t)(rel0 + j) * row_bytes : kRowOutOfRange));
+      for (int j = 0; j < NR; ++j) {
+        const int row = rel0 + j + lane_rows;
+        out[j] = buffer_load16_nt(rsrc, lane_off + (row < lane_n ? (uint32_t)row * row_bytes : kRowOutOfRange));
+      }
     } else if constexpr (LAYOUT == kLayoutPagedBlock) {
       const int valid = n - rel0 < 0 ? 0 : (n - rel0 > NR ? NR : n - rel0);
       const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid);
@@ -214,10 +237,11 @@ __device__ __forceinline__ uint64_t t_block_base(const SplitArgs& a, uint64_t b,
   return ((b * (uint64_t)a.nblk + (uint64_t)blk) * (uint64_t)a.num_heads_q) * kSplitBlockRows;
 }
 
-// NB blocks of 16 rows per wave, all of their K rows requested at once.
-// The G query heads of a KV head are scored GH at a time against the same K
-// registers (GH = 4 bounds the partial sums a lane holds to 64).
-template <int D, int G, int NB, int LAYOUT = kLayoutPacked>
+// One 16-row block per lane group, all of its K rows requested at once: a
+// wave serves 2^sub_shift consecutive blocks (SubUnits).  The G query heads
+// of a KV head are scored GH at a time against the same K registers (GH = 4
+// bounds the partial sums a lane holds to 64).
+template <int D, int G, int LAYOUT = kLayoutPacked>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
@@ -232,9 +256,10 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   const int lane = threadIdx.x & (kWaveSize - 1);
   // Wave order (batch, block group, head group): consecutive waves read
   // neighbouring heads of the same rows.
+  const SubUnits<HPW> su(a.sub_shift);
   const uint32_t id = blockIdx.x;
   const uint32_t upb = (uint32_t)a.units_per_batch;
-  const uint32_t nwb = ((uint32_t)a.nblk + NB - 1) / NB;
+  const uint32_t nwb = ((uint32_t)a.nblk + (1u << a.sub_shift) - 1) >> a.sub_shift;
   const uint32_t per_b = nwb * upb;
   const uint32_t b = id / per_b;
   if (b >= (uint32_t)a.batch) return;
@@ -242,48 +267,43 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   const uint32_t wb = rem / upb;
   const uint32_t hg = rem - wb * upb;
   const int S = split_len_l<LAYOUT>(a, b);
-  const int j0 = (int)wb * NB * NR;
+  const int j0 = (int)(wb << a.sub_shift) * NR;  // the wave's first row
   if (S < 0 || S > a.max_rows || j0 >= S) return;
-  const int hk = (int)hg * HPW + lane / LPH;
+  const int hkl = lane / LPH;
+  const int p = su.unit(hkl);           // this lane group's block of the wave
+  const int hk = su.head(hg, hkl);
   const bool head_ok = hk < a.num_heads_kv;
   const int r = lane % LPH;
   const int hq = a.num_heads_q;
+  const int blk = (int)(wb << a.sub_shift) + p;
+  const int jb = j0 + p * NR;           // first row of this lane group's block
+  const bool block_ok = jb < S;         // else past the row (and maybe past nblk): no writes
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
   // Rows [0, S) of the batch: rows past S read 0 without access.
   LongRows<D, LAYOUT> kv;
-  kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, hk, head_ok, r);
+  kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, hk, head_ok, r, p * NR);
   const uint32_t q_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
 
   u32x4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, q_off + g * D * 2);
-  u32x4 kr[NB * NR];
-#pragma unroll
-  for (int q = 0; q < NB; ++q) {
-    u32x4 kq[NR];
-    kv.template load<NR>(kq, j0 + q * NR);
-#pragma unroll
-    for (int j = 0; j < NR; ++j) kr[q * NR + j] = kq[j];
-  }
+  u32x4 ks[NR];
+  kv.template load<NR>(ks, j0);
   __builtin_amdgcn_sched_barrier(0);
 
   // After the butterfly, lane r holds scores [blkl*W, blkl*W + W) of the
   // GH*NR (query head, row) pairs; lanes equal in r >> (NS - L) hold copies.
   const int blkl = r >> (NS - L);
-  const bool writer = head_ok && (r & ((1 << (NS - L)) - 1)) == 0;
-#pragma unroll
-  for (int q = 0; q < NB; ++q) {
-    const int blk = (int)wb * NB + q;
-    const int jb = j0 + q * NR;
-    if (jb >= S) break;
-    u32x4 ks[NR];
-#pragma unroll
-    for (int j = 0; j < NR; ++j) ks[j] = kr[q * NR + j];
-    // This block's scores [Hq][16], written non-temporally (read once, by
-    // the P.V pass): 4-6% faster on long-context shapes than default-policy
-    // stores.
-    const __amdgpu_buffer_rsrc_t t_rsrc = make_rsrc(a.t + t_block_base(a, b, blk), (uint32_t)hq * NR * 4u);
-    const uint32_t t_lane = head_ok ? (uint32_t)hk * G * NR * 4u : kLaneOutOfRange;
+  const bool writer = head_ok && block_ok && (r & ((1 << (NS - L)) - 1)) == 0;
+  {
+    // The wave's blocks' scores [Hq][16] each, written non-temporally (read
+    // once, by the P.V pass): 4-6% faster on long-context shapes than
+    // default-policy stores.  The range ends at the batch's last block.
+    const int wblk = (int)(wb << a.sub_shift);
+    const int nwblk = a.nblk - wblk < (1 << a.sub_shift) ? a.nblk - wblk : (1 << a.sub_shift);
+    const __amdgpu_buffer_rsrc_t t_rsrc =
+        make_rsrc(a.t + t_block_base(a, b, wblk), (uint32_t)nwblk * (uint32_t)hq * NR * 4u);
+    const uint32_t t_lane = head_ok ? ((uint32_t)p * hq + (uint32_t)hk * G) * NR * 4u : kLaneOutOfRange;
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GH) {
       u32x4 qh[GH];
@@ -465,7 +485,8 @@ struct PvSlots {
 template <int D, int G, int NR>
 __device__ __forceinline__ void pv_sub_block(const u32x4 (&vr)[NR], const float (&tv)[PvSlots<D, G, NR>::PER_LANE],
                                              const float (&gm)[PvSlots<D, G, NR>::PER_LANE],
-                                             const float (&gsum)[PvSlots<D, G, NR>::PER_LANE], int rows_left,
+                                             const float (&gsum)[PvSlots<D, G, NR>::PER_LANE],
+                                             const int (&rows_left)[PvSlots<D, G, NR>::PER_LANE],
                                              bool (&slot_ok)[PvSlots<D, G, NR>::PER_LANE], uint16_t* lds_p, int hkl,
                                              int lane, float (&acc)[G][8]) {
   using P = PvSlots<D, G, NR>;
@@ -474,7 +495,7 @@ __device__ __forceinline__ void pv_sub_block(const u32x4 (&vr)[NR], const float 
   for (int i = 0; i < P::PER_LANE; ++i) {
     const int f = lane + kWaveSize * i;
     const int jf = f % NR;
-    const bool valid = slot_ok[i] && jf < rows_left;
+    const bool valid = slot_ok[i] && jf < rows_left[i];
     const float p = valid ? expf(tv[i] - gm[i]) / gsum[i] : 0.0f;
     if (f < P::SLOTS)
       lds_p[(f / (G * NR)) * VP + ((f / NR) % G) * kMaxSeq + jf] = __builtin_bit_cast(uint16_t, (__bf16)p);
@@ -504,23 +525,30 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   static_assert(NR % 2 == 0 && NR <= kMaxSeq, "sub-block rows");
   __shared__ __attribute__((aligned(16))) uint16_t lds_p[HPW * VP];
   const int lane = threadIdx.x & (kWaveSize - 1);
+  // A wave serves 2^sub_shift consecutive chunks (one per lane group,
+  // SubUnits); DIRECT launches have one chunk per batch and sub_shift = 0.
+  const SubUnits<HPW> su(a.sub_shift);
   const uint32_t id = blockIdx.x;
   const uint32_t upb = (uint32_t)a.units_per_batch;
-  const uint32_t per_b = (uint32_t)a.nchunks * upb;
+  const uint32_t nwc = ((uint32_t)a.nchunks + (1u << a.sub_shift) - 1) >> a.sub_shift;
+  const uint32_t per_b = nwc * upb;
   const uint32_t b = id / per_b;
   if (b >= (uint32_t)a.batch) return;
   const uint32_t rem = id - b * per_b;
-  const uint32_t c = rem / upb;
-  const uint32_t hg = rem - c * upb;
+  const uint32_t wc = rem / upb;
+  const uint32_t hg = rem - wc * upb;
   const int S = split_len_l<LAYOUT>(a, b);
   const bool bad = S < 0 || S > a.max_rows;
-  const int row0 = (int)c * a.chunk_rows;
+  const int roww = (int)(wc << a.sub_shift) * a.chunk_rows;  // the wave's first row
   const int hkl = lane / LPH;
-  const int hk = (int)hg * HPW + hkl;
+  const int p = su.unit(hkl);
+  const uint32_t c = (wc << a.sub_shift) + (uint32_t)p;     // this lane group's chunk
+  const int row0 = (int)c * a.chunk_rows;
+  const int hk = su.head(hg, hkl);
   const bool head_ok = hk < a.num_heads_kv;
   const int r = lane % LPH;
   const int hq = a.num_heads_q;
-  if (bad || row0 >= S) {
+  if (bad || roww >= S) {
     // Only chunk 0 of a DIRECT launch owns the output of an empty or invalid
     // batch; the combine kernel covers them otherwise.
     if constexpr (DIRECT) {
@@ -533,29 +561,41 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     }
     return;
   }
+  // Rows of this lane group's chunk (<= 0: a chunk past the row's end).
   const int rows = min(S - row0, a.chunk_rows);
-  // The chunk's rows only: sub-blocks past its end read 0 without access.
+  const int rows_w = min(S - roww, a.chunk_rows);  // the wave's first chunk: the most rows
+  // Each lane group reads its own chunk's rows only: sub-blocks past its
+  // end read 0 without access.
   LongRows<D, LAYOUT> vrows;
-  vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), row0, row0 + rows, hk, head_ok, r);
+  const int rowe = S - roww < (a.chunk_rows << a.sub_shift) ? S : roww + (a.chunk_rows << a.sub_shift);
+  vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), roww, rowe, hk, head_ok, r, row0 - roww,
+             row0 - roww + (rows > 0 ? rows : 0));
   // This batch's scores, [nblk, Hq, 16].
   const __amdgpu_buffer_rsrc_t t_rsrc =
       make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * kSplitBlockRows * 4u);
-  const int hk0 = hk - hkl;  // first KV head of this wave
 
+  // Weight slot f = lane + 64*i is (wave lane group f / (G*NR), query g =
+  // (f / NR) % G, row f % NR); the lane group gives its head and chunk.
   float gm[PL], gsum[PL];
   uint32_t t_off[PL];
   bool slot_ok[PL];
+  int slot_rows[PL];
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int f = lane + kWaveSize * i;
-    const int hkf = hk0 + f / (G * NR);
+    const int hklf = f / (G * NR);
+    const int hkf = su.head(hg, hklf);
     const int gf = (f / NR) % G;
     const int jf = f % NR;
-    slot_ok[i] = f < P::SLOTS && hkf < a.num_heads_kv;
+    const int row0f = (int)((wc << a.sub_shift) + (uint32_t)su.unit(hklf)) * a.chunk_rows;
+    slot_rows[i] = min(S - row0f, a.chunk_rows);
+    slot_ok[i] = f < P::SLOTS && hkf < a.num_heads_kv && slot_rows[i] > 0;
     const uint64_t hqi = (uint64_t)b * hq + hkf * G + gf;
     gm[i] = slot_ok[i] ? a.ml[2 * hqi] : 0.0f;
     gsum[i] = slot_ok[i] ? a.ml[2 * hqi + 1] : 1.0f;
-    t_off[i] = slot_ok[i] ? (uint32_t)((hkf * G + gf) * kSplitBlockRows + jf) * 4u : kLaneOutOfRange;
+    t_off[i] = slot_ok[i] ? (uint32_t)((row0f / kSplitBlockRows) * hq * kSplitBlockRows +
+                                       (hkf * G + gf) * kSplitBlockRows + jf) * 4u
+                          : kLaneOutOfRange;
   }
 
   float acc[G][8];
@@ -565,25 +605,34 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
 
   // Two register sets: sub-block s+1 is requested before s is processed.
-  // Requests past the chunk's last row return 0 without memory access (V)
-  // or read scores of other rows that the row check masks (T).
-  const int nsub = (rows + NR - 1) / NR;
+  // Requests past a chunk's last row return 0 without memory access (V)
+  // or read scores of other rows (or nothing, past the batch's blocks) that
+  // the row check masks (T).  The wave runs as many sub-blocks as its first
+  // chunk has.
+  const int nsub = (rows_w + NR - 1) / NR;
   u32x4 va[NR], vb[NR];
   float ta[PL], tb[PL];
   auto load = [&](u32x4 (&vr)[NR], float (&tv)[PL], int s) {
     vrows.template load<NR>(vr, s * NR);
-    // Sub-blocks never straddle a 16-row block (row0 is a multiple of 16).
-    const uint32_t sub = (uint32_t)(((row0 + s * NR) / kSplitBlockRows) * hq * kSplitBlockRows +
+    // Sub-blocks never straddle a 16-row block (chunks start on multiples of 16).
+    const uint32_t sub = (uint32_t)(((s * NR) / kSplitBlockRows) * hq * kSplitBlockRows +
                                     (s * NR) % kSplitBlockRows) * 4u;
 #pragma unroll
     for (int i = 0; i < PL; ++i) tv[i] = buffer_load_f32(t_rsrc, t_off[i] + sub);
   };
+  auto left = [&](int (&rl)[PL], int s) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) rl[i] = slot_rows[i] - s * NR;
+  };
   load(va, ta, 0);
   for (int s = 0; s < nsub; s += 2) {
+    int rl[PL];
     load(vb, tb, s + 1);
-    pv_sub_block<D, G, NR>(va, ta, gm, gsum, rows - s * NR, slot_ok, lds_p, hkl, lane, acc);
+    left(rl, s);
+    pv_sub_block<D, G, NR>(va, ta, gm, gsum, rl, slot_ok, lds_p, hkl, lane, acc);
     load(va, ta, s + 2);
-    if (s + 1 < nsub) pv_sub_block<D, G, NR>(vb, tb, gm, gsum, rows - (s + 1) * NR, slot_ok, lds_p, hkl, lane, acc);
+    left(rl, s + 1);
+    if (s + 1 < nsub) pv_sub_block<D, G, NR>(vb, tb, gm, gsum, rl, slot_ok, lds_p, hkl, lane, acc);
   }
 
   if constexpr (DIRECT) {
@@ -598,7 +647,8 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     const uint32_t part_bytes = (uint32_t)a.nchunks * D * 4u;
     const __amdgpu_buffer_rsrc_t p_rsrc =
         make_rsrc(a.opart + (uint64_t)b * hq * a.nchunks * D, (uint32_t)hq * part_bytes);
-    const uint32_t p_off = head_ok ? (uint32_t)hk * G * part_bytes + (c * D + r * 8) * 4u : kLaneOutOfRange;
+    // A lane group whose chunk starts past the row's end writes nothing.
+    const uint32_t p_off = head_ok && rows > 0 ? (uint32_t)hk * G * part_bytes + (c * D + r * 8) * 4u : kLaneOutOfRange;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       u32x4 lo, hi;

@@ -191,3 +191,19 @@ def test_paged_short_bound_through_long_entry():
                                     max_seqlen_kv=10).float()
     torch.cuda.synchronize()
     assert torch.isnan(o2[3]).all()
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 8, 1), (64, 16, 2), (256, 8, 1)])
+def test_strided_long_sub_units(D, Hq, Hkv):
+    """BHSD with fewer KV heads than a wave holds (lane groups on different
+    blocks and chunks), NaN padding between the heads' rows."""
+    import fmha_amd
+    import torch
+    B, cap = 4, 1000
+    seqlens = np.array([1000, 999, 15, 400], np.int32)
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=1400 + D)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd sub-units D={D} Hq={Hq} Hkv={Hkv}")

@@ -168,3 +168,27 @@ def test_onepass_edge_lengths():
     o = oracle.f16_to_f32(_run(q, k, v, cu, Hq, Hkv, D, max_len).reshape(B, Hq, D))
     assert np.all(np.isnan(o[5])) and np.all(np.isfinite(np.delete(o, 5, axis=0)))
     assert np.all(o[0] == 0)
+
+
+# Fewer KV heads than a wave holds (64 / (D/8)): the split kernels give each
+# lane group its own block (scores) or chunk (P.V), 2^shift per wave.
+def _sub_units(Hkv, D):
+    hpw = 64 // (D // 8)
+    r = 1
+    while Hkv * r * 2 <= hpw and hpw % (Hkv * r * 2) == 0:
+        r *= 2
+    return r
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 1), (64, 16, 2), (64, 32, 4), (128, 8, 1), (128, 16, 2),
+                                     (256, 8, 1), (128, 4, 2)])
+@pytest.mark.parametrize("max_len", [300, 2050])
+def test_sub_units(D, Hq, Hkv, max_len):
+    """Lane groups serving different blocks and chunks: block and chunk
+    counts that are not multiples of the groups per wave, empty and short
+    rows next to long ones."""
+    assert _sub_units(Hkv, D) > 1
+    B = 5
+    assert not _onepass_taken(B, Hq, Hkv, D, max_len)
+    seqlens = np.array([max_len, 1, 0, max_len - 17, 33], np.int32)
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=1300 + D + Hkv + max_len)
