@@ -141,6 +141,40 @@ hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStrea
   }
 }
 
+// Batches with fewer KV heads than a wave holds: the wave serves R = HPW /
+// Hkv batches (fmha_decode_multi_kernel).  Returns log2 R (0: not used).
+int multi_shift(int hkv, int dq) {
+  const int hpw = kWaveSize / (dq / 8);
+  int shift = 0;
+  while ((hkv << (shift + 1)) <= hpw && hpw % (hkv << (shift + 1)) == 0) ++shift;
+  return shift;
+}
+
+template <int D, int G, int LAYOUT, bool PF32>
+hipError_t launch_multi_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32>;
+  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
+  return hipGetLastError();
+}
+
+template <int LAYOUT, bool PF32>
+hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t stream) {
+#define FMHA_DECODE_MULTI_G(DD)                                                  \
+  switch (g) {                                                                   \
+    case 1: return launch_multi_one<DD, 1, LAYOUT, PF32>(a, w, stream);          \
+    case 2: return launch_multi_one<DD, 2, LAYOUT, PF32>(a, w, stream);          \
+    case 4: return launch_multi_one<DD, 4, LAYOUT, PF32>(a, w, stream);          \
+    default: return launch_multi_one<DD, 8, LAYOUT, PF32>(a, w, stream);         \
+  }
+  switch (d) {
+    case 64: FMHA_DECODE_MULTI_G(64)
+    case 128: FMHA_DECODE_MULTI_G(128)
+    default: FMHA_DECODE_MULTI_G(256)
+  }
+#undef FMHA_DECODE_MULTI_G
+}
+
 // Waves per CU for a unit that moves `rows` K/V rows and G query heads:
 // each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
 // of Q in and 1 KiB of O out.  Caps of 16 or more are dropped (no cap).
@@ -207,6 +241,33 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   const int w = waves_per_cu_for(rows_hint, g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
+  // Fewer KV heads than a wave holds: R batches per wave, every lane busy.
+  // Strided only when R batches' spans fit one descriptor.
+  const int shift = layout == fmha_decode::kLayoutPaged ? 0 : multi_shift(a.num_heads_kv, dq);
+  bool multi = shift > 0;
+  if (multi && layout == fmha_decode::kLayoutStrided) {
+    const int64_t rows = a.max_rows > 0 ? a.max_rows : 1;
+    const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (rows - 1) * a.row_stride +
+                          (int64_t)(a.num_heads_kv - 1) * a.head_stride + dq) * 2;
+    multi = span < (int64_t(1) << 30);
+  }
+  if (multi) {
+    int hs = 0;
+    while ((1 << hs) < a.num_heads_kv) ++hs;
+    a.sub_shift = shift;
+    a.hkv_shift = hs;
+    a.units_per_batch = batch;  // the batch count, for this kernel
+    a.total_units = (uint32_t)(((int64_t)batch + (1 << shift) - 1) >> shift);
+    switch (layout) {
+      case fmha_decode::kLayoutPacked:
+        err = fp32_weights ? launch_multi<fmha_decode::kLayoutPacked, true>(a, dq, g, w, s)
+                           : launch_multi<fmha_decode::kLayoutPacked, false>(a, dq, g, w, s);
+        break;
+      default: err = launch_multi<fmha_decode::kLayoutStrided, false>(a, dq, g, w, s); break;
+    }
+    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+    return FMHA_DECODE_SUCCESS;
+  }
   switch (layout) {
     case fmha_decode::kLayoutPacked:
       err = fp32_weights ? launch_dim<fmha_decode::kLayoutPacked, true>(a, dq, g, sb, w, s)

@@ -93,6 +93,10 @@ struct DecodeArgs {
   int32_t units_per_batch;  // waves per batch: ceil(Hkv / HPW)
   uint32_t total_units;     // batch * units_per_batch
   float scale;
+  // fmha_decode_multi_kernel only: log2 of the batches per wave and of
+  // num_heads_kv (a power of two below the heads a wave holds).
+  int32_t sub_shift;
+  int32_t hkv_shift;
 };
 
 // One batch's K/V as the kernel reads it: byte strides relative to k/v, the
@@ -308,11 +312,14 @@ __device__ __forceinline__ u32x4 pack_f16x8(const float (&a)[8]) {
 }
 
 // ---------------------------------------------------------------------------
-// One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
+// Scores, masked softmax and P.V of one wave whose Q, K and V registers are
+// loaded (rows >= S read as 0): S valid rows (per lane group when the
+// groups serve different batches), weights through LDS slot
+// [hkl][g*16 + j] of lds_p, fp32 result per query head in acc.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX, int LAYOUT, bool PF32>
-__device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, const KVSpan& kv, int hk,
-                                            bool head_ok, int lane, uint16_t* lds_p) {
+template <int D, int G, int SMAX, bool PF32>
+__device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX], const u32x4 (&vr)[SMAX],
+                                            int S, float scale, int lane, uint16_t* lds_p, float (&acc)[G][8]) {
   constexpr int LPH = D / 8;                 // lanes per KV head
   constexpr int NS = ilog2(LPH);             // butterfly steps
   constexpr int V = G * SMAX;                // scores per KV head
@@ -321,9 +328,114 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   constexpr int GS = W < SMAX ? W : SMAX;    // scores of one query head inside a lane
   constexpr int C = ilog2(SMAX / GS);        // steps spanning one query head's lanes
   constexpr int VP = G * kMaxSeq;            // LDS bf16 slots per KV head
-
   const int r = lane % LPH;
   const int hkl = lane / LPH;
+
+  // ---- partial scores over this lane's 8 dims ----
+  float x[V];
+  partial_scores<G, SMAX>(qv, kr, x);
+
+  // ---- reduce over the head's lanes; lane keeps scores [blk*W, blk*W + W) ----
+  TransposeReduce<LPH, V, 0>::run(x, lane);
+  const int blk = r >> (NS - L);
+
+  // ---- masked softmax (per query head) ----
+  float p[W];
+#pragma unroll
+  for (int h0 = 0; h0 < W; h0 += GS) {
+    float t[GS];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < GS; ++w) {
+      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
+      const bool ok = j < S;
+      t[w] = x[h0 + w] * scale;
+      m = ok ? fmaxf(m, t[w]) : m;
+    }
+    m = GroupReduce<LPH, L - C, L, true>::run(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < GS; ++w) {
+      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
+      const bool ok = j < S;
+      t[w] = ok ? expf(t[w] - m) : 0.0f;
+      sum += t[w];
+    }
+    sum = GroupReduce<LPH, L - C, L, false>::run(sum);
+#pragma unroll
+    for (int w = 0; w < GS; ++w) p[h0 + w] = (sum > 0.0f) ? (t[w] / sum) : 0.0f;
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+
+  if constexpr (!PF32) {
+    // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
+    uint16_t* lds_head = lds_p + hkl * VP;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int vi = blk * W + w;
+      const int g = vi / SMAX;
+      const int j = vi % SMAX;
+      lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- P.V over row pairs ----
+    constexpr int NP = (SMAX + 1) / 2;
+    const uint32_t* lds_pairs = reinterpret_cast<const uint32_t*>(lds_head);
+    uint32_t pp[G][NP];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int jp = 0; jp < NP; ++jp) {
+        uint32_t w2 = lds_pairs[g * (kMaxSeq / 2) + jp];
+        if constexpr (SMAX == 1) w2 &= 0xffffu;  // slot 1 is not part of this bucket
+        pp[g][jp] = w2;
+      }
+    }
+    accumulate_pv<G, SMAX>(vr, pp, acc);
+  } else {
+    // ---- fp32 weights -> LDS slot [hkl][g*16 + j] (4 bytes each) ----
+    float* lds_head = reinterpret_cast<float*>(lds_p) + hkl * VP;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int vi = blk * W + w;
+      lds_head[(vi / SMAX) * kMaxSeq + vi % SMAX] = p[w];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- P.V row by row in row order, one fused multiply-add per element ----
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < SMAX; ++j) {
+        const float w = lds_head[g * kMaxSeq + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t x = vr[j][i];
+          acc[g][2 * i] = __builtin_fmaf(w, __builtin_bit_cast(float, x << 16), acc[g][2 * i]);
+          acc[g][2 * i + 1] = __builtin_fmaf(w, __builtin_bit_cast(float, x & 0xffff0000u), acc[g][2 * i + 1]);
+        }
+      }
+    }
+  }
+
+}
+
+// ---------------------------------------------------------------------------
+// One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
+// ---------------------------------------------------------------------------
+template <int D, int G, int SMAX, int LAYOUT, bool PF32>
+__device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, const KVSpan& kv, int hk,
+                                            bool head_ok, int lane, uint16_t* lds_p) {
+  constexpr int LPH = D / 8;  // lanes per KV head
+  const int r = lane % LPH;
   const int hq_count = a.num_heads_q;
 
   const int S = kv.S;
@@ -384,101 +496,8 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   // 1 + 2*SMAX requests of the unit are in flight before the first wait.
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- partial scores over this lane's 8 dims ----
-  float x[V];
-  partial_scores<G, SMAX>(qv, kr, x);
-
-  // ---- reduce over the head's lanes; lane keeps scores [blk*W, blk*W + W) ----
-  TransposeReduce<LPH, V, 0>::run(x, lane);
-  const int blk = r >> (NS - L);
-
-  // ---- masked softmax (per query head) ----
-  float p[W];
-#pragma unroll
-  for (int h0 = 0; h0 < W; h0 += GS) {
-    float t[GS];
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int w = 0; w < GS; ++w) {
-      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
-      const bool ok = j < S;
-      t[w] = x[h0 + w] * a.scale;
-      m = ok ? fmaxf(m, t[w]) : m;
-    }
-    m = GroupReduce<LPH, L - C, L, true>::run(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < GS; ++w) {
-      const int j = (W >= SMAX) ? w : ((blk & ((1 << C) - 1)) * W + w);
-      const bool ok = j < S;
-      t[w] = ok ? expf(t[w] - m) : 0.0f;
-      sum += t[w];
-    }
-    sum = GroupReduce<LPH, L - C, L, false>::run(sum);
-#pragma unroll
-    for (int w = 0; w < GS; ++w) p[h0 + w] = (sum > 0.0f) ? (t[w] / sum) : 0.0f;
-  }
-
   float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-
-  if constexpr (!PF32) {
-    // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
-    uint16_t* lds_head = lds_p + hkl * VP;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int vi = blk * W + w;
-      const int g = vi / SMAX;
-      const int j = vi % SMAX;
-      lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- P.V over row pairs ----
-    constexpr int NP = (SMAX + 1) / 2;
-    const uint32_t* lds_pairs = reinterpret_cast<const uint32_t*>(lds_head);
-    uint32_t pp[G][NP];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int jp = 0; jp < NP; ++jp) {
-        uint32_t w2 = lds_pairs[g * (kMaxSeq / 2) + jp];
-        if constexpr (SMAX == 1) w2 &= 0xffffu;  // slot 1 is not part of this bucket
-        pp[g][jp] = w2;
-      }
-    }
-    accumulate_pv<G, SMAX>(vr, pp, acc);
-  } else {
-    // ---- fp32 weights -> LDS slot [hkl][g*16 + j] (4 bytes each) ----
-    float* lds_head = reinterpret_cast<float*>(lds_p) + hkl * VP;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int vi = blk * W + w;
-      lds_head[(vi / SMAX) * kMaxSeq + vi % SMAX] = p[w];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- P.V row by row in row order, one fused multiply-add per element ----
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int j = 0; j < SMAX; ++j) {
-        const float w = lds_head[g * kMaxSeq + j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t x = vr[j][i];
-          acc[g][2 * i] = __builtin_fmaf(w, __builtin_bit_cast(float, x << 16), acc[g][2 * i]);
-          acc[g][2 * i + 1] = __builtin_fmaf(w, __builtin_bit_cast(float, x & 0xffff0000u), acc[g][2 * i + 1]);
-        }
-      }
-    }
-  }
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
@@ -592,6 +611,156 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
       decode_unit<D, G, 16, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Batches with fewer KV heads than a wave holds (Hkv < HPW = 64 / (D/8),
+// HPW a multiple of Hkv: MQA, or GQA after tensor-parallel sharding).  One
+// (batch, head group) per wave would leave 1 - Hkv/HPW of the lanes idle;
+// here the HPW lane groups serve R = HPW / Hkv consecutive batches, all Hkv
+// heads of each (lane group hkl: batch b0 + hkl / Hkv, head hkl % Hkv).
+// Packed and strided layouts: one descriptor spans the R batches' rows, each
+// lane group offsets its own batch's rows and ends them at its own length.
+// The KV bucket is the longest of the R lengths; arithmetic, numerics and
+// the NaN of an invalid length are those of fmha_decode_fwd_kernel.
+// ---------------------------------------------------------------------------
+
+// One wave of R batches, bucket SMAX.  kbase/vbase: the wave's first batch;
+// records: the descriptor range over the R batches; lane_rows: byte offset
+// of this lane group's batch from kbase; S: its length (0 when invalid).
+template <int D, int G, int SMAX, bool PF32>
+__device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t b0, uint32_t nb, const uint16_t* kbase,
+                                                  const uint16_t* vbase, uint32_t records, uint32_t lane_rows, int S,
+                                                  bool bad, bool lane_ok, int sub, int hk, int lane,
+                                                  uint16_t* lds_p) {
+  constexpr int LPH = D / 8;
+  const int r = lane % LPH;
+  const int hq = a.num_heads_q;
+  const uint32_t q_bytes = nb * (uint32_t)hq * D * 2u;
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b0 * hq * D, q_bytes);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, q_bytes);
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
+  const uint32_t row_bytes = (uint32_t)a.row_stride * 2u;
+  const uint32_t qo_off =
+      lane_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+  const uint32_t kv_off =
+      lane_ok ? lane_rows + (uint32_t)hk * (uint32_t)a.head_stride * 2u + (uint32_t)r * 16u : kLaneOutOfRange;
+  // Rows at or past this lane group's own length are moved out of range.
+  uint32_t row_off[SMAX];
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) row_off[j] = j < S ? (uint32_t)j * row_bytes : kRowOutOfRange;
+
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, qo_off + g * D * 2);
+  u32x4 kr[SMAX];
+  u32x4 vr[SMAX];
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + row_off[j]);
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float acc[G][8];
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
+  const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+#pragma unroll
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, bad ? nan4 : pack_f16x8(acc[g]));
+}
+
+// a.units_per_batch holds the batch count here, a.total_units the waves
+// (ceil(batch / R)); lengths from a.lens (packed: offsets, strided: lengths)
+// or a.seqlen_uniform when a.lens is null.
+template <int D, int G, int LAYOUT, bool PF32 = false>
+__global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(DecodeArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  constexpr int LPH = D / 8;
+  constexpr int HPW = kWaveSize / LPH;
+  constexpr int VP = G * kMaxSeq;
+  constexpr int WB = PF32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP * WB];
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+  const uint32_t unit = blockIdx.x * kWavesPerBlock + wave;
+  if (unit >= a.total_units) return;
+  const uint32_t batch = (uint32_t)a.units_per_batch;
+  const uint32_t b0 = unit << a.sub_shift;
+  const uint32_t nb = batch - b0 < (1u << a.sub_shift) ? batch - b0 : (1u << a.sub_shift);
+  const int hkl = lane / LPH;
+  const int sub = hkl >> a.hkv_shift;
+  const int hk = hkl & ((1 << a.hkv_shift) - 1);
+  const bool lane_ok = (uint32_t)sub < nb;
+  const uint32_t b = b0 + (lane_ok ? (uint32_t)sub : 0u);
+  const uint32_t row_bytes = (uint32_t)a.row_stride * 2u;
+  int S;
+  const uint16_t* kbase;
+  const uint16_t* vbase;
+  uint32_t records, lane_rows;
+  if constexpr (LAYOUT == kLayoutPacked) {
+    int32_t c0, ce, cb, cb1;
+    if (a.lens) {
+      c0 = a.lens[b0];
+      ce = a.lens[b0 + nb];
+      cb = a.lens[b];
+      cb1 = a.lens[b + 1];
+    } else {
+      c0 = (int32_t)b0 * a.seqlen_uniform;
+      ce = (int32_t)(b0 + nb) * a.seqlen_uniform;
+      cb = (int32_t)b * a.seqlen_uniform;
+      cb1 = cb + a.seqlen_uniform;
+    }
+    (void)ce;
+    S = cb1 - cb;
+    kbase = a.k + (int64_t)c0 * a.row_stride;
+    vbase = a.v + (int64_t)c0 * a.row_stride;
+    // This lane group's rows relative to the wave's first batch.  A batch
+    // that a broken table (a huge invalid length earlier in the wave) puts
+    // beyond the descriptor's reach counts as invalid too.
+    const int64_t rel = (int64_t)cb - c0;
+    if (rel < 0 || rel > (int64_t)((1u << 30) / row_bytes) - kMaxSeq) S = -1;
+    lane_rows = (uint32_t)(rel < 0 ? 0 : rel) * row_bytes;
+  } else {
+    S = a.lens ? a.lens[b] : a.seqlen_uniform;
+    kbase = a.k + (uint64_t)b0 * (uint64_t)a.batch_stride;
+    vbase = a.v + (uint64_t)b0 * (uint64_t)a.batch_stride;
+    const int rows = a.max_rows > 0 ? a.max_rows : 1;
+    records = ((uint32_t)(nb - 1) * (uint32_t)a.batch_stride + (uint32_t)(rows - 1) * (uint32_t)a.row_stride +
+               (uint32_t)((1 << a.hkv_shift) - 1) * (uint32_t)a.head_stride + D) * 2u;
+    lane_rows = (uint32_t)sub * (uint32_t)a.batch_stride * 2u;
+  }
+  const bool bad = lane_ok && (S < 0 || S > a.max_rows);
+  if (bad || !lane_ok) {
+    // Nothing to read: every row out of range (offsets below 2^31 + 2^30).
+    S = 0;
+    lane_rows = 0;
+  }
+  // The longest length of the wave picks the bucket (a uniform value); the
+  // packed descriptor ends at the last row a valid lane group reads.
+  int smax = S;
+  uint32_t end = LAYOUT == kLayoutPacked ? lane_rows + (uint32_t)S * row_bytes : 0u;
+#pragma unroll
+  for (int m = 1; m < kWaveSize; m <<= 1) {
+    smax = max(smax, __shfl_xor(smax, m, kWaveSize));
+    if constexpr (LAYOUT == kLayoutPacked) end = max(end, (uint32_t)__shfl_xor((int)end, m, kWaveSize));
+  }
+  smax = __builtin_amdgcn_readfirstlane(smax);
+  if constexpr (LAYOUT == kLayoutPacked) records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
+  uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
+#define FMHA_DECODE_MULTI(SM)                                                                                  \
+  decode_multi_unit<D, G, SM, PF32>(a, b0, nb, kbase, vbase, records, lane_rows, S, bad, lane_ok, sub, hk, lane, \
+                                    lds_wave)
+  if (smax <= 1)
+    FMHA_DECODE_MULTI(1);
+  else if (smax <= 2)
+    FMHA_DECODE_MULTI(2);
+  else if (smax <= 4)
+    FMHA_DECODE_MULTI(4);
+  else if (smax <= 8)
+    FMHA_DECODE_MULTI(8);
+  else
+    FMHA_DECODE_MULTI(16);
+#undef FMHA_DECODE_MULTI
 }
 
 }  // namespace fmha_decode
