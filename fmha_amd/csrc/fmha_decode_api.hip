@@ -384,38 +384,60 @@ constexpr int64_t kOnepassMinUnits = 512;
 constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
 constexpr int kOnepassWavesPerCU = 8;
 
+// Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
+// the KV-head groups of one.
+int64_t onepass_waves(const SplitArgs& a) {
+  return (((int64_t)a.batch + (1 << a.sub_shift) - 1) >> a.sub_shift) * a.units_per_batch;
+}
+
 template <int D, int G>
 bool onepass_fits(const SplitArgs& a) {
-  return (int64_t)a.batch * a.units_per_batch >= kOnepassMinUnits &&
+  return onepass_waves(a) >= kOnepassMinUnits &&
          fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
 }
 
-template <int D, int G, int LAYOUT>
+template <int D, int G, int LAYOUT, bool MULTI>
 hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT>;
+  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>;
   const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
   const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
-  const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
-  hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), need > cap ? need : cap, stream, a);
+  hipLaunchKernelGGL(kernel, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
+                     a);
   return hipGetLastError();
 }
 
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
 template <int D, int G, int LAYOUT>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
-  if (onepass_fits<D, G>(a)) return launch_onepass_dg<D, G, LAYOUT>(a, stream);
-  // The combine grid has one workgroup per (batch, query head, 32 dims).
-  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
-  constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
   // With fewer KV heads than a wave holds, its lane groups serve 2^shift
-  // blocks (scores) or chunks (P.V) of the same heads instead of idling:
-  // packed and strided layouts, whose descriptor spans the batch's rows
-  // (the paged ones address one page at a time).  One block per scores
-  // wave otherwise (two measured 1-3% slower).
+  // batches (single pass), blocks (scores) or chunks (P.V) instead of
+  // idling: packed and strided layouts, whose descriptor spans the rows
+  // (the paged ones address one page at a time).
   constexpr int HPW = kWaveSize / (D / 8);
   int shift = 0;
   if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
+  {
+    // The single pass spans 2^shift batches with one descriptor: for the
+    // strided layout only when their span stays below 1 GiB.
+    SplitArgs ao = a;
+    ao.sub_shift = shift;
+    if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
+      const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
+                            (int64_t)(a.num_heads_kv - 1) * a.head_stride + D) * 2;
+      if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
+    }
+    ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
+    if (onepass_fits<D, G>(ao)) {
+      if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+        if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
+      return launch_onepass_dg<D, G, LAYOUT, false>(ao, stream);
+    }
+  }
+  // The combine grid has one workgroup per (batch, query head, 32 dims).
+  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
+  constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
+  // One block per scores wave otherwise (two measured 1-3% slower).
   SplitArgs as = a;
   as.sub_shift = shift;
   as.units_per_batch = (a.num_heads_kv + (HPW >> shift) - 1) / (HPW >> shift);

@@ -48,7 +48,10 @@ constexpr size_t onepass_lds_bytes(int sp) {
   return (size_t)OnepassShape<D, G>::HPW * G * sp * 6;
 }
 
-template <int D, int G, int LAYOUT = kLayoutPacked>
+// MULTI: several batches per wave (fewer KV heads than a wave holds,
+// SplitArgs::sub_shift > 0; packed and strided layouts); otherwise one
+// batch per wave with its length read once for the whole wave.
+template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false>
 __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs a) {
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
@@ -65,36 +68,99 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   extern __shared__ __attribute__((aligned(16))) float onepass_lds[];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
-  const uint32_t unit = blockIdx.x;
-  const uint32_t upb = (uint32_t)a.units_per_batch;
-  const uint32_t b = unit / upb;
-  if (b >= (uint32_t)a.batch) return;
-  const uint32_t hg = unit - b * upb;
   const int hkl = lane / LPH;
   const int r = lane % LPH;
-  const int hk = (int)hg * HPW + hkl;
-  const bool head_ok = hk < a.num_heads_kv;
   const int hq = a.num_heads_q;
-  const int S = split_len_l<LAYOUT>(a, b);
-  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
-  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
-  if (S <= 0 || S > a.max_rows) {
-    // Empty rows give 0 (the reference loop's result), invalid ones NaN.
-    const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+  const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+  uint32_t b0, nb, b;
+  int sub, hk, S, smax, rel_rows = 0;
+  bool head_ok, bad = false;
+  if constexpr (!MULTI) {
+    // One (batch, KV-head group) per wave; the length is the wave's.
+    const uint32_t unit = blockIdx.x;
+    const uint32_t upb = (uint32_t)a.units_per_batch;
+    b = unit / upb;
+    if (b >= (uint32_t)a.batch) return;
+    const uint32_t hg = unit - b * upb;
+    b0 = b;
+    nb = 1;
+    sub = 0;
+    hk = (int)hg * HPW + hkl;
+    head_ok = hk < a.num_heads_kv;
+    S = split_len_l<LAYOUT>(a, b);
+    smax = S;
+    if (S <= 0 || S > a.max_rows) {
+      // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+      const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
+      const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+      const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : nan4;
 #pragma unroll
-    for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, fill);
-    return;
+      for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, fill);
+      return;
+    }
+  } else {
+    // The lane groups serve 2^sub_shift consecutive batches (SubUnits);
+    // lengths are per lane group and the loops run to the longest.
+    const SubUnits<HPW> su(a.sub_shift);
+    const uint32_t unit = blockIdx.x;
+    const uint32_t upb = (uint32_t)a.units_per_batch;
+    const uint32_t bw = unit / upb;
+    b0 = bw << a.sub_shift;
+    if (b0 >= (uint32_t)a.batch) return;
+    const uint32_t hg = unit - bw * upb;
+    nb = (uint32_t)a.batch - b0 < (1u << a.sub_shift) ? (uint32_t)a.batch - b0 : (1u << a.sub_shift);
+    sub = su.unit(hkl);
+    const bool lane_ok = (uint32_t)sub < nb;
+    b = b0 + (lane_ok ? (uint32_t)sub : 0u);
+    hk = su.head(hg, hkl);
+    head_ok = lane_ok && hk < a.num_heads_kv;
+    S = split_len_l<LAYOUT>(a, b);
+    bad = lane_ok && (S < 0 || S > a.max_rows);
+    if constexpr (LAYOUT == kLayoutPacked) {
+      // This batch's rows relative to the wave's first batch; one that a
+      // broken table puts beyond the descriptor's reach counts as invalid.
+      const int64_t rel = (int64_t)a.cu[b] - a.cu[b0];
+      if (rel < 0 || rel > (int64_t)((1u << 30) / ((uint32_t)a.num_heads_kv * D * 2u)) - a.max_rows) bad = lane_ok;
+      else rel_rows = (int)rel;
+    }
+    if (bad || !lane_ok) {
+      S = 0;
+      rel_rows = 0;
+    }
+    smax = S;
+#pragma unroll
+    for (int k = 1; k < kWaveSize; k <<= 1) smax = max(smax, __shfl_xor(smax, k, kWaveSize));
+    smax = __builtin_amdgcn_readfirstlane(smax);
+    if (smax == 0) {
+      // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+      const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, nb * (uint32_t)hq * D * 2u);
+      const uint32_t qo_off =
+          head_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+      const u32x4 fill = bad ? nan4 : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, fill);
+      return;
+    }
   }
+  const uint32_t q_bytes = nb * (uint32_t)hq * D * 2u;
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, q_bytes);
+  const uint32_t qo_off =
+      head_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
   const int sp = onepass_lds_rows(a.nblk);  // LDS row stride
   float* sc = onepass_lds + (size_t)hkl * G * sp;                                         // [G][sp] fp32
   uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sp) + (size_t)hkl * G * sp;  // [G][sp]
 
-  // Rows [0, S) of the batch: later rows read 0 without access.
-  const int64_t row_base = split_row_base<LAYOUT>(a, b);
+  // Rows [0, S) of each lane group's batch: later rows read 0 without access.
   LongRows<D, LAYOUT> krows, vrows;
-  krows.init(a, a.k, b, row_base, 0, S, hk, head_ok, r);
-  vrows.init(a, a.v, b, row_base, 0, S, hk, head_ok, r);
-  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
+  if constexpr (!MULTI) {
+    const int64_t row_base = split_row_base<LAYOUT>(a, b);
+    krows.init(a, a.k, b, row_base, 0, S, hk, head_ok, r);
+    vrows.init(a, a.v, b, row_base, 0, S, hk, head_ok, r);
+  } else {
+    krows.init_multi(a, a.k, b0, nb, b, S, rel_rows, hk, head_ok, r);
+    vrows.init_multi(a, a.v, b0, nb, b, S, rel_rows, hk, head_ok, r);
+  }
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b0 * hq * D, q_bytes);
 
   u32x4 qv[G];
 #pragma unroll
@@ -103,7 +169,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   // ---- 1. scores of every row -> LDS ----
   const int blkl = r >> (NS - L);
   const bool writer = (r & ((1 << (NS - L)) - 1)) == 0;
-  const int nsub = ((S + NR - 1) / NR + 1) / 2 * 2;  // even
+  const int nsub = ((smax + NR - 1) / NR + 1) / 2 * 2;  // even
   auto load_k = [&](u32x4 (&kr)[NR], int s) { krows.template load<NR>(kr, s * NR); };
   auto score = [&](const u32x4 (&kr)[NR], int s) {
 #pragma unroll
@@ -176,7 +242,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
 #pragma unroll
     for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
     uint16_t* p = pw + g * sp;
-    const int pad = (S + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
+    const int pad = (smax + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
     for (int j = j0; j < pad; j += LPG)
       p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? t[j] / l : 0.0f)) : (uint16_t)0;
   }
@@ -190,7 +256,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-  const int nsv = ((S + NRV - 1) / NRV + 1) / 2 * 2;  // even
+  const int nsv = ((smax + NRV - 1) / NRV + 1) / 2 * 2;  // even
   auto pv = [&](const u32x4 (&vr)[NRV], int s) {
     uint32_t pp[G][NRV / 2];
 #pragma unroll
@@ -212,7 +278,12 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
-  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, pack_f16x8(acc[g]));
+  for (int g = 0; g < G; ++g) {
+    if constexpr (MULTI)
+      buffer_store16(o_rsrc, qo_off + g * D * 2, bad ? nan4 : pack_f16x8(acc[g]));
+    else
+      buffer_store16(o_rsrc, qo_off + g * D * 2, pack_f16x8(acc[g]));
+  }
 }
 
 }  // namespace fmha_decode

@@ -183,6 +183,40 @@ struct LongRows {
     }
   }
 
+  // The rows of batches b0 .. b0+nb-1 through one descriptor (packed and
+  // strided; lane groups serving different batches): this lane's batch b
+  // has S rows (0: nothing is read).  Packed: rows relative to batch b0's
+  // first, rel_rows the lane's offset (checked by the caller: rel_rows + S
+  // rows stay below 2^30 bytes), the range ending at the last row any lane
+  // reads; strided: the nb batches' span with max_rows rows each (checked on
+  // the host).  load() then works as for init with lo = 0.
+  __device__ __forceinline__ void init_multi(const SplitArgs& a, const uint16_t* t, uint32_t b0, uint32_t nb,
+                                             uint32_t b, int S, int rel_rows, int hk, bool head_ok, int r) {
+    static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+    lo = 0;
+    if constexpr (LAYOUT == kLayoutPacked) {
+      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+      lane_rows = rel_rows;
+      lane_n = rel_rows + S;
+      int m = lane_n;
+#pragma unroll
+      for (int k = 1; k < kWaveSize; k <<= 1) m = max(m, __shfl_xor(m, k, kWaveSize));
+      n = __builtin_amdgcn_readfirstlane(m);
+      rsrc = make_rsrc(t + (uint64_t)a.cu[b0] * a.num_heads_kv * D, (uint32_t)n * row_bytes);
+    } else {
+      row_bytes = (uint32_t)a.row_stride * 2u;
+      lane_off = head_ok ? (uint32_t)(hk * a.head_stride + r * 8) * 2u + (b - b0) * (uint32_t)a.batch_stride * 2u
+                         : kLaneOutOfRange;
+      lane_rows = 0;
+      lane_n = S;
+      n = a.max_rows;
+      const uint32_t span = ((nb - 1) * (uint32_t)a.batch_stride + (uint32_t)(a.max_rows - 1) * (uint32_t)a.row_stride +
+                             (uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+      rsrc = make_rsrc(t + (uint64_t)b0 * (uint64_t)a.batch_stride, span);
+    }
+  }
+
   // Descriptor of `rows` rows from row `row` on, inside one page.  A row past
   // the end looks up block-table entry 0 of the batch (present whenever the
   // batch has a row) and gets an empty range.

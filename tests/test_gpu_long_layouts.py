@@ -207,3 +207,21 @@ def test_strided_long_sub_units(D, Hq, Hkv):
     o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd sub-units D={D} Hq={Hq} Hkv={Hkv}")
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2049), (64, 16, 2, 2100)])
+def test_strided_single_pass_batches_per_wave(D, Hq, Hkv, B):
+    """Single pass, several batches per wave through one strided descriptor,
+    BHSD with NaN padding."""
+    import fmha_amd
+    import torch
+    cap = 80
+    rng = np.random.default_rng(D + B)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[:4] = [cap, 0, 1, 17]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=1700 + D)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, "bhsd"), "bhsd")
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd single pass per-wave batches D={D} Hkv={Hkv}")

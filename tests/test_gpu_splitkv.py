@@ -127,10 +127,13 @@ def test_bad_and_empty_lengths():
 # when batch * ceil(Hkv / (64 / (D/8))) >= 512 and the wave's scores and
 # weights (HPW * G * rows * 6 bytes, rows rounded up to 32) fit 40 KiB of LDS.
 def _onepass_taken(B, Hq, Hkv, D, max_len):
+    """Waves = batch groups (2^shift batches each when Hkv is below the
+    heads a wave holds, see _sub_units) times KV-head groups."""
     hpw = 64 // (D // 8)
-    units = B * ((Hkv + hpw - 1) // hpw)
+    r = _sub_units(Hkv, D)
+    waves = (B + r - 1) // r * ((Hkv + hpw // r - 1) // (hpw // r))
     sp = (max_len + 31) // 32 * 32
-    return units >= 512 and hpw * (Hq // Hkv) * sp * 6 <= 40 * 1024
+    return waves >= 512 and hpw * (Hq // Hkv) * sp * 6 <= 40 * 1024
 
 
 def test_split_path_still_covered():
@@ -192,3 +195,42 @@ def test_sub_units(D, Hq, Hkv, max_len):
     assert not _onepass_taken(B, Hq, Hkv, D, max_len)
     seqlens = np.array([max_len, 1, 0, max_len - 17, 33], np.int32)
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=1300 + D + Hkv + max_len)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2047), (64, 16, 2, 2050), (256, 8, 1, 1030), (128, 8, 2, 1100)])
+def test_onepass_batches_per_wave(D, Hq, Hkv, B):
+    """Single pass with several batches per wave (fewer KV heads than a wave
+    holds): mixed lengths in one wave, empty rows, a last wave partly empty."""
+    max_len = 96
+    assert _sub_units(Hkv, D) > 1 and _onepass_taken(B, Hq, Hkv, D, max_len)
+    rng = np.random.default_rng(D + Hkv + B)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:6] = [max_len, 0, 1, 17, 33, 95]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=1500 + D + Hkv)
+
+
+def test_onepass_batches_per_wave_invalid_length():
+    """An invalid length gives NaN for its batch only, the other batches of
+    its wave stay exact."""
+    import torch
+    B, Hq, Hkv, D, max_len = 2048, 8, 1, 128, 64
+    assert _onepass_taken(B, Hq, Hkv, D, max_len)
+    rng = np.random.default_rng(77)
+    seqlens = rng.integers(1, max_len + 1, size=B).astype(np.int32)
+    bad = 5
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=1600)
+    lens_bad = seqlens.copy()
+    lens_bad[bad] = max_len + 3
+    cu_bad = cu_from_seqlens(lens_bad)
+    k2 = np.concatenate([k[:cu[bad + 1]], np.zeros((max_len + 3 - seqlens[bad], Hkv, D), np.uint16), k[cu[bad + 1]:]])
+    v2 = np.concatenate([v[:cu[bad + 1]], np.zeros((max_len + 3 - seqlens[bad], Hkv, D), np.uint16), v[cu[bad + 1]:]])
+    bits = _run(q, k2, v2, cu_bad, Hq, Hkv, D, max_len).reshape(B, Hq, D)
+    f = oracle.f16_to_f32(bits)
+    assert np.all(np.isnan(f[bad]))
+    keep = np.array([b for b in range(B) if b != bad])
+    assert np.all(np.isfinite(f[keep]))
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True, max_seqlen=max_len)
+    st = oracle.compare(np.ascontiguousarray(bits[keep]).ravel(),
+                        np.ascontiguousarray(r.reshape(B, Hq, D)[keep]).ravel(),
+                        np.ascontiguousarray(slack.reshape(B, Hq, D)[keep]).ravel())
+    assert_pass(st, "neighbours of an invalid length, single pass")
