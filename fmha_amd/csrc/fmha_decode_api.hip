@@ -13,8 +13,11 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 
 #include "fmha_decode.h"
+#include "fmha_decode_group.hpp"
 #include "fmha_decode_kernel.hpp"
 #include "fmha_decode_onepass.hpp"
 #include "fmha_decode_splitkv.hpp"
@@ -47,6 +50,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // units (S=1) want every wave the registers allow.  The library reserves
 // unused LDS per workgroup so that only that many waves fit on a CU.
 constexpr int kInflightBytesPerCU = 80 * 1024;
+// The same target for the matrix-core kernel (fmha_decode_group_kernel),
+// whose waves compute longer after their loads land.
+constexpr int kMfmaInflightBytesPerCU = 224 * 1024;
 constexpr int kMaxWavesPerCU = 32;
 
 // Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
@@ -178,11 +184,16 @@ hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t st
 // Waves per CU for a unit that moves `rows` K/V rows and G query heads:
 // each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
 // of Q in and 1 KiB of O out.  Caps of 16 or more are dropped (no cap).
+// The floor is 3 waves, 4 for G = 8, whose waves compute for about as long
+// as their loads take (sweep at B=30720 Hq=128 Hkv=16 D=128, µs for 3/4/6
+// waves: S=16 1000/966/997, S=4 489/454/484; G = 4 and below are fastest
+// at 3).
 int waves_per_cu_for(int rows, int g) {
   const int unit_bytes = 1024 * (2 * rows + 2 * g);
   int w = kInflightBytesPerCU / unit_bytes;
   if (w >= 16) return kMaxWavesPerCU;
-  return w < 3 ? 3 : w;
+  const int floor_w = g >= 8 ? 4 : 3;
+  return w < floor_w ? floor_w : w;
 }
 
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
@@ -192,8 +203,12 @@ int bucket_for(int s) {
   return b;
 }
 
+// any_group: the entry point takes any G = Hq / Hkv (the packed-layout
+// entries, which can run the matrix-core kernel); the others take G in
+// {1, 2, 4, 8}.
 int check_common(const void* Q, const void* K, const void* V, void* O, int32_t batch, int32_t hq,
-                 int32_t hkv, int32_t seqlen_q, int32_t dq, int32_t dkv, float scale, bool kv_may_be_null) {
+                 int32_t hkv, int32_t seqlen_q, int32_t dq, int32_t dkv, float scale, bool kv_may_be_null,
+                 bool any_group = false) {
   if (batch < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch must be >= 0 (got %d)", batch);
   if (hq <= 0 || hkv <= 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head counts must be > 0 (num_heads_q=%d, num_heads_kv=%d)", hq,
@@ -202,7 +217,7 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "num_heads_q (%d) must be a multiple of num_heads_kv (%d)", hq,
                   hkv);
   const int g = hq / hkv;
-  if (g != 1 && g != 2 && g != 4 && g != 8)
+  if (!any_group && g != 1 && g != 2 && g != 4 && g != 8)
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be 1, 2, 4 or 8 (got %d)", g);
   if (seqlen_q != 1) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_q must be 1 (got %d)", seqlen_q);
   if (dq != dkv)
@@ -275,6 +290,113 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
       break;
     case fmha_decode::kLayoutStrided: err = launch_dim<fmha_decode::kLayoutStrided>(a, dq, g, sb, w, s); break;
     default: err = launch_dim<fmha_decode::kLayoutPaged>(a, dq, g, sb, w, s); break;
+  }
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return FMHA_DECODE_SUCCESS;
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core kernel (fmha_decode_group_kernel): packed layout, any G.
+// ---------------------------------------------------------------------------
+
+// G values the VALU kernel is instantiated for.
+bool valu_group(int g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+
+// Kernel choice for a packed-layout call: the matrix-core kernel for every G
+// the VALU kernel does not cover.  FMHA_DECODE_GQA_KERNEL=mfma runs it for
+// every G, =valu keeps the VALU kernel wherever it exists (for comparisons).
+bool use_mfma_kernel(int g) {
+  if (const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL")) {
+    if (std::strcmp(e, "mfma") == 0) return true;
+    if (std::strcmp(e, "valu") == 0) return !valu_group(g);
+  }
+  return !valu_group(g);
+}
+
+template <int D, int QT>
+hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, QT>;
+  hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
+  return hipGetLastError();
+}
+
+// QT: 16-row blocks of query rows a wave holds (a power of two up to the
+// streams per wave).
+template <int D>
+hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int qt, int w, hipStream_t stream) {
+  constexpr int HPW = fmha_decode::GroupShape<D>::HPW;
+  switch (qt) {
+    case 1: return launch_mfma_one<D, 1>(g, w, stream);
+    case 2: return launch_mfma_one<D, 2>(g, w, stream);
+    case 4:
+      if constexpr (HPW >= 4) return launch_mfma_one<D, 4>(g, w, stream);
+      [[fallthrough]];
+    default: return launch_mfma_one<D, HPW>(g, w, stream);
+  }
+}
+
+// Query rows a wave holds, in 16-row blocks: its HPW tiles of one stream
+// each, i.e. HPW * G rows when G <= 16 (rounded up to a power of two), else
+// HPW full tiles.
+int mfma_row_blocks(int64_t g, int hpw) {
+  if (g > 16) return hpw;
+  const int64_t rows = g * hpw;
+  int qt = 1;
+  while (16 * qt < rows) qt <<= 1;
+  return qt;
+}
+
+// a: the fields base_args and the packed entry points fill (lens = cu offsets
+// or null with seqlen_uniform).  rows_hint as for launch().
+int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, int rows_hint) {
+  const int hpw = kWaveSize / (dq / 8);
+  const int64_t hkv = a.num_heads_kv;
+  const int64_t g = a.num_heads_q / a.num_heads_kv;
+  const int64_t row_bytes = hkv * dq * 2;
+  // A wave's streams span at most hpw / hkv + 2 batches of up to 16 rows;
+  // their byte range must stay below the out-of-range offsets (2^30).
+  if (row_bytes * FMHA_DECODE_MAX_SEQLEN_KV * (hpw / hkv + 2) >= (int64_t(1) << 30))
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
+  const int qt = mfma_row_blocks(g, hpw);
+  const int64_t tps = (g + 15) / 16;  // tiles per stream = waves per stream group
+  const int64_t streams = (int64_t)batch * hkv;
+  const int64_t groups = (streams + hpw - 1) / hpw;
+  const int64_t waves = tps == 1 ? groups : 8 * tps * ((groups + 7) / 8);
+  if (streams > (int64_t)UINT32_MAX || waves > (int64_t)INT32_MAX)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
+  fmha_decode::GroupArgs ga = {};
+  ga.q = a.q;
+  ga.k = a.k;
+  ga.v = a.v;
+  ga.o = a.o;
+  ga.cu = a.lens;
+  ga.seqlen_uniform = a.seqlen_uniform;
+  ga.num_heads_kv = a.num_heads_kv;
+  ga.group = (int32_t)g;
+  ga.streams = (uint32_t)streams;
+  ga.stream_groups = (uint32_t)groups;
+  ga.tiles_per_stream = (int32_t)tps;
+  ga.chunks = (int32_t)tps;
+  ga.waves = (uint32_t)waves;
+  ga.scale = a.scale;
+  // Waves per CU.  A wave spends a fixed stretch on LDS round trips, the
+  // softmax and the MFMAs after its loads land, so the best cap keeps about
+  // 224 KiB in flight per CU (the VALU kernel: 80 KiB), rounded up, at least
+  // 4 waves, none from 8 up.  Sweeps at B=30720 Hkv=16 S=16 D=128, µs for 3/4/6/8
+  // waves per CU: G=3 1194/938/783/813, G=4 1199/951/818/835, G=5
+  // 1199/953/914/918, G=7 1201/967/987/995, G=8 1208/972/1013/1008, G=16
+  // 1290/1308/1306/1309; G=8 at S=4 985/773/564/552 (551 uncapped); D=64
+  // G=5 (Hkv=8) 401/318/231/232 (5 waves: 270).
+  const int64_t qrows = g <= 16 ? hpw * g : 16 * hpw;
+  const int64_t unit_bytes = 2LL * rows_hint * hpw * dq * 2 + 2LL * qrows * dq * 2;
+  int w = (int)((kMfmaInflightBytesPerCU + unit_bytes - 1) / unit_bytes);
+  w = w >= 8 ? kMaxWavesPerCU : (w < 4 ? 4 : w);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  switch (dq) {
+    case 64: err = launch_mfma_d<64>(ga, qt, w, s); break;
+    case 128: err = launch_mfma_d<128>(ga, qt, w, s); break;
+    default: err = launch_mfma_d<256>(ga, qt, w, s); break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
@@ -515,7 +637,7 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
                                float softmax_scale) {
   g_detail[0] = '\0';
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
+                        softmax_scale, false, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
@@ -524,6 +646,7 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
+  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, a, batch, head_dim_q, kVarlenRowsHint);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
 }
 
@@ -554,12 +677,13 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_kv must lie in [0, %d] (got %d)",
                   FMHA_DECODE_MAX_SEQLEN_KV, seqlen_kv);
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, seqlen_kv == 0);
+                        softmax_scale, seqlen_kv == 0, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
   a.seqlen_uniform = seqlen_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
+  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, a, batch, head_dim_q, seqlen_kv);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), seqlen_kv);
 }
 

@@ -1,0 +1,380 @@
+// fmha_decode_group.hpp -- gfx950 decode attention on the matrix cores for
+// any number of query heads per KV head (G = Hq / Hkv >= 1), KV length 0..16
+// per sequence, bf16 Q/K/V, fp32 accumulation, fp16 output.
+//
+// Same semantics as fmha_decode_fwd_kernel (the reference CPU loop,
+// fmha_host.cpp:169-245, with KV head h / G): fp32 scores, scale, masked
+// max-subtracted softmax with a sum > 0 guard, weights rounded to bf16 after
+// normalisation, fp32 P.V, one RNE rounding to fp16.  Only the order of the
+// fp32 sums differs (matrix-core accumulation).
+//
+// Why a second kernel: the VALU kernel spends about 4*G*S v_dot2 per lane on
+// Q.K^T plus a butterfly over G*S partial scores, so from G = 4 its waves
+// compute for about as long as their loads take, and it holds G query
+// vectors in registers (G <= 8).  Here the two products are MFMAs:
+//
+//   * A "stream" is one (batch, KV head); stream sigma = b * Hkv + h owns
+//     query rows [sigma*G, sigma*G + G) of Q and O, so the query rows of
+//     consecutive streams are contiguous whatever Hkv is.  A wave takes HPW =
+//     64 / (D/8) consecutive streams (several batches when Hkv < HPW) and
+//     loads K and V exactly like the VALU kernel: D/8 lanes per stream, one
+//     16-byte chunk of one row per lane and instruction, all rows issued at
+//     once, rows past a stream's length out of range.
+//   * Query rows are taken in tiles of 16 (an MFMA's M) of one stream: tile
+//     c of stream p holds its query heads [16c, 16c + 16), rows at or past G
+//     being padding that is never stored.  A wave handles HPW tiles, one
+//     per stream when G <= 16; larger groups take ceil(G / 16) waves per
+//     stream group, placed on one XCD so that their K/V re-reads hit its L2.
+//     The rows of a wave's tiles are one contiguous range of Q.
+//   * K goes to LDS as rows; per tile S^T = K_p . Q^T is D/32
+//     v_mfma_f32_16x16x32_bf16 (A = 16 K rows of stream p, B = the tile's 16
+//     query rows).  No product ever mixes two streams' data, so a
+//     non-finite value in one stream cannot reach another.
+//   * The 16x16 accumulator holds, per lane, rows 4q..4q+3 of one query
+//     column: the softmax reduces over those 4 values and across the 4 lane
+//     groups (v_permlane16/32_swap), and the bf16 weights it leaves are
+//     already the A operand of a v_mfma_f32_16x16x16_bf16 (rows 4q..4q+3 of
+//     query i in lane (q, i)).
+//   * V is transposed into LDS with v_perm from the coalesced registers
+//     ([stream][8-dim block][dim][16 rows], 16 bytes of padding per block),
+//     over the K rows, which are dead by then; P.V is D/16 MFMAs per tile,
+//     column n covering dims [n*D/16, (n+1)*D/16) so each lane stores whole
+//     8/16/32-byte runs of O.
+//   * 48 MFMAs per wave for G <= 16 at every D, no lane selects: what the
+//     wave spends after its loads land is LDS round trips and the softmax.
+#pragma once
+
+#include "fmha_decode_kernel.hpp"
+
+namespace fmha_decode {
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_v __attribute__((ext_vector_type(4)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct GroupArgs {
+  const uint16_t* q;       // [streams * G, D] bf16 bits (= [batch, Hq, D])
+  const uint16_t* k;       // packed [rows, Hkv, D] bf16 bits
+  const uint16_t* v;
+  uint16_t* o;             // [batch, Hq, D] fp16 bits
+  const int32_t* cu;       // [batch + 1] row offsets, or null (uniform lengths)
+  int32_t seqlen_uniform;  // rows per batch when cu is null
+  int32_t num_heads_kv;
+  int32_t group;           // G = Hq / Hkv
+  uint32_t streams;        // batch * Hkv
+  uint32_t stream_groups;  // ceil(streams / HPW)
+  int32_t tiles_per_stream;  // ceil(G / 16): 16-row query tiles per stream
+  int32_t chunks;          // waves per stream group: ceil(HPW * tiles_per_stream / HPW) = tiles_per_stream
+  uint32_t waves;          // grid size (>= stream_groups * chunks)
+  float scale;
+};
+
+template <int D>
+struct GroupShape {
+  static constexpr int LPH = D / 8;               // lanes per stream (one 16-byte chunk each)
+  static constexpr int HPW = kWaveSize / LPH;     // streams per wave
+  static constexpr int KS = HPW * D * 2 + 16;     // LDS bytes per K row (all streams) + padding
+  static constexpr int QS = D * 2 + 16;           // LDS bytes per query row + padding
+  static constexpr int VB = 8 * kMaxSeq * 2 + 16; // LDS bytes per 8-dim block of V^T + padding
+  static constexpr int VSTREAM = (D / 8) * VB;    // LDS bytes of one stream's V^T
+  static constexpr int DPC = D / 16;              // output dims per P.V column
+  static constexpr int QLD = D / 32;              // 16-byte Q loads per lane per tile
+  // K rows are dead once every tile's scores are formed, so V^T reuses them.
+  static constexpr int KV_LDS = (kMaxSeq * KS > HPW * VSTREAM) ? kMaxSeq * KS : HPW * VSTREAM;
+  template <int QT>
+  static constexpr int lds_bytes() {
+    return KV_LDS + QT * 16 * QS;
+  }
+};
+
+__device__ __forceinline__ int shfl_i(int x, int src) { return __shfl(x, src, kWaveSize); }
+
+// Max or sum over lanes l, l^16, l^32, l^48 (one column of a 16x16 MFMA
+// tile).  v_permlane16_swap / v_permlane32_swap with both operands x return
+// x of this lane and of its partner (l^16, l^32), in some order: combining
+// the two halves needs no lane select and gives every lane the same bits.
+template <bool IS_MAX>
+__device__ __forceinline__ float column_reduce(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const float a0 = __builtin_bit_cast(float, (uint32_t)a[0]);
+  const float a1 = __builtin_bit_cast(float, (uint32_t)a[1]);
+  x = IS_MAX ? fmaxf(a0, a1) : a0 + a1;
+  const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const float b0 = __builtin_bit_cast(float, (uint32_t)b[0]);
+  const float b1 = __builtin_bit_cast(float, (uint32_t)b[1]);
+  return IS_MAX ? fmaxf(b0, b1) : b0 + b1;
+}
+
+// v_perm selector: low halves / high halves of two dwords (lo, hi) -> one dword.
+constexpr uint32_t kPermLo = 0x05040100u;
+constexpr uint32_t kPermHi = 0x07060302u;
+
+// One wave: HPW consecutive streams of stream group sg (wave-local stream
+// p = 0..HPW-1), query tiles [chunk*HPW, chunk*HPW + HPW) of the group's tile
+// list, KV bucket SMAX.  Tile tau covers query rows [16c, 16c + 16) of stream
+// p = tau / TPS, c = tau % TPS (TPS = ceil(G / 16) tiles per stream; rows at
+// or past G are padding that is never stored).  The tiles of a wave cover one
+// contiguous range of query rows, [R0, R0 + nrows), loaded whole into LDS.
+template <int D, int SMAX, int QT>
+__device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int chunk, int lane, int S,
+                                           uint32_t kv_off, int64_t row_first, uint32_t records, uint64_t bad_mask,
+                                           char* lds) {
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  const int s = lane / LPH;
+  const int r = lane % LPH;
+  const int q = lane >> 4;   // MFMA lane group
+  const int n = lane & 15;   // MFMA row / column inside the 16x16 tile
+  const int G = a.group;
+  const int TPS = a.tiles_per_stream;
+  const uint32_t Hkv = (uint32_t)a.num_heads_kv;
+  const uint32_t row_bytes = Hkv * D * 2u;
+
+  char* k_lds = lds;
+  char* v_lds = lds;  // written after the last read of k_lds
+  char* q_lds = lds + Sh::KV_LDS;
+
+  // ---- this wave's tiles and query rows ----
+  const uint32_t sigma0 = sg * HPW;
+  const int nstreams = (int)min(a.streams - sigma0, (uint32_t)HPW);  // valid streams of the group
+  const int tau0 = chunk * HPW;
+  const int ntiles = min(nstreams * TPS - tau0, HPW);                 // > 0
+  const int p0 = tau0 / TPS;
+  const int p1 = (tau0 + ntiles - 1) / TPS;
+  const int c1 = (tau0 + ntiles - 1) - p1 * TPS;
+  const int R0 = p0 * G + (tau0 - p0 * TPS) * 16;
+  const int nrows = p1 * G + min(16 * c1 + 16, G) - R0;                // <= 16 * QT
+  const uint64_t qrow0 = (uint64_t)sigma0 * G + R0;
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + qrow0 * D, (uint32_t)nrows * D * 2u);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + qrow0 * D, (uint32_t)nrows * D * 2u);
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + (uint64_t)row_first * Hkv * D, records);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + (uint64_t)row_first * Hkv * D, records);
+
+  // ---- issue every load: the query rows, K rows, V rows ----
+  u32x4 qr[QT][Sh::QLD];
+#pragma unroll
+  for (int t = 0; t < QT; ++t)
+#pragma unroll
+    for (int i = 0; i < Sh::QLD; ++i)
+      qr[t][i] = buffer_load16<kPolicyDefault>(q_rsrc, (uint32_t)(t * 16 * D * 2 + (lane + 64 * i) * 16));
+  u32x4 kr[SMAX];
+  u32x4 vr[SMAX];
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j)
+    kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j)
+    vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- query rows and K rows to LDS ----
+#pragma unroll
+  for (int t = 0; t < QT; ++t)
+#pragma unroll
+    for (int i = 0; i < Sh::QLD; ++i) {
+      const int flat = lane + 64 * i;  // 16-byte chunk of 16 rows
+      *reinterpret_cast<u32x4*>(q_lds + (t * 16 + flat / (D / 8)) * Sh::QS + (flat % (D / 8)) * 16) = qr[t][i];
+    }
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) *reinterpret_cast<u32x4*>(k_lds + j * Sh::KS + s * D * 2 + r * 16) = kr[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- per tile: S^T = K_p . Q^T, masked softmax; bf16 weights stay in registers ----
+  bf16x4_v pa[HPW];
+  const int krow = n < SMAX ? n : 0;  // K rows past the bucket are never valid: any finite row will do
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    pa[i] = bf16x4_v{0, 0, 0, 0};
+    if (i >= ntiles) continue;
+    const int tau = tau0 + i;
+    const int p = tau / TPS;
+    const int c = tau - p * TPS;
+    // Query column n of the tile: row 16c + n of stream p (padding columns
+    // read row 0 of the range; their scores are never used).
+    const int qrow = 16 * c + n < G ? p * G + 16 * c + n - R0 : 0;
+    f32x4_v st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int cc = 0; cc < Sh::QLD; ++cc) {
+      const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(k_lds + krow * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
+      const bf16x8_v qb = *reinterpret_cast<const bf16x8_v*>(q_lds + qrow * Sh::QS + (4 * cc + q) * 16);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb, st, 0, 0, 0);
+    }
+    // Masked softmax over the 16 rows of this lane's query column: rows
+    // 4q..4q+3 here, the rest in lanes n + 16, n + 32, n + 48.
+    const int S_p = __builtin_amdgcn_readlane(S, p * LPH);
+    float x[4];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = st[e] * a.scale;
+      m = (4 * q + e < S_p) ? fmaxf(m, x[e]) : m;
+    }
+    m = column_reduce<true>(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = (4 * q + e < S_p) ? expf(x[e] - m) : 0.0f;
+      sum += x[e];
+    }
+    sum = column_reduce<false>(sum);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pa[i][e] = (__bf16)((sum > 0.0f) ? (x[e] / sum) : 0.0f);
+    // A stream with an invalid length gets NaN weights, so every output of
+    // its tile is NaN (NaN times any V value, zero included).
+    if ((bad_mask >> (uint32_t)(p * LPH)) & 1u) pa[i] = bf16x4_v{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+  }
+
+  // ---- V^T to LDS (over the K rows, whose last read is above): block r of
+  //      stream s, [dim e][16 rows], from the row registers ----
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      u32x4 w;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const int j0 = 8 * half + 2 * pp;
+        const uint32_t v0 = j0 < SMAX ? (uint32_t)vr[j0 < SMAX ? j0 : 0][e / 2] : 0u;
+        const uint32_t v1 = j0 + 1 < SMAX ? (uint32_t)vr[j0 + 1 < SMAX ? j0 + 1 : 0][e / 2] : 0u;
+        w[pp] = __builtin_amdgcn_perm(v1, v0, (e & 1) ? kPermHi : kPermLo);
+      }
+      *reinterpret_cast<u32x4*>(v_lds + s * Sh::VSTREAM + r * Sh::VB + e * (kMaxSeq * 2) + half * 16) = w;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- per tile: P.V; lane (q, n) ends with query rows 16c + 4q..4q+3 of
+  //      stream p, dims [n*DPC, n*DPC + DPC) ----
+  constexpr int DPC = Sh::DPC;
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    if (i >= ntiles) continue;
+    const int tau = tau0 + i;
+    const int p = tau / TPS;
+    const int c = tau - p * TPS;
+    const char* vs = v_lds + p * Sh::VSTREAM;
+    f32x4_v acc[DPC];
+#pragma unroll
+    for (int dt = 0; dt < DPC; ++dt) {
+      const int dim = n * DPC + dt;
+      const bf16x4_v vb = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (kMaxSeq * 2) + q * 8);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[i], vb, f32x4_v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    }
+    // ---- fp16 (RNE) output ----
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 16 * c + 4 * q + e;  // query head inside the group
+      const uint32_t off = g < G ? (uint32_t)((p * G + g - R0) * D + n * DPC) * 2u : kLaneOutOfRange;
+#pragma unroll
+      for (int h8 = 0; h8 < (DPC + 7) / 8; ++h8) {
+        constexpr int W = DPC < 8 ? DPC : 8;  // dims per store
+        float vals[8];
+#pragma unroll
+        for (int k8 = 0; k8 < 8; ++k8) vals[k8] = k8 < W ? acc[h8 * 8 + (k8 < W ? k8 : 0)][e] : 0.0f;
+        const u32x4 pk = pack_f16x8(vals);
+        if constexpr (W == 8) {
+          buffer_store16(o_rsrc, off + h8 * 16, pk);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{pk[0], pk[1]}, o_rsrc, (int)off, 0, kPolicyStreamStore);
+        }
+      }
+    }
+  }
+}
+
+// Grid: a.waves one-wave workgroups.  Workgroup w serves stream group
+// ((w / 8) / chunks) * 8 + w % 8 and tile chunk (w / 8) % chunks, so the
+// chunks of one stream group (G > 16) run on one XCD (dispatch is
+// round-robin over the 8 XCDs) at nearly the same time and their K/V re-reads
+// hit its L2; with chunks == 1 it is stream group w.
+// SB = 1, 2, 4, 8, 16: uniform lengths (cu == null, seqlen_uniform <= SB);
+// SB = 0: lengths from cu (or uniform), the bucket chosen per wave.
+template <int D, int SB, int QT>
+__global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupArgs a) {
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  __shared__ __attribute__((aligned(16))) char lds[Sh::template lds_bytes<QT>()];
+
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t w = blockIdx.x;
+  const uint32_t chunks = (uint32_t)a.chunks;
+  const uint32_t rest = w >> 3;
+  const uint32_t sg = (rest / chunks) * 8u + (w & 7u);
+  const int chunk = (int)(rest % chunks);
+  if (sg >= a.stream_groups) return;
+  const uint32_t sigma0 = sg * HPW;
+  if ((int)min(a.streams - sigma0, (uint32_t)HPW) * a.tiles_per_stream <= chunk * HPW) return;
+
+  // ---- this lane's stream: batch, head, first row relative to the wave's first batch ----
+  const int s = lane / LPH;
+  const int r = lane % LPH;
+  const uint32_t Hkv = (uint32_t)a.num_heads_kv;
+  const uint32_t sig = sigma0 + (uint32_t)s;
+  const bool sok = sig < a.streams;
+  const uint32_t bq = sok ? sig / Hkv : 0u;
+  const uint32_t h = sok ? sig - bq * Hkv : 0u;
+  const uint32_t b_first = sigma0 / Hkv;
+  int S;
+  int64_t row_first, row0;
+  if (a.cu) {
+    row_first = a.cu[b_first];
+    row0 = a.cu[bq];
+    S = (int)(a.cu[bq + 1] - row0);
+  } else {
+    S = a.seqlen_uniform;
+    row_first = (int64_t)b_first * S;
+    row0 = (int64_t)bq * S;
+  }
+  const uint32_t row_bytes = Hkv * D * 2u;
+  const int64_t rel = row0 - row_first;
+  // A length outside [0, 16], or a table that puts this batch beyond the
+  // reach of the wave's descriptor, makes the stream invalid (NaN output).
+  const bool bad = sok && (S < 0 || S > kMaxSeq || rel < 0 ||
+                           (rel + kMaxSeq) * (int64_t)row_bytes >= (int64_t)kLaneOutOfRange);
+  if (!sok || bad) S = 0;
+  const uint32_t kv_off =
+      (sok && !bad) ? (uint32_t)rel * row_bytes + h * D * 2u + (uint32_t)r * 16u : kLaneOutOfRange;
+  // Descriptor range: the end of the last row any lane reads; bucket: the
+  // longest length of the wave; invalid streams as a bit per stream.
+  uint32_t end = S > 0 ? (uint32_t)(rel + S) * row_bytes : 0u;
+  int smax = S;
+#pragma unroll
+  for (int m = 1; m < kWaveSize; m <<= 1) {
+    smax = max(smax, __shfl_xor(smax, m, kWaveSize));
+    end = max(end, (uint32_t)__shfl_xor((int)end, m, kWaveSize));
+  }
+  const uint32_t records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
+  smax = __builtin_amdgcn_readfirstlane(smax);
+  const uint64_t bad_mask = __ballot(bad && r == 0);
+
+#define FMHA_GROUP_UNIT(SM) group_unit<D, SM, QT>(a, sg, chunk, lane, S, kv_off, row_first, records, bad_mask, lds)
+  if constexpr (SB != 0) {
+    FMHA_GROUP_UNIT(SB);
+  } else {
+    if (smax <= 1)
+      FMHA_GROUP_UNIT(1);
+    else if (smax <= 2)
+      FMHA_GROUP_UNIT(2);
+    else if (smax <= 4)
+      FMHA_GROUP_UNIT(4);
+    else if (smax <= 8)
+      FMHA_GROUP_UNIT(8);
+    else
+      FMHA_GROUP_UNIT(16);
+  }
+#undef FMHA_GROUP_UNIT
+}
+
+}  // namespace fmha_decode

@@ -62,7 +62,15 @@ extern "C" {
  *                   [0, 16] gets O = NaN: the kernel cannot return an error.
  *   batch           >= 0 (0 launches nothing)
  *   num_heads_q     > 0, a multiple of num_heads_kv
- *   num_heads_kv    > 0; num_heads_q / num_heads_kv must be 1, 2, 4 or 8
+ *   num_heads_kv    > 0; any group size G = num_heads_q / num_heads_kv.
+ *                   G = 1, 2, 4, 8 run the VALU kernel, every other G the
+ *                   matrix-core kernel (which needs num_heads_kv * head_dim
+ *                   below 2^24, else FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   The environment variable FMHA_DECODE_GQA_KERNEL=mfma
+ *                   runs the matrix-core kernel for every G, =valu keeps the
+ *                   VALU kernel wherever it exists.  This entry point and
+ *                   fmha_decode_fwd_uniform take any G; the others take
+ *                   G = 1, 2, 4 or 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q

@@ -80,8 +80,9 @@ def uni(lib, **kw):
     (dict(hq=0), BAD, "head counts"),
     (dict(hkv=0), BAD, "head counts"),
     (dict(hq=16, hkv=5), BAD, "multiple"),
-    (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
-    (dict(hq=32, hkv=2), NOTSUP, "1, 2, 4 or 8"),
+    # Any group size runs (the matrix-core kernel takes those outside
+    # {1, 2, 4, 8}), but not when a wave's K/V span reaches 2^30 bytes.
+    (dict(hq=3 << 17, hkv=1 << 17), NOTSUP, "too large"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(sq=0), BAD, "seqlen_q"),
     (dict(dq=128, dkv=256), BAD, "head_dim_q"),
@@ -106,12 +107,19 @@ def test_varlen_rejects(lib, kw, code, needle):
     (dict(s=-1), BAD, "seqlen_kv"),
     (dict(s=17), BAD, "seqlen_kv"),
     (dict(s=1000), BAD, "seqlen_kv"),
-    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    (dict(hq=5 << 17, hkv=1 << 17), NOTSUP, "too large"),
     (dict(v=None), BAD, "non-null"),
 ])
 def test_uniform_rejects(lib, kw, code, needle):
     assert uni(lib, **kw) == code
     assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+@pytest.mark.parametrize("hq,hkv", [(48, 16), (32, 2), (24, 8), (7, 1)])
+def test_fp32_weights_group_sizes(lib, hq, hkv):
+    """The fp32-weight entry keeps the VALU kernel's group sizes 1, 2, 4, 8."""
+    assert fwd32(lib, hq=hq, hkv=hkv) == NOTSUP
+    assert "1, 2, 4 or 8" in lib.fmha_decode_last_error_detail().decode()
 
 
 def strided(lib, **kw):

@@ -1,0 +1,161 @@
+"""GPU parity of the matrix-core kernel (fmha_decode_group_kernel) against the
+CPU oracle, through the packed-layout entry points.
+
+The kernel serves every group size G = Hq / Hkv outside {1, 2, 4, 8} (which
+the VALU kernel cannot), and any G when FMHA_DECODE_GQA_KERNEL=mfma.  The
+reference has no GQA (its kernels index K/V with the query head,
+fmha_mfma_4x4x4_kernel.hpp:195-196); the oracle's mapping is KV head h / G
+(fmha_host.cpp:169-245 otherwise).  Coverage: non-power-of-two and large G,
+every length 0..16 in one varlen batch, uniform lengths, KV-head counts below
+and not dividing a wave's 64 / (D/8) streams (waves spanning batches),
+several waves per stream group (G * streams per wave > 64 query rows),
+the S = 1 known answer, NaN-poisoned neighbour streams and batches, and
+invalid lengths.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.common import (assert_pass, check, cu_from_seqlens, default_scale, make_inputs,
+                          run_gpu)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def mfma(monkeypatch):
+    monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "mfma")
+
+
+def _case(B, Hq, Hkv, D, seqlens, seed, std=1.0, uniform=False):
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed, std)
+    o = run_gpu(q, k, v, cu, Hq, Hkv, D, uniform_s=(int(seqlens[0]) if uniform else None))
+    st = check(o, q, k, v, cu, Hq, Hkv, D)
+    assert_pass(st, f"B={B} Hq={Hq} Hkv={Hkv} D={D} seed={seed} uniform={uniform}")
+    return o, (q, k, v, cu)
+
+
+def _all_lengths(seed, reps=2):
+    seqlens = np.array(list(range(17)) * reps, dtype=np.int32)
+    np.random.default_rng(seed).shuffle(seqlens)
+    return seqlens
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [3, 5, 6, 7, 12, 16])
+def test_group_sizes_varlen(D, G):
+    """Group sizes the VALU kernel does not take, every length 0..16."""
+    Hkv = 4
+    seqlens = _all_lengths(D * 31 + G)
+    _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=1000 + D + G)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [24, 32, 64])
+def test_large_groups(D, G):
+    """More query rows per stream group than one wave takes: several waves
+    per stream group (query chunks), MQA-like shapes."""
+    for Hkv in (1, 2):
+        seqlens = np.random.default_rng(G + Hkv).integers(0, 17, size=21).astype(np.int32)
+        _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=1100 + D + G + Hkv)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("Hkv", [1, 2, 3, 5, 6, 7, 9])
+def test_kv_heads_across_waves(D, Hkv):
+    """KV-head counts below a wave's streams, or not dividing them: one wave
+    reads several batches, or ends inside a batch."""
+    G = 5
+    seqlens = np.random.default_rng(Hkv * 13 + D).integers(0, 17, size=23).astype(np.int32)
+    _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=1200 + D + Hkv)
+
+
+@pytest.mark.parametrize("S", [0, 1, 2, 3, 5, 8, 9, 16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_uniform_lengths(S, D):
+    _case(29, 24, 8, D, np.full(29, S, np.int32), seed=1300 + S + D, uniform=True)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_forced_on_valu_group_sizes(mfma, D, G):
+    """The matrix-core kernel on the group sizes the VALU kernel also serves,
+    including the reference's own Poisson-length workload shape."""
+    Hkv = 4 if G > 1 else 16
+    seqlens = _all_lengths(D + G)
+    _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=1400 + D + G)
+    ref = oracle.generate_seqlens(10, 16)
+    _case(10, 16, 16, 128, ref, seed=1450 + G)
+
+
+@pytest.mark.parametrize("std", [0.25, 2.0, 4.0])
+def test_logit_spread(std):
+    seqlens = oracle.generate_seqlens(48, 16)
+    _case(48, 40, 8, 128, seqlens, seed=1500, std=std)
+    _case(48, 48, 8, 256, seqlens, seed=1501, std=std)
+
+
+def test_s1_known_answer_bitexact():
+    """S = 1: the weight is exactly 1, so O = fp16(V of the query's KV head)."""
+    B, Hq, Hkv, D = 17, 20, 4, 128
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, np.ones(B, np.int32), seed=1600)
+    vf = oracle.f32_to_f16(oracle.bf16_to_f32(v)).reshape(B, Hkv, D)
+    expect = np.repeat(vf, Hq // Hkv, axis=1)
+    for uniform in (False, True):
+        o = run_gpu(q, k, v, cu, Hq, Hkv, D, uniform_s=1 if uniform else None)
+        assert np.array_equal(o.reshape(B, Hq, D), expect)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_poisoned_neighbour_streams(D):
+    """No product mixes two streams: NaN in every other (batch, KV head) --
+    including streams that share a wave with the one checked -- leaves the
+    checked stream's outputs equal to running it alone."""
+    nan = np.uint16(0x7FC0)
+    for Hkv, G in ((3, 5), (1, 6), (8, 3)):
+        Hq = Hkv * G
+        seqlens = np.array([16, 7, 16, 9], np.int32)
+        q, k, v, cu = make_inputs(4, Hq, Hkv, D, seqlens, seed=1700 + Hkv + D)
+        b, h = 1, Hkv - 1
+        kp = np.full_like(k, nan)
+        vp = np.full_like(v, nan)
+        kp[cu[b]:cu[b + 1], h] = k[cu[b]:cu[b + 1], h]
+        vp[cu[b]:cu[b + 1], h] = v[cu[b]:cu[b + 1], h]
+        o = run_gpu(q, kp, vp, cu, Hq, Hkv, D).reshape(4, Hq, D)
+        got = o[b, h * G:(h + 1) * G]
+        cb = cu_from_seqlens([seqlens[b]])
+        ks = k[cu[b]:cu[b + 1], h:h + 1]
+        vs = v[cu[b]:cu[b + 1], h:h + 1]
+        qs = q[b:b + 1, h * G:(h + 1) * G]
+        r, slack = oracle.decode(qs, ks, vs, cb, G, 1, D, default_scale(D), with_slack=True)
+        assert_pass(oracle.compare(got.reshape(r.shape), r, slack), f"Hkv={Hkv} G={G} D={D}")
+
+
+def test_bad_lengths_give_nan():
+    """A cu_seqlens span outside [0, 16]: that batch's rows are NaN, the
+    batches that share its waves are unaffected."""
+    Hkv, G, D = 1, 6, 128
+    seqlens = np.array([4, 17, 3, 16, 2], np.int32)
+    q, k, v, cu = make_inputs(5, Hkv * G, Hkv, D, seqlens, seed=1800)
+    o = run_gpu(q, k, v, cu, Hkv * G, Hkv, D).reshape(5, Hkv * G, D)
+    assert np.all(np.isnan(oracle.f16_to_f32(o[1])))
+    for b in (0, 2, 3, 4):
+        cb = cu_from_seqlens([seqlens[b]])
+        r, slack = oracle.decode(q[b:b + 1], k[cu[b]:cu[b + 1]], v[cu[b]:cu[b + 1]], cb, Hkv * G, Hkv, D,
+                                 default_scale(D), with_slack=True)
+        assert_pass(oracle.compare(o[b:b + 1], r, slack), f"batch {b}")
+
+
+def test_mfma_matches_valu_within_gate(mfma, monkeypatch):
+    """Same inputs through both kernels (G = 4): each passes the oracle gate
+    and they agree within it."""
+    B, Hq, Hkv, D = 64, 32, 8, 128
+    seqlens = oracle.generate_seqlens(B, 16)
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=1900)
+    o_mfma = run_gpu(q, k, v, cu, Hq, Hkv, D)
+    monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "valu")
+    o_valu = run_gpu(q, k, v, cu, Hq, Hkv, D)
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True)
+    assert_pass(oracle.compare(o_mfma, r, slack), "mfma")
+    assert_pass(oracle.compare(o_valu, r, slack), "valu")
+    assert_pass(oracle.compare(o_mfma, o_valu, slack), "mfma vs valu")
