@@ -21,6 +21,10 @@ HIPCC_FLAGS = [
     "-Wall",
     # Packed-FP32 VALU forms are kept out of every build.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs rather than AGPRs: the matrix-core kernel reads
+    # every result with VALU instructions, which cannot take AGPR operands
+    # (saves one v_accvgpr_read per value).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

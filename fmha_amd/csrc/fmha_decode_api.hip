@@ -50,9 +50,6 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // units (S=1) want every wave the registers allow.  The library reserves
 // unused LDS per workgroup so that only that many waves fit on a CU.
 constexpr int kInflightBytesPerCU = 80 * 1024;
-// The same target for the matrix-core kernel (fmha_decode_group_kernel),
-// whose waves compute longer after their loads land.
-constexpr int kMfmaInflightBytesPerCU = 224 * 1024;
 constexpr int kMaxWavesPerCU = 32;
 
 // Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
@@ -313,37 +310,29 @@ bool use_mfma_kernel(int g) {
   return !valu_group(g);
 }
 
-template <int D, int QT>
+template <int D, int NS>
 hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, QT>;
+  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS>;
   hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
   return hipGetLastError();
 }
 
-// QT: 16-row blocks of query rows a wave holds (a power of two up to the
-// streams per wave).
 template <int D>
-hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int qt, int w, hipStream_t stream) {
-  constexpr int HPW = fmha_decode::GroupShape<D>::HPW;
-  switch (qt) {
+hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int ns, int w, hipStream_t stream) {
+  switch (ns) {
     case 1: return launch_mfma_one<D, 1>(g, w, stream);
     case 2: return launch_mfma_one<D, 2>(g, w, stream);
-    case 4:
-      if constexpr (HPW >= 4) return launch_mfma_one<D, 4>(g, w, stream);
-      [[fallthrough]];
-    default: return launch_mfma_one<D, HPW>(g, w, stream);
+    default:
+      if constexpr (fmha_decode::GroupShape<D>::HPW >= 4) return launch_mfma_one<D, 4>(g, w, stream);
+      else return launch_mfma_one<D, 2>(g, w, stream);
   }
 }
 
-// Query rows a wave holds, in 16-row blocks: its HPW tiles of one stream
-// each, i.e. HPW * G rows when G <= 16 (rounded up to a power of two), else
-// HPW full tiles.
-int mfma_row_blocks(int64_t g, int hpw) {
-  if (g > 16) return hpw;
-  const int64_t rows = g * hpw;
-  int qt = 1;
-  while (16 * qt < rows) qt <<= 1;
-  return qt;
+// Streams per 16-column query tile: 4 for G <= 4, 2 for G <= 8, else 1
+// (capped at the streams a wave holds).
+int mfma_streams_per_tile(int64_t g, int hpw) {
+  const int ns = g <= 4 ? 4 : (g <= 8 ? 2 : 1);
+  return ns < hpw ? ns : hpw;
 }
 
 // a: the fields base_args and the packed entry points fill (lens = cu offsets
@@ -357,8 +346,8 @@ int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, in
   // their byte range must stay below the out-of-range offsets (2^30).
   if (row_bytes * FMHA_DECODE_MAX_SEQLEN_KV * (hpw / hkv + 2) >= (int64_t(1) << 30))
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
-  const int qt = mfma_row_blocks(g, hpw);
-  const int64_t tps = (g + 15) / 16;  // tiles per stream = waves per stream group
+  const int ns = mfma_streams_per_tile(g, hpw);
+  const int64_t tps = ns > 1 ? 1 : (g + 15) / 16;  // tiles per stream = waves per stream group
   const int64_t streams = (int64_t)batch * hkv;
   const int64_t groups = (streams + hpw - 1) / hpw;
   const int64_t waves = tps == 1 ? groups : 8 * tps * ((groups + 7) / 8);
@@ -379,24 +368,26 @@ int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, in
   ga.chunks = (int32_t)tps;
   ga.waves = (uint32_t)waves;
   ga.scale = a.scale;
-  // Waves per CU.  A wave spends a fixed stretch on LDS round trips, the
-  // softmax and the MFMAs after its loads land, so the best cap keeps about
-  // 224 KiB in flight per CU (the VALU kernel: 80 KiB), rounded up, at least
-  // 4 waves, none from 8 up.  Sweeps at B=30720 Hkv=16 S=16 D=128, µs for 3/4/6/8
-  // waves per CU: G=3 1194/938/783/813, G=4 1199/951/818/835, G=5
-  // 1199/953/914/918, G=7 1201/967/987/995, G=8 1208/972/1013/1008, G=16
-  // 1290/1308/1306/1309; G=8 at S=4 985/773/564/552 (551 uncapped); D=64
-  // G=5 (Hkv=8) 401/318/231/232 (5 waves: 270).
+  // Waves per CU, from sweeps of 3-8 waves (B=30720, S=16, µs): the best cap
+  // follows the tiles a wave computes more than its bytes.  D=128: 4 waves
+  // (G=3 886/749/796/805/812 for 3/4/5/6/8, G=6 972/914/928/940/941, G=7
+  // 981/970/985/988/982), 6 from four tiles per wave (G=12
+  // 1187/1148/1147/1143/1143, MQA G=32 Hkv=1 151/131/129/130/129); D=64: 6
+  // (Hkv=8, G=3 250/203/178/186/186, G=5 299/243/205/196/194, G=12
+  // 400/320/317/316/318); D=256: 4 (G=3 557/483/484/488/490, G=5
+  // 603/633/637/638/632).  Waves of under 32 KiB (short rows) run uncapped
+  // (G=5 at S=4 725/569/476/417/413).
+  const int tiles_per_wave = hpw / ns;
   const int64_t qrows = g <= 16 ? hpw * g : 16 * hpw;
   const int64_t unit_bytes = 2LL * rows_hint * hpw * dq * 2 + 2LL * qrows * dq * 2;
-  int w = (int)((kMfmaInflightBytesPerCU + unit_bytes - 1) / unit_bytes);
-  w = w >= 8 ? kMaxWavesPerCU : (w < 4 ? 4 : w);
+  int w = dq == 64 || tiles_per_wave >= 4 ? 6 : 4;
+  if (unit_bytes < 32 * 1024) w = kMaxWavesPerCU;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   switch (dq) {
-    case 64: err = launch_mfma_d<64>(ga, qt, w, s); break;
-    case 128: err = launch_mfma_d<128>(ga, qt, w, s); break;
-    default: err = launch_mfma_d<256>(ga, qt, w, s); break;
+    case 64: err = launch_mfma_d<64>(ga, ns, w, s); break;
+    case 128: err = launch_mfma_d<128>(ga, ns, w, s); break;
+    default: err = launch_mfma_d<256>(ga, ns, w, s); break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;

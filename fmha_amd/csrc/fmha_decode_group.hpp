@@ -20,16 +20,18 @@
 //     loads K and V exactly like the VALU kernel: D/8 lanes per stream, one
 //     16-byte chunk of one row per lane and instruction, all rows issued at
 //     once, rows past a stream's length out of range.
-//   * Query rows are taken in tiles of 16 (an MFMA's M) of one stream: tile
-//     c of stream p holds its query heads [16c, 16c + 16), rows at or past G
-//     being padding that is never stored.  A wave handles HPW tiles, one
-//     per stream when G <= 16; larger groups take ceil(G / 16) waves per
-//     stream group, placed on one XCD so that their K/V re-reads hit its L2.
-//     The rows of a wave's tiles are one contiguous range of Q.
-//   * K goes to LDS as rows; per tile S^T = K_p . Q^T is D/32
+//   * Query columns are taken in tiles of 16 (an MFMA's N): NS = 4 streams
+//     of 4 columns for G <= 4, NS = 2 of 8 for G <= 8, one stream per tile
+//     above (query heads [16c, 16c + 16) of tile c); columns at or past G
+//     are padding that is never stored.  A wave handles HPW / NS tiles;
+//     larger groups take ceil(G / 16) waves per stream group, placed on one
+//     XCD so that their K/V re-reads hit its L2.  The query rows of a wave's
+//     tiles are one contiguous range of Q.
+//   * K goes to LDS as rows; per tile and stream S^T = K_p . Q^T is D/32
 //     v_mfma_f32_16x16x32_bf16 (A = 16 K rows of stream p, B = the tile's 16
-//     query rows).  No product ever mixes two streams' data, so a
-//     non-finite value in one stream cannot reach another.
+//     query columns), each column keeping its own stream's pass.  No product
+//     ever mixes two streams' data, so a non-finite value in one stream
+//     cannot reach another.
 //   * The 16x16 accumulator holds, per lane, rows 4q..4q+3 of one query
 //     column: the softmax reduces over those 4 values and across the 4 lane
 //     groups (v_permlane16/32_swap), and the bf16 weights it leaves are
@@ -37,11 +39,10 @@
 //     query i in lane (q, i)).
 //   * V is transposed into LDS with v_perm from the coalesced registers
 //     ([stream][8-dim block][dim][16 rows], 16 bytes of padding per block),
-//     over the K rows, which are dead by then; P.V is D/16 MFMAs per tile,
-//     column n covering dims [n*D/16, (n+1)*D/16) so each lane stores whole
-//     8/16/32-byte runs of O.
-//   * 48 MFMAs per wave for G <= 16 at every D, no lane selects: what the
-//     wave spends after its loads land is LDS round trips and the softmax.
+//     over the K rows, which are dead by then; per tile and stream P.V is
+//     D/16 MFMAs, each output row keeping its own stream's; column n covers
+//     dims [n*D/16, (n+1)*D/16) so each lane stores whole 8/16/32-byte runs.
+//   * 48 MFMAs per wave for G <= 16 at every D.
 #pragma once
 
 #include "fmha_decode_kernel.hpp"
@@ -113,24 +114,30 @@ constexpr uint32_t kPermLo = 0x05040100u;
 constexpr uint32_t kPermHi = 0x07060302u;
 
 // One wave: HPW consecutive streams of stream group sg (wave-local stream
-// p = 0..HPW-1), query tiles [chunk*HPW, chunk*HPW + HPW) of the group's tile
-// list, KV bucket SMAX.  Tile tau covers query rows [16c, 16c + 16) of stream
-// p = tau / TPS, c = tau % TPS (TPS = ceil(G / 16) tiles per stream; rows at
-// or past G are padding that is never stored).  The tiles of a wave cover one
-// contiguous range of query rows, [R0, R0 + nrows), loaded whole into LDS.
-template <int D, int SMAX, int QT>
+// p = 0..HPW-1), KV bucket SMAX, query tiles [chunk*TW, chunk*TW + TW) of the
+// group's tile list (TW = HPW / NS tiles per wave).  A tile's 16 columns hold
+// NS streams of CPS = 16 / NS query columns each: with NS > 1 (G <= CPS)
+// tile tau holds streams [tau*NS, tau*NS + NS) and column n query head n %
+// CPS of stream tau*NS + n / CPS; with NS = 1 tile tau holds query heads
+// [16c, 16c + 16) of stream tau / TPS, c = tau % TPS (TPS = ceil(G / 16)).
+// Columns whose query head is at or past G are padding, never stored.  The
+// rows of a wave's tiles are one contiguous range [R0, R0 + nrows) of Q.
+template <int D, int SMAX, int NS>
 __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int chunk, int lane, int S,
                                            uint32_t kv_off, int64_t row_first, uint32_t records, uint64_t bad_mask,
                                            char* lds) {
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
+  constexpr int TW = HPW / NS;   // tiles per wave
+  constexpr int QT = TW;         // 16-row blocks of query rows per wave
+  constexpr int CPS = 16 / NS;   // query columns per stream in a tile
   const int s = lane / LPH;
   const int r = lane % LPH;
   const int q = lane >> 4;   // MFMA lane group
   const int n = lane & 15;   // MFMA row / column inside the 16x16 tile
   const int G = a.group;
-  const int TPS = a.tiles_per_stream;
+  const int TPS = a.tiles_per_stream;  // 1 when NS > 1
   const uint32_t Hkv = (uint32_t)a.num_heads_kv;
   const uint32_t row_bytes = Hkv * D * 2u;
 
@@ -141,13 +148,13 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   // ---- this wave's tiles and query rows ----
   const uint32_t sigma0 = sg * HPW;
   const int nstreams = (int)min(a.streams - sigma0, (uint32_t)HPW);  // valid streams of the group
-  const int tau0 = chunk * HPW;
-  const int ntiles = min(nstreams * TPS - tau0, HPW);                 // > 0
-  const int p0 = tau0 / TPS;
-  const int p1 = (tau0 + ntiles - 1) / TPS;
-  const int c1 = (tau0 + ntiles - 1) - p1 * TPS;
-  const int R0 = p0 * G + (tau0 - p0 * TPS) * 16;
-  const int nrows = p1 * G + min(16 * c1 + 16, G) - R0;                // <= 16 * QT
+  const int ntiles_group = ((nstreams + NS - 1) / NS) * TPS;
+  const int tau0 = chunk * TW;
+  const int ntiles = min(ntiles_group - tau0, TW);                    // > 0
+  const int tau1 = tau0 + ntiles - 1;
+  const int R0 = (tau0 / TPS) * NS * G + (tau0 % TPS) * 16;
+  const int p1 = min((tau1 / TPS) * NS + NS, nstreams) - 1;
+  const int nrows = p1 * G + min(16 * (tau1 % TPS) + 16, G) - R0;     // <= 16 * QT
   const uint64_t qrow0 = (uint64_t)sigma0 * G + R0;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + qrow0 * D, (uint32_t)nrows * D * 2u);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + qrow0 * D, (uint32_t)nrows * D * 2u);
@@ -185,49 +192,72 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- per tile: S^T = K_p . Q^T, masked softmax; bf16 weights stay in registers ----
-  bf16x4_v pa[HPW];
+  // ---- per tile: one S^T = K_p . Q^T pass per stream, each column keeping
+  //      its own stream's; masked softmax; bf16 weights stay in registers ----
+  bf16x4_v pa[TW];
   const int krow = n < SMAX ? n : 0;  // K rows past the bucket are never valid: any finite row will do
+  const int slot_col = n / CPS;       // stream slot of this lane's column
 #pragma unroll
-  for (int i = 0; i < HPW; ++i) {
+  for (int i = 0; i < TW; ++i) {
     pa[i] = bf16x4_v{0, 0, 0, 0};
     if (i >= ntiles) continue;
     const int tau = tau0 + i;
-    const int p = tau / TPS;
-    const int c = tau - p * TPS;
-    // Query column n of the tile: row 16c + n of stream p (padding columns
-    // read row 0 of the range; their scores are never used).
-    const int qrow = 16 * c + n < G ? p * G + 16 * c + n - R0 : 0;
-    f32x4_v st = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int pt = (tau / TPS) * NS;    // the tile's first stream
+    const int c16 = (tau % TPS) * 16;   // its first query head inside the group
+    const int p_col = pt + slot_col;
+    const int g_col = c16 + n % CPS;
+    // Padding columns read row 0 of the range; their scores are never used.
+    const int qrow = (g_col < G && p_col < nstreams) ? p_col * G + g_col - R0 : 0;
+    bf16x8_v qb[Sh::QLD];
 #pragma unroll
-    for (int cc = 0; cc < Sh::QLD; ++cc) {
-      const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(k_lds + krow * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
-      const bf16x8_v qb = *reinterpret_cast<const bf16x8_v*>(q_lds + qrow * Sh::QS + (4 * cc + q) * 16);
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb, st, 0, 0, 0);
+    for (int cc = 0; cc < Sh::QLD; ++cc)
+      qb[cc] = *reinterpret_cast<const bf16x8_v*>(q_lds + qrow * Sh::QS + (4 * cc + q) * 16);
+    f32x4_v st;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int p = min(pt + k, HPW - 1);
+      f32x4_v c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cc = 0; cc < Sh::QLD; ++cc) {
+        const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(k_lds + krow * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[cc], c4, 0, 0, 0);
+      }
+      if (k == 0) {
+        st = c4;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[e] = slot_col == k ? c4[e] : st[e];
+      }
     }
     // Masked softmax over the 16 rows of this lane's query column: rows
     // 4q..4q+3 here, the rest in lanes n + 16, n + 32, n + 48.
-    const int S_p = __builtin_amdgcn_readlane(S, p * LPH);
+    int S_col = __builtin_amdgcn_readlane(S, min(pt, HPW - 1) * LPH);
+#pragma unroll
+    for (int k = 1; k < NS; ++k) {
+      const int S_k = __builtin_amdgcn_readlane(S, min(pt + k, HPW - 1) * LPH);
+      S_col = slot_col == k ? S_k : S_col;
+    }
     float x[4];
     float m = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       x[e] = st[e] * a.scale;
-      m = (4 * q + e < S_p) ? fmaxf(m, x[e]) : m;
+      m = (4 * q + e < S_col) ? fmaxf(m, x[e]) : m;
     }
     m = column_reduce<true>(m);
     float sum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[e] = (4 * q + e < S_p) ? expf(x[e] - m) : 0.0f;
+      x[e] = (4 * q + e < S_col) ? expf(x[e] - m) : 0.0f;
       sum += x[e];
     }
     sum = column_reduce<false>(sum);
 #pragma unroll
     for (int e = 0; e < 4; ++e) pa[i][e] = (__bf16)((sum > 0.0f) ? (x[e] / sum) : 0.0f);
     // A stream with an invalid length gets NaN weights, so every output of
-    // its tile is NaN (NaN times any V value, zero included).
-    if ((bad_mask >> (uint32_t)(p * LPH)) & 1u) pa[i] = bf16x4_v{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+    // its columns is NaN (NaN times any V value, zero included).
+    if ((bad_mask >> (uint32_t)(min(p_col, HPW - 1) * LPH)) & 1u)
+      pa[i] = bf16x4_v{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
   }
 
   // ---- V^T to LDS (over the K rows, whose last read is above): block r of
@@ -254,28 +284,43 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- per tile: P.V; lane (q, n) ends with query rows 16c + 4q..4q+3 of
-  //      stream p, dims [n*DPC, n*DPC + DPC) ----
+  // ---- per tile: one P.V pass per stream, each row keeping its own
+  //      stream's; lane (q, n) ends with rows 4q..4q+3 of the tile, dims
+  //      [n*DPC, n*DPC + DPC) ----
   constexpr int DPC = Sh::DPC;
 #pragma unroll
-  for (int i = 0; i < HPW; ++i) {
+  for (int i = 0; i < TW; ++i) {
     if (i >= ntiles) continue;
     const int tau = tau0 + i;
-    const int p = tau / TPS;
-    const int c = tau - p * TPS;
-    const char* vs = v_lds + p * Sh::VSTREAM;
+    const int pt = (tau / TPS) * NS;
+    const int c16 = (tau % TPS) * 16;
     f32x4_v acc[DPC];
 #pragma unroll
-    for (int dt = 0; dt < DPC; ++dt) {
-      const int dim = n * DPC + dt;
-      const bf16x4_v vb = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (kMaxSeq * 2) + q * 8);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[i], vb, f32x4_v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    for (int k = 0; k < NS; ++k) {
+      const char* vs = v_lds + min(pt + k, HPW - 1) * Sh::VSTREAM;
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const int dim = n * DPC + dt;
+        const bf16x4_v vb =
+            *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (kMaxSeq * 2) + q * 8);
+        const f32x4_v c4 =
+            __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[i], vb, f32x4_v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        if (k == 0) {
+          acc[dt] = c4;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[dt][e] = (4 * q + e) / CPS == k ? c4[e] : acc[dt][e];
+        }
+      }
     }
-    // ---- fp16 (RNE) output ----
+    // ---- fp16 (RNE) output: row 4q + e is query head c16 + (4q+e) % CPS of
+    //      stream pt + (4q+e) / CPS ----
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int g = 16 * c + 4 * q + e;  // query head inside the group
-      const uint32_t off = g < G ? (uint32_t)((p * G + g - R0) * D + n * DPC) * 2u : kLaneOutOfRange;
+      const int p = pt + (4 * q + e) / CPS;
+      const int g = c16 + (4 * q + e) % CPS;
+      const uint32_t off =
+          (g < G && p < nstreams) ? (uint32_t)((p * G + g - R0) * D + n * DPC) * 2u : kLaneOutOfRange;
 #pragma unroll
       for (int h8 = 0; h8 < (DPC + 7) / 8; ++h8) {
         constexpr int W = DPC < 8 ? DPC : 8;  // dims per store
@@ -300,12 +345,13 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
 // hit its L2; with chunks == 1 it is stream group w.
 // SB = 1, 2, 4, 8, 16: uniform lengths (cu == null, seqlen_uniform <= SB);
 // SB = 0: lengths from cu (or uniform), the bucket chosen per wave.
-template <int D, int SB, int QT>
+template <int D, int SB, int NS>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupArgs a) {
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
-  __shared__ __attribute__((aligned(16))) char lds[Sh::template lds_bytes<QT>()];
+  constexpr int TW = HPW / NS;  // tiles per wave
+  __shared__ __attribute__((aligned(16))) char lds[Sh::template lds_bytes<TW>()];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
   const uint32_t w = blockIdx.x;
@@ -315,7 +361,8 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const int chunk = (int)(rest % chunks);
   if (sg >= a.stream_groups) return;
   const uint32_t sigma0 = sg * HPW;
-  if ((int)min(a.streams - sigma0, (uint32_t)HPW) * a.tiles_per_stream <= chunk * HPW) return;
+  const int nstreams = (int)min(a.streams - sigma0, (uint32_t)HPW);
+  if (((nstreams + NS - 1) / NS) * a.tiles_per_stream <= chunk * TW) return;
 
   // ---- this lane's stream: batch, head, first row relative to the wave's first batch ----
   const int s = lane / LPH;
@@ -359,7 +406,7 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   smax = __builtin_amdgcn_readfirstlane(smax);
   const uint64_t bad_mask = __ballot(bad && r == 0);
 
-#define FMHA_GROUP_UNIT(SM) group_unit<D, SM, QT>(a, sg, chunk, lane, S, kv_off, row_first, records, bad_mask, lds)
+#define FMHA_GROUP_UNIT(SM) group_unit<D, SM, NS>(a, sg, chunk, lane, S, kv_off, row_first, records, bad_mask, lds)
   if constexpr (SB != 0) {
     FMHA_GROUP_UNIT(SB);
   } else {
