@@ -57,7 +57,10 @@ def main():
                  meta=np.array([B, H, H, D], np.int32))
 
     gqa_cases = [("gqa_sdpa_g2_d128", 3, 4, 2, 128, [3, 16, 7]),
-                 ("gqa_sdpa_g4_d64", 2, 8, 2, 64, [16, 1])]
+                 ("gqa_sdpa_g4_d64", 2, 8, 2, 64, [16, 1]),
+                 # group sizes outside {1, 2, 4, 8} (the matrix-core kernel's)
+                 ("gqa_sdpa_g5_d128", 3, 10, 2, 128, [16, 5, 1]),
+                 ("gqa_sdpa_g3_d256", 2, 6, 2, 256, [9, 16])]
     for name, B, Hq, Hkv, D, seqlens in gqa_cases:
         cu = np.concatenate([[0], np.cumsum(seqlens)]).astype(np.int32)
         q = bf16_normal(rng, (B, Hq, D))

@@ -114,7 +114,8 @@ def test_f64_against_sdpa_fixtures(path):
     assert np.max(np.abs(o - z["o"])) < 1e-12
 
 
-@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 64), (8, 2, 128), (4, 1, 256)])
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 4, 64), (8, 2, 128), (4, 1, 256), (15, 5, 128), (12, 2, 64),
+                                      (7, 1, 256), (40, 8, 128)])
 def test_f64_against_sdpa_live(Hq, Hkv, D):
     import torch
     seqlens = [1, 2, 9, 16]
@@ -230,7 +231,7 @@ def test_fp32_weights_within_fp16_rounding_of_f64():
 # ---------------------------------------------------------------- invariants
 def test_gqa_equals_mha_on_repeated_kv():
     seqlens = oracle.generate_seqlens(20, 16)
-    for g in (2, 4, 8):
+    for g in (2, 3, 4, 5, 7, 8, 12):
         q, k, v, cu = make_inputs(20, 2 * g, 2, 128, seqlens, seed=g)
         o_g, _ = oracle.decode(q, k, v, cu, 2 * g, 2, 128, default_scale(128))
         o_m, _ = oracle.decode(q, np.repeat(k, g, 1), np.repeat(v, g, 1), cu, 2 * g, 2 * g, 128,
