@@ -310,21 +310,30 @@ bool use_mfma_kernel(int g) {
   return !valu_group(g);
 }
 
-template <int D, int NS>
+template <int D, int NS, int LAYOUT>
 hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS>;
+  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS, LAYOUT>;
   hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
   return hipGetLastError();
 }
 
-template <int D>
+template <int D, int LAYOUT>
 hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int ns, int w, hipStream_t stream) {
   switch (ns) {
-    case 1: return launch_mfma_one<D, 1>(g, w, stream);
-    case 2: return launch_mfma_one<D, 2>(g, w, stream);
+    case 1: return launch_mfma_one<D, 1, LAYOUT>(g, w, stream);
+    case 2: return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
     default:
-      if constexpr (fmha_decode::GroupShape<D>::HPW >= 4) return launch_mfma_one<D, 4>(g, w, stream);
-      else return launch_mfma_one<D, 2>(g, w, stream);
+      if constexpr (fmha_decode::GroupShape<D>::HPW >= 4) return launch_mfma_one<D, 4, LAYOUT>(g, w, stream);
+      else return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
+  }
+}
+
+template <int LAYOUT>
+hipError_t launch_mfma_layout(const fmha_decode::GroupArgs& g, int dq, int ns, int w, hipStream_t stream) {
+  switch (dq) {
+    case 64: return launch_mfma_d<64, LAYOUT>(g, ns, w, stream);
+    case 128: return launch_mfma_d<128, LAYOUT>(g, ns, w, stream);
+    default: return launch_mfma_d<256, LAYOUT>(g, ns, w, stream);
   }
 }
 
@@ -335,17 +344,29 @@ int mfma_streams_per_tile(int64_t g, int hpw) {
   return ns < hpw ? ns : hpw;
 }
 
-// a: the fields base_args and the packed entry points fill (lens = cu offsets
-// or null with seqlen_uniform).  rows_hint as for launch().
-int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, int rows_hint) {
+// a: the fields base_args and the entry points fill (packed: lens = cu
+// offsets or null with seqlen_uniform, row and head strides of [rows, Hkv,
+// D]; strided: lens = lengths or null, strides, max_rows).  rows_hint as for
+// launch().
+int launch_mfma(void* stream, int layout, const DecodeArgs& a, int32_t batch, int32_t dq, int rows_hint) {
   const int hpw = kWaveSize / (dq / 8);
   const int64_t hkv = a.num_heads_kv;
   const int64_t g = a.num_heads_q / a.num_heads_kv;
-  const int64_t row_bytes = hkv * dq * 2;
-  // A wave's streams span at most hpw / hkv + 2 batches of up to 16 rows;
-  // their byte range must stay below the out-of-range offsets (2^30).
-  if (row_bytes * FMHA_DECODE_MAX_SEQLEN_KV * (hpw / hkv + 2) >= (int64_t(1) << 30))
-    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
+  // One descriptor covers a wave's streams, which span at most hpw / hkv + 2
+  // batches; that byte range must stay below the out-of-range offsets (2^30).
+  const int64_t batches = hpw / hkv + 2;
+  if (layout == fmha_decode::kLayoutPacked) {
+    const int64_t row_bytes = hkv * dq * 2;
+    if (row_bytes * FMHA_DECODE_MAX_SEQLEN_KV * batches >= (int64_t(1) << 30))
+      return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
+  } else {
+    const int64_t rows = a.max_rows > 0 ? a.max_rows : 1;
+    const int64_t span = ((batches - 1) * a.batch_stride + (rows - 1) * a.row_stride + (hkv - 1) * a.head_stride + dq) * 2;
+    if (span >= (int64_t(1) << 30))
+      return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
+                    "K/V span of %lld batches exceeds 1 GiB for the matrix-core kernel (group size %lld)",
+                    (long long)batches, (long long)g);
+  }
   const int ns = mfma_streams_per_tile(g, hpw);
   const int64_t tps = ns > 1 ? 1 : (g + 15) / 16;  // tiles per stream = waves per stream group
   const int64_t streams = (int64_t)batch * hkv;
@@ -358,8 +379,12 @@ int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, in
   ga.k = a.k;
   ga.v = a.v;
   ga.o = a.o;
-  ga.cu = a.lens;
+  ga.lens = a.lens;
   ga.seqlen_uniform = a.seqlen_uniform;
+  ga.max_rows = a.max_rows;
+  ga.batch_stride = a.batch_stride;
+  ga.row_stride = a.row_stride;
+  ga.head_stride = a.head_stride;
   ga.num_heads_kv = a.num_heads_kv;
   ga.group = (int32_t)g;
   ga.streams = (uint32_t)streams;
@@ -383,12 +408,9 @@ int launch_mfma(void* stream, const DecodeArgs& a, int32_t batch, int32_t dq, in
   int w = dq == 64 || tiles_per_wave >= 4 ? 6 : 4;
   if (unit_bytes < 32 * 1024) w = kMaxWavesPerCU;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t err;
-  switch (dq) {
-    case 64: err = launch_mfma_d<64>(ga, ns, w, s); break;
-    case 128: err = launch_mfma_d<128>(ga, ns, w, s); break;
-    default: err = launch_mfma_d<256>(ga, ns, w, s); break;
-  }
+  const hipError_t err = layout == fmha_decode::kLayoutPacked
+                             ? launch_mfma_layout<fmha_decode::kLayoutPacked>(ga, dq, ns, w, s)
+                             : launch_mfma_layout<fmha_decode::kLayoutStrided>(ga, dq, ns, w, s);
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
 }
@@ -637,7 +659,7 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, a, batch, head_dim_q, kVarlenRowsHint);
+  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
 }
 
@@ -674,7 +696,7 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
   a.seqlen_uniform = seqlen_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, a, batch, head_dim_q, seqlen_kv);
+  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), seqlen_kv);
 }
 
@@ -690,7 +712,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
                   seqlen_kv);
   const int cap = seqlen_kv < FMHA_DECODE_MAX_SEQLEN_KV ? seqlen_kv : FMHA_DECODE_MAX_SEQLEN_KV;
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, cap == 0);
+                        softmax_scale, cap == 0, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
@@ -712,8 +734,10 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
   a.row_stride = (int32_t)kv_row_stride;
   a.head_stride = (int32_t)kv_head_stride;
   const int sb = seqlens_kv ? 0 : bucket_for(seqlen_kv);
-  return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb,
-                seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv);
+  const int rows_hint = seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv;
+  if (use_mfma_kernel(num_heads_q / num_heads_kv))
+    return launch_mfma(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, rows_hint);
+  return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb, rows_hint);
 }
 
 namespace {

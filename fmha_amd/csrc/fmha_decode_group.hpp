@@ -56,11 +56,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct GroupArgs {
   const uint16_t* q;       // [streams * G, D] bf16 bits (= [batch, Hq, D])
-  const uint16_t* k;       // packed [rows, Hkv, D] bf16 bits
+  const uint16_t* k;       // bf16 bits, packed or strided (LAYOUT)
   const uint16_t* v;
   uint16_t* o;             // [batch, Hq, D] fp16 bits
-  const int32_t* cu;       // [batch + 1] row offsets, or null (uniform lengths)
-  int32_t seqlen_uniform;  // rows per batch when cu is null
+  const int32_t* lens;     // packed: [batch + 1] row offsets; strided: [batch] lengths; or null
+  int32_t seqlen_uniform;  // rows per batch when lens is null
+  int32_t max_rows;        // longest valid length (16; strided: the rows each batch has, capped at 16)
+  int64_t batch_stride;    // strided: elements between batches
+  int32_t row_stride;      // elements between rows (packed: Hkv * D)
+  int32_t head_stride;     // elements between KV heads (packed: D)
   int32_t num_heads_kv;
   int32_t group;           // G = Hq / Hkv
   uint32_t streams;        // batch * Hkv
@@ -124,8 +128,8 @@ constexpr uint32_t kPermHi = 0x07060302u;
 // rows of a wave's tiles are one contiguous range [R0, R0 + nrows) of Q.
 template <int D, int SMAX, int NS>
 __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int chunk, int lane, int S,
-                                           uint32_t kv_off, int64_t row_first, uint32_t records, uint64_t bad_mask,
-                                           char* lds) {
+                                           uint32_t kv_off, const uint16_t* kbase, const uint16_t* vbase,
+                                           uint32_t row_bytes, uint32_t records, uint64_t bad_mask, char* lds) {
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -138,8 +142,6 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   const int n = lane & 15;   // MFMA row / column inside the 16x16 tile
   const int G = a.group;
   const int TPS = a.tiles_per_stream;  // 1 when NS > 1
-  const uint32_t Hkv = (uint32_t)a.num_heads_kv;
-  const uint32_t row_bytes = Hkv * D * 2u;
 
   char* k_lds = lds;
   char* v_lds = lds;  // written after the last read of k_lds
@@ -158,8 +160,8 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   const uint64_t qrow0 = (uint64_t)sigma0 * G + R0;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + qrow0 * D, (uint32_t)nrows * D * 2u);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + qrow0 * D, (uint32_t)nrows * D * 2u);
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k + (uint64_t)row_first * Hkv * D, records);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v + (uint64_t)row_first * Hkv * D, records);
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
 
   // ---- issue every load: the query rows, K rows, V rows ----
   u32x4 qr[QT][Sh::QLD];
@@ -343,10 +345,15 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
 // chunks of one stream group (G > 16) run on one XCD (dispatch is
 // round-robin over the 8 XCDs) at nearly the same time and their K/V re-reads
 // hit its L2; with chunks == 1 it is stream group w.
-// SB = 1, 2, 4, 8, 16: uniform lengths (cu == null, seqlen_uniform <= SB);
-// SB = 0: lengths from cu (or uniform), the bucket chosen per wave.
-template <int D, int SB, int NS>
+// SB = 1, 2, 4, 8, 16: uniform lengths (lens == null, seqlen_uniform <= SB);
+// SB = 0: lengths from lens (or uniform), the bucket chosen per wave.
+// LAYOUT: kLayoutPacked (rows [lens[b], lens[b+1]) of [rows, Hkv, D]) or
+// kLayoutStrided (element (b, j, h, d) at b*batch_stride + j*row_stride +
+// h*head_stride + d, lengths lens[b]); one descriptor spans the wave's
+// streams from its first batch (the host bounds that span below 1 GiB).
+template <int D, int SB, int NS, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -364,7 +371,8 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const int nstreams = (int)min(a.streams - sigma0, (uint32_t)HPW);
   if (((nstreams + NS - 1) / NS) * a.tiles_per_stream <= chunk * TW) return;
 
-  // ---- this lane's stream: batch, head, first row relative to the wave's first batch ----
+  // ---- this lane's stream: batch, head, first element relative to the
+  //      wave's base (its first batch) ----
   const int s = lane / LPH;
   const int r = lane % LPH;
   const uint32_t Hkv = (uint32_t)a.num_heads_kv;
@@ -373,29 +381,42 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const uint32_t bq = sok ? sig / Hkv : 0u;
   const uint32_t h = sok ? sig - bq * Hkv : 0u;
   const uint32_t b_first = sigma0 / Hkv;
+  const uint32_t row_bytes = (uint32_t)a.row_stride * 2u;
   int S;
-  int64_t row_first, row0;
-  if (a.cu) {
-    row_first = a.cu[b_first];
-    row0 = a.cu[bq];
-    S = (int)(a.cu[bq + 1] - row0);
+  bool bad;
+  uint64_t base_elem;
+  int64_t lane_elem;  // row 0 of this lane's stream, relative to base_elem
+  uint32_t end;       // byte just past the last row this lane reads
+  if constexpr (LAYOUT == kLayoutPacked) {
+    int64_t row_first, row0;
+    if (a.lens) {
+      row_first = a.lens[b_first];
+      row0 = a.lens[bq];
+      S = (int)(a.lens[bq + 1] - row0);
+    } else {
+      S = a.seqlen_uniform;
+      row_first = (int64_t)b_first * S;
+      row0 = (int64_t)bq * S;
+    }
+    const int64_t rel = row0 - row_first;
+    // A length outside [0, 16], or a table that puts this batch beyond the
+    // reach of the wave's descriptor, makes the stream invalid (NaN output).
+    bad = sok && (S < 0 || S > kMaxSeq || rel < 0 ||
+                  (rel + kMaxSeq) * (int64_t)row_bytes >= (int64_t)kLaneOutOfRange);
+    base_elem = (uint64_t)row_first * a.row_stride;
+    lane_elem = rel * a.row_stride + (int64_t)h * a.head_stride;
+    end = (sok && !bad && S > 0) ? (uint32_t)((rel + S) * (int64_t)row_bytes) : 0u;
   } else {
-    S = a.seqlen_uniform;
-    row_first = (int64_t)b_first * S;
-    row0 = (int64_t)bq * S;
+    S = a.lens ? a.lens[bq] : a.seqlen_uniform;
+    bad = sok && (S < 0 || S > a.max_rows);
+    base_elem = (uint64_t)b_first * (uint64_t)a.batch_stride;
+    lane_elem = (int64_t)(bq - b_first) * a.batch_stride + (int64_t)h * a.head_stride;
+    end = (sok && !bad && S > 0) ? (uint32_t)((lane_elem + (int64_t)(S - 1) * a.row_stride + D) * 2) : 0u;
   }
-  const uint32_t row_bytes = Hkv * D * 2u;
-  const int64_t rel = row0 - row_first;
-  // A length outside [0, 16], or a table that puts this batch beyond the
-  // reach of the wave's descriptor, makes the stream invalid (NaN output).
-  const bool bad = sok && (S < 0 || S > kMaxSeq || rel < 0 ||
-                           (rel + kMaxSeq) * (int64_t)row_bytes >= (int64_t)kLaneOutOfRange);
   if (!sok || bad) S = 0;
-  const uint32_t kv_off =
-      (sok && !bad) ? (uint32_t)rel * row_bytes + h * D * 2u + (uint32_t)r * 16u : kLaneOutOfRange;
+  const uint32_t kv_off = (sok && !bad) ? (uint32_t)(lane_elem * 2) + (uint32_t)r * 16u : kLaneOutOfRange;
   // Descriptor range: the end of the last row any lane reads; bucket: the
   // longest length of the wave; invalid streams as a bit per stream.
-  uint32_t end = S > 0 ? (uint32_t)(rel + S) * row_bytes : 0u;
   int smax = S;
 #pragma unroll
   for (int m = 1; m < kWaveSize; m <<= 1) {
@@ -405,8 +426,11 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const uint32_t records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
   smax = __builtin_amdgcn_readfirstlane(smax);
   const uint64_t bad_mask = __ballot(bad && r == 0);
+  const uint16_t* kbase = a.k + base_elem;
+  const uint16_t* vbase = a.v + base_elem;
 
-#define FMHA_GROUP_UNIT(SM) group_unit<D, SM, NS>(a, sg, chunk, lane, S, kv_off, row_first, records, bad_mask, lds)
+#define FMHA_GROUP_UNIT(SM) \
+  group_unit<D, SM, NS>(a, sg, chunk, lane, S, kv_off, kbase, vbase, row_bytes, records, bad_mask, lds)
   if constexpr (SB != 0) {
     FMHA_GROUP_UNIT(SB);
   } else {

@@ -68,9 +68,10 @@ extern "C" {
  *                   below 2^24, else FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *                   The environment variable FMHA_DECODE_GQA_KERNEL=mfma
  *                   runs the matrix-core kernel for every G, =valu keeps the
- *                   VALU kernel wherever it exists.  This entry point and
- *                   fmha_decode_fwd_uniform take any G; the others take
- *                   G = 1, 2, 4 or 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   VALU kernel wherever it exists.  This entry point,
+ *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
+ *                   any G; the others take G = 1, 2, 4 or 8 (else
+ *                   FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q
@@ -136,8 +137,10 @@ int fmha_decode_fwd_uniform(void* stream,
  *                the rows each batch has room for: a length above
  *                min(seqlen_kv, 16) gets NaN outputs, rows past a batch's
  *                length are never read (padding may hold anything)
- * One batch's span (rows and heads) must stay below 1 GiB.  Other arguments
- * as fmha_decode_fwd.
+ * One batch's span (rows and heads) must stay below 1 GiB; with G outside
+ * {1, 2, 4, 8} (the matrix-core kernel) so must the span of the
+ * 64/(head_dim/8)/num_heads_kv + 2 batches a wave may touch, else
+ * FMHA_DECODE_ERROR_NOT_SUPPORTED.  Other arguments as fmha_decode_fwd.
  */
 int fmha_decode_fwd_strided(void* stream,
                             const void* Q, const void* K, const void* V, void* O,

@@ -148,7 +148,9 @@ def paged(lib, **kw):
     (dict(hs=4), BAD, "multiples of 8"),
     (dict(rs=1 << 26), BAD, "1 GiB"),
     (dict(lens=CU + 2), BAD, "seqlens_kv"),
-    (dict(hq=24, hkv=8), NOTSUP, "1, 2, 4 or 8"),
+    # Any group size runs; outside {1, 2, 4, 8} the matrix-core kernel's
+    # descriptor spans the batches a wave touches (here 2 of 1 GiB each).
+    (dict(hq=24, hkv=8, bs=1 << 29), NOTSUP, "exceeds 1 GiB"),
     (dict(k=None), BAD, "non-null"),
     (dict(dq=128, dkv=64), BAD, "head_dim_q"),
 ])

@@ -1,5 +1,5 @@
 """GPU parity of the matrix-core kernel (fmha_decode_group_kernel) against the
-CPU oracle, through the packed-layout entry points.
+CPU oracle, through the packed-layout and strided entry points.
 
 The kernel serves every group size G = Hq / Hkv outside {1, 2, 4, 8} (which
 the VALU kernel cannot), and any G when FMHA_DECODE_GQA_KERNEL=mfma.  The
@@ -9,8 +9,8 @@ fmha_mfma_4x4x4_kernel.hpp:195-196); the oracle's mapping is KV head h / G
 every length 0..16 in one varlen batch, uniform lengths, KV-head counts below
 and not dividing a wave's 64 / (D/8) streams (waves spanning batches),
 several waves per stream group (G * streams per wave > 64 query rows),
-the S = 1 known answer, NaN-poisoned neighbour streams and batches, and
-invalid lengths.
+the S = 1 known answer, NaN-poisoned neighbour streams and batches,
+invalid lengths, and strided caches (BHSD, padded BSHD with NaN padding).
 """
 import numpy as np
 import pytest
@@ -159,3 +159,76 @@ def test_mfma_matches_valu_within_gate(mfma, monkeypatch):
     assert_pass(oracle.compare(o_mfma, r, slack), "mfma")
     assert_pass(oracle.compare(o_valu, r, slack), "valu")
     assert_pass(oracle.compare(o_mfma, o_valu, slack), "mfma vs valu")
+
+
+def _bf16_dev(gen, shape, dev):
+    import torch
+    return torch.randn(*shape, generator=gen, device=dev, dtype=torch.bfloat16)
+
+
+def _bits(t):
+    import torch
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 15, 5), (64, 24, 8), (256, 12, 2), (128, 6, 1), (128, 40, 2)])
+def test_strided_layouts(layout, D, Hq, Hkv):
+    """Strided caches (BHSD through a transposed view, padded BSHD) with
+    per-batch lengths below the padding; padding rows hold NaN and must not
+    be read."""
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(D * 100 + Hq + Hkv)
+    B, cap = 23, 12
+    seqlens = np.random.default_rng(Hq + Hkv).integers(0, cap + 1, size=B).astype(np.int32)
+    q = _bf16_dev(gen, (B, Hq, 1, D), dev)
+    if layout == "bhsd":
+        kc = _bf16_dev(gen, (B, Hkv, cap, D), dev)
+        vc = _bf16_dev(gen, (B, Hkv, cap, D), dev)
+        for b in range(B):
+            kc[b, :, seqlens[b]:] = float("nan")
+            vc[b, :, seqlens[b]:] = float("nan")
+        k, v = kc.transpose(1, 2), vc.transpose(1, 2)
+    else:
+        k = _bf16_dev(gen, (B, cap, Hkv, D), dev)
+        v = _bf16_dev(gen, (B, cap, Hkv, D), dev)
+        for b in range(B):
+            k[b, seqlens[b]:] = float("nan")
+            v[b, seqlens[b]:] = float("nan")
+    o = fmha_amd.fmha_decode_strided(q, k, v, seqlens_kv=torch.from_numpy(seqlens).to(dev))
+    torch.cuda.synchronize()
+    pk = np.concatenate([_bits(k[b, :seqlens[b]]).reshape(-1, Hkv, D) for b in range(B)])
+    pv = np.concatenate([_bits(v[b, :seqlens[b]]).reshape(-1, Hkv, D) for b in range(B)])
+    r, slack = oracle.decode(_bits(q).reshape(B, Hq, D), pk, pv, cu_from_seqlens(seqlens), Hq, Hkv, D,
+                             default_scale(D), with_slack=True)
+    assert_pass(oracle.compare(_bits(o).reshape(r.shape), r, slack), f"{layout} D={D} Hq={Hq} Hkv={Hkv}")
+
+
+@pytest.mark.parametrize("S", [1, 7, 16])
+def test_strided_uniform_and_bad_length(S):
+    """Uniform strided lengths; a per-batch length above the cache's rows gives
+    NaN for that batch only."""
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(S)
+    B, Hq, Hkv, D = 19, 21, 3, 128
+    q = _bf16_dev(gen, (B, Hq, 1, D), dev)
+    k = _bf16_dev(gen, (B, S, Hkv, D), dev)
+    v = _bf16_dev(gen, (B, S, Hkv, D), dev)
+    o = fmha_amd.fmha_decode_strided(q, k, v)
+    torch.cuda.synchronize()
+    seqlens = np.full(B, S, np.int32)
+    r, slack = oracle.decode(_bits(q).reshape(B, Hq, D), _bits(k).reshape(-1, Hkv, D), _bits(v).reshape(-1, Hkv, D),
+                             cu_from_seqlens(seqlens), Hq, Hkv, D, default_scale(D), with_slack=True)
+    assert_pass(oracle.compare(_bits(o).reshape(r.shape), r, slack), f"uniform S={S}")
+    lens = np.full(B, S, np.int32)
+    lens[4] = S + 1
+    o2 = fmha_amd.fmha_decode_strided(q, k, v, seqlens_kv=torch.from_numpy(lens).to(dev))
+    torch.cuda.synchronize()
+    o2b = oracle.f16_to_f32(_bits(o2).reshape(B, Hq, D))
+    assert np.all(np.isnan(o2b[4]))
+    keep = [b for b in range(B) if b != 4]
+    assert np.array_equal(_bits(o2).reshape(B, Hq, D)[keep], _bits(o).reshape(B, Hq, D)[keep])
