@@ -751,9 +751,9 @@ int log2_pow2(int x) {
 int paged_checks(const void* Q, const void* K_cache, const void* V_cache, void* O, const int32_t* block_table,
                  int32_t block_table_stride, const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
                  int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
-                 int32_t head_dim_kv, float softmax_scale) {
+                 int32_t head_dim_kv, float softmax_scale, bool any_group = false) {
   int rc = check_common(Q, K_cache, V_cache, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
+                        softmax_scale, false, any_group);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (page_size < 1 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "page_size must be a power of two in [1, 2^20] (got %d)",
@@ -808,12 +808,37 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
                      FMHA_DECODE_MAX_SEQLEN_KV, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
 }
 
+namespace {
+
+// Group size the long-row kernels run a call with G query heads per KV head:
+// G itself for 1, 2, 4, 8; 4 for 3 and 8 for 5-7 (query-group padding); 0
+// when they cannot (G > 8 outside those).
+int split_group(int g) {
+  if (valu_group(g)) return g;
+  if (g == 3) return 4;
+  if (g >= 5 && g <= 7) return 8;
+  return 0;
+}
+
+// Bytes of one query-group-padded copy of Q or O ([batch, Hkv * GP, D]),
+// aligned for the workspace.
+size_t group_pad_bytes(int64_t batch, int hkv, int gp, int d) {
+  return align_up((size_t)batch * (size_t)hkv * (size_t)gp * (size_t)d * 2);
+}
+
+}  // namespace
+
 extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                                      int32_t max_seqlen_kv, int32_t head_dim) {
   if (batch <= 0 || num_heads_q <= 0 || num_heads_kv <= 0 || max_seqlen_kv < 0 ||
       (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
-  return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
+  const int g = num_heads_q % num_heads_kv == 0 ? num_heads_q / num_heads_kv : 0;
+  const int gp = split_group(g);
+  if (gp == 0 || gp == g) return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
+  // Padded query group: its Q and O copies, then the plan for Hkv * GP heads.
+  return 2 * group_pad_bytes(batch, num_heads_kv, gp, head_dim) +
+         plan_split(batch, num_heads_kv * gp, num_heads_kv, max_seqlen_kv, head_dim).total;
 }
 
 namespace {
@@ -881,6 +906,50 @@ int split_check_workspace_args(int32_t max_seqlen_kv) {
   return FMHA_DECODE_SUCCESS;
 }
 
+// Runs body(Q, O, num_heads_q, workspace, workspace_bytes) for a long-row
+// call.  With G outside {1, 2, 4, 8} (and at most 8) the body sees copies of
+// Q and O padded to GP query heads per KV head, placed at the start of the
+// workspace (the rest goes to the body), and the copies are made and read
+// back around it on the same stream.
+template <class BODY>
+int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int32_t hq, int32_t hkv, int32_t d,
+                       void* workspace, size_t workspace_bytes, BODY body) {
+  const int g = hq / hkv;
+  const int gp = split_group(g);
+  if (gp == 0)
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
+                  "lengths beyond 16 (and paged caches) take num_heads_q / num_heads_kv of 1-8 (got %d)", g);
+  if (gp == g) return body(Q, O, hq, workspace, workspace_bytes);
+  const size_t pb = group_pad_bytes(batch, hkv, gp, d);
+  if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
+  if ((reinterpret_cast<uintptr_t>(workspace) & (kWorkspaceAlign - 1)) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be 256-byte aligned");
+  if (workspace_bytes < 2 * pb)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace too small (%zu bytes) for the padded query group",
+                  workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* qp = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* op = reinterpret_cast<uint16_t*>(ws + pb);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t streams = (uint64_t)batch * (uint64_t)hkv;
+  const uint64_t pad_chunks = streams * (uint64_t)gp * (uint64_t)(d / 8);
+  const uint64_t out_chunks = streams * (uint64_t)g * (uint64_t)(d / 8);
+  const uint64_t pad_blocks = (pad_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
+  const uint64_t out_blocks = (out_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
+  if (pad_blocks > (uint64_t)INT32_MAX) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
+  hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks), dim3(fmha_decode::kPadThreads),
+                     0, st, static_cast<const uint16_t*>(Q), qp, streams, g, gp, d);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  const int rc = body(qp, op, hkv * gp, ws + 2 * pb, workspace_bytes - 2 * pb);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
+                     dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, gp, d);
+  err = hipGetLastError();
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return FMHA_DECODE_SUCCESS;
+}
+
 }  // namespace
 
 extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -890,33 +959,44 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
                                        void* workspace, size_t workspace_bytes) {
   g_detail[0] = '\0';
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
+                        softmax_scale, false, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
   if ((rc = split_check_workspace_args(max_seqlen_kv)) != FMHA_DECODE_SUCCESS) return rc;
+  const int rows_hint = max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint;
+  DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  d.lens = cu_seqlens_kv;
+  d.row_stride = num_heads_kv * head_dim_q;
+  d.head_stride = head_dim_q;
+  d.max_rows = max_seqlen_kv;
+  // Rows that fit the short kernels take them (same numerics, lengths above
+  // max_seqlen_kv give NaN there too); the matrix-core kernel needs no
+  // workspace.
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV && use_mfma_kernel(num_heads_q / num_heads_kv))
+    return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
   // One batch's K/V rows (up to nblk * 16) are addressed through one range.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
   const int64_t padded_rows = ((int64_t)max_seqlen_kv + 15) / 16 * 16;
-  SplitArgs a;
-  rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale, workspace,
-                     workspace_bytes, (padded_rows > 16 ? padded_rows : 16) * row_bytes, a);
-  if (rc != FMHA_DECODE_SUCCESS) return rc;
-  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
-    // Rows that fit the short kernel take it (same numerics, lengths above
-    // max_seqlen_kv give NaN there too); the workspace goes unused.
-    DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
-    d.lens = cu_seqlens_kv;
-    d.row_stride = num_heads_kv * head_dim_q;
-    d.head_stride = head_dim_q;
-    d.max_rows = max_seqlen_kv;
-    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
-                  max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint);
-  }
-  a.cu = cu_seqlens_kv;
-  a.len_mode = fmha_decode::kLenCu;
-  return split_launch(stream, fmha_decode::kLayoutPacked, a, head_dim_q);
+  return with_group_padding(
+      stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
+      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
+        SplitArgs a;
+        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale, ws,
+                                ws_bytes, (padded_rows > 16 ? padded_rows : 16) * row_bytes, a);
+        if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
+        if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
+          DecodeArgs dd = d;
+          dd.q = static_cast<const uint16_t*>(q);
+          dd.o = static_cast<uint16_t*>(o);
+          dd.num_heads_q = hq;
+          return launch(stream, fmha_decode::kLayoutPacked, dd, batch, head_dim_q, 0, rows_hint);
+        }
+        a.cu = cu_seqlens_kv;
+        a.len_mode = fmha_decode::kLenCu;
+        return split_launch(stream, fmha_decode::kLayoutPacked, a, head_dim_q);
+      });
 }
 
 extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -934,7 +1014,7 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
                                    kv_head_stride, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
                                    head_dim_kv, softmax_scale);
   rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale,
-                    false);
+                    false, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
@@ -947,16 +1027,20 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
       ((int64_t)(max_seqlen_kv - 1) * kv_row_stride + (int64_t)(num_heads_kv - 1) * kv_head_stride + head_dim_q) * 2;
   if (extent >= (int64_t(1) << 30))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "one batch's K/V span exceeds 1 GiB");
-  SplitArgs a;
-  rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale, workspace,
-                     workspace_bytes, extent, a);
-  if (rc != FMHA_DECODE_SUCCESS) return rc;
-  a.cu = seqlens_kv;
-  a.len_mode = seqlens_kv ? fmha_decode::kLenArray : fmha_decode::kLenUniform;
-  a.batch_stride = kv_batch_stride;
-  a.row_stride = (int32_t)kv_row_stride;
-  a.head_stride = (int32_t)kv_head_stride;
-  return split_launch(stream, fmha_decode::kLayoutStrided, a, head_dim_q);
+  return with_group_padding(
+      stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
+      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
+        SplitArgs a;
+        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale, ws,
+                                ws_bytes, extent, a);
+        if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
+        a.cu = seqlens_kv;
+        a.len_mode = seqlens_kv ? fmha_decode::kLenArray : fmha_decode::kLenUniform;
+        a.batch_stride = kv_batch_stride;
+        a.row_stride = (int32_t)kv_row_stride;
+        a.head_stride = (int32_t)kv_head_stride;
+        return split_launch(stream, fmha_decode::kLayoutStrided, a, head_dim_q);
+      });
 }
 
 extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const void* K_cache, const void* V_cache,
@@ -969,26 +1053,30 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
   int rc = split_check_workspace_args(max_seqlen_kv);
   if (rc != FMHA_DECODE_SUCCESS) return rc;
   rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
-                    num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
+                    num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale, true);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   max_seqlen_kv = paged_capacity(block_table_stride, page_size, max_seqlen_kv);
-  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
-    return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
-                       max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
   // A sub-block's range covers at most 16 rows of one page.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
-  SplitArgs a;
-  rc = split_prepare(Q, K_cache, V_cache, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q,
-                     softmax_scale, workspace, workspace_bytes, 16 * row_bytes, a);
-  if (rc != FMHA_DECODE_SUCCESS) return rc;
-  a.cu = seqlens_kv;
-  a.len_mode = fmha_decode::kLenArray;
-  a.block_table = block_table;
-  a.bt_stride = block_table_stride;
-  a.page_shift = log2_pow2(page_size);
-  a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
-  return split_launch(stream, page_size >= 16 ? fmha_decode::kLayoutPagedBlock : fmha_decode::kLayoutPaged, a,
-                      head_dim_q);
+  return with_group_padding(
+      stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
+      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
+        if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
+          return paged_short(stream, q, K_cache, V_cache, o, block_table, block_table_stride, seqlens_kv, page_size,
+                             max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale);
+        SplitArgs a;
+        int rc2 = split_prepare(q, K_cache, V_cache, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q,
+                                softmax_scale, ws, ws_bytes, 16 * row_bytes, a);
+        if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
+        a.cu = seqlens_kv;
+        a.len_mode = fmha_decode::kLenArray;
+        a.block_table = block_table;
+        a.bt_stride = block_table_stride;
+        a.page_shift = log2_pow2(page_size);
+        a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
+        return split_launch(stream, page_size >= 16 ? fmha_decode::kLayoutPagedBlock : fmha_decode::kLayoutPaged, a,
+                            head_dim_q);
+      });
 }
 
 extern "C" const char* fmha_decode_error_string(int code) {

@@ -399,9 +399,10 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
       row0 = (int64_t)bq * S;
     }
     const int64_t rel = row0 - row_first;
-    // A length outside [0, 16], or a table that puts this batch beyond the
-    // reach of the wave's descriptor, makes the stream invalid (NaN output).
-    bad = sok && (S < 0 || S > kMaxSeq || rel < 0 ||
+    // A length outside [0, max_rows] (max_rows <= 16), or a table that puts
+    // this batch beyond the reach of the wave's descriptor, makes the stream
+    // invalid (NaN output).
+    bad = sok && (S < 0 || S > a.max_rows || rel < 0 ||
                   (rel + kMaxSeq) * (int64_t)row_bytes >= (int64_t)kLaneOutOfRange);
     base_elem = (uint64_t)row_first * a.row_stride;
     lane_elem = rel * a.row_stride + (int64_t)h * a.head_stride;
@@ -446,6 +447,43 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
       FMHA_GROUP_UNIT(16);
   }
 #undef FMHA_GROUP_UNIT
+}
+
+// ---------------------------------------------------------------------------
+// Query-group padding for the long-row paths (split-KV, single pass, paged
+// short kernel), whose kernels exist for G in {1, 2, 4, 8}: another G up to
+// 8 runs as GP (4 for 3, 8 for 5-7) on copies of Q and O with GP rows per
+// stream, the rows g >= G of Q zero and those of O dropped.  Row sigma*G + g
+// of Q / O ([streams, G, D]) is row sigma*GP + g of the copy.  One thread per
+// 16-byte chunk; every index is checked against the element counts.
+// ---------------------------------------------------------------------------
+constexpr int kPadThreads = 256;
+
+__global__ __launch_bounds__(kPadThreads) void pad_query_group_kernel(const uint16_t* q, uint16_t* qp,
+                                                                       uint64_t streams, int G, int GP, int D) {
+  const uint64_t cpr = (uint64_t)(D / 8);  // 16-byte chunks per row
+  const uint64_t i = (uint64_t)blockIdx.x * kPadThreads + threadIdx.x;
+  if (i >= streams * (uint64_t)GP * cpr) return;
+  const uint64_t row = i / cpr;
+  const uint64_t c = i - row * cpr;
+  const uint64_t sigma = row / (uint64_t)GP;
+  const int g = (int)(row - sigma * (uint64_t)GP);
+  u32x4 x = {0u, 0u, 0u, 0u};
+  if (g < G) x = *reinterpret_cast<const u32x4*>(q + ((sigma * (uint64_t)G + g) * D + c * 8));
+  *reinterpret_cast<u32x4*>(qp + (row * D + c * 8)) = x;
+}
+
+__global__ __launch_bounds__(kPadThreads) void unpad_output_group_kernel(const uint16_t* op, uint16_t* o,
+                                                                          uint64_t streams, int G, int GP, int D) {
+  const uint64_t cpr = (uint64_t)(D / 8);
+  const uint64_t i = (uint64_t)blockIdx.x * kPadThreads + threadIdx.x;
+  if (i >= streams * (uint64_t)G * cpr) return;
+  const uint64_t row = i / cpr;  // row of O
+  const uint64_t c = i - row * cpr;
+  const uint64_t sigma = row / (uint64_t)G;
+  const uint64_t g = row - sigma * (uint64_t)G;
+  *reinterpret_cast<u32x4*>(o + (row * D + c * 8)) =
+      *reinterpret_cast<const u32x4*>(op + ((sigma * (uint64_t)GP + g) * D + c * 8));
 }
 
 }  // namespace fmha_decode

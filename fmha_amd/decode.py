@@ -243,7 +243,8 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     max_pages * page_size give NaN.  With max_seqlen_kv given the call goes
     through fmha_decode_fwd_splitkv_paged with workspace (a uint8 device
     tensor of splitkv_workspace_size(B, Hq, Hkv, max_seqlen_kv, D) bytes,
-    allocated here when None; unused for max_seqlen_kv <= 16)."""
+    allocated here when None; for max_seqlen_kv <= 16 it only holds the
+    padded query group of a group size outside {1, 2, 4, 8})."""
     import torch
     B, Hq, D = _q_shape(q)
     out = _check_q_out(q, out)

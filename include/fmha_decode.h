@@ -70,8 +70,9 @@ extern "C" {
  *                   runs the matrix-core kernel for every G, =valu keeps the
  *                   VALU kernel wherever it exists.  This entry point,
  *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
- *                   any G; the others take G = 1, 2, 4 or 8 (else
- *                   FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   any G; the split-KV entries G = 1-8 beyond 16 rows;
+ *                   fmha_decode_fwd_paged and fmha_decode_fwd_fp32_weights
+ *                   G = 1, 2, 4 or 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q
@@ -189,6 +190,14 @@ int fmha_decode_fwd_paged(void* stream,
  * fmha_decode_splitkv_workspace_size(batch, Hq, Hkv, max_seqlen_kv, head_dim)
  * bytes, 256-byte aligned; its contents on entry do not matter.  Calls that
  * share a workspace must be ordered (same stream or synchronised).
+ *
+ * Group sizes G = num_heads_q / num_heads_kv: with max_seqlen_kv <= 16 any G
+ * (as fmha_decode_fwd); beyond 16 (and for the paged entry at any length)
+ * G = 1-8: the long-row kernels exist for 1, 2, 4, 8, and G = 3, 5, 6, 7 run
+ * as 4 or 8 on copies of Q and O padded to that many query heads per KV head,
+ * which the workspace size includes (two copies of [batch, Hkv * 4 or 8,
+ * head_dim] bf16/fp16, ahead of the split-KV data).  Larger G beyond 16 rows
+ * returns FMHA_DECODE_ERROR_NOT_SUPPORTED.
  */
 size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                           int32_t max_seqlen_kv, int32_t head_dim);
@@ -212,7 +221,8 @@ int fmha_decode_fwd_splitkv(void* stream,
  * One batch's span (max_seqlen_kv rows, all heads) must stay below 1 GiB.
  * The workspace is sized by fmha_decode_splitkv_workspace_size(batch, Hq,
  * Hkv, max_seqlen_kv, head_dim) and unused when max_seqlen_kv <= 16 (the
- * call then runs fmha_decode_fwd_strided).  No counterpart in the reference,
+ * call then runs fmha_decode_fwd_strided, any G).  Group sizes as for
+ * fmha_decode_fwd_splitkv.  No counterpart in the reference,
  * which has neither layout nor lengths beyond 16 (README.md:166-168,
  * README.md:233).
  */
@@ -230,8 +240,10 @@ int fmha_decode_fwd_splitkv_strided(void* stream,
  * min(max_seqlen_kv, block_table_stride * page_size) gets NaN outputs (so no
  * batch reads past its row of the block table); rows past a batch's length
  * and pages it does not map are never read.  Workspace as for
- * fmha_decode_fwd_splitkv_strided (unused when that bound is <= 16: the call
- * then runs fmha_decode_fwd_paged's kernel).  No counterpart in the
+ * fmha_decode_fwd_splitkv_strided (when that bound is <= 16 the call runs
+ * fmha_decode_fwd_paged's kernel, and the workspace only holds a padded
+ * query group).  Group sizes 1-8 (3, 5, 6, 7 padded, as for
+ * fmha_decode_fwd_splitkv) at any length.  No counterpart in the
  * reference.
  */
 int fmha_decode_fwd_splitkv_paged(void* stream,

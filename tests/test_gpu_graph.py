@@ -129,3 +129,51 @@ def test_graph_long_rows_replay_match_eager():
             assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
         fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 64)
         torch.cuda.synchronize()
+
+
+def test_graph_matrix_core_kernel_replays_match_eager():
+    """The matrix-core kernel (group sizes outside {1, 2, 4, 8}) in a graph:
+    varlen, uniform and strided calls, an MQA shape with two waves per stream
+    group, every replay bit-equal to the eager result."""
+    import torch
+    import fmha_amd
+    seqlens = oracle.generate_seqlens(48, 16)
+    q, k, v, cu = make_inputs(48, 20, 4, 128, seqlens, seed=95)
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    cud = torch.from_numpy(cu).cuda()
+    _, ku, vu, _ = make_inputs(48, 20, 4, 128, [7] * 48, seed=96)
+    kb = to_dev(ku).reshape(48, 7, 4, 128)
+    vb = to_dev(vu).reshape(48, 7, 4, 128)
+    qm, km, vm, cum = make_inputs(40, 32, 1, 64, seqlens[:40], seed=97)
+    qmd, kmd, vmd, cumd = to_dev(qm), to_dev(km), to_dev(vm), torch.from_numpy(cum).cuda()
+    outs = [torch.empty(48, 20, 128, dtype=torch.float16, device="cuda") for _ in range(3)]
+    outs.append(torch.empty(40, 32, 64, dtype=torch.float16, device="cuda"))
+
+    def calls():
+        fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, out=outs[0])
+        fmha_amd.fmha_decode(qd, kb, vb, out=outs[1])
+        fmha_amd.fmha_decode_strided(qd, kb, vb, out=outs[2])
+        fmha_amd.fmha_decode(qmd, kmd, vmd, cu_seqlens_kv=cumd, out=outs[3])
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    assert torch.equal(eager[1].view(torch.int16), eager[2].view(torch.int16))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        calls()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
+        fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud)
+        torch.cuda.synchronize()

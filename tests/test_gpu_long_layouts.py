@@ -225,3 +225,42 @@ def test_strided_single_pass_batches_per_wave(D, Hq, Hkv, B):
     o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd single pass per-wave batches D={D} Hkv={Hkv}")
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("B,cap", [(5, 300), (600, 40)])
+def test_strided_long_padded_group(layout, B, cap):
+    """G = 5 beyond 16 rows over a strided cache (padded query group)."""
+    import fmha_amd
+    import torch
+    D, Hq, Hkv = 128, 20, 4
+    rng = np.random.default_rng(B + cap)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[0] = cap
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=B + cap + 3)
+    kc = _strided_cache(kp, seqlens, cap, Hkv, D, layout)
+    vc = _strided_cache(vp, seqlens, cap, Hkv, D, layout)
+    o = fmha_amd.fmha_decode_strided(to_dev(q), _strided_view(kc, layout), _strided_view(vc, layout),
+                                     seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"strided {layout} G=5 B={B} cap={cap}")
+
+
+@pytest.mark.parametrize("page_size", [1, 16])
+@pytest.mark.parametrize("B,max_len", [(4, 300), (700, 40), (40, 10)])
+def test_paged_padded_group(page_size, B, max_len):
+    """G = 7 over a paged cache through the workspace entry: split, single
+    pass and (max_seqlen_kv <= 16) the short paged kernel, all on the padded
+    query group."""
+    import fmha_amd
+    import torch
+    D, Hq, Hkv = 128, 14, 2
+    rng = np.random.default_rng(page_size * 7 + B + max_len)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + B + max_len + 5)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max(max_len, 16), f"paged G=7 ps={page_size} B={B} max={max_len}")

@@ -234,3 +234,28 @@ def test_onepass_batches_per_wave_invalid_length():
                         np.ascontiguousarray(r.reshape(B, Hq, D)[keep]).ravel(),
                         np.ascontiguousarray(slack.reshape(B, Hq, D)[keep]).ravel())
     assert_pass(st, "neighbours of an invalid length, single pass")
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 24, 8), (64, 20, 4), (256, 14, 2), (128, 7, 1), (128, 12, 2)])
+@pytest.mark.parametrize("B,max_len", [(5, 700), (600, 48), (3, 17)])
+def test_padded_query_group(D, Hq, Hkv, B, max_len):
+    """Group sizes 3, 5, 6, 7 beyond 16 rows: the split-KV launches (few
+    batches) and the single pass (many) run on copies of Q and O padded to 4
+    or 8 query heads per KV head in the workspace."""
+    rng = np.random.default_rng(B + max_len + D + Hq)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(24, 8), (48, 4), (32, 1)])
+def test_any_group_short_rows_through_split_entry(Hq, Hkv):
+    """max_seqlen_kv <= 16 with a group size the VALU kernel lacks: the split
+    entry runs the matrix-core kernel (G = 12 and 32 included)."""
+    rng = np.random.default_rng(Hq)
+    seqlens = rng.integers(0, 11, size=33).astype(np.int32)
+    _case(33, Hq, Hkv, 128, seqlens, 10, seed=Hq + 7)
+    q, k, v, cu = make_inputs(3, Hq, Hkv, 128, np.array([4, 12, 9], np.int32), seed=Hq + 8)
+    o = _run(q, k, v, cu, Hq, Hkv, 128, 10).reshape(3, Hq, 128)
+    assert np.all(np.isnan(oracle.f16_to_f32(o[1])))      # 12 > max_seqlen_kv
+    assert np.all(np.isfinite(oracle.f16_to_f32(o[[0, 2]])))

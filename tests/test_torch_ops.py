@@ -59,6 +59,26 @@ def test_op_matches_direct_call_and_oracle():
 
 
 @pytest.mark.gpu
+def test_op_any_group_size():
+    """torch.ops.fmha_amd.decode with a group size outside {1, 2, 4, 8} (the
+    matrix-core kernel): same bits as the direct call, oracle parity."""
+    import torch
+    import fmha_amd
+    import fmha_amd.torch_ops  # noqa: F401
+    from tests.common import assert_pass
+    seqlens = oracle.generate_seqlens(24, 16)
+    q, k, v, cu = make_inputs(24, 21, 3, 128, seqlens, seed=1001)
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    cud = torch.from_numpy(cu).cuda()
+    o_op = torch.ops.fmha_amd.decode(qd, kd, vd, cud, -1, 0.0)
+    o_dir = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud)
+    torch.cuda.synchronize()
+    assert torch.equal(o_op.view(torch.int16), o_dir.view(torch.int16))
+    r, slack = oracle.decode(q, k, v, cu, 21, 3, 128, default_scale(128), with_slack=True)
+    assert_pass(oracle.compare(o_op.view(torch.int16).cpu().numpy().view(np.uint16), r, slack), "torch op G=7")
+
+
+@pytest.mark.gpu
 def test_opcheck_and_compile():
     import torch
     import fmha_amd.torch_ops  # noqa: F401
