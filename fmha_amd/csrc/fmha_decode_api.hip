@@ -811,13 +811,12 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
 namespace {
 
 // Group size the long-row kernels run a call with G query heads per KV head:
-// G itself for 1, 2, 4, 8; 4 for 3 and 8 for 5-7 (query-group padding); 0
-// when they cannot (G > 8 outside those).
+// G itself for 1, 2, 4, 8; 4 for 3 and 8 for 5-7 and above 8 (query-group
+// padding; above 8 in slices of 8 heads, one after the other); 0 for G < 1.
 int split_group(int g) {
+  if (g < 1) return 0;
   if (valu_group(g)) return g;
-  if (g == 3) return 4;
-  if (g >= 5 && g <= 7) return 8;
-  return 0;
+  return g == 3 ? 4 : 8;
 }
 
 // Bytes of one query-group-padded copy of Q or O ([batch, Hkv * GP, D]),
@@ -907,18 +906,16 @@ int split_check_workspace_args(int32_t max_seqlen_kv) {
 }
 
 // Runs body(Q, O, num_heads_q, workspace, workspace_bytes) for a long-row
-// call.  With G outside {1, 2, 4, 8} (and at most 8) the body sees copies of
-// Q and O padded to GP query heads per KV head, placed at the start of the
-// workspace (the rest goes to the body), and the copies are made and read
-// back around it on the same stream.
+// call.  With G outside {1, 2, 4, 8} the body sees copies of Q and O padded
+// to GP query heads per KV head, placed at the start of the workspace (the
+// rest goes to the body), made and read back around it on the same stream;
+// G > 8 runs the body once per slice of up to 8 query heads (K and V are
+// then read once per slice).
 template <class BODY>
 int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int32_t hq, int32_t hkv, int32_t d,
                        void* workspace, size_t workspace_bytes, BODY body) {
   const int g = hq / hkv;
   const int gp = split_group(g);
-  if (gp == 0)
-    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
-                  "lengths beyond 16 (and paged caches) take num_heads_q / num_heads_kv of 1-8 (got %d)", g);
   if (gp == g) return body(Q, O, hq, workspace, workspace_bytes);
   const size_t pb = group_pad_bytes(batch, hkv, gp, d);
   if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
@@ -933,23 +930,27 @@ int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int3
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint64_t streams = (uint64_t)batch * (uint64_t)hkv;
   const uint64_t pad_chunks = streams * (uint64_t)gp * (uint64_t)(d / 8);
-  const uint64_t out_chunks = streams * (uint64_t)g * (uint64_t)(d / 8);
   const uint64_t pad_blocks = (pad_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
-  const uint64_t out_blocks = (out_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
   if (pad_blocks > (uint64_t)INT32_MAX) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
-  hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks), dim3(fmha_decode::kPadThreads),
-                     0, st, static_cast<const uint16_t*>(Q), qp, streams, g, gp, d);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
-  const int rc = body(qp, op, hkv * gp, ws + 2 * pb, workspace_bytes - 2 * pb);
-  if (rc != FMHA_DECODE_SUCCESS) return rc;
-  hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
-                     dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, gp, d);
-  err = hipGetLastError();
-  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  for (int g0 = 0; g0 < g; g0 += gp) {
+    const int gn = g - g0 < gp ? g - g0 : gp;
+    const uint64_t out_blocks =
+        (streams * (uint64_t)gn * (uint64_t)(d / 8) + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
+    hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks),
+                       dim3(fmha_decode::kPadThreads), 0, st, static_cast<const uint16_t*>(Q), qp, streams, g, g0, gn,
+                       gp, d);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+    const int rc = body(qp, op, hkv * gp, ws + 2 * pb, workspace_bytes - 2 * pb);
+    if (rc != FMHA_DECODE_SUCCESS) return rc;
+    hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
+                       dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, g0, gn, gp,
+                       d);
+    err = hipGetLastError();
+    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  }
   return FMHA_DECODE_SUCCESS;
 }
-
 }  // namespace
 
 extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,

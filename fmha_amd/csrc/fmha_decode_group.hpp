@@ -451,16 +451,18 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
 
 // ---------------------------------------------------------------------------
 // Query-group padding for the long-row paths (split-KV, single pass, paged
-// short kernel), whose kernels exist for G in {1, 2, 4, 8}: another G up to
-// 8 runs as GP (4 for 3, 8 for 5-7) on copies of Q and O with GP rows per
-// stream, the rows g >= G of Q zero and those of O dropped.  Row sigma*G + g
-// of Q / O ([streams, G, D]) is row sigma*GP + g of the copy.  One thread per
+// short kernel), whose kernels exist for G in {1, 2, 4, 8}: another G runs
+// on copies of Q and O with GP (4 or 8) rows per stream.  The copy for query
+// heads [g0, g0 + gn) of every stream (gn <= GP; G > 8 takes several such
+// slices in turn) holds Q row sigma*G + g0 + g at row sigma*GP + g for g < gn
+// and zero rows above; the O rows go back the same way.  One thread per
 // 16-byte chunk; every index is checked against the element counts.
 // ---------------------------------------------------------------------------
 constexpr int kPadThreads = 256;
 
 __global__ __launch_bounds__(kPadThreads) void pad_query_group_kernel(const uint16_t* q, uint16_t* qp,
-                                                                       uint64_t streams, int G, int GP, int D) {
+                                                                       uint64_t streams, int G, int g0, int gn,
+                                                                       int GP, int D) {
   const uint64_t cpr = (uint64_t)(D / 8);  // 16-byte chunks per row
   const uint64_t i = (uint64_t)blockIdx.x * kPadThreads + threadIdx.x;
   if (i >= streams * (uint64_t)GP * cpr) return;
@@ -469,20 +471,21 @@ __global__ __launch_bounds__(kPadThreads) void pad_query_group_kernel(const uint
   const uint64_t sigma = row / (uint64_t)GP;
   const int g = (int)(row - sigma * (uint64_t)GP);
   u32x4 x = {0u, 0u, 0u, 0u};
-  if (g < G) x = *reinterpret_cast<const u32x4*>(q + ((sigma * (uint64_t)G + g) * D + c * 8));
+  if (g < gn) x = *reinterpret_cast<const u32x4*>(q + ((sigma * (uint64_t)G + g0 + g) * D + c * 8));
   *reinterpret_cast<u32x4*>(qp + (row * D + c * 8)) = x;
 }
 
 __global__ __launch_bounds__(kPadThreads) void unpad_output_group_kernel(const uint16_t* op, uint16_t* o,
-                                                                          uint64_t streams, int G, int GP, int D) {
+                                                                          uint64_t streams, int G, int g0, int gn,
+                                                                          int GP, int D) {
   const uint64_t cpr = (uint64_t)(D / 8);
   const uint64_t i = (uint64_t)blockIdx.x * kPadThreads + threadIdx.x;
-  if (i >= streams * (uint64_t)G * cpr) return;
-  const uint64_t row = i / cpr;  // row of O
+  if (i >= streams * (uint64_t)gn * cpr) return;
+  const uint64_t row = i / cpr;  // row of the slice: stream sigma, head g
   const uint64_t c = i - row * cpr;
-  const uint64_t sigma = row / (uint64_t)G;
-  const uint64_t g = row - sigma * (uint64_t)G;
-  *reinterpret_cast<u32x4*>(o + (row * D + c * 8)) =
+  const uint64_t sigma = row / (uint64_t)gn;
+  const uint64_t g = row - sigma * (uint64_t)gn;
+  *reinterpret_cast<u32x4*>(o + ((sigma * (uint64_t)G + g0 + g) * D + c * 8)) =
       *reinterpret_cast<const u32x4*>(op + ((sigma * (uint64_t)GP + g) * D + c * 8));
 }
 

@@ -70,7 +70,8 @@ extern "C" {
  *                   runs the matrix-core kernel for every G, =valu keeps the
  *                   VALU kernel wherever it exists.  This entry point,
  *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
- *                   any G; the split-KV entries G = 1-8 beyond 16 rows;
+ *                   any G, and so do the split-KV entries (through a
+ *                   padded query group beyond 16 rows);
  *                   fmha_decode_fwd_paged and fmha_decode_fwd_fp32_weights
  *                   G = 1, 2, 4 or 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
@@ -191,13 +192,13 @@ int fmha_decode_fwd_paged(void* stream,
  * bytes, 256-byte aligned; its contents on entry do not matter.  Calls that
  * share a workspace must be ordered (same stream or synchronised).
  *
- * Group sizes G = num_heads_q / num_heads_kv: with max_seqlen_kv <= 16 any G
- * (as fmha_decode_fwd); beyond 16 (and for the paged entry at any length)
- * G = 1-8: the long-row kernels exist for 1, 2, 4, 8, and G = 3, 5, 6, 7 run
- * as 4 or 8 on copies of Q and O padded to that many query heads per KV head,
- * which the workspace size includes (two copies of [batch, Hkv * 4 or 8,
- * head_dim] bf16/fp16, ahead of the split-KV data).  Larger G beyond 16 rows
- * returns FMHA_DECODE_ERROR_NOT_SUPPORTED.
+ * Group sizes G = num_heads_q / num_heads_kv: any.  With max_seqlen_kv <= 16
+ * as fmha_decode_fwd; beyond 16 (and for the paged entry at any length) the
+ * long-row kernels exist for G = 1, 2, 4, 8, and other G run on copies of Q
+ * and O padded to 4 (G = 3) or 8 query heads per KV head, which the
+ * workspace size includes (two copies of [batch, Hkv * 4 or 8, head_dim],
+ * ahead of the split-KV data); G > 8 runs in slices of 8 query heads one
+ * after the other, each reading K and V again.
  */
 size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                           int32_t max_seqlen_kv, int32_t head_dim);

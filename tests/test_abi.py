@@ -194,6 +194,8 @@ def test_splitkv_workspace_size(lib):
     # plus the two copies (4 * 8 * 4 * 128 * 2 bytes each)
     assert f(4, 24, 8, 100, 128) == f(4, 32, 8, 100, 128) + 2 * 4 * 8 * 4 * 128 * 2
     assert f(4, 56, 8, 100, 128) == f(4, 64, 8, 100, 128) + 2 * 4 * 8 * 8 * 128 * 2
+    # G = 12 runs as two slices of up to 8 heads through the same copies
+    assert f(4, 96, 8, 100, 128) == f(4, 64, 8, 100, 128) + 2 * 4 * 8 * 8 * 128 * 2
 
 
 @pytest.mark.parametrize("kw,code,needle", [
@@ -203,10 +205,10 @@ def test_splitkv_workspace_size(lib):
     (dict(ws=P * 64 + 16), BAD, "256-byte"),
     (dict(wsb=1024), BAD, "too small"),
     (dict(cu=None), BAD, "cu_seqlens_kv"),
-    # lengths beyond 16 take group sizes 1-8 (3, 5, 6, 7 through a padded
-    # query group in the workspace)
-    (dict(hq=96, hkv=8), NOTSUP, "of 1-8"),
+    # lengths beyond 16 take group sizes outside {1, 2, 4, 8} through a
+    # padded query group in the workspace
     (dict(hq=24, hkv=8, wsb=1024), BAD, "padded query group"),
+    (dict(hq=96, hkv=8, ws=None), BAD, "workspace"),
     (dict(sq=3), BAD, "seqlen_q"),
 ])
 def test_splitkv_rejects(lib, kw, code, needle):
@@ -240,7 +242,7 @@ def splitkv_paged(lib, **kw):
     (dict(lens=CU + 2), BAD, "seqlens_kv"),
     (dict(ws=None), BAD, "workspace"),
     (dict(wsb=1024), BAD, "too small"),
-    (dict(hq=96, hkv=8), NOTSUP, "of 1-8"),
+    (dict(hq=96, hkv=8, wsb=1024), BAD, "padded query group"),
     (dict(k=None), BAD, "non-null"),
     (dict(maxs=16, lens=None, rs=12), BAD, "multiples of 8"),   # <= 16 rows: fmha_decode_fwd_strided's checks
 ])
@@ -258,8 +260,8 @@ def test_splitkv_strided_rejects(lib, kw, code, needle):
     (dict(ws=None), BAD, "workspace"),
     (dict(wsb=1024), BAD, "too small"),
     (dict(sq=2), BAD, "seqlen_q"),
-    (dict(hq=192, hkv=16), NOTSUP, "of 1-8"),
     (dict(hq=48, hkv=16, wsb=1024), BAD, "padded query group"),
+    (dict(hq=192, hkv=16, wsb=1024), BAD, "padded query group"),
 ])
 def test_splitkv_paged_rejects(lib, kw, code, needle):
     assert splitkv_paged(lib, **kw) == code

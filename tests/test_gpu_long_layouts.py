@@ -264,3 +264,28 @@ def test_paged_padded_group(page_size, B, max_len):
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max(max_len, 16), f"paged G=7 ps={page_size} B={B} max={max_len}")
+
+
+def test_long_layouts_group_slices():
+    """G = 12 beyond 16 rows over BHSD and 16-row pages (two slices of the
+    query group), and G = 12 on the short paged kernel through the workspace
+    entry."""
+    import fmha_amd
+    import torch
+    D, Hq, Hkv, B = 128, 24, 2, 5
+    rng = np.random.default_rng(31)
+    for cap in (200, 12):
+        seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+        seqlens[0] = cap
+        q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=cap + 32)
+        kc = _strided_cache(kp, seqlens, cap, Hkv, D, "bhsd")
+        vc = _strided_cache(vp, seqlens, cap, Hkv, D, "bhsd")
+        o = fmha_amd.fmha_decode_strided(to_dev(q), _strided_view(kc, "bhsd"), _strided_view(vc, "bhsd"),
+                                         seqlens_kv=torch.from_numpy(seqlens).cuda())
+        torch.cuda.synchronize()
+        _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"bhsd G=12 cap={cap}")
+        kc2, vc2, bt = _paged_cache(kp, vp, seqlens, 16, Hkv, D, rng)
+        o2 = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc2), to_dev(vc2), torch.from_numpy(bt).cuda(),
+                                        torch.from_numpy(seqlens).cuda(), max_seqlen_kv=cap)
+        torch.cuda.synchronize()
+        _check(o2, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"paged G=12 cap={cap}")

@@ -259,3 +259,14 @@ def test_any_group_short_rows_through_split_entry(Hq, Hkv):
     o = _run(q, k, v, cu, Hq, Hkv, 128, 10).reshape(3, Hq, 128)
     assert np.all(np.isnan(oracle.f16_to_f32(o[1])))      # 12 > max_seqlen_kv
     assert np.all(np.isfinite(oracle.f16_to_f32(o[[0, 2]])))
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 24, 2), (128, 32, 1), (64, 48, 4), (256, 20, 2)])
+@pytest.mark.parametrize("B,max_len", [(4, 500), (700, 40)])
+def test_group_slices_beyond_eight(D, Hq, Hkv, B, max_len):
+    """G = 12, 32, 10 beyond 16 rows: slices of up to 8 query heads run one
+    after the other on the padded copies (K and V read once per slice)."""
+    rng = np.random.default_rng(B + max_len + Hq + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 1)
