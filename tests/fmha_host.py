@@ -24,6 +24,9 @@ Suites:
   reference  the reference's own table (fmha_host.cpp:511-517): index 0 is
              B=10, H=16, D=128; 1..4 are B=30720 with H in {16, 32} and
              D in {128, 256}; all with Poisson lengths in [2, 16]
+  gqa        full-size group sizes outside {1, 2, 4, 8} (the matrix-core
+             kernel; the reference has no GQA): G = 3, 5, 7, 12, MQA G = 32,
+             G = 5 with Poisson lengths, D = 256 with std 2, D = 64
 """
 import argparse
 import json
@@ -52,7 +55,19 @@ SUITES = {
         3: (30720, 32, 32, None, 128, 1.0),
         4: (30720, 32, 32, None, 256, 1.0),
     },
+    "gqa": {
+        1: (30720, 48, 16, 16, 128, 1.0),
+        2: (30720, 80, 16, 16, 128, 1.0),
+        3: (30720, 112, 16, 16, 128, 1.0),
+        4: (30720, 192, 16, 16, 128, 1.0),
+        5: (30720, 32, 1, 16, 128, 1.0),
+        6: (30720, 40, 8, None, 128, 1.0),
+        7: (15360, 48, 8, 16, 256, 2.0),
+        8: (30720, 40, 8, 16, 64, 1.0),
+    },
 }
+
+SEED_OFFSET = {"baseline": 0, "reference": 8, "gqa": 12}
 
 
 def algorithmic_bytes(B, Hq, Hkv, rows, D):
@@ -75,7 +90,7 @@ def run_config(suite, idx, args):
         seqlens = np.full(B, S, np.int32)
     cu_h = np.concatenate([[0], np.cumsum(seqlens)]).astype(np.int32)
     rows = int(cu_h[-1])
-    seed = 0xF3A00000 + 16 * idx + (0 if suite == "baseline" else 8)
+    seed = 0xF3A00000 + 16 * idx + SEED_OFFSET[suite]
     gen = torch.Generator(device=dev).manual_seed(seed)
     # --rotate N: N independent input/output sets used in turn, so that a
     # small configuration cannot be served from the 256 MB MALL between calls.

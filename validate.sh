@@ -8,4 +8,5 @@ ROOT=$(cd "$(dirname "$0")" && pwd)
 # rotated input sets (2 GB) so that no call is served from the cache.
 python3 "$ROOT/tests/fmha_host.py" 1 --suite baseline --validate full --iters 20 --rotate 4 && \
 python3 "$ROOT/tests/fmha_host.py" all --suite baseline --validate full --iters 20 && \
-python3 "$ROOT/tests/fmha_host.py" all --suite reference --validate full --iters 20
+python3 "$ROOT/tests/fmha_host.py" all --suite reference --validate full --iters 20 && \
+python3 "$ROOT/tests/fmha_host.py" all --suite gqa --validate full --iters 20
