@@ -178,6 +178,19 @@ hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t st
 #undef FMHA_DECODE_MULTI_G
 }
 
+// G values the VALU kernel is instantiated for.
+bool valu_group(int g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+
+// The VALU instantiation a call with G query heads per KV head runs: G for
+// 1, 2, 4, 8; 4 for 3 and 8 for 5-7 (the extra query heads load and store
+// nothing, DecodeArgs::group); 0 above 8.
+int valu_kernel_group(int g) {
+  if (valu_group(g)) return g;
+  if (g == 3) return 4;
+  if (g >= 5 && g <= 7) return 8;
+  return 0;
+}
+
 // Waves per CU for a unit that moves `rows` K/V rows and G query heads:
 // each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
 // of Q in and 1 KiB of O out.  Caps of 16 or more are dropped (no cap).
@@ -200,12 +213,10 @@ int bucket_for(int s) {
   return b;
 }
 
-// any_group: the entry point takes any G = Hq / Hkv (the packed-layout
-// entries, which can run the matrix-core kernel); the others take G in
-// {1, 2, 4, 8}.
+// Checks every entry point shares.  Any group size G = Hq / Hkv passes here;
+// the kernel choice rejects what a path cannot run.
 int check_common(const void* Q, const void* K, const void* V, void* O, int32_t batch, int32_t hq,
-                 int32_t hkv, int32_t seqlen_q, int32_t dq, int32_t dkv, float scale, bool kv_may_be_null,
-                 bool any_group = false) {
+                 int32_t hkv, int32_t seqlen_q, int32_t dq, int32_t dkv, float scale, bool kv_may_be_null) {
   if (batch < 0) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch must be >= 0 (got %d)", batch);
   if (hq <= 0 || hkv <= 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head counts must be > 0 (num_heads_q=%d, num_heads_kv=%d)", hq,
@@ -213,9 +224,6 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
   if (hq % hkv != 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "num_heads_q (%d) must be a multiple of num_heads_kv (%d)", hq,
                   hkv);
-  const int g = hq / hkv;
-  if (!any_group && g != 1 && g != 2 && g != 4 && g != 8)
-    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be 1, 2, 4 or 8 (got %d)", g);
   if (seqlen_q != 1) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_q must be 1 (got %d)", seqlen_q);
   if (dq != dkv)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "head_dim_q (%d) must equal head_dim_kv (%d)", dq, dkv);
@@ -249,7 +257,11 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
   a.units_per_batch = (int32_t)upb;
   a.total_units = (uint32_t)units;
-  const int g = a.num_heads_q / a.num_heads_kv;
+  a.group = a.num_heads_q / a.num_heads_kv;
+  const int g = valu_kernel_group(a.group);
+  if (g == 0)
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be at most 8 here (got %d)",
+                  a.group);
   const int w = waves_per_cu_for(rows_hint, g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
@@ -296,18 +308,27 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // Matrix-core kernel (fmha_decode_group_kernel): packed layout, any G.
 // ---------------------------------------------------------------------------
 
-// G values the VALU kernel is instantiated for.
-bool valu_group(int g) { return g == 1 || g == 2 || g == 4 || g == 8; }
-
-// Kernel choice for a packed-layout call: the matrix-core kernel for every G
-// the VALU kernel does not cover.  FMHA_DECODE_GQA_KERNEL=mfma runs it for
-// every G, =valu keeps the VALU kernel wherever it exists (for comparisons).
-bool use_mfma_kernel(int g) {
+// Kernel choice for the packed and strided layouts, G query heads per KV
+// head, head dim dq, rows_hint rows per batch (the uniform length, or 4 when
+// lengths live on the device): the VALU kernel for G <= 8 (3 and 5-7 on its
+// 4- and 8-head instantiations), the matrix-core kernel above, and for the
+// shapes where it measured as fast or faster than the padded VALU kernel
+// (B=30720, µs VALU / MFMA, two boxes): D=64 with rows >= 8 (Hkv=8, S=16:
+// G=5 213/202 and 215/201; G=3 and 7 within 2% on one box, 4-10% faster on
+// the other) and D=128 G=3 with rows >= 8 (Hkv=16, S=8 482/460 and 481/462;
+// S=16 a tie on one box, 5% faster on the other).  Elsewhere the VALU kernel
+// wins: D=128 G=5-7 (S=16 863/885, 876/914, 933/988), short rows (G=3 S=4
+// 264/324, G=7 S=2 370/421), D=256 (G=3 365/490, G=6 443/691).
+// FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
+// keeps the VALU kernel wherever it exists (for comparisons).
+bool use_mfma_kernel(int g, int dq, int rows_hint) {
   if (const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL")) {
     if (std::strcmp(e, "mfma") == 0) return true;
-    if (std::strcmp(e, "valu") == 0) return !valu_group(g);
+    if (std::strcmp(e, "valu") == 0) return valu_kernel_group(g) == 0;
   }
-  return !valu_group(g);
+  if (valu_kernel_group(g) == 0) return true;
+  if (valu_group(g) || rows_hint < 8 || dq == 256) return false;
+  return dq == 64 || g == 3;
 }
 
 template <int D, int NS, int LAYOUT>
@@ -423,6 +444,7 @@ DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32
   a.o = static_cast<uint16_t*>(O);
   a.num_heads_q = hq;
   a.num_heads_kv = hkv;
+  a.group = hq / hkv;
   a.scale = scale;
   a.max_rows = FMHA_DECODE_MAX_SEQLEN_KV;
   return a;
@@ -650,7 +672,7 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
                                float softmax_scale) {
   g_detail[0] = '\0';
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false, true);
+                        softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
@@ -659,7 +681,8 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
+  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, kVarlenRowsHint))
+    return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
 }
 
@@ -690,13 +713,14 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_kv must lie in [0, %d] (got %d)",
                   FMHA_DECODE_MAX_SEQLEN_KV, seqlen_kv);
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, seqlen_kv == 0, true);
+                        softmax_scale, seqlen_kv == 0);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
   a.seqlen_uniform = seqlen_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv)) return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
+  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, seqlen_kv))
+    return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), seqlen_kv);
 }
 
@@ -712,7 +736,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
                   seqlen_kv);
   const int cap = seqlen_kv < FMHA_DECODE_MAX_SEQLEN_KV ? seqlen_kv : FMHA_DECODE_MAX_SEQLEN_KV;
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, cap == 0, true);
+                        softmax_scale, cap == 0);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
@@ -735,7 +759,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
   a.head_stride = (int32_t)kv_head_stride;
   const int sb = seqlens_kv ? 0 : bucket_for(seqlen_kv);
   const int rows_hint = seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv))
+  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
     return launch_mfma(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, rows_hint);
   return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb, rows_hint);
 }
@@ -751,9 +775,9 @@ int log2_pow2(int x) {
 int paged_checks(const void* Q, const void* K_cache, const void* V_cache, void* O, const int32_t* block_table,
                  int32_t block_table_stride, const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
                  int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
-                 int32_t head_dim_kv, float softmax_scale, bool any_group = false) {
+                 int32_t head_dim_kv, float softmax_scale) {
   int rc = check_common(Q, K_cache, V_cache, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false, any_group);
+                        softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (page_size < 1 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "page_size must be a power of two in [1, 2^20] (got %d)",
@@ -960,40 +984,40 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
                                        void* workspace, size_t workspace_bytes) {
   g_detail[0] = '\0';
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false, true);
+                        softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
   if ((rc = split_check_workspace_args(max_seqlen_kv)) != FMHA_DECODE_SUCCESS) return rc;
   const int rows_hint = max_seqlen_kv < kVarlenRowsHint ? max_seqlen_kv : kVarlenRowsHint;
-  DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
-  d.lens = cu_seqlens_kv;
-  d.row_stride = num_heads_kv * head_dim_q;
-  d.head_stride = head_dim_q;
-  d.max_rows = max_seqlen_kv;
-  // Rows that fit the short kernels take them (same numerics, lengths above
-  // max_seqlen_kv give NaN there too); the matrix-core kernel needs no
-  // workspace.
-  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV && use_mfma_kernel(num_heads_q / num_heads_kv))
-    return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
   // One batch's K/V rows (up to nblk * 16) are addressed through one range.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
   const int64_t padded_rows = ((int64_t)max_seqlen_kv + 15) / 16 * 16;
+  const int64_t span = (padded_rows > 16 ? padded_rows : 16) * row_bytes;
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
+    // Rows that fit the short kernels take them (same numerics, lengths above
+    // max_seqlen_kv give NaN there too); the workspace is checked but unused.
+    DecodeArgs d = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+    d.lens = cu_seqlens_kv;
+    d.row_stride = num_heads_kv * head_dim_q;
+    d.head_stride = head_dim_q;
+    d.max_rows = max_seqlen_kv;
+    if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
+      return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
+    SplitArgs unused;
+    rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale,
+                       workspace, workspace_bytes, span, unused);
+    if (rc != FMHA_DECODE_SUCCESS) return rc;
+    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0, rows_hint);
+  }
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
       [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
         SplitArgs a;
         int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale, ws,
-                                ws_bytes, (padded_rows > 16 ? padded_rows : 16) * row_bytes, a);
+                                ws_bytes, span, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
-        if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV) {
-          DecodeArgs dd = d;
-          dd.q = static_cast<const uint16_t*>(q);
-          dd.o = static_cast<uint16_t*>(o);
-          dd.num_heads_q = hq;
-          return launch(stream, fmha_decode::kLayoutPacked, dd, batch, head_dim_q, 0, rows_hint);
-        }
         a.cu = cu_seqlens_kv;
         a.len_mode = fmha_decode::kLenCu;
         return split_launch(stream, fmha_decode::kLayoutPacked, a, head_dim_q);
@@ -1015,7 +1039,7 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
                                    kv_head_stride, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
                                    head_dim_kv, softmax_scale);
   rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale,
-                    false, true);
+                    false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   if (kv_batch_stride < 0 || kv_row_stride < 0 || kv_head_stride < 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "K/V strides must be >= 0");
@@ -1054,9 +1078,14 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
   int rc = split_check_workspace_args(max_seqlen_kv);
   if (rc != FMHA_DECODE_SUCCESS) return rc;
   rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
-                    num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale, true);
+                    num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   max_seqlen_kv = paged_capacity(block_table_stride, page_size, max_seqlen_kv);
+  // Short rows with G <= 8 take the VALU paged kernel directly; larger G
+  // run it on slices of the query group.
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV && valu_kernel_group(num_heads_q / num_heads_kv) != 0)
+    return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
+                       max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
   // A sub-block's range covers at most 16 rows of one page.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
   return with_group_padding(

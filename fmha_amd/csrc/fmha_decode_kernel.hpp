@@ -97,7 +97,21 @@ struct DecodeArgs {
   // num_heads_kv (a power of two below the heads a wave holds).
   int32_t sub_shift;
   int32_t hkv_shift;
+  // Query heads per KV head, num_heads_q / num_heads_kv.  The kernels are
+  // instantiated for G = 1, 2, 4, 8; a call with 3 runs the G = 4 kernel and
+  // 5-7 the G = 8 one, the query heads at or past `group` of each KV head
+  // loading and storing nothing (out-of-range offsets).
+  int32_t group;
 };
+
+// Byte offset of query head g of the lane's KV head from qo_off (the head's
+// first query row), out of range for padding heads g >= group.  G = 1 and 2
+// kernels are never padded.
+template <int G>
+__device__ __forceinline__ uint32_t group_row_off(uint32_t qo_off, int g, int group, int D) {
+  if constexpr (G >= 4) return g < group ? qo_off + (uint32_t)(g * D * 2) : kLaneOutOfRange;
+  return qo_off + (uint32_t)(g * D * 2);
+}
 
 // One batch's K/V as the kernel reads it: byte strides relative to k/v, the
 // descriptor range, the length.
@@ -447,7 +461,8 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(kv.v, kv.records);
 
   const uint32_t kv_off = head_ok ? (uint32_t)hk * kv.head_bytes + (uint32_t)r * 16u : kLaneOutOfRange;
-  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+  const int grp = G >= 4 ? a.group : G;
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * grp * D + r * 8) * 2u : kLaneOutOfRange;
   // Row j's byte offset.  Packed rows past S already fall outside the
   // descriptor's range; a strided batch's range can include padding rows of
   // other heads, so there rows at or past S are moved out of range.
@@ -463,7 +478,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   // ---- issue every load of this unit ----
   u32x4 qv[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, qo_off + g * D * 2);
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, group_row_off<G>(qo_off, g, grp, D));
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
   if constexpr (LAYOUT != kLayoutPaged) {
@@ -501,7 +516,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
-  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, pack_f16x8(acc[g]));
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, group_row_off<G>(qo_off, g, grp, D), pack_f16x8(acc[g]));
 }
 
 // Batches whose length is outside [0, max_rows] get NaN outputs so that a
@@ -512,10 +527,11 @@ __device__ __forceinline__ void decode_bad_length(const DecodeArgs& a, uint32_t 
   const int r = lane % LPH;
   const uint32_t q_bytes = (uint32_t)a.num_heads_q * D * 2;
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * a.num_heads_q * D, q_bytes);
-  const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+  const int grp = G >= 4 ? a.group : G;
+  const uint32_t qo_off = head_ok ? (uint32_t)(hk * grp * D + r * 8) * 2u : kLaneOutOfRange;
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
-  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, nan4);
+  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, group_row_off<G>(qo_off, g, grp, D), nan4);
 }
 
 // This batch's K/V span for the layout.  Returns false when the batch's
@@ -642,8 +658,9 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
   const uint32_t row_bytes = (uint32_t)a.row_stride * 2u;
+  const int grp = G >= 4 ? a.group : G;
   const uint32_t qo_off =
-      lane_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
+      lane_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * grp * D + r * 8) * 2u : kLaneOutOfRange;
   const uint32_t kv_off =
       lane_ok ? lane_rows + (uint32_t)hk * (uint32_t)a.head_stride * 2u + (uint32_t)r * 16u : kLaneOutOfRange;
   // Rows at or past this lane group's own length are moved out of range.
@@ -653,7 +670,7 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
 
   u32x4 qv[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, qo_off + g * D * 2);
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, group_row_off<G>(qo_off, g, grp, D));
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
 #pragma unroll
@@ -666,7 +683,8 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
   decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
-  for (int g = 0; g < G; ++g) buffer_store16(o_rsrc, qo_off + g * D * 2, bad ? nan4 : pack_f16x8(acc[g]));
+  for (int g = 0; g < G; ++g)
+    buffer_store16(o_rsrc, group_row_off<G>(qo_off, g, grp, D), bad ? nan4 : pack_f16x8(acc[g]));
 }
 
 // a.units_per_batch holds the batch count here, a.total_units the waves

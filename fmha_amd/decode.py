@@ -244,7 +244,7 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     through fmha_decode_fwd_splitkv_paged with workspace (a uint8 device
     tensor of splitkv_workspace_size(B, Hq, Hkv, max_seqlen_kv, D) bytes,
     allocated here when None; for max_seqlen_kv <= 16 it only holds the
-    padded query group of a group size outside {1, 2, 4, 8})."""
+    padded query group of a group size above 8)."""
     import torch
     B, Hq, D = _q_shape(q)
     out = _check_q_out(q, out)

@@ -63,17 +63,22 @@ extern "C" {
  *   batch           >= 0 (0 launches nothing)
  *   num_heads_q     > 0, a multiple of num_heads_kv
  *   num_heads_kv    > 0; any group size G = num_heads_q / num_heads_kv.
- *                   G = 1, 2, 4, 8 run the VALU kernel, every other G the
- *                   matrix-core kernel (which needs num_heads_kv * head_dim
- *                   below 2^24, else FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   G <= 8 runs the VALU kernel (G = 3 on its 4-head and
+ *                   5-7 on its 8-head instantiation, the extra heads
+ *                   reading and writing nothing), except for head_dim 64 and
+ *                   for G = 3 at head_dim 128 with a uniform length of 8 or
+ *                   more, which run the matrix-core kernel, as does every
+ *                   G > 8 (it needs num_heads_kv * head_dim below 2^24,
+ *                   else FMHA_DECODE_ERROR_NOT_SUPPORTED).  The same
+ *                   numerics within the comparison gate, not the same bits.
  *                   The environment variable FMHA_DECODE_GQA_KERNEL=mfma
- *                   runs the matrix-core kernel for every G, =valu keeps the
- *                   VALU kernel wherever it exists.  This entry point,
+ *                   runs the matrix-core kernel for every G, =valu the VALU
+ *                   kernel wherever it exists (G <= 8).  This entry point,
  *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
  *                   any G, and so do the split-KV entries (through a
  *                   padded query group beyond 16 rows);
  *                   fmha_decode_fwd_paged and fmha_decode_fwd_fp32_weights
- *                   G = 1, 2, 4 or 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   G <= 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q
@@ -100,7 +105,8 @@ int fmha_decode_fwd(void* stream,
  * parameter list, :243-296 for the weights and the accumulation), which has
  * no launch helper in the reference; the wired-in fmha_mfma_4x4x4 and the
  * reference CPU check round the weights to bf16 (fmha_decode_fwd).  Same
- * arguments, layouts, checks and errors as fmha_decode_fwd.
+ * arguments, layouts, checks and errors as fmha_decode_fwd, with group sizes
+ * up to 8 only (the VALU kernel).
  */
 int fmha_decode_fwd_fp32_weights(void* stream,
                                  const void* Q, const void* K, const void* V, void* O,
@@ -139,8 +145,8 @@ int fmha_decode_fwd_uniform(void* stream,
  *                the rows each batch has room for: a length above
  *                min(seqlen_kv, 16) gets NaN outputs, rows past a batch's
  *                length are never read (padding may hold anything)
- * One batch's span (rows and heads) must stay below 1 GiB; with G outside
- * {1, 2, 4, 8} (the matrix-core kernel) so must the span of the
+ * One batch's span (rows and heads) must stay below 1 GiB; on the
+ * matrix-core kernel (see fmha_decode_fwd) so must the span of the
  * 64/(head_dim/8)/num_heads_kv + 2 batches a wave may touch, else
  * FMHA_DECODE_ERROR_NOT_SUPPORTED.  Other arguments as fmha_decode_fwd.
  */
@@ -163,8 +169,10 @@ int fmha_decode_fwd_strided(void* stream,
  *                       block_table_stride * page_size)]; a length outside
  *                       that range gets NaN outputs
  *   page_size           a power of two in [1, 2^20]
- * Other arguments as fmha_decode_fwd.  The reference has no paged layout;
- * this entry point is the KV-cache format of serving engines.
+ * Other arguments as fmha_decode_fwd, with group sizes up to 8 only (the
+ * VALU kernel; fmha_decode_fwd_splitkv_paged takes any).  The reference has
+ * no paged layout; this entry point is the KV-cache format of serving
+ * engines.
  */
 int fmha_decode_fwd_paged(void* stream,
                           const void* Q, const void* K_cache, const void* V_cache, void* O,

@@ -3,15 +3,16 @@
 profile under profiles/.
 
 For each shape (uniform lengths, bf16 N(0,1) inputs generated on the GPU)
-and each kernel choice (FMHA_DECODE_GQA_KERNEL=valu: the VALU kernel, which
-exists for G = 1, 2, 4, 8; =mfma: the matrix-core kernel), calls
+and each kernel choice (FMHA_DECODE_GQA_KERNEL=valu: the VALU kernel, for
+G <= 8, G = 3 and 5-7 on its 4- and 8-head instantiations; =mfma: the
+matrix-core kernel; default: the library's own choice), calls
 fmha_decode_fwd_uniform --warmup times, then times --iters calls with a HIP
 event pair per call on the launch stream, and prints one JSON line: median
 µs per call and algorithmic TB/s (Q + K + V + O as the reference counts
 them, fmha_host.cpp:428-430, with Hkv heads for K/V).  Run it under
 `rocprofv3 --kernel-trace --stats` (or `--pmc ...`) for the per-kernel view.
 
-    python3 tests/profiling/gqa_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...] [--modes valu,mfma]
+    python3 tests/profiling/gqa_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...] [--modes valu,mfma,default]
 """
 import argparse
 import json
@@ -22,10 +23,12 @@ import sys
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
 
-# Hkv = 16, S = 16, D = 128 (the headline batch) with G = 1..16, MQA, and the
-# other head dims.
+# Hkv = 16, S = 16, D = 128 (the headline batch) with G = 1..16, MQA, short
+# rows, and the other head dims.
 SHAPES = [(30720, 16 * g, 16, 16, 128) for g in (1, 2, 3, 4, 5, 6, 7, 8, 12, 16)] + [
-    (30720, 32, 1, 16, 128), (30720, 64, 8, 4, 128), (30720, 40, 8, 16, 64), (15360, 48, 8, 16, 256)]
+    (30720, 32, 1, 16, 128), (30720, 64, 8, 4, 128), (30720, 48, 16, 8, 128), (30720, 48, 16, 4, 128),
+    (30720, 112, 16, 8, 128), (30720, 112, 16, 2, 128), (30720, 24, 8, 16, 64), (30720, 40, 8, 16, 64),
+    (30720, 56, 8, 16, 64), (15360, 24, 8, 16, 256), (15360, 48, 8, 16, 256)]
 
 
 def main():
@@ -33,7 +36,7 @@ def main():
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--shapes", default="")
-    ap.add_argument("--modes", default="valu,mfma")
+    ap.add_argument("--modes", default="valu,mfma,default")
     a = ap.parse_args()
     import torch
     import fmha_amd
@@ -52,9 +55,12 @@ def main():
         G = hq // hkv
         row = {"B": B, "Hq": hq, "Hkv": hkv, "G": G, "S": S, "D": D}
         for mode in modes:
-            if mode == "valu" and G not in (1, 2, 4, 8):
+            if mode == "valu" and G > 8:
                 continue
-            os.environ["FMHA_DECODE_GQA_KERNEL"] = mode
+            if mode == "default":
+                os.environ.pop("FMHA_DECODE_GQA_KERNEL", None)
+            else:
+                os.environ["FMHA_DECODE_GQA_KERNEL"] = mode
             call = lambda: fmha_amd.fmha_decode(q, k, v, seqlen_kv=S, out=o)
             for _ in range(a.warmup):
                 call()

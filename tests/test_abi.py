@@ -80,9 +80,9 @@ def uni(lib, **kw):
     (dict(hq=0), BAD, "head counts"),
     (dict(hkv=0), BAD, "head counts"),
     (dict(hq=16, hkv=5), BAD, "multiple"),
-    # Any group size runs (the matrix-core kernel takes those outside
-    # {1, 2, 4, 8}), but not when a wave's K/V span reaches 2^30 bytes.
-    (dict(hq=3 << 17, hkv=1 << 17), NOTSUP, "too large"),
+    # Any group size runs (the matrix-core kernel takes those above 8), but
+    # not when a wave's K/V span reaches 2^30 bytes.
+    (dict(hq=12 << 17, hkv=1 << 17), NOTSUP, "too large"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(sq=0), BAD, "seqlen_q"),
     (dict(dq=128, dkv=256), BAD, "head_dim_q"),
@@ -107,7 +107,7 @@ def test_varlen_rejects(lib, kw, code, needle):
     (dict(s=-1), BAD, "seqlen_kv"),
     (dict(s=17), BAD, "seqlen_kv"),
     (dict(s=1000), BAD, "seqlen_kv"),
-    (dict(hq=5 << 17, hkv=1 << 17), NOTSUP, "too large"),
+    (dict(hq=16 << 17, hkv=1 << 17), NOTSUP, "too large"),
     (dict(v=None), BAD, "non-null"),
 ])
 def test_uniform_rejects(lib, kw, code, needle):
@@ -115,11 +115,12 @@ def test_uniform_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
-@pytest.mark.parametrize("hq,hkv", [(48, 16), (32, 2), (24, 8), (7, 1)])
+@pytest.mark.parametrize("hq,hkv", [(32, 2), (96, 8), (18, 1)])
 def test_fp32_weights_group_sizes(lib, hq, hkv):
-    """The fp32-weight entry keeps the VALU kernel's group sizes 1, 2, 4, 8."""
+    """The fp32-weight entry runs the VALU kernel only: group sizes up to 8
+    (3, 5, 6, 7 on the 4- and 8-head instantiations), nothing above."""
     assert fwd32(lib, hq=hq, hkv=hkv) == NOTSUP
-    assert "1, 2, 4 or 8" in lib.fmha_decode_last_error_detail().decode()
+    assert "at most 8" in lib.fmha_decode_last_error_detail().decode()
 
 
 def strided(lib, **kw):
@@ -148,9 +149,9 @@ def paged(lib, **kw):
     (dict(hs=4), BAD, "multiples of 8"),
     (dict(rs=1 << 26), BAD, "1 GiB"),
     (dict(lens=CU + 2), BAD, "seqlens_kv"),
-    # Any group size runs; outside {1, 2, 4, 8} the matrix-core kernel's
-    # descriptor spans the batches a wave touches (here 2 of 1 GiB each).
-    (dict(hq=24, hkv=8, bs=1 << 29), NOTSUP, "exceeds 1 GiB"),
+    # Any group size runs; above 8 the matrix-core kernel's descriptor spans
+    # the batches a wave touches (here 2 of 1 GiB each).
+    (dict(hq=96, hkv=8, bs=1 << 29), NOTSUP, "exceeds 1 GiB"),
     (dict(k=None), BAD, "non-null"),
     (dict(dq=128, dkv=64), BAD, "head_dim_q"),
 ])
@@ -169,6 +170,8 @@ def test_strided_rejects(lib, kw, code, needle):
     (dict(bts=0), BAD, "block_table_stride"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(v=None), BAD, "non-null"),
+    # no workspace: the VALU kernel only, group sizes up to 8
+    (dict(hq=192, hkv=16), NOTSUP, "at most 8"),
 ])
 def test_paged_rejects(lib, kw, code, needle):
     assert paged(lib, **kw) == code
@@ -280,7 +283,7 @@ def test_splitkv_paged_bound_is_the_block_table_row(lib):
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(batch=-1), BAD, "batch"),
-    (dict(hq=48, hkv=16), NOTSUP, "1, 2, 4 or 8"),
+    (dict(hq=96, hkv=8), NOTSUP, "at most 8"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(dq=96, dkv=96), BAD, "64, 128 or 256"),
     (dict(scale=float("nan")), BAD, "finite"),

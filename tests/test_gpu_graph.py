@@ -131,10 +131,17 @@ def test_graph_long_rows_replay_match_eager():
         torch.cuda.synchronize()
 
 
-def test_graph_matrix_core_kernel_replays_match_eager():
-    """The matrix-core kernel (group sizes outside {1, 2, 4, 8}) in a graph:
-    varlen, uniform and strided calls, an MQA shape with two waves per stream
-    group, every replay bit-equal to the eager result."""
+@pytest.mark.parametrize("kernel", ["mfma", "default"])
+def test_graph_matrix_core_kernel_replays_match_eager(monkeypatch, kernel):
+    """Group sizes outside {1, 2, 4, 8} in a graph: varlen, uniform and
+    strided calls with G = 5, an MQA shape with two waves per stream group,
+    every replay bit-equal to the eager result; once with the matrix-core
+    kernel forced for all of them, once with the library's choice (the VALU
+    kernel's 8-head instantiation for G = 5)."""
+    if kernel == "mfma":
+        monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "mfma")
+    else:
+        monkeypatch.delenv("FMHA_DECODE_GQA_KERNEL", raising=False)
     import torch
     import fmha_amd
     seqlens = oracle.generate_seqlens(48, 16)

@@ -1,8 +1,11 @@
 """GPU parity of the matrix-core kernel (fmha_decode_group_kernel) against the
 CPU oracle, through the packed-layout and strided entry points.
 
-The kernel serves every group size G = Hq / Hkv outside {1, 2, 4, 8} (which
-the VALU kernel cannot), and any G when FMHA_DECODE_GQA_KERNEL=mfma.  The
+The library runs the kernel for every group size G = Hq / Hkv above 8 and
+for the G <= 8 shapes where it measures faster than the VALU kernel; here
+every test but the last ones forces it (FMHA_DECODE_GQA_KERNEL=mfma) so that
+it meets every G, and the last ones cover the VALU kernel on G = 3, 5, 6, 7
+and the library's own choice.  The
 reference has no GQA (its kernels index K/V with the query head,
 fmha_mfma_4x4x4_kernel.hpp:195-196); the oracle's mapping is KV head h / G
 (fmha_host.cpp:169-245 otherwise).  Coverage: non-power-of-two and large G,
@@ -22,8 +25,10 @@ from tests.common import (assert_pass, check, cu_from_seqlens, default_scale, ma
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
+@pytest.fixture(autouse=True)
 def mfma(monkeypatch):
+    """Every test here runs the matrix-core kernel unless it asks otherwise
+    (the valu and default_policy fixtures, requested after this one)."""
     monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "mfma")
 
 
@@ -232,3 +237,80 @@ def test_strided_uniform_and_bad_length(S):
     assert np.all(np.isnan(o2b[4]))
     keep = [b for b in range(B) if b != 4]
     assert np.array_equal(_bits(o2).reshape(B, Hq, D)[keep], _bits(o).reshape(B, Hq, D)[keep])
+
+
+@pytest.fixture
+def valu(monkeypatch):
+    monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "valu")
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [3, 5, 6, 7])
+def test_valu_padded_group_sizes(valu, D, G):
+    """G = 3, 5, 6, 7 on the VALU kernel's 4- and 8-head instantiations (the
+    extra query heads of each KV head load and store nothing): every length
+    0..16, a wave spanning several batches (Hkv = 1), and neighbouring rows
+    of Q and O left untouched."""
+    for Hkv in (4, 1):
+        seqlens = _all_lengths(D * 7 + G + Hkv)
+        o, _ = _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=2000 + D + G + Hkv)
+
+
+def test_valu_padded_fp32_weights_and_paged():
+    """The fp32-weight and workspace-less paged entries (VALU kernel only)
+    with G = 5 and 3: oracle parity (fp32 weights against the oracle's
+    fp32-weight mode)."""
+    import torch
+    import fmha_amd
+    seqlens = oracle.generate_seqlens(40, 16)
+    q, k, v, cu = make_inputs(40, 20, 4, 128, seqlens, seed=2100)
+    qd = torch.from_numpy(q.view(np.int16)).cuda().view(torch.bfloat16)
+    kd = torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16)
+    vd = torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16)
+    cud = torch.from_numpy(cu).cuda()
+    o32 = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, fp32_weights=True)
+    torch.cuda.synchronize()
+    r32, _ = oracle.decode(q, k, v, cu, 20, 4, 128, default_scale(128), p_mode=1)
+    assert_pass(oracle.compare(o32.view(torch.int16).cpu().numpy().view(np.uint16).reshape(r32.shape), r32),
+                "fp32 weights G=5")
+    # paged, 4-row pages, G = 3
+    Hq, Hkv, D, ps = 12, 4, 128, 4
+    q2, k2, v2, cu2 = make_inputs(40, Hq, Hkv, D, seqlens, seed=2101)
+    need = [(int(s) + ps - 1) // ps for s in seqlens]
+    bt = np.zeros((40, max(need)), np.int32)
+    kc = np.zeros((sum(need), ps, Hkv, D), np.uint16)
+    vc = np.zeros_like(kc)
+    page = 0
+    for b in range(40):
+        for p in range(need[b]):
+            r0, r1 = cu2[b] + p * ps, min(cu2[b] + (p + 1) * ps, cu2[b + 1])
+            kc[page, :r1 - r0] = k2[r0:r1]
+            vc[page, :r1 - r0] = v2[r0:r1]
+            bt[b, p] = page
+            page += 1
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    o2 = fmha_amd.fmha_decode_paged(to(q2), to(kc), to(vc), torch.from_numpy(bt).cuda(),
+                                    torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    r2, slack = oracle.decode(q2, k2, v2, cu2, Hq, Hkv, D, default_scale(D), with_slack=True)
+    assert_pass(oracle.compare(o2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(r2.shape), r2, slack),
+                "paged G=3")
+
+
+@pytest.fixture
+def default_policy(monkeypatch):
+    monkeypatch.delenv("FMHA_DECODE_GQA_KERNEL", raising=False)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [3, 5, 7, 12])
+def test_default_kernel_choice(default_policy, D, G):
+    """The library's own kernel choice (no override): varlen lengths 0..16
+    and uniform lengths 4 and 16, which take different kernels for some
+    (G, D)."""
+    Hkv = 4
+    seqlens = _all_lengths(D * 13 + G)
+    _case(len(seqlens), Hkv * G, Hkv, D, seqlens, seed=2200 + D + G)
+    for S in (4, 16):
+        seqlens = np.full(24, S, np.int32)
+        _case(24, Hkv * G, Hkv, D, seqlens, seed=2300 + D + G + S, uniform=True)

@@ -250,8 +250,9 @@ def test_padded_query_group(D, Hq, Hkv, B, max_len):
 
 @pytest.mark.parametrize("Hq,Hkv", [(24, 8), (48, 4), (32, 1)])
 def test_any_group_short_rows_through_split_entry(Hq, Hkv):
-    """max_seqlen_kv <= 16 with a group size the VALU kernel lacks: the split
-    entry runs the matrix-core kernel (G = 12 and 32 included)."""
+    """max_seqlen_kv <= 16 with a group size outside {1, 2, 4, 8}: the split
+    entry runs the short-row kernels directly (G = 3 on the VALU kernel's
+    4-head instantiation, G = 12 and 32 on the matrix-core kernel)."""
     rng = np.random.default_rng(Hq)
     seqlens = rng.integers(0, 11, size=33).astype(np.int32)
     _case(33, Hq, Hkv, 128, seqlens, 10, seed=Hq + 7)

@@ -60,8 +60,8 @@ def test_op_matches_direct_call_and_oracle():
 
 @pytest.mark.gpu
 def test_op_any_group_size():
-    """torch.ops.fmha_amd.decode with a group size outside {1, 2, 4, 8} (the
-    matrix-core kernel): same bits as the direct call, oracle parity."""
+    """torch.ops.fmha_amd.decode with a group size outside {1, 2, 4, 8}
+    (G = 7): same bits as the direct call, oracle parity."""
     import torch
     import fmha_amd
     import fmha_amd.torch_ops  # noqa: F401
