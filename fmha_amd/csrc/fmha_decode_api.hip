@@ -581,7 +581,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     ao.sub_shift = shift;
     if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
       const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
-                            (int64_t)(a.num_heads_kv - 1) * a.head_stride + D) * 2;
+                            (int64_t)(fmha_decode::kv_heads_mem(a) - 1) * a.head_stride + D) * 2;
       if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
@@ -834,14 +834,11 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
 
 namespace {
 
-// Group size the long-row kernels run a call with G query heads per KV head:
-// G itself for 1, 2, 4, 8; 4 for 3 and 8 for 5-7 and above 8 (query-group
-// padding; above 8 in slices of 8 heads, one after the other); 0 for G < 1.
-int split_group(int g) {
-  if (g < 1) return 0;
-  if (valu_group(g)) return g;
-  return g == 3 ? 4 : 8;
-}
+// Query heads per KV head the long-row kernels (instantiated for 1, 2, 4, 8)
+// run a call with G of them: G itself for 1, 2, 4, 8; 4 for 3 and 8 for 5-7
+// (query-group padding); above 8 the next multiple of 8, as G / 8 rounded up
+// launch KV heads of 8 per KV head; 0 for G < 1.
+int long_row_group(int g) { return g > 8 ? (g + 7) / 8 * 8 : valu_kernel_group(g); }
 
 // Bytes of one query-group-padded copy of Q or O ([batch, Hkv * GP, D]),
 // aligned for the workspace.
@@ -857,11 +854,14 @@ extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_
       (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
   const int g = num_heads_q % num_heads_kv == 0 ? num_heads_q / num_heads_kv : 0;
-  const int gp = split_group(g);
-  if (gp == 0 || gp == g) return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
-  // Padded query group: its Q and O copies, then the plan for Hkv * GP heads.
-  return 2 * group_pad_bytes(batch, num_heads_kv, gp, head_dim) +
-         plan_split(batch, num_heads_kv * gp, num_heads_kv, max_seqlen_kv, head_dim).total;
+  if (g == 0 || valu_group(g)) return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
+  // G > 8: ns groups of 8 per KV head on Hkv * ns launch KV heads; Q and O
+  // copies unless G is a multiple of 8.  G = 3, 5-7: the copies padded to
+  // 4 or 8, and the plan for Hkv * GP heads.
+  const int gp = long_row_group(g);
+  const int ns = g > 8 ? gp / 8 : 1;
+  const size_t pad = gp == g ? 0 : 2 * group_pad_bytes(batch, num_heads_kv, gp, head_dim);
+  return pad + plan_split(batch, num_heads_kv * gp, num_heads_kv * ns, max_seqlen_kv, head_dim).total;
 }
 
 namespace {
@@ -871,8 +871,8 @@ namespace {
 // range one wave's K/V descriptor covers in the caller's layout (must stay
 // below 2^30, as must one batch's scores and partial outputs).
 int split_prepare(const void* Q, const void* K, const void* V, void* O, int32_t max_seqlen_kv, int32_t batch,
-                  int32_t num_heads_q, int32_t num_heads_kv, int32_t head_dim, float softmax_scale, void* workspace,
-                  size_t workspace_bytes, int64_t kv_span_bytes, SplitArgs& a) {
+                  int32_t num_heads_q, int32_t num_heads_kv, int32_t kv_groups, int32_t head_dim, float softmax_scale,
+                  void* workspace, size_t workspace_bytes, int64_t kv_span_bytes, SplitArgs& a) {
   const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim);
   const int64_t padded_rows = (int64_t)plan.nblk * fmha_decode::kSplitBlockRows;
   const int64_t part_bytes = (int64_t)num_heads_q * plan.nchunks * head_dim * 4;  // one batch's partials
@@ -900,6 +900,7 @@ int split_prepare(const void* Q, const void* K, const void* V, void* O, int32_t 
   a.opart = reinterpret_cast<float*>(ws + plan.off_opart);
   a.num_heads_q = num_heads_q;
   a.num_heads_kv = num_heads_kv;
+  a.kv_groups = kv_groups;
   a.units_per_batch = (int32_t)(plan.units / batch);
   a.nblk = plan.nblk;
   a.nchunks = plan.nchunks;
@@ -929,18 +930,23 @@ int split_check_workspace_args(int32_t max_seqlen_kv) {
   return FMHA_DECODE_SUCCESS;
 }
 
-// Runs body(Q, O, num_heads_q, workspace, workspace_bytes) for a long-row
-// call.  With G outside {1, 2, 4, 8} the body sees copies of Q and O padded
-// to GP query heads per KV head, placed at the start of the workspace (the
-// rest goes to the body), made and read back around it on the same stream;
-// G > 8 runs the body once per slice of up to 8 query heads (K and V are
-// then read once per slice).
+// Runs body(Q, O, num_heads_q, num_heads_kv, kv_groups, workspace,
+// workspace_bytes) for a long-row call, whose kernels exist for G in {1, 2,
+// 4, 8}.  G = 3 and 5-7 run as 4 and 8 on copies of Q and O padded to that
+// many query heads per KV head, placed at the start of the workspace (the
+// rest goes to the body), made and read back around it on the same stream.
+// G > 8 runs as ns = ceil(G / 8) groups of 8 on one launch: the body sees
+// Hkv * ns launch KV heads, launch head h reading KV head h / ns (kv_groups
+// = ns), so that K and V are read once, and Q and O padded to ns * 8 query
+// heads per KV head (no copies when G is a multiple of 8).
 template <class BODY>
 int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int32_t hq, int32_t hkv, int32_t d,
                        void* workspace, size_t workspace_bytes, BODY body) {
   const int g = hq / hkv;
-  const int gp = split_group(g);
-  if (gp == g) return body(Q, O, hq, workspace, workspace_bytes);
+  if (valu_group(g)) return body(Q, O, hq, hkv, 1, workspace, workspace_bytes);
+  const int gp = long_row_group(g);
+  const int ns = g > 8 ? gp / 8 : 1;
+  if (gp == g) return body(Q, O, hq, hkv * ns, ns, workspace, workspace_bytes);
   const size_t pb = group_pad_bytes(batch, hkv, gp, d);
   if (!workspace) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "workspace must be non-null");
   if ((reinterpret_cast<uintptr_t>(workspace) & (kWorkspaceAlign - 1)) != 0)
@@ -956,23 +962,18 @@ int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int3
   const uint64_t pad_chunks = streams * (uint64_t)gp * (uint64_t)(d / 8);
   const uint64_t pad_blocks = (pad_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
   if (pad_blocks > (uint64_t)INT32_MAX) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
-  for (int g0 = 0; g0 < g; g0 += gp) {
-    const int gn = g - g0 < gp ? g - g0 : gp;
-    const uint64_t out_blocks =
-        (streams * (uint64_t)gn * (uint64_t)(d / 8) + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
-    hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks),
-                       dim3(fmha_decode::kPadThreads), 0, st, static_cast<const uint16_t*>(Q), qp, streams, g, g0, gn,
-                       gp, d);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
-    const int rc = body(qp, op, hkv * gp, ws + 2 * pb, workspace_bytes - 2 * pb);
-    if (rc != FMHA_DECODE_SUCCESS) return rc;
-    hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
-                       dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, g0, gn, gp,
-                       d);
-    err = hipGetLastError();
-    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
-  }
+  const uint64_t out_blocks =
+      (streams * (uint64_t)g * (uint64_t)(d / 8) + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
+  hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks), dim3(fmha_decode::kPadThreads),
+                     0, st, static_cast<const uint16_t*>(Q), qp, streams, g, 0, g, gp, d);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  const int rc = body(qp, op, hkv * gp, hkv * ns, ns, ws + 2 * pb, workspace_bytes - 2 * pb);
+  if (rc != FMHA_DECODE_SUCCESS) return rc;
+  hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
+                     dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, 0, g, gp, d);
+  err = hipGetLastError();
+  if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
 }
 }  // namespace
@@ -1006,16 +1007,16 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
     if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
       return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
     SplitArgs unused;
-    rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale,
+    rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1, head_dim_q, softmax_scale,
                        workspace, workspace_bytes, span, unused);
     if (rc != FMHA_DECODE_SUCCESS) return rc;
     return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0, rows_hint);
   }
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
-      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
+      [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale, ws,
+        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q, softmax_scale, ws,
                                 ws_bytes, span, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = cu_seqlens_kv;
@@ -1054,9 +1055,9 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "one batch's K/V span exceeds 1 GiB");
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
-      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
+      [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale, ws,
+        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q, softmax_scale, ws,
                                 ws_bytes, extent, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = seqlens_kv;
@@ -1081,8 +1082,9 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
                     num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   max_seqlen_kv = paged_capacity(block_table_stride, page_size, max_seqlen_kv);
-  // Short rows with G <= 8 take the VALU paged kernel directly; larger G
-  // run it on slices of the query group.
+  // Short rows with G <= 8 take the VALU paged kernel directly; with G > 8
+  // they go through the split kernels below like longer rows (one 16-row
+  // block, one chunk).
   if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV && valu_kernel_group(num_heads_q / num_heads_kv) != 0)
     return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
                        max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
@@ -1090,12 +1092,9 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
-      [&](const void* q, void* o, int32_t hq, void* ws, size_t ws_bytes) {
-        if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
-          return paged_short(stream, q, K_cache, V_cache, o, block_table, block_table_stride, seqlens_kv, page_size,
-                             max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q, softmax_scale);
+      [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K_cache, V_cache, o, max_seqlen_kv, batch, hq, num_heads_kv, head_dim_q,
+        int rc2 = split_prepare(q, K_cache, V_cache, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q,
                                 softmax_scale, ws, ws_bytes, 16 * row_bytes, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = seqlens_kv;

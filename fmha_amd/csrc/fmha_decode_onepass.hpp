@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
       // This batch's rows relative to the wave's first batch; one that a
       // broken table puts beyond the descriptor's reach counts as invalid.
       const int64_t rel = (int64_t)a.cu[b] - a.cu[b0];
-      if (rel < 0 || rel > (int64_t)((1u << 30) / ((uint32_t)a.num_heads_kv * D * 2u)) - a.max_rows) bad = lane_ok;
+      if (rel < 0 || rel > (int64_t)((1u << 30) / ((uint32_t)kv_heads_mem(a) * D * 2u)) - a.max_rows) bad = lane_ok;
       else rel_rows = (int)rel;
     }
     if (bad || !lane_ok) {

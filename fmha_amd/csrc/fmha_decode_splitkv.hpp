@@ -74,7 +74,17 @@ struct SplitArgs {
   // wave holds, its lane groups take 2^sub_shift blocks (scores) or chunks
   // (P.V) of the same heads instead of idling (packed and strided layouts).
   int32_t sub_shift;
+  // Launch KV heads per KV head in memory (>= 1): a query group larger than
+  // the kernels' G runs as kv_groups groups of G on one launch, launch head
+  // hk reading memory head hk / kv_groups of num_heads_kv / kv_groups.
+  int32_t kv_groups;
 };
+
+// KV heads of the cache in memory, and the one launch head hk reads.
+__host__ __device__ __forceinline__ int kv_heads_mem(const SplitArgs& a) { return a.num_heads_kv / a.kv_groups; }
+__device__ __forceinline__ int kv_head_mem(const SplitArgs& a, int hk) {
+  return a.kv_groups == 1 ? hk : hk / a.kv_groups;
+}
 
 // Lane groups of a wave under SplitArgs::sub_shift: group hkl (of HPW)
 // serves KV head hg * (HPW >> sub_shift) + hkl % (HPW >> sub_shift) for
@@ -162,20 +172,22 @@ struct LongRows {
     n = hi > lo_ ? hi - lo_ : 0;
     lane_rows = lane_rows_;
     lane_n = lane_end < n ? lane_end : n;
+    const int hkv = kv_heads_mem(a);
+    const int hm = kv_head_mem(a, hk);
     if constexpr (LAYOUT == kLayoutPacked) {
-      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
-      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
-      rsrc = make_rsrc(t + ((uint64_t)row_base + lo) * a.num_heads_kv * D, (uint32_t)n * row_bytes);
+      row_bytes = (uint32_t)hkv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hm * D + r * 8) * 2u : kLaneOutOfRange;
+      rsrc = make_rsrc(t + ((uint64_t)row_base + lo) * hkv * D, (uint32_t)n * row_bytes);
     } else if constexpr (LAYOUT == kLayoutStrided) {
       row_bytes = (uint32_t)a.row_stride * 2u;
-      lane_off = head_ok ? (uint32_t)(hk * a.head_stride + r * 8) * 2u : kLaneOutOfRange;
+      lane_off = head_ok ? (uint32_t)(hm * a.head_stride + r * 8) * 2u : kLaneOutOfRange;
       const uint32_t span = n == 0 ? 0u
                                    : ((uint32_t)(n - 1) * (uint32_t)a.row_stride +
-                                      (uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+                                      (uint32_t)(hkv - 1) * (uint32_t)a.head_stride + D) * 2u;
       rsrc = make_rsrc(t + (uint64_t)b * (uint64_t)a.batch_stride + (uint64_t)lo * (uint64_t)a.row_stride, span);
     } else {
-      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
-      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+      row_bytes = (uint32_t)hkv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hm * D + r * 8) * 2u : kLaneOutOfRange;
       base = t;
       pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
       page_shift = (uint32_t)a.page_shift;
@@ -194,25 +206,27 @@ struct LongRows {
                                              uint32_t b, int S, int rel_rows, int hk, bool head_ok, int r) {
     static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
     lo = 0;
+    const int hkv = kv_heads_mem(a);
+    const int hm = kv_head_mem(a, hk);
     if constexpr (LAYOUT == kLayoutPacked) {
-      row_bytes = (uint32_t)a.num_heads_kv * D * 2u;
-      lane_off = head_ok ? (uint32_t)(hk * D + r * 8) * 2u : kLaneOutOfRange;
+      row_bytes = (uint32_t)hkv * D * 2u;
+      lane_off = head_ok ? (uint32_t)(hm * D + r * 8) * 2u : kLaneOutOfRange;
       lane_rows = rel_rows;
       lane_n = rel_rows + S;
       int m = lane_n;
 #pragma unroll
       for (int k = 1; k < kWaveSize; k <<= 1) m = max(m, __shfl_xor(m, k, kWaveSize));
       n = __builtin_amdgcn_readfirstlane(m);
-      rsrc = make_rsrc(t + (uint64_t)a.cu[b0] * a.num_heads_kv * D, (uint32_t)n * row_bytes);
+      rsrc = make_rsrc(t + (uint64_t)a.cu[b0] * hkv * D, (uint32_t)n * row_bytes);
     } else {
       row_bytes = (uint32_t)a.row_stride * 2u;
-      lane_off = head_ok ? (uint32_t)(hk * a.head_stride + r * 8) * 2u + (b - b0) * (uint32_t)a.batch_stride * 2u
+      lane_off = head_ok ? (uint32_t)(hm * a.head_stride + r * 8) * 2u + (b - b0) * (uint32_t)a.batch_stride * 2u
                          : kLaneOutOfRange;
       lane_rows = 0;
       lane_n = S;
       n = a.max_rows;
       const uint32_t span = ((nb - 1) * (uint32_t)a.batch_stride + (uint32_t)(a.max_rows - 1) * (uint32_t)a.row_stride +
-                             (uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
+                             (uint32_t)(hkv - 1) * (uint32_t)a.head_stride + D) * 2u;
       rsrc = make_rsrc(t + (uint64_t)b0 * (uint64_t)a.batch_stride, span);
     }
   }

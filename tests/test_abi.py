@@ -197,8 +197,13 @@ def test_splitkv_workspace_size(lib):
     # plus the two copies (4 * 8 * 4 * 128 * 2 bytes each)
     assert f(4, 24, 8, 100, 128) == f(4, 32, 8, 100, 128) + 2 * 4 * 8 * 4 * 128 * 2
     assert f(4, 56, 8, 100, 128) == f(4, 64, 8, 100, 128) + 2 * 4 * 8 * 8 * 128 * 2
-    # G = 12 runs as two slices of up to 8 heads through the same copies
-    assert f(4, 96, 8, 100, 128) == f(4, 64, 8, 100, 128) + 2 * 4 * 8 * 8 * 128 * 2
+    # G > 8 runs as ceil(G / 8) groups of 8 on Hkv * ceil(G / 8) launch KV
+    # heads: G = 16 needs the plan for 16 KV heads of G = 8 and no copies,
+    # G = 12 the same plan plus copies padded to 16 query heads per KV head
+    assert f(4, 128, 8, 100, 128) == f(4, 128, 16, 100, 128)
+    assert f(4, 96, 8, 100, 128) == f(4, 128, 16, 100, 128) + 2 * 4 * 8 * 16 * 128 * 2
+    # MQA with G = 40 = 5 * 8: five launch KV heads, no copies
+    assert f(2, 40, 1, 5000, 64) == f(2, 40, 5, 5000, 64)
 
 
 @pytest.mark.parametrize("kw,code,needle", [

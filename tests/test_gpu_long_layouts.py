@@ -267,9 +267,10 @@ def test_paged_padded_group(page_size, B, max_len):
 
 
 def test_long_layouts_group_slices():
-    """G = 12 beyond 16 rows over BHSD and 16-row pages (two slices of the
-    query group), and G = 12 on the short paged kernel through the workspace
-    entry."""
+    """G = 12 beyond 16 rows over BHSD and 16-row pages (two groups of 8 on
+    one launch, padded to 16 query heads per KV head), and G = 12 with at
+    most 16 rows through the paged workspace entry (the split kernels, one
+    block)."""
     import fmha_amd
     import torch
     D, Hq, Hkv, B = 128, 24, 2, 5
@@ -289,3 +290,28 @@ def test_long_layouts_group_slices():
                                         torch.from_numpy(seqlens).cuda(), max_seqlen_kv=cap)
         torch.cuda.synchronize()
         _check(o2, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"paged G=12 cap={cap}")
+
+
+@pytest.mark.parametrize("B,cap", [(3, 400), (600, 40), (7, 9)])
+def test_long_layouts_grouped_launch_kv_heads(B, cap):
+    """G = 16 with one KV head (two launch KV heads reading the same cache
+    head, no copies of Q and O) over BHSD and over 1- and 16-row pages."""
+    import fmha_amd
+    import torch
+    D, Hq, Hkv = 128, 16, 1
+    rng = np.random.default_rng(B * 5 + cap)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[0] = cap
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=B + cap + 41)
+    kc = _strided_cache(kp, seqlens, cap, Hkv, D, "bhsd")
+    vc = _strided_cache(vp, seqlens, cap, Hkv, D, "bhsd")
+    o = fmha_amd.fmha_decode_strided(to_dev(q), _strided_view(kc, "bhsd"), _strided_view(vc, "bhsd"),
+                                     seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"bhsd G=16 B={B} cap={cap}")
+    for ps in (1, 16):
+        kc2, vc2, bt = _paged_cache(kp, vp, seqlens, ps, Hkv, D, rng)
+        o2 = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc2), to_dev(vc2), torch.from_numpy(bt).cuda(),
+                                        torch.from_numpy(seqlens).cuda(), max_seqlen_kv=cap)
+        torch.cuda.synchronize()
+        _check(o2, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"paged G=16 ps={ps} B={B} cap={cap}")

@@ -265,9 +265,53 @@ def test_any_group_short_rows_through_split_entry(Hq, Hkv):
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 24, 2), (128, 32, 1), (64, 48, 4), (256, 20, 2)])
 @pytest.mark.parametrize("B,max_len", [(4, 500), (700, 40)])
 def test_group_slices_beyond_eight(D, Hq, Hkv, B, max_len):
-    """G = 12, 32, 10 beyond 16 rows: slices of up to 8 query heads run one
-    after the other on the padded copies (K and V read once per slice)."""
+    """G = 12, 32, 10 beyond 16 rows: ceil(G / 8) groups of 8 query heads
+    per KV head on one launch (launch KV head h reading KV head h / ceil(G /
+    8)), on copies of Q and O padded to a multiple of 8 heads (G = 12, 10) or
+    on Q and O themselves (G = 32)."""
     rng = np.random.default_rng(B + max_len + Hq + D)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 1)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 1), (128, 24, 1), (64, 32, 2), (256, 16, 1), (128, 48, 2)])
+@pytest.mark.parametrize("B,max_len", [(3, 900), (600, 33), (9, 17)])
+def test_grouped_launch_kv_heads(D, Hq, Hkv, B, max_len):
+    """G = 16, 24, 16, 16, 24 beyond 16 rows, multiples of 8 (no copies of Q
+    and O): launch KV heads = Hkv * G / 8, which the lane groups of a wave
+    share as sub-units (Hkv * G / 8 = 2 at D = 128: blocks, chunks or
+    batches per lane group) or leave partly idle (3 launch heads)."""
+    rng = np.random.default_rng(B * 3 + max_len + Hq + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 2)
+
+
+@pytest.mark.parametrize("B,max_len", [(4, 300), (700, 40)])
+def test_grouped_launch_kv_heads_bad_lengths(B, max_len):
+    """A length above max_seqlen_kv with G = 16 (split and single pass): NaN
+    for that batch only, oracle parity for the rest."""
+    import fmha_amd
+    import torch
+    D, Hq, Hkv = 128, 32, 2
+    rng = np.random.default_rng(B + 77)
+    seqlens = rng.integers(1, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    bad = B // 2
+    seqlens_big = seqlens.copy()
+    seqlens_big[bad] = max_len + 5
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens_big, seed=B + 78)
+    o = fmha_amd.fmha_decode_splitkv(to_dev(q), to_dev(k), to_dev(v), torch.from_numpy(cu).cuda(), max_len,
+                                     softmax_scale=default_scale(D))
+    torch.cuda.synchronize()
+    bits = o.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, Hq, D)
+    f = oracle.f16_to_f32(bits)
+    assert np.all(np.isnan(f[bad]))
+    keep = np.array([b for b in range(B) if b != bad])
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True,
+                             max_seqlen=max_len + 5)
+    st = oracle.compare(np.ascontiguousarray(bits[keep]).ravel(),
+                        np.ascontiguousarray(r.reshape(B, Hq, D)[keep]).ravel(),
+                        np.ascontiguousarray(slack.reshape(B, Hq, D)[keep]).ravel())
+    assert_pass(st, f"G=16 neighbours of an invalid length B={B}")
