@@ -21,6 +21,7 @@
 #include "fmha_decode_kernel.hpp"
 #include "fmha_decode_onepass.hpp"
 #include "fmha_decode_splitkv.hpp"
+#include "fmha_decode_splitkv_group.hpp"
 
 namespace {
 
@@ -321,6 +322,18 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // 264/324, G=7 S=2 370/421), D=256 (G=3 365/490, G=6 443/691).
 // FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
 // keeps the VALU kernel wherever it exists (for comparisons).
+// Long rows on packed and strided caches: the matrix-core split passes for
+// G > 8 (kv_groups > 1 on entry), the VALU passes otherwise.
+// FMHA_DECODE_GQA_KERNEL=valu keeps every G on the VALU passes (G > 8 on
+// ceil(G / 8) launch KV heads of 8 query heads), =mfma puts every G on the
+// matrix cores.
+bool split_on_matrix_cores(int kv_groups) {
+  const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL");
+  if (e && std::strcmp(e, "valu") == 0) return false;
+  if (e && std::strcmp(e, "mfma") == 0) return true;
+  return kv_groups > 1;
+}
+
 bool use_mfma_kernel(int g, int dq, int rows_hint) {
   if (const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL")) {
     if (std::strcmp(e, "mfma") == 0) return true;
@@ -563,6 +576,40 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Pass 2 of split-KV: the global max and sum per (batch, query head).  One
+// lane per head for rows of at most 16 blocks, else one workgroup per head
+// sized to the row's block count (8 blocks per thread and round).
+void launch_split_stats(const SplitArgs& a, hipStream_t stream) {
+  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
+  if (a.nblk <= 16)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_lane_kernel, dim3((heads + 255) / 256), dim3(256), 0, stream, a);
+  else if (a.nblk <= 8 * 64)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<64>, dim3(heads), dim3(64), 0, stream, a);
+  else if (a.nblk <= 8 * 256)
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<256>, dim3(heads), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
+}
+
+// Pass 4 of split-KV (more than one chunk per row): partial outputs summed
+// in chunk order, one lane per 8 dims for few chunks, else a workgroup per
+// (head, 32 dims).
+template <int D>
+void launch_split_combine(const SplitArgs& a, hipStream_t stream) {
+  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
+  if (a.nchunks <= 16) {
+    const uint64_t lanes = (uint64_t)heads * (D / 8);
+    hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                       stream, a);
+  } else if (a.nchunks <= 256) {
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads * (D / 32)), dim3(256), 0,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads * (D / 32)), dim3(1024), 0,
+                       stream, a);
+  }
+}
+
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
 template <int D, int G, int LAYOUT>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
@@ -606,18 +653,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
                        lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, as);
   }
-  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
-  // One lane per (batch, query head) for rows of at most 16 blocks, else one
-  // workgroup per head sized to the row's block count (8 blocks per thread
-  // and round).
-  if (a.nblk <= 16)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_lane_kernel, dim3((heads + 255) / 256), dim3(256), 0, stream, a);
-  else if (a.nblk <= 8 * 64)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<64>, dim3(heads), dim3(64), 0, stream, a);
-  else if (a.nblk <= 8 * 256)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<256>, dim3(heads), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
+  launch_split_stats(a, stream);
   if (a.nchunks == 1) {
     // One chunk per batch: the P.V wave writes O itself, one chunk per wave.
     constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
@@ -631,17 +667,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
                        stream, as);
   }
-  if (a.nchunks <= 16) {
-    const uint64_t lanes = (uint64_t)heads * (D / 8);
-    hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
-                       stream, a);
-  } else if (a.nchunks <= 256) {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads * (D / 32)), dim3(256), 0,
-                       stream, a);
-  } else {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads * (D / 32)), dim3(1024), 0,
-                       stream, a);
-  }
+  launch_split_combine<D>(a, stream);
   return hipGetLastError();
 }
 
@@ -661,6 +687,54 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
     case 64: return launch_split_d<64, LAYOUT>(a, g, stream);
     case 128: return launch_split_d<128, LAYOUT>(a, g, stream);
     default: return launch_split_d<256, LAYOUT>(a, g, stream);
+  }
+}
+
+// Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
+// are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
+// size.  Scores, stats, P.V (O directly with one chunk per row), combine.
+// P.V waves take TW tiles of 16 query heads, their accumulators TW * D/16 *
+// 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
+template <int D, int LAYOUT>
+hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
+  constexpr int HPW = kWaveSize / (D / 8);
+  constexpr int TW = D == 256 ? 1 : 2;
+  const int64_t g = a.num_heads_q / a.num_heads_kv;
+  const int64_t tiles = (g + 15) / 16;
+  const int64_t tc = (tiles + TW - 1) / TW;
+  const int64_t score_waves = (int64_t)a.batch * ((a.nblk + HPW - 1) / HPW) * a.num_heads_kv;
+  const int64_t units = (int64_t)a.batch * a.nchunks * a.num_heads_kv;
+  const int64_t pv_waves = (units + 7) / 8 * 8 * tc;
+  if (score_waves > INT32_MAX || pv_waves > INT32_MAX ||
+      (uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX)
+    return hipErrorInvalidValue;
+  {
+    constexpr auto kernel = fmha_decode::splitkv_scores_group_kernel<D, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
+  }
+  launch_split_stats(a, stream);
+  if (a.nchunks == 1) {
+    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, true, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+    return hipGetLastError();
+  }
+  {
+    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, false, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+  }
+  launch_split_combine<D>(a, stream);
+  return hipGetLastError();
+}
+
+template <int LAYOUT>
+hipError_t launch_split_group_layout(const SplitArgs& a, int d, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_split_group_d<64, LAYOUT>(a, stream);
+    case 128: return launch_split_group_d<128, LAYOUT>(a, stream);
+    default: return launch_split_group_d<256, LAYOUT>(a, stream);
   }
 }
 
@@ -915,6 +989,20 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = a.num_heads_q / a.num_heads_kv;
   hipError_t err;
+  if ((layout == fmha_decode::kLayoutPacked || layout == fmha_decode::kLayoutStrided) &&
+      split_on_matrix_cores(a.kv_groups)) {
+    // The matrix cores take the cache's KV heads with all of their query
+    // heads (a group above 8: ns * 8 of them, the same workspace plan).
+    SplitArgs m = a;
+    m.num_heads_kv = fmha_decode::kv_heads_mem(a);
+    m.kv_groups = 1;
+    m.sub_shift = 0;
+    err = layout == fmha_decode::kLayoutPacked
+              ? launch_split_group_layout<fmha_decode::kLayoutPacked>(m, head_dim, s)
+              : launch_split_group_layout<fmha_decode::kLayoutStrided>(m, head_dim, s);
+    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+    return FMHA_DECODE_SUCCESS;
+  }
   switch (layout) {
     case fmha_decode::kLayoutPacked: err = launch_split_layout<fmha_decode::kLayoutPacked>(a, head_dim, g, s); break;
     case fmha_decode::kLayoutStrided: err = launch_split_layout<fmha_decode::kLayoutStrided>(a, head_dim, g, s); break;

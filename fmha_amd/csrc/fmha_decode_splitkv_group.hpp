@@ -1,0 +1,332 @@
+// fmha_decode_splitkv_group.hpp -- the split-KV scores and P.V passes on the
+// matrix cores, for query groups larger than 8 (lengths beyond 16 rows).
+//
+// The VALU passes (fmha_decode_splitkv.hpp) spend per lane about G * D / 8
+// multiply-adds per row on Q.K^T and as many on P.V, so their time grows
+// with G: the host runs a group above 8 on them as ceil(G / 8) launch KV
+// heads of 8 query heads (SplitArgs::kv_groups), which reads K and V once
+// but still doubles the arithmetic per doubling of G.  Here both products
+// are MFMAs over 16-column tiles of query heads, as in fmha_decode_group.hpp,
+// and one wave serves one KV head with all of its query heads:
+//
+//   * Scores: a wave takes HPW = 64 / (D/8) consecutive 16-row blocks of
+//     one (batch, KV head), one block per lane group, loads their K rows as
+//     the VALU pass does (LongRows, rows past the length read as 0) and
+//     stages them in LDS; per 16-column tile of query heads (B operand read
+//     straight from Q in the MFMA's layout) and block, S^T = K_blk . Q^T is
+//     D/32 v_mfma_f32_16x16x32_bf16.  The scaled scores, the block max and
+//     the block sum of exp(t - max) go to the same workspace arrays as the
+//     VALU pass's, so the stats and combine kernels are shared.
+//   * P.V: a wave takes one (batch, KV head, chunk) and up to TW tiles of
+//     query heads; its lane groups load successive 16-row sub-blocks of the
+//     chunk (HPW per round), V is transposed into LDS with v_perm as in the
+//     short kernel, and per tile and sub-block the bf16 weights
+//     bf16(exp(t - max) / sum) -- the row's global max and sum -- are the A
+//     operand of D/16 v_mfma_f32_16x16x16_bf16 accumulating O[tile, D] over
+//     the chunk's rows.  One chunk per row: fp16 O directly; otherwise fp32
+//     partial outputs for the combine pass.
+//
+// Same numerics as the VALU passes (fp32 scores, scale, block and global
+// softmax statistics, weights rounded to bf16 after normalisation, fp32
+// accumulation, chunk partials summed in chunk order, one RNE rounding to
+// fp16); only the order of the fp32 sums inside a product differs.  Packed
+// and strided layouts (the lane groups of a wave read different rows,
+// which a paged layout's one-page descriptor cannot cover).  The query
+// heads of a KV head may be padded (Q and O copies with a multiple of 8
+// heads): the kernels take G = num_heads_q / num_heads_kv as given.
+#pragma once
+
+#include "fmha_decode_group.hpp"
+#include "fmha_decode_splitkv.hpp"
+
+namespace fmha_decode {
+
+// Wave barrier between LDS writes and reads of one wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Grid: batch * ceil(nblk / HPW) * Hkv one-wave workgroups, workgroup
+// (b * nwb + wb) * Hkv + hk serving blocks [wb * HPW, wb * HPW + HPW) of KV
+// head hk of batch b (consecutive waves: neighbouring heads of the same
+// rows).
+template <int D, int LAYOUT>
+__global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(SplitArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "lane groups read different rows");
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  constexpr int NR = kSplitBlockRows;
+  __shared__ __attribute__((aligned(16))) char k_lds[NR * Sh::KS];
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t hkv = (uint32_t)a.num_heads_kv;
+  const uint32_t nwb = ((uint32_t)a.nblk + HPW - 1) / HPW;
+  const uint32_t id = blockIdx.x;
+  const uint32_t hk = id % hkv;
+  const uint32_t rest = id / hkv;
+  const uint32_t wb = rest % nwb;
+  const uint32_t b = rest / nwb;
+  if (b >= (uint32_t)a.batch) return;
+  const int S = split_len_l<LAYOUT>(a, b);
+  const int j0 = (int)wb * HPW * NR;  // the wave's first row
+  if (S < 0 || S > a.max_rows || j0 >= S) return;
+  const int s = lane / LPH;  // this lane group's block of the wave
+  const int r = lane % LPH;
+  const int q = lane >> 4;   // MFMA lane group
+  const int n = lane & 15;   // MFMA row / column
+  const int hq = a.num_heads_q;
+  const int G = hq / (int)hkv;
+  const int tiles = (G + 15) / 16;
+
+  // K rows of the wave's blocks (lane group s: rows j0 + 16 s + j).
+  LongRows<D, LAYOUT> kv;
+  kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
+  u32x4 kr[NR];
+  kv.template load<NR>(kr, j0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(k_lds + j * Sh::KS + s * D * 2 + r * 16) = kr[j];
+  wave_lds_sync();
+
+  // This KV head's query rows, and the scores of the wave's blocks.
+  const __amdgpu_buffer_rsrc_t q_rsrc =
+      make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  const int blk0 = (int)wb * HPW;
+  const int nb = a.nblk - blk0 < HPW ? a.nblk - blk0 : HPW;
+  const __amdgpu_buffer_rsrc_t t_rsrc =
+      make_rsrc(a.t + t_block_base(a, b, blk0), (uint32_t)nb * (uint32_t)hq * NR * 4u);
+  for (int tile = 0; tile < tiles; ++tile) {
+    const int g = tile * 16 + n;  // this lane's query column
+    const bool gok = g < G;
+    bf16x8_v qb[Sh::QLD];
+#pragma unroll
+    for (int cc = 0; cc < Sh::QLD; ++cc)
+      qb[cc] = __builtin_bit_cast(
+          bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, gok ? (uint32_t)(g * D + (4 * cc + q) * 8) * 2u
+                                                              : kLaneOutOfRange));
+#pragma unroll
+    for (int p = 0; p < HPW; ++p) {
+      const int jb = j0 + p * NR;  // first row of block p
+      if (jb >= S) break;
+      f32x4_v c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cc = 0; cc < Sh::QLD; ++cc) {
+        const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(k_lds + n * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[cc], c4, 0, 0, 0);
+      }
+      // Rows 4q..4q+3 of block p for query column g; the block's max and
+      // sum of exponentials over its valid rows (row jb is valid, so the
+      // max is finite for finite scores).
+      float x[4];
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = c4[e] * a.scale;
+        m = jb + 4 * q + e < S ? fmaxf(m, x[e]) : m;
+      }
+      m = column_reduce<true>(m);
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum += jb + 4 * q + e < S ? expf(x[e] - m) : 0.0f;
+      sum = column_reduce<false>(sum);
+      // Scores of rows past S (their K rows read as 0) land in the block's
+      // padding, which nothing reads as a weight.
+      if (gok) {
+        const u32x4 v4 = {__builtin_bit_cast(uint32_t, x[0]), __builtin_bit_cast(uint32_t, x[1]),
+                          __builtin_bit_cast(uint32_t, x[2]), __builtin_bit_cast(uint32_t, x[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, v4), t_rsrc,
+                                               (int)((((uint32_t)p * hq + hk * G + g) * NR + 4 * q) * 4u), 0,
+                                               kPolicyStreamStore);
+        if (q == 0) {
+          const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk0 + p;
+          a.m[idx] = m;
+          a.l[idx] = sum;
+        }
+      }
+    }
+  }
+}
+
+// fp16 output of DPC dims per query row (8, 16 or 32 bytes) at byte offset off.
+template <int DPC>
+__device__ __forceinline__ void store_f16_run(__amdgpu_buffer_rsrc_t o_rsrc, uint32_t off, const float* v) {
+#pragma unroll
+  for (int h8 = 0; h8 < (DPC + 7) / 8; ++h8) {
+    constexpr int W = DPC < 8 ? DPC : 8;
+    float vals[8];
+#pragma unroll
+    for (int k8 = 0; k8 < 8; ++k8) vals[k8] = k8 < W ? v[h8 * 8 + (k8 < W ? k8 : 0)] : 0.0f;
+    const u32x4 pk = pack_f16x8(vals);
+    if constexpr (W == 8) {
+      buffer_store16(o_rsrc, off + h8 * 16, pk);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{pk[0], pk[1]}, o_rsrc, (int)off, 0, kPolicyStreamStore);
+    }
+  }
+}
+
+// Grid: units = batch * nchunks * Hkv (unit (b * nchunks + c) * Hkv + hk),
+// each in TC = ceil(tiles / TW) tile chunks; ceil(units / 8) * 8 * TC
+// one-wave workgroups, workgroup w serving unit ((w / 8) / TC) * 8 + w % 8
+// and tile chunk (w / 8) % TC, so that the tile chunks of one unit run on
+// one XCD (dispatch is round-robin over the 8 XCDs) and re-read its V from
+// that XCD's L2.  DIRECT: one chunk per row (nchunks == 1), O written here.
+template <int D, int TW, bool DIRECT, int LAYOUT>
+__global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "lane groups read different rows");
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  constexpr int NR = kSplitBlockRows;
+  constexpr int DPC = Sh::DPC;
+  __shared__ __attribute__((aligned(16))) char v_lds[HPW * Sh::VSTREAM];
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const uint32_t hkv = (uint32_t)a.num_heads_kv;
+  const int hq = a.num_heads_q;
+  const int G = hq / (int)hkv;
+  const int tiles = (G + 15) / 16;
+  const uint32_t tc_count = (uint32_t)((tiles + TW - 1) / TW);
+  const uint32_t w = blockIdx.x;
+  const uint32_t rest = w >> 3;
+  const uint32_t unit = (rest / tc_count) * 8u + (w & 7u);
+  const int tile0 = (int)(rest % tc_count) * TW;
+  const uint32_t nchunks = (uint32_t)a.nchunks;
+  if (unit >= (uint32_t)a.batch * nchunks * hkv) return;
+  const uint32_t hk = unit % hkv;
+  const uint32_t c = (unit / hkv) % nchunks;
+  const uint32_t b = unit / hkv / nchunks;
+  const int ntl = tiles - tile0 < TW ? tiles - tile0 : TW;  // > 0
+  const int S = split_len_l<LAYOUT>(a, b);
+  const bool bad = S < 0 || S > a.max_rows;
+  const int row0 = (int)c * a.chunk_rows;
+  const int q = lane >> 4;
+  const int n = lane & 15;
+  const __amdgpu_buffer_rsrc_t o_rsrc =
+      make_rsrc(a.o + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  if (bad || row0 >= S) {
+    // Only a DIRECT launch (one chunk) owns the output of an empty or
+    // invalid row; the combine kernel covers them otherwise.
+    if constexpr (DIRECT) {
+      const u32x4 fill = bad ? u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u} : u32x4{0u, 0u, 0u, 0u};
+      for (int k = lane; k < ntl * 16 * (D / 8); k += kWaveSize) {
+        const int g = tile0 * 16 + k / (D / 8);
+        if (g < G) buffer_store16(o_rsrc, (uint32_t)(g * D + (k % (D / 8)) * 8) * 2u, fill);
+      }
+    }
+    return;
+  }
+  const int s = lane / LPH;  // lane group: sub-block s of each round
+  const int r = lane % LPH;
+  const int rows = S - row0 < a.chunk_rows ? S - row0 : a.chunk_rows;  // > 0
+  const int rounds = (rows + HPW * NR - 1) / (HPW * NR);
+  // Lane group s reads rows row0 + 16 (HPW k + s) + j in round k.
+  LongRows<D, LAYOUT> vrows;
+  vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), row0, row0 + rows, (int)hk, true, r, s * NR, rows);
+  const __amdgpu_buffer_rsrc_t t_rsrc =
+      make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * NR * 4u);
+  // The row's global max and sum for this lane's query column of each tile.
+  float gm[TW], gl[TW];
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    const int g = (tile0 + i) * 16 + n;
+    const bool ok = i < ntl && g < G;
+    const uint64_t hqi = (uint64_t)b * hq + (uint64_t)hk * G + (ok ? g : 0);
+    gm[i] = ok ? a.ml[2 * hqi] : 0.0f;
+    gl[i] = ok ? a.ml[2 * hqi + 1] : 1.0f;
+  }
+  f32x4_v acc[TW][DPC];
+#pragma unroll
+  for (int i = 0; i < TW; ++i)
+#pragma unroll
+    for (int dt = 0; dt < DPC; ++dt) acc[i][dt] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  u32x4 vr[NR];
+  vrows.template load<NR>(vr, 0);
+  for (int k = 0; k < rounds; ++k) {
+    // V^T of the round's sub-blocks: sub-block s at s * VSTREAM, 8-dim block
+    // r at r * VB, dim e at e * 32 bytes, 16 rows of bf16.
+    wave_lds_sync();  // the previous round's reads of v_lds are done
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 wv;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const int j = 8 * half + 2 * pp;
+          wv[pp] = __builtin_amdgcn_perm((uint32_t)vr[j + 1][e / 2], (uint32_t)vr[j][e / 2],
+                                         (e & 1) ? kPermHi : kPermLo);
+        }
+        *reinterpret_cast<u32x4*>(v_lds + s * Sh::VSTREAM + r * Sh::VB + e * (NR * 2) + half * 16) = wv;
+      }
+    }
+    wave_lds_sync();
+    // The next round's rows are in flight during this round's products.
+    if (k + 1 < rounds) vrows.template load<NR>(vr, (k + 1) * HPW * NR);
+#pragma unroll
+    for (int p = 0; p < HPW; ++p) {
+      const int jr = (k * HPW + p) * NR;  // sub-block's first row, relative to row0
+      if (jr >= rows) break;
+      const int blk = (row0 + jr) / NR;
+      const char* vs = v_lds + p * Sh::VSTREAM;
+      bf16x4_v vb[DPC];
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const int dim = n * DPC + dt;
+        vb[dt] = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (NR * 2) + q * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < TW; ++i) {
+        if (i >= ntl) break;
+        const int g = (tile0 + i) * 16 + n;
+        const u32x4 t4 = buffer_load16<kPolicyDefault>(
+            t_rsrc, g < G ? (((uint32_t)blk * hq + hk * G + g) * NR + 4 * q) * 4u : kLaneOutOfRange);
+        bf16x4_v pa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool valid = g < G && jr + 4 * q + e < rows;
+          const float pw = valid ? expf(__builtin_bit_cast(float, (uint32_t)t4[e]) - gm[i]) / gl[i] : 0.0f;
+          pa[e] = (__bf16)pw;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DPC; ++dt)
+          acc[i][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[dt], acc[i][dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // Lane (q, n) holds query rows 4q..4q+3 of each tile, dims [n DPC, n DPC + DPC).
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    if (i >= ntl) break;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = (tile0 + i) * 16 + 4 * q + e;
+      float v[DPC];
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[i][dt][e];
+      if constexpr (DIRECT) {
+        store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
+      } else {
+        // Partial outputs [Hq][nchunks][D] of this batch (default policy:
+        // the combine pass reads them right after).
+        const uint32_t part_bytes = nchunks * D * 4u;
+        const __amdgpu_buffer_rsrc_t p_rsrc =
+            make_rsrc(a.opart + ((uint64_t)b * hq + (uint64_t)hk * G) * nchunks * D, (uint32_t)G * part_bytes);
+        const uint32_t off = g < G ? (uint32_t)g * part_bytes + (c * D + n * DPC) * 4u : kLaneOutOfRange;
+#pragma unroll
+        for (int h4 = 0; h4 < DPC / 4; ++h4) {
+          const u32x4 x4 = {__builtin_bit_cast(uint32_t, v[4 * h4]), __builtin_bit_cast(uint32_t, v[4 * h4 + 1]),
+                            __builtin_bit_cast(uint32_t, v[4 * h4 + 2]), __builtin_bit_cast(uint32_t, v[4 * h4 + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x4), p_rsrc, (int)(off + h4 * 16), 0,
+                                                 kPolicyDefault);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace fmha_decode

@@ -292,12 +292,18 @@ def test_long_layouts_group_slices():
         _check(o2, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"paged G=12 cap={cap}")
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
 @pytest.mark.parametrize("B,cap", [(3, 400), (600, 40), (7, 9)])
-def test_long_layouts_grouped_launch_kv_heads(B, cap):
-    """G = 16 with one KV head (two launch KV heads reading the same cache
-    head, no copies of Q and O) over BHSD and over 1- and 16-row pages."""
+def test_long_layouts_grouped_launch_kv_heads(monkeypatch, kernel, B, cap):
+    """G = 16 with one KV head, no copies of Q and O, over BHSD (the
+    matrix-core split passes, or two VALU launch KV heads reading the same
+    cache head) and over 1- and 16-row pages (launch KV heads)."""
     import fmha_amd
     import torch
+    if kernel == "valu":
+        monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "valu")
+    else:
+        monkeypatch.delenv("FMHA_DECODE_GQA_KERNEL", raising=False)
     D, Hq, Hkv = 128, 16, 1
     rng = np.random.default_rng(B * 5 + cap)
     seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)

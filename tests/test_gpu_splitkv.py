@@ -262,13 +262,26 @@ def test_any_group_short_rows_through_split_entry(Hq, Hkv):
     assert np.all(np.isfinite(oracle.f16_to_f32(o[[0, 2]])))
 
 
+@pytest.fixture(params=["mfma", "valu"])
+def long_group_kernel(request, monkeypatch):
+    """The two paths of a query group above 8 beyond 16 rows: the
+    matrix-core split passes (the default) and the VALU passes on ceil(G / 8)
+    launch KV heads of 8 query heads (FMHA_DECODE_GQA_KERNEL=valu)."""
+    if request.param == "valu":
+        monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "valu")
+    else:
+        monkeypatch.delenv("FMHA_DECODE_GQA_KERNEL", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 24, 2), (128, 32, 1), (64, 48, 4), (256, 20, 2)])
 @pytest.mark.parametrize("B,max_len", [(4, 500), (700, 40)])
-def test_group_slices_beyond_eight(D, Hq, Hkv, B, max_len):
-    """G = 12, 32, 10 beyond 16 rows: ceil(G / 8) groups of 8 query heads
-    per KV head on one launch (launch KV head h reading KV head h / ceil(G /
-    8)), on copies of Q and O padded to a multiple of 8 heads (G = 12, 10) or
-    on Q and O themselves (G = 32)."""
+def test_group_slices_beyond_eight(long_group_kernel, D, Hq, Hkv, B, max_len):
+    """G = 12, 32, 10 beyond 16 rows, on copies of Q and O padded to a
+    multiple of 8 query heads per KV head (G = 12, 10) or on Q and O
+    themselves (G = 32): the matrix-core passes over each KV head's padded
+    group, or ceil(G / 8) launch KV heads of 8 (launch head h reading KV head
+    h / ceil(G / 8))."""
     rng = np.random.default_rng(B + max_len + Hq + D)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
@@ -277,11 +290,13 @@ def test_group_slices_beyond_eight(D, Hq, Hkv, B, max_len):
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 1), (128, 24, 1), (64, 32, 2), (256, 16, 1), (128, 48, 2)])
 @pytest.mark.parametrize("B,max_len", [(3, 900), (600, 33), (9, 17)])
-def test_grouped_launch_kv_heads(D, Hq, Hkv, B, max_len):
+def test_grouped_launch_kv_heads(long_group_kernel, D, Hq, Hkv, B, max_len):
     """G = 16, 24, 16, 16, 24 beyond 16 rows, multiples of 8 (no copies of Q
-    and O): launch KV heads = Hkv * G / 8, which the lane groups of a wave
-    share as sub-units (Hkv * G / 8 = 2 at D = 128: blocks, chunks or
-    batches per lane group) or leave partly idle (3 launch heads)."""
+    and O).  Matrix cores: one or two 16-column tiles per KV head (24: the
+    second half padding).  VALU: launch KV heads = Hkv * G / 8, which the
+    lane groups of a wave share as sub-units (Hkv * G / 8 = 2 at D = 128:
+    blocks, chunks or batches per lane group) or leave partly idle (3 launch
+    heads)."""
     rng = np.random.default_rng(B * 3 + max_len + Hq + D)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
@@ -289,7 +304,7 @@ def test_grouped_launch_kv_heads(D, Hq, Hkv, B, max_len):
 
 
 @pytest.mark.parametrize("B,max_len", [(4, 300), (700, 40)])
-def test_grouped_launch_kv_heads_bad_lengths(B, max_len):
+def test_grouped_launch_kv_heads_bad_lengths(long_group_kernel, B, max_len):
     """A length above max_seqlen_kv with G = 16 (split and single pass): NaN
     for that batch only, oracle parity for the rest."""
     import fmha_amd
@@ -315,3 +330,28 @@ def test_grouped_launch_kv_heads_bad_lengths(B, max_len):
                         np.ascontiguousarray(r.reshape(B, Hq, D)[keep]).ravel(),
                         np.ascontiguousarray(slack.reshape(B, Hq, D)[keep]).ravel())
     assert_pass(st, f"G=16 neighbours of an invalid length B={B}")
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,B,max_len", [(128, 64, 1, 2, 3000), (64, 128, 1, 3, 700), (256, 48, 2, 5, 300),
+                                               (128, 40, 1, 3, 1100), (128, 96, 3, 9, 77)])
+def test_matrix_core_split_many_tiles(D, Hq, Hkv, B, max_len):
+    """The matrix-core split passes with more tiles than a P.V wave holds
+    (G = 64, 128, 24 at D = 256, 40, 32): several tile chunks
+    per (batch, KV head, chunk), every length 0..max_len region covered."""
+    rng = np.random.default_rng(B * 11 + max_len + Hq + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 3)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 8, 8), (128, 32, 8), (64, 8, 2), (256, 12, 4), (128, 20, 4)])
+@pytest.mark.parametrize("B,max_len", [(4, 600), (300, 40)])
+def test_matrix_core_split_small_groups(monkeypatch, D, Hq, Hkv, B, max_len):
+    """FMHA_DECODE_GQA_KERNEL=mfma puts every group size on the matrix-core
+    split passes: G = 1, 4, 4, 3 (padded to 4), 5 (padded to 8), one tile
+    whose columns past G are padding (never stored, zero weights)."""
+    monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "mfma")
+    rng = np.random.default_rng(B * 13 + max_len + Hq + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 4)
