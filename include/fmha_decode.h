@@ -201,12 +201,19 @@ int fmha_decode_fwd_paged(void* stream,
  * share a workspace must be ordered (same stream or synchronised).
  *
  * Group sizes G = num_heads_q / num_heads_kv: any.  With max_seqlen_kv <= 16
- * as fmha_decode_fwd; beyond 16 (and for the paged entry at any length) the
- * long-row kernels exist for G = 1, 2, 4, 8, and other G run on copies of Q
- * and O padded to 4 (G = 3) or 8 query heads per KV head, which the
- * workspace size includes (two copies of [batch, Hkv * 4 or 8, head_dim],
- * ahead of the split-KV data); G > 8 runs in slices of 8 query heads one
- * after the other, each reading K and V again.
+ * as fmha_decode_fwd (the paged entry: G <= 8 as fmha_decode_fwd_paged, G > 8
+ * as beyond 16).  Beyond 16 the VALU kernels exist for G = 1, 2, 4, 8; G = 3
+ * and 5-7 run on copies of Q and O padded to 4 or 8 query heads per KV head.
+ * G > 8 runs with Q and O padded to a multiple of 8 query heads per KV head
+ * (copies only when G is not one): on packed and strided caches through
+ * split-KV passes on the matrix cores (all query heads of a KV head per
+ * wave), on paged caches as ceil(G / 8) groups of 8 query heads per KV head
+ * on the VALU kernels; either way K and V are read once.  The workspace size
+ * includes the copies (two of [batch, Hkv * padded group, head_dim], ahead
+ * of the split-KV data).  FMHA_DECODE_GQA_KERNEL=valu keeps packed and
+ * strided caches on the VALU kernels for every G (G > 8 as the paged entry
+ * does), =mfma puts every G on the matrix-core passes (G <= 8 measures
+ * slower there), for comparisons.
  */
 size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                           int32_t max_seqlen_kv, int32_t head_dim);
