@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import make_inputs, to_dev
+from tests.common import assert_pass, default_scale, make_inputs, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -183,4 +183,72 @@ def test_graph_matrix_core_kernel_replays_match_eager(monkeypatch, kernel):
         for i, (o, e) in enumerate(zip(outs, eager)):
             assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
         fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud)
+        torch.cuda.synchronize()
+
+
+def test_graph_long_rows_large_group_replays_match_eager():
+    """Lengths beyond 16 with G > 8 in a graph: the matrix-core split passes
+    (G = 16 on Q and O themselves, several chunks; G = 12 on the padded
+    copies, one chunk per row) and the paged route (launch KV heads of 8
+    query heads), each replay bit-equal to the eager result."""
+    import torch
+    import fmha_amd
+    s1 = np.array([900, 3, 517, 0], np.int32)
+    q1, k1, v1, cu1 = make_inputs(4, 32, 2, 128, s1, seed=101)
+    q1d, k1d, v1d, cu1d = to_dev(q1), to_dev(k1), to_dev(v1), torch.from_numpy(cu1).cuda()
+    ws1 = torch.empty(fmha_amd.splitkv_workspace_size(4, 32, 2, 900, 128), dtype=torch.uint8, device="cuda")
+    s2 = np.random.default_rng(102).integers(0, 41, size=300).astype(np.int32)
+    q2, k2, v2, cu2 = make_inputs(300, 24, 2, 64, s2, seed=103)
+    q2d, k2d, v2d, cu2d = to_dev(q2), to_dev(k2), to_dev(v2), torch.from_numpy(cu2).cuda()
+    ws2 = torch.empty(fmha_amd.splitkv_workspace_size(300, 24, 2, 40, 64), dtype=torch.uint8, device="cuda")
+    # the first case over 16-row pages
+    kc = torch.zeros(4 * 57, 16, 2, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(4 * 57, dtype=torch.int32, device="cuda").view(4, 57)
+    for b in range(4):
+        n, r0 = int(s1[b]), int(cu1[b])
+        for j in range(0, n, 16):
+            m = min(16, n - j)
+            kc[bt[b, j // 16], :m] = k1d[r0 + j:r0 + j + m]
+            vc[bt[b, j // 16], :m] = v1d[r0 + j:r0 + j + m]
+    lens1 = torch.from_numpy(s1).cuda()
+    ws3 = torch.empty_like(ws1)
+    outs = [torch.empty(4, 32, 128, dtype=torch.float16, device="cuda"),
+            torch.empty(300, 24, 64, dtype=torch.float16, device="cuda"),
+            torch.empty(4, 32, 128, dtype=torch.float16, device="cuda")]
+
+    def calls():
+        fmha_amd.fmha_decode_splitkv(q1d, k1d, v1d, cu1d, 900, out=outs[0], workspace=ws1)
+        fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 40, out=outs[1], workspace=ws2)
+        fmha_amd.fmha_decode_paged(q1d, kc, vc, bt, lens1, out=outs[2], max_seqlen_kv=900, workspace=ws3)
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    r1, slack1 = oracle.decode(q1, k1, v1, cu1, 32, 2, 128, default_scale(128), with_slack=True, max_seqlen=900)
+    for i in (0, 2):
+        assert_pass(oracle.compare(eager[i].view(torch.int16).cpu().numpy().view(np.uint16).reshape(r1.shape), r1,
+                                   slack1), f"G=16 long rows, call {i}")
+    r2, slack2 = oracle.decode(q2, k2, v2, cu2, 24, 2, 64, default_scale(64), with_slack=True, max_seqlen=40)
+    assert_pass(oracle.compare(eager[1].view(torch.int16).cpu().numpy().view(np.uint16).reshape(r2.shape), r2,
+                               slack2), "G=12 padded, one chunk")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        calls()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        ws1.fill_(255)
+        ws2.fill_(255)
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
+        fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 40)
         torch.cuda.synchronize()
