@@ -85,14 +85,25 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
   kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
   u32x4 kr[NR];
   kv.template load<NR>(kr, j0);
+  // This KV head's query rows: tile t's B operands (lane (q, n): query
+  // column 16 t + n, 16-byte chunks 4 cc + q), requested one tile ahead.
+  const __amdgpu_buffer_rsrc_t q_rsrc =
+      make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  auto load_q = [&](u32x4 (&dst)[Sh::QLD], int tile) {
+    const int g = tile * 16 + n;
+#pragma unroll
+    for (int cc = 0; cc < Sh::QLD; ++cc)
+      dst[cc] = buffer_load16<kPolicyDefault>(
+          q_rsrc, g < G && tile < tiles ? (uint32_t)(g * D + (4 * cc + q) * 8) * 2u : kLaneOutOfRange);
+  };
+  u32x4 qn[Sh::QLD];
+  load_q(qn, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(k_lds + j * Sh::KS + s * D * 2 + r * 16) = kr[j];
   wave_lds_sync();
 
-  // This KV head's query rows, and the scores of the wave's blocks.
-  const __amdgpu_buffer_rsrc_t q_rsrc =
-      make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  // The scores of the wave's blocks.
   const int blk0 = (int)wb * HPW;
   const int nb = a.nblk - blk0 < HPW ? a.nblk - blk0 : HPW;
   const __amdgpu_buffer_rsrc_t t_rsrc =
@@ -102,10 +113,8 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
     const bool gok = g < G;
     bf16x8_v qb[Sh::QLD];
 #pragma unroll
-    for (int cc = 0; cc < Sh::QLD; ++cc)
-      qb[cc] = __builtin_bit_cast(
-          bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, gok ? (uint32_t)(g * D + (4 * cc + q) * 8) * 2u
-                                                              : kLaneOutOfRange));
+    for (int cc = 0; cc < Sh::QLD; ++cc) qb[cc] = __builtin_bit_cast(bf16x8_v, qn[cc]);
+    if (tile + 1 < tiles) load_q(qn, tile + 1);
 #pragma unroll
     for (int p = 0; p < HPW; ++p) {
       const int jb = j0 + p * NR;  // first row of block p
@@ -245,6 +254,23 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
   u32x4 vr[NR];
   vrows.template load<NR>(vr, 0);
   for (int k = 0; k < rounds; ++k) {
+    // The round's scores (lane (q, n): rows 4q..4q+3 of sub-block p, query
+    // column 16 (tile0 + i) + n), requested before the V transpose so that
+    // their latency overlaps it.  Sub-blocks past the chunk's rows read
+    // nothing (their weights are 0 by the row check).
+    u32x4 t4[HPW][TW];
+#pragma unroll
+    for (int p = 0; p < HPW; ++p) {
+      const int jr = (k * HPW + p) * NR;
+      const int blk = (row0 + jr) / NR;
+#pragma unroll
+      for (int i = 0; i < TW; ++i) {
+        const int g = (tile0 + i) * 16 + n;
+        t4[p][i] = buffer_load16<kPolicyDefault>(
+            t_rsrc, jr < rows && i < ntl && g < G ? (((uint32_t)blk * hq + hk * G + g) * NR + 4 * q) * 4u
+                                                  : kLaneOutOfRange);
+      }
+    }
     // V^T of the round's sub-blocks: sub-block s at s * VSTREAM, 8-dim block
     // r at r * VB, dim e at e * 32 bytes, 16 rows of bf16.
     wave_lds_sync();  // the previous round's reads of v_lds are done
@@ -270,7 +296,6 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
     for (int p = 0; p < HPW; ++p) {
       const int jr = (k * HPW + p) * NR;  // sub-block's first row, relative to row0
       if (jr >= rows) break;
-      const int blk = (row0 + jr) / NR;
       const char* vs = v_lds + p * Sh::VSTREAM;
       bf16x4_v vb[DPC];
 #pragma unroll
@@ -282,13 +307,11 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
       for (int i = 0; i < TW; ++i) {
         if (i >= ntl) break;
         const int g = (tile0 + i) * 16 + n;
-        const u32x4 t4 = buffer_load16<kPolicyDefault>(
-            t_rsrc, g < G ? (((uint32_t)blk * hq + hk * G + g) * NR + 4 * q) * 4u : kLaneOutOfRange);
         bf16x4_v pa;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool valid = g < G && jr + 4 * q + e < rows;
-          const float pw = valid ? expf(__builtin_bit_cast(float, (uint32_t)t4[e]) - gm[i]) / gl[i] : 0.0f;
+          const float pw = valid ? expf(__builtin_bit_cast(float, (uint32_t)t4[p][i][e]) - gm[i]) / gl[i] : 0.0f;
           pa[e] = (__bf16)pw;
         }
 #pragma unroll
