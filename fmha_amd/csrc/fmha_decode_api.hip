@@ -322,11 +322,10 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // 264/324, G=7 S=2 370/421), D=256 (G=3 365/490, G=6 443/691).
 // FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
 // keeps the VALU kernel wherever it exists (for comparisons).
-// Long rows on packed and strided caches: the matrix-core split passes for
-// G > 8 (kv_groups > 1 on entry), the VALU passes otherwise.
-// FMHA_DECODE_GQA_KERNEL=valu keeps every G on the VALU passes (G > 8 on
-// ceil(G / 8) launch KV heads of 8 query heads), =mfma puts every G on the
-// matrix cores.
+// Long rows: the matrix-core split passes for G > 8 (kv_groups > 1 on
+// entry), the VALU passes otherwise.  FMHA_DECODE_GQA_KERNEL=valu keeps
+// every G on the VALU passes (G > 8 on ceil(G / 8) launch KV heads of 8
+// query heads), =mfma puts every G on the matrix cores.
 bool split_on_matrix_cores(int kv_groups) {
   const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL");
   if (e && std::strcmp(e, "valu") == 0) return false;
@@ -989,17 +988,27 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = a.num_heads_q / a.num_heads_kv;
   hipError_t err;
-  if ((layout == fmha_decode::kLayoutPacked || layout == fmha_decode::kLayoutStrided) &&
-      split_on_matrix_cores(a.kv_groups)) {
+  if (split_on_matrix_cores(a.kv_groups)) {
     // The matrix cores take the cache's KV heads with all of their query
     // heads (a group above 8: ns * 8 of them, the same workspace plan).
     SplitArgs m = a;
     m.num_heads_kv = fmha_decode::kv_heads_mem(a);
     m.kv_groups = 1;
     m.sub_shift = 0;
-    err = layout == fmha_decode::kLayoutPacked
-              ? launch_split_group_layout<fmha_decode::kLayoutPacked>(m, head_dim, s)
-              : launch_split_group_layout<fmha_decode::kLayoutStrided>(m, head_dim, s);
+    switch (layout) {
+      case fmha_decode::kLayoutPacked:
+        err = launch_split_group_layout<fmha_decode::kLayoutPacked>(m, head_dim, s);
+        break;
+      case fmha_decode::kLayoutStrided:
+        err = launch_split_group_layout<fmha_decode::kLayoutStrided>(m, head_dim, s);
+        break;
+      case fmha_decode::kLayoutPaged:
+        err = launch_split_group_layout<fmha_decode::kLayoutPaged>(m, head_dim, s);
+        break;
+      default:
+        err = launch_split_group_layout<fmha_decode::kLayoutPagedBlock>(m, head_dim, s);
+        break;
+    }
     if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
     return FMHA_DECODE_SUCCESS;
   }

@@ -30,11 +30,15 @@
 // softmax statistics, weights rounded to bf16 after normalisation, fp32
 // accumulation, chunk partials summed in chunk order, one RNE rounding to
 // fp16); only the order of the fp32 sums inside a product differs.  Packed
-// and strided layouts (the lane groups of a wave read different rows,
-// which a paged layout's one-page descriptor cannot cover).  The query
-// heads of a KV head may be padded (Q and O copies with a multiple of 8
-// heads): the kernels take G = num_heads_q / num_heads_kv as given.
+// and strided layouts read rows through LongRows' one descriptor per wave;
+// on paged layouts the lane groups of a wave read rows of different pages,
+// which one page's descriptor cannot cover, so PagedLaneRows gives every
+// lane its own 64-bit addresses instead.  The query heads of a KV head may
+// be padded (Q and O copies with a multiple of 8 heads): the kernels take
+// G = num_heads_q / num_heads_kv as given.
 #pragma once
+
+#include <type_traits>
 
 #include "fmha_decode_group.hpp"
 #include "fmha_decode_splitkv.hpp"
@@ -48,13 +52,78 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The rows [lo, hi) of one (batch, KV head) of a paged cache ([pages,
+// page_size, Hkv, D], row j in slot j % page_size of page block_table[b][j /
+// page_size]) for waves whose lane groups read different rows: the same
+// init / load interface as LongRows, with per-lane addresses.  Each lane
+// looks up the pages of its own rows (BLOCK, page_size >= 16: one lookup per
+// 16-row block, which lies in one page); rows at or past the lane's end
+// issue no access, so unused block-table entries are never followed.
+template <int D, bool BLOCK>
+struct PagedLaneRows {
+  const uint16_t* base;   // the cache at this lane's head and dims
+  const int32_t* pages;   // this batch's block-table row
+  uint32_t page_shift;
+  uint64_t page_stride;   // elements per page
+  uint64_t row_elems;     // elements per slot (Hkv * D)
+  int lo, lane_rows, lane_n;
+
+  __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t, int lo_, int hi,
+                                       int hk, bool head_ok, int r, int lane_rows_ = 0, int lane_end = 1 << 30) {
+    const int n = hi > lo_ ? hi - lo_ : 0;
+    lo = lo_;
+    lane_rows = lane_rows_;
+    lane_n = head_ok ? (lane_end < n ? lane_end : n) : 0;
+    base = t + (uint64_t)kv_head_mem(a, hk) * D + r * 8;
+    pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+    page_shift = (uint32_t)a.page_shift;
+    page_stride = (uint64_t)a.batch_stride;
+    row_elems = (uint64_t)kv_heads_mem(a) * D;
+  }
+
+  // Rows lo + rel0 + lane_rows + j, j < NR (rel0 and lane_rows multiples of
+  // NR = 16, lo a multiple of 16).
+  template <int NR>
+  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
+    const int row0 = rel0 + lane_rows;
+    const uint32_t mask = (1u << page_shift) - 1u;
+    if constexpr (BLOCK) {
+      const uint32_t abs0 = (uint32_t)(lo + row0);
+      const uint64_t page = row0 < lane_n ? (uint64_t)(uint32_t)pages[abs0 >> page_shift] : 0u;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        out[j] = u32x4{0u, 0u, 0u, 0u};
+        if (row0 + j < lane_n)
+          out[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+              base + page * page_stride + (uint64_t)((abs0 + j) & mask) * row_elems));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        out[j] = u32x4{0u, 0u, 0u, 0u};
+        if (row0 + j < lane_n) {
+          const uint32_t abs = (uint32_t)(lo + row0 + j);
+          const uint64_t page = (uint64_t)(uint32_t)pages[abs >> page_shift];
+          out[j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(base + page * page_stride + (uint64_t)(abs & mask) * row_elems));
+        }
+      }
+    }
+  }
+};
+
+// The row loader of the matrix-core split passes for a layout.
+template <int D, int LAYOUT>
+using GroupRows = typename std::conditional<LAYOUT == kLayoutPaged || LAYOUT == kLayoutPagedBlock,
+                                            PagedLaneRows<D, LAYOUT == kLayoutPagedBlock>,
+                                            LongRows<D, LAYOUT>>::type;
+
 // Grid: batch * ceil(nblk / HPW) * Hkv one-wave workgroups, workgroup
 // (b * nwb + wb) * Hkv + hk serving blocks [wb * HPW, wb * HPW + HPW) of KV
 // head hk of batch b (consecutive waves: neighbouring heads of the same
 // rows).
 template <int D, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(SplitArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "lane groups read different rows");
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -81,7 +150,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
   const int tiles = (G + 15) / 16;
 
   // K rows of the wave's blocks (lane group s: rows j0 + 16 s + j).
-  LongRows<D, LAYOUT> kv;
+  GroupRows<D, LAYOUT> kv;
   kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
   u32x4 kr[NR];
   kv.template load<NR>(kr, j0);
@@ -89,14 +158,16 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
   // column 16 t + n, 16-byte chunks 4 cc + q), requested one tile ahead.
   const __amdgpu_buffer_rsrc_t q_rsrc =
       make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
-  auto load_q = [&](u32x4 (&dst)[Sh::QLD], int tile) {
+  auto load_q = [&](bf16x8_v (&dst)[Sh::QLD], int tile) {
     const int g = tile * 16 + n;
 #pragma unroll
     for (int cc = 0; cc < Sh::QLD; ++cc)
-      dst[cc] = buffer_load16<kPolicyDefault>(
-          q_rsrc, g < G && tile < tiles ? (uint32_t)(g * D + (4 * cc + q) * 8) * 2u : kLaneOutOfRange);
+      dst[cc] = __builtin_bit_cast(
+          bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, g < G && tile < tiles
+                                                              ? (uint32_t)(g * D + (4 * cc + q) * 8) * 2u
+                                                              : kLaneOutOfRange));
   };
-  u32x4 qn[Sh::QLD];
+  bf16x8_v qn[Sh::QLD];
   load_q(qn, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -113,7 +184,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
     const bool gok = g < G;
     bf16x8_v qb[Sh::QLD];
 #pragma unroll
-    for (int cc = 0; cc < Sh::QLD; ++cc) qb[cc] = __builtin_bit_cast(bf16x8_v, qn[cc]);
+    for (int cc = 0; cc < Sh::QLD; ++cc) qb[cc] = qn[cc];
     if (tile + 1 < tiles) load_q(qn, tile + 1);
 #pragma unroll
     for (int p = 0; p < HPW; ++p) {
@@ -184,7 +255,6 @@ __device__ __forceinline__ void store_f16_run(__amdgpu_buffer_rsrc_t o_rsrc, uin
 // that XCD's L2.  DIRECT: one chunk per row (nchunks == 1), O written here.
 template <int D, int TW, bool DIRECT, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "lane groups read different rows");
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -231,7 +301,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
   const int rows = S - row0 < a.chunk_rows ? S - row0 : a.chunk_rows;  // > 0
   const int rounds = (rows + HPW * NR - 1) / (HPW * NR);
   // Lane group s reads rows row0 + 16 (HPW k + s) + j in round k.
-  LongRows<D, LAYOUT> vrows;
+  GroupRows<D, LAYOUT> vrows;
   vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), row0, row0 + rows, (int)hk, true, r, s * NR, rows);
   const __amdgpu_buffer_rsrc_t t_rsrc =
       make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * NR * 4u);
