@@ -617,14 +617,16 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   // idling: packed and strided layouts, whose descriptor spans the rows
   // (the paged ones address one page at a time).
   constexpr int HPW = kWaveSize / (D / 8);
+  constexpr bool LANES = LAYOUT == fmha_decode::kLayoutPagedLanes || LAYOUT == fmha_decode::kLayoutPagedBlockLanes;
   int shift = 0;
-  if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+  if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
   {
     // The single pass spans 2^shift batches with one descriptor: for the
-    // strided layout only when their span stays below 1 GiB.
+    // strided layout only when their span stays below 1 GiB; paged layouts
+    // run it with one batch and one page descriptor per wave.
     SplitArgs ao = a;
-    ao.sub_shift = shift;
+    ao.sub_shift = LANES ? 0 : shift;
     if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
       const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
                             (int64_t)(fmha_decode::kv_heads_mem(a) - 1) * a.head_stride + D) * 2;
@@ -634,7 +636,10 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     if (onepass_fits<D, G>(ao)) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
-      return launch_onepass_dg<D, G, LAYOUT, false>(ao, stream);
+      constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
+                         : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
+                                                                         : LAYOUT;
+      return launch_onepass_dg<D, G, OL, false>(ao, stream);
     }
   }
   // The combine grid has one workgroup per (batch, query head, 32 dims).
@@ -1012,11 +1017,22 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
     if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
     return FMHA_DECODE_SUCCESS;
   }
+  // Paged caches with fewer KV heads than a wave holds read through
+  // per-lane addresses, so that the idle lane groups take other blocks or
+  // chunks of the same heads (sub-units, as on packed caches).
+  const int hpw = kWaveSize / (head_dim / 8);
+  const bool lanes = 2 * a.num_heads_kv <= hpw && hpw % (2 * a.num_heads_kv) == 0;
   switch (layout) {
     case fmha_decode::kLayoutPacked: err = launch_split_layout<fmha_decode::kLayoutPacked>(a, head_dim, g, s); break;
     case fmha_decode::kLayoutStrided: err = launch_split_layout<fmha_decode::kLayoutStrided>(a, head_dim, g, s); break;
-    case fmha_decode::kLayoutPaged: err = launch_split_layout<fmha_decode::kLayoutPaged>(a, head_dim, g, s); break;
-    default: err = launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s); break;
+    case fmha_decode::kLayoutPaged:
+      err = lanes ? launch_split_layout<fmha_decode::kLayoutPagedLanes>(a, head_dim, g, s)
+                  : launch_split_layout<fmha_decode::kLayoutPaged>(a, head_dim, g, s);
+      break;
+    default:
+      err = lanes ? launch_split_layout<fmha_decode::kLayoutPagedBlockLanes>(a, head_dim, g, s)
+                  : launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s);
+      break;
   }
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;

@@ -31,6 +31,8 @@
 // Opart 4*D bytes per chunk and query head.
 #pragma once
 
+#include <type_traits>
+
 #include "fmha_decode_kernel.hpp"
 
 namespace fmha_decode {
@@ -126,6 +128,14 @@ __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint3
 // lookup per row).  The host picks between the two, so that no pipelined loop
 // carries a branch (the compiler would wait for every request at its head).
 constexpr int kLayoutPagedBlock = 3;
+// The same two paged layouts read through per-lane addresses
+// (PagedLaneRows), so that the lane groups of a wave can read rows of
+// different pages: sub-units (SplitArgs::sub_shift) with fewer KV heads than
+// a wave holds.
+constexpr int kLayoutPagedLanes = 4;
+constexpr int kLayoutPagedBlockLanes = 5;
+
+constexpr bool is_paged_layout(int layout) { return layout >= kLayoutPaged && layout <= kLayoutPagedBlockLanes; }
 
 // A pointer the whole wave holds, moved to scalar registers: a buffer
 // descriptor built from a value the compiler keeps in vector registers
@@ -267,6 +277,80 @@ struct LongRows {
   }
 };
 
+// The rows [lo, hi) of one (batch, KV head) of a paged cache ([pages,
+// page_size, Hkv, D], row j in slot j % page_size of page block_table[b][j /
+// page_size]) for waves whose lane groups read different rows: the same
+// init / load interface as LongRows, with per-lane addresses.  Each lane
+// looks up the pages of its own rows (BLOCK, page_size >= 16: one lookup per
+// 16-row block, which lies in one page).  The loads carry no branch (a
+// branch in a pipelined loop makes the compiler wait for every request at
+// its head): a row at or past the lane's end reads slot 0 of the batch's
+// first page instead, with block-table entry 0, and is replaced by 0.  That
+// page exists whenever the batch has a row, which every wave that loads
+// rows checks first; unused block-table entries are never followed.
+template <int D, bool BLOCK>
+struct PagedLaneRows {
+  const uint16_t* base;   // the cache at this lane's head and dims
+  const int32_t* pages;   // this batch's block-table row
+  uint32_t page_shift;
+  uint64_t page_stride;   // elements per page
+  uint64_t row_elems;     // elements per slot (Hkv * D)
+  int lo, lane_rows, lane_n;
+
+  __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t, int lo_, int hi,
+                                       int hk, bool head_ok, int r, int lane_rows_ = 0, int lane_end = 1 << 30) {
+    const int n = hi > lo_ ? hi - lo_ : 0;
+    lo = lo_;
+    lane_rows = lane_rows_;
+    lane_n = head_ok ? (lane_end < n ? lane_end : n) : 0;
+    base = t + (uint64_t)kv_head_mem(a, hk) * D + r * 8;
+    pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+    page_shift = (uint32_t)a.page_shift;
+    page_stride = (uint64_t)a.batch_stride;
+    row_elems = (uint64_t)kv_heads_mem(a) * D;
+  }
+
+  // Rows lo + rel0 + lane_rows + j, j < NR (lo and lane_rows multiples of
+  // 16, rel0 a multiple of NR <= 16: with BLOCK the NR rows lie in one
+  // 16-row block, hence in one page).
+  template <int NR>
+  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
+    const int row0 = rel0 + lane_rows;
+    const uint32_t mask = (1u << page_shift) - 1u;
+    u32x4 v[NR];
+    if constexpr (BLOCK) {
+      const bool any = row0 < lane_n;
+      const uint32_t abs0 = (uint32_t)(lo + row0);
+      const uint64_t page = (uint64_t)(uint32_t)pages[any ? abs0 >> page_shift : 0u];
+      const uint16_t* blk = base + page * page_stride + (uint64_t)(any ? abs0 & mask : 0u) * row_elems;
+#pragma unroll
+      for (int j = 0; j < NR; ++j)
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(blk + (row0 + j < lane_n ? j * row_elems : 0)));
+    } else {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const bool ok = row0 + j < lane_n;
+        const uint32_t abs = (uint32_t)(lo + row0 + j);
+        const uint64_t page = (uint64_t)(uint32_t)pages[ok ? abs >> page_shift : 0u];
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            base + page * page_stride + (uint64_t)(ok ? abs & mask : 0u) * row_elems));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const bool ok = row0 + j < lane_n;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[j][k] = ok ? (uint32_t)v[j][k] : 0u;
+    }
+  }
+};
+
+// The row loader of the split-KV passes for a layout.
+template <int D, int LAYOUT>
+using SplitRows = typename std::conditional<LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes,
+                                            PagedLaneRows<D, LAYOUT == kLayoutPagedBlockLanes>,
+                                            LongRows<D, LAYOUT>>::type;
+
 // First packed row of batch b (0 for the other layouts, which address rows
 // per batch).
 template <int LAYOUT>
@@ -328,7 +412,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   const bool block_ok = jb < S;         // else past the row (and maybe past nblk): no writes
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
   // Rows [0, S) of the batch: rows past S read 0 without access.
-  LongRows<D, LAYOUT> kv;
+  SplitRows<D, LAYOUT> kv;
   kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, hk, head_ok, r, p * NR);
   const uint32_t q_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
 
@@ -614,7 +698,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   const int rows_w = min(S - roww, a.chunk_rows);  // the wave's first chunk: the most rows
   // Each lane group reads its own chunk's rows only: sub-blocks past its
   // end read 0 without access.
-  LongRows<D, LAYOUT> vrows;
+  SplitRows<D, LAYOUT> vrows;
   const int rowe = S - roww < (a.chunk_rows << a.sub_shift) ? S : roww + (a.chunk_rows << a.sub_shift);
   vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), roww, rowe, hk, head_ok, r, row0 - roww,
              row0 - roww + (rows > 0 ? rows : 0));

@@ -38,8 +38,6 @@
 // G = num_heads_q / num_heads_kv as given.
 #pragma once
 
-#include <type_traits>
-
 #include "fmha_decode_group.hpp"
 #include "fmha_decode_splitkv.hpp"
 
@@ -52,71 +50,12 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The rows [lo, hi) of one (batch, KV head) of a paged cache ([pages,
-// page_size, Hkv, D], row j in slot j % page_size of page block_table[b][j /
-// page_size]) for waves whose lane groups read different rows: the same
-// init / load interface as LongRows, with per-lane addresses.  Each lane
-// looks up the pages of its own rows (BLOCK, page_size >= 16: one lookup per
-// 16-row block, which lies in one page); rows at or past the lane's end
-// issue no access, so unused block-table entries are never followed.
-template <int D, bool BLOCK>
-struct PagedLaneRows {
-  const uint16_t* base;   // the cache at this lane's head and dims
-  const int32_t* pages;   // this batch's block-table row
-  uint32_t page_shift;
-  uint64_t page_stride;   // elements per page
-  uint64_t row_elems;     // elements per slot (Hkv * D)
-  int lo, lane_rows, lane_n;
-
-  __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t, int lo_, int hi,
-                                       int hk, bool head_ok, int r, int lane_rows_ = 0, int lane_end = 1 << 30) {
-    const int n = hi > lo_ ? hi - lo_ : 0;
-    lo = lo_;
-    lane_rows = lane_rows_;
-    lane_n = head_ok ? (lane_end < n ? lane_end : n) : 0;
-    base = t + (uint64_t)kv_head_mem(a, hk) * D + r * 8;
-    pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
-    page_shift = (uint32_t)a.page_shift;
-    page_stride = (uint64_t)a.batch_stride;
-    row_elems = (uint64_t)kv_heads_mem(a) * D;
-  }
-
-  // Rows lo + rel0 + lane_rows + j, j < NR (rel0 and lane_rows multiples of
-  // NR = 16, lo a multiple of 16).
-  template <int NR>
-  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
-    const int row0 = rel0 + lane_rows;
-    const uint32_t mask = (1u << page_shift) - 1u;
-    if constexpr (BLOCK) {
-      const uint32_t abs0 = (uint32_t)(lo + row0);
-      const uint64_t page = row0 < lane_n ? (uint64_t)(uint32_t)pages[abs0 >> page_shift] : 0u;
-#pragma unroll
-      for (int j = 0; j < NR; ++j) {
-        out[j] = u32x4{0u, 0u, 0u, 0u};
-        if (row0 + j < lane_n)
-          out[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-              base + page * page_stride + (uint64_t)((abs0 + j) & mask) * row_elems));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NR; ++j) {
-        out[j] = u32x4{0u, 0u, 0u, 0u};
-        if (row0 + j < lane_n) {
-          const uint32_t abs = (uint32_t)(lo + row0 + j);
-          const uint64_t page = (uint64_t)(uint32_t)pages[abs >> page_shift];
-          out[j] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(base + page * page_stride + (uint64_t)(abs & mask) * row_elems));
-        }
-      }
-    }
-  }
-};
-
-// The row loader of the matrix-core split passes for a layout.
+// The row loader of the matrix-core split passes for a layout: per-lane
+// addresses on every paged layout.
 template <int D, int LAYOUT>
-using GroupRows = typename std::conditional<LAYOUT == kLayoutPaged || LAYOUT == kLayoutPagedBlock,
-                                            PagedLaneRows<D, LAYOUT == kLayoutPagedBlock>,
-                                            LongRows<D, LAYOUT>>::type;
+using GroupRows = typename std::conditional<
+    is_paged_layout(LAYOUT), PagedLaneRows<D, LAYOUT == kLayoutPagedBlock || LAYOUT == kLayoutPagedBlockLanes>,
+    LongRows<D, LAYOUT>>::type;
 
 // Grid: batch * ceil(nblk / HPW) * Hkv one-wave workgroups, workgroup
 // (b * nwb + wb) * Hkv + hk serving blocks [wb * HPW, wb * HPW + HPW) of KV

@@ -321,3 +321,25 @@ def test_long_layouts_grouped_launch_kv_heads(monkeypatch, kernel, B, cap):
                                         torch.from_numpy(seqlens).cuda(), max_seqlen_kv=cap)
         torch.cuda.synchronize()
         _check(o2, q, kp, vp, seqlens, Hq, Hkv, D, max(cap, 16), f"paged G=16 ps={ps} B={B} cap={cap}")
+
+
+@pytest.mark.parametrize("page_size", [1, 8, 16, 32])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 8, 1), (128, 8, 2), (256, 4, 1), (128, 2, 2), (64, 20, 4)])
+@pytest.mark.parametrize("B,max_len", [(3, 2000), (9, 100)])
+def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
+    """Paged caches with fewer KV heads than a wave holds (MQA, GQA after
+    tensor-parallel sharding): the split passes read through per-lane
+    addresses, each lane group taking its own blocks and chunks (sub-units),
+    with several chunks per row (2000) or one (100, the P.V pass writing O);
+    G = 8, 4, 4, 1 and 5 (padded to 8)."""
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(page_size * 7 + D + Hq + Hkv + B)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + D + Hq + B + 61)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged ps={page_size} D={D} {Hq}/{Hkv} B={B}")
