@@ -621,10 +621,15 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   int shift = 0;
   if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
-  {
-    // The single pass spans 2^shift batches with one descriptor: for the
-    // strided layout only when their span stays below 1 GiB; paged layouts
-    // run it with one batch and one page descriptor per wave.
+  // The single pass spans 2^shift batches with one descriptor: for the
+  // strided layout only when their span stays below 1 GiB.  Paged layouts
+  // run it with one batch and one page descriptor per wave, which leaves
+  // the lanes of missing KV heads idle: at D = 64 and 128 the split passes,
+  // whose lane groups take their own blocks and chunks, measured faster
+  // (16-row pages, B=2048 S=128 D=128: Hq/Hkv 8/1 129.3 -> 58.2 µs, 16/2
+  // 131.8 -> 85.3), at D = 256 (two heads per wave) the single pass (B=4096
+  // S=64 4/1: 55.8 against 86.1).
+  if (!LANES || D == 256) {
     SplitArgs ao = a;
     ao.sub_shift = LANES ? 0 : shift;
     if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
