@@ -266,9 +266,10 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   const int w = waves_per_cu_for(rows_hint, g);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
-  // Fewer KV heads than a wave holds: R batches per wave, every lane busy.
-  // Strided only when R batches' spans fit one descriptor.
-  const int shift = layout == fmha_decode::kLayoutPaged ? 0 : multi_shift(a.num_heads_kv, dq);
+  // Fewer KV heads than a wave holds: R batches per wave, every lane busy
+  // (paged: per-lane page lookups and addresses).  Strided only when R
+  // batches' spans fit one descriptor.
+  const int shift = fp32_weights && layout != fmha_decode::kLayoutPacked ? 0 : multi_shift(a.num_heads_kv, dq);
   bool multi = shift > 0;
   if (multi && layout == fmha_decode::kLayoutStrided) {
     const int64_t rows = a.max_rows > 0 ? a.max_rows : 1;
@@ -288,7 +289,8 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
         err = fp32_weights ? launch_multi<fmha_decode::kLayoutPacked, true>(a, dq, g, w, s)
                            : launch_multi<fmha_decode::kLayoutPacked, false>(a, dq, g, w, s);
         break;
-      default: err = launch_multi<fmha_decode::kLayoutStrided, false>(a, dq, g, w, s); break;
+      case fmha_decode::kLayoutStrided: err = launch_multi<fmha_decode::kLayoutStrided, false>(a, dq, g, w, s); break;
+      default: err = launch_multi<fmha_decode::kLayoutPaged, false>(a, dq, g, w, s); break;
     }
     if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
     return FMHA_DECODE_SUCCESS;

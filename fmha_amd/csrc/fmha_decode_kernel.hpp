@@ -687,12 +687,88 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
     buffer_store16(o_rsrc, group_row_off<G>(qo_off, g, grp, D), bad ? nan4 : pack_f16x8(acc[g]));
 }
 
+// The same for a paged cache (lengths in a.lens, log2(page_size) in
+// a.seqlen_uniform, page stride in a.batch_stride): the lane groups' batches
+// have their own pages, so every lane loads through its own 64-bit
+// addresses, with no branch.  A row with nothing to read (past the lane
+// group's length, or a lane group with no valid row) reads row 0 of the
+// first lane group whose batch has one (head 0) and is replaced by 0; the
+// block-table entry looked up for such a row is entry 0 of its batch, so
+// no lookup leaves the batch's table row.  A wave with no valid row reads
+// nothing.
+template <int D, int G, int SMAX, bool PF32>
+__device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uint32_t b0, uint32_t nb, uint32_t b,
+                                                        int S, bool bad, bool lane_ok, int sub, int hk, int lane,
+                                                        uint16_t* lds_p) {
+  constexpr int LPH = D / 8;
+  const int r = lane % LPH;
+  const int hq = a.num_heads_q;
+  const uint32_t q_bytes = nb * (uint32_t)hq * D * 2u;
+  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + (uint64_t)b0 * hq * D, q_bytes);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, q_bytes);
+  const int grp = G >= 4 ? a.group : G;
+  const uint32_t qo_off =
+      lane_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * grp * D + r * 8) * 2u : kLaneOutOfRange;
+
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, group_row_off<G>(qo_off, g, grp, D));
+  u32x4 kr[SMAX];
+  u32x4 vr[SMAX];
+  const bool has = lane_ok && !bad && S > 0;
+  const uint64_t with_rows = __builtin_amdgcn_ballot_w64(has);
+  if (with_rows == 0) {
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) kr[j] = vr[j] = u32x4{0u, 0u, 0u, 0u};
+  } else {
+    const int32_t* pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+    const uint32_t shift = (uint32_t)a.seqlen_uniform;
+    const uint32_t mask = (1u << shift) - 1u;
+    const uint64_t page_stride = (uint64_t)a.batch_stride;
+    const uint64_t row_elems = (uint64_t)a.row_stride;
+    const uint64_t lane_elem = (uint64_t)hk * (uint64_t)a.head_stride + (uint64_t)r * 8u;
+    // Row 0 of the first lane group with a row, head 0, this lane's dims.
+    const int src = (int)__builtin_ctzll(with_rows);
+    const uint64_t own0 = has ? (uint64_t)(uint32_t)pages[0] * page_stride : 0u;
+    const uint32_t lo0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)own0, src);
+    const uint32_t hi0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(own0 >> 32), src);
+    const uint64_t safe = (((uint64_t)hi0 << 32) | lo0) + (uint64_t)r * 8u;
+    uint64_t off[SMAX];
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+      const bool ok = has && j < S;
+      const uint64_t page = (uint64_t)(uint32_t)pages[ok ? (uint32_t)j >> shift : 0u];
+      off[j] = ok ? page * page_stride + (uint64_t)((uint32_t)j & mask) * row_elems + lane_elem : safe;
+    }
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + off[j]));
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + off[j]));
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+      const bool ok = has && j < S;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        kr[j][k] = ok ? (uint32_t)kr[j][k] : 0u;
+        vr[j][k] = ok ? (uint32_t)vr[j][k] : 0u;
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  float acc[G][8];
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
+  const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    buffer_store16(o_rsrc, group_row_off<G>(qo_off, g, grp, D), bad ? nan4 : pack_f16x8(acc[g]));
+}
+
 // a.units_per_batch holds the batch count here, a.total_units the waves
-// (ceil(batch / R)); lengths from a.lens (packed: offsets, strided: lengths)
-// or a.seqlen_uniform when a.lens is null.
+// (ceil(batch / R)); lengths from a.lens (packed: offsets, strided and
+// paged: lengths) or a.seqlen_uniform when a.lens is null (not paged).
 template <int D, int G, int LAYOUT, bool PF32 = false>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(DecodeArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
   constexpr int VP = G * kMaxSeq;
@@ -712,10 +788,12 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(Decode
   const uint32_t b = b0 + (lane_ok ? (uint32_t)sub : 0u);
   const uint32_t row_bytes = (uint32_t)a.row_stride * 2u;
   int S;
-  const uint16_t* kbase;
-  const uint16_t* vbase;
-  uint32_t records, lane_rows;
-  if constexpr (LAYOUT == kLayoutPacked) {
+  const uint16_t* kbase = a.k;
+  const uint16_t* vbase = a.v;
+  uint32_t records = 0, lane_rows = 0;
+  if constexpr (LAYOUT == kLayoutPaged) {
+    S = a.lens[b];
+  } else if constexpr (LAYOUT == kLayoutPacked) {
     int32_t c0, ce, cb, cb1;
     if (a.lens) {
       c0 = a.lens[b0];
@@ -765,9 +843,12 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(Decode
   smax = __builtin_amdgcn_readfirstlane(smax);
   if constexpr (LAYOUT == kLayoutPacked) records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
   uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
-#define FMHA_DECODE_MULTI(SM)                                                                                  \
-  decode_multi_unit<D, G, SM, PF32>(a, b0, nb, kbase, vbase, records, lane_rows, S, bad, lane_ok, sub, hk, lane, \
-                                    lds_wave)
+#define FMHA_DECODE_MULTI(SM)                                                                                      \
+  if constexpr (LAYOUT == kLayoutPaged)                                                                              \
+    decode_multi_unit_paged<D, G, SM, PF32>(a, b0, nb, b, S, bad, lane_ok, sub, hk, lane, lds_wave);                \
+  else                                                                                                               \
+    decode_multi_unit<D, G, SM, PF32>(a, b0, nb, kbase, vbase, records, lane_rows, S, bad, lane_ok, sub, hk, lane, \
+                                      lds_wave)
   if (smax <= 1)
     FMHA_DECODE_MULTI(1);
   else if (smax <= 2)

@@ -145,3 +145,62 @@ def test_paged_bad_length_is_nan():
     o = fmha_amd.fmha_decode_paged(q, kc, kc, bt, lens).float()
     torch.cuda.synchronize()
     assert torch.isnan(o[0]).all() and torch.isfinite(o[1]).all()
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 16])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 8, 1), (128, 16, 2), (256, 4, 1), (128, 2, 2), (64, 20, 4)])
+def test_paged_few_kv_heads_batches_per_wave(page_size, D, Hq, Hkv):
+    """Fewer KV heads than a wave holds on a paged cache: the lane groups of
+    a wave serve different batches, each lane with its own page lookups and
+    addresses.  Block tables of 12 rows (below the 16-row bucket the longest
+    length picks), NaN in every slot no batch owns and -1 in unused
+    entries, empty batches, and a length beyond what the table addresses
+    (NaN for that batch only, its neighbours in the same wave exact); G = 8,
+    8, 4, 1, 5."""
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(page_size * 31 + D + Hq)
+    B = 37
+    cap = 12
+    rng = np.random.default_rng(page_size * 5 + D + Hq + Hkv)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[0] = cap
+    seqlens[5] = 0
+    ps_pages = (cap + page_size - 1) // page_size
+    need = [(int(s) + page_size - 1) // page_size for s in seqlens]
+    num_pages = sum(need) + 3
+    perm = rng.permutation(num_pages)
+    bt = np.full((B, ps_pages), -1, np.int32)
+    i = 0
+    for b in range(B):
+        for p in range(need[b]):
+            bt[b, p] = perm[i]
+            i += 1
+    kc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    rows_k, rows_v = [], []
+    for b in range(B):
+        for j in range(seqlens[b]):
+            page, slot = bt[b, j // page_size], j % page_size
+            kr, vr = _bf16(gen, (Hkv, D), dev), _bf16(gen, (Hkv, D), dev)
+            kc[page, slot], vc[page, slot] = kr, vr
+            rows_k.append(_bits(kr))
+            rows_v.append(_bits(vr))
+    bt_dev = torch.from_numpy(bt).to(dev)
+    o = fmha_amd.fmha_decode_paged(q, kc, vc, bt_dev, torch.from_numpy(seqlens).to(dev))
+    torch.cuda.synchronize()
+    _check(o, q, np.stack(rows_k), np.stack(rows_v), seqlens, Hq, Hkv, D, f"paged few heads ps={page_size} D={D}")
+    # A length beyond the rows the table addresses (its entries times the
+    # page size, at most 16): NaN for that batch only, nothing read.  (A
+    # length within them promises pages for its rows, which the kernels
+    # follow: 13 with one 16-row page per batch would send an empty batch's
+    # -1 entry to memory.)
+    bad = seqlens.copy()
+    bad[3] = min(16, ps_pages * page_size) + 1
+    o2 = fmha_amd.fmha_decode_paged(q, kc, vc, bt_dev, torch.from_numpy(bad).to(dev))
+    torch.cuda.synchronize()
+    assert torch.isnan(o2[3].float()).all()
+    keep = [b for b in range(B) if b != 3]
+    assert torch.equal(o2[keep].view(torch.int16), o[keep].view(torch.int16))
