@@ -17,19 +17,13 @@
 #include <cstring>
 
 #include "fmha_decode.h"
-#include "fmha_decode_group.hpp"
-#include "fmha_decode_kernel.hpp"
-#include "fmha_decode_onepass.hpp"
-#include "fmha_decode_splitkv.hpp"
-#include "fmha_decode_splitkv_group.hpp"
+#include "fmha_decode_launch.hpp"
 
 namespace {
 
-using fmha_decode::DecodeArgs;
-using fmha_decode::SplitArgs;
-using fmha_decode::kBlockThreads;
-using fmha_decode::kWaveSize;
-using fmha_decode::kWavesPerBlock;
+// Launchers and their instantiations: fmha_decode_launch.hpp,
+// fmha_decode_inst.hip.
+using namespace fmha_decode::host;
 
 thread_local char g_detail[256] = "";
 
@@ -43,108 +37,6 @@ int reject(int code, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Concurrency cap.  Each wave issues all of its loads at once, and MI355X
-// streams fastest with a bounded amount of them in flight per CU: measured
-// sweeps put the best at about 80 KiB for units of 10-36 KiB (3 waves of the
-// S=16, D=128 unit: 7.13 TB/s, against 6.63 TB/s uncapped; 6 waves of the
-// S=5, D=256 unit; 8 waves of the reference's Poisson(4) varlen unit).  Tiny
-// units (S=1) want every wave the registers allow.  The library reserves
-// unused LDS per workgroup so that only that many waves fit on a CU.
-constexpr int kInflightBytesPerCU = 80 * 1024;
-constexpr int kMaxWavesPerCU = 32;
-
-// Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
-// on a CU with `lds_per_cu` bytes (0 when no cap is needed).
-size_t lds_reserve_for(int waves, int lds_per_cu, size_t static_lds) {
-  if (waves >= kMaxWavesPerCU || lds_per_cu <= 0) return 0;
-  // Midway between the per-group share that fits `waves` groups and the one
-  // that would fit `waves + 1`, so allocation granularity cannot tip it.
-  const size_t hi = (size_t)lds_per_cu / waves;
-  const size_t lo = (size_t)lds_per_cu / (waves + 1);
-  const size_t per_group = (hi + lo) / 2;
-  return per_group > static_lds ? per_group - static_lds : 0;
-}
-
-// LDS bytes per CU of the current device, queried once per device.
-int lds_per_cu() {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> cache[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  const bool cacheable = dev >= 0 && dev < kMaxDevices;
-  if (cacheable) {
-    const int v = cache[dev].load(std::memory_order_relaxed);
-    if (v > 0) return v;
-  }
-  int bytes = 0;
-  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess) return 0;
-  if (cacheable) cache[dev].store(bytes, std::memory_order_relaxed);
-  return bytes;
-}
-
-// Static LDS of a kernel, queried once (a property of the code object).
-template <auto KERNEL>
-size_t static_lds() {
-  static const size_t bytes = [] {
-    hipFuncAttributes attr;
-    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(KERNEL)) == hipSuccess ? attr.sharedSizeBytes
-                                                                                           : size_t(0);
-  }();
-  return bytes;
-}
-
-// Dynamic LDS that caps KERNEL at `waves` one-wave workgroups per CU.
-template <auto KERNEL>
-size_t lds_reserve_kernel(int waves) {
-  return lds_reserve_for(waves, lds_per_cu(), static_lds<KERNEL>());
-}
-
-template <int D, int G, int LAYOUT, int SB, bool PF32>
-hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32>;
-  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
-  return hipGetLastError();
-}
-
-// sb: 0 = lengths from a.lens (bucket picked per wave), else the uniform
-// length's power-of-two bucket.  The paged layout always reads lengths.
-// PF32: fp32 softmax weights (instantiated for the packed layout only).
-template <int D, int G, int LAYOUT, bool PF32>
-hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
-  if constexpr (LAYOUT == fmha_decode::kLayoutPaged) {
-    return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
-  } else {
-    switch (sb) {
-      case 0: return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
-      case 1: return launch_one<D, G, LAYOUT, 1, PF32>(a, w, stream);
-      case 2: return launch_one<D, G, LAYOUT, 2, PF32>(a, w, stream);
-      case 4: return launch_one<D, G, LAYOUT, 4, PF32>(a, w, stream);
-      case 8: return launch_one<D, G, LAYOUT, 8, PF32>(a, w, stream);
-      default: return launch_one<D, G, LAYOUT, 16, PF32>(a, w, stream);
-    }
-  }
-}
-
-template <int D, int LAYOUT, bool PF32>
-hipError_t launch_group(const DecodeArgs& a, int g, int sb, int w, hipStream_t stream) {
-  switch (g) {
-    case 1: return launch_bucket<D, 1, LAYOUT, PF32>(a, sb, w, stream);
-    case 2: return launch_bucket<D, 2, LAYOUT, PF32>(a, sb, w, stream);
-    case 4: return launch_bucket<D, 4, LAYOUT, PF32>(a, sb, w, stream);
-    default: return launch_bucket<D, 8, LAYOUT, PF32>(a, sb, w, stream);
-  }
-}
-
-template <int LAYOUT, bool PF32 = false>
-hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStream_t stream) {
-  switch (d) {
-    case 64: return launch_group<64, LAYOUT, PF32>(a, g, sb, w, stream);
-    case 128: return launch_group<128, LAYOUT, PF32>(a, g, sb, w, stream);
-    default: return launch_group<256, LAYOUT, PF32>(a, g, sb, w, stream);
-  }
-}
-
 // Batches with fewer KV heads than a wave holds: the wave serves R = HPW /
 // Hkv batches (fmha_decode_multi_kernel).  Returns log2 R (0: not used).
 int multi_shift(int hkv, int dq) {
@@ -152,31 +44,6 @@ int multi_shift(int hkv, int dq) {
   int shift = 0;
   while ((hkv << (shift + 1)) <= hpw && hpw % (hkv << (shift + 1)) == 0) ++shift;
   return shift;
-}
-
-template <int D, int G, int LAYOUT, bool PF32>
-hipError_t launch_multi_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32>;
-  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
-  return hipGetLastError();
-}
-
-template <int LAYOUT, bool PF32>
-hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t stream) {
-#define FMHA_DECODE_MULTI_G(DD)                                                  \
-  switch (g) {                                                                   \
-    case 1: return launch_multi_one<DD, 1, LAYOUT, PF32>(a, w, stream);          \
-    case 2: return launch_multi_one<DD, 2, LAYOUT, PF32>(a, w, stream);          \
-    case 4: return launch_multi_one<DD, 4, LAYOUT, PF32>(a, w, stream);          \
-    default: return launch_multi_one<DD, 8, LAYOUT, PF32>(a, w, stream);         \
-  }
-  switch (d) {
-    case 64: FMHA_DECODE_MULTI_G(64)
-    case 128: FMHA_DECODE_MULTI_G(128)
-    default: FMHA_DECODE_MULTI_G(256)
-  }
-#undef FMHA_DECODE_MULTI_G
 }
 
 // G values the VALU kernel is instantiated for.
@@ -345,33 +212,6 @@ bool use_mfma_kernel(int g, int dq, int rows_hint) {
   return dq == 64 || g == 3;
 }
 
-template <int D, int NS, int LAYOUT>
-hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS, LAYOUT>;
-  hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
-  return hipGetLastError();
-}
-
-template <int D, int LAYOUT>
-hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int ns, int w, hipStream_t stream) {
-  switch (ns) {
-    case 1: return launch_mfma_one<D, 1, LAYOUT>(g, w, stream);
-    case 2: return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
-    default:
-      if constexpr (fmha_decode::GroupShape<D>::HPW >= 4) return launch_mfma_one<D, 4, LAYOUT>(g, w, stream);
-      else return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
-  }
-}
-
-template <int LAYOUT>
-hipError_t launch_mfma_layout(const fmha_decode::GroupArgs& g, int dq, int ns, int w, hipStream_t stream) {
-  switch (dq) {
-    case 64: return launch_mfma_d<64, LAYOUT>(g, ns, w, stream);
-    case 128: return launch_mfma_d<128, LAYOUT>(g, ns, w, stream);
-    default: return launch_mfma_d<256, LAYOUT>(g, ns, w, stream);
-  }
-}
-
 // Streams per 16-column query tile: 4 for G <= 4, 2 for G <= 8, else 1
 // (capped at the streams a wave holds).
 int mfma_streams_per_tile(int64_t g, int hpw) {
@@ -533,220 +373,6 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
   if (p.nchunks > 1) off += align_up(heads * (size_t)p.nchunks * d * 4);
   p.total = off;
   return p;
-}
-
-// Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
-// Scores waves request 16 KiB of K plus G KiB of Q at once; P.V waves keep
-// two 16-row (8-row for G = 8) sub-blocks of V in flight.  Sweeps over
-// long-context shapes (B=64 S=4096, B=8 S=32768, B=256 S=1024 G=8, B=1
-// S=131072) put both optima at 8 (4-6 cost 2-5%, 12-16 within 1%).
-constexpr int kSplitScoresWavesPerCU = 8;
-constexpr int kSplitPvWavesPerCU = 8;
-
-// Rows longer than 16 go through one pass (onepass_decode_kernel: one wave
-// per batch and head group, no workspace traffic, one launch) when there are
-// at least 512 such units and the row's scores and weights fit the wave's
-// LDS budget; otherwise through the four split-KV launches.  Measured
-// (µs, split -> one pass, 8 waves per CU): B=2048 Hq=32 Hkv=8 S=128 201 ->
-// 171; B=4096 S=64 206 -> 178; B=16384 S=24 327 -> 296; B=256 S=256 (512
-// units) 69 -> 58; B=128 S=256 (256 units) 43 -> 49 and B=16 S=256 23 -> 49,
-// where a wave's walk over its row outlasts split-KV's shorter waves.
-constexpr int64_t kOnepassMinUnits = 512;
-constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
-constexpr int kOnepassWavesPerCU = 8;
-
-// Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
-// the KV-head groups of one.
-int64_t onepass_waves(const SplitArgs& a) {
-  return (((int64_t)a.batch + (1 << a.sub_shift) - 1) >> a.sub_shift) * a.units_per_batch;
-}
-
-template <int D, int G>
-bool onepass_fits(const SplitArgs& a) {
-  return onepass_waves(a) >= kOnepassMinUnits &&
-         fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
-}
-
-template <int D, int G, int LAYOUT, bool MULTI>
-hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>;
-  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
-  const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
-  hipLaunchKernelGGL(kernel, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
-                     a);
-  return hipGetLastError();
-}
-
-// Pass 2 of split-KV: the global max and sum per (batch, query head).  One
-// lane per head for rows of at most 16 blocks, else one workgroup per head
-// sized to the row's block count (8 blocks per thread and round).
-void launch_split_stats(const SplitArgs& a, hipStream_t stream) {
-  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
-  if (a.nblk <= 16)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_lane_kernel, dim3((heads + 255) / 256), dim3(256), 0, stream, a);
-  else if (a.nblk <= 8 * 64)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<64>, dim3(heads), dim3(64), 0, stream, a);
-  else if (a.nblk <= 8 * 256)
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<256>, dim3(heads), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
-}
-
-// Pass 4 of split-KV (more than one chunk per row): partial outputs summed
-// in chunk order, one lane per 8 dims for few chunks, else a workgroup per
-// (head, 32 dims).
-template <int D>
-void launch_split_combine(const SplitArgs& a, hipStream_t stream) {
-  const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
-  if (a.nchunks <= 16) {
-    const uint64_t lanes = (uint64_t)heads * (D / 8);
-    hipLaunchKernelGGL(fmha_decode::splitkv_combine_kernel<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
-                       stream, a);
-  } else if (a.nchunks <= 256) {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 256>), dim3(heads * (D / 32)), dim3(256), 0,
-                       stream, a);
-  } else {
-    hipLaunchKernelGGL((fmha_decode::splitkv_combine_block_kernel<D, 1024>), dim3(heads * (D / 32)), dim3(1024), 0,
-                       stream, a);
-  }
-}
-
-// LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
-template <int D, int G, int LAYOUT>
-hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
-  // With fewer KV heads than a wave holds, its lane groups serve 2^shift
-  // batches (single pass), blocks (scores) or chunks (P.V) instead of
-  // idling: packed and strided layouts, whose descriptor spans the rows
-  // (the paged ones address one page at a time).
-  constexpr int HPW = kWaveSize / (D / 8);
-  constexpr bool LANES = LAYOUT == fmha_decode::kLayoutPagedLanes || LAYOUT == fmha_decode::kLayoutPagedBlockLanes;
-  int shift = 0;
-  if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
-    while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
-  // The single pass spans 2^shift batches with one descriptor: for the
-  // strided layout only when their span stays below 1 GiB.  Paged layouts
-  // run it with one batch and one page descriptor per wave, which leaves
-  // the lanes of missing KV heads idle: at D = 64 and 128 the split passes,
-  // whose lane groups take their own blocks and chunks, measured faster
-  // (16-row pages, B=2048 S=128 D=128: Hq/Hkv 8/1 129.3 -> 58.2 µs, 16/2
-  // 131.8 -> 85.3), at D = 256 (two heads per wave) the single pass (B=4096
-  // S=64 4/1: 55.8 against 86.1).
-  if (!LANES || D == 256) {
-    SplitArgs ao = a;
-    ao.sub_shift = LANES ? 0 : shift;
-    if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
-      const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
-                            (int64_t)(fmha_decode::kv_heads_mem(a) - 1) * a.head_stride + D) * 2;
-      if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
-    }
-    ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
-    if (onepass_fits<D, G>(ao)) {
-      if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
-        if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
-      constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
-                         : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
-                                                                         : LAYOUT;
-      return launch_onepass_dg<D, G, OL, false>(ao, stream);
-    }
-  }
-  // The combine grid has one workgroup per (batch, query head, 32 dims).
-  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
-  constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
-  // One block per scores wave otherwise (two measured 1-3% slower).
-  SplitArgs as = a;
-  as.sub_shift = shift;
-  as.units_per_batch = (a.num_heads_kv + (HPW >> shift) - 1) / (HPW >> shift);
-  const uint32_t upb = (uint32_t)as.units_per_batch;
-  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + (1 << shift) - 1) >> shift) * upb;
-  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)((a.nchunks + (1 << shift) - 1) >> shift) * upb;
-  {
-    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, as);
-  }
-  launch_split_stats(a, stream);
-  if (a.nchunks == 1) {
-    // One chunk per batch: the P.V wave writes O itself, one chunk per wave.
-    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
-    const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
-    hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
-                       stream, a);
-    return hipGetLastError();
-  }
-  {
-    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
-                       stream, as);
-  }
-  launch_split_combine<D>(a, stream);
-  return hipGetLastError();
-}
-
-template <int D, int LAYOUT>
-hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream) {
-  switch (g) {
-    case 1: return launch_split_dg<D, 1, LAYOUT>(a, stream);
-    case 2: return launch_split_dg<D, 2, LAYOUT>(a, stream);
-    case 4: return launch_split_dg<D, 4, LAYOUT>(a, stream);
-    default: return launch_split_dg<D, 8, LAYOUT>(a, stream);
-  }
-}
-
-template <int LAYOUT>
-hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t stream) {
-  switch (d) {
-    case 64: return launch_split_d<64, LAYOUT>(a, g, stream);
-    case 128: return launch_split_d<128, LAYOUT>(a, g, stream);
-    default: return launch_split_d<256, LAYOUT>(a, g, stream);
-  }
-}
-
-// Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
-// are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
-// size.  Scores, stats, P.V (O directly with one chunk per row), combine.
-// P.V waves take TW tiles of 16 query heads, their accumulators TW * D/16 *
-// 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
-template <int D, int LAYOUT>
-hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
-  constexpr int HPW = kWaveSize / (D / 8);
-  constexpr int TW = D == 256 ? 1 : 2;
-  const int64_t g = a.num_heads_q / a.num_heads_kv;
-  const int64_t tiles = (g + 15) / 16;
-  const int64_t tc = (tiles + TW - 1) / TW;
-  const int64_t score_waves = (int64_t)a.batch * ((a.nblk + HPW - 1) / HPW) * a.num_heads_kv;
-  const int64_t units = (int64_t)a.batch * a.nchunks * a.num_heads_kv;
-  const int64_t pv_waves = (units + 7) / 8 * 8 * tc;
-  if (score_waves > INT32_MAX || pv_waves > INT32_MAX ||
-      (uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX)
-    return hipErrorInvalidValue;
-  {
-    constexpr auto kernel = fmha_decode::splitkv_scores_group_kernel<D, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
-  }
-  launch_split_stats(a, stream);
-  if (a.nchunks == 1) {
-    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, true, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
-    return hipGetLastError();
-  }
-  {
-    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, false, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
-  }
-  launch_split_combine<D>(a, stream);
-  return hipGetLastError();
-}
-
-template <int LAYOUT>
-hipError_t launch_split_group_layout(const SplitArgs& a, int d, hipStream_t stream) {
-  switch (d) {
-    case 64: return launch_split_group_d<64, LAYOUT>(a, stream);
-    case 128: return launch_split_group_d<128, LAYOUT>(a, stream);
-    default: return launch_split_group_d<256, LAYOUT>(a, stream);
-  }
 }
 
 }  // namespace
@@ -1080,19 +706,14 @@ int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int3
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint64_t streams = (uint64_t)batch * (uint64_t)hkv;
   const uint64_t pad_chunks = streams * (uint64_t)gp * (uint64_t)(d / 8);
-  const uint64_t pad_blocks = (pad_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
-  if (pad_blocks > (uint64_t)INT32_MAX) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
-  const uint64_t out_blocks =
-      (streams * (uint64_t)g * (uint64_t)(d / 8) + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads;
-  hipLaunchKernelGGL(fmha_decode::pad_query_group_kernel, dim3((uint32_t)pad_blocks), dim3(fmha_decode::kPadThreads),
-                     0, st, static_cast<const uint16_t*>(Q), qp, streams, g, 0, g, gp, d);
-  hipError_t err = hipGetLastError();
+  // The output copy has G <= GP rows per stream: fewer blocks than the input copy.
+  if ((pad_chunks + fmha_decode::kPadThreads - 1) / fmha_decode::kPadThreads > (uint64_t)INT32_MAX)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "batch too large (%d)", batch);
+  hipError_t err = launch_pad_query_group(static_cast<const uint16_t*>(Q), qp, streams, g, gp, d, st);
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   const int rc = body(qp, op, hkv * gp, hkv * ns, ns, ws + 2 * pb, workspace_bytes - 2 * pb);
   if (rc != FMHA_DECODE_SUCCESS) return rc;
-  hipLaunchKernelGGL(fmha_decode::unpad_output_group_kernel, dim3((uint32_t)out_blocks),
-                     dim3(fmha_decode::kPadThreads), 0, st, op, static_cast<uint16_t*>(O), streams, g, 0, g, gp, d);
-  err = hipGetLastError();
+  err = launch_unpad_output_group(op, static_cast<uint16_t*>(O), streams, g, gp, d, st);
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
 }

@@ -460,6 +460,9 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
 // ---------------------------------------------------------------------------
 constexpr int kPadThreads = 256;
 
+// Defined in one translation unit only (FMHA_DECODE_SHARED_KERNELS): they
+// are not templates, so every other one must not emit them again.
+#ifdef FMHA_DECODE_SHARED_KERNELS
 __global__ __launch_bounds__(kPadThreads) void pad_query_group_kernel(const uint16_t* q, uint16_t* qp,
                                                                        uint64_t streams, int G, int g0, int gn,
                                                                        int GP, int D) {
@@ -488,5 +491,6 @@ __global__ __launch_bounds__(kPadThreads) void unpad_output_group_kernel(const u
   *reinterpret_cast<u32x4*>(o + ((sigma * (uint64_t)G + g0 + g) * D + c * 8)) =
       *reinterpret_cast<const u32x4*>(op + ((sigma * (uint64_t)GP + g) * D + c * 8));
 }
+#endif  // FMHA_DECODE_SHARED_KERNELS
 
 }  // namespace fmha_decode

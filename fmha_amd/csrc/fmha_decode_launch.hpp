@@ -1,0 +1,438 @@
+// fmha_decode_launch.hpp -- host-side launchers of the decode kernels.
+//
+// Shared by fmha_decode_api.hip (argument checks, plans and kernel choice
+// behind the C ABI) and fmha_decode_inst.hip, which is compiled once per
+// part (FMHA_DECODE_PART): each part explicitly instantiates one slice of
+// the launchers below, and with them their kernels, so that the library's
+// few hundred kernel instantiations compile in parallel.  The extern
+// template declarations at the end keep every other translation unit from
+// instantiating them again.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+
+#include "fmha_decode_group.hpp"
+#include "fmha_decode_kernel.hpp"
+#include "fmha_decode_onepass.hpp"
+#include "fmha_decode_splitkv.hpp"
+#include "fmha_decode_splitkv_group.hpp"
+
+namespace fmha_decode {
+namespace host {
+
+using fmha_decode::DecodeArgs;
+using fmha_decode::SplitArgs;
+using fmha_decode::kBlockThreads;
+using fmha_decode::kWaveSize;
+using fmha_decode::kWavesPerBlock;
+
+// Concurrency cap.  Each wave issues all of its loads at once, and MI355X
+// streams fastest with a bounded amount of them in flight per CU: measured
+// sweeps put the best at about 80 KiB for units of 10-36 KiB (3 waves of the
+// S=16, D=128 unit: 7.13 TB/s, against 6.63 TB/s uncapped; 6 waves of the
+// S=5, D=256 unit; 8 waves of the reference's Poisson(4) varlen unit).  Tiny
+// units (S=1) want every wave the registers allow.  The library reserves
+// unused LDS per workgroup so that only that many waves fit on a CU.
+constexpr int kInflightBytesPerCU = 80 * 1024;
+constexpr int kMaxWavesPerCU = 32;
+
+// Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
+// on a CU with `lds_per_cu` bytes (0 when no cap is needed).
+inline size_t lds_reserve_for(int waves, int lds_per_cu, size_t static_lds) {
+  if (waves >= kMaxWavesPerCU || lds_per_cu <= 0) return 0;
+  // Midway between the per-group share that fits `waves` groups and the one
+  // that would fit `waves + 1`, so allocation granularity cannot tip it.
+  const size_t hi = (size_t)lds_per_cu / waves;
+  const size_t lo = (size_t)lds_per_cu / (waves + 1);
+  const size_t per_group = (hi + lo) / 2;
+  return per_group > static_lds ? per_group - static_lds : 0;
+}
+
+// LDS bytes per CU of the current device, queried once per device.
+inline int lds_per_cu() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cacheable = dev >= 0 && dev < kMaxDevices;
+  if (cacheable) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int bytes = 0;
+  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess) return 0;
+  if (cacheable) cache[dev].store(bytes, std::memory_order_relaxed);
+  return bytes;
+}
+
+// Static LDS of a kernel, queried once (a property of the code object).
+template <auto KERNEL>
+size_t static_lds() {
+  static const size_t bytes = [] {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(KERNEL)) == hipSuccess ? attr.sharedSizeBytes
+                                                                                           : size_t(0);
+  }();
+  return bytes;
+}
+
+// Dynamic LDS that caps KERNEL at `waves` one-wave workgroups per CU.
+template <auto KERNEL>
+size_t lds_reserve_kernel(int waves) {
+  return lds_reserve_for(waves, lds_per_cu(), static_lds<KERNEL>());
+}
+
+template <int D, int G, int LAYOUT, int SB, bool PF32>
+hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32>;
+  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
+  return hipGetLastError();
+}
+
+// sb: 0 = lengths from a.lens (bucket picked per wave), else the uniform
+// length's power-of-two bucket.  The paged layout always reads lengths.
+// PF32: fp32 softmax weights (instantiated for the packed layout only).
+template <int D, int G, int LAYOUT, bool PF32>
+hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
+  if constexpr (LAYOUT == fmha_decode::kLayoutPaged) {
+    return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
+  } else {
+    switch (sb) {
+      case 0: return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
+      case 1: return launch_one<D, G, LAYOUT, 1, PF32>(a, w, stream);
+      case 2: return launch_one<D, G, LAYOUT, 2, PF32>(a, w, stream);
+      case 4: return launch_one<D, G, LAYOUT, 4, PF32>(a, w, stream);
+      case 8: return launch_one<D, G, LAYOUT, 8, PF32>(a, w, stream);
+      default: return launch_one<D, G, LAYOUT, 16, PF32>(a, w, stream);
+    }
+  }
+}
+
+template <int D, int LAYOUT, bool PF32>
+hipError_t launch_group(const DecodeArgs& a, int g, int sb, int w, hipStream_t stream) {
+  switch (g) {
+    case 1: return launch_bucket<D, 1, LAYOUT, PF32>(a, sb, w, stream);
+    case 2: return launch_bucket<D, 2, LAYOUT, PF32>(a, sb, w, stream);
+    case 4: return launch_bucket<D, 4, LAYOUT, PF32>(a, sb, w, stream);
+    default: return launch_bucket<D, 8, LAYOUT, PF32>(a, sb, w, stream);
+  }
+}
+
+template <int LAYOUT, bool PF32 = false>
+hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_group<64, LAYOUT, PF32>(a, g, sb, w, stream);
+    case 128: return launch_group<128, LAYOUT, PF32>(a, g, sb, w, stream);
+    default: return launch_group<256, LAYOUT, PF32>(a, g, sb, w, stream);
+  }
+}
+
+template <int D, int G, int LAYOUT, bool PF32>
+hipError_t launch_multi_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32>;
+  const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
+  return hipGetLastError();
+}
+
+template <int LAYOUT, bool PF32>
+hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t stream) {
+#define FMHA_DECODE_MULTI_G(DD)                                                  \
+  switch (g) {                                                                   \
+    case 1: return launch_multi_one<DD, 1, LAYOUT, PF32>(a, w, stream);          \
+    case 2: return launch_multi_one<DD, 2, LAYOUT, PF32>(a, w, stream);          \
+    case 4: return launch_multi_one<DD, 4, LAYOUT, PF32>(a, w, stream);          \
+    default: return launch_multi_one<DD, 8, LAYOUT, PF32>(a, w, stream);         \
+  }
+  switch (d) {
+    case 64: FMHA_DECODE_MULTI_G(64)
+    case 128: FMHA_DECODE_MULTI_G(128)
+    default: FMHA_DECODE_MULTI_G(256)
+  }
+#undef FMHA_DECODE_MULTI_G
+}
+
+template <int D, int NS, int LAYOUT>
+hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS, LAYOUT>;
+  hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
+  return hipGetLastError();
+}
+
+template <int D, int LAYOUT>
+hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int ns, int w, hipStream_t stream) {
+  switch (ns) {
+    case 1: return launch_mfma_one<D, 1, LAYOUT>(g, w, stream);
+    case 2: return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
+    default:
+      if constexpr (fmha_decode::GroupShape<D>::HPW >= 4) return launch_mfma_one<D, 4, LAYOUT>(g, w, stream);
+      else return launch_mfma_one<D, 2, LAYOUT>(g, w, stream);
+  }
+}
+
+template <int LAYOUT>
+hipError_t launch_mfma_layout(const fmha_decode::GroupArgs& g, int dq, int ns, int w, hipStream_t stream) {
+  switch (dq) {
+    case 64: return launch_mfma_d<64, LAYOUT>(g, ns, w, stream);
+    case 128: return launch_mfma_d<128, LAYOUT>(g, ns, w, stream);
+    default: return launch_mfma_d<256, LAYOUT>(g, ns, w, stream);
+  }
+}
+
+// Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
+// Scores waves request 16 KiB of K plus G KiB of Q at once; P.V waves keep
+// two 16-row (8-row for G = 8) sub-blocks of V in flight.  Sweeps over
+// long-context shapes (B=64 S=4096, B=8 S=32768, B=256 S=1024 G=8, B=1
+// S=131072) put both optima at 8 (4-6 cost 2-5%, 12-16 within 1%).
+constexpr int kSplitScoresWavesPerCU = 8;
+constexpr int kSplitPvWavesPerCU = 8;
+
+// Rows longer than 16 go through one pass (onepass_decode_kernel: one wave
+// per batch and head group, no workspace traffic, one launch) when there are
+// at least 512 such units and the row's scores and weights fit the wave's
+// LDS budget; otherwise through the four split-KV launches.  Measured
+// (µs, split -> one pass, 8 waves per CU): B=2048 Hq=32 Hkv=8 S=128 201 ->
+// 171; B=4096 S=64 206 -> 178; B=16384 S=24 327 -> 296; B=256 S=256 (512
+// units) 69 -> 58; B=128 S=256 (256 units) 43 -> 49 and B=16 S=256 23 -> 49,
+// where a wave's walk over its row outlasts split-KV's shorter waves.
+constexpr int64_t kOnepassMinUnits = 512;
+constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
+constexpr int kOnepassWavesPerCU = 8;
+
+// Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
+// the KV-head groups of one.
+inline int64_t onepass_waves(const SplitArgs& a) {
+  return (((int64_t)a.batch + (1 << a.sub_shift) - 1) >> a.sub_shift) * a.units_per_batch;
+}
+
+template <int D, int G>
+bool onepass_fits(const SplitArgs& a) {
+  return onepass_waves(a) >= kOnepassMinUnits &&
+         fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
+}
+
+template <int D, int G, int LAYOUT, bool MULTI>
+hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
+  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>;
+  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
+  const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
+  hipLaunchKernelGGL(kernel, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
+                     a);
+  return hipGetLastError();
+}
+
+
+// Launchers of the kernels every long-row path shares, defined once in the
+// part that owns them (fmha_decode_inst.hip, FMHA_DECODE_PART 0).
+// Pass 2 of split-KV: the global max and sum per (batch, query head).
+void launch_split_stats(const SplitArgs& a, hipStream_t stream);
+// Pass 4 of split-KV (more than one chunk per row): the partial outputs
+// summed in chunk order.
+void launch_split_combine(const SplitArgs& a, int d, hipStream_t stream);
+// Q rows copied to, and O rows back from, a query group padded to GP rows
+// per (batch, KV head) stream (fmha_decode_group.hpp).
+hipError_t launch_pad_query_group(const uint16_t* q, uint16_t* qp, uint64_t streams, int G, int GP, int D,
+                                  hipStream_t stream);
+hipError_t launch_unpad_output_group(const uint16_t* op, uint16_t* o, uint64_t streams, int G, int GP, int D,
+                                     hipStream_t stream);
+
+// LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
+template <int D, int G, int LAYOUT>
+hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
+  // With fewer KV heads than a wave holds, its lane groups serve 2^shift
+  // batches (single pass), blocks (scores) or chunks (P.V) instead of
+  // idling: packed and strided layouts, whose descriptor spans the rows
+  // (the paged ones address one page at a time).
+  constexpr int HPW = kWaveSize / (D / 8);
+  constexpr bool LANES = LAYOUT == fmha_decode::kLayoutPagedLanes || LAYOUT == fmha_decode::kLayoutPagedBlockLanes;
+  int shift = 0;
+  if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
+    while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
+  // The single pass spans 2^shift batches with one descriptor: for the
+  // strided layout only when their span stays below 1 GiB.  Paged layouts
+  // run it with one batch and one page descriptor per wave, which leaves
+  // the lanes of missing KV heads idle: at D = 64 and 128 the split passes,
+  // whose lane groups take their own blocks and chunks, measured faster
+  // (16-row pages, B=2048 S=128 D=128: Hq/Hkv 8/1 129.3 -> 58.2 µs, 16/2
+  // 131.8 -> 85.3), at D = 256 (two heads per wave) the single pass (B=4096
+  // S=64 4/1: 55.8 against 86.1).
+  if (!LANES || D == 256) {
+    SplitArgs ao = a;
+    ao.sub_shift = LANES ? 0 : shift;
+    if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
+      const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
+                            (int64_t)(fmha_decode::kv_heads_mem(a) - 1) * a.head_stride + D) * 2;
+      if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
+    }
+    ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
+    if (onepass_fits<D, G>(ao)) {
+      if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+        if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
+      constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
+                         : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
+                                                                         : LAYOUT;
+      return launch_onepass_dg<D, G, OL, false>(ao, stream);
+    }
+  }
+  // The combine grid has one workgroup per (batch, query head, 32 dims).
+  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
+  constexpr int NR = G >= 8 ? 8 : 16;  // P.V sub-block rows (register budget)
+  // One block per scores wave otherwise (two measured 1-3% slower).
+  SplitArgs as = a;
+  as.sub_shift = shift;
+  as.units_per_batch = (a.num_heads_kv + (HPW >> shift) - 1) / (HPW >> shift);
+  const uint32_t upb = (uint32_t)as.units_per_batch;
+  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + (1 << shift) - 1) >> shift) * upb;
+  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)((a.nchunks + (1 << shift) - 1) >> shift) * upb;
+  {
+    constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, as);
+  }
+  launch_split_stats(a, stream);
+  if (a.nchunks == 1) {
+    // One chunk per batch: the P.V wave writes O itself, one chunk per wave.
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
+    const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
+    hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
+                       stream, a);
+    return hipGetLastError();
+  }
+  {
+    constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
+                       stream, as);
+  }
+  launch_split_combine(a, D, stream);
+  return hipGetLastError();
+}
+
+template <int D, int LAYOUT>
+hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream) {
+  switch (g) {
+    case 1: return launch_split_dg<D, 1, LAYOUT>(a, stream);
+    case 2: return launch_split_dg<D, 2, LAYOUT>(a, stream);
+    case 4: return launch_split_dg<D, 4, LAYOUT>(a, stream);
+    default: return launch_split_dg<D, 8, LAYOUT>(a, stream);
+  }
+}
+
+template <int LAYOUT>
+hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_split_d<64, LAYOUT>(a, g, stream);
+    case 128: return launch_split_d<128, LAYOUT>(a, g, stream);
+    default: return launch_split_d<256, LAYOUT>(a, g, stream);
+  }
+}
+
+// Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
+// are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
+// size.  Scores, stats, P.V (O directly with one chunk per row), combine.
+// P.V waves take TW tiles of 16 query heads, their accumulators TW * D/16 *
+// 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
+template <int D, int LAYOUT>
+hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
+  constexpr int HPW = kWaveSize / (D / 8);
+  constexpr int TW = D == 256 ? 1 : 2;
+  const int64_t g = a.num_heads_q / a.num_heads_kv;
+  const int64_t tiles = (g + 15) / 16;
+  const int64_t tc = (tiles + TW - 1) / TW;
+  const int64_t score_waves = (int64_t)a.batch * ((a.nblk + HPW - 1) / HPW) * a.num_heads_kv;
+  const int64_t units = (int64_t)a.batch * a.nchunks * a.num_heads_kv;
+  const int64_t pv_waves = (units + 7) / 8 * 8 * tc;
+  if (score_waves > INT32_MAX || pv_waves > INT32_MAX ||
+      (uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX)
+    return hipErrorInvalidValue;
+  {
+    constexpr auto kernel = fmha_decode::splitkv_scores_group_kernel<D, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
+  }
+  launch_split_stats(a, stream);
+  if (a.nchunks == 1) {
+    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, true, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+    return hipGetLastError();
+  }
+  {
+    constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, false, LAYOUT>;
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+  }
+  launch_split_combine(a, D, stream);
+  return hipGetLastError();
+}
+
+template <int LAYOUT>
+hipError_t launch_split_group_layout(const SplitArgs& a, int d, hipStream_t stream) {
+  switch (d) {
+    case 64: return launch_split_group_d<64, LAYOUT>(a, stream);
+    case 128: return launch_split_group_d<128, LAYOUT>(a, stream);
+    default: return launch_split_group_d<256, LAYOUT>(a, stream);
+  }
+}
+
+// Explicitly instantiated in fmha_decode_inst.hip (one part each).
+#ifndef FMHA_DECODE_INSTANTIATING
+extern template hipError_t launch_group<64, kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<64, kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<64, kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<64, kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<128, kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<128, kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<128, kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<128, kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<256, kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<256, kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<256, kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_group<256, kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_multi<kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_multi<kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_multi<kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_multi<kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<64, kLayoutPacked>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<64, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<128, kLayoutPacked>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<128, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<256, kLayoutPacked>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_mfma_d<256, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<128, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<256, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_group_d<64, kLayoutPacked>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<64, kLayoutStrided>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<64, kLayoutPaged>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<64, kLayoutPagedBlock>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<128, kLayoutPacked>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<128, kLayoutStrided>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<128, kLayoutPaged>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<128, kLayoutPagedBlock>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<256, kLayoutPacked>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<256, kLayoutStrided>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<256, kLayoutPaged>(const SplitArgs&, hipStream_t);
+extern template hipError_t launch_split_group_d<256, kLayoutPagedBlock>(const SplitArgs&, hipStream_t);
+#endif
+
+}  // namespace host
+}  // namespace fmha_decode

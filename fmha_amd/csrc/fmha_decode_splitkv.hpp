@@ -528,6 +528,7 @@ __device__ __forceinline__ float block_reduce(float x, float* red) {
 // over the row's 16-row blocks.
 // ---------------------------------------------------------------------------
 // Rows of at most 16 blocks: one lane per head, all loads in flight.
+#ifdef FMHA_DECODE_SHARED_KERNELS  // one translation unit emits it (not a template)
 __global__ __launch_bounds__(256) void splitkv_stats_lane_kernel(SplitArgs a) {
   constexpr int NB = 16;
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // b * Hq + h
@@ -553,6 +554,7 @@ __global__ __launch_bounds__(256) void splitkv_stats_lane_kernel(SplitArgs a) {
   a.ml[2 * i] = gm;
   a.ml[2 * i + 1] = gl;
 }
+#endif  // FMHA_DECODE_SHARED_KERNELS
 
 // Longer rows: one THREADS-thread group per head, U loads in flight per
 // thread, reduction order fixed.
