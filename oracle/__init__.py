@@ -47,7 +47,7 @@ def lib():
         L.oracle_decode.restype = ctypes.c_int
         L.oracle_decode.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f32, i32, vp, vp, f64, i32, i32]
         L.oracle_decode_f64.restype = ctypes.c_int
-        L.oracle_decode_f64.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f64, vp, i32, i32]
+        L.oracle_decode_f64.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, f64, vp, i32, i32, vp]
         L.oracle_compare.restype = None
         L.oracle_compare.argtypes = [vp, vp, vp, i64, f64, f64, vp]
         L.oracle_generate_seqlens.restype = None
@@ -68,10 +68,14 @@ def _u16(a):
 
 
 def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps=SLACK_EPS,
-           nthreads=0, max_seqlen=16):
+           nthreads=0, max_seqlen=16, slack_fixed=False):
     """Restated reference loop.  q [B,Hq,D], k/v [rows,Hkv,D] as uint16 bf16
     bits; cu int32 [B+1]; lengths up to max_seqlen (the reference's 16 by
-    default).  Returns (o fp16 bits [B,Hq,D], slack or None)."""
+    default).  Returns (o fp16 bits [B,Hq,D], slack or None).  The slack's
+    half-width is max(slack_eps, 4x the oracle's own float32 error) per head,
+    or exactly slack_eps with slack_fixed."""
+    if slack_fixed:
+        slack_eps = -abs(slack_eps)
     q, k, v = _u16(q), _u16(k), _u16(v)
     cu = np.ascontiguousarray(cu, dtype=np.int32)
     B = cu.shape[0] - 1
@@ -85,18 +89,22 @@ def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps
     return o, slack
 
 
-def decode_f64(q, k, v, cu, hq, hkv, d, scale, nthreads=0, max_seqlen=16):
-    """Float64 decode attention; returns float64 [B,Hq,D]."""
+def decode_f64(q, k, v, cu, hq, hkv, d, scale, nthreads=0, max_seqlen=16, with_bound=False):
+    """Float64 decode attention; returns float64 [B,Hq,D], or (that, bound)
+    with with_bound: the per-element bound on |o - t| that a bf16-weight
+    float32 implementation meets without tie slack (head_f64 in
+    fmha_oracle.cpp)."""
     q, k, v = _u16(q), _u16(k), _u16(v)
     cu = np.ascontiguousarray(cu, dtype=np.int32)
     B = cu.shape[0] - 1
     o = np.empty((B, hq, d), dtype=np.float64)
+    bound = np.empty((B, hq, d), dtype=np.float64) if with_bound else None
     nt = nthreads if nthreads > 0 else (os.cpu_count() or 1)
     rc = lib().oracle_decode_f64(_p(q), _p(k), _p(v), _p(cu), B, hq, hkv, d, float(scale), _p(o), nt,
-                                 max_seqlen)
+                                 max_seqlen, _p(bound))
     if rc != 0:
         raise ValueError("oracle_decode_f64 rejected its arguments")
-    return o
+    return (o, bound) if with_bound else o
 
 
 def compare(o, r, slack=None, atol=2e-3, rtol=1e-2):
@@ -161,7 +169,8 @@ def ref_lib():
         R.ref_generate_seqlens.argtypes = [i32, i32, vp]
         R.ref_do_validation.restype = ctypes.c_int
         R.ref_do_validation.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp]
-        for name in ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma"):
+        for name in ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma", "ref_launch_mfma",
+                     "ref_launch_mfma_v3"):
             fn = getattr(R, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32]

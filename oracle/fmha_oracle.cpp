@@ -30,6 +30,18 @@
 #include <random>
 #include <vector>
 
+// Planted mistakes for the oracle's own mutation tests: tests/test_oracle.py
+// compiles copies of this file with ORACLE_MUTANT set to 1..4 and checks
+// that its long-row checks reject every one.  The oracle the tests use is
+// built without it (0: no mistake).
+//   1: rows 16 and beyond score against the previous row's K;
+//   2: P.V drops the last row of rows longer than 16;
+//   3: the max runs over the first 16 rows only;
+//   4: the sum of exponentials runs over the first 16 rows only.
+#ifndef ORACLE_MUTANT
+#define ORACLE_MUTANT 0
+#endif
+
 namespace {
 
 inline float bf16_to_f32(uint16_t h) {
@@ -97,17 +109,19 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   p_buf.resize(S > 16 ? S : 16);
   jump_buf.resize(S > 16 ? S : 16);
   float* scores = scores_buf.data();
+  const int S16 = S < 16 ? S : 16;
+  (void)S16;
   for (int s = 0; s < S; s++) {
     float sum = 0;
-    const uint16_t* kr = k + (int64_t)s * kv_stride;
+    const uint16_t* kr = k + (int64_t)((ORACLE_MUTANT == 1 && s >= 16) ? s - 1 : s) * kv_stride;
     for (int d = 0; d < D; d++) sum += bf16_to_f32(q[d]) * bf16_to_f32(kr[d]);
     scores[s] = sum;
   }
   for (int s = 0; s < S; s++) scores[s] *= scale;
   float maxv = -INFINITY;
-  for (int s = 0; s < S; s++) maxv = fmaxf(maxv, scores[s]);
+  for (int s = 0; s < (ORACLE_MUTANT == 3 ? S16 : S); s++) maxv = fmaxf(maxv, scores[s]);
   float sum_exp = 0.0f;
-  for (int s = 0; s < S; s++) sum_exp += expf(scores[s] - maxv);
+  for (int s = 0; s < (ORACLE_MUTANT == 4 ? S16 : S); s++) sum_exp += expf(scores[s] - maxv);
   float* p = p_buf.data();
   float* jump = jump_buf.data();
   // How far this loop's own float32 weights may sit from the exact ones:
@@ -117,8 +131,9 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   // order is uncertain by about as much, so a weight within
   // eps = max(slack_eps, 4 * that) of a bf16 rounding midpoint may round
   // either way there.
-  double eps = slack_eps;
-  if (slack) {
+  // A negative slack_eps asks for the fixed half-width |slack_eps| instead.
+  double eps = slack_eps < 0 ? -slack_eps : slack_eps;
+  if (slack && slack_eps > 0) {
     double dt = 0.0, l64 = 0.0;
     for (int s = 0; s < S; s++) {
       double acc = 0.0;
@@ -144,7 +159,7 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   for (int d = 0; d < D; d++) {
     float sum = 0;
     float sl = 0;
-    for (int s = 0; s < S; s++) {
+    for (int s = 0; s < ((ORACLE_MUTANT == 2 && S > 16) ? S - 1 : S); s++) {
       const float vv = bf16_to_f32(v[(int64_t)s * kv_stride + d]);
       sum += p[s] * vv;
       if (slack) sl += jump[s] * fabsf(vv);
@@ -155,9 +170,20 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
 }
 
 // Same head in float64 throughout (no intermediate rounding), for reference
-// "truth" comparisons.
+// "truth" comparisons.  With bound non-null, also a per-element bound on
+// |o - t| that any bf16-weight implementation in float32 meets without tie
+// slack (the bf16 rounding of a weight may go either way there):
+//     2^-8 * M              each weight rounded to bf16 (unit roundoff 2^-8;
+//                           sum_j p_j |V_jd| <= M = max_j |V_jd|)
+//   + 2 * dt * M            float32 scores: the weight and its normaliser
+//                           move by at most dt relative each
+//   + 2^-10 * |t|           the fp16 rounding of the output (2^-11), doubled
+//   + 1e-5 * (1 + M)        float32 sums of the output and the weights
+// with dt = scale * D * 2^-23 * max_j sum_d |q_d k_jd|: a float32 dot product
+// of D terms, in any order, is within D * 2^-24 * sum |terms| of the exact
+// one (doubled here).
 void head_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t kv_stride, int S, int D, double scale,
-              double* o) {
+              double* o, double* bound) {
   thread_local std::vector<double> t_buf;
   t_buf.resize(S > 16 ? S : 16);
   double* t = t_buf.data();
@@ -171,10 +197,26 @@ void head_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   }
   double z = 0;
   for (int s = 0; s < S; s++) z += exp(t[s] - m);
+  for (int s = 0; s < S; s++) t[s] = exp(t[s] - m) / z;  // the weights
   for (int d = 0; d < D; d++) {
     double acc = 0;
-    for (int s = 0; s < S; s++) acc += exp(t[s] - m) / z * (double)bf16_to_f32(v[(int64_t)s * kv_stride + d]);
+    for (int s = 0; s < S; s++) acc += t[s] * (double)bf16_to_f32(v[(int64_t)s * kv_stride + d]);
     o[d] = S > 0 ? acc : 0.0;
+  }
+  if (bound) {
+    double dots = 0.0;
+    for (int s = 0; s < S; s++) {
+      double a = 0.0;
+      const uint16_t* kr = k + (int64_t)s * kv_stride;
+      for (int d = 0; d < D; d++) a += fabs((double)bf16_to_f32(q[d]) * (double)bf16_to_f32(kr[d]));
+      dots = a > dots ? a : dots;
+    }
+    const double dt = scale * D * ldexp(1.0, -23) * dots;
+    for (int d = 0; d < D; d++) {
+      double M = 0.0;
+      for (int s = 0; s < S; s++) M = fmax(M, fabs((double)bf16_to_f32(v[(int64_t)s * kv_stride + d])));
+      bound[d] = ldexp(1.0, -8) * M + 2.0 * dt * M + 1e-5 * (1.0 + M) + ldexp(1.0, -10) * fabs(o[d]);
+    }
   }
 }
 
@@ -185,7 +227,8 @@ extern "C" {
 // Decode attention over a packed batch (layouts as include/fmha_decode.h).
 // cu: [batch+1] row offsets.  p_mode 0 = bf16 weights (reference CPU loop),
 // 1 = fp32 weights.  o: fp16 bits [batch, hq, d].  slack: optional float
-// [batch, hq, d] (see head_f32; slack_eps is its floor).  Returns 0, or -1
+// [batch, hq, d] (see head_f32; slack_eps is its floor, or with a negative
+// value the fixed half-width -slack_eps).  Returns 0, or -1
 // for a length outside
 // [0, max_seqlen] or bad arguments (nothing is written then).  The
 // reference's bound is 16; longer rows run the same loop.
@@ -213,9 +256,10 @@ int oracle_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
   return 0;
 }
 
-// Float64 decode attention (no rounding anywhere but the bf16 inputs).
+// Float64 decode attention (no rounding anywhere but the bf16 inputs);
+// bound (nullable, [batch, hq, d]): see head_f64.
 int oracle_decode_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* cu, int64_t batch,
-                      int hq, int hkv, int d, double scale, double* o, int nthreads, int max_seqlen) {
+                      int hq, int hkv, int d, double scale, double* o, int nthreads, int max_seqlen, double* bound) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0 || max_seqlen < 0) return -1;
   for (int64_t b = 0; b < batch; b++) {
     const int S = cu[b + 1] - cu[b];
@@ -231,7 +275,7 @@ int oracle_decode_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
       const int hk = h / g;
       const int64_t qo = ((int64_t)b * hq + h) * d;
       head_f64(q + qo, k + row0 * kv_stride + (int64_t)hk * d, v + row0 * kv_stride + (int64_t)hk * d, kv_stride, S,
-               d, scale, o + qo);
+               d, scale, o + qo, bound ? bound + qo : nullptr);
     }
   }
   return 0;

@@ -13,6 +13,8 @@
 #define main fmha_reference_main
 #include "fmha_host.cpp"
 #undef main
+// The fourth variant, which fmha_host.cpp does not include.
+#include "fmha_mfma_16x16x16_v3_kernel.hpp"
 
 #include <cstdint>
 
@@ -65,6 +67,35 @@ int ref_launch_vectorized_fma(void* stream, const void* Q, const void* K, const 
   dim3 block(256, 1, 1);
   hipLaunchKernelGGL(fmha_vectorized_fma, grid, block, 0, (hipStream_t)stream, (const bhalf_t*)Q,
                      (const bhalf_t*)K, (const bhalf_t*)V, (half_t*)O, cu, batch, hq, hkv, 1, d, d, scale);
+  return (int)hipGetLastError();
+}
+
+// fmha_mfma (fmha_mfma_kernel.hpp:51-239): one query head per 256-thread
+// workgroup, grid (1, Hq, B) as README.md:173-179 documents.  Every global
+// access stays inside the batch's rows [cu[b], cu[b+1]) and the head's D
+// elements: K and V rows r < seqlen_kv only (:119-122, :194-197), Q by D/8
+// threads (:107-110), O dims < D (:236).  Valid for Hq == Hkv (K/V indexed with the
+// query head), D in {64, 128, 256}, every length in [1, 16] (the LDS tile is
+// 16 rows).
+int ref_launch_mfma(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu, int batch,
+                    int hq, int hkv, int d, float scale) {
+  dim3 grid(1, hq, batch);
+  dim3 block(256, 1, 1);
+  hipLaunchKernelGGL(fmha_mfma, grid, block, 0, (hipStream_t)stream, (const bhalf_t*)Q, (const bhalf_t*)K,
+                     (const bhalf_t*)V, (half_t*)O, cu, batch, hq, hkv, 1, d, d, scale);
+  return (int)hipGetLastError();
+}
+
+// fmha_mfma_v3 (fmha_mfma_16x16x16_v3_kernel.hpp:51-291), grid (1, Hq, B)
+// from its header (:47).  K rows r < seqlen_kv (:123-126); V rows clamped to
+// [0, seqlen_kv - 1] (:213-218), in range for lengths >= 1.  Same validity
+// limits as fmha_mfma.
+int ref_launch_mfma_v3(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu,
+                       int batch, int hq, int hkv, int d, float scale) {
+  dim3 grid(1, hq, batch);
+  dim3 block(256, 1, 1);
+  hipLaunchKernelGGL(fmha_mfma_v3, grid, block, 0, (hipStream_t)stream, (const bhalf_t*)Q, (const bhalf_t*)K,
+                     (const bhalf_t*)V, (half_t*)O, cu, batch, hq, hkv, 1, d, d, scale);
   return (int)hipGetLastError();
 }
 

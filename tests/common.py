@@ -100,3 +100,26 @@ def assert_pass(st, ctx=""):
     assert st["nonfinite"] == 0, f"{ctx}: non-finite outputs {st}"
     assert st["fails"] == 0, f"{ctx}: gate failures {st}"
     assert st["ref_rule_fails"] == 0, f"{ctx}: reference-rule failures {st}"
+
+
+def f64_bound(q, k, v, cu, Hq, Hkv, D, scale=None):
+    """float64 truth t [B,Hq,D] and a per-element bound on |o - t| that any
+    bf16-weight implementation with float32 arithmetic meets, with no tie
+    slack (the bf16 rounding of a weight may go either way): 2^-8 M (the
+    weights' bf16 rounding, M = max_j |V_jd|) + 2 dt M (float32 scores) +
+    2^-10 |t| (the fp16 output) + 1e-5 (1 + M) (float32 sums); the oracle
+    computes it beside t (head_f64 in oracle/fmha_oracle.cpp)."""
+    scale = default_scale(D) if scale is None else scale
+    seqlens = np.diff(np.asarray(cu, dtype=np.int64))
+    return oracle.decode_f64(q, k, v, cu, Hq, Hkv, D, scale, max_seqlen=int(seqlens.max(initial=0)),
+                             with_bound=True)
+
+
+def f64_check(o_bits, t, bound):
+    """Elements of o (fp16 bits) outside t +- bound, and the largest
+    |o - t| / bound."""
+    o = oracle.f16_to_f32(np.asarray(o_bits).reshape(t.shape)).astype(np.float64)
+    err = np.abs(o - t)
+    err[~np.isfinite(o)] = np.inf
+    return {"f64_violations": int((err > bound).sum()), "f64_max_ratio": float((err / bound).max()),
+            "f64_max_abs": float(err.max()), "f64_mean_abs": float(err.mean())}

@@ -7,13 +7,15 @@ sample of batches:
   * the cu_seqlens path and the uniform path give identical bits;
   * a seeded sample of batches (plus the first and last) passes the gate
     against the oracle (the gate is documented in tests/common.py);
+  * the same sample lies within the bf16-weight bound of float64 truth,
+    with no tie slack (tests/common.py: f64_bound);
   * config 1 (S=1): the whole output equals fp16(V) bit for bit.
 """
 import numpy as np
 import pytest
 
 import oracle
-from tests.common import CONFIGS, assert_pass, cu_from_seqlens, default_scale
+from tests.common import CONFIGS, assert_pass, cu_from_seqlens, default_scale, f64_bound, f64_check
 
 pytestmark = pytest.mark.gpu
 
@@ -62,3 +64,7 @@ def test_baseline_config(cfg):
     st = oracle.compare(os_, r, slack)
     print(f"config {cfg}: sampled {len(sample)} batches: {st}", flush=True)
     assert_pass(st, f"config {cfg}")
+    t, bound = f64_bound(qs, ks, vs, cus, Hq, Hkv, D, scale)
+    sf = f64_check(os_, t, bound)
+    print(f"config {cfg}: sampled batches against float64, no slack: {sf}", flush=True)
+    assert sf["f64_violations"] == 0, f"config {cfg}: outside the bf16-weight bound of float64: {sf}"

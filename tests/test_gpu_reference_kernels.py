@@ -2,13 +2,16 @@
 oracle/_ref, on the same inputs as this library's kernel.
 
 North-star parity: the new kernel must agree with the CPU reference and with
-the existing GPU kernel.  These tests run the wired-in fmha_mfma_4x4x4
-(fmha_mfma_4x4x4_kernel.hpp:370-389) and fmha_vectorized_fma
-(fmha_vectorized_fma_kernel.hpp:69-331) beside this library's bf16-weight
-and fp32-weight paths, check each against the oracle gate (the fp32-weight
-path against the oracle's fp32-weight loop and against fmha_vectorized_fma,
-whose semantics it has), and time all four on the same stream (the timings
-are printed; profiles/ keeps the summary).
+the existing GPU kernel.  These tests run all four reference variants -- the
+wired-in fmha_mfma_4x4x4 (fmha_mfma_4x4x4_kernel.hpp:370-389),
+fmha_vectorized_fma (fmha_vectorized_fma_kernel.hpp:69-331), fmha_mfma
+(fmha_mfma_kernel.hpp:51-239) and fmha_mfma_v3
+(fmha_mfma_16x16x16_v3_kernel.hpp:51-291), the last two on the grid
+(1, Hq, B) x 256 their documentation gives -- beside this library's
+bf16-weight and fp32-weight paths, check each against the oracle gate (the
+fp32-weight path against the oracle's fp32-weight loop and against
+fmha_vectorized_fma, whose semantics it has), and time all six on the same
+stream (the timings are printed; profiles/ keeps the summary).
 
 The reference kernels are only launched inside the shapes where their
 indexing stays in bounds: Hq == Hkv (they index K/V with the query head,
@@ -29,7 +32,7 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not oracle.ref_available(),
                                  reason="oracle/_ref not built (reference not mounted at build time)")]
 
-REF_KERNELS = ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma")
+REF_KERNELS = ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma", "ref_launch_mfma", "ref_launch_mfma_v3")
 
 
 def _inputs(B, H, D, seqlens, seed, std=1.0):

@@ -288,3 +288,130 @@ def test_rejects_bad_lengths():
         oracle.decode(q, k, v, np.array([0, 17, 6], np.int32), 1, 1, 64, 0.125)
     with pytest.raises(ValueError):
         oracle.decode(q, k, v, np.array([0, 4, 3], np.int32), 1, 1, 64, 0.125)
+
+
+# ------------------------------------------- rows longer than 16: pins
+# The reference stops at 16 rows (fmha_mfma_4x4x4_kernel.hpp:179, README.md:
+# 233); the oracle runs the same loop over longer rows for the split-KV,
+# single-pass and paged kernels.  These checks pin that extension through
+# closed forms and through float64 (itself checked against torch's SDPA at
+# long rows), and test_long_row_checks_reject_planted_mistakes shows that each
+# of four plausible mistakes in the long-row loop fails at least one of them.
+LONG_S = (17, 100, 2048, 40000)
+
+
+def _uniform_expected(v, cu, b, S, w, hq, hkv):
+    """fp16(sum_j w * V_j) with the fp32 sum in row order (np.cumsum is
+    sequential), query head h reading KV head h // (hq // hkv)."""
+    rows = _f32(v[cu[b]:cu[b] + S]) * np.float32(w)
+    acc = np.cumsum(rows, axis=0, dtype=np.float32)[-1]        # [Hkv, D]
+    return oracle.f32_to_f16(np.repeat(acc, hq // hkv, axis=0))
+
+
+def _long_row_failures():
+    """Runs the long-row checks with whatever oracle library is loaded;
+    returns the names of the checks that fail."""
+    failed = []
+    # Q = 0: every weight is exp(0)/S; bf16 and fp32 weight modes
+    for S in LONG_S:
+        D, hq, hkv = (64, 2, 1) if S > 2048 else (128, 4, 2)
+        q, k, v, cu = make_inputs(2, hq, hkv, D, [S, 3], seed=S)
+        q[:] = 0
+        o, _ = oracle.decode(q, k, v, cu, hq, hkv, D, default_scale(D), max_seqlen=S)
+        w = _f32(oracle.f32_to_bf16(np.float32(1.0) / np.float32(S)))
+        if not np.array_equal(o[0], _uniform_expected(v, cu, 0, S, w, hq, hkv)):
+            failed.append(f"zero-query S={S}")
+        o1, _ = oracle.decode(q, k, v, cu, hq, hkv, D, default_scale(D), p_mode=1, max_seqlen=S)
+        if not np.array_equal(o1[0], _uniform_expected(v, cu, 0, S, np.float32(1.0) / np.float32(S), hq, hkv)):
+            failed.append(f"zero-query fp32 weights S={S}")
+    # one dominant key (logit gap > 104): one-hot weights, O = fp16(V_j)
+    for S in LONG_S[:3]:
+        for j in sorted({16, S // 2, S - 1}):
+            D = 128
+            q, k, v, cu = make_inputs(1, 2, 2, D, [S], seed=S + j)
+            q[:] = oracle.f32_to_bf16(np.ones((1, 2, D), np.float32))
+            k[:] = oracle.f32_to_bf16(np.full((S, 2, D), -1.0, np.float32))
+            k[j] = oracle.f32_to_bf16(np.full((2, D), 16.0, np.float32))
+            for pm in (0, 1):
+                o, _ = oracle.decode(q, k, v, cu, 2, 2, D, default_scale(D), p_mode=pm, max_seqlen=S)
+                if not np.array_equal(o[0], oracle.f32_to_f16(_f32(v[j]))):
+                    failed.append(f"dominant key S={S} j={j} p_mode={pm}")
+    # random rows against float64 within the bf16-weight bound (no slack)
+    from tests.common import f64_bound, f64_check
+    for S, std in ((17, 1.0), (100, 2.0), (2048, 1.0)):
+        seqlens = [S, 5, S - 1]
+        q, k, v, cu = make_inputs(3, 4, 2, 128, seqlens, seed=3 * S, std=std)
+        o, _ = oracle.decode(q, k, v, cu, 4, 2, 128, default_scale(128), max_seqlen=S)
+        t, bound = f64_bound(q, k, v, cu, 4, 2, 128)
+        if f64_check(o, t, bound)["f64_violations"]:
+            failed.append(f"f64 bound S={S}")
+    return failed
+
+
+def test_long_rows_closed_forms_and_f64_bound():
+    assert _long_row_failures() == []
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,seqlens", [(4, 2, 128, [17, 100, 2048]), (8, 1, 64, [40000, 33]),
+                                              (6, 3, 256, [1000, 16, 17])])
+def test_f64_against_sdpa_long_rows(Hq, Hkv, D, seqlens):
+    import torch
+    q, k, v, cu = make_inputs(len(seqlens), Hq, Hkv, D, seqlens, seed=Hq * D + len(seqlens))
+    o = oracle.decode_f64(q, k, v, cu, Hq, Hkv, D, 1.0 / np.sqrt(D), max_seqlen=max(seqlens))
+    t = lambda a: torch.from_numpy(_f32(a)).double()
+    for b in range(len(seqlens)):
+        kb = t(k[cu[b]:cu[b + 1]]).repeat_interleave(Hq // Hkv, 1).transpose(0, 1)
+        vb = t(v[cu[b]:cu[b + 1]]).repeat_interleave(Hq // Hkv, 1).transpose(0, 1)
+        ref = torch.nn.functional.scaled_dot_product_attention(t(q[b]).unsqueeze(1), kb, vb,
+                                                               scale=1.0 / np.sqrt(D))[:, 0]
+        assert np.max(np.abs(o[b] - ref.numpy())) < 1e-12
+
+
+def test_f64_bound_is_tight_enough_to_catch_mistakes():
+    """The bound passes the oracle's bf16 and fp32 weights, and rejects the
+    output with one row left out, or with every weight moved by 2^-7."""
+    from tests.common import f64_bound, f64_check
+    seqlens = [16, 40, 300]
+    q, k, v, cu = make_inputs(3, 4, 4, 128, seqlens, seed=77, std=2.0)
+    t, bound = f64_bound(q, k, v, cu, 4, 4, 128)
+    for pm in (0, 1):
+        o, _ = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128), p_mode=pm, max_seqlen=300)
+        assert f64_check(o, t, bound)["f64_violations"] == 0
+    # drop the last row of each batch: the truth of the shorter rows
+    cu_short = cu.copy()
+    ks = np.concatenate([k[cu[b]:cu[b + 1] - 1] for b in range(3)])
+    vs = np.concatenate([v[cu[b]:cu[b + 1] - 1] for b in range(3)])
+    cu_short = cu_from_seqlens([s - 1 for s in seqlens])
+    o_drop, _ = oracle.decode(q, ks, vs, cu_short, 4, 4, 128, default_scale(128), max_seqlen=300)
+    assert f64_check(o_drop, t, bound)["f64_violations"] > 0
+    o_scaled = oracle.f32_to_f16(t.astype(np.float32) * np.float32(1 + 2.0 ** -6))
+    assert f64_check(o_scaled, t, bound)["f64_violations"] > 0
+
+
+def _build_mutant(tmp_path, n):
+    import subprocess
+    src = os.path.join(os.path.dirname(oracle.LIB_PATH), "fmha_oracle.cpp")
+    out = os.path.join(str(tmp_path), f"liboracle_mutant{n}.so")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-fopenmp", "-fPIC", "-shared", f"-DORACLE_MUTANT={n}", "-o", out,
+                    src], check=True)
+    return out
+
+
+@pytest.mark.parametrize("mutant", [1, 2, 3, 4])
+def test_long_row_checks_reject_planted_mistakes(mutant, tmp_path, monkeypatch):
+    """Each planted mistake (ORACLE_MUTANT in fmha_oracle.cpp) in the loop over
+    rows past 16 makes at least one long-row check fail; the short-row
+    fixtures still pass, so only the long-row checks see these mistakes."""
+    import ctypes
+    path = _build_mutant(tmp_path, mutant)
+    monkeypatch.setattr(oracle, "_lib", None)
+    monkeypatch.setattr(oracle, "LIB_PATH", path)
+    oracle.lib()
+    assert isinstance(oracle._lib, ctypes.CDLL)
+    failed = _long_row_failures()
+    assert failed, f"mutant {mutant} passed every long-row check"
+    for path_fx in sorted(glob.glob(os.path.join(GOLDEN, "mha_*.npz"))):
+        z = np.load(path_fx, allow_pickle=False)
+        B, Hq, Hkv, D = z["meta"].tolist()
+        o, _ = oracle.decode(z["q"], z["k"], z["v"], z["cu"], Hq, Hkv, D, default_scale(D))
+        assert np.array_equal(o, z["o"])
