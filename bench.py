@@ -22,6 +22,12 @@ Prints one JSON line:
                 turn (no call finds Q or O of the previous call in the MALL);
                 the timed loop above reuses one set, as the reference's
                 harness does (fmha_host.cpp:377-389);
+  cu_seqlens    the same workload and bytes through fmha_decode_fwd, the
+                entry point the reference's host program reaches
+                (fmha_host.cpp:367/382/437 through launch_fmha_mfma_4x4x4):
+                lengths from a device cu_seqlens array, timed as `value` is
+                after the warm-up calls (whose first call runs under the
+                default wave cap, its time reported as first_call_us);
   cpu_baseline  the reference's own CPU loop (fmha_host.cpp:158-284, built from
                 /root/reference into oracle/_ref) -- or the restated oracle
                 when that build is absent -- timed single-threaded on this
@@ -159,22 +165,22 @@ def main():
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def timed_loop(ptr_sets):
+    def timed_loop(ptr_sets, call=step):
         """K back-to-back calls between one event pair: ms per call."""
         torch.cuda.synchronize()
         e_start.record(stream)
         for i in range(K):
-            step(ptr_sets[i % len(ptr_sets)])
+            call(ptr_sets[i % len(ptr_sets)])
         e_end.record(stream)
         torch.cuda.synchronize()
         return e_start.elapsed_time(e_end) / K
 
-    def per_launch_loop(ptr_sets):
+    def per_launch_loop(ptr_sets, call=step):
         """K calls, each between its own event pair: per-launch ms."""
         torch.cuda.synchronize()
         for i in range(K):
             ev[i][0].record(stream)
-            step(ptr_sets[i % len(ptr_sets)])
+            call(ptr_sets[i % len(ptr_sets)])
             ev[i][1].record(stream)
         torch.cuda.synchronize()
         return [a.elapsed_time(b) for a, b in ev]
@@ -218,6 +224,37 @@ def main():
         }
         del keep
 
+    # Third leg: the drop-in entry point on the same inputs, lengths from a
+    # device cu_seqlens array.  Its wave cap comes from the mean length the
+    # previous call on this device reported (the first call, timed alone
+    # here, has none and runs under the default cap).
+    cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32, device=dev)
+    cup = cu.data_ptr()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def step_cu(ptrs=(qp, kp, vp, op)):
+        fmha_amd.launch_fmha_decode(sptr, *ptrs, cup, B, Hq, Hkv, 1, D, D, scale)
+
+    torch.cuda.synchronize()
+    e0.record(stream)
+    step_cu()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    first_cu_ms = e0.elapsed_time(e1)
+    for _ in range(args.warmup):
+        step_cu()
+    cu_ms = timed_loop(one_set, step_cu)
+    cu_kern_ms = sum(per_launch_loop(one_set, step_cu)) / K
+    cu_leg = {
+        "entry_point": "fmha_decode_fwd (cu_seqlens)",
+        "us_per_call": round(cu_ms * 1e3, 2),
+        "us_per_call_kernel_mean": round(cu_kern_ms * 1e3, 2),
+        "tb_s": round(nbytes / (cu_ms * 1e-3) / 1e12, 4),
+        "pct_of_peak": round(100.0 * nbytes / (cu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        "vs_uniform_entry": round(ms_per_step / cu_ms, 4),
+        "first_call_us": round(first_cu_ms * 1e3, 2),
+    }
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -260,6 +297,7 @@ def main():
             "traffic": traffic,
         },
         "rotated_inputs": rotated,
+        "cu_seqlens": cu_leg,
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }

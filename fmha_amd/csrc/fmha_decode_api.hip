@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "fmha_decode.h"
 #include "fmha_decode_launch.hpp"
@@ -59,19 +60,32 @@ int valu_kernel_group(int g) {
   return 0;
 }
 
-// Waves per CU for a unit that moves `rows` K/V rows and G query heads:
-// each row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB
-// of Q in and 1 KiB of O out.  Caps of 16 or more are dropped (no cap).
-// The floor is 3 waves, 4 for G = 8, whose waves compute for about as long
-// as their loads take (sweep at B=30720 Hq=128 Hkv=16 D=128, µs for 3/4/6
-// waves: S=16 1000/966/997, S=4 489/454/484; G = 4 and below are fastest
-// at 3).
-int waves_per_cu_for(int rows, int g) {
-  const int unit_bytes = 1024 * (2 * rows + 2 * g);
-  int w = kInflightBytesPerCU / unit_bytes;
+// Waves per CU for a unit that moves `rows16` / 16 K/V rows (a mean, in
+// sixteenths) and G query heads: each row costs 1 KiB of K plus 1 KiB of V
+// per wave, each query head 1 KiB of Q in and 1 KiB of O out.  Caps of 16 or
+// more are dropped (no cap).  The floor is 3 waves, 4 for G = 8, whose waves
+// compute for about as long as their loads take (sweep at B=30720 Hq=128
+// Hkv=16 D=128, µs for 3/4/6 waves: S=16 1000/966/997, S=4 489/454/484;
+// G = 4 and below are fastest at 3).
+//
+// Waves whose lengths come from a device array first wait for them (one
+// dependent load before any K/V request), so they carry requests for a
+// shorter part of their life and want more of them per CU: 144 KiB against
+// the 80 KiB of known lengths.  Sweep through fmha_decode_fwd (B=30720, µs
+// for 4/6/8/10/12/16 waves): S=16 H=16 D=128 614/634/654/660/667/665;
+// S=16 H=32 D=256 2516/2544/2569/2593/2617/2621; S=5 D=256
+// 643/504/446/433/423/427; the reference's Poisson(4) lengths (mean 4.3)
+// H=16 D=128 291/233/206/198/191/191, H=16 D=256 595/460/409/393/374/376,
+// H=32 D=128 570/446/409/393/377/377, H=32 D=256 1165/918/833/812/813/817.
+constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
+
+int waves_per_cu_for(int rows16, int g, bool device_lengths) {
+  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g);  // 16 x bytes
+  const int64_t budget = device_lengths ? kInflightBytesPerCUDeviceLengths : kInflightBytesPerCU;
+  const int64_t w = 16 * budget / unit_bytes16;
   if (w >= 16) return kMaxWavesPerCU;
   const int floor_w = g >= 8 ? 4 : 3;
-  return w < floor_w ? floor_w : w;
+  return w < floor_w ? floor_w : (int)w;
 }
 
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
@@ -114,10 +128,12 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
 }
 
 // Fills the layout-independent fields, picks the wave cap and launches.
-// rows_hint: KV rows per batch used to size the per-CU wave cap; fp32_weights
-// selects the fp32-weight kernels (packed layout only).
-int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows_hint,
-           bool fp32_weights = false) {
+// rows16: 16 x the KV rows per batch used to size the per-CU wave cap (the
+// uniform length, or an estimate when lengths live on the device, which
+// device_lengths says); fp32_weights selects the fp32-weight kernels
+// (packed layout only).
+int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows16,
+           bool device_lengths, bool fp32_weights = false) {
   const int heads_per_wave = kWaveSize / (dq / 8);
   const int64_t upb = (a.num_heads_kv + heads_per_wave - 1) / heads_per_wave;
   const int64_t units = upb * batch;
@@ -130,7 +146,12 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   if (g == 0)
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be at most 8 here (got %d)",
                   a.group);
-  const int w = waves_per_cu_for(rows_hint, g);
+  int w = waves_per_cu_for(rows16, g, device_lengths);
+  // FMHA_DECODE_WAVE_CAP=<waves per CU> overrides the cap (for sweeps).
+  if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {
+    const int v = std::atoi(e);
+    if (v > 0) w = v;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   // Fewer KV heads than a wave holds: R batches per wave, every lane busy
@@ -309,6 +330,58 @@ DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32
 // in [2, 16], averages 4.3 rows, and its best cap is the 4-row one.
 constexpr int kVarlenRowsHint = 4;
 
+// Mean-length feedback for the packed cu_seqlens entry points.  The best
+// wave cap depends on the rows per batch (4-row batches: 8 waves per CU;
+// 16-row batches: 3, 7% faster than under the 4-row cap at B=30720 H=16
+// D=128), which the host cannot read without a synchronisation.  So the
+// first wave of each call writes 16 x its mean length, 16 * (cu[batch] -
+// cu[0]) / batch, into one word of pinned host memory per device, and the
+// next call on that device sizes its cap from it (the default 4-row cap
+// until a call has reported).  Decoding loops call with lengths that change
+// by one row per step, so the previous call's mean is a close estimate; a
+// stale or foreign value changes speed, never results.  The word is
+// allocated on the first call that is not being captured into a graph (a
+// capture does not report), never freed, and read without a lock.
+constexpr int kMaxFeedbackDevices = 64;
+std::atomic<int32_t*> g_feedback[kMaxFeedbackDevices];
+std::atomic<bool> g_feedback_failed[kMaxFeedbackDevices];
+std::mutex g_feedback_mutex;
+
+int32_t* feedback_word(void* stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxFeedbackDevices) return nullptr;
+  int32_t* word = g_feedback[dev].load(std::memory_order_acquire);
+  if (word || g_feedback_failed[dev].load(std::memory_order_relaxed)) return word;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) != hipSuccess ||
+      capture != hipStreamCaptureStatusNone)
+    return nullptr;
+  std::lock_guard<std::mutex> lock(g_feedback_mutex);
+  word = g_feedback[dev].load(std::memory_order_acquire);
+  if (word) return word;
+  void* host = nullptr;
+  void* mapped = nullptr;
+  if (hipHostMalloc(&host, 64, hipHostMallocMapped | hipHostMallocCoherent | hipHostMallocPortable) != hipSuccess ||
+      hipHostGetDevicePointer(&mapped, host, 0) != hipSuccess) {
+    (void)hipGetLastError();  // no feedback on this device: the default cap
+    g_feedback_failed[dev].store(true, std::memory_order_relaxed);
+    return nullptr;
+  }
+  *static_cast<volatile int32_t*>(host) = 0;
+  word = static_cast<int32_t*>(mapped);
+  g_feedback[dev].store(word, std::memory_order_release);
+  return word;
+}
+
+// 16 x the rows per batch for the wave cap of a cu_seqlens call: the mean
+// the last reporting call left (within [1, max_rows] rows), or the default.
+int feedback_rows16(const int32_t* word, int max_rows) {
+  const int32_t mean16 = word ? __atomic_load_n(word, __ATOMIC_RELAXED) : 0;
+  int rows16 = mean16 > 0 ? mean16 : 16 * kVarlenRowsHint;
+  if (rows16 > 16 * max_rows) rows16 = 16 * max_rows;
+  return rows16 < 16 ? 16 : rows16;
+}
+
 // ---------------------------------------------------------------------------
 // Split-KV (lengths beyond 16)
 // ---------------------------------------------------------------------------
@@ -394,7 +467,9 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.head_stride = head_dim_q;
   if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, kVarlenRowsHint))
     return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
-  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint);
+  a.rows_feedback = feedback_word(stream);
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
+                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true);
 }
 
 extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -412,7 +487,9 @@ extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const v
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0, kVarlenRowsHint, true);
+  a.rows_feedback = feedback_word(stream);
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
+                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, true);
 }
 
 extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -432,7 +509,8 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
   a.head_stride = head_dim_q;
   if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, seqlen_kv))
     return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
-  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), seqlen_kv);
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), 16 * seqlen_kv,
+                false);
 }
 
 extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -472,7 +550,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
   const int rows_hint = seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv;
   if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
     return launch_mfma(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, rows_hint);
-  return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb, rows_hint);
+  return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb, 16 * rows_hint, seqlens_kv != nullptr);
 }
 
 namespace {
@@ -525,7 +603,7 @@ int paged_short(void* stream, const void* Q, const void* K_cache, const void* V_
   a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
   a.max_rows = max_rows;
   return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0,
-                max_rows < kVarlenRowsHint ? max_rows : kVarlenRowsHint);
+                16 * (max_rows < kVarlenRowsHint ? max_rows : kVarlenRowsHint), true);
 }
 
 }  // namespace
@@ -751,7 +829,9 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
     rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1, head_dim_q, softmax_scale,
                        workspace, workspace_bytes, span, unused);
     if (rc != FMHA_DECODE_SUCCESS) return rc;
-    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0, rows_hint);
+    d.rows_feedback = feedback_word(stream);
+    return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
+                  feedback_rows16(d.rows_feedback, max_seqlen_kv), true);
   }
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,

@@ -37,6 +37,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fmha_decode_paged.hpp"
+
 namespace fmha_decode {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -59,6 +61,9 @@ constexpr int kBufferWord3 = 0x00020000;
 // kRowOutOfRange; the sum of both still fits 32 bits.
 constexpr uint32_t kLaneOutOfRange = 0x40000000u;
 constexpr uint32_t kRowOutOfRange = 0x80000000u;
+// Two bf16 quiet NaNs: what the paged loaders put in place of a row whose
+// page is unmapped, so that the batch's outputs turn NaN.
+constexpr uint32_t kNaNBf16x2 = 0x7fc07fc0u;
 
 // Where a batch's K/V rows live.
 //   kLayoutPacked:  rows [cu[b], cu[b+1]) of a [rows, Hkv, D] tensor, or
@@ -102,7 +107,22 @@ struct DecodeArgs {
   // 5-7 the G = 8 one, the query heads at or past `group` of each KV head
   // loading and storing nothing (out-of-range offsets).
   int32_t group;
+  // Packed layout with cu offsets only, else null: a word of host-visible
+  // memory where the call's first wave leaves 16 x the mean length,
+  // 16 * (cu[batch] - cu[0]) / batch, for the host to size the next call's
+  // wave cap (the host cannot read the lengths of this one).
+  int32_t* rows_feedback;
 };
+
+// The first wave of a packed cu_seqlens call reports 16 x its mean length to
+// the host (DecodeArgs::rows_feedback): one lane, one vector store.
+__device__ __forceinline__ void report_mean_rows(const DecodeArgs& a, uint32_t unit, uint32_t batch, int lane) {
+  if (a.rows_feedback != nullptr && unit == 0 && lane == 0 && batch > 0) {
+    const int64_t rows = (int64_t)a.lens[batch] - (int64_t)a.lens[0];
+    const int64_t mean16 = rows * 16 / (int64_t)batch;
+    *a.rows_feedback = (int32_t)(mean16 < 0 ? 0 : (mean16 > 0x7fffffff ? 0x7fffffff : mean16));
+  }
+}
 
 // Byte offset of query head g of the lane's KV head from qo_off (the head's
 // first query row), out of range for padding heads g >= group.  G = 1 and 2
@@ -142,6 +162,16 @@ __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t x) { return __builtin_bit_c
 __device__ __forceinline__ int32_t load_uniform_i32(const int32_t* p, uint64_t idx) {
   typedef const __attribute__((address_space(4))) int32_t constant_i32;
   return ((constant_i32*)p)[idx];
+}
+
+// True when rows [0, S) of a batch (S <= 16) use a negative block-table
+// entry: such a batch is invalid (NaN outputs, no row read).
+__device__ __forceinline__ bool paged_rows_unmapped(const int32_t* pages, int S, uint32_t page_shift) {
+  const int n = paged_entries_used(S, page_shift);
+  int32_t sign = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxSeq; ++i) sign |= i < n ? load_uniform_i32(pages, (uint32_t)i) : 0;
+  return sign < 0;
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
@@ -488,17 +518,18 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
     for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
   } else {
     // Row j sits in page pages[j >> page_shift] at slot j & (page_size-1):
-    // one descriptor per row, spanning that row's heads, empty past S (the
-    // block-table entry read for such a row is entry 0, which always exists).
+    // one descriptor per row, spanning that row's heads, empty past S and
+    // for an unmapped (negative) entry; rows past S read no entry.  The
+    // caller has already turned a batch with an unmapped row into NaN, so
+    // the empty range for one is a second guard.
     uint64_t row_elem[SMAX];
     uint32_t row_rec[SMAX];
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) {
-      const int jj = j < S ? j : 0;
-      const uint32_t page = (uint32_t)load_uniform_i32(kv.pages, (uint32_t)jj >> kv.page_shift);
-      const uint32_t slot = (uint32_t)jj & ((1u << kv.page_shift) - 1u);
-      row_elem[j] = (uint64_t)page * kv.page_stride + (uint64_t)slot * (kv.row_bytes >> 1);
-      row_rec[j] = j < S ? kv.row_extent : 0u;
+      const int32_t entry = j < S ? load_uniform_i32(kv.pages, (uint32_t)j >> kv.page_shift) : -1;
+      const int64_t el = paged_row_elem(entry, (uint32_t)j, kv.page_shift, kv.page_stride, kv.row_bytes >> 1);
+      row_elem[j] = el < 0 ? 0u : (uint64_t)el;
+      row_rec[j] = el < 0 ? 0u : kv.row_extent;
     }
 #pragma unroll
     for (int j = 0; j < SMAX; ++j)
@@ -604,10 +635,15 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
   const bool head_ok = hk < a.num_heads_kv;
   uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
 
+  if constexpr (SB == 0 && LAYOUT == kLayoutPacked) report_mean_rows(a, unit, a.total_units / upb, lane);
   KVSpan kv;
   const bool length_ok = batch_span<D, LAYOUT, SB != 0>(a, b, kv);
-  // A uniform length was validated on the host; only table lengths can be bad.
-  if (SB == 0 && !length_ok) {
+  // A uniform length was validated on the host; only table lengths can be
+  // bad, and on a paged cache a negative block-table entry for a row the
+  // batch has.
+  bool valid = length_ok;
+  if constexpr (LAYOUT == kLayoutPaged) valid = valid && !paged_rows_unmapped(kv.pages, kv.S, kv.page_shift);
+  if (SB == 0 && !valid) {
     decode_bad_length<D, G>(a, b, hk, head_ok, lane);
     return;
   }
@@ -690,12 +726,14 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
 // The same for a paged cache (lengths in a.lens, log2(page_size) in
 // a.seqlen_uniform, page stride in a.batch_stride): the lane groups' batches
 // have their own pages, so every lane loads through its own 64-bit
-// addresses, with no branch.  A row with nothing to read (past the lane
-// group's length, or a lane group with no valid row) reads row 0 of the
-// first lane group whose batch has one (head 0) and is replaced by 0; the
-// block-table entry looked up for such a row is entry 0 of its batch, so
-// no lookup leaves the batch's table row.  A wave with no valid row reads
-// nothing.
+// addresses, with no branch.  A lane group whose rows use a negative
+// block-table entry has an invalid batch (NaN outputs) and reads nothing.
+// A row with nothing to read (past the lane group's length, or a lane group
+// with no valid row) reads row 0 of the first lane group whose batch has
+// one (head 0) and is replaced by 0; the block-table entry looked up for
+// such a row is entry 0 of its batch, so no lookup leaves the batch's table
+// row, and no address is formed from an entry that was not checked.  A wave
+// with no valid row reads nothing.
 template <int D, int G, int SMAX, bool PF32>
 __device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uint32_t b0, uint32_t nb, uint32_t b,
                                                         int S, bool bad, bool lane_ok, int sub, int hk, int lane,
@@ -715,30 +753,42 @@ __device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uin
   for (int g = 0; g < G; ++g) qv[g] = buffer_load16<kPolicyDefault>(q_rsrc, group_row_off<G>(qo_off, g, grp, D));
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
-  const bool has = lane_ok && !bad && S > 0;
+  const int32_t* pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+  const uint32_t shift = (uint32_t)a.seqlen_uniform;
+  // This lane group's block-table entries (entry 0 for rows it does not
+  // have); a negative one for a row it has makes its batch invalid.
+  const bool live = lane_ok && !bad && S > 0;
+  int32_t entry[SMAX];
+  int32_t sign = 0;
+#pragma unroll
+  for (int j = 0; j < SMAX; ++j) {
+    const bool ok = live && j < S;
+    entry[j] = pages[ok ? (uint32_t)j >> shift : 0u];
+    sign |= ok ? entry[j] : 0;
+  }
+  const bool unmapped = live && sign < 0;
+  bad = bad || unmapped;
+  const bool has = live && !unmapped;
   const uint64_t with_rows = __builtin_amdgcn_ballot_w64(has);
   if (with_rows == 0) {
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) kr[j] = vr[j] = u32x4{0u, 0u, 0u, 0u};
   } else {
-    const int32_t* pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
-    const uint32_t shift = (uint32_t)a.seqlen_uniform;
-    const uint32_t mask = (1u << shift) - 1u;
     const uint64_t page_stride = (uint64_t)a.batch_stride;
     const uint64_t row_elems = (uint64_t)a.row_stride;
     const uint64_t lane_elem = (uint64_t)hk * (uint64_t)a.head_stride + (uint64_t)r * 8u;
-    // Row 0 of the first lane group with a row, head 0, this lane's dims.
+    // Row 0 of the first lane group with a row (its entries all checked),
+    // head 0, this lane's dims.
     const int src = (int)__builtin_ctzll(with_rows);
-    const uint64_t own0 = has ? (uint64_t)(uint32_t)pages[0] * page_stride : 0u;
-    const uint32_t lo0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)own0, src);
-    const uint32_t hi0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(own0 >> 32), src);
+    const int64_t own0 = has ? paged_row_elem(entry[0], 0u, shift, page_stride, row_elems) : 0;
+    const uint32_t lo0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)own0, src);
+    const uint32_t hi0 = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)own0 >> 32), src);
     const uint64_t safe = (((uint64_t)hi0 << 32) | lo0) + (uint64_t)r * 8u;
     uint64_t off[SMAX];
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) {
-      const bool ok = has && j < S;
-      const uint64_t page = (uint64_t)(uint32_t)pages[ok ? (uint32_t)j >> shift : 0u];
-      off[j] = ok ? page * page_stride + (uint64_t)((uint32_t)j & mask) * row_elems + lane_elem : safe;
+      const int64_t el = has && j < S ? paged_row_elem(entry[j], (uint32_t)j, shift, page_stride, row_elems) : -1;
+      off[j] = el >= 0 ? (uint64_t)el + lane_elem : safe;
     }
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + off[j]));
@@ -779,6 +829,9 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(Decode
   const uint32_t unit = blockIdx.x * kWavesPerBlock + wave;
   if (unit >= a.total_units) return;
   const uint32_t batch = (uint32_t)a.units_per_batch;
+  if constexpr (LAYOUT == kLayoutPacked) {
+    if (a.lens) report_mean_rows(a, unit, batch, lane);
+  }
   const uint32_t b0 = unit << a.sub_shift;
   const uint32_t nb = batch - b0 < (1u << a.sub_shift) ? batch - b0 : (1u << a.sub_shift);
   const int hkl = lane / LPH;

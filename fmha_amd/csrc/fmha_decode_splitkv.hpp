@@ -242,13 +242,17 @@ struct LongRows {
   }
 
   // Descriptor of `rows` rows from row `row` on, inside one page.  A row past
-  // the end looks up block-table entry 0 of the batch (present whenever the
-  // batch has a row) and gets an empty range.
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows) const {
-    const uint32_t page = (uint32_t)load_uniform_i32(pages, (uint32_t)row >> page_shift);
-    const uint32_t slot = (uint32_t)row & ((1u << page_shift) - 1u);
-    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(rows * (int)row_bytes);
-    return make_rsrc(uniform_ptr(base + (uint64_t)page * page_stride + (uint64_t)slot * (row_bytes >> 1)), range);
+  // the end looks up the entry of a row the wave's range has and gets an
+  // empty range.  An unmapped page (a negative block-table entry) gets an
+  // empty range too, nothing is read, and `unmapped` tells the caller to
+  // poison what it loads with NaN: the batch is invalid, and the NaN rows
+  // carry that to its outputs (scores and their sums turn NaN).
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows, bool& unmapped) const {
+    const int32_t entry = load_uniform_i32(pages, (uint32_t)row >> page_shift);
+    const int64_t el = paged_row_elem(entry, (uint32_t)row, page_shift, page_stride, row_bytes >> 1);
+    unmapped = rows > 0 && el < 0;
+    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(el < 0 ? 0 : rows * (int)row_bytes);
+    return make_rsrc(uniform_ptr(base + (el < 0 ? 0u : (uint64_t)el)), range);
   }
 
   template <int NR>
@@ -264,14 +268,22 @@ struct LongRows {
       }
     } else if constexpr (LAYOUT == kLayoutPagedBlock) {
       const int valid = n - rel0 < 0 ? 0 : (n - rel0 > NR ? NR : n - rel0);
-      const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid);
+      bool unmapped;
+      const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid, unmapped);
 #pragma unroll
       for (int j = 0; j < NR; ++j) out[j] = buffer_load16_nt(pr, lane_off + (uint32_t)j * row_bytes);
+      if (unmapped) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j)
+          if (j < valid) out[j] = u32x4{kNaNBf16x2, kNaNBf16x2, kNaNBf16x2, kNaNBf16x2};
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         const bool ok = rel0 + j < n;
-        out[j] = buffer_load16_nt(page_rsrc(lo + (ok ? rel0 + j : 0), ok ? 1 : 0), lane_off);
+        bool unmapped;
+        out[j] = buffer_load16_nt(page_rsrc(lo + (ok ? rel0 + j : 0), ok ? 1 : 0, unmapped), lane_off);
+        if (unmapped) out[j] = u32x4{kNaNBf16x2, kNaNBf16x2, kNaNBf16x2, kNaNBf16x2};
       }
     }
   }
@@ -284,13 +296,16 @@ struct LongRows {
 // looks up the pages of its own rows (BLOCK, page_size >= 16: one lookup per
 // 16-row block, which lies in one page).  The loads carry no branch (a
 // branch in a pipelined loop makes the compiler wait for every request at
-// its head): a row at or past the lane's end reads slot 0 of the batch's
-// first page instead, with block-table entry 0, and is replaced by 0.  That
-// page exists whenever the batch has a row, which every wave that loads
-// rows checks first; unused block-table entries are never followed.
+// its head): a row at or past the lane's end, or in an unmapped page (a
+// negative block-table entry), reads 16 bytes of Q's first row instead --
+// memory that always exists -- and is replaced by 0, or for the unmapped
+// page by NaN, which makes the batch's outputs NaN (an invalid batch).
+// Block-table lookups stay inside the batch's row (entry 0 for rows past
+// the end), and no address is formed from a negative entry.
 template <int D, bool BLOCK>
 struct PagedLaneRows {
   const uint16_t* base;   // the cache at this lane's head and dims
+  const uint16_t* safe;   // 16 readable bytes (Q's first row, this lane's dims)
   const int32_t* pages;   // this batch's block-table row
   uint32_t page_shift;
   uint64_t page_stride;   // elements per page
@@ -304,6 +319,7 @@ struct PagedLaneRows {
     lane_rows = lane_rows_;
     lane_n = head_ok ? (lane_end < n ? lane_end : n) : 0;
     base = t + (uint64_t)kv_head_mem(a, hk) * D + r * 8;
+    safe = a.q + r * 8;
     pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
     page_shift = (uint32_t)a.page_shift;
     page_stride = (uint64_t)a.batch_stride;
@@ -316,31 +332,36 @@ struct PagedLaneRows {
   template <int NR>
   __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
     const int row0 = rel0 + lane_rows;
-    const uint32_t mask = (1u << page_shift) - 1u;
     u32x4 v[NR];
+    bool unmapped[NR];
     if constexpr (BLOCK) {
       const bool any = row0 < lane_n;
       const uint32_t abs0 = (uint32_t)(lo + row0);
-      const uint64_t page = (uint64_t)(uint32_t)pages[any ? abs0 >> page_shift : 0u];
-      const uint16_t* blk = base + page * page_stride + (uint64_t)(any ? abs0 & mask : 0u) * row_elems;
+      const int32_t entry = pages[any ? abs0 >> page_shift : 0u];
+      const int64_t el = any ? paged_row_elem(entry, abs0, page_shift, page_stride, row_elems) : -1;
 #pragma unroll
-      for (int j = 0; j < NR; ++j)
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(blk + (row0 + j < lane_n ? j * row_elems : 0)));
+      for (int j = 0; j < NR; ++j) {
+        const bool ok = el >= 0 && row0 + j < lane_n;
+        v[j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(ok ? base + (uint64_t)el + (uint64_t)j * row_elems : safe));
+        unmapped[j] = any && entry < 0;
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         const bool ok = row0 + j < lane_n;
         const uint32_t abs = (uint32_t)(lo + row0 + j);
-        const uint64_t page = (uint64_t)(uint32_t)pages[ok ? abs >> page_shift : 0u];
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            base + page * page_stride + (uint64_t)(ok ? abs & mask : 0u) * row_elems));
+        const int32_t entry = pages[ok ? abs >> page_shift : 0u];
+        const int64_t el = ok ? paged_row_elem(entry, abs, page_shift, page_stride, row_elems) : -1;
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(el >= 0 ? base + (uint64_t)el : safe));
+        unmapped[j] = ok && entry < 0;
       }
     }
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
       const bool ok = row0 + j < lane_n;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) out[j][k] = ok ? (uint32_t)v[j][k] : 0u;
+      for (int k = 0; k < 4; ++k) out[j][k] = unmapped[j] ? kNaNBf16x2 : (ok ? (uint32_t)v[j][k] : 0u);
     }
   }
 };

@@ -141,6 +141,7 @@ def fmha_decode_splitkv(q, k, v, cu_seqlens_kv, max_seqlen_kv, softmax_scale=Non
     for name, t in (("k", k), ("v", v)):
         if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 3 or not t.is_contiguous() or t.shape[2] != D:
             raise ValueError(f"{name} must be a contiguous bfloat16 GPU tensor [rows, Hkv, D]")
+    _check_device(q, k=k, v=v)
     if k.shape != v.shape:
         raise ValueError("k and v must have the same shape")
     if (cu_seqlens_kv.dtype != torch.int32 or cu_seqlens_kv.numel() != B + 1
@@ -179,7 +180,16 @@ def _check_q_out(q, out):
         return torch.empty(q.shape, dtype=torch.float16, device=q.device)
     if out.dtype != torch.float16 or out.shape != q.shape or not out.is_contiguous():
         raise ValueError("out must be a contiguous float16 tensor shaped like q")
+    _check_device(q, out=out)
     return out
+
+
+def _check_device(q, **tensors):
+    """Every tensor must live on q's device: the kernels dereference their
+    pointers there, and a host or other-device pointer would fault."""
+    for name, t in tensors.items():
+        if t is not None and t.device != q.device:
+            raise ValueError(f"{name} must be on q's device ({q.device}), not {t.device}")
 
 
 def _check_lengths(t, B, device):
@@ -217,6 +227,7 @@ def fmha_decode_strided(q, k, v, seqlens_kv=None, softmax_scale=None, out=None, 
             raise ValueError(f"{name} must be a bfloat16 GPU tensor [B, S, Hkv, D]")
         if t.stride(3) != 1:
             raise ValueError(f"{name} must have unit stride in the head dimension")
+    _check_device(q, k=k, v=v)
     if k.shape != v.shape or k.stride() != v.stride():
         raise ValueError("k and v must have the same shape and strides")
     S, Hkv = k.shape[1], k.shape[2]
@@ -251,6 +262,7 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
         if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or not t.is_contiguous() or t.shape[3] != D:
             raise ValueError(f"{name} must be a contiguous bfloat16 GPU tensor [pages, page_size, Hkv, D]")
+    _check_device(q, k_cache=k_cache, v_cache=v_cache)
     if k_cache.shape != v_cache.shape:
         raise ValueError("k_cache and v_cache must have the same shape")
     if (block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B
@@ -310,12 +322,15 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
     Hkv = k.shape[-2]
     if k.shape[-1] != D:
         raise ValueError("k/v head_dim must equal q head_dim")
+    _check_device(q, k=k, v=v)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
     if out is None:
         out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
     elif out.dtype != torch.float16 or out.shape != q.shape or not out.is_contiguous():
         raise ValueError("out must be a contiguous float16 tensor shaped like q")
+    else:
+        _check_device(q, out=out)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     if cu_seqlens_kv is not None:
         if cu_seqlens_kv.dtype != torch.int32 or cu_seqlens_kv.numel() != B + 1:

@@ -20,8 +20,15 @@
  *
  * All pointers are device pointers owned by the caller.  Calls are
  * asynchronous on the given stream (a hipStream_t passed as void*, NULL for
- * the null stream), allocate nothing, keep no mutable global state and may be
- * issued from any number of host threads.
+ * the null stream) and may be issued from any number of host threads.  They
+ * allocate no device memory.  The one piece of library state: the entry
+ * points that read lengths from a device cu_seqlens_kv array
+ * (fmha_decode_fwd, fmha_decode_fwd_fp32_weights, and
+ * fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
+ * per device (64 bytes, allocated by the first such call that is not being
+ * captured into a graph, never freed) in which each call's first wave leaves
+ * the call's mean length; the next call sizes its launch (waves per CU) from
+ * it.  Results never depend on it.
  *
  * Return value: 0 (hipSuccess) or a hipError_t value.  Arguments are checked
  * before anything touches the GPU; a rejected call launches nothing.
@@ -257,9 +264,10 @@ int fmha_decode_fwd_splitkv_strided(void* stream,
  * and pages it does not map are never read.  Workspace as for
  * fmha_decode_fwd_splitkv_strided (when that bound is <= 16 the call runs
  * fmha_decode_fwd_paged's kernel, and the workspace only holds a padded
- * query group).  Group sizes 1-8 (3, 5, 6, 7 padded, as for
- * fmha_decode_fwd_splitkv) at any length.  No counterpart in the
- * reference.
+ * query group).  Any group size: G <= 8 on the VALU passes (3 and 5-7 on
+ * padded query groups), G > 8 on the matrix-core split passes; with that
+ * bound <= 16, G > 8 also takes the split passes and needs the workspace.
+ * No counterpart in the reference.
  */
 int fmha_decode_fwd_splitkv_paged(void* stream,
                                   const void* Q, const void* K_cache, const void* V_cache, void* O,

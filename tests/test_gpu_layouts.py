@@ -204,3 +204,100 @@ def test_paged_few_kv_heads_batches_per_wave(page_size, D, Hq, Hkv):
     assert torch.isnan(o2[3].float()).all()
     keep = [b for b in range(B) if b != 3]
     assert torch.equal(o2[keep].view(torch.int16), o[keep].view(torch.int16))
+
+
+def test_tensors_on_another_device_are_rejected_before_launch():
+    """out, k, v, caches, block tables and lengths must be on q's device: a
+    host tensor's pointer handed to the kernel would fault, so every wrapper
+    raises ValueError before anything is launched."""
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    B, H, D = 4, 4, 128
+    q = torch.zeros(B, H, 1, D, device=dev, dtype=torch.bfloat16)
+    k = torch.zeros(B * 3, H, D, device=dev, dtype=torch.bfloat16)
+    cu = torch.arange(0, 3 * (B + 1), 3, dtype=torch.int32, device=dev)
+    cpu_out = torch.empty(B, H, 1, D, dtype=torch.float16)
+    with pytest.raises(ValueError, match="device"):
+        fmha_amd.fmha_decode(q, k, k, cu_seqlens_kv=cu, out=cpu_out)
+    with pytest.raises(ValueError, match="device"):
+        fmha_amd.fmha_decode(q, k, k.cpu(), cu_seqlens_kv=cu)
+    with pytest.raises(ValueError, match="device"):
+        fmha_amd.fmha_decode_splitkv(q, k, k, cu, 3, out=cpu_out)
+    k4 = k.view(B, 3, H, D)
+    with pytest.raises(ValueError, match="device"):
+        fmha_amd.fmha_decode_strided(q, k4, k4, out=cpu_out)
+    pages = torch.zeros(B, 16, H, D, device=dev, dtype=torch.bfloat16)
+    bt = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
+    lens = torch.full((B,), 3, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="device"):
+        fmha_amd.fmha_decode_paged(q, pages, pages, bt, lens, out=cpu_out)
+    with pytest.raises(ValueError):
+        fmha_amd.fmha_decode_paged(q, pages, pages, bt.cpu(), lens)
+    with pytest.raises(ValueError):
+        fmha_amd.fmha_decode_paged(q, pages, pages, bt, lens.cpu())
+    torch.cuda.synchronize()
+
+
+# (max_seqlen_kv or None for the short kernel, page_size, D, Hq, Hkv, B): the
+# short kernel one batch per wave (16 KV heads) and several batches per wave
+# (1 and 2 KV heads); beyond 16 rows the single pass (>= 512 waves), the
+# split passes over one page per wave (page size 16) and per-lane pages
+# (few KV heads, page sizes 4 and 16), and the matrix-core split passes
+# (G = 16, 12).
+NEG_CASES = [
+    (None, 4, 128, 16, 16, 23), (None, 1, 128, 8, 1, 37), (None, 16, 128, 16, 2, 37), (None, 8, 256, 4, 1, 19),
+    (40, 16, 128, 8, 4, 600), (70, 16, 128, 16, 16, 9), (70, 4, 128, 16, 2, 9), (70, 16, 128, 8, 2, 9),
+    (70, 4, 64, 16, 1, 9),
+    (100, 16, 128, 24, 2, 7), (100, 4, 256, 24, 2, 7),
+]
+
+
+@pytest.mark.parametrize("max_s,page_size,D,Hq,Hkv,B", NEG_CASES)
+def test_paged_negative_entries_give_nan(max_s, page_size, D, Hq, Hkv, B):
+    """A negative block-table entry (serving engines pad with -1) for a row a
+    batch has: that batch's outputs are NaN and its unmapped pages are never
+    read; every other batch keeps its exact bits.  -1 entries past a
+    batch's rows are padding, as always."""
+    import torch
+    import fmha_amd
+    print(f"paged negative entries: max_s={max_s} ps={page_size} D={D} Hq={Hq} Hkv={Hkv} B={B}", flush=True)
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(page_size * 7 + D + Hq + B)
+    rng = np.random.default_rng(page_size * 3 + D + Hq + Hkv + B)
+    cap = 16 if max_s is None else max_s
+    seqlens = rng.integers(1, cap + 1, size=B).astype(np.int32)
+    seqlens[0] = cap
+    need = [(int(s) + page_size - 1) // page_size for s in seqlens]
+    max_pages = (cap + page_size - 1) // page_size
+    num_pages = sum(need) + 2
+    perm = rng.permutation(num_pages)
+    bt = np.full((B, max_pages), -1, np.int32)
+    i = 0
+    for b in range(B):
+        for p in range(need[b]):
+            bt[b, p] = perm[i]
+            i += 1
+    kc = torch.randn(num_pages, page_size, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(num_pages, page_size, Hkv, D, generator=gen, device=dev, dtype=torch.bfloat16)
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    lens = torch.from_numpy(seqlens).to(dev)
+
+    def run(table):
+        o = fmha_amd.fmha_decode_paged(q, kc, vc, torch.from_numpy(table).to(dev), lens, max_seqlen_kv=max_s)
+        torch.cuda.synchronize()
+        return o
+
+    o = run(bt)
+    assert bool(torch.isfinite(o.float()).all())
+    poisoned = sorted(set(rng.choice(B, size=max(1, B // 4), replace=False).tolist()) | {0})
+    bad = bt.copy()
+    for n, b in enumerate(poisoned):
+        e = int(rng.integers(0, need[b]))            # an entry the batch's rows use
+        bad[b, e] = -1 if n % 2 == 0 else -(2 ** 31)
+    o2 = run(bad)
+    for b in range(B):
+        if b in poisoned:
+            assert bool(torch.isnan(o2[b].float()).all()), f"batch {b} with an unmapped page is not NaN"
+        else:
+            assert torch.equal(o2[b].view(torch.int16), o[b].view(torch.int16)), f"batch {b} changed"

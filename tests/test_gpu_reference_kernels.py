@@ -34,6 +34,31 @@ pytestmark = [pytest.mark.gpu,
 
 REF_KERNELS = ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma", "ref_launch_mfma", "ref_launch_mfma_v3")
 
+# Reference kernels whose output is wrong on gfx950, with the reason; they are
+# timed and their statistics printed, but no correctness is asserted of them.
+# fmha_mfma_v3 builds its P.V A operand inside `if (lane_col == 0)` with
+# __shfl(sm_val, lane_row * 4 + i) (fmha_mfma_16x16x16_v3_kernel.hpp:250-255):
+# the source lanes 1-15 of that shuffle are inactive in the branch, the
+# ds_bpermute it compiles to returns 0 for them, and only the first row's
+# weight reaches P.V.
+REF_BROKEN = {"ref_launch_mfma_v3": "P.V weights shuffled from inactive lanes (fmha_mfma_16x16x16_v3_kernel.hpp:250-255)"}
+
+
+def _first_row_only(q, k, v, cu_h, sel, B, H, D):
+    """What a kernel that keeps only row 0's weight computes: fp16(bf16(p_0)
+    * V_0), with p_0 the float32 softmax weight of row 0."""
+    import torch
+    qf = q.view(B, H, D)[torch.from_numpy(sel).to(q.device)].float().cpu().numpy()
+    out = np.empty((len(sel), H, D), np.float32)
+    for i, b in enumerate(sel):
+        kk = k[cu_h[b]:cu_h[b + 1]].float().cpu().numpy()            # [S, H, D]
+        t = np.einsum("hd,shd->hs", qf[i], kk).astype(np.float32) * np.float32(default_scale(D))
+        e = np.exp(t - t.max(axis=1, keepdims=True))
+        p0 = (e[:, 0] / e.sum(axis=1)).astype(np.float32)
+        p0 = torch.from_numpy(p0).to(torch.bfloat16).float().numpy()
+        out[i] = p0[:, None] * v[cu_h[b]].float().cpu().numpy()
+    return oracle.f32_to_f16(out)
+
 
 def _inputs(B, H, D, seqlens, seed, std=1.0):
     import torch
@@ -141,6 +166,12 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
             st32 = oracle.compare(_bits(o.view(B, H, D)[idx]), r32)
             print(f"{label}: {name} vs fp32-weight oracle: {st32}", flush=True)
             assert_pass(st32, f"{label} ours, fp32 weights")
+        elif name in REF_BROKEN:
+            # known defect: print how far off it is, and how close it is to
+            # a P.V over the first row's weight alone
+            p0 = _first_row_only(q, k, v, cu_h, sel, B, H, D)
+            st0 = oracle.compare(_bits(o.view(B, H, D)[idx]), p0)
+            print(f"{label}: {name} ({REF_BROKEN[name]}) vs first-row-only P.V: {st0}", flush=True)
         else:
             # the reference's own rule (fmha_host.cpp:260) is what its kernels promise
             assert st["ref_rule_fails"] == 0 and st["nonfinite"] == 0, f"{label} {name}: {st}"
