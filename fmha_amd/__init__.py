@@ -3,14 +3,15 @@
 grouped-query attention.  The kernels are hand-written HIP in fmha_amd/csrc;
 the C ABI is include/fmha_decode.h; this package is its host-side interface.
 """
-from .decode import (MAX_SEQLEN_KV, FmhaDecodeError, fmha_decode, fmha_decode_paged, fmha_decode_splitkv,
-                     fmha_decode_strided, launch_fmha_decode, launch_fmha_decode_fp32_weights, launch_fmha_decode_paged,
+from .decode import (MAX_SEQLEN_KV, NOALLOC_SCRATCH_BYTES, FmhaDecodeError, fmha_decode, fmha_decode_paged,
+                     fmha_decode_splitkv, fmha_decode_strided, launch_fmha_decode, launch_fmha_decode_fp32_weights, launch_fmha_decode_paged,
                      launch_fmha_decode_splitkv, launch_fmha_decode_splitkv_paged, launch_fmha_decode_splitkv_strided,
                      launch_fmha_decode_strided, launch_fmha_decode_uniform, splitkv_workspace_size)
 from ._lib import LIB_PATH, EXPORTED
 
 __all__ = [
     "MAX_SEQLEN_KV",
+    "NOALLOC_SCRATCH_BYTES",
     "FmhaDecodeError",
     "fmha_decode",
     "fmha_decode_strided",

@@ -18,6 +18,7 @@ EXPORTED = (
     "fmha_decode_fwd_paged",
     "fmha_decode_splitkv_workspace_size",
     "fmha_decode_fwd_splitkv",
+    "fmha_decode_fwd_splitkv_noalloc",
     "fmha_decode_fwd_splitkv_strided",
     "fmha_decode_fwd_splitkv_paged",
     "fmha_decode_error_string",
@@ -55,6 +56,8 @@ def load():
     lib.fmha_decode_splitkv_workspace_size.argtypes = [i32, i32, i32, i32, i32]
     lib.fmha_decode_fwd_splitkv.restype = ctypes.c_int
     lib.fmha_decode_fwd_splitkv.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32, vp, sz]
+    lib.fmha_decode_fwd_splitkv_noalloc.restype = ctypes.c_int
+    lib.fmha_decode_fwd_splitkv_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_splitkv_strided.restype = ctypes.c_int
     lib.fmha_decode_fwd_splitkv_strided.argtypes = [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, i32,
                                                     i32, i32, f32, vp, sz]

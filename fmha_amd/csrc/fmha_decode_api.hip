@@ -347,11 +347,11 @@ std::atomic<int32_t*> g_feedback[kMaxFeedbackDevices];
 std::atomic<bool> g_feedback_failed[kMaxFeedbackDevices];
 std::mutex g_feedback_mutex;
 
-int32_t* feedback_word(void* stream) {
+int32_t* feedback_word(void* stream, bool may_allocate = true) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxFeedbackDevices) return nullptr;
   int32_t* word = g_feedback[dev].load(std::memory_order_acquire);
-  if (word || g_feedback_failed[dev].load(std::memory_order_relaxed)) return word;
+  if (word || !may_allocate || g_feedback_failed[dev].load(std::memory_order_relaxed)) return word;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) != hipSuccess ||
       capture != hipStreamCaptureStatusNone)
@@ -797,12 +797,14 @@ int with_group_padding(void* stream, const void* Q, void* O, int32_t batch, int3
 }
 }  // namespace
 
-extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
-                                       const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
-                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
-                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
-                                       void* workspace, size_t workspace_bytes) {
-  g_detail[0] = '\0';
+namespace {
+
+// fmha_decode_fwd_splitkv with the workspace given; may_allocate: whether the
+// short route may allocate the mean-length feedback word.
+int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu_seqlens_kv,
+                   int32_t max_seqlen_kv, int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                   int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale, void* workspace,
+                   size_t workspace_bytes, bool may_allocate) {
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
@@ -829,7 +831,7 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
     rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1, head_dim_q, softmax_scale,
                        workspace, workspace_bytes, span, unused);
     if (rc != FMHA_DECODE_SUCCESS) return rc;
-    d.rows_feedback = feedback_word(stream);
+    d.rows_feedback = feedback_word(stream, may_allocate);
     return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
                   feedback_rows16(d.rows_feedback, max_seqlen_kv), true);
   }
@@ -844,6 +846,80 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
         a.len_mode = fmha_decode::kLenCu;
         return split_launch(stream, fmha_decode::kLayoutPacked, a, head_dim_q);
       });
+}
+
+// Scratch of fmha_decode_fwd_splitkv_noalloc: the split-KV workspace as a
+// device array, one copy per GPU (each holds it from load until the process
+// ends).  Host code never uses the array's name as an address: the device
+// address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)FMHA_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::atomic<void*> g_scratch[kMaxFeedbackDevices];
+std::mutex g_scratch_mutex;
+
+// This device's scratch address, or null (detail set) when it cannot be had.
+void* scratch_address(int* rc) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    *rc = reject((int)err, "hipGetDevice failed: %s", hipGetErrorString(err));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxFeedbackDevices) {
+    *rc = reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "device %d is beyond the %d this library serves", dev,
+                 kMaxFeedbackDevices);
+    return nullptr;
+  }
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || p == nullptr) {
+    *rc = reject(err != hipSuccess ? (int)err : FMHA_DECODE_ERROR_NOT_SUPPORTED,
+                 "no device address for the scratch array: %s", hipGetErrorString(err));
+    return nullptr;
+  }
+  g_scratch[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+}  // namespace
+
+extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
+                                       int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                       int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
+                                       void* workspace, size_t workspace_bytes) {
+  g_detail[0] = '\0';
+  return splitkv_packed(stream, Q, K, V, O, cu_seqlens_kv, max_seqlen_kv, batch, num_heads_q, num_heads_kv,
+                        seqlen_q, head_dim_q, head_dim_kv, softmax_scale, workspace, workspace_bytes, true);
+}
+
+extern "C" int fmha_decode_fwd_splitkv_noalloc(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                               const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
+                                               int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
+                                               int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if ((rc = split_check_workspace_args(max_seqlen_kv)) != FMHA_DECODE_SUCCESS) return rc;
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  {
+    const size_t need =
+        fmha_decode_splitkv_workspace_size(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim_q);
+    if (need > kNoAllocScratchBytes)
+      return reject(FMHA_DECODE_ERROR_INVALID_VALUE,
+                    "this call needs %zu bytes of scratch; fmha_decode_fwd_splitkv_noalloc has %zu (use "
+                    "fmha_decode_fwd_splitkv with a workspace)",
+                    need, kNoAllocScratchBytes);
+  }
+  void* ws = scratch_address(&rc);
+  if (ws == nullptr) return rc;
+  return splitkv_packed(stream, Q, K, V, O, cu_seqlens_kv, max_seqlen_kv, batch, num_heads_q, num_heads_kv,
+                        seqlen_q, head_dim_q, head_dim_kv, softmax_scale, ws, kNoAllocScratchBytes, false);
 }
 
 extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, const void* K, const void* V, void* O,

@@ -17,6 +17,9 @@ import math
 from . import _lib
 
 MAX_SEQLEN_KV = 16
+# Bytes of the device array fmha_decode_fwd_splitkv_noalloc uses as its
+# workspace (FMHA_DECODE_NOALLOC_SCRATCH_BYTES in include/fmha_decode.h).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class FmhaDecodeError(RuntimeError):

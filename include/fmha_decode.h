@@ -232,6 +232,28 @@ int fmha_decode_fwd_splitkv(void* stream,
                             float softmax_scale, void* workspace, size_t workspace_bytes);
 
 /*
+ * fmha_decode_fwd_splitkv without the workspace arguments, for callers that
+ * cannot allocate device memory (code under graph capture, serving loops,
+ * harnesses that forbid hipMalloc); it has no counterpart in the reference.
+ * The workspace is a device array inside the library, one per GPU, of
+ * FMHA_DECODE_NOALLOC_SCRATCH_BYTES bytes (held from library load until the
+ * process ends); the call allocates nothing, and a call whose
+ * fmha_decode_splitkv_workspace_size exceeds the array is rejected
+ * (FMHA_DECODE_ERROR_INVALID_VALUE) before anything is launched.  Every call
+ * on one GPU uses the same array: calls that overlap on a GPU (different
+ * streams, not ordered) race and must be serialised by the caller.  Same
+ * kernels, arguments and results as fmha_decode_fwd_splitkv.
+ */
+#define FMHA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+int fmha_decode_fwd_splitkv_noalloc(void* stream,
+                                    const void* Q, const void* K, const void* V, void* O,
+                                    const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv,
+                                    int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                    int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                    float softmax_scale);
+
+/*
  * fmha_decode_fwd_splitkv over the strided K/V of fmha_decode_fwd_strided
  * (BHSD, padded BSHD, any batch/row/head strides in elements, multiples of
  * 8): lengths beyond 16 for those caches.

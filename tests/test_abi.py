@@ -35,7 +35,8 @@ def test_exports_every_declared_function(lib):
     assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_uniform",
                           "fmha_decode_fwd_strided",
                           "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
-                          "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_strided",
+                          "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_noalloc",
+                          "fmha_decode_fwd_splitkv_strided",
                           "fmha_decode_fwd_splitkv_paged", "fmha_decode_error_string",
                           "fmha_decode_last_error_detail", "fmha_decode_version"}
     from fmha_amd import _lib
@@ -404,3 +405,37 @@ def test_header_is_plain_c():
         r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I",
                             os.path.join(ROOT, "include"), p], capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def splitkv_noalloc(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, maxs=1000, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_splitkv_noalloc(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["maxs"],
+                                               a["batch"], a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(maxs=-1), BAD, "max_seqlen_kv"),
+    (dict(cu=None), BAD, "cu_seqlens_kv"),
+    (dict(dq=96, dkv=96), BAD, "head_dim"),
+    (dict(sq=3), BAD, "seqlen_q"),
+    (dict(q=None), BAD, "non-null"),
+    # more scratch than the library's array holds: rejected before any GPU call
+    (dict(batch=4096, hq=32, hkv=8, maxs=4096), BAD, "scratch"),
+])
+def test_splitkv_noalloc_rejects(lib, kw, code, needle):
+    """The no-allocation entry point checks its arguments, and its scratch
+    need against FMHA_DECODE_NOALLOC_SCRATCH_BYTES, on the host first."""
+    assert splitkv_noalloc(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
+def test_noalloc_scratch_size_matches_header(lib):
+    import re
+    import fmha_amd
+    text = open(os.path.join(ROOT, "include", "fmha_decode.h")).read()
+    m = re.search(r"#define FMHA_DECODE_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == fmha_amd.NOALLOC_SCRATCH_BYTES
+    # a long-context batch of the size the array is meant for fits it
+    assert lib.fmha_decode_splitkv_workspace_size(64, 32, 8, 4096, 128) <= fmha_amd.NOALLOC_SCRATCH_BYTES
