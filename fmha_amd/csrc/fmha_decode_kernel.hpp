@@ -297,10 +297,18 @@ struct GroupReduce {
 };
 
 // Partial dot products of this lane's 8 dims: x[g*NR + j] = q_g . k_j.
+// Query heads at or past `active` (padding of a group size the kernel is
+// not instantiated for; a wave-uniform value) get 0 without arithmetic.
 template <int G, int NR>
-__device__ __forceinline__ void partial_scores(const u32x4 (&qv)[G], const u32x4 (&kr)[NR], float* x) {
+__device__ __forceinline__ void partial_scores(const u32x4 (&qv)[G], const u32x4 (&kr)[NR], float* x,
+                                               int active = G) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+    if (g >= active) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) x[g * NR + j] = 0.0f;
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
       float acc = 0.0f;
@@ -317,9 +325,10 @@ __device__ __forceinline__ void partial_scores(const u32x4 (&qv)[G], const u32x4
 
 // acc[g][d] += sum_j P_g,j * V_j[d] over NR rows, rows taken in pairs:
 // pp[g][jp] holds the bf16 weights of rows 2jp (low half) and 2jp+1.
+// Query heads at or past `active` (wave-uniform) are skipped.
 template <int G, int NR>
 __device__ __forceinline__ void accumulate_pv(const u32x4 (&vr)[NR], const uint32_t (&pp)[G][(NR + 1) / 2],
-                                              float (&acc)[G][8]) {
+                                              float (&acc)[G][8], int active = G) {
   constexpr int NP = (NR + 1) / 2;
 #pragma unroll
   for (int jp = 0; jp < NP; ++jp) {
@@ -333,6 +342,7 @@ __device__ __forceinline__ void accumulate_pv(const u32x4 (&vr)[NR], const uint3
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+      if (g >= active) continue;
       const bf16x2 pw = as_bf16x2(pp[g][jp]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -356,28 +366,29 @@ __device__ __forceinline__ u32x4 pack_f16x8(const float (&a)[8]) {
 }
 
 // ---------------------------------------------------------------------------
-// Scores, masked softmax and P.V of one wave whose Q, K and V registers are
-// loaded (rows >= S read as 0): S valid rows (per lane group when the
-// groups serve different batches), weights through LDS slot
-// [hkl][g*16 + j] of lds_p, fp32 result per query head in acc.
+// Scores and masked softmax of GH query heads (g0 .. g0+GH-1 of the wave's
+// KV heads) against SMAX loaded K rows, the weights written to LDS slot
+// [hkl][g*16 + j] of lds_p (bf16, or fp32 with PF32; VP slots per KV head).
+// Each score is the tree sum of its lanes' partial dot products over the
+// butterfly masks, whatever GH is; only the lanes that hold it afterwards,
+// and so the order of the softmax sums, depend on GH.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX, bool PF32>
-__device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX], const u32x4 (&vr)[SMAX],
-                                            int S, float scale, int lane, uint16_t* lds_p, float (&acc)[G][8]) {
+template <int D, int GH, int SMAX, bool PF32, int VP>
+__device__ __forceinline__ void score_softmax(const u32x4 (&qv)[GH], const u32x4 (&kr)[SMAX], int S, float scale,
+                                              int lane, uint16_t* lds_p, int g0, int active) {
   constexpr int LPH = D / 8;                 // lanes per KV head
   constexpr int NS = ilog2(LPH);             // butterfly steps
-  constexpr int V = G * SMAX;                // scores per KV head
+  constexpr int V = GH * SMAX;               // scores per KV head
   constexpr int L = NS < ilog2(V) ? NS : ilog2(V);  // splitting steps
   constexpr int W = (V >> NS) > 1 ? (V >> NS) : 1;  // scores per lane after the butterfly
   constexpr int GS = W < SMAX ? W : SMAX;    // scores of one query head inside a lane
   constexpr int C = ilog2(SMAX / GS);        // steps spanning one query head's lanes
-  constexpr int VP = G * kMaxSeq;            // LDS bf16 slots per KV head
   const int r = lane % LPH;
   const int hkl = lane / LPH;
 
   // ---- partial scores over this lane's 8 dims ----
   float x[V];
-  partial_scores<G, SMAX>(qv, kr, x);
+  partial_scores<GH, SMAX>(qv, kr, x, active);
 
   // ---- reduce over the head's lanes; lane keeps scores [blk*W, blk*W + W) ----
   TransposeReduce<LPH, V, 0>::run(x, lane);
@@ -410,21 +421,69 @@ __device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&
     for (int w = 0; w < GS; ++w) p[h0 + w] = (sum > 0.0f) ? (t[w] / sum) : 0.0f;
   }
 
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-
   if constexpr (!PF32) {
     // ---- bf16 weights -> LDS slot [hkl][g*16 + j] ----
     uint16_t* lds_head = lds_p + hkl * VP;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       const int vi = blk * W + w;
-      const int g = vi / SMAX;
-      const int j = vi % SMAX;
-      lds_head[g * kMaxSeq + j] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
+      lds_head[(g0 + vi / SMAX) * kMaxSeq + vi % SMAX] = __builtin_bit_cast(uint16_t, (__bf16)p[w]);
     }
+  } else {
+    // ---- fp32 weights -> LDS slot [hkl][g*16 + j] (4 bytes each) ----
+    float* lds_head = reinterpret_cast<float*>(lds_p) + hkl * VP;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int vi = blk * W + w;
+      lds_head[(g0 + vi / SMAX) * kMaxSeq + vi % SMAX] = p[w];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scores, masked softmax and P.V of one wave whose Q, K and V registers are
+// loaded (rows >= S read as 0): S valid rows (per lane group when the
+// groups serve different batches), weights through LDS slot
+// [hkl][g*16 + j] of lds_p, fp32 result per query head in acc.  Query heads
+// at or past `active` (the padding of a group size without its own
+// instantiation; wave-uniform) are neither scored nor accumulated.
+// Groups of 4 or 8 query heads at D <= 128 are scored two heads at a time:
+// the same exchanges in total, but 2/G of the partial scores live at once
+// (G = 8 with 16 rows: 32 instead of 128 registers, 144 VGPRs in all
+// instead of 256, so three waves fit a SIMD instead of one), and a pass of
+// padding heads only is skipped.
+// ---------------------------------------------------------------------------
+template <int D, int G, int SMAX, bool PF32>
+__device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX], const u32x4 (&vr)[SMAX],
+                                            int S, float scale, int lane, uint16_t* lds_p, float (&acc)[G][8],
+                                            int active = G) {
+  constexpr int LPH = D / 8;                 // lanes per KV head
+  constexpr int VP = G * kMaxSeq;            // LDS slots per KV head
+  // Query heads per score pass: 2 for G = 4, 8 at D <= 128 (µs, B=30720
+  // Hkv=16 D=128, 1 / 2 / 4 / 8 heads per pass: G=5 S=16 1155/831/860/857,
+  // G=7 S=16 1299/932/927/919; Hq=40 Hkv=8 with Poisson(4) lengths
+  // 224/218/226/254; one head per pass leaves too little independent work
+  // to hide the exchanges' latency), all G at D = 256 (G=6 S=16 Hkv=8:
+  // 657/499/490/484).
+  constexpr int GH = G >= 4 ? (D == 256 ? G : 2) : G;
+  const int hkl = lane / LPH;
+
+#pragma unroll
+  for (int g0 = 0; g0 < G; g0 += GH) {
+    if (g0 >= active) break;
+    u32x4 qs[GH];
+#pragma unroll
+    for (int i = 0; i < GH; ++i) qs[i] = qv[g0 + i];
+    score_softmax<D, GH, SMAX, PF32, VP>(qs, kr, S, scale, lane, lds_p, g0, active - g0);
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+
+  if constexpr (!PF32) {
+    uint16_t* lds_head = lds_p + hkl * VP;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -442,21 +501,16 @@ __device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&
         pp[g][jp] = w2;
       }
     }
-    accumulate_pv<G, SMAX>(vr, pp, acc);
+    accumulate_pv<G, SMAX>(vr, pp, acc, active);
   } else {
-    // ---- fp32 weights -> LDS slot [hkl][g*16 + j] (4 bytes each) ----
-    float* lds_head = reinterpret_cast<float*>(lds_p) + hkl * VP;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int vi = blk * W + w;
-      lds_head[(vi / SMAX) * kMaxSeq + vi % SMAX] = p[w];
-    }
+    const float* lds_head = reinterpret_cast<const float*>(lds_p) + hkl * VP;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- P.V row by row in row order, one fused multiply-add per element ----
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+      if (g >= active) continue;
 #pragma unroll
       for (int j = 0; j < SMAX; ++j) {
         const float w = lds_head[g * kMaxSeq + j];
@@ -543,7 +597,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
@@ -716,7 +770,7 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -807,7 +861,7 @@ __device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uin
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc);
+  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
   for (int g = 0; g < G; ++g)

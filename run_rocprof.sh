@@ -4,7 +4,12 @@
 #   ./run_rocprof.sh [OUTDIR] [WORKLOAD]
 #     OUTDIR    default gpurun_out/rocprof
 #     WORKLOAD  bench (default: bench.py's headline workload, BASELINE C2),
-#               bN (BASELINE config N, 1..5) or rN (the reference's config N, 0..4)
+#               bN (BASELINE config N, 1..5), bNv (the same through the
+#               cu_seqlens entry point fmha_decode_fwd), rN (the reference's
+#               config N, 0..4, Poisson lengths through fmha_decode_fwd) or gN
+#               (tests/fmha_host.py's GQA suite, config N, 1..8)
+#     KERNEL    (environment) regular expression of the kernel summarised,
+#               default fmha_decode:: (every kernel of the library)
 #
 # Runs rocprofv3 once per pass (kernel trace; FETCH_SIZE; WRITE_SIZE; busy
 # counters; cache/LDS counters; FETCH_SIZE and WRITE_SIZE of a 1 GiB copy for
@@ -23,6 +28,10 @@ case "$WL" in
   bench) CMD=(python3 "$ROOT/bench.py" --no-cpu --rotate 1); TRACE_ARGS=(--steps 50 --warmup 5); PMC_ARGS=(--steps 3 --warmup 1) ;;
   b[1-5]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#b}" --suite baseline --validate none)
           TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
+  b[1-5]v) N=${WL#b}; CMD=(python3 "$ROOT/tests/fmha_host.py" "${N%v}" --suite baseline --validate none --varlen)
+          TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
+  g[1-8]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#g}" --suite gqa --validate none)
+          TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
   r[0-4]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#r}" --suite reference --validate none)
           TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
   *) echo "unknown workload $WL"; exit 2 ;;
@@ -35,7 +44,8 @@ from tests.fmha_host import SUITES, algorithmic_bytes
 if wl == "bench":
     B, Hq, Hkv, S, D, _ = SUITES["baseline"][2]
 else:
-    B, Hq, Hkv, S, D, _ = SUITES["baseline" if wl[0] == "b" else "reference"][int(wl[1:])]
+    suite = {"b": "baseline", "r": "reference", "g": "gqa"}[wl[0]]
+    B, Hq, Hkv, S, D, _ = SUITES[suite][int(wl[1:].rstrip("v"))]
 if S is None:
     import oracle
     rows = int(oracle.generate_seqlens(B, 16).sum())
@@ -59,5 +69,6 @@ pass_ busy 120 --pmc SQ_WAVES SQ_INSTS_VALU SQ_INSTS_VMEM_RD SQ_INSTS_SALU SQ_AC
 pass_ cache 120 --pmc TCC_HIT_sum TCC_MISS_sum SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT --output-format csv -d "$OUT/cache" -o run -- "${CMD[@]}" "${PMC_ARGS[@]}"
 pass_ calib_fetch 120 --pmc FETCH_SIZE --output-format csv -d "$OUT/calib_fetch" -o run -- python3 "$ROOT/tests/profiling/calib_copy.py"
 pass_ calib_write 120 --pmc WRITE_SIZE --output-format csv -d "$OUT/calib_write" -o run -- python3 "$ROOT/tests/profiling/calib_copy.py"
-python3 "$ROOT/tests/profiling/summarize.py" "$OUT" --bytes "$BYTES" --label "fmha_decode_fwd_kernel, workload $WL" \
+KRE=${KERNEL:-fmha_decode::}
+python3 "$ROOT/tests/profiling/summarize.py" "$OUT" --bytes "$BYTES" --kernel "$KRE" --label "workload $WL" \
   --command "./run_rocprof.sh gpurun_out/rocprof_$WL $WL"
