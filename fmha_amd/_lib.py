@@ -7,7 +7,10 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libfmha_decode.so")
+# FMHA_DECODE_LIB selects another build of the same sources (the
+# host-sanitizer build of tests/test_sanitizers.py); by default the in-tree
+# library that fmha_amd/_build.py writes.
+LIB_PATH = os.environ.get("FMHA_DECODE_LIB") or os.path.join(_HERE, "libfmha_decode.so")
 
 # Every symbol include/fmha_decode.h declares.
 EXPORTED = (

@@ -20,7 +20,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# FMHA_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of tests/test_sanitizers.py).
+LIB_PATH = os.environ.get("FMHA_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_LIB_PATH = os.path.join(HERE, "_ref", "libfmha_ref.so")
 
 # Floor of the half-width of the relative perturbation of a softmax weight

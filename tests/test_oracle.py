@@ -390,7 +390,7 @@ def test_f64_bound_is_tight_enough_to_catch_mistakes():
 
 def _build_mutant(tmp_path, n):
     import subprocess
-    src = os.path.join(os.path.dirname(oracle.LIB_PATH), "fmha_oracle.cpp")
+    src = os.path.join(oracle.HERE, "fmha_oracle.cpp")
     out = os.path.join(str(tmp_path), f"liboracle_mutant{n}.so")
     subprocess.run(["g++", "-O2", "-std=c++17", "-fopenmp", "-fPIC", "-shared", f"-DORACLE_MUTANT={n}", "-o", out,
                     src], check=True)
