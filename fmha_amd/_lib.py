@@ -16,6 +16,7 @@ LIB_PATH = os.environ.get("FMHA_DECODE_LIB") or os.path.join(_HERE, "libfmha_dec
 EXPORTED = (
     "fmha_decode_fwd",
     "fmha_decode_fwd_fp32_weights",
+    "fmha_decode_fwd_exact",
     "fmha_decode_fwd_uniform",
     "fmha_decode_fwd_strided",
     "fmha_decode_fwd_paged",
@@ -46,6 +47,8 @@ def load():
     lib.fmha_decode_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_fp32_weights.restype = ctypes.c_int
     lib.fmha_decode_fwd_fp32_weights.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_fwd_exact.restype = ctypes.c_int
+    lib.fmha_decode_fwd_exact.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_uniform.restype = ctypes.c_int
     lib.fmha_decode_fwd_uniform.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
     i64 = ctypes.c_int64

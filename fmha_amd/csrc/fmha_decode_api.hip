@@ -130,10 +130,14 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
 // Fills the layout-independent fields, picks the wave cap and launches.
 // rows16: 16 x the KV rows per batch used to size the per-CU wave cap (the
 // uniform length, or an estimate when lengths live on the device, which
-// device_lengths says); fp32_weights selects the fp32-weight kernels
-// (packed layout only).
+// device_lengths says); numerics selects the fp32-weight or the
+// exact-arithmetic kernels (packed layout only; exact: G = 1).
+enum class Numerics { kBf16Weights, kFp32Weights, kExact };
+
 int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows16,
-           bool device_lengths, bool fp32_weights = false) {
+           bool device_lengths, Numerics numerics = Numerics::kBf16Weights) {
+  const bool fp32_weights = numerics == Numerics::kFp32Weights;
+  const bool exact = numerics == Numerics::kExact;
   const int heads_per_wave = kWaveSize / (dq / 8);
   const int64_t upb = (a.num_heads_kv + heads_per_wave - 1) / heads_per_wave;
   const int64_t units = upb * batch;
@@ -154,6 +158,8 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
+  if (exact && (layout != fmha_decode::kLayoutPacked || g != 1))
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "the exact kernels read the packed layout with G = 1");
   // Fewer KV heads than a wave holds: R batches per wave, every lane busy
   // (paged: per-lane page lookups and addresses).  Strided only when R
   // batches' spans fit one descriptor.
@@ -164,6 +170,23 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
     const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (rows - 1) * a.row_stride +
                           (int64_t)(a.num_heads_kv - 1) * a.head_stride + dq) * 2;
     multi = span < (int64_t(1) << 30);
+  }
+  if (exact) {
+    if (multi) {
+      int hs = 0;
+      while ((1 << hs) < a.num_heads_kv) ++hs;
+      a.sub_shift = shift;
+      a.hkv_shift = hs;
+      a.units_per_batch = batch;
+      a.total_units = (uint32_t)(((int64_t)batch + (1 << shift) - 1) >> shift);
+    }
+    switch (dq) {
+      case 64: err = launch_exact<64>(a, multi, sb, w, s); break;
+      case 128: err = launch_exact<128>(a, multi, sb, w, s); break;
+      default: err = launch_exact<256>(a, multi, sb, w, s); break;
+    }
+    if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+    return FMHA_DECODE_SUCCESS;
   }
   if (multi) {
     int hs = 0;
@@ -489,7 +512,31 @@ extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const v
   a.head_stride = head_dim_q;
   a.rows_feedback = feedback_word(stream);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
-                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, true);
+                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, Numerics::kFp32Weights);
+}
+
+extern "C" int fmha_decode_fwd_exact(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                     const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                                     int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                     float softmax_scale) {
+  g_detail[0] = '\0';
+  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                        softmax_scale, false);
+  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
+  if (num_heads_q != num_heads_kv)
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
+                  "the exact path computes one query head per KV head (num_heads_q == num_heads_kv; got %d and %d)",
+                  num_heads_q, num_heads_kv);
+  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
+  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
+    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
+  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
+  a.lens = cu_seqlens_kv;
+  a.row_stride = num_heads_kv * head_dim_q;
+  a.head_stride = head_dim_q;
+  a.rows_feedback = feedback_word(stream);
+  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
+                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, Numerics::kExact);
 }
 
 extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,

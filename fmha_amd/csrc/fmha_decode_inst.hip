@@ -6,7 +6,7 @@
 // padding); every other part instantiates launchers, and with them kernels,
 // that no other part does.
 //
-// FMHA_DECODE_PARTS 51
+// FMHA_DECODE_PARTS 54
 #ifndef FMHA_DECODE_PART
 #error "compile with -DFMHA_DECODE_PART=<part>"
 #endif
@@ -181,6 +181,12 @@ template hipError_t launch_split_group_d<256, kLayoutStrided>(const SplitArgs&, 
 template hipError_t launch_split_group_d<256, kLayoutPaged>(const SplitArgs&, hipStream_t);
 #elif FMHA_DECODE_PART == 50
 template hipError_t launch_split_group_d<256, kLayoutPagedBlock>(const SplitArgs&, hipStream_t);
+#elif FMHA_DECODE_PART == 51
+template hipError_t launch_exact<64>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 52
+template hipError_t launch_exact<128>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 53
+template hipError_t launch_exact<256>(const DecodeArgs&, bool, int, int, hipStream_t);
 #else
 #error "FMHA_DECODE_PART out of range"
 #endif

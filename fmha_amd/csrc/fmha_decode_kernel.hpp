@@ -527,9 +527,271 @@ __device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&
 }
 
 // ---------------------------------------------------------------------------
+// The reference CPU loop's arithmetic, step for step (fmha_host.cpp:179-244):
+// every score a float32 sum over dims 0, 1, ..., D-1 in order, each product
+// exact (bf16 x bf16) and each addition rounded; scale; max; exponentials
+// rounded once from a double evaluation; their sum in row order; IEEE
+// division; the weight rounded to bf16; O a float32 sum over rows in order,
+// each product exact, then rounded to fp16.  The outputs are the loop's bits
+// wherever its expf returns the nearest float.
+//
+// A bf16 x bf16 product is exact in float32, so fma(x, y, acc) is the loop's
+// acc + x * y with its one rounding.  (v_dot2_f32_bf16 with a zero partner
+// is not: it differed from the loop on a few outputs per million at logit
+// spreads of 2-4.)
+//
+// Data movement: the K rows a wave loaded as 16-byte chunks per lane go
+// through LDS so that one lane holds a whole row, [head][row][dims] with a
+// 16-byte pad per row (NSTAGE = 2 stages of D / 2 dims halve that LDS: K row
+// j is then loaded as the chunk exact_k_chunk(r, j), so that every lane
+// writes half its rows in each stage and holds only the other half while
+// the first stage's dims are summed); the query vectors go to LDS as
+// float32, one word per dim.  Lanes take the (head, query head, row) scores
+// in turn, SMAX consecutive lanes per head and query head, so the masked
+// max is an exchange within those lanes and the sum of exponentials a
+// sequential read of SMAX values from LDS.  P.V: one fma per output element
+// and row, rows in order.
+// ---------------------------------------------------------------------------
+
+// 16-byte chunk of K row j that lane r of a head loads for the exact path's
+// NSTAGE-stage staging: r itself for one stage; for two, r or its partner in
+// the other half of the row, alternating with j.
+template <int D, int NSTAGE>
+__device__ __forceinline__ int exact_k_chunk(int r, int j) {
+  static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two stages");
+  return NSTAGE == 1 ? r : (r + (D / 16) * (j & 1)) % (D / 8);
+}
+
+template <int D, int G, int SMAX, int NSTAGE>
+struct ExactLayout {
+  static constexpr int LPH = D / 8;
+  static constexpr int HPW = kWaveSize / LPH;
+  static constexpr int CH = LPH / NSTAGE;       // 16-byte chunks per row and stage
+  static constexpr int KRS = CH * 16 + 16;      // LDS bytes per staged K row
+  static constexpr int QRS = D * 4 + 16;        // LDS bytes per query vector (a word per dim)
+  static constexpr int K_BYTES = HPW * SMAX * KRS;
+  static constexpr int Q_BYTES = HPW * G * QRS;
+  static constexpr int E_BYTES = HPW * G * SMAX * 4;
+  static constexpr int BYTES = K_BYTES + Q_BYTES + E_BYTES;
+};
+
+// lds: LDS of the weights (VP bf16 slots per KV head, as decode_core), then
+// ExactLayout::BYTES of staging.  GROUP_S: the lane groups serve different
+// batches, so a score lane takes the length of the head it scores from that
+// head's lanes.
+template <int D, int G, int SMAX, int NSTAGE, bool GROUP_S>
+__device__ __forceinline__ void decode_core_exact(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX],
+                                                  const u32x4 (&vr)[SMAX], int S, float scale, int lane,
+                                                  uint16_t* lds_p, float (&acc)[G][8]) {
+  // Every multiply and add below rounds on its own, as in the loop restated
+  // (the compiler would otherwise fuse t = s * scale into t - max).
+#pragma clang fp contract(off)
+  using L = ExactLayout<D, G, SMAX, NSTAGE>;
+  constexpr int LPH = L::LPH;
+  constexpr int VP = G * kMaxSeq;
+  constexpr int N = L::HPW * G * SMAX;          // scores of the wave
+  constexpr int NSLOT = (N + kWaveSize - 1) / kWaveSize;
+  constexpr int RS = ilog2(SMAX);               // row steps of the max exchange
+  unsigned char* ks = reinterpret_cast<unsigned char*>(lds_p + L::HPW * VP);
+  unsigned char* qz = ks + L::K_BYTES;
+  float* es = reinterpret_cast<float*>(qz + L::Q_BYTES);
+  const int r = lane % LPH;
+  const int hkl = lane / LPH;
+
+  // ---- the query as float32 words, one per dim ----
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    unsigned char* dst = qz + (hkl * G + g) * L::QRS + r * 32;
+    const u32x4 lo = {qv[g][0] << 16, qv[g][0] & 0xffff0000u, qv[g][1] << 16, qv[g][1] & 0xffff0000u};
+    const u32x4 hi = {qv[g][2] << 16, qv[g][2] & 0xffff0000u, qv[g][3] << 16, qv[g][3] & 0xffff0000u};
+    *reinterpret_cast<u32x4*>(dst) = lo;
+    *reinterpret_cast<u32x4*>(dst + 16) = hi;
+  }
+
+  // ---- this lane's scores: slot s is score sigma = lane + 64 s ----
+  int sj[NSLOT], sh[NSLOT], sg[NSLOT];
+  float sacc[NSLOT];
+#pragma unroll
+  for (int sl = 0; sl < NSLOT; ++sl) {
+    const int sigma = lane + kWaveSize * sl;
+    const int c = sigma / SMAX;                 // (head, query head) pair
+    sj[sl] = sigma % SMAX;
+    sg[sl] = c % G;
+    sh[sl] = (c / G) % L::HPW;                  // in range for slots past N (unused)
+    sacc[sl] = 0.0f;
+  }
+
+  // Two stages: the lane's chunk of row j belongs to stage (r / CH + j) % 2,
+  // so in stage 0 it writes rows j = 2i + u (u = r / CH) and keeps rows
+  // 2i + 1 - u for stage 1.
+  constexpr int NH = NSTAGE == 2 ? SMAX / 2 : 1;
+  u32x4 rest[NH];
+  const int u = NSTAGE == 2 ? r / L::CH : 0;
+#pragma unroll
+  for (int st = 0; st < NSTAGE; ++st) {
+    if (st > 0) {  // every lane is done with the previous stage's rows
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if constexpr (NSTAGE == 1) {
+#pragma unroll
+      for (int j = 0; j < SMAX; ++j) *reinterpret_cast<u32x4*>(ks + (hkl * SMAX + j) * L::KRS + r * 16) = kr[j];
+    } else {
+      static_assert(NSTAGE != 2 || SMAX % 2 == 0, "two stages need an even bucket");
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        const int j = 2 * i + (st == 0 ? u : 1 - u);
+        u32x4 val;
+        if (st == 0) {
+          val = u ? kr[2 * i + 1] : kr[2 * i];
+          rest[i] = u ? kr[2 * i] : kr[2 * i + 1];
+          // selected here, so that kr is dead once stage 0 is written
+          asm volatile("" : "+v"(rest[i]));
+        } else {
+          val = rest[i];
+        }
+        *reinterpret_cast<u32x4*>(ks + (hkl * SMAX + j) * L::KRS + (r % L::CH) * 16) = val;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int sl = 0; sl < NSLOT; ++sl) {
+      if (lane + kWaveSize * sl >= N) continue;
+      const unsigned char* krow = ks + (sh[sl] * SMAX + sj[sl]) * L::KRS;
+      const unsigned char* qrow = qz + (sh[sl] * G + sg[sl]) * L::QRS + st * L::CH * 32;
+      float a = sacc[sl];
+#pragma unroll
+      for (int cc = 0; cc < L::CH; ++cc) {
+        const u32x4 k = *reinterpret_cast<const u32x4*>(krow + cc * 16);
+        const u32x4 q0 = *reinterpret_cast<const u32x4*>(qrow + cc * 32);
+        const u32x4 q1 = *reinterpret_cast<const u32x4*>(qrow + cc * 32 + 16);
+        const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t kp = k[i];
+          a = __builtin_fmaf(__builtin_bit_cast(float, qw[2 * i]), __builtin_bit_cast(float, kp << 16), a);
+          a = __builtin_fmaf(__builtin_bit_cast(float, qw[2 * i + 1]), __builtin_bit_cast(float, kp & 0xffff0000u), a);
+        }
+      }
+      sacc[sl] = a;
+    }
+  }
+
+  // ---- softmax: max over the pair's SMAX lanes, exponentials, ----
+  // ---- their sum in row order through LDS, the bf16 weights    ----
+  float se[NSLOT];
+  bool sv[NSLOT];
+#pragma unroll
+  for (int sl = 0; sl < NSLOT; ++sl) {
+    const int Sh = GROUP_S ? __shfl(S, sh[sl] * LPH, kWaveSize) : S;
+    sv[sl] = lane + kWaveSize * sl < N && sj[sl] < Sh;
+    const float t = sacc[sl] * scale;
+    float m = sv[sl] ? t : -__builtin_inff();
+    m = GroupReduce<SMAX, 0, RS, true>::run(m);
+    se[sl] = sv[sl] ? (float)exp((double)(t - m)) : 0.0f;
+    if (lane + kWaveSize * sl < N) es[lane + kWaveSize * sl] = se[sl];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int sl = 0; sl < NSLOT; ++sl) {
+    if (lane + kWaveSize * sl >= N) continue;
+    const float* row = es + ((lane + kWaveSize * sl) / SMAX) * SMAX;
+    float sum = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < SMAX; ++jj) sum += row[jj];
+    const float p = sv[sl] ? se[sl] / sum : 0.0f;
+    lds_p[sh[sl] * VP + sg[sl] * kMaxSeq + sj[sl]] = __builtin_bit_cast(uint16_t, (__bf16)p);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- P.V: rows in order, one exact product per element and row ----
+  // (rows at or past S have weight 0 and V 0: adding +0 changes nothing)
+  const uint16_t* wrow = lds_p + hkl * VP;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+      const uint32_t w = wrow[g * kMaxSeq + j];
+      const float wf = __builtin_bit_cast(float, w << 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t vp = vr[j][i];
+        acc[g][2 * i] = __builtin_fmaf(wf, __builtin_bit_cast(float, vp << 16), acc[g][2 * i]);
+        acc[g][2 * i + 1] = __builtin_fmaf(wf, __builtin_bit_cast(float, vp & 0xffff0000u), acc[g][2 * i + 1]);
+      }
+    }
+    // The sums leave as float32 values: without this the compiler fuses the
+    // last multiply-add with the caller's fp16 conversion (v_fma_mix), one
+    // rounding where the loop restated has two.
+#pragma unroll
+    for (int d = 0; d < 8; ++d) asm volatile("" : "+v"(acc[g][d]));
+  }
+}
+
+// Stages of the exact path's K staging.  Kernels that choose the bucket per
+// wave (VARLEN) size their LDS for the longest bucket; there bucket 16
+// stages in two halves, which keeps that size near bucket 8's (11.7 KiB per
+// wave at D = 128 against 19.9 KiB in one stage).
+__device__ __forceinline__ constexpr int exact_stages(int smax, bool varlen) { return varlen && smax >= 16 ? 2 : 1; }
+
+// Whether a bucket takes the exact path: kernels instantiated for it (one
+// query head per KV head, bf16 weights) and more than one row (one row has
+// weight 1 and output fp16(V) on either path).
+template <int G, int SMAX, bool PF32, bool EXACT>
+__device__ __forceinline__ constexpr bool exact_taken() {
+  static_assert(!EXACT || (G == 1 && !PF32), "the exact path computes one query head per KV head, bf16 weights");
+  return EXACT && SMAX > 1;
+}
+
+// LDS bytes past the weights that the exact path of buckets 2 .. SMAX_TOP
+// stages through (0 when no bucket takes it).
+template <int D, int G, int SMAX_TOP, bool PF32, bool VARLEN, bool EXACT>
+__device__ __forceinline__ constexpr int exact_extra_bytes() {
+  if constexpr (!exact_taken<G, SMAX_TOP, PF32, EXACT>()) {
+    return 0;
+  } else {
+    int m = ExactLayout<D, G, SMAX_TOP, exact_stages(SMAX_TOP, VARLEN)>::BYTES;
+    if constexpr (VARLEN && SMAX_TOP > 2) {
+      const int n = exact_extra_bytes<D, G, SMAX_TOP / 2, PF32, VARLEN, EXACT>();
+      m = n > m ? n : m;
+    }
+    return m;
+  }
+}
+
+// Byte offset of the K chunk lane r loads for row j, relative to chunk r.
+template <int D, int G, int SMAX, bool PF32, bool VARLEN, bool EXACT>
+__device__ __forceinline__ uint32_t exact_k_delta(int r, int j) {
+  if constexpr (exact_taken<G, SMAX, PF32, EXACT>())
+    return (uint32_t)((exact_k_chunk<D, exact_stages(SMAX, VARLEN)>(r, j) - r) * 16);
+  return 0u;
+}
+
+// decode_core, or the exact core for the buckets that take it.
+template <int D, int G, int SMAX, bool PF32, bool GROUP_S, bool VARLEN, bool EXACT>
+__device__ __forceinline__ void decode_core_any(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX],
+                                                const u32x4 (&vr)[SMAX], int S, float scale, int lane,
+                                                uint16_t* lds_p, float (&acc)[G][8], int active) {
+  if constexpr (exact_taken<G, SMAX, PF32, EXACT>()) {
+    decode_core_exact<D, G, SMAX, exact_stages(SMAX, VARLEN), GROUP_S>(qv, kr, vr, S, scale, lane, lds_p, acc);
+  } else {
+    decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, scale, lane, lds_p, acc, active);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // One wave, one (batch, group of HPW KV heads), KV bucket SMAX >= S.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX, int LAYOUT, bool PF32>
+template <int D, int G, int SMAX, int LAYOUT, bool PF32, bool VARLEN, bool EXACT>
 __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, const KVSpan& kv, int hk,
                                             bool head_ok, int lane, uint16_t* lds_p) {
   constexpr int LPH = D / 8;  // lanes per KV head
@@ -567,7 +829,9 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   u32x4 vr[SMAX];
   if constexpr (LAYOUT != kLayoutPaged) {
 #pragma unroll
-    for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + row_off[j]);
+    for (int j = 0; j < SMAX; ++j)
+      kr[j] = buffer_load16<kPolicyStream>(
+          k_rsrc, kv_off + row_off[j] + (head_ok ? exact_k_delta<D, G, SMAX, PF32, VARLEN, EXACT>(r, j) : 0u));
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
   } else {
@@ -587,7 +851,9 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
     }
 #pragma unroll
     for (int j = 0; j < SMAX; ++j)
-      kr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.k + row_elem[j], row_rec[j]), kv_off);
+      kr[j] = buffer_load16<kPolicyStream>(
+          make_rsrc(kv.k + row_elem[j], row_rec[j]),
+          kv_off + (head_ok ? exact_k_delta<D, G, SMAX, PF32, VARLEN, EXACT>(r, j) : 0u));
 #pragma unroll
     for (int j = 0; j < SMAX; ++j)
       vr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.v + row_elem[j], row_rec[j]), kv_off);
@@ -597,7 +863,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
+  decode_core_any<D, G, SMAX, PF32, false, VARLEN, EXACT>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
 
   // ---- fp16 (RNE) output, 16 bytes per lane per query head ----
 #pragma unroll
@@ -670,13 +936,14 @@ __device__ __forceinline__ bool batch_span(const DecodeArgs& a, uint32_t b, KVSp
 // row in row order (the semantics of the reference's fmha_vectorized_fma,
 // fmha_vectorized_fma_kernel.hpp:243-296); otherwise weights rounded to bf16
 // (the reference CPU loop and fmha_mfma_4x4x4).
-template <int D, int G, int LAYOUT, int SB, bool PF32 = false>
+template <int D, int G, int LAYOUT, int SB, bool PF32 = false, bool EXACT = false>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeArgs a) {
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
   constexpr int VP = G * kMaxSeq;
   constexpr int WB = PF32 ? 2 : 1;  // 16-bit LDS words per weight
-  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP * WB];
+  constexpr int XW = exact_extra_bytes<D, G, SB == 0 ? kMaxSeq : SB, PF32, SB == 0, EXACT>() / 2;  // exact staging
+  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * (HPW * VP * WB + XW)];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -687,7 +954,7 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
   const uint32_t hg = unit - b * upb;
   const int hk = (int)hg * HPW + lane / LPH;
   const bool head_ok = hk < a.num_heads_kv;
-  uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
+  uint16_t* lds_wave = lds_p + wave * (HPW * VP * WB + XW);
 
   if constexpr (SB == 0 && LAYOUT == kLayoutPacked) report_mean_rows(a, unit, a.total_units / upb, lane);
   KVSpan kv;
@@ -702,19 +969,19 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
     return;
   }
   if constexpr (SB != 0) {
-    decode_unit<D, G, SB, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+    decode_unit<D, G, SB, LAYOUT, PF32, false, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
   } else {
     const int S = kv.S;
     if (S <= 1) {
-      decode_unit<D, G, 1, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 1, LAYOUT, PF32, true, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 2) {
-      decode_unit<D, G, 2, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 2, LAYOUT, PF32, true, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 4) {
-      decode_unit<D, G, 4, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 4, LAYOUT, PF32, true, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else if (S <= 8) {
-      decode_unit<D, G, 8, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 8, LAYOUT, PF32, true, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
     } else {
-      decode_unit<D, G, 16, LAYOUT, PF32>(a, b, kv, hk, head_ok, lane, lds_wave);
+      decode_unit<D, G, 16, LAYOUT, PF32, true, EXACT>(a, b, kv, hk, head_ok, lane, lds_wave);
     }
   }
 }
@@ -734,7 +1001,7 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
 // One wave of R batches, bucket SMAX.  kbase/vbase: the wave's first batch;
 // records: the descriptor range over the R batches; lane_rows: byte offset
 // of this lane group's batch from kbase; S: its length (0 when invalid).
-template <int D, int G, int SMAX, bool PF32>
+template <int D, int G, int SMAX, bool PF32, bool EXACT>
 __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t b0, uint32_t nb, const uint16_t* kbase,
                                                   const uint16_t* vbase, uint32_t records, uint32_t lane_rows, int S,
                                                   bool bad, bool lane_ok, int sub, int hk, int lane,
@@ -764,13 +1031,15 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
 #pragma unroll
-  for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + row_off[j]);
+  for (int j = 0; j < SMAX; ++j)
+    kr[j] = buffer_load16<kPolicyStream>(
+        k_rsrc, kv_off + row_off[j] + (lane_ok ? exact_k_delta<D, G, SMAX, PF32, true, EXACT>(r, j) : 0u));
 #pragma unroll
   for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
+  decode_core_any<D, G, SMAX, PF32, true, true, EXACT>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -861,7 +1130,7 @@ __device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uin
   __builtin_amdgcn_sched_barrier(0);
 
   float acc[G][8];
-  decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
+  decode_core_any<D, G, SMAX, PF32, true, true, false>(qv, kr, vr, S, a.scale, lane, lds_p, acc, grp);
   const u32x4 nan4 = {0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -871,13 +1140,15 @@ __device__ __forceinline__ void decode_multi_unit_paged(const DecodeArgs& a, uin
 // a.units_per_batch holds the batch count here, a.total_units the waves
 // (ceil(batch / R)); lengths from a.lens (packed: offsets, strided and
 // paged: lengths) or a.seqlen_uniform when a.lens is null (not paged).
-template <int D, int G, int LAYOUT, bool PF32 = false>
+template <int D, int G, int LAYOUT, bool PF32 = false, bool EXACT = false>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(DecodeArgs a) {
+  static_assert(!EXACT || LAYOUT != kLayoutPaged, "the exact path reads the packed and strided layouts");
   constexpr int LPH = D / 8;
   constexpr int HPW = kWaveSize / LPH;
   constexpr int VP = G * kMaxSeq;
   constexpr int WB = PF32 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * HPW * VP * WB];
+  constexpr int XW = exact_extra_bytes<D, G, kMaxSeq, PF32, true, EXACT>() / 2;  // exact staging
+  __shared__ __attribute__((aligned(16))) uint16_t lds_p[kWavesPerBlock * (HPW * VP * WB + XW)];
   const int lane = threadIdx.x & (kWaveSize - 1);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const uint32_t unit = blockIdx.x * kWavesPerBlock + wave;
@@ -949,13 +1220,13 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(Decode
   }
   smax = __builtin_amdgcn_readfirstlane(smax);
   if constexpr (LAYOUT == kLayoutPacked) records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
-  uint16_t* lds_wave = lds_p + wave * HPW * VP * WB;
+  uint16_t* lds_wave = lds_p + wave * (HPW * VP * WB + XW);
 #define FMHA_DECODE_MULTI(SM)                                                                                      \
   if constexpr (LAYOUT == kLayoutPaged)                                                                              \
     decode_multi_unit_paged<D, G, SM, PF32>(a, b0, nb, b, S, bad, lane_ok, sub, hk, lane, lds_wave);                \
   else                                                                                                               \
-    decode_multi_unit<D, G, SM, PF32>(a, b0, nb, kbase, vbase, records, lane_rows, S, bad, lane_ok, sub, hk, lane, \
-                                      lds_wave)
+    decode_multi_unit<D, G, SM, PF32, EXACT>(a, b0, nb, kbase, vbase, records, lane_rows, S, bad, lane_ok, sub, hk, \
+                                             lane, lds_wave)
   if (smax <= 1)
     FMHA_DECODE_MULTI(1);
   else if (smax <= 2)

@@ -85,9 +85,9 @@ size_t lds_reserve_kernel(int waves) {
   return lds_reserve_for(waves, lds_per_cu(), static_lds<KERNEL>());
 }
 
-template <int D, int G, int LAYOUT, int SB, bool PF32>
+template <int D, int G, int LAYOUT, int SB, bool PF32, bool EXACT = false>
 hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32>;
+  constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32, EXACT>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
@@ -96,18 +96,19 @@ hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream)
 // sb: 0 = lengths from a.lens (bucket picked per wave), else the uniform
 // length's power-of-two bucket.  The paged layout always reads lengths.
 // PF32: fp32 softmax weights (instantiated for the packed layout only).
-template <int D, int G, int LAYOUT, bool PF32>
+// EXACT: the exact-arithmetic kernels (packed layout, G = 1).
+template <int D, int G, int LAYOUT, bool PF32, bool EXACT = false>
 hipError_t launch_bucket(const DecodeArgs& a, int sb, int w, hipStream_t stream) {
   if constexpr (LAYOUT == fmha_decode::kLayoutPaged) {
-    return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
+    return launch_one<D, G, LAYOUT, 0, PF32, EXACT>(a, w, stream);
   } else {
     switch (sb) {
-      case 0: return launch_one<D, G, LAYOUT, 0, PF32>(a, w, stream);
-      case 1: return launch_one<D, G, LAYOUT, 1, PF32>(a, w, stream);
-      case 2: return launch_one<D, G, LAYOUT, 2, PF32>(a, w, stream);
-      case 4: return launch_one<D, G, LAYOUT, 4, PF32>(a, w, stream);
-      case 8: return launch_one<D, G, LAYOUT, 8, PF32>(a, w, stream);
-      default: return launch_one<D, G, LAYOUT, 16, PF32>(a, w, stream);
+      case 0: return launch_one<D, G, LAYOUT, 0, PF32, EXACT>(a, w, stream);
+      case 1: return launch_one<D, G, LAYOUT, 1, PF32, EXACT>(a, w, stream);
+      case 2: return launch_one<D, G, LAYOUT, 2, PF32, EXACT>(a, w, stream);
+      case 4: return launch_one<D, G, LAYOUT, 4, PF32, EXACT>(a, w, stream);
+      case 8: return launch_one<D, G, LAYOUT, 8, PF32, EXACT>(a, w, stream);
+      default: return launch_one<D, G, LAYOUT, 16, PF32, EXACT>(a, w, stream);
     }
   }
 }
@@ -131,9 +132,9 @@ hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStrea
   }
 }
 
-template <int D, int G, int LAYOUT, bool PF32>
+template <int D, int G, int LAYOUT, bool PF32, bool EXACT = false>
 hipError_t launch_multi_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32>;
+  constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32, EXACT>;
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
@@ -154,6 +155,14 @@ hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t st
     default: FMHA_DECODE_MULTI_G(256)
   }
 #undef FMHA_DECODE_MULTI_G
+}
+
+// The exact-arithmetic kernels: packed layout, one query head per KV head;
+// multi: R batches per wave (fewer KV heads than a wave holds).
+template <int D>
+hipError_t launch_exact(const DecodeArgs& a, bool multi, int sb, int w, hipStream_t stream) {
+  return multi ? launch_multi_one<D, 1, kLayoutPacked, false, true>(a, w, stream)
+               : launch_bucket<D, 1, kLayoutPacked, false, true>(a, sb, w, stream);
 }
 
 template <int D, int NS, int LAYOUT>
@@ -392,6 +401,9 @@ extern template hipError_t launch_group<256, kLayoutPacked, false>(const DecodeA
 extern template hipError_t launch_group<256, kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_group<256, kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_group<256, kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
+extern template hipError_t launch_exact<64>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<128>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<256>(const DecodeArgs&, bool, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);

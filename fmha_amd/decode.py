@@ -61,6 +61,17 @@ def launch_fmha_decode_fp32_weights(stream, Q, K, V, O, cu_seqlens_kv, batch, nu
     _raise_if(rc)
 
 
+def launch_fmha_decode_exact(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv,
+                             seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
+    """launch_fmha_decode with the reference CPU loop's arithmetic step for
+    step (fmha_host.cpp:179-244): its outputs bit for bit wherever that
+    loop's expf returns the nearest float; num_heads_q == num_heads_kv."""
+    rc = _lib.load().fmha_decode_fwd_exact(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q,
+                                           num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                           float(softmax_scale))
+    _raise_if(rc)
+
+
 def launch_fmha_decode_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv,
                                seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
     """Uniform-length decode attention (K/V as [batch, seqlen_kv, Hkv, D])."""
@@ -291,7 +302,8 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     return out
 
 
-def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None, out=None, fp32_weights=False):
+def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None, out=None, fp32_weights=False,
+                exact=False):
     """Decode attention on torch tensors; returns O (fp16, shaped like q).
 
     q: [B, Hq, 1, D] or [B, Hq, D], bfloat16, contiguous, on a GPU.
@@ -302,6 +314,9 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
       (fmha_host.cpp:371).
     fp32_weights: keep the softmax weights in fp32 (fmha_vectorized_fma's
       semantics) instead of rounding them to bf16; needs cu_seqlens_kv.
+    exact: the reference CPU loop's arithmetic step for step (its outputs
+      bit for bit wherever its expf returns the nearest float); needs
+      cu_seqlens_kv and Hq == Hkv.
     """
     import torch
 
@@ -342,12 +357,15 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
             raise ValueError("cu_seqlens_kv must be a contiguous tensor on q's device")
         if k.dim() != 3:
             raise ValueError("packed k/v must be [rows, Hkv, D]")
-        launch = launch_fmha_decode_fp32_weights if fp32_weights else launch_fmha_decode
+        if fp32_weights and exact:
+            raise ValueError("fp32_weights and exact are different numerics; pick one")
+        launch = (launch_fmha_decode_fp32_weights if fp32_weights else
+                  launch_fmha_decode_exact if exact else launch_fmha_decode)
         launch(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                cu_seqlens_kv.data_ptr(), B, Hq, Hkv, 1, D, D, softmax_scale)
     else:
-        if fp32_weights:
-            raise ValueError("fp32_weights needs the packed layout with cu_seqlens_kv")
+        if fp32_weights or exact:
+            raise ValueError("fp32_weights and exact need the packed layout with cu_seqlens_kv")
         if seqlen_kv is None:
             if k.dim() != 4 or k.shape[0] != B:
                 raise ValueError("uniform k/v must be [B, S, Hkv, D] when seqlen_kv is not given")

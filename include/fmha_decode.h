@@ -23,8 +23,8 @@
  * the null stream) and may be issued from any number of host threads.  They
  * allocate no device memory.  The one piece of library state: the entry
  * points that read lengths from a device cu_seqlens_kv array
- * (fmha_decode_fwd, fmha_decode_fwd_fp32_weights, and
- * fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
+ * (fmha_decode_fwd, fmha_decode_fwd_fp32_weights, fmha_decode_fwd_exact
+ * and fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
  * per device (64 bytes, allocated by the first such call that is not being
  * captured into a graph, never freed) in which each call's first wave leaves
  * the call's mean length; the next call sizes its launch (waves per CU) from
@@ -121,6 +121,34 @@ int fmha_decode_fwd_fp32_weights(void* stream,
                                  int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                  int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                                  float softmax_scale);
+
+/*
+ * fmha_decode_fwd computed with the arithmetic of the reference CPU loop
+ * (fmha_host.cpp:179-244) step for step, for the inputs that loop is written
+ * for (num_heads_q == num_heads_kv, lengths up to 16): each score a float32
+ * sum over d = 0, 1, ..., D-1 in order (every product exact, every addition
+ * rounded), then * softmax_scale; the max; each exponential the float
+ * nearest exp(s_j*scale - max) (evaluated in double and rounded once); their
+ * float32 sum in row order; the IEEE quotient rounded to bf16; O a float32
+ * sum over rows in order, rounded to fp16.  The outputs equal that loop's
+ * bit for bit wherever its expf returns the nearest float (glibc 2.35's
+ * expf misses it on about 0.07% of arguments, and an output can differ only
+ * where such a miss also flips a bf16 weight: none in ten million random
+ * heads).  fmha_decode_fwd sums in a tree order, uses the device expf and
+ * rounds its last multiply-add straight to fp16, so there a few outputs in
+ * ten thousand differ from the loop in the last bit.  Same arguments,
+ * layouts, checks and errors as fmha_decode_fwd, and num_heads_q !=
+ * num_heads_kv gives FMHA_DECODE_ERROR_NOT_SUPPORTED.  0.99-1.05x the time
+ * of fmha_decode_fwd on the BASELINE and reference configurations.  No
+ * counterpart in the reference, which has no GPU kernel with these results;
+ * for callers that need the CPU loop's outputs.
+ */
+int fmha_decode_fwd_exact(void* stream,
+                          const void* Q, const void* K, const void* V, void* O,
+                          const int32_t* cu_seqlens_kv,
+                          int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                          int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                          float softmax_scale);
 
 /*
  * Uniform-length decode attention: every batch has seqlen_kv KV rows, K and V

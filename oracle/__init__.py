@@ -58,6 +58,8 @@ def lib():
         L.oracle_f32_to_bf16.argtypes = [vp, i64, vp]
         L.oracle_f32_to_f16.restype = None
         L.oracle_f32_to_f16.argtypes = [vp, i64, vp]
+        L.oracle_exp_nearest.restype = None
+        L.oracle_exp_nearest.argtypes = [vp, i64, vp]
         _lib = L
     return _lib
 
@@ -73,7 +75,9 @@ def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps
            nthreads=0, max_seqlen=16, slack_fixed=False):
     """Restated reference loop.  q [B,Hq,D], k/v [rows,Hkv,D] as uint16 bf16
     bits; cu int32 [B+1]; lengths up to max_seqlen (the reference's 16 by
-    default).  Returns (o fp16 bits [B,Hq,D], slack or None).  The slack's
+    default).  p_mode 0: bf16 weights (the reference loop), 1: fp32
+    weights, 2: bf16 weights from exp_nearest in place of the C library's
+    expf.  Returns (o fp16 bits [B,Hq,D], slack or None).  The slack's
     half-width is max(slack_eps, 4x the oracle's own float32 error) per head,
     or exactly slack_eps with slack_fixed."""
     if slack_fixed:
@@ -89,6 +93,15 @@ def decode(q, k, v, cu, hq, hkv, d, scale, p_mode=0, with_slack=False, slack_eps
     if rc != 0:
         raise ValueError("oracle_decode rejected its arguments")
     return o, slack
+
+
+def exp_nearest(x):
+    """The exponential of decode(p_mode=2): float32 x -> the float nearest
+    exp(x), evaluated in double and rounded once."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oracle_exp_nearest(_p(x), x.size, _p(out))
+    return out
 
 
 def decode_f64(q, k, v, cu, hq, hkv, d, scale, nthreads=0, max_seqlen=16, with_bound=False):

@@ -96,10 +96,18 @@ inline uint16_t f32_to_f16(float f) {
   return (uint16_t)(sign | h);
 }
 
+// The float nearest exp(x): exp evaluated in double (within one double ulp)
+// and rounded once, which gives the nearest float except when the double
+// result lies within an ulp of a float rounding midpoint.
+float exp_nearest(float x) { return (float)std::exp((double)x); }
+
 // One (batch, query head) of the reference loop, fmha_host.cpp:179-244, with
 // the KV head chosen by the caller.  p_mode 0: weights rounded to bf16
 // (fmha_host.cpp:225); 1: weights kept in fp32 (the semantics of
-// fmha_vectorized_fma_kernel.hpp:256).
+// fmha_vectorized_fma_kernel.hpp:256); 2: as 0, with every exponential the
+// float nearest exp(x) (evaluated in double, rounded once) in place of the
+// C library's expf, which misses the nearest float on a few arguments in
+// ten thousand (the loop the library's exact path restates).
 void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t kv_stride, int S, int D, float scale,
               int p_mode, uint16_t* o, float* slack, double slack_eps) {
   // The reference sizes these arrays for 16 rows (fmha_host.cpp:164, :215);
@@ -120,8 +128,9 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
   for (int s = 0; s < S; s++) scores[s] *= scale;
   float maxv = -INFINITY;
   for (int s = 0; s < (ORACLE_MUTANT == 3 ? S16 : S); s++) maxv = fmaxf(maxv, scores[s]);
+  auto ex = [p_mode](float x) { return p_mode == 2 ? exp_nearest(x) : expf(x); };
   float sum_exp = 0.0f;
-  for (int s = 0; s < (ORACLE_MUTANT == 4 ? S16 : S); s++) sum_exp += expf(scores[s] - maxv);
+  for (int s = 0; s < (ORACLE_MUTANT == 4 ? S16 : S); s++) sum_exp += ex(scores[s] - maxv);
   float* p = p_buf.data();
   float* jump = jump_buf.data();
   // How far this loop's own float32 weights may sit from the exact ones:
@@ -146,8 +155,8 @@ void head_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
     eps = fmax(slack_eps, 4.0 * (2.0 * dt + dl));
   }
   for (int s = 0; s < S; s++) {
-    const float pf = expf(scores[s] - maxv) / sum_exp;
-    p[s] = p_mode == 0 ? bf16_to_f32(f32_to_bf16(pf)) : pf;
+    const float pf = ex(scores[s] - maxv) / sum_exp;
+    p[s] = p_mode != 1 ? bf16_to_f32(f32_to_bf16(pf)) : pf;
     // Size of the bf16 rounding step reachable by a relative perturbation of
     // pf by eps: non-zero only near a rounding midpoint.
     if (slack) {
@@ -224,9 +233,14 @@ void head_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t k
 
 extern "C" {
 
+// The exponential of p_mode 2 over x[0..n), for its own test.
+void oracle_exp_nearest(const float* x, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; i++) out[i] = exp_nearest(x[i]);
+}
+
 // Decode attention over a packed batch (layouts as include/fmha_decode.h).
 // cu: [batch+1] row offsets.  p_mode 0 = bf16 weights (reference CPU loop),
-// 1 = fp32 weights.  o: fp16 bits [batch, hq, d].  slack: optional float
+// 1 = fp32 weights, 2 = bf16 weights from nearest-float exponentials.  o: fp16 bits [batch, hq, d].  slack: optional float
 // [batch, hq, d] (see head_f32; slack_eps is its floor, or with a negative
 // value the fixed half-width -slack_eps).  Returns 0, or -1
 // for a length outside
@@ -236,6 +250,7 @@ int oracle_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
                   int hkv, int d, float scale, int p_mode, uint16_t* o, float* slack, double slack_eps,
                   int nthreads, int max_seqlen) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || d <= 0 || max_seqlen < 0) return -1;
+  if (p_mode < 0 || p_mode > 2) return -1;
   for (int64_t b = 0; b < batch; b++) {
     const int S = cu[b + 1] - cu[b];
     if (S < 0 || S > max_seqlen) return -1;

@@ -32,7 +32,8 @@ def lib():
 
 def test_exports_every_declared_function(lib):
     names = header_functions()
-    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_uniform",
+    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_exact",
+                          "fmha_decode_fwd_uniform",
                           "fmha_decode_fwd_strided",
                           "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
                           "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_noalloc",
@@ -66,6 +67,14 @@ def fwd32(lib, **kw):
     a.update(kw)
     return lib.fmha_decode_fwd_fp32_weights(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"],
                                             a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
+def fwd_exact(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_exact(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"],
+                                     a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
 
 
 def uni(lib, **kw):
@@ -303,10 +312,29 @@ def test_fp32_weights_rejects(lib, kw, code, needle):
     assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(batch=-1), BAD, "batch"),
+    (dict(hq=32, hkv=16), NOTSUP, "one query head per KV head"),
+    (dict(hq=16, hkv=1), NOTSUP, "one query head per KV head"),
+    (dict(hq=16, hkv=5), BAD, "multiple"),
+    (dict(sq=2), BAD, "seqlen_q"),
+    (dict(dq=96, dkv=96), BAD, "64, 128 or 256"),
+    (dict(scale=float("inf")), BAD, "finite"),
+    (dict(k=None), BAD, "non-null"),
+    (dict(o=O + 2), BAD, "aligned"),
+    (dict(cu=None), BAD, "cu_seqlens_kv"),
+    (dict(cu=CU + 2), BAD, "cu_seqlens_kv"),
+])
+def test_exact_rejects(lib, kw, code, needle):
+    assert fwd_exact(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
+
+
 def test_batch_zero_is_a_noop(lib):
     # Nothing is launched and no pointer is needed for an empty batch.
     assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert fwd32(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
+    assert fwd_exact(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
     assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
     assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0

@@ -183,6 +183,78 @@ def test_dominant_key_is_one_hot():
     assert np.array_equal(o[0], oracle.f32_to_f16(_f32(v[6])))
 
 
+# ------------------------------- nearest-float exponentials (p_mode=2): pins
+# The loop the library's exact path (fmha_decode_fwd_exact) restates:
+# p_mode 0 with exp_nearest, the float nearest exp(x), in place of the C
+# library's expf.
+def _exp_args(seed):
+    rng = np.random.default_rng(seed)
+    return np.concatenate([-rng.exponential(4.0, 200000), rng.uniform(-103.0, 88.0, 20000),
+                           [0.0, -0.0, -1e-30, 1e-30]]).astype(np.float32)
+
+
+def test_exp_nearest_is_the_nearest_float():
+    x = _exp_args(50)
+    e = oracle.exp_nearest(x)
+    t = np.exp(x.astype(np.float64))
+    assert np.array_equal(e, t.astype(np.float32))
+    err = np.abs(e.astype(np.float64) - t)
+    for side in (np.inf, -np.inf):
+        nb = np.nextafter(e, np.float32(side)).astype(np.float64)
+        assert np.all(err <= np.abs(nb - t))
+    assert oracle.exp_nearest(np.float32([0.0]))[0] == 1.0
+
+
+def test_c_library_expf_is_the_one_that_misses():
+    """Where the C library's expf and exp_nearest disagree, expf's float is
+    the farther one from exp(x) (glibc 2.35: about 7 arguments in 10 000)."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    x = _exp_args(51)[:60000]
+    g = np.array([libm.expf(float(a)) for a in x], dtype=np.float32)
+    e = oracle.exp_nearest(x)
+    t = np.exp(x.astype(np.float64))
+    miss = np.nonzero(g != e)[0]
+    print(f"expf differs from the nearest float on {len(miss)} of {len(x)} arguments")
+    assert len(miss) < len(x) // 200
+    assert np.all(np.abs(g[miss].astype(np.float64) - t[miss]) > np.abs(e[miss].astype(np.float64) - t[miss]))
+
+
+def test_nearest_exp_loop_equals_expf_loop_on_random_heads():
+    """Apart from the exponential, p_mode 2 is p_mode 0: a misrounded expf
+    changes an output only where it also flips a bf16 weight (none in ten
+    million random heads measured), so on random heads both give the same
+    bits, and so does any other change to p_mode 2 fail here."""
+    seqlens = oracle.generate_seqlens(3000, 16)
+    q, k, v, cu = make_inputs(3000, 8, 8, 128, seqlens, seed=52, std=2.0)
+    r0, _ = oracle.decode(q, k, v, cu, 8, 8, 128, default_scale(128), p_mode=0)
+    r2, _ = oracle.decode(q, k, v, cu, 8, 8, 128, default_scale(128), p_mode=2)
+    assert np.array_equal(r0, r2)
+
+
+@pytest.mark.parametrize("S", [1, 3, 16])
+def test_nearest_exp_known_answers(S):
+    """One row: fp16(V); zero query: the uniform bf16 weights bf16(1/S)."""
+    q, k, v, cu = make_inputs(2, 4, 4, 128, [S, S], seed=53 + S)
+    q[:] = 0
+    o, _ = oracle.decode(q, k, v, cu, 4, 4, 128, default_scale(128), p_mode=2)
+    w = _f32(oracle.f32_to_bf16(np.float32(1.0) / np.float32(S)))
+    for b in range(2):
+        acc = np.zeros((4, 128), np.float32)
+        for j in range(S):
+            acc = acc + w * _f32(v[cu[b] + j])
+        assert np.array_equal(o[b], oracle.f32_to_f16(acc))
+
+
+def test_unknown_p_mode_is_rejected():
+    q, k, v, cu = make_inputs(2, 4, 4, 64, [3, 3], seed=60)
+    with pytest.raises(ValueError):
+        oracle.decode(q, k, v, cu, 4, 4, 64, default_scale(64), p_mode=3)
+
+
 # ------------------------------------------- fp32 weights (p_mode=1): pins
 # The fp32-weight loop (the numerics of fmha_vectorized_fma_kernel.hpp:243-296)
 # keeps the weights unrounded; these checks would catch a stray bf16 rounding,
