@@ -28,6 +28,8 @@ Prints one JSON line:
                 lengths from a device cu_seqlens array, timed as `value` is
                 after the warm-up calls (whose first call runs under the
                 default wave cap, its time reported as first_call_us);
+  exact         the same through fmha_decode_fwd_exact, whose outputs equal
+                the reference CPU loop's bit for bit, timed as cu_seqlens;
   cpu_baseline  the reference's own CPU loop (fmha_host.cpp:158-284, built from
                 /root/reference into oracle/_ref) -- or the restated oracle
                 when that build is absent -- timed single-threaded on this
@@ -255,6 +257,22 @@ def main():
         "first_call_us": round(first_cu_ms * 1e3, 2),
     }
 
+    # Fourth leg: the exact-arithmetic entry point on the same inputs and
+    # cu_seqlens array.
+    def step_exact(ptrs=(qp, kp, vp, op)):
+        fmha_amd.launch_fmha_decode_exact(sptr, *ptrs, cup, B, Hq, Hkv, 1, D, D, scale)
+
+    for _ in range(args.warmup):
+        step_exact()
+    ex_ms = timed_loop(one_set, step_exact)
+    exact_leg = {
+        "entry_point": "fmha_decode_fwd_exact (cu_seqlens)",
+        "us_per_call": round(ex_ms * 1e3, 2),
+        "tb_s": round(nbytes / (ex_ms * 1e-3) / 1e12, 4),
+        "pct_of_peak": round(100.0 * nbytes / (ex_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        "vs_cu_entry": round(cu_ms / ex_ms, 4),
+    }
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -298,6 +316,7 @@ def main():
         },
         "rotated_inputs": rotated,
         "cu_seqlens": cu_leg,
+        "exact": exact_leg,
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }

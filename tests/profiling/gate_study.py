@@ -2,7 +2,8 @@
 """Tie-slack evidence on a whole BASELINE configuration (default C5: B=30720,
 Hq=Hkv=32, S=16, D=256, inputs N(0, 2)).
 
-Runs this library's bf16-weight and fp32-weight entry points and the
+Runs this library's bf16-weight, fp32-weight and exact (Hq == Hkv) entry
+points and the
 reference's four kernels (built from /root/reference into oracle/_ref; only
 where their indexing stays in bounds: Hq == Hkv, Hq a multiple of 16, D in
 {128, 256}, lengths in [1, 16]) on the same inputs, then compares every
@@ -66,6 +67,9 @@ def main():
         "ours_fp32_weights": lambda o: fmha_amd.launch_fmha_decode_fp32_weights(
             sp, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), cu.data_ptr(), B, Hq, Hkv, 1, D, D, scale),
     }
+    if Hq == Hkv:
+        kernels["ours_exact"] = lambda o: fmha_amd.launch_fmha_decode_exact(
+            sp, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), cu.data_ptr(), B, Hq, Hkv, 1, D, D, scale)
     ref_ok = (oracle.ref_available() and Hq == Hkv and Hq % 16 == 0 and D in (128, 256) and 1 <= S <= 16)
     if ref_ok:
         for name in ("ref_launch_mfma_4x4x4", "ref_launch_vectorized_fma", "ref_launch_mfma", "ref_launch_mfma_v3"):
