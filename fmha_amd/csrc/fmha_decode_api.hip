@@ -77,6 +77,12 @@ int valu_kernel_group(int g) {
 // 643/504/446/433/423/427; the reference's Poisson(4) lengths (mean 4.3)
 // H=16 D=128 291/233/206/198/191/191, H=16 D=256 595/460/409/393/374/376,
 // H=32 D=128 570/446/409/393/377/377, H=32 D=256 1165/918/833/812/813/817.
+// The 8-head kernel (G = 5-8) computes for longer than its short rows take
+// to load, so with a mean of 8 rows or fewer it gets every wave its
+// registers allow (8 per CU) whatever the bytes say: Hq=40 Hkv=8 D=128 with
+// those Poisson lengths, µs for 5/6/8/12 waves 217/197/181/179; Hq=64
+// Hkv=8 263 at 5, 253 at 8.  G = 2 keeps the byte count (Hq=32 Hkv=16: 227
+// at 11 against 236 at 13).
 constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
 
 int waves_per_cu_for(int rows16, int g, bool device_lengths) {
@@ -84,7 +90,7 @@ int waves_per_cu_for(int rows16, int g, bool device_lengths) {
   const int64_t budget = device_lengths ? kInflightBytesPerCUDeviceLengths : kInflightBytesPerCU;
   const int64_t w = 16 * budget / unit_bytes16;
   if (w >= 16) return kMaxWavesPerCU;
-  const int floor_w = g >= 8 ? 4 : 3;
+  const int floor_w = g >= 8 ? (device_lengths && rows16 <= 16 * 8 ? 8 : 4) : 3;
   return w < floor_w ? floor_w : (int)w;
 }
 

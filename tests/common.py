@@ -123,3 +123,24 @@ def f64_check(o_bits, t, bound):
     err[~np.isfinite(o)] = np.inf
     return {"f64_violations": int((err > bound).sum()), "f64_max_ratio": float((err / bound).max()),
             "f64_max_abs": float(err.max()), "f64_mean_abs": float(err.mean())}
+
+
+def gpu_warmup(call, min_calls=10, min_seconds=0.1):
+    """Untimed calls until at least min_calls have run and min_seconds of
+    wall time have passed, synchronising every 16 calls.  A GPU that has
+    just started working runs short kernels slower for its first tens of
+    milliseconds (Hq=40 Hkv=8 with Poisson lengths, about 0.2 ms per call:
+    70.8% of peak after 10 warm-up calls, 81.1% after 200 and 81.4% after
+    2000), so a count alone under-warms short kernels."""
+    import time
+
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_calls or time.perf_counter() - t0 < min_seconds:
+        call()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n

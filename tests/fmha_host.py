@@ -10,7 +10,8 @@ selected configuration it:
     own generator (Poisson(4) rejected outside [2, max], mt19937(42),
     fmha_host.cpp:58-72) for the reference-suite configurations;
   * times `--iters` calls (HIP events per call on the launch stream, after
-    `--warmup` calls; with --rotate N, N input sets used in turn so that a
+    at least `--warmup` calls and 0.1 s of them, tests/common.py: gpu_warmup;
+    with --rotate N, N input sets used in turn so that a
     small configuration is not served from the 256 MB MALL) and reports
     µs/call, algorithmic TB/s and % of the 8 TB/s HBM peak, counting bytes
     as fmha_host.cpp:428-430 does;
@@ -82,7 +83,7 @@ def run_config(suite, idx, args):
 
     import fmha_amd
     import oracle
-    from tests.common import ATOL, RTOL
+    from tests.common import ATOL, RTOL, gpu_warmup
 
     B, Hq, Hkv, S, D, std = SUITES[suite][idx]
     dev = torch.device("cuda", 0)
@@ -121,9 +122,13 @@ def run_config(suite, idx, args):
             fmha_amd.launch_fmha_decode(sp, qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), oo.data_ptr(),
                                         cu.data_ptr(), B, Hq, Hkv, 1, D, D, scale)
 
-    for i in range(args.warmup):
-        call(i)
-    torch.cuda.synchronize()
+    n_warm = [0]
+
+    def warm_call():
+        call(n_warm[0])
+        n_warm[0] += 1
+
+    gpu_warmup(warm_call, min_calls=args.warmup)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.iters)]
     for i, (a, b) in enumerate(ev):

@@ -6,7 +6,8 @@ For each shape (uniform lengths, bf16 N(0,1) inputs generated on the GPU)
 and each kernel choice (FMHA_DECODE_GQA_KERNEL=valu: the VALU kernel, for
 G <= 8, G = 3 and 5-7 on its 4- and 8-head instantiations; =mfma: the
 matrix-core kernel; default: the library's own choice), calls
-fmha_decode_fwd_uniform --warmup times, then times --iters calls with a HIP
+fmha_decode_fwd_uniform at least --warmup times and for at least 0.1 s
+(tests/common.py: gpu_warmup), then times --iters calls with a HIP
 event pair per call on the launch stream, and prints one JSON line: median
 µs per call and algorithmic TB/s (Q + K + V + O as the reference counts
 them, fmha_host.cpp:428-430, with Hkv heads for K/V).  Run it under
@@ -22,6 +23,8 @@ import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
+
+from tests.common import gpu_warmup  # noqa: E402
 
 # Hkv = 16, S = 16, D = 128 (the headline batch) with G = 1..16, MQA, short
 # rows, and the other head dims.
@@ -62,8 +65,7 @@ def main():
             else:
                 os.environ["FMHA_DECODE_GQA_KERNEL"] = mode
             call = lambda: fmha_amd.fmha_decode(q, k, v, seqlen_kv=S, out=o)
-            for _ in range(a.warmup):
-                call()
+            gpu_warmup(call, min_calls=a.warmup)
             times = []
             for _ in range(a.iters):
                 e0 = torch.cuda.Event(enable_timing=True)

@@ -3,7 +3,8 @@
 long-context shapes, for the profile under profiles/.
 
 For each shape (uniform lengths, bf16 N(0,1) inputs on the GPU), calls the
-library --warmup times, then times --iters calls with a HIP event pair per
+library at least --warmup times and for at least 0.1 s (tests/common.py:
+gpu_warmup), then times --iters calls with a HIP event pair per
 call on the launch stream and prints one JSON line: median µs per call and
 algorithmic TB/s (Q + K + V + O as the reference counts them,
 fmha_host.cpp:428-430, with Hkv heads for K/V; workspace traffic not
@@ -26,6 +27,8 @@ import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
+
+from tests.common import gpu_warmup  # noqa: E402
 
 # Long rows over few sequences (split path), many sequences of 24-256 rows
 # (single pass; the last one below its threshold), and the 16-row headline
@@ -89,9 +92,7 @@ def main():
         else:
             raise SystemExit(f"unknown layout {a.layout}")
 
-        for _ in range(a.warmup):
-            call()
-        torch.cuda.synchronize()
+        gpu_warmup(call, min_calls=a.warmup)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.iters)]
         for e0, e1 in ev:
             e0.record(stream)

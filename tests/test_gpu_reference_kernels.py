@@ -8,10 +8,11 @@ fmha_vectorized_fma (fmha_vectorized_fma_kernel.hpp:69-331), fmha_mfma
 (fmha_mfma_kernel.hpp:51-239) and fmha_mfma_v3
 (fmha_mfma_16x16x16_v3_kernel.hpp:51-291), the last two on the grid
 (1, Hq, B) x 256 their documentation gives -- beside this library's
-bf16-weight and fp32-weight paths, check each against the oracle gate (the
-fp32-weight path against the oracle's fp32-weight loop and against
-fmha_vectorized_fma, whose semantics it has), and time all six on the same
-stream (the timings are printed; profiles/ keeps the summary).
+bf16-weight, fp32-weight and exact paths, check each against the oracle
+gate (the fp32-weight path against the oracle's fp32-weight loop and against
+fmha_vectorized_fma, whose semantics it has; the exact path against the CPU
+loop's bits), and time all seven on the same stream (the timings are
+printed; profiles/ keeps the summary).
 
 The reference kernels are only launched inside the shapes where their
 indexing stays in bounds: Hq == Hkv (they index K/V with the query head,
@@ -84,10 +85,11 @@ def _launch_ref(name, q, k, v, o, cu, cu_h, B, H, D):
     assert rc == 0, f"{name} launch failed: {rc}"
 
 
-def _launch_ours(q, k, v, o, cu, B, H, D, fp32_weights=False):
+def _launch_ours(q, k, v, o, cu, B, H, D, variant="ours"):
     import torch
     import fmha_amd
-    launch = fmha_amd.launch_fmha_decode_fp32_weights if fp32_weights else fmha_amd.launch_fmha_decode
+    launch = {"ours": fmha_amd.launch_fmha_decode, "ours_fp32_weights": fmha_amd.launch_fmha_decode_fp32_weights,
+              "ours_exact": fmha_amd.launch_fmha_decode_exact}[variant]
     launch(torch.cuda.current_stream().cuda_stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
            cu.data_ptr(), B, H, H, 1, D, D, default_scale(D))
 
@@ -99,9 +101,9 @@ def _bits(t):
 
 def _time(fn, iters=20, warmup=3):
     import torch
+    from tests.common import gpu_warmup
     s = torch.cuda.current_stream()
-    for _ in range(warmup):
-        fn()
+    gpu_warmup(fn, min_calls=warmup)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
     for a, b in ev:
         a.record(s)
@@ -132,10 +134,10 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
     q, k, v, cu, cu_h = _inputs(B, H, D, seqlens, seed=B + H + D)
     outs = {}
     times = {}
-    for name in ("ours", "ours_fp32_weights") + REF_KERNELS:
+    for name in ("ours", "ours_fp32_weights", "ours_exact") + REF_KERNELS:
         o = torch.zeros(B, H, 1, D, device=q.device, dtype=torch.float16)
         if name.startswith("ours"):
-            run = lambda o=o, f=(name != "ours"): _launch_ours(q, k, v, o, cu, B, H, D, fp32_weights=f)
+            run = lambda o=o, name=name: _launch_ours(q, k, v, o, cu, B, H, D, variant=name)
         else:
             run = lambda name=name: _launch_ref(name, q, k, v, o, cu, cu_h, B, H, D)
         run()
@@ -161,6 +163,13 @@ def test_reference_kernels_agree_and_timing(label, B, H, D, lengths, std):
         print(f"{label}: {name} vs oracle: {st}", flush=True)
         if name == "ours":
             assert_pass(st, f"{label} ours")
+        elif name == "ours_exact":
+            # the CPU loop's arithmetic: its bits exactly (nearest-float exponentials)
+            r2, _ = oracle.decode(_bits(q.view(B, H, D)[idx]), _bits(ks), _bits(vs), cus, H, H, D,
+                                  default_scale(D), p_mode=2)
+            diff = int(np.count_nonzero(_bits(o.view(B, H, D)[idx]) != r2))
+            print(f"{label}: {name}: {diff} outputs differ from the CPU loop's bits", flush=True)
+            assert diff == 0
         elif name == "ours_fp32_weights":
             # fp32 weights: checked against the oracle's fp32-weight loop, no slack
             st32 = oracle.compare(_bits(o.view(B, H, D)[idx]), r32)
