@@ -20,6 +20,10 @@ import statistics
 
 CU_NUM = 256
 SIMD_NUM = 1024
+# GRBM_GUI_ACTIVE counts the cycles of each XCD's graphics block and the
+# counter sums the 8 XCDs of an MI355X: the kernel's cycles are an eighth of
+# it (at C2 that gives 1.25e6 cycles in 607 µs, a 2.07 GHz clock).
+XCD_NUM = 8
 
 
 def _rows(pattern):
@@ -107,18 +111,28 @@ def main():
         med = {k: statistics.median(v) for k, v in busy.items()}
         g = med.get("GRBM_GUI_ACTIVE")
         if g:
+            cycles = g / XCD_NUM
+            out["kernel_cycles"] = cycles
+            if durs:
+                out["clock_ghz"] = cycles / (statistics.median(durs) * 1e-6) / 1e9
+            # SQ_ACTIVE_INST_VALU counts quad-cycles summed over the SIMDs;
+            # SQ_VALU_MFMA_BUSY_CYCLES cycles summed over the SIMDs.
             if "SQ_ACTIVE_INST_VALU" in med:
-                out["valu_busy_pct"] = 100 * med["SQ_ACTIVE_INST_VALU"] / CU_NUM / g
+                out["valu_busy_pct"] = 100 * 4 * med["SQ_ACTIVE_INST_VALU"] / (SIMD_NUM * cycles)
             if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
-                out["mfma_busy_pct"] = 100 * med["SQ_VALU_MFMA_BUSY_CYCLES"] / (g * SIMD_NUM)
+                out["mfma_busy_pct"] = 100 * med["SQ_VALU_MFMA_BUSY_CYCLES"] / (SIMD_NUM * cycles)
         w = med.get("SQ_WAVES")
         lines += ["Busy counters (median over dispatches):", "", "| counter | value | per wave |", "|---|---|---|"]
         for k in sorted(med):
             pw = f"{med[k] / w:.1f}" if w and k.startswith("SQ_INSTS") else ""
             lines.append(f"| {k} | {med[k]:.6g} | {pw} |")
         if "valu_busy_pct" in out:
+            clk = f", {out['clock_ghz']:.2f} GHz over the median kernel time" if "clock_ghz" in out else ""
             lines += ["", f"VALUBusy = {out['valu_busy_pct']:.1f}%  "
-                          f"MfmaUtil = {out.get('mfma_busy_pct', 0):.2f}%"]
+                          f"MfmaUtil = {out.get('mfma_busy_pct', 0):.2f}%  "
+                          f"(per SIMD and kernel cycle; kernel cycles = GRBM_GUI_ACTIVE / {XCD_NUM} XCDs = "
+                          f"{out['kernel_cycles']:.4g}{clk}; VALUBusy = 4 SQ_ACTIVE_INST_VALU / "
+                          f"({SIMD_NUM} SIMDs x cycles), MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / ({SIMD_NUM} x cycles))"]
         out["busy"] = med
         lines.append("")
     cache = counters(os.path.join(a.dir, "cache"), a.kernel)
