@@ -318,20 +318,25 @@ int launch_mfma(void* stream, int layout, const DecodeArgs& a, int32_t batch, in
   ga.chunks = (int32_t)tps;
   ga.waves = (uint32_t)waves;
   ga.scale = a.scale;
-  // Waves per CU, from sweeps of 3-8 waves (B=30720, S=16, µs): the best cap
-  // follows the tiles a wave computes more than its bytes.  D=128: 4 waves
-  // (G=3 886/749/796/805/812 for 3/4/5/6/8, G=6 972/914/928/940/941, G=7
-  // 981/970/985/988/982), 6 from four tiles per wave (G=12
-  // 1187/1148/1147/1143/1143, MQA G=32 Hkv=1 151/131/129/130/129); D=64: 6
-  // (Hkv=8, G=3 250/203/178/186/186, G=5 299/243/205/196/194, G=12
-  // 400/320/317/316/318); D=256: 4 (G=3 557/483/484/488/490, G=5
-  // 603/633/637/638/632).  Waves of under 32 KiB (short rows) run uncapped
-  // (G=5 at S=4 725/569/476/417/413).
-  const int tiles_per_wave = hpw / ns;
+  // Waves per CU, from sweeps (B=30720, S=16, µs for 4/5/6/8 waves; the
+  // kernel's 17 KiB of LDS and 172-215 VGPRs allow 8): the best cap follows
+  // the tiles a wave computes more than its bytes.  D=128: 4 (G=3
+  // 773/810/813/818, G=12 1126/1167/1164/1190); 8 where a stream group's
+  // query heads take more than one wave (G > 16: their K/V re-reads are L2
+  // hits, so a wave brings mostly Q and O; MQA G=32 Hkv=1
+  // 132/121/124/117); D=64: 6 (Hkv=8, G=5 227/194/210/207, G=12
+  // 400/320/317/316 with an earlier form); D=256: 4 (G=3 557/483/484/488/490
+  // for 3/4/5/6/8, G=5 603/633/637/638/632, an earlier form).  Waves of
+  // under 32 KiB (short rows) run uncapped (G=5 at S=4 725/569/476/417/413
+  // for 3/4/5/6/8, an earlier form).
   const int64_t qrows = g <= 16 ? hpw * g : 16 * hpw;
   const int64_t unit_bytes = 2LL * rows_hint * hpw * dq * 2 + 2LL * qrows * dq * 2;
-  int w = dq == 64 || tiles_per_wave >= 4 ? 6 : 4;
+  int w = dq == 64 ? 6 : (tps >= 2 ? 8 : 4);
   if (unit_bytes < 32 * 1024) w = kMaxWavesPerCU;
+  if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {  // as in launch(): for sweeps
+    const int v = std::atoi(e);
+    if (v > 0) w = v;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t err = layout == fmha_decode::kLayoutPacked
                              ? launch_mfma_layout<fmha_decode::kLayoutPacked>(ga, dq, ns, w, s)

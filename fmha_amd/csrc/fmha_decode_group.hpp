@@ -26,7 +26,9 @@
 //     are padding that is never stored.  A wave handles HPW / NS tiles;
 //     larger groups take ceil(G / 16) waves per stream group, placed on one
 //     XCD so that their K/V re-reads hit its L2.  The query rows of a wave's
-//     tiles are one contiguous range of Q.
+//     tiles are one contiguous range of Q; each lane loads its column's query
+//     words straight into the B operand (8 dims per MFMA step), so Q takes
+//     no LDS.
 //   * K goes to LDS as rows; per tile and stream S^T = K_p . Q^T is D/32
 //     v_mfma_f32_16x16x32_bf16 (A = 16 K rows of stream p, B = the tile's 16
 //     query columns), each column keeping its own stream's pass.  No product
@@ -80,17 +82,13 @@ struct GroupShape {
   static constexpr int LPH = D / 8;               // lanes per stream (one 16-byte chunk each)
   static constexpr int HPW = kWaveSize / LPH;     // streams per wave
   static constexpr int KS = HPW * D * 2 + 16;     // LDS bytes per K row (all streams) + padding
-  static constexpr int QS = D * 2 + 16;           // LDS bytes per query row + padding
   static constexpr int VB = 8 * kMaxSeq * 2 + 16; // LDS bytes per 8-dim block of V^T + padding
   static constexpr int VSTREAM = (D / 8) * VB;    // LDS bytes of one stream's V^T
   static constexpr int DPC = D / 16;              // output dims per P.V column
   static constexpr int QLD = D / 32;              // 16-byte Q loads per lane per tile
   // K rows are dead once every tile's scores are formed, so V^T reuses them.
   static constexpr int KV_LDS = (kMaxSeq * KS > HPW * VSTREAM) ? kMaxSeq * KS : HPW * VSTREAM;
-  template <int QT>
-  static constexpr int lds_bytes() {
-    return KV_LDS + QT * 16 * QS;
-  }
+  static constexpr int lds_bytes() { return KV_LDS; }
 };
 
 __device__ __forceinline__ int shfl_i(int x, int src) { return __shfl(x, src, kWaveSize); }
@@ -134,7 +132,6 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
   constexpr int TW = HPW / NS;   // tiles per wave
-  constexpr int QT = TW;         // 16-row blocks of query rows per wave
   constexpr int CPS = 16 / NS;   // query columns per stream in a tile
   const int s = lane / LPH;
   const int r = lane % LPH;
@@ -145,7 +142,6 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
 
   char* k_lds = lds;
   char* v_lds = lds;  // written after the last read of k_lds
-  char* q_lds = lds + Sh::KV_LDS;
 
   // ---- this wave's tiles and query rows ----
   const uint32_t sigma0 = sg * HPW;
@@ -156,20 +152,30 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   const int tau1 = tau0 + ntiles - 1;
   const int R0 = (tau0 / TPS) * NS * G + (tau0 % TPS) * 16;
   const int p1 = min((tau1 / TPS) * NS + NS, nstreams) - 1;
-  const int nrows = p1 * G + min(16 * (tau1 % TPS) + 16, G) - R0;     // <= 16 * QT
+  const int nrows = p1 * G + min(16 * (tau1 % TPS) + 16, G) - R0;     // <= 16 * TW
   const uint64_t qrow0 = (uint64_t)sigma0 * G + R0;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + qrow0 * D, (uint32_t)nrows * D * 2u);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + qrow0 * D, (uint32_t)nrows * D * 2u);
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
 
-  // ---- issue every load: the query rows, K rows, V rows ----
-  u32x4 qr[QT][Sh::QLD];
+  // ---- issue every load: the query words straight into the B operand of
+  //      the score MFMA (lane (q, n): 8 dims of column n's query row per
+  //      step), K rows, V rows ----
+  const int slot_col = n / CPS;  // stream slot of this lane's column
+  bf16x8_v qb[TW][Sh::QLD];
 #pragma unroll
-  for (int t = 0; t < QT; ++t)
+  for (int i = 0; i < TW; ++i) {
+    const int tau = tau0 + i;
+    const int p_col = (tau / TPS) * NS + slot_col;
+    const int g_col = (tau % TPS) * 16 + n % CPS;
+    // Padding columns (and tiles past the wave's) read nothing: zero scores, never used.
+    const bool col_ok = i < ntiles && g_col < G && p_col < nstreams;
+    const uint32_t qoff = col_ok ? (uint32_t)((p_col * G + g_col - R0) * D + 8 * q) * 2u : kLaneOutOfRange;
 #pragma unroll
-    for (int i = 0; i < Sh::QLD; ++i)
-      qr[t][i] = buffer_load16<kPolicyDefault>(q_rsrc, (uint32_t)(t * 16 * D * 2 + (lane + 64 * i) * 16));
+    for (int cc = 0; cc < Sh::QLD; ++cc)
+      qb[i][cc] = __builtin_bit_cast(bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, qoff + (uint32_t)cc * 64u));
+  }
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
 #pragma unroll
@@ -180,14 +186,7 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
     vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- query rows and K rows to LDS ----
-#pragma unroll
-  for (int t = 0; t < QT; ++t)
-#pragma unroll
-    for (int i = 0; i < Sh::QLD; ++i) {
-      const int flat = lane + 64 * i;  // 16-byte chunk of 16 rows
-      *reinterpret_cast<u32x4*>(q_lds + (t * 16 + flat / (D / 8)) * Sh::QS + (flat % (D / 8)) * 16) = qr[t][i];
-    }
+  // ---- K rows to LDS ----
 #pragma unroll
   for (int j = 0; j < SMAX; ++j) *reinterpret_cast<u32x4*>(k_lds + j * Sh::KS + s * D * 2 + r * 16) = kr[j];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -198,22 +197,13 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   //      its own stream's; masked softmax; bf16 weights stay in registers ----
   bf16x4_v pa[TW];
   const int krow = n < SMAX ? n : 0;  // K rows past the bucket are never valid: any finite row will do
-  const int slot_col = n / CPS;       // stream slot of this lane's column
 #pragma unroll
   for (int i = 0; i < TW; ++i) {
     pa[i] = bf16x4_v{0, 0, 0, 0};
     if (i >= ntiles) continue;
     const int tau = tau0 + i;
     const int pt = (tau / TPS) * NS;    // the tile's first stream
-    const int c16 = (tau % TPS) * 16;   // its first query head inside the group
     const int p_col = pt + slot_col;
-    const int g_col = c16 + n % CPS;
-    // Padding columns read row 0 of the range; their scores are never used.
-    const int qrow = (g_col < G && p_col < nstreams) ? p_col * G + g_col - R0 : 0;
-    bf16x8_v qb[Sh::QLD];
-#pragma unroll
-    for (int cc = 0; cc < Sh::QLD; ++cc)
-      qb[cc] = *reinterpret_cast<const bf16x8_v*>(q_lds + qrow * Sh::QS + (4 * cc + q) * 16);
     f32x4_v st;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
@@ -222,7 +212,7 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
 #pragma unroll
       for (int cc = 0; cc < Sh::QLD; ++cc) {
         const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(k_lds + krow * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
-        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[cc], c4, 0, 0, 0);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[i][cc], c4, 0, 0, 0);
       }
       if (k == 0) {
         st = c4;
@@ -358,7 +348,7 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
   constexpr int TW = HPW / NS;  // tiles per wave
-  __shared__ __attribute__((aligned(16))) char lds[Sh::template lds_bytes<TW>()];
+  __shared__ __attribute__((aligned(16))) char lds[Sh::lds_bytes()];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
   const uint32_t w = blockIdx.x;
