@@ -262,16 +262,20 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   if (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
   // The single pass spans 2^shift batches with one descriptor: for the
-  // strided layout only when their span stays below 1 GiB.  Paged layouts
-  // run it with one batch and one page descriptor per wave, which leaves
-  // the lanes of missing KV heads idle: at D = 64 and 128 the split passes,
-  // whose lane groups take their own blocks and chunks, measured faster
-  // (16-row pages, B=2048 S=128 D=128: Hq/Hkv 8/1 129.3 -> 58.2 µs, 16/2
-  // 131.8 -> 85.3), at D = 256 (two heads per wave) the single pass (B=4096
-  // S=64 4/1: 55.8 against 86.1).
-  if (!LANES || D == 256) {
+  // strided layout only when their span stays below 1 GiB.  On paged caches
+  // (LANES) its lane groups can look up their own batches' pages, which pays
+  // for rows of one or two 16-row blocks; longer rows, whose lookups the
+  // single pass's two sub-blocks in flight cannot hide, take the split
+  // passes at D = 64 and 128 and the one-batch single pass at D = 256
+  // (16-row pages, µs, per-lane single pass against the previous choice:
+  // B=16384 S=24 Hq/Hkv 8/1 D=128 73.7 against 142.4 split; B=2048 S=128
+  // 8/1 74.5 against 57.8 split, 16/2 83.1 / 87.6; D=64 8/1 49.8 / 47.1,
+  // 16/2 68.8 / 64.8; B=4096 S=64 4/1 D=256 66.0 against 57.1 one batch
+  // per wave).
+  const bool lanes_onepass = LANES && a.nblk <= 2;
+  if (!LANES || D == 256 || lanes_onepass) {
     SplitArgs ao = a;
-    ao.sub_shift = LANES ? 0 : shift;
+    ao.sub_shift = LANES && !lanes_onepass ? 0 : shift;
     if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
       const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (int64_t)(a.max_rows - 1) * a.row_stride +
                             (int64_t)(fmha_decode::kv_heads_mem(a) - 1) * a.head_stride + D) * 2;
@@ -279,7 +283,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
     if (onepass_fits<D, G>(ao)) {
-      if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+      if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
       constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
                          : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock

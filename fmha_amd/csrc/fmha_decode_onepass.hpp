@@ -49,8 +49,10 @@ constexpr size_t onepass_lds_bytes(int sp) {
 }
 
 // MULTI: several batches per wave (fewer KV heads than a wave holds,
-// SplitArgs::sub_shift > 0; packed and strided layouts); otherwise one
-// batch per wave with its length read once for the whole wave.
+// SplitArgs::sub_shift > 0; packed and strided layouts through one
+// descriptor over the batches, paged caches through per-lane page lookups,
+// kLayoutPagedLanes / kLayoutPagedBlockLanes); otherwise one batch per wave
+// with its length read once for the whole wave.
 template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false>
 __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs a) {
   using P = OnepassShape<D, G>;
@@ -151,8 +153,12 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sp) + (size_t)hkl * G * sp;  // [G][sp]
 
   // Rows [0, S) of each lane group's batch: later rows read 0 without access.
-  LongRows<D, LAYOUT> krows, vrows;
-  if constexpr (!MULTI) {
+  constexpr bool LANES = LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes;
+  static_assert(!LANES || MULTI, "per-lane page lookups serve several batches per wave");
+  SplitRows<D, LAYOUT> krows, vrows;
+  if constexpr (!MULTI || LANES) {
+    // One batch per wave, or per-lane pages: each lane group addresses its
+    // own batch's rows.
     const int64_t row_base = split_row_base<LAYOUT>(a, b);
     krows.init(a, a.k, b, row_base, 0, S, hk, head_ok, r);
     vrows.init(a, a.v, b, row_base, 0, S, hk, head_ok, r);

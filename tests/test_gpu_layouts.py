@@ -250,6 +250,9 @@ NEG_CASES = [
     (40, 16, 128, 8, 4, 600), (70, 16, 128, 16, 16, 9), (70, 4, 128, 16, 2, 9), (70, 16, 128, 8, 2, 9),
     (70, 4, 64, 16, 1, 9),
     (100, 16, 128, 24, 2, 7), (100, 4, 256, 24, 2, 7),
+    # one or two 16-row blocks with few KV heads and >= 512 waves: the single
+    # pass with per-lane page lookups
+    (32, 16, 128, 8, 1, 2100), (24, 4, 128, 16, 2, 1100), (32, 1, 64, 8, 1, 4200), (32, 8, 256, 4, 1, 1100),
 ]
 
 

@@ -343,3 +343,28 @@ def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged ps={page_size} D={D} {Hq}/{Hkv} B={B}")
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 16, 32])
+@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2100), (128, 16, 2, 1100), (256, 4, 1, 1100), (64, 8, 1, 4200),
+                                        (128, 40, 8, 700)])
+@pytest.mark.parametrize("max_len", [17, 32])
+def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
+    """Rows of one or two 16-row blocks over paged caches with fewer KV heads
+    than a wave holds and >= 512 waves: the single pass with each lane group
+    looking up its own batch's pages (several batches per wave); the last
+    shape fills a wave and runs one batch per wave."""
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(page_size * 11 + D + Hq + Hkv + B + max_len)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    seqlens[-1] = 0
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + D + Hq + B + max_len)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    print(f"paged single pass: ps={page_size} D={D} {Hq}/{Hkv} B={B} max={max_len}", flush=True)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass ps={page_size} D={D} {Hq}/{Hkv} B={B}")
+
