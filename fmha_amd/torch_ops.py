@@ -1,8 +1,10 @@
 """PyTorch custom-op registration of the decode-attention kernel.
 
 Importing this module registers
-  torch.ops.fmha_amd.decode(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, fp32_weights=False) -> O
-  torch.ops.fmha_amd.decode_out(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, out, fp32_weights=False) -> ()
+  torch.ops.fmha_amd.decode(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, fp32_weights=False,
+                            exact=False) -> O
+  torch.ops.fmha_amd.decode_out(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, out, fp32_weights=False,
+                                exact=False) -> ()
   torch.ops.fmha_amd.decode_splitkv(q, k, v, cu_seqlens_kv, max_seqlen_kv, softmax_scale) -> O
   torch.ops.fmha_amd.decode_strided(q, k, v, seqlens_kv, softmax_scale) -> O
   torch.ops.fmha_amd.decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scale,
@@ -16,7 +18,9 @@ paged ops allocate their workspace through torch's caching allocator.
 Arguments are those of fmha_decode: cu_seqlens_kv may be None (uniform
 lengths), seqlen_kv < 0 means "infer from k's shape", softmax_scale <= 0
 means 1/sqrt(head_dim), fp32_weights keeps the softmax weights in fp32 (the
-numerics of the reference's fmha_vectorized_fma; needs cu_seqlens_kv).
+numerics of the reference's fmha_vectorized_fma; needs cu_seqlens_kv),
+exact computes the reference CPU loop's arithmetic step for step (its
+outputs bit for bit; needs cu_seqlens_kv and Hq == Hkv).
 decode_strided takes k/v as [B, S, Hkv, D] views (any strides with a unit
 innermost one: BHSD caches as k.transpose(1, 2)); decode_paged's
 max_seqlen_kv < 0 keeps the bound of 16.
@@ -36,27 +40,28 @@ def _args(cu_seqlens_kv, seqlen_kv, softmax_scale):
 
 @torch.library.custom_op("fmha_amd::decode", mutates_args=(), device_types="cuda")
 def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_kv: Optional[torch.Tensor],
-           seqlen_kv: int, softmax_scale: float, fp32_weights: bool = False) -> torch.Tensor:
+           seqlen_kv: int, softmax_scale: float, fp32_weights: bool = False, exact: bool = False) -> torch.Tensor:
     seq, scale = _args(cu_seqlens_kv, seqlen_kv, softmax_scale)
     return fmha_decode(q, k, v, cu_seqlens_kv=cu_seqlens_kv, seqlen_kv=seq, softmax_scale=scale,
-                       fp32_weights=fp32_weights)
+                       fp32_weights=fp32_weights, exact=exact)
 
 
 @decode.register_fake
-def _decode_fake(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, fp32_weights=False):
+def _decode_fake(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, fp32_weights=False, exact=False):
     return torch.empty(q.shape, dtype=torch.float16, device=q.device)
 
 
 @torch.library.custom_op("fmha_amd::decode_out", mutates_args=("out",), device_types="cuda")
 def decode_out(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_kv: Optional[torch.Tensor],
-               seqlen_kv: int, softmax_scale: float, out: torch.Tensor, fp32_weights: bool = False) -> None:
+               seqlen_kv: int, softmax_scale: float, out: torch.Tensor, fp32_weights: bool = False,
+               exact: bool = False) -> None:
     seq, scale = _args(cu_seqlens_kv, seqlen_kv, softmax_scale)
     fmha_decode(q, k, v, cu_seqlens_kv=cu_seqlens_kv, seqlen_kv=seq, softmax_scale=scale, out=out,
-                fp32_weights=fp32_weights)
+                fp32_weights=fp32_weights, exact=exact)
 
 
 @decode_out.register_fake
-def _decode_out_fake(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, out, fp32_weights=False):
+def _decode_out_fake(q, k, v, cu_seqlens_kv, seqlen_kv, softmax_scale, out, fp32_weights=False, exact=False):
     return None
 
 

@@ -15,6 +15,11 @@
 //     library's message, where the reference either runs the D=256 kernel for
 //     any head_dim other than 128 or fails later at the caller's next
 //     HIP_CHECK (which throws std::runtime_error, fmha_host.cpp:26-35).
+//
+// Compiled with FMHA_DECODE_COMPAT_EXACT defined, the launches go to
+// fmha_decode_fwd_exact instead: the reference CPU loop's arithmetic step
+// for step, so its own check (fmha_host.cpp:158-284) sees its own bits
+// (num_heads_q == num_heads_kv, the case that loop is written for).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -31,11 +36,19 @@ inline void launch_fmha_mfma_4x4x4(dim3 /*grid*/, dim3 /*block*/, hipStream_t st
                                    const bhalf_t* K, const bhalf_t* V, half_t* O, const int* cu_seqlens_kv,
                                    int batch, int num_heads_q, int num_heads_kv, int seqlen_q, int head_dim_q,
                                    int head_dim_kv, float softmax_scale) {
+#ifdef FMHA_DECODE_COMPAT_EXACT
+  const int rc = fmha_decode_fwd_exact(static_cast<void*>(stream), Q, K, V, O,
+                                       reinterpret_cast<const int32_t*>(cu_seqlens_kv), batch, num_heads_q,
+                                       num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
+  const char* entry = "fmha_decode_fwd_exact: ";
+#else
   const int rc = fmha_decode_fwd(static_cast<void*>(stream), Q, K, V, O,
                                  reinterpret_cast<const int32_t*>(cu_seqlens_kv), batch, num_heads_q,
                                  num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
+  const char* entry = "fmha_decode_fwd: ";
+#endif
   if (rc != FMHA_DECODE_SUCCESS) {
-    throw std::runtime_error(std::string("fmha_decode_fwd: ") + fmha_decode_error_string(rc) + ": " +
+    throw std::runtime_error(std::string(entry) + fmha_decode_error_string(rc) + ": " +
                              fmha_decode_last_error_detail());
   }
 }

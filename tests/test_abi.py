@@ -351,9 +351,11 @@ def test_python_wrapper_raises(lib):
     assert ei.value.code == BAD and "seqlen_q" in ei.value.detail
 
 
-def test_compat_header_compiles():
+@pytest.mark.parametrize("defines", [[], ["-DFMHA_DECODE_COMPAT_EXACT"]])
+def test_compat_header_compiles(defines):
     """include/fmha_decode_compat.hpp (the drop-in for the reference's
-    launch_fmha_mfma_4x4x4) compiles as host code against the C ABI."""
+    launch_fmha_mfma_4x4x4) compiles as host code against the C ABI, also
+    routed to the exact entry point."""
     import subprocess
     import tempfile
     src = ('#include "fmha_decode_compat.hpp"\n'
@@ -364,7 +366,7 @@ def test_compat_header_compiles():
         p = os.path.join(d, "t.cpp")
         open(p, "w").write(src)
         r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-fsyntax-only", "-x", "hip",
-                            "--offload-arch=gfx950", "-I", os.path.join(ROOT, "include"), p],
+                            "--offload-arch=gfx950", "-I", os.path.join(ROOT, "include"), *defines, p],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
 

@@ -59,6 +59,28 @@ def test_op_matches_direct_call_and_oracle():
 
 
 @pytest.mark.gpu
+def test_op_exact():
+    """torch.ops.fmha_amd.decode(..., exact=True) and decode_out: the bits of
+    the direct exact call, which are the CPU loop's (oracle p_mode=2)."""
+    import torch
+    import fmha_amd
+    import fmha_amd.torch_ops  # noqa: F401
+    seqlens = oracle.generate_seqlens(40, 16)
+    q, k, v, cu = make_inputs(40, 8, 8, 128, seqlens, seed=1002)
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    cud = torch.from_numpy(cu).cuda()
+    o_op = torch.ops.fmha_amd.decode(qd, kd, vd, cud, -1, 0.0, False, True)
+    o_dir = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, exact=True)
+    out = torch.empty_like(o_dir)
+    torch.ops.fmha_amd.decode_out(qd, kd, vd, cud, -1, 0.0, out, exact=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_op.view(torch.int16), o_dir.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), o_dir.view(torch.int16))
+    r, _ = oracle.decode(q, k, v, cu, 8, 8, 128, default_scale(128), p_mode=2)
+    assert np.array_equal(o_op.view(torch.int16).cpu().numpy().view(np.uint16), r)
+
+
+@pytest.mark.gpu
 def test_op_any_group_size():
     """torch.ops.fmha_amd.decode with a group size outside {1, 2, 4, 8}
     (G = 7): same bits as the direct call, oracle parity."""
