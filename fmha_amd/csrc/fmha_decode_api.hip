@@ -61,36 +61,49 @@ int valu_kernel_group(int g) {
 }
 
 // Waves per CU for a unit that moves `rows16` / 16 K/V rows (a mean, in
-// sixteenths) and G query heads: each row costs 1 KiB of K plus 1 KiB of V
-// per wave, each query head 1 KiB of Q in and 1 KiB of O out.  Caps of 16 or
-// more are dropped (no cap).  The floor is 3 waves, 4 for G = 8, whose waves
-// compute for about as long as their loads take (sweep at B=30720 Hq=128
-// Hkv=16 D=128, µs for 3/4/6 waves: S=16 1000/966/997, S=4 489/454/484;
-// G = 4 and below are fastest at 3).
+// sixteenths) and g_real query heads per KV head on the g-head kernel: each
+// row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB of Q
+// in and 1 KiB of O out, and the cap is the in-flight budget over that.
+// Caps of 16 or more are dropped (no cap); the floor is 3 waves, 4 for the
+// 8-head kernel.
 //
-// Waves whose lengths come from a device array first wait for them (one
-// dependent load before any K/V request), so they carry requests for a
-// shorter part of their life and want more of them per CU: 144 KiB against
-// the 80 KiB of known lengths.  Sweep through fmha_decode_fwd (B=30720, µs
-// for 4/6/8/10/12/16 waves): S=16 H=16 D=128 614/634/654/660/667/665;
-// S=16 H=32 D=256 2516/2544/2569/2593/2617/2621; S=5 D=256
-// 643/504/446/433/423/427; the reference's Poisson(4) lengths (mean 4.3)
-// H=16 D=128 291/233/206/198/191/191, H=16 D=256 595/460/409/393/374/376,
-// H=32 D=128 570/446/409/393/377/377, H=32 D=256 1165/918/833/812/813/817.
-// The 8-head kernel (G = 5-8) computes for longer than its short rows take
-// to load, so with a mean of 8 rows or fewer it gets every wave its
-// registers allow (8 per CU) whatever the bytes say: Hq=40 Hkv=8 D=128 with
-// those Poisson lengths, µs for 5/6/8/12 waves 217/197/181/179; Hq=64
-// Hkv=8 263 at 5, 253 at 8.  G = 2 keeps the byte count (Hq=32 Hkv=16: 227
-// at 11 against 236 at 13).
+// Known lengths: 80 KiB per CU for the 1- and 2-head kernels (3 waves of the
+// 34 KiB C2 unit, 7.13 TB/s against 6.63 uncapped; 6 of the 12 KiB C3 unit,
+// 6.60 against 6.05).  The 4- and 8-head kernels compute longer per byte
+// and want 200 KiB (B=30720 Hkv=16 D=128, µs for 3/4/5/6/8 waves:
+// G=4 S=4 604/480/412/364/314, S=8 757/613/529/478/484, S=12
+// 943/778/689/649/669, S=16 967/834/806/829/857; G=8 S=4
+// 813/639/547/492/464, S=8 956/763/665/618/658, S=16 1137/973/985/1008/1013;
+// G=5 S=8 848/670/574/521/531, S=16 937/848/867/897/921: the budget puts
+// each within 2% of its best; 80 KiB had given 3-4 waves and up to 57%
+// more time).
+//
+// Waves of the 1- and 2-head kernels whose lengths come from a device
+// array first wait for them (one dependent load before any K/V request),
+// so they carry requests for a shorter part of their life and want more of
+// them per CU: 144 KiB against the 80 KiB of known lengths.  Sweep through
+// fmha_decode_fwd (B=30720, µs for 4/6/8/10/12/16 waves): S=16 H=16 D=128
+// 614/634/654/660/667/665; S=16 H=32 D=256 2516/2544/2569/2593/2617/2621;
+// S=5 D=256 643/504/446/433/423/427; the reference's Poisson(4) lengths
+// (mean 4.3) H=16 D=128 291/233/206/198/191/191, H=16 D=256
+// 595/460/409/393/374/376, H=32 D=128 570/446/409/393/377/377, H=32 D=256
+// 1165/918/833/812/813/817.  The 4- and 8-head kernels keep their 200 KiB
+// there (µs for 4/5/6/7/8 waves: G=4 S=8 514/480/481/496/496, S=16
+// 862/790/806/831/843, Poisson 429/374/341/323/316; G=5 S=8
+// 568/517/503/534/546, Hq=40 Hkv=8 Poisson 253/217/198/185/181; G=8 S=8
+// 670/615/631/655/662, S=16 1006/935/987/1000/1007, Poisson
+// 298/260/243/242/252: within 2-8% of each best).
 constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
+constexpr int kInflightBytesPerCUWideGroups = 200 * 1024;
 
-int waves_per_cu_for(int rows16, int g, bool device_lengths) {
-  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g);  // 16 x bytes
-  const int64_t budget = device_lengths ? kInflightBytesPerCUDeviceLengths : kInflightBytesPerCU;
+int waves_per_cu_for(int rows16, int g, int g_real, bool device_lengths) {
+  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
+  const int64_t budget = g >= 4           ? kInflightBytesPerCUWideGroups
+                         : device_lengths ? kInflightBytesPerCUDeviceLengths
+                                          : kInflightBytesPerCU;
   const int64_t w = 16 * budget / unit_bytes16;
   if (w >= 16) return kMaxWavesPerCU;
-  const int floor_w = g >= 8 ? (device_lengths && rows16 <= 16 * 8 ? 8 : 4) : 3;
+  const int floor_w = g >= 8 ? 4 : 3;
   return w < floor_w ? floor_w : (int)w;
 }
 
@@ -156,7 +169,7 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   if (g == 0)
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be at most 8 here (got %d)",
                   a.group);
-  int w = waves_per_cu_for(rows16, g, device_lengths);
+  int w = waves_per_cu_for(rows16, g, a.group, device_lengths);
   // FMHA_DECODE_WAVE_CAP=<waves per CU> overrides the cap (for sweeps).
   if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {
     const int v = std::atoi(e);

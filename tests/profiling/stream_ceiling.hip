@@ -84,12 +84,16 @@ __global__ __launch_bounds__(64) void stream_kernel(const uint16_t* q, const uin
   }
 }
 
-// The library's cap: about 80 KiB of K/V/Q/O requests per CU, at least 3
-// waves, no cap at 16 or more (fmha_decode_api.hip, waves_per_cu_for).
+// The library's cap for known lengths: about 80 KiB of K/V/Q/O requests per
+// CU (2.5 times that for G >= 3, which runs the 4- and 8-head kernels), at
+// least 3 waves (4 for G > 4), no cap at 16 or more (fmha_decode_api.hip,
+// waves_per_cu_for).
 int waves_for(int rows, int g) {
-  int w = 80 * 1024 / (1024 * (2 * rows + 2 * g));
+  const int budget = (g >= 3 ? 200 : 80) * 1024;
+  int w = budget / (1024 * (2 * rows + 2 * g));
   if (w >= 16) return 32;
-  return w < 3 ? 3 : w;
+  const int floor_w = g > 4 ? 4 : 3;
+  return w < floor_w ? floor_w : w;
 }
 
 size_t lds_reserve(int waves, size_t static_lds) {
