@@ -245,13 +245,13 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // head, head dim dq, rows_hint rows per batch (the uniform length, or 4 when
 // lengths live on the device): the VALU kernel for G <= 8 (3 and 5-7 on its
 // 4- and 8-head instantiations), the matrix-core kernel above, and for the
-// shapes where it measured as fast or faster than the padded VALU kernel
-// (B=30720, µs VALU / MFMA, two boxes): D=64 with rows >= 8 (Hkv=8, S=16:
-// G=5 213/202 and 215/201; G=3 and 7 within 2% on one box, 4-10% faster on
-// the other) and D=128 G=3 with rows >= 8 (Hkv=16, S=8 482/460 and 481/462;
-// S=16 a tie on one box, 5% faster on the other).  Elsewhere the VALU kernel
-// wins: D=128 G=5-7 (S=16 863/885, 876/914, 933/988), short rows (G=3 S=4
-// 264/324, G=7 S=2 370/421), D=256 (G=3 365/490, G=6 443/691).
+// one family of shapes where it measured faster than the padded VALU kernel
+// with the VALU kernel's in-flight caps (B=30720, µs VALU / MFMA): D=64
+// G=5-7 with rows >= 8 (Hkv=8, G=5: S=8 122/120, S=16 212/203).  Elsewhere
+// the VALU kernel wins or ties: G=3 (D=128 Hkv=16 S=8 455/465, S=12
+// 592/641, S=16 766/754; D=64 S=16 177/187), D=128 G=5-7 (G=5 S=12
+// 676/727, G=6 S=12 707/738, G=7 S=8 587/630, S=12 774/751, S=16 936/978),
+// short rows and D=256.
 // FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
 // keeps the VALU kernel wherever it exists (for comparisons).
 // Long rows: the matrix-core split passes for G > 8 (kv_groups > 1 on
@@ -272,7 +272,7 @@ bool use_mfma_kernel(int g, int dq, int rows_hint) {
   }
   if (valu_kernel_group(g) == 0) return true;
   if (valu_group(g) || rows_hint < 8 || dq == 256) return false;
-  return dq == 64 || g == 3;
+  return dq == 64 && g != 3;
 }
 
 // Streams per 16-column query tile: 4 for G <= 4, 2 for G <= 8, else 1
