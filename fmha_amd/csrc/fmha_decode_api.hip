@@ -61,22 +61,39 @@ int valu_kernel_group(int g) {
 }
 
 // Waves per CU for a unit that moves `rows16` / 16 K/V rows (a mean, in
-// sixteenths) and g_real query heads per KV head on the g-head kernel: each
-// row costs 1 KiB of K plus 1 KiB of V per wave, each query head 1 KiB of Q
-// in and 1 KiB of O out, and the cap is the in-flight budget over that.
-// Caps of 16 or more are dropped (no cap); the floor is 3 waves, 4 for the
-// 8-head kernel.
+// sixteenths) and g_real query heads per KV head on the g-head kernel at
+// head dim dq: each row costs 1 KiB of K plus 1 KiB of V per wave, each
+// query head 1 KiB of Q in and 1 KiB of O out, and the cap is the in-flight
+// budget over that, or a measured table where no one budget fits.  Caps of
+// 16 or more are dropped (no cap); the floor is 3 waves, 4 for the 8-head
+// kernel.
 //
 // Known lengths: 80 KiB per CU for the 1- and 2-head kernels (3 waves of the
 // 34 KiB C2 unit, 7.13 TB/s against 6.63 uncapped; 6 of the 12 KiB C3 unit,
-// 6.60 against 6.05).  The 4- and 8-head kernels compute longer per byte
-// and want 200 KiB (B=30720 Hkv=16 D=128, µs for 3/4/5/6/8 waves:
-// G=4 S=4 604/480/412/364/314, S=8 757/613/529/478/484, S=12
-// 943/778/689/649/669, S=16 967/834/806/829/857; G=8 S=4
-// 813/639/547/492/464, S=8 956/763/665/618/658, S=16 1137/973/985/1008/1013;
-// G=5 S=8 848/670/574/521/531, S=16 937/848/867/897/921: the budget puts
-// each within 2% of its best; 80 KiB had given 3-4 waves and up to 57%
-// more time).
+// 6.60 against 6.05).
+//
+// The 4-head kernel with known lengths scores all its query heads in one
+// pass; its best cap falls with the row count faster than any budget does
+// (B=30720, µs for 3/4/5/6/7/8 waves; D=128 Hkv=16: G=4 S=1
+// 311/251/216/199/191/193, S=2 325/268/241/231/232/233, S=4
+// 378/320/302/315/322/321, S=6 466/401/392/400/404/409, S=8
+// 497/477/492/497/498/499, S=12 665/637/661/671/676/676, S=16
+// 781/810/825/838/850/856; G=3 S=3 353/285/247/228/226/236, S=12
+// 638/582/613/626/631/634, S=16 754/777/799/803/807/812; D=64 Hkv=8 and
+// D=256 Hkv=8 B=15360, which want more waves on short rows: G=3 D=256 S=4
+// 182/146/126/116/123/127, S=16 360/346/361/368/370/375; D=64 S=2 best
+// with no cap, S=16 184/175/184/185/187/188).
+//
+// The 8-head kernel scores two query heads per pass at D <= 128 and wants
+// 200 KiB at D = 128 (Hkv=16, µs for 3/4/5/6/8 waves: G=8 S=4
+// 813/639/547/492/464, S=8 956/763/665/618/658, S=16
+// 1137/973/985/1008/1013; G=5 S=8 848/670/574/521/531, S=16
+// 937/848/867/897/921: each within 2% of its best).  At D = 64 (Hkv=8) its
+// waves want more in flight on 16 rows (G=8: 258/225/216/229 µs for
+// 4/5/6/8 waves, G=7 247/216/206/218, G=5 211/191/199/205) and no cap on 4
+// (G=8 149/128/119/114 and 108 uncapped); at D = 256 (one pass, Hkv=8
+// B=15360) fewer on short rows (G=6 S=4 209/191/195/206 for 4/5/6/8, S=8
+// 276/268/292/294).
 //
 // Waves of the 1- and 2-head kernels whose lengths come from a device
 // array first wait for them (one dependent load before any K/V request),
@@ -87,8 +104,9 @@ int valu_kernel_group(int g) {
 // S=5 D=256 643/504/446/433/423/427; the reference's Poisson(4) lengths
 // (mean 4.3) H=16 D=128 291/233/206/198/191/191, H=16 D=256
 // 595/460/409/393/374/376, H=32 D=128 570/446/409/393/377/377, H=32 D=256
-// 1165/918/833/812/813/817.  The 4- and 8-head kernels keep their 200 KiB
-// there (µs for 4/5/6/7/8 waves: G=4 S=8 514/480/481/496/496, S=16
+// 1165/918/833/812/813/817.  The 4- and 8-head kernels that pick a bucket
+// per wave score two query heads per pass at D <= 128 and take the 200 KiB
+// budget there (µs for 4/5/6/7/8 waves: G=4 S=8 514/480/481/496/496, S=16
 // 862/790/806/831/843, Poisson 429/374/341/323/316; G=5 S=8
 // 568/517/503/534/546, Hq=40 Hkv=8 Poisson 253/217/198/185/181; G=8 S=8
 // 670/615/631/655/662, S=16 1006/935/987/1000/1007, Poisson
@@ -96,7 +114,18 @@ int valu_kernel_group(int g) {
 constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
 constexpr int kInflightBytesPerCUWideGroups = 200 * 1024;
 
-int waves_per_cu_for(int rows16, int g, int g_real, bool device_lengths) {
+// bucket_per_wave: the kernel picks a bucket per wave (lengths on the
+// device, or several batches per wave), whose 4-head form scores two query
+// heads per pass.
+int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths, bool bucket_per_wave) {
+  const int s = (rows16 + 15) / 16;  // rows, rounded up
+  if (!bucket_per_wave && g == 4) {
+    static const int8_t kWaves128[17] = {8, 8, 7, 6, 5, 5, 5, 4, 4, 4, 4, 4, 4, 3, 3, 3, 3};
+    if (dq == 128) return kWaves128[s < 16 ? s : 16];
+    return s <= 2 ? kMaxWavesPerCU : (s <= 4 ? 6 : 4);
+  }
+  if (!bucket_per_wave && g == 8 && dq == 64) return s <= 4 ? kMaxWavesPerCU : (s <= 8 || g_real > 5 ? 6 : 5);
+  if (!bucket_per_wave && g == 8 && dq == 256 && s > 2 && s <= 8) return 5;
   const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
   const int64_t budget = g >= 4           ? kInflightBytesPerCUWideGroups
                          : device_lengths ? kInflightBytesPerCUDeviceLengths
@@ -169,12 +198,6 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   if (g == 0)
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_q / num_heads_kv must be at most 8 here (got %d)",
                   a.group);
-  int w = waves_per_cu_for(rows16, g, a.group, device_lengths);
-  // FMHA_DECODE_WAVE_CAP=<waves per CU> overrides the cap (for sweeps).
-  if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {
-    const int v = std::atoi(e);
-    if (v > 0) w = v;
-  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   if (exact && (layout != fmha_decode::kLayoutPacked || g != 1))
@@ -189,6 +212,12 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
     const int64_t span = ((int64_t)((1 << shift) - 1) * a.batch_stride + (rows - 1) * a.row_stride +
                           (int64_t)(a.num_heads_kv - 1) * a.head_stride + dq) * 2;
     multi = span < (int64_t(1) << 30);
+  }
+  int w = waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
+  // FMHA_DECODE_WAVE_CAP=<waves per CU> overrides the cap (for sweeps).
+  if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {
+    const int v = std::atoi(e);
+    if (v > 0) w = v;
   }
   if (exact) {
     if (multi) {
@@ -242,16 +271,13 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // ---------------------------------------------------------------------------
 
 // Kernel choice for the packed and strided layouts, G query heads per KV
-// head, head dim dq, rows_hint rows per batch (the uniform length, or 4 when
-// lengths live on the device): the VALU kernel for G <= 8 (3 and 5-7 on its
-// 4- and 8-head instantiations), the matrix-core kernel above, and for the
-// one family of shapes where it measured faster than the padded VALU kernel
-// with the VALU kernel's in-flight caps (B=30720, µs VALU / MFMA): D=64
-// G=5-7 with rows >= 8 (Hkv=8, G=5: S=8 122/120, S=16 212/203).  Elsewhere
-// the VALU kernel wins or ties: G=3 (D=128 Hkv=16 S=8 455/465, S=12
-// 592/641, S=16 766/754; D=64 S=16 177/187), D=128 G=5-7 (G=5 S=12
-// 676/727, G=6 S=12 707/738, G=7 S=8 587/630, S=12 774/751, S=16 936/978),
-// short rows and D=256.
+// head: the VALU kernel for G <= 8 (3 and 5-7 on its 4- and 8-head
+// instantiations), the matrix-core kernel above.  With the VALU kernel's
+// wave caps it is the faster of the two or within 2% at every G <= 8 shape
+// measured (B=30720, µs VALU / MFMA: D=128 Hkv=16 G=3 S=8 418/469, S=16
+// 754/763, G=5 S=16 834/889, G=7 S=8 595/634, G=8 S=16 966/1002; D=64
+// Hkv=8 G=5 S=16 191/210, G=7 S=16 206/225; D=256 Hkv=8 B=15360 G=6 S=16
+// 435/692).
 // FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
 // keeps the VALU kernel wherever it exists (for comparisons).
 // Long rows: the matrix-core split passes for G > 8 (kv_groups > 1 on
@@ -265,14 +291,10 @@ bool split_on_matrix_cores(int kv_groups) {
   return kv_groups > 1;
 }
 
-bool use_mfma_kernel(int g, int dq, int rows_hint) {
-  if (const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL")) {
+bool use_mfma_kernel(int g) {
+  if (const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL"))
     if (std::strcmp(e, "mfma") == 0) return true;
-    if (std::strcmp(e, "valu") == 0) return valu_kernel_group(g) == 0;
-  }
-  if (valu_kernel_group(g) == 0) return true;
-  if (valu_group(g) || rows_hint < 8 || dq == 256) return false;
-  return dq == 64 && g != 3;
+  return valu_kernel_group(g) == 0;
 }
 
 // Streams per 16-column query tile: 4 for G <= 4, 2 for G <= 8, else 1
@@ -512,7 +534,7 @@ extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, kVarlenRowsHint))
+  if (use_mfma_kernel(num_heads_q / num_heads_kv))
     return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
   a.rows_feedback = feedback_word(stream);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
@@ -578,7 +600,7 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
   a.seqlen_uniform = seqlen_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, seqlen_kv))
+  if (use_mfma_kernel(num_heads_q / num_heads_kv))
     return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), 16 * seqlen_kv,
                 false);
@@ -619,7 +641,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
   a.head_stride = (int32_t)kv_head_stride;
   const int sb = seqlens_kv ? 0 : bucket_for(seqlen_kv);
   const int rows_hint = seqlens_kv ? (cap < kVarlenRowsHint ? cap : kVarlenRowsHint) : seqlen_kv;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
+  if (use_mfma_kernel(num_heads_q / num_heads_kv))
     return launch_mfma(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, rows_hint);
   return launch(stream, fmha_decode::kLayoutStrided, a, batch, head_dim_q, sb, 16 * rows_hint, seqlens_kv != nullptr);
 }
@@ -896,7 +918,7 @@ int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, vo
     d.row_stride = num_heads_kv * head_dim_q;
     d.head_stride = head_dim_q;
     d.max_rows = max_seqlen_kv;
-    if (use_mfma_kernel(num_heads_q / num_heads_kv, head_dim_q, rows_hint))
+    if (use_mfma_kernel(num_heads_q / num_heads_kv))
       return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
     SplitArgs unused;
     rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1, head_dim_q, softmax_scale,

@@ -446,26 +446,30 @@ __device__ __forceinline__ void score_softmax(const u32x4 (&qv)[GH], const u32x4
 // groups serve different batches), weights through LDS slot
 // [hkl][g*16 + j] of lds_p, fp32 result per query head in acc.  Query heads
 // at or past `active` (the padding of a group size without its own
-// instantiation; wave-uniform) are neither scored nor accumulated.
-// Groups of 4 or 8 query heads at D <= 128 are scored two heads at a time:
-// the same exchanges in total, but 2/G of the partial scores live at once
-// (G = 8 with 16 rows: 32 instead of 128 registers, 144 VGPRs in all
-// instead of 256, so three waves fit a SIMD instead of one), and a pass of
-// padding heads only is skipped.
+// instantiation; wave-uniform) are neither scored nor accumulated where the
+// heads are scored in several passes; a kernel that scores them in one
+// pass computes the padding heads too (their Q reads as 0, their O is
+// dropped), which measured faster than testing for them inside the
+// unrolled loops.
 // ---------------------------------------------------------------------------
-template <int D, int G, int SMAX, bool PF32>
+template <int D, int G, int SMAX, bool PF32, bool VARLEN>
 __device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX], const u32x4 (&vr)[SMAX],
                                             int S, float scale, int lane, uint16_t* lds_p, float (&acc)[G][8],
-                                            int active = G) {
+                                            int active_heads = G) {
   constexpr int LPH = D / 8;                 // lanes per KV head
   constexpr int VP = G * kMaxSeq;            // LDS slots per KV head
-  // Query heads per score pass: 2 for G = 4, 8 at D <= 128 (µs, B=30720
-  // Hkv=16 D=128, 1 / 2 / 4 / 8 heads per pass: G=5 S=16 1155/831/860/857,
-  // G=7 S=16 1299/932/927/919; Hq=40 Hkv=8 with Poisson(4) lengths
-  // 224/218/226/254; one head per pass leaves too little independent work
-  // to hide the exchanges' latency), all G at D = 256 (G=6 S=16 Hkv=8:
-  // 657/499/490/484).
-  constexpr int GH = G >= 4 ? (D == 256 ? G : 2) : G;
+  // Query heads per score pass: 2 for G = 8 at D <= 128, which keeps 2/G of
+  // the partial scores live at once (G = 8 with 16 rows: 32 instead of 128
+  // registers, 200 VGPRs in all instead of 256) (µs, B=30720 Hkv=16 D=128,
+  // 1 / 2 / 4 / 8 heads per pass: G=5 S=16 1155/831/860/857, G=7 S=16
+  // 1299/932/927/919; Hq=40 Hkv=8 with Poisson(4) lengths 224/218/226/254;
+  // one head per pass leaves too little independent work to hide the
+  // exchanges' latency), and for G = 4 in the kernels that pick a bucket per
+  // wave (Hq=64 Hkv=16 Poisson(4): 317 against 327 µs); all G otherwise
+  // (G = 4, uniform lengths, µs with two / one heads per pass at each one's
+  // best wave cap: G=3 S=4 284/262, S=8 441/418, G=4 S=16 795/782).
+  constexpr int GH = D != 256 && (G == 8 || (G == 4 && VARLEN)) ? 2 : G;
+  const int active = GH < G ? active_heads : G;
   const int hkl = lane / LPH;
 
 #pragma unroll
@@ -784,7 +788,7 @@ __device__ __forceinline__ void decode_core_any(const u32x4 (&qv)[G], const u32x
   if constexpr (exact_taken<G, SMAX, PF32, EXACT>()) {
     decode_core_exact<D, G, SMAX, exact_stages(SMAX, VARLEN), GROUP_S>(qv, kr, vr, S, scale, lane, lds_p, acc);
   } else {
-    decode_core<D, G, SMAX, PF32>(qv, kr, vr, S, scale, lane, lds_p, acc, active);
+    decode_core<D, G, SMAX, PF32, VARLEN>(qv, kr, vr, S, scale, lane, lds_p, acc, active);
   }
 }
 
