@@ -280,15 +280,31 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // 435/692).
 // FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G, =valu
 // keeps the VALU kernel wherever it exists (for comparisons).
-// Long rows: the matrix-core split passes for G > 8 (kv_groups > 1 on
-// entry), the VALU passes otherwise.  FMHA_DECODE_GQA_KERNEL=valu keeps
-// every G on the VALU passes (G > 8 on ceil(G / 8) launch KV heads of 8
-// query heads), =mfma puts every G on the matrix cores.
-bool split_on_matrix_cores(int kv_groups) {
+// Long rows, by the launch's group (g_launch = launch query heads per launch
+// KV head: 8 for G = 5-8 and, as kv_groups groups of 8, for every G > 8):
+// the matrix-core split passes for G > 8 and for G = 5-8 on the packed,
+// strided and 16-row-page layouts, and on pages under 16 rows when the
+// batch has fewer KV heads than half a wave (hkv launch KV heads, head dim
+// d); the VALU passes otherwise.  Against the VALU passes at G = 8 and 5-7
+// (µs, each at its best chunk size; D = 128 unless given): B=8 S=32768
+// Hq/Hkv 64/8 232 vs 223, B=256 S=1024 64/8 233 vs 221, B=64 S=4096 64/8
+// 219 vs 218, 32/4 125 vs 123, 8/1 52 vs 46, D=64 B=32 64/8 99 vs 87,
+// D=256 B=16 64/8 115 vs 108, 40/8 236 vs 227; BHSD 64/8 B=8 260 vs 211;
+// 16-row pages 250 vs 233; one-row pages 64/8 B=64 273 vs 381 (the VALU
+// passes' per-row descriptors against per-lane addresses), 8/1 92 vs 66.
+// At G = 4 the VALU passes stay faster (B=64 S=4096 32/8 189 vs 206).
+// FMHA_DECODE_GQA_KERNEL=valu keeps every G on the VALU passes (G > 8 on
+// ceil(G / 8) launch KV heads of 8 query heads), =mfma puts every G on the
+// matrix cores.
+bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d) {
   const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL");
   if (e && std::strcmp(e, "valu") == 0) return false;
   if (e && std::strcmp(e, "mfma") == 0) return true;
-  return kv_groups > 1;
+  if (kv_groups > 1) return true;
+  if (g_launch < 8) return false;
+  if (layout != fmha_decode::kLayoutPaged) return true;
+  const int hpw = kWaveSize / (d / 8);
+  return 2 * hkv <= hpw && hpw % (2 * hkv) == 0;
 }
 
 bool use_mfma_kernel(int g) {
@@ -466,18 +482,17 @@ struct SplitPlan {
   size_t off_t = 0, off_m = 0, off_l = 0, off_ml = 0, off_opart = 0, total = 0;
 };
 
-// P.V waves the split pass aims for.  A wave keeps two sub-blocks of V in
-// flight: 2 * 16 rows of 1 KiB (the wave's heads' share of a row) for G <= 4,
-// half that for G = 8 (8-row sub-blocks), and less again when the batch has
-// fewer KV heads than a wave holds (idle lanes).  The target is 512 waves of
-// the full kind, scaled up by those two factors, so that the V requests in
-// flight per CU stay about the same and the pass runs in one round of long
-// waves: fewer, longer chunks also mean fewer partial outputs to combine.
-// Measured against a fixed 2048 (µs): B=1 S=131072 Hq=32 Hkv=8 D=128
-// 118.4 -> 105.5; B=64 S=4096 200.5 -> 188.7; B=16 Hq=16 Hkv=8 S=8192 D=256
-// 186.7 -> 175.5; B=32 Hq=64 Hkv=8 S=8192 234.0 -> 216.5; B=4 Hq=32 Hkv=4
-// S=32768 D=64 (half the lanes idle) 72.0 -> 72.1; B=256 Hq=64 Hkv=8 S=1024
-// 230.1 -> 240.1, the one shape measured slower.
+// P.V waves the VALU split pass aims for.  A wave keeps two sub-blocks of V
+// in flight: 2 * 16 rows of 1 KiB (the wave's heads' share of a row) for
+// G <= 4, half that for G = 8 (8-row sub-blocks), and less again when the
+// batch has fewer KV heads than a wave holds (idle lanes).  The target is
+// 512 waves of the full kind, scaled up by those two factors, so that the V
+// requests in flight per CU stay about the same and the pass runs in one
+// round of long waves: fewer, longer chunks also mean fewer partial outputs
+// to combine.  Measured against a fixed 2048 (µs): B=1 S=131072 Hq=32 Hkv=8
+// D=128 118.4 -> 105.5; B=64 S=4096 200.5 -> 188.7; B=16 Hq=16 Hkv=8 S=8192
+// D=256 186.7 -> 175.5; B=32 Hq=64 Hkv=8 S=8192 234.0 -> 216.5; B=4 Hq=32
+// Hkv=4 S=32768 D=64 (half the lanes idle) 72.0 -> 72.1.
 int64_t split_target_waves(int hq, int hkv, int d) {
   const int heads_per_wave = kWaveSize / (d / 8);
   const int g = hq / hkv;
@@ -486,16 +501,41 @@ int64_t split_target_waves(int hq, int hkv, int d) {
 }
 
 // Scores: one wave per 16-row block.  P.V: chunks of C rows (C in
-// {64, ..., 512}, or the rows' own multiple of 16 when shorter), the largest
-// that still gives split_target_waves waves where the work allows.
-SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d) {
+// {64, ..., 1024}, or the rows' own multiple of 16 when shorter), the
+// largest that still gives the pass's target wave count where the work
+// allows.  VALU passes: split_target_waves waves of HPW KV heads (1024 rows
+// against 512 measured 0-3% faster where it keeps that count: B=256 S=1024
+// Hq=32 Hkv=8 192.9 -> 187.9 µs).  Matrix-core passes (kv_groups launch KV
+// heads per cache head): one wave per (batch, cache KV head, chunk, pair of
+// 16-column tiles; one tile at D = 256), 2048 of them for groups of up to 8
+// query heads and 1024 above (whose waves fill their tiles), half that at
+// D = 256 (µs by C = 256 / 512 / 1024: B=8 S=32768 64/8 239/226/223, 40/8
+// 244/233/227; B=64 S=4096 32/4 129/123/122, 64/4 (G = 16) 150/143/136;
+// B=8 S=32768 8/1 48/55/74 (C = 128: 46); D=64 B=32 S=4096 64/8
+// 90/87/91; D=256 B=16 S=4096 64/8 110/108/136; MQA B=8 S=32768 32/1
+// 72/82/111).
+SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv_groups, int layout) {
   SplitPlan p;
   const int heads_per_wave = kWaveSize / (d / 8);
   const int64_t upb = (hkv + heads_per_wave - 1) / heads_per_wave;
   p.units = upb * batch;
-  const int64_t target = split_target_waves(hq, hkv, d);
-  int c = 512;
-  while (c > 64 && p.units * ((max_rows + c - 1) / c) < target) c /= 2;
+  int64_t per_chunk = p.units;  // P.V waves per chunk of every batch
+  int64_t target = split_target_waves(hq, hkv, d);
+  if (split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d)) {
+    const int hkv_mem = hkv / kv_groups;
+    const int g_mem = hq / hkv_mem;
+    const int tw = d == 256 ? 1 : 2;
+    per_chunk = batch * hkv_mem * (((g_mem + 15) / 16 + tw - 1) / tw);
+    target = (g_mem <= 8 ? 2048 : 1024) / (d == 256 ? 2 : 1);
+  }
+  int c = 1024;
+  while (c > 64 && per_chunk * ((max_rows + c - 1) / c) < target) c /= 2;
+  // FMHA_DECODE_SPLIT_CHUNK=<64|...|2048> overrides C (for sweeps; the
+  // workspace size follows, and a launch checks its workspace against it).
+  if (const char* e = std::getenv("FMHA_DECODE_SPLIT_CHUNK")) {
+    const int v = std::atoi(e);
+    if (v >= 64 && v <= 2048 && (v & (v - 1)) == 0) c = v;
+  }
   const int fit = max_rows <= 16 ? 16 : (max_rows + 15) / 16 * 16;  // no longer than the rows need
   if (c > fit) c = fit;
   p.chunk_rows = c;
@@ -736,14 +776,21 @@ extern "C" size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_
       (head_dim != 64 && head_dim != 128 && head_dim != 256))
     return 0;
   const int g = num_heads_q % num_heads_kv == 0 ? num_heads_q / num_heads_kv : 0;
-  if (g == 0 || valu_group(g)) return plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim).total;
+  // The plan of whichever passes the layout takes: the larger of the packed
+  // layout's and the short-page layout's, which can differ.
+  auto plan_total = [&](int hq, int hkv, int kvg) {
+    const size_t a = plan_split(batch, hq, hkv, max_seqlen_kv, head_dim, kvg, fmha_decode::kLayoutPacked).total;
+    const size_t b = plan_split(batch, hq, hkv, max_seqlen_kv, head_dim, kvg, fmha_decode::kLayoutPaged).total;
+    return a > b ? a : b;
+  };
+  if (g == 0 || valu_group(g)) return plan_total(num_heads_q, num_heads_kv, 1);
   // G > 8: ns groups of 8 per KV head on Hkv * ns launch KV heads; Q and O
   // copies unless G is a multiple of 8.  G = 3, 5-7: the copies padded to
   // 4 or 8, and the plan for Hkv * GP heads.
   const int gp = long_row_group(g);
   const int ns = g > 8 ? gp / 8 : 1;
   const size_t pad = gp == g ? 0 : 2 * group_pad_bytes(batch, num_heads_kv, gp, head_dim);
-  return pad + plan_split(batch, num_heads_kv * gp, num_heads_kv * ns, max_seqlen_kv, head_dim).total;
+  return pad + plan_total(num_heads_kv * gp, num_heads_kv * ns, ns);
 }
 
 namespace {
@@ -752,10 +799,10 @@ namespace {
 // layout-independent fields of the launch.  kv_span_bytes: the largest byte
 // range one wave's K/V descriptor covers in the caller's layout (must stay
 // below 2^30, as must one batch's scores and partial outputs).
-int split_prepare(const void* Q, const void* K, const void* V, void* O, int32_t max_seqlen_kv, int32_t batch,
-                  int32_t num_heads_q, int32_t num_heads_kv, int32_t kv_groups, int32_t head_dim, float softmax_scale,
-                  void* workspace, size_t workspace_bytes, int64_t kv_span_bytes, SplitArgs& a) {
-  const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim);
+int split_prepare(int layout, const void* Q, const void* K, const void* V, void* O, int32_t max_seqlen_kv,
+                  int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t kv_groups, int32_t head_dim,
+                  float softmax_scale, void* workspace, size_t workspace_bytes, int64_t kv_span_bytes, SplitArgs& a) {
+  const SplitPlan plan = plan_split(batch, num_heads_q, num_heads_kv, max_seqlen_kv, head_dim, kv_groups, layout);
   const int64_t padded_rows = (int64_t)plan.nblk * fmha_decode::kSplitBlockRows;
   const int64_t part_bytes = (int64_t)num_heads_q * plan.nchunks * head_dim * 4;  // one batch's partials
   if (kv_span_bytes >= (int64_t(1) << 30) || padded_rows * num_heads_q * 4 >= (int64_t(1) << 30) ||
@@ -797,7 +844,7 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = a.num_heads_q / a.num_heads_kv;
   hipError_t err;
-  if (split_on_matrix_cores(a.kv_groups)) {
+  if (split_on_matrix_cores(a.num_heads_q / a.num_heads_kv, a.kv_groups, layout, a.num_heads_kv, head_dim)) {
     // The matrix cores take the cache's KV heads with all of their query
     // heads (a group above 8: ns * 8 of them, the same workspace plan).
     SplitArgs m = a;
@@ -921,8 +968,8 @@ int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, vo
     if (use_mfma_kernel(num_heads_q / num_heads_kv))
       return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
     SplitArgs unused;
-    rc = split_prepare(Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1, head_dim_q, softmax_scale,
-                       workspace, workspace_bytes, span, unused);
+    rc = split_prepare(fmha_decode::kLayoutPacked, Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1,
+                       head_dim_q, softmax_scale, workspace, workspace_bytes, span, unused);
     if (rc != FMHA_DECODE_SUCCESS) return rc;
     d.rows_feedback = feedback_word(stream, may_allocate);
     return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
@@ -932,8 +979,8 @@ int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, vo
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
       [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q, softmax_scale, ws,
-                                ws_bytes, span, a);
+        int rc2 = split_prepare(fmha_decode::kLayoutPacked, q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg,
+                                head_dim_q, softmax_scale, ws, ws_bytes, span, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = cu_seqlens_kv;
         a.len_mode = fmha_decode::kLenCu;
@@ -1047,8 +1094,8 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
       [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q, softmax_scale, ws,
-                                ws_bytes, extent, a);
+        int rc2 = split_prepare(fmha_decode::kLayoutStrided, q, K, V, o, max_seqlen_kv, batch, hq, hkv, kvg,
+                                head_dim_q, softmax_scale, ws, ws_bytes, extent, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = seqlens_kv;
         a.len_mode = seqlens_kv ? fmha_decode::kLenArray : fmha_decode::kLenUniform;
@@ -1080,11 +1127,12 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
                        max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
   // A sub-block's range covers at most 16 rows of one page.
   const int64_t row_bytes = (int64_t)num_heads_kv * head_dim_q * 2;
+  const int page_layout = page_size >= 16 ? fmha_decode::kLayoutPagedBlock : fmha_decode::kLayoutPaged;
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,
       [&](const void* q, void* o, int32_t hq, int32_t hkv, int32_t kvg, void* ws, size_t ws_bytes) {
         SplitArgs a;
-        int rc2 = split_prepare(q, K_cache, V_cache, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q,
+        int rc2 = split_prepare(page_layout, q, K_cache, V_cache, o, max_seqlen_kv, batch, hq, hkv, kvg, head_dim_q,
                                 softmax_scale, ws, ws_bytes, 16 * row_bytes, a);
         if (rc2 != FMHA_DECODE_SUCCESS) return rc2;
         a.cu = seqlens_kv;
@@ -1093,8 +1141,7 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
         a.bt_stride = block_table_stride;
         a.page_shift = log2_pow2(page_size);
         a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
-        return split_launch(stream, page_size >= 16 ? fmha_decode::kLayoutPagedBlock : fmha_decode::kLayoutPaged, a,
-                            head_dim_q);
+        return split_launch(stream, page_layout, a, head_dim_q);
       });
 }
 
