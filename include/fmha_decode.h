@@ -237,17 +237,18 @@ int fmha_decode_fwd_paged(void* stream,
  *
  * Group sizes G = num_heads_q / num_heads_kv: any.  With max_seqlen_kv <= 16
  * as fmha_decode_fwd (the paged entry: G <= 8 as fmha_decode_fwd_paged, G > 8
- * as beyond 16).  Beyond 16 the VALU kernels exist for G = 1, 2, 4, 8; G = 3
- * and 5-7 run on copies of Q and O padded to 4 or 8 query heads per KV head.
- * G > 8 runs with Q and O padded to a multiple of 8 query heads per KV head
- * (copies only when G is not one) through split-KV passes on the matrix
- * cores (all query heads of a KV head per wave; K and V read once).  The
- * workspace size
- * includes the copies (two of [batch, Hkv * padded group, head_dim], ahead
- * of the split-KV data).  FMHA_DECODE_GQA_KERNEL=valu keeps every G on the
- * VALU kernels (G > 8 as ceil(G / 8) groups of 8 query heads per KV head,
- * still reading K and V once), =mfma puts every G on the matrix-core passes
- * (G <= 8 measures slower there), for comparisons.
+ * as beyond 16).  Beyond 16, G = 3 and 5-7 run on copies of Q and O padded
+ * to 4 or 8 query heads per KV head, and G > 8 on copies padded to a
+ * multiple of 8 (copies only when G is not one).  G <= 4 runs on the VALU
+ * split-KV passes; G = 5-8 and G > 8 on split-KV passes on the matrix cores
+ * (all query heads of a KV head per wave; K and V read once), except G = 5-8
+ * on pages of fewer than 16 rows with at least half a wave of KV heads,
+ * which takes the VALU passes.  The workspace size includes the copies (two
+ * of [batch, Hkv * padded group, head_dim], ahead of the split-KV data) and
+ * covers whichever passes the layout takes.  FMHA_DECODE_GQA_KERNEL=valu
+ * keeps every G on the VALU kernels (G > 8 as ceil(G / 8) groups of 8 query
+ * heads per KV head, still reading K and V once), =mfma puts every G on the
+ * matrix-core passes (G <= 4 measures slower there), for comparisons.
  */
 size_t fmha_decode_splitkv_workspace_size(int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                           int32_t max_seqlen_kv, int32_t head_dim);
