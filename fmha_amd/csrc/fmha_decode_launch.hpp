@@ -288,13 +288,12 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
       constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
                          : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
                                                                          : LAYOUT;
-      // Pages under 16 rows, one batch per wave: a descriptor per row takes
-      // the single pass's registers (SGPRs spilled, one wave per SIMD), and
-      // the split passes run those rows faster (µs, one-row pages, single
-      // pass against split: B=2048 S=128 Hq/Hkv 32/8 293 / 227, B=4096 S=64
-      // 332 / 232, B=16384 S=24 777 / 393, B=8192 S=64 16/16 1056 / 754,
-      // B=1024 S=128 16/16 D=256 456 / 369; 4- and 8-row pages alike).
-      if constexpr (OL != fmha_decode::kLayoutPaged) return launch_onepass_dg<D, G, OL, false>(ao, stream);
+      // Pages under 16 rows with G = 8: a descriptor per row for eight
+      // query heads' registers spills SGPRs, and the split passes run those
+      // rows faster (one-row pages, B=2048 S=128 Hq/Hkv 64/8: 249 against
+      // 272 µs); G <= 4 keeps the single pass (32/8: 185 against 221 µs,
+      // B=16384 S=24 357 / 388, 16/16 D=256 352 / 368; D=64 111 / 141).
+      if constexpr (OL != fmha_decode::kLayoutPaged || G < 8) return launch_onepass_dg<D, G, OL, false>(ao, stream);
     }
   }
   // The combine grid has one workgroup per (batch, query head, 32 dims).

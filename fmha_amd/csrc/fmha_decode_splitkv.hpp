@@ -171,6 +171,12 @@ struct LongRows {
   uint32_t page_shift;
   uint64_t page_stride;         // elements
   int lo, n;                    // first row, rows in range
+  // Paged layouts: set once a load has met an unmapped page (a negative
+  // block-table entry) among the rows in range; those rows read 0, and the
+  // caller makes the batch's outputs NaN (it is invalid).  Wave-uniform: a
+  // flag instead of NaN rows keeps the loads free of per-element selects
+  // (which took the single pass from 206-221 to 376-382 VGPRs).
+  int bad = 0;
 
   // lane_rows_: this lane's rows start that many rows after lo, and end at
   // lane_end (relative to lo, at most hi - lo): lane groups serving
@@ -244,19 +250,22 @@ struct LongRows {
   // Descriptor of `rows` rows from row `row` on, inside one page.  A row past
   // the end looks up the entry of a row the wave's range has and gets an
   // empty range.  An unmapped page (a negative block-table entry) gets an
-  // empty range too, nothing is read, and `unmapped` tells the caller to
-  // poison what it loads with NaN: the batch is invalid, and the NaN rows
-  // carry that to its outputs (scores and their sums turn NaN).
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows, bool& unmapped) const {
+  // empty range too, nothing is read, and `bad` is set when rows > 0.
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows) {
     const int32_t entry = load_uniform_i32(pages, (uint32_t)row >> page_shift);
-    const int64_t el = paged_row_elem(entry, (uint32_t)row, page_shift, page_stride, row_bytes >> 1);
-    unmapped = rows > 0 && el < 0;
-    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(el < 0 ? 0 : rows * (int)row_bytes);
-    return make_rsrc(uniform_ptr(base + (el < 0 ? 0u : (uint64_t)el)), range);
+    // paged_row_elem's arithmetic in unsigned 32-bit factors (a negative
+    // entry as page 0 with an empty range), which keeps it on the scalar
+    // unit: the signed 64-bit form cost the single pass about 90 VGPRs.
+    const bool neg = entry < 0;
+    const uint32_t page = neg ? 0u : (uint32_t)entry;
+    const uint32_t slot = (uint32_t)row & ((1u << page_shift) - 1u);
+    bad |= __builtin_amdgcn_readfirstlane(rows > 0 && neg ? 1 : 0);
+    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(neg ? 0 : rows * (int)row_bytes);
+    return make_rsrc(uniform_ptr(base + (uint64_t)page * page_stride + (uint64_t)slot * (row_bytes >> 1)), range);
   }
 
   template <int NR>
-  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
+  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) {
     static_assert(NR <= 16, "a sub-block fits a 16-row page");
     if constexpr (LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided) {
       // Rows past this lane's end are moved out of range (a strided range
@@ -268,22 +277,14 @@ struct LongRows {
       }
     } else if constexpr (LAYOUT == kLayoutPagedBlock) {
       const int valid = n - rel0 < 0 ? 0 : (n - rel0 > NR ? NR : n - rel0);
-      bool unmapped;
-      const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid, unmapped);
+      const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid);
 #pragma unroll
       for (int j = 0; j < NR; ++j) out[j] = buffer_load16_nt(pr, lane_off + (uint32_t)j * row_bytes);
-      if (unmapped) {
-#pragma unroll
-        for (int j = 0; j < NR; ++j)
-          if (j < valid) out[j] = u32x4{kNaNBf16x2, kNaNBf16x2, kNaNBf16x2, kNaNBf16x2};
-      }
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         const bool ok = rel0 + j < n;
-        bool unmapped;
-        out[j] = buffer_load16_nt(page_rsrc(lo + (ok ? rel0 + j : 0), ok ? 1 : 0, unmapped), lane_off);
-        if (unmapped) out[j] = u32x4{kNaNBf16x2, kNaNBf16x2, kNaNBf16x2, kNaNBf16x2};
+        out[j] = buffer_load16_nt(page_rsrc(lo + (ok ? rel0 + j : 0), ok ? 1 : 0), lane_off);
       }
     }
   }
@@ -311,6 +312,7 @@ struct PagedLaneRows {
   uint64_t page_stride;   // elements per page
   uint64_t row_elems;     // elements per slot (Hkv * D)
   int lo, lane_rows, lane_n;
+  static constexpr int bad = 0;  // unmapped pages give NaN rows instead (per lane)
 
   __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t, int lo_, int hi,
                                        int hk, bool head_ok, int r, int lane_rows_ = 0, int lane_end = 1 << 30) {
@@ -506,7 +508,9 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
         if (writer && (blkl & ((1 << C) - 1)) == 0) {
           const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk;
           a.m[idx] = bm;
-          a.l[idx] = bs;
+          // An unmapped page among the block's rows: a NaN sum makes every
+          // weight of the batch's heads, hence its outputs, NaN.
+          a.l[idx] = kv.bad ? __builtin_nanf("") : bs;
         }
       }
     }
