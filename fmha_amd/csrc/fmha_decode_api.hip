@@ -531,13 +531,13 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv
   int c = 1024;
   while (c > 64 && per_chunk * ((max_rows + c - 1) / c) < target) c /= 2;
   // Pages of fewer than 16 rows put every row at its own place in memory:
-  // the VALU P.V waves, which walk their chunk a sub-block at a time, then
-  // wait on scattered requests, and shorter chunks (more waves) hide that
-  // (µs by C = 128 / 256 / 512 / 1024 on one-row pages, B=64 S=4096 Hq=32
-  // Hkv=8: 243/220/227/309; B=8 S=32768: 239/230/256/312; Hq=64 Hkv=8
-  // 268/251/314/387; B=16 S=8192 16/16: 206/193/195/255).
-  if (layout == fmha_decode::kLayoutPaged && !split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d) && c > 256)
-    c = 256;
+  // the P.V waves, which walk their chunk a sub-block at a time, then wait
+  // on scattered requests, and shorter chunks (more waves) hide that (µs by
+  // C = 128 / 256 / 512 / 1024 on one-row pages, B=64 S=4096 Hq=32 Hkv=8:
+  // 243/220/227/309; B=8 S=32768: 239/230/256/312; Hq=64 Hkv=8
+  // 268/251/314/387; B=16 S=8192 16/16: 206/193/195/255; matrix cores,
+  // B=64 S=4096 64/4: 245/219/-/274).
+  if (layout == fmha_decode::kLayoutPaged && c > 256) c = 256;
   // FMHA_DECODE_SPLIT_CHUNK=<64|...|2048> overrides C (for sweeps; the
   // workspace size follows, and a launch checks its workspace against it).
   if (const char* e = std::getenv("FMHA_DECODE_SPLIT_CHUNK")) {

@@ -298,9 +298,10 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
   }
   // The combine grid has one workgroup per (batch, query head, 32 dims).
   if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
-  // P.V sub-block rows (register budget; pages under 16 rows build a
-  // descriptor per row, four SGPRs each).
-  constexpr int NR = G >= 8 || LAYOUT == fmha_decode::kLayoutPaged ? 8 : 16;
+  // P.V sub-block rows (register budget: pages under 16 rows address every
+  // row on its own, a descriptor or a 64-bit address per row; 16 rows there
+  // leave one wave per SIMD).
+  constexpr int NR = G >= 8 || LAYOUT == fmha_decode::kLayoutPaged || LAYOUT == fmha_decode::kLayoutPagedLanes ? 8 : 16;
   // One block per scores wave otherwise (two measured 1-3% slower).
   SplitArgs as = a;
   as.sub_shift = shift;

@@ -284,12 +284,13 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
     __builtin_amdgcn_sched_barrier(0);
   }
   // An unmapped page among rows [0, S) (seen by the K phase, which reads
-  // them all): the batch is invalid.
+  // them all): the batch is invalid (per lane group with MULTI, whose lane
+  // groups serve different batches).
   const bool poisoned = krows.bad != 0;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if constexpr (MULTI)
-      buffer_store16(o_rsrc, qo_off + g * D * 2, bad ? nan4 : pack_f16x8(acc[g]));
+      buffer_store16(o_rsrc, qo_off + g * D * 2, bad || poisoned ? nan4 : pack_f16x8(acc[g]));
     else
       buffer_store16(o_rsrc, qo_off + g * D * 2, poisoned ? nan4 : pack_f16x8(acc[g]));
   }

@@ -177,6 +177,7 @@ struct LongRows {
   // flag instead of NaN rows keeps the loads free of per-element selects
   // (which took the single pass from 206-221 to 376-382 VGPRs).
   int bad = 0;
+  __device__ __forceinline__ bool any_bad() const { return bad != 0; }
 
   // lane_rows_: this lane's rows start that many rows after lo, and end at
   // lane_end (relative to lo, at most hi - lo): lane groups serving
@@ -299,8 +300,10 @@ struct LongRows {
 // branch in a pipelined loop makes the compiler wait for every request at
 // its head): a row at or past the lane's end, or in an unmapped page (a
 // negative block-table entry), reads 16 bytes of Q's first row instead --
-// memory that always exists -- and is replaced by 0, or for the unmapped
-// page by NaN, which makes the batch's outputs NaN (an invalid batch).
+// memory that always exists -- and is replaced by 0; an unmapped page also
+// sets the lane's `bad`, and the caller makes the batch's outputs NaN (an
+// invalid batch; a flag rather than NaN rows keeps the loads to one select
+// per element: NaN rows took the VALU P.V pass from 245 to 352 VGPRs).
 // Block-table lookups stay inside the batch's row (entry 0 for rows past
 // the end), and no address is formed from a negative entry.
 template <int D, bool BLOCK>
@@ -312,7 +315,10 @@ struct PagedLaneRows {
   uint64_t page_stride;   // elements per page
   uint64_t row_elems;     // elements per slot (Hkv * D)
   int lo, lane_rows, lane_n;
-  static constexpr int bad = 0;  // unmapped pages give NaN rows instead (per lane)
+  int bad = 0;  // per lane: a load met an unmapped page among this lane's rows
+  // Some lane of the wave met one (the wave's lane groups serve one batch in
+  // the split passes).
+  __device__ __forceinline__ bool any_bad() const { return __builtin_amdgcn_ballot_w64(bad != 0) != 0; }
 
   __device__ __forceinline__ void init(const SplitArgs& a, const uint16_t* t, uint32_t b, int64_t, int lo_, int hi,
                                        int hk, bool head_ok, int r, int lane_rows_ = 0, int lane_end = 1 << 30) {
@@ -330,41 +336,77 @@ struct PagedLaneRows {
 
   // Rows lo + rel0 + lane_rows + j, j < NR (lo and lane_rows multiples of
   // 16, rel0 a multiple of NR <= 16: with BLOCK the NR rows lie in one
-  // 16-row block, hence in one page).
+  // 16-row block, hence in one page).  entries() requests their block-table
+  // entries (one per row, or one with BLOCK) and load_entries() the rows
+  // through them, so that a caller can request the entries a step ahead:
+  // the entries and rows are vector loads, which complete in order, so
+  // requesting both in one step makes every step wait a table round trip
+  // after the previous rows.
   template <int NR>
-  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) const {
+  static constexpr int kEntries = BLOCK ? 1 : NR;
+
+  template <int NR>
+  __device__ __forceinline__ void entries(int32_t (&e)[kEntries<NR>], int rel0) const {
+    const int row0 = rel0 + lane_rows;
+    if constexpr (BLOCK) {
+      const uint32_t abs0 = (uint32_t)(lo + row0);
+      e[0] = pages[row0 < lane_n ? abs0 >> page_shift : 0u];
+    } else {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const uint32_t abs = (uint32_t)(lo + row0 + j);
+        e[j] = pages[row0 + j < lane_n ? abs >> page_shift : 0u];
+      }
+    }
+  }
+
+  template <int NR>
+  __device__ __forceinline__ void load_entries(u32x4 (&out)[NR], int rel0, const int32_t (&e)[kEntries<NR>]) {
     const int row0 = rel0 + lane_rows;
     u32x4 v[NR];
     bool unmapped[NR];
+    // paged_row_elem's guard in unsigned factors (a negative entry as page 0,
+    // never read): the signed 64-bit form cost registers.
+    const uint32_t slot_mask = (1u << page_shift) - 1u;
     if constexpr (BLOCK) {
       const bool any = row0 < lane_n;
       const uint32_t abs0 = (uint32_t)(lo + row0);
-      const int32_t entry = pages[any ? abs0 >> page_shift : 0u];
-      const int64_t el = any ? paged_row_elem(entry, abs0, page_shift, page_stride, row_elems) : -1;
+      const bool neg = e[0] < 0;
+      const uint64_t el =
+          (uint64_t)(neg ? 0u : (uint32_t)e[0]) * page_stride + (uint64_t)(abs0 & slot_mask) * row_elems;
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        const bool ok = el >= 0 && row0 + j < lane_n;
+        const bool ok = !neg && row0 + j < lane_n;
         v[j] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(ok ? base + (uint64_t)el + (uint64_t)j * row_elems : safe));
-        unmapped[j] = any && entry < 0;
+            reinterpret_cast<const u32x4*>(ok ? base + el + (uint64_t)j * row_elems : safe));
+        unmapped[j] = any && neg;
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         const bool ok = row0 + j < lane_n;
         const uint32_t abs = (uint32_t)(lo + row0 + j);
-        const int32_t entry = pages[ok ? abs >> page_shift : 0u];
-        const int64_t el = ok ? paged_row_elem(entry, abs, page_shift, page_stride, row_elems) : -1;
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(el >= 0 ? base + (uint64_t)el : safe));
-        unmapped[j] = ok && entry < 0;
+        const bool neg = e[j] < 0;
+        const uint64_t el =
+            (uint64_t)(neg ? 0u : (uint32_t)e[j]) * page_stride + (uint64_t)(abs & slot_mask) * row_elems;
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ok && !neg ? base + el : safe));
+        unmapped[j] = ok && neg;
       }
     }
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
-      const bool ok = row0 + j < lane_n;
+      const bool ok = row0 + j < lane_n && !unmapped[j];
+      bad |= unmapped[j] ? 1 : 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) out[j][k] = unmapped[j] ? kNaNBf16x2 : (ok ? (uint32_t)v[j][k] : 0u);
+      for (int k = 0; k < 4; ++k) out[j][k] = ok ? (uint32_t)v[j][k] : 0u;
     }
+  }
+
+  template <int NR>
+  __device__ __forceinline__ void load(u32x4 (&out)[NR], int rel0) {
+    int32_t e[kEntries<NR>];
+    entries<NR>(e, rel0);
+    load_entries<NR>(out, rel0, e);
   }
 };
 
@@ -445,6 +487,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
   u32x4 ks[NR];
   kv.template load<NR>(ks, j0);
   __builtin_amdgcn_sched_barrier(0);
+  const bool kv_bad = kv.any_bad();
 
   // After the butterfly, lane r holds scores [blkl*W, blkl*W + W) of the
   // GH*NR (query head, row) pairs; lanes equal in r >> (NS - L) hold copies.
@@ -510,7 +553,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_kernel(SplitArgs
           a.m[idx] = bm;
           // An unmapped page among the block's rows: a NaN sum makes every
           // weight of the batch's heads, hence its outputs, NaN.
-          a.l[idx] = kv.bad ? __builtin_nanf("") : bs;
+          a.l[idx] = kv_bad ? __builtin_nanf("") : bs;
         }
       }
     }
@@ -771,25 +814,42 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   const int nsub = (rows_w + NR - 1) / NR;
   u32x4 va[NR], vb[NR];
   float ta[PL], tb[PL];
-  auto load = [&](u32x4 (&vr)[NR], float (&tv)[PL], int s) {
-    vrows.template load<NR>(vr, s * NR);
+  // Per-lane page lookups on pages under 16 rows (an entry per row): each
+  // sub-block's block-table entries are requested a step ahead of its rows
+  // (PF).  16-row pages look up one entry per sub-block and keep the
+  // registers (two more would cost the 16-row P.V its second wave per SIMD).
+  constexpr bool PF = LAYOUT == kLayoutPagedLanes;
+  constexpr int NE = PF ? NR : 1;
+  int32_t ea[NE], eb[NE];
+  auto load = [&](u32x4 (&vr)[NR], float (&tv)[PL], int s, const int32_t (&e)[NE]) {
+    if constexpr (PF)
+      vrows.template load_entries<NR>(vr, s * NR, e);
+    else
+      vrows.template load<NR>(vr, s * NR);
     // Sub-blocks never straddle a 16-row block (chunks start on multiples of 16).
     const uint32_t sub = (uint32_t)(((s * NR) / kSplitBlockRows) * hq * kSplitBlockRows +
                                     (s * NR) % kSplitBlockRows) * 4u;
 #pragma unroll
     for (int i = 0; i < PL; ++i) tv[i] = buffer_load_f32(t_rsrc, t_off[i] + sub);
   };
+  auto entries = [&](int32_t (&e)[NE], int s) {
+    if constexpr (PF) vrows.template entries<NR>(e, s * NR);
+  };
   auto left = [&](int (&rl)[PL], int s) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) rl[i] = slot_rows[i] - s * NR;
   };
-  load(va, ta, 0);
+  entries(ea, 0);
+  load(va, ta, 0, ea);
+  entries(eb, 1);
   for (int s = 0; s < nsub; s += 2) {
     int rl[PL];
-    load(vb, tb, s + 1);
+    load(vb, tb, s + 1, eb);
+    entries(ea, s + 2);
     left(rl, s);
     pv_sub_block<D, G, NR>(va, ta, gm, gsum, rl, slot_ok, lds_p, hkl, lane, acc);
-    load(va, ta, s + 2);
+    load(va, ta, s + 2, ea);
+    entries(eb, s + 3);
     left(rl, s + 1);
     if (s + 1 < nsub) pv_sub_block<D, G, NR>(vb, tb, gm, gsum, rl, slot_ok, lds_p, hkl, lane, acc);
   }

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
   kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
   u32x4 kr[NR];
   kv.template load<NR>(kr, j0);
+  const bool kv_bad = kv.any_bad();
   // This KV head's query rows: tile t's B operands (lane (q, n): query
   // column 16 t + n, 16-byte chunks 4 cc + q), requested one tile ahead.
   const __amdgpu_buffer_rsrc_t q_rsrc =
@@ -161,7 +162,9 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_scores_group_kernel(Spl
         if (q == 0) {
           const uint64_t idx = ((uint64_t)b * hq + (uint64_t)hk * G + g) * a.nblk + blk0 + p;
           a.m[idx] = m;
-          a.l[idx] = sum;
+          // An unmapped page among the wave's rows: a NaN sum makes the
+          // batch's weights, hence its outputs, NaN.
+          a.l[idx] = kv_bad ? __builtin_nanf("") : sum;
         }
       }
     }
