@@ -214,6 +214,12 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
     multi = span < (int64_t(1) << 30);
   }
   int w = waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
+  // Waves that serve several batches (each lane group its own length and
+  // rows) want at least 8 per CU at D <= 128 (B=30720 with lengths on the
+  // device, µs at the byte model's cap / 8 waves: Hq/Hkv 8/1 S=16 79.0 /
+  // 65.0, 4/1 60.4 / 56.6, 2/1 51.6 / 48.4, 8/2 109.5 / 102.7, D=64 8/1
+  // 49.1 / 38.6; short rows and D = 256 flat).
+  if (multi && dq <= 128 && w < 8) w = 8;
   // FMHA_DECODE_WAVE_CAP=<waves per CU> overrides the cap (for sweeps).
   if (const char* e = std::getenv("FMHA_DECODE_WAVE_CAP")) {
     const int v = std::atoi(e);
