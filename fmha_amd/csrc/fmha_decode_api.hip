@@ -126,6 +126,17 @@ int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths,
   }
   if (!bucket_per_wave && g == 8 && dq == 64) return s <= 4 ? kMaxWavesPerCU : (s <= 8 || g_real > 5 ? 6 : 5);
   if (!bucket_per_wave && g == 8 && dq == 256 && s > 2 && s <= 8) return 5;
+  if (device_lengths && g == 8 && dq == 128) {
+    // The 8-head kernel with lengths on the device: a budget of (120 + 7.5
+    // rows) KiB, which puts every shape swept within 1% of its best cap
+    // (B=30720, Hkv = 4 / 8 / 16, G = 5 and 8, S = 4 / 8 / 16 and the
+    // reference's Poisson lengths; µs with 200 KiB against this: Hq/Hkv
+    // 32/4 S=16 252.2 / 212.3, 128/16 S=16 1006.0 / 922.4, 64/8 S=16 510.9 /
+    // 475.3, 128/16 S=4 492.5 / 460.4, 80/16 S=8 535.4 / 499.1).
+    const int64_t w = (3840LL + 15LL * rows16) / (4LL * rows16 + 64LL * g_real);
+    if (w >= 16) return kMaxWavesPerCU;
+    return w < 4 ? 4 : (int)w;
+  }
   const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
   const int64_t budget = g >= 4           ? kInflightBytesPerCUWideGroups
                          : device_lengths ? kInflightBytesPerCUDeviceLengths
