@@ -72,15 +72,13 @@ extern "C" {
  *   num_heads_kv    > 0; any group size G = num_heads_q / num_heads_kv.
  *                   G <= 8 runs the VALU kernel (G = 3 on its 4-head and
  *                   5-7 on its 8-head instantiation, the extra heads
- *                   reading and writing nothing), except for head_dim 64 and
- *                   for G = 3 at head_dim 128 with a uniform length of 8 or
- *                   more, which run the matrix-core kernel, as does every
- *                   G > 8 (it needs num_heads_kv * head_dim below 2^24,
- *                   else FMHA_DECODE_ERROR_NOT_SUPPORTED).  The same
- *                   numerics within the comparison gate, not the same bits.
- *                   The environment variable FMHA_DECODE_GQA_KERNEL=mfma
- *                   runs the matrix-core kernel for every G, =valu the VALU
- *                   kernel wherever it exists (G <= 8).  This entry point,
+ *                   reading and writing nothing); G > 8 runs the
+ *                   matrix-core kernel (it needs num_heads_kv * head_dim
+ *                   below 2^24, else FMHA_DECODE_ERROR_NOT_SUPPORTED).  The
+ *                   same numerics within the comparison gate, not the same
+ *                   bits.  The environment variable
+ *                   FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel
+ *                   for every G.  This entry point,
  *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
  *                   any G, and so do the split-KV entries (through a
  *                   padded query group beyond 16 rows);
