@@ -194,10 +194,13 @@ hipError_t launch_mfma_layout(const fmha_decode::GroupArgs& g, int dq, int ns, i
 
 // Per-CU wave caps of the two streaming passes (dynamic LDS reservation).
 // Scores waves request 16 KiB of K plus G KiB of Q at once; P.V waves keep
-// two 16-row (8-row for G = 8) sub-blocks of V in flight.  Sweeps over
-// long-context shapes (B=64 S=4096, B=8 S=32768, B=256 S=1024 G=8, B=1
-// S=131072) put both optima at 8 (4-6 cost 2-5%, 12-16 within 1%).
-constexpr int kSplitScoresWavesPerCU = 8;
+// two 16-row (8-row for G = 8) sub-blocks of V in flight.  Swept apart
+// (µs at scores caps 4 / 6 / 8 / 12 / 16, P.V at 8; Hq/Hkv 32/8 D=128):
+// B=64 S=4096 210.8/192.7/190.9/188.7/187.9, B=8 S=32768
+// 213.9/194.0/191.7/189.9/190.3, B=1 S=131072 116.8/107.7/106.7/104.4/105.2;
+// Hq=Hkv=16 B=16 S=8192 and the matrix-core passes (64/8 B=256 S=1024)
+// flat from 6 up.  P.V caps of 4-12 are within 1% everywhere.
+constexpr int kSplitScoresWavesPerCU = 12;
 constexpr int kSplitPvWavesPerCU = 8;
 
 // Rows longer than 16 go through one pass (onepass_decode_kernel: one wave
