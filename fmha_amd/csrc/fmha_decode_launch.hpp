@@ -213,7 +213,15 @@ constexpr int kSplitPvWavesPerCU = 8;
 // where a wave's walk over its row outlasts split-KV's shorter waves.
 constexpr int64_t kOnepassMinUnits = 512;
 constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
+// Waves per CU of the single pass: 8, and 4 for one or two query heads per
+// KV head with rows of at most 48 (three 16-row blocks), whose waves compute
+// little per byte (µs at 4 / 8 waves, D=128 unless given: B=16384 S=24
+// Hq/Hkv 16/16 497.5 / 545.9, 16/8 S=32 341.4 / 363.8, B=8192 S=48 32/16
+// 503.2 / 539.2, B=4096 S=32 16/16 D=256 326.0 / 344.4; longer rows are
+// flat or faster at 8, B=1024 S=128 16/16 172.8 / 163.8; G = 4 and 8 flat
+// from 8 up).
 constexpr int kOnepassWavesPerCU = 8;
+constexpr int kOnepassWavesPerCUNarrow = 4;
 
 // Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
 // the KV-head groups of one.
@@ -231,7 +239,8 @@ template <int D, int G, int LAYOUT, bool MULTI>
 hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>;
   const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
-  const size_t cap = lds_reserve_kernel<kernel>(kOnepassWavesPerCU);
+  const int waves = !MULTI && G <= 2 && a.nblk <= 3 ? kOnepassWavesPerCUNarrow : kOnepassWavesPerCU;
+  const size_t cap = lds_reserve_kernel<kernel>(waves);
   hipLaunchKernelGGL(kernel, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
                      a);
   return hipGetLastError();
