@@ -313,10 +313,14 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // FMHA_DECODE_GQA_KERNEL=valu keeps every G on the VALU passes (G > 8 on
 // ceil(G / 8) launch KV heads of 8 query heads), =mfma puts every G on the
 // matrix cores.
-bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d) {
+bool gqa_kernel_forced(const char* kind) {
   const char* e = std::getenv("FMHA_DECODE_GQA_KERNEL");
-  if (e && std::strcmp(e, "valu") == 0) return false;
-  if (e && std::strcmp(e, "mfma") == 0) return true;
+  return e && std::strcmp(e, kind) == 0;
+}
+
+bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d) {
+  if (gqa_kernel_forced("valu")) return false;
+  if (gqa_kernel_forced("mfma")) return true;
   if (kv_groups > 1) return true;
   if (g_launch < 8) return false;
   if (layout != fmha_decode::kLayoutPaged) return true;
@@ -869,7 +873,45 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int g = a.num_heads_q / a.num_heads_kv;
   hipError_t err;
+  // Paged caches with fewer KV heads than a wave holds read through
+  // per-lane addresses, so that the idle lane groups take other blocks or
+  // chunks of the same heads (sub-units, as on packed caches).
+  const int hpw = kWaveSize / (head_dim / 8);
+  const bool lanes = 2 * a.num_heads_kv <= hpw && hpw % (2 * a.num_heads_kv) == 0;
+  // The VALU long-row kernels; onepass_only: their single pass or nothing.
+  auto valu = [&](bool onepass_only) -> hipError_t {
+    switch (layout) {
+      case fmha_decode::kLayoutPacked:
+        return launch_split_layout<fmha_decode::kLayoutPacked>(a, head_dim, g, s, onepass_only);
+      case fmha_decode::kLayoutStrided:
+        return launch_split_layout<fmha_decode::kLayoutStrided>(a, head_dim, g, s, onepass_only);
+      case fmha_decode::kLayoutPaged:
+        return lanes ? launch_split_layout<fmha_decode::kLayoutPagedLanes>(a, head_dim, g, s, onepass_only)
+                     : launch_split_layout<fmha_decode::kLayoutPaged>(a, head_dim, g, s, onepass_only);
+      default:
+        return lanes ? launch_split_layout<fmha_decode::kLayoutPagedBlockLanes>(a, head_dim, g, s, onepass_only)
+                     : launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s, onepass_only);
+    }
+  };
   if (split_on_matrix_cores(a.num_heads_q / a.num_heads_kv, a.kv_groups, layout, a.num_heads_kv, head_dim)) {
+    // Groups of 5-8 on rows that the VALU single pass holds (enough waves,
+    // a row's scores in LDS) and of at most 96 rows at D = 128, 128 at
+    // D = 256, 32 at D = 64 or with several batches per wave take it: one
+    // launch against four (µs, packed, D = 128 unless given, matrix-core
+    // split vs single pass: B=16384 S=24 Hq/Hkv 64/8 486 vs 348, B=8192
+    // S=32 56/8 337 vs 299, B=4096 S=64 64/8 230 vs 209, 128/16 451 vs 412,
+    // B=2730 S=96 235 vs 211, D=256 B=1024 S=128 48/8 246 vs 209, D=64
+    // B=16384 S=24 64/8 451 vs 310, S=32 40/8 520 vs 444, B=8192 S=32 8/1
+    // 47 vs 41).  Longer rows favour the split: S=112 231 vs 232, S=160 222
+    // vs 249, D=256 S=160 240 vs 227 but 16-row pages 247 vs 273, D=64
+    // B=8192 S=48 262 vs 346.
+    if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma")) {
+      err = valu(true);
+      if (err != kOnepassNotTaken) {
+        if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+        return FMHA_DECODE_SUCCESS;
+      }
+    }
     // The matrix cores take the cache's KV heads with all of their query
     // heads (a group above 8: ns * 8 of them, the same workspace plan).
     SplitArgs m = a;
@@ -893,23 +935,7 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
     if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
     return FMHA_DECODE_SUCCESS;
   }
-  // Paged caches with fewer KV heads than a wave holds read through
-  // per-lane addresses, so that the idle lane groups take other blocks or
-  // chunks of the same heads (sub-units, as on packed caches).
-  const int hpw = kWaveSize / (head_dim / 8);
-  const bool lanes = 2 * a.num_heads_kv <= hpw && hpw % (2 * a.num_heads_kv) == 0;
-  switch (layout) {
-    case fmha_decode::kLayoutPacked: err = launch_split_layout<fmha_decode::kLayoutPacked>(a, head_dim, g, s); break;
-    case fmha_decode::kLayoutStrided: err = launch_split_layout<fmha_decode::kLayoutStrided>(a, head_dim, g, s); break;
-    case fmha_decode::kLayoutPaged:
-      err = lanes ? launch_split_layout<fmha_decode::kLayoutPagedLanes>(a, head_dim, g, s)
-                  : launch_split_layout<fmha_decode::kLayoutPaged>(a, head_dim, g, s);
-      break;
-    default:
-      err = lanes ? launch_split_layout<fmha_decode::kLayoutPagedBlockLanes>(a, head_dim, g, s)
-                  : launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s);
-      break;
-  }
+  err = valu(false);
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
 }

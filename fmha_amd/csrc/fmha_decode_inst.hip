@@ -124,39 +124,39 @@ template hipError_t launch_mfma_d<256, kLayoutPacked>(const GroupArgs&, int, int
 #elif FMHA_DECODE_PART == 22
 template hipError_t launch_mfma_d<256, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
 #elif FMHA_DECODE_PART == 23
-template hipError_t launch_split_d<64, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 24
-template hipError_t launch_split_d<64, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 25
-template hipError_t launch_split_d<64, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 26
-template hipError_t launch_split_d<64, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 27
-template hipError_t launch_split_d<64, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 28
-template hipError_t launch_split_d<64, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<64, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 29
-template hipError_t launch_split_d<128, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 30
-template hipError_t launch_split_d<128, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 31
-template hipError_t launch_split_d<128, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 32
-template hipError_t launch_split_d<128, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 33
-template hipError_t launch_split_d<128, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 34
-template hipError_t launch_split_d<128, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<128, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 35
-template hipError_t launch_split_d<256, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<256, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 36
-template hipError_t launch_split_d<256, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<256, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 37
-template hipError_t launch_split_d<256, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
-template hipError_t launch_split_d<256, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<256, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
+template hipError_t launch_split_d<256, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 38
-template hipError_t launch_split_d<256, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
-template hipError_t launch_split_d<256, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+template hipError_t launch_split_d<256, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
+template hipError_t launch_split_d<256, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
 #elif FMHA_DECODE_PART == 39
 template hipError_t launch_split_group_d<64, kLayoutPacked>(const SplitArgs&, hipStream_t);
 #elif FMHA_DECODE_PART == 40

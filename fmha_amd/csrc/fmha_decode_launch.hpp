@@ -261,9 +261,17 @@ hipError_t launch_pad_query_group(const uint16_t* q, uint16_t* qp, uint64_t stre
 hipError_t launch_unpad_output_group(const uint16_t* op, uint16_t* o, uint64_t streams, int G, int GP, int D,
                                      hipStream_t stream);
 
+// Returned by the long-row launchers with onepass_only when the single pass
+// does not apply (nothing launched).
+constexpr hipError_t kOnepassNotTaken = hipErrorNotReady;
+
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
+// onepass_only: launch the single pass if it applies, on rows of at most
+// six 16-row blocks at D = 128, eight at D = 256, two at D = 64 or with
+// several batches per wave, else nothing (kOnepassNotTaken), for callers
+// that run the split passes elsewhere.
 template <int D, int G, int LAYOUT>
-hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
+hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_only = false) {
   // With fewer KV heads than a wave holds, its lane groups serve 2^shift
   // batches (single pass), blocks (scores) or chunks (P.V) instead of
   // idling: packed and strided layouts, whose descriptor spans the rows
@@ -294,7 +302,8 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
       if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
-    if (onepass_fits<D, G>(ao)) {
+    const int only_nblk = ao.sub_shift > 0 || D == 64 ? 2 : (D == 256 ? 8 : 6);
+    if (onepass_fits<D, G>(ao) && (!onepass_only || a.nblk <= only_nblk)) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
       constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
@@ -308,6 +317,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
       if constexpr (OL != fmha_decode::kLayoutPaged || G < 8) return launch_onepass_dg<D, G, OL, false>(ao, stream);
     }
   }
+  if (onepass_only) return kOnepassNotTaken;
   // The combine grid has one workgroup per (batch, query head, 32 dims).
   if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   // P.V sub-block rows (register budget: pages under 16 rows address every
@@ -345,21 +355,21 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream) {
 }
 
 template <int D, int LAYOUT>
-hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream) {
+hipError_t launch_split_d(const SplitArgs& a, int g, hipStream_t stream, bool onepass_only) {
   switch (g) {
-    case 1: return launch_split_dg<D, 1, LAYOUT>(a, stream);
-    case 2: return launch_split_dg<D, 2, LAYOUT>(a, stream);
-    case 4: return launch_split_dg<D, 4, LAYOUT>(a, stream);
-    default: return launch_split_dg<D, 8, LAYOUT>(a, stream);
+    case 1: return launch_split_dg<D, 1, LAYOUT>(a, stream, onepass_only);
+    case 2: return launch_split_dg<D, 2, LAYOUT>(a, stream, onepass_only);
+    case 4: return launch_split_dg<D, 4, LAYOUT>(a, stream, onepass_only);
+    default: return launch_split_dg<D, 8, LAYOUT>(a, stream, onepass_only);
   }
 }
 
 template <int LAYOUT>
-hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t stream) {
+hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t stream, bool onepass_only = false) {
   switch (d) {
-    case 64: return launch_split_d<64, LAYOUT>(a, g, stream);
-    case 128: return launch_split_d<128, LAYOUT>(a, g, stream);
-    default: return launch_split_d<256, LAYOUT>(a, g, stream);
+    case 64: return launch_split_d<64, LAYOUT>(a, g, stream, onepass_only);
+    case 128: return launch_split_d<128, LAYOUT>(a, g, stream, onepass_only);
+    default: return launch_split_d<256, LAYOUT>(a, g, stream, onepass_only);
   }
 }
 
@@ -438,24 +448,24 @@ extern template hipError_t launch_mfma_d<128, kLayoutPacked>(const GroupArgs&, i
 extern template hipError_t launch_mfma_d<128, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
 extern template hipError_t launch_mfma_d<256, kLayoutPacked>(const GroupArgs&, int, int, hipStream_t);
 extern template hipError_t launch_mfma_d<256, kLayoutStrided>(const GroupArgs&, int, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<64, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<128, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutPacked>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutStrided>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutPaged>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t);
-extern template hipError_t launch_split_d<256, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t);
+extern template hipError_t launch_split_d<64, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<64, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<64, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<64, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<64, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<64, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<128, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutPacked>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutStrided>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutPaged>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutPagedLanes>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutPagedBlock>(const SplitArgs&, int, hipStream_t, bool);
+extern template hipError_t launch_split_d<256, kLayoutPagedBlockLanes>(const SplitArgs&, int, hipStream_t, bool);
 extern template hipError_t launch_split_group_d<64, kLayoutPacked>(const SplitArgs&, hipStream_t);
 extern template hipError_t launch_split_group_d<64, kLayoutStrided>(const SplitArgs&, hipStream_t);
 extern template hipError_t launch_split_group_d<64, kLayoutPaged>(const SplitArgs&, hipStream_t);

@@ -209,13 +209,12 @@ def test_strided_long_sub_units(D, Hq, Hkv):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd sub-units D={D} Hq={Hq} Hkv={Hkv}")
 
 
-@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2049), (64, 16, 2, 2100)])
-def test_strided_single_pass_batches_per_wave(D, Hq, Hkv, B):
+@pytest.mark.parametrize("D,Hq,Hkv,B,cap", [(128, 8, 1, 2049, 32), (128, 4, 1, 2049, 80), (64, 16, 2, 2100, 80)])
+def test_strided_single_pass_batches_per_wave(D, Hq, Hkv, B, cap):
     """Single pass, several batches per wave through one strided descriptor,
-    BHSD with NaN padding."""
+    BHSD with NaN padding (G = 8 takes it on rows of up to 32)."""
     import fmha_amd
     import torch
-    cap = 80
     rng = np.random.default_rng(D + B)
     seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
     seqlens[:4] = [cap, 0, 1, 17]

@@ -125,7 +125,10 @@ def test_bad_and_empty_lengths():
 
 # Single-pass path (onepass_decode_kernel): taken by fmha_decode_fwd_splitkv
 # when batch * ceil(Hkv / (64 / (D/8))) >= 512 and the wave's scores and
-# weights (HPW * G * rows * 6 bytes, rows rounded up to 32) fit 40 KiB of LDS.
+# weights (HPW * G * rows * 6 bytes, rows rounded up to 32) fit 40 KiB of LDS;
+# at G = 8 (packed layout) only on rows of at most 96 at D = 128, 128 at
+# D = 256, 32 at D = 64 or with several batches per wave (else the
+# matrix-core split).
 def _onepass_taken(B, Hq, Hkv, D, max_len):
     """Waves = batch groups (2^shift batches each when Hkv is below the
     heads a wave holds, see _sub_units) times KV-head groups."""
@@ -133,6 +136,8 @@ def _onepass_taken(B, Hq, Hkv, D, max_len):
     r = _sub_units(Hkv, D)
     waves = (B + r - 1) // r * ((Hkv + hpw // r - 1) // (hpw // r))
     sp = (max_len + 31) // 32 * 32
+    if Hq // Hkv == 8 and max_len > (32 if r > 1 or D == 64 else 128 if D == 256 else 96):
+        return False
     return waves >= 512 and hpw * (Hq // Hkv) * sp * 6 <= 40 * 1024
 
 
@@ -148,10 +153,27 @@ def test_split_path_still_covered():
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 def test_onepass_all_shapes(D, B, G):
     Hkv, max_len = 16, 96
-    assert _onepass_taken(B, Hkv * G, Hkv, D, max_len)
+    # G = 8 at D = 64 takes the matrix-core split on rows above 32 (same
+    # cases, same gate).
+    assert _onepass_taken(B, Hkv * G, Hkv, D, max_len) == (G < 8 or D > 64)
     seqlens = np.random.default_rng(D + G).integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hkv * G, Hkv, D, seqlens, max_len, seed=900 + D + G)
+
+
+@pytest.mark.parametrize("D,Hkv,B,max_len", [(64, 16, 1024, 32), (64, 1, 4100, 32), (128, 8, 1100, 96),
+                                             (128, 2, 2050, 32), (256, 8, 600, 128)])
+def test_onepass_group_of_eight(D, Hkv, B, max_len):
+    """G = 8 on the single pass at the longest rows it takes there for each
+    head dim (one batch per wave, and several: Hkv = 1, 2), with the 16-row
+    edges, empty rows and a last wave partly empty."""
+    Hq = 8 * Hkv
+    assert _onepass_taken(B, Hq, Hkv, D, max_len) and not _onepass_taken(B, Hq, Hkv, D, max_len + 1)
+    rng = np.random.default_rng(D * 3 + Hkv + B)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:7] = np.minimum([max_len, 0, 1, 15, 16, 17, 31], max_len)
+    seqlens[-1] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=2000 + D + Hkv)
 
 
 def test_onepass_edge_lengths():
@@ -197,15 +219,15 @@ def test_sub_units(D, Hq, Hkv, max_len):
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=1300 + D + Hkv + max_len)
 
 
-@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2047), (64, 16, 2, 2050), (256, 8, 1, 1030), (128, 8, 2, 1100)])
-def test_onepass_batches_per_wave(D, Hq, Hkv, B):
+@pytest.mark.parametrize("D,Hq,Hkv,B,max_len", [(128, 8, 1, 2047, 32), (128, 4, 1, 2047, 96), (64, 8, 2, 2050, 96),
+                                                 (256, 8, 1, 1030, 32), (256, 4, 1, 1030, 96), (128, 8, 2, 1100, 96)])
+def test_onepass_batches_per_wave(D, Hq, Hkv, B, max_len):
     """Single pass with several batches per wave (fewer KV heads than a wave
     holds): mixed lengths in one wave, empty rows, a last wave partly empty."""
-    max_len = 96
     assert _sub_units(Hkv, D) > 1 and _onepass_taken(B, Hq, Hkv, D, max_len)
     rng = np.random.default_rng(D + Hkv + B)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
-    seqlens[:6] = [max_len, 0, 1, 17, 33, 95]
+    seqlens[:6] = np.minimum([max_len, 0, 1, 17, 33, 95], max_len)
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=1500 + D + Hkv)
 
 
@@ -213,7 +235,7 @@ def test_onepass_batches_per_wave_invalid_length():
     """An invalid length gives NaN for its batch only, the other batches of
     its wave stay exact."""
     import torch
-    B, Hq, Hkv, D, max_len = 2048, 8, 1, 128, 64
+    B, Hq, Hkv, D, max_len = 2048, 8, 1, 128, 32
     assert _onepass_taken(B, Hq, Hkv, D, max_len)
     rng = np.random.default_rng(77)
     seqlens = rng.integers(1, max_len + 1, size=B).astype(np.int32)
