@@ -895,16 +895,17 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
   };
   if (split_on_matrix_cores(a.num_heads_q / a.num_heads_kv, a.kv_groups, layout, a.num_heads_kv, head_dim)) {
     // Groups of 5-8 on rows that the VALU single pass holds (enough waves,
-    // a row's scores in LDS) and of at most 96 rows at D = 128, 128 at
-    // D = 256, 32 at D = 64 or with several batches per wave take it: one
-    // launch against four (µs, packed, D = 128 unless given, matrix-core
-    // split vs single pass: B=16384 S=24 Hq/Hkv 64/8 486 vs 348, B=8192
-    // S=32 56/8 337 vs 299, B=4096 S=64 64/8 230 vs 209, 128/16 451 vs 412,
-    // B=2730 S=96 235 vs 211, D=256 B=1024 S=128 48/8 246 vs 209, D=64
-    // B=16384 S=24 64/8 451 vs 310, S=32 40/8 520 vs 444, B=8192 S=32 8/1
-    // 47 vs 41).  Longer rows favour the split: S=112 231 vs 232, S=160 222
-    // vs 249, D=256 S=160 240 vs 227 but 16-row pages 247 vs 273, D=64
-    // B=8192 S=48 262 vs 346.
+    // a row's scores in LDS, every lane group busy) take it on rows of at
+    // most 128 at D = 128 and 256 and any it holds at D = 64 (with several
+    // batches per wave: 32 at D = 128, 64 at D = 64, 128 at D = 256): one
+    // launch against four (µs, packed,
+    // D = 128 unless given, matrix-core split vs single pass: B=16384 S=24
+    // Hq/Hkv 64/8 486 vs 332, B=4096 S=64 64/8 230 vs 204, B=2048 S=128
+    // 225 vs 221, D=256 B=1024 S=128 48/8 246 vs 207, D=64 B=12288 S=32
+    // 343 vs 165, B=4096 S=96 216 vs 201, MQA-like 8/1 D=64 B=16384 S=64
+    // 87 vs 67, D=256 B=8192 S=64 135 vs 119).  Longer rows favour the
+    // split: D=128 S=160 224 vs 237, D=256 S=256 222 vs 252, 8/1 S=48 124
+    // vs 148.
     if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma")) {
       err = valu(true);
       if (err != kOnepassNotTaken) {

@@ -266,10 +266,10 @@ hipError_t launch_unpad_output_group(const uint16_t* op, uint16_t* o, uint64_t s
 constexpr hipError_t kOnepassNotTaken = hipErrorNotReady;
 
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
-// onepass_only: launch the single pass if it applies, on rows of at most
-// six 16-row blocks at D = 128, eight at D = 256, two at D = 64 or with
-// several batches per wave, else nothing (kOnepassNotTaken), for callers
-// that run the split passes elsewhere.
+// onepass_only: launch the single pass if it applies with every lane group
+// busy, on rows of at most eight 16-row blocks at D = 128 and 256 (with
+// several batches per wave: two at D = 128, four at D = 64), else nothing
+// (kOnepassNotTaken), for callers that run the split passes elsewhere.
 template <int D, int G, int LAYOUT>
 hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_only = false) {
   // With fewer KV heads than a wave holds, its lane groups serve 2^shift
@@ -302,8 +302,10 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
       if (span >= (int64_t(1) << 30)) ao.sub_shift = 0;
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
-    const int only_nblk = ao.sub_shift > 0 || D == 64 ? 2 : (D == 256 ? 8 : 6);
-    if (onepass_fits<D, G>(ao) && (!onepass_only || a.nblk <= only_nblk)) {
+    // onepass_only: waves with no idle lane groups, on rows up to where the
+    // single pass measured faster than the matrix-core split.
+    const int only_nblk = shift > 0 ? (D == 64 ? 4 : D == 128 ? 2 : 8) : (D == 64 ? a.nblk : 8);
+    if (onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
       constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged

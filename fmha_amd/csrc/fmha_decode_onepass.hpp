@@ -19,8 +19,10 @@
 //      fp16 O.
 //
 // K and V are each read once and nothing else touches memory (no workspace),
-// in one launch.  LDS per wave: HPW * G * SP * 6 bytes (fp32 scores and bf16
-// weights for SP = the row bound rounded up to 32).  Both loops run an even
+// in one launch.  LDS per wave: HPW * G * (6 SP + 8) bytes (fp32 scores and
+// bf16 weights for SP = the row bound rounded up to 32, each (KV head, query
+// head) row padded by one dword, so that the softmax lanes, one row each,
+// and the P.V lane groups fall in different banks).  Both loops run an even
 // number of sub-blocks with no branch inside, so every wait is a fixed count:
 // an odd row's last sub-block pairs with one past its end, whose requests
 // read 0 without memory access, whose scores land in LDS padding the softmax
@@ -42,10 +44,15 @@ struct OnepassShape {
 // blocks, so the loops' paired sub-blocks always have room.
 constexpr int onepass_lds_rows(int nblk) { return (nblk + 1) / 2 * 2 * kSplitBlockRows; }
 
-// LDS bytes one wave needs for a row stride of sp.
+// LDS strides for sp rows: fp32 scores (floats) and bf16 weights (halves),
+// both an odd number of dwords.
+constexpr int onepass_score_stride(int sp) { return sp + 1; }
+constexpr int onepass_weight_stride(int sp) { return sp + 2; }
+
+// LDS bytes one wave needs for sp rows.
 template <int D, int G>
 constexpr size_t onepass_lds_bytes(int sp) {
-  return (size_t)OnepassShape<D, G>::HPW * G * sp * 6;
+  return (size_t)OnepassShape<D, G>::HPW * G * (onepass_score_stride(sp) * 4 + onepass_weight_stride(sp) * 2);
 }
 
 // MULTI: several batches per wave (fewer KV heads than a wave holds,
@@ -148,9 +155,11 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, q_bytes);
   const uint32_t qo_off =
       head_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
-  const int sp = onepass_lds_rows(a.nblk);  // LDS row stride
-  float* sc = onepass_lds + (size_t)hkl * G * sp;                                         // [G][sp] fp32
-  uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sp) + (size_t)hkl * G * sp;  // [G][sp]
+  const int sp = onepass_lds_rows(a.nblk);
+  const int sps = onepass_score_stride(sp);   // floats
+  const int spw = onepass_weight_stride(sp);  // halves (even: the P.V reads pairs)
+  float* sc = onepass_lds + (size_t)hkl * G * sps;                                          // [G][sps] fp32
+  uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sps) + (size_t)hkl * G * spw;  // [G][spw]
 
   // Rows [0, S) of each lane group's batch: later rows read 0 without access.
   constexpr bool LANES = LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes;
@@ -190,7 +199,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
 #pragma unroll
         for (int w = 0; w < W; ++w) {
           const int vi = blkl * W + w;
-          sc[(g0 + vi / NR) * sp + s * NR + vi % NR] = x[w] * a.scale;
+          sc[(g0 + vi / NR) * sps + s * NR + vi % NR] = x[w] * a.scale;
         }
       }
     }
@@ -234,7 +243,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
   {
     const int g = r % G;
     const int j0 = r / G;
-    float* t = sc + g * sp;
+    float* t = sc + g * sps;
     float m = -__builtin_inff();
     for (int j = j0; j < S; j += LPG) m = fmaxf(m, t[j]);
 #pragma unroll
@@ -247,7 +256,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
     }
 #pragma unroll
     for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
-    uint16_t* p = pw + g * sp;
+    uint16_t* p = pw + g * spw;
     const int pad = (smax + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
     for (int j = j0; j < pad; j += LPG)
       p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? t[j] / l : 0.0f)) : (uint16_t)0;
@@ -267,7 +276,7 @@ __global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs
     uint32_t pp[G][NRV / 2];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint32_t* pairs = reinterpret_cast<const uint32_t*>(pw + g * sp + s * NRV);
+      const uint32_t* pairs = reinterpret_cast<const uint32_t*>(pw + g * spw + s * NRV);
 #pragma unroll
       for (int jp = 0; jp < NRV / 2; ++jp) pp[g][jp] = pairs[jp];
     }
