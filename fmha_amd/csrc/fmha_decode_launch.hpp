@@ -312,11 +312,17 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
                          : LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
                                                                          : LAYOUT;
       // Pages under 16 rows with G = 8: a descriptor per row for eight
-      // query heads' registers spills SGPRs, and the split passes run those
-      // rows faster (one-row pages, B=2048 S=128 Hq/Hkv 64/8: 249 against
-      // 272 µs); G <= 4 keeps the single pass (32/8: 185 against 221 µs,
+      // query heads' registers spills SGPRs into VGPR lanes, and beyond
+      // six 16-row blocks (four at D = 64, eight at D = 256) the split
+      // passes run those rows faster (one-row pages, Hq/Hkv 64/8, µs, single
+      // pass against split: B=16384 S=24 424 / 455, B=4096 S=64 220 / 259,
+      // B=2730 S=96 229 / 247, B=2048 S=128 265 / 239, B=1365 S=192 340 /
+      // 243; D=64 B=12288 S=32 183 / 261, B=6144 S=64 202 / 251, B=4096
+      // S=96 265 / 251; D=256 48/8 B=1024 S=128 224 / 242, B=512 S=256
+      // 314 / 231).  G <= 4 keeps the single pass (32/8: 185 against 221 µs,
       // B=16384 S=24 357 / 388, 16/16 D=256 352 / 368; D=64 111 / 141).
-      if constexpr (OL != fmha_decode::kLayoutPaged || G < 8) return launch_onepass_dg<D, G, OL, false>(ao, stream);
+      if (OL != fmha_decode::kLayoutPaged || G < 8 || a.nblk <= (D == 64 ? 4 : D == 128 ? 6 : 8))
+        return launch_onepass_dg<D, G, OL, false>(ao, stream);
     }
   }
   if (onepass_only) return kOnepassNotTaken;

@@ -367,3 +367,24 @@ def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass ps={page_size} D={D} {Hq}/{Hkv} B={B}")
 
+
+
+@pytest.mark.parametrize("page_size", [1, 4])
+@pytest.mark.parametrize("D,max_len", [(64, 64), (128, 96), (256, 128)])
+def test_paged_single_pass_group_of_eight(page_size, D, max_len):
+    """Pages under 16 rows, eight query heads per KV head on the single pass
+    (one batch per wave, per-row page lookups), at the longest rows it takes
+    there for each head dim, with empty rows and 16-row edges."""
+    import fmha_amd
+    import torch
+    B, Hq, Hkv = 600, 64, 8
+    rng = np.random.default_rng(page_size * 13 + D + max_len)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:6] = [max_len, 0, 1, 15, 16, 17]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + D + max_len + 71)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    print(f"paged single pass G=8: ps={page_size} D={D} B={B} max={max_len}", flush=True)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass G=8 ps={page_size} D={D}")
