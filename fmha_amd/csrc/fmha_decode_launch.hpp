@@ -283,16 +283,19 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
   // The single pass spans 2^shift batches with one descriptor: for the
   // strided layout only when their span stays below 1 GiB.  On paged caches
-  // (LANES) its lane groups can look up their own batches' pages, which pays
-  // for rows of one or two 16-row blocks; longer rows, whose lookups the
-  // single pass's two sub-blocks in flight cannot hide, take the split
-  // passes at D = 64 and 128 and the one-batch single pass at D = 256
-  // (16-row pages, µs, per-lane single pass against the previous choice:
-  // B=16384 S=24 Hq/Hkv 8/1 D=128 73.7 against 142.4 split; B=2048 S=128
-  // 8/1 74.5 against 57.8 split, 16/2 83.1 / 87.6; D=64 8/1 49.8 / 47.1,
-  // 16/2 68.8 / 64.8; B=4096 S=64 4/1 D=256 66.0 against 57.1 one batch
-  // per wave).
-  const bool lanes_onepass = LANES && a.nblk <= 2;
+  // (LANES) its lane groups look up their own batches' pages.  With up to 4
+  // query heads per KV head and D <= 128 that pays for rows of up to eight
+  // 16-row blocks,
+  // where the split passes, with one or two chunks per row, leave most lane
+  // groups idle (µs, Hq/Hkv, split against single pass: 16-row pages
+  // B=16384 S=48 4/1 D=64 191 / 49, D=128 202 / 91, 1/1 195 / 88; B=8192
+  // S=96 4/1 D=64 145 / 56, 1/1 151 / 69; B=6144 S=128 4/1 D=128 155 / 78;
+  // one-row pages B=16384 S=48 4/1 D=64 147 / 79, B=8192 S=96 1/1 149 / 87).
+  // Groups of 8 and D = 256 keep it to one or two blocks (B=6144 S=128 8/1
+  // D=128: 16-row pages 101 split / 113, one-row pages 102 / 176); longer
+  // rows take the split passes at D = 64 and 128 and the one-batch single
+  // pass at D = 256 (B=4096 S=64 4/1: 57 against 66 per-lane).
+  const bool lanes_onepass = LANES && a.nblk <= (G <= 4 && D < 256 ? 8 : 2);
   if (!LANES || D == 256 || lanes_onepass) {
     SplitArgs ao = a;
     ao.sub_shift = LANES && !lanes_onepass ? 0 : shift;

@@ -388,3 +388,27 @@ def test_paged_single_pass_group_of_eight(page_size, D, max_len):
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass G=8 ps={page_size} D={D}")
+
+
+@pytest.mark.parametrize("page_size", [1, 4, 16, 32])
+@pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 4, 1, 2100), (64, 2, 1, 4200), (128, 8, 2, 1100), (64, 1, 1, 4200)])
+@pytest.mark.parametrize("max_len", [48, 128])
+def test_paged_single_pass_few_kv_heads_longer_rows(page_size, D, Hq, Hkv, B, max_len):
+    """Rows of three to eight 16-row blocks over paged caches with fewer KV
+    heads than a wave holds, up to 4 query heads per KV head, >= 512 waves:
+    the single pass with per-lane page lookups, several batches per wave,
+    empty rows, rows on and next to the 16-row edges."""
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(page_size * 17 + D + Hq + Hkv + B + max_len)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:7] = [max_len, 0, 1, 15, 16, 17, 33]
+    seqlens[-1] = max_len
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + D + Hq + B + max_len + 3)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    print(f"paged single pass longer rows: ps={page_size} D={D} {Hq}/{Hkv} B={B} max={max_len}", flush=True)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len,
+           f"paged single pass longer rows ps={page_size} D={D} {Hq}/{Hkv} B={B} max={max_len}")
