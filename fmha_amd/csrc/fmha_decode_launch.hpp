@@ -222,6 +222,12 @@ constexpr size_t kOnepassMaxLdsPerWave = 40 * 1024;
 // from 8 up).
 constexpr int kOnepassWavesPerCU = 8;
 constexpr int kOnepassWavesPerCUNarrow = 4;
+// Pages under 16 rows, one or two query heads per KV head: 12 (157 VGPRs
+// leave room), the per-row page lookups wanting more waves in flight (µs at
+// 4 or 8 / 12: B=5461 S=24 Hq/Hkv 8/8 158 / 108, B=2730 S=48 129 / 102,
+// B=16384 S=24 16/16 895 / 597, S=48 1391 / 1065; 16-row pages measured
+// 2-6% slower at 12 and keep the caps above).
+constexpr int kOnepassWavesPerCUPagedRows = 12;
 
 // Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
 // the KV-head groups of one.
@@ -235,15 +241,26 @@ bool onepass_fits(const SplitArgs& a) {
          fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
 }
 
-template <int D, int G, int LAYOUT, bool MULTI>
-hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
-  constexpr auto kernel = fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>;
-  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
-  const int waves = !MULTI && G <= 2 && a.nblk <= 3 ? kOnepassWavesPerCUNarrow : kOnepassWavesPerCU;
-  const size_t cap = lds_reserve_kernel<kernel>(waves);
-  hipLaunchKernelGGL(kernel, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
+template <auto KERNEL>
+hipError_t launch_onepass_kernel(const SplitArgs& a, size_t need, int waves, hipStream_t stream) {
+  const size_t cap = lds_reserve_kernel<KERNEL>(waves);
+  hipLaunchKernelGGL(KERNEL, dim3((uint32_t)onepass_waves(a)), dim3(kBlockThreads), need > cap ? need : cap, stream,
                      a);
   return hipGetLastError();
+}
+
+template <int D, int G, int LAYOUT, bool MULTI>
+hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
+  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
+  const int waves = LAYOUT == fmha_decode::kLayoutPaged && G <= 2 ? kOnepassWavesPerCUPagedRows
+                    : !MULTI && G <= 2 && a.nblk <= 3     ? kOnepassWavesPerCUNarrow
+                                                          : kOnepassWavesPerCU;
+  // 16-row pages, eight query heads per KV head, rows of up to four blocks:
+  // the kernel scheduled for two waves per SIMD.
+  if constexpr (!MULTI && G == 8 && LAYOUT == fmha_decode::kLayoutPagedBlock)
+    if (a.nblk <= 4)
+      return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI, 2>>(a, need, waves, stream);
+  return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>>(a, need, waves, stream);
 }
 
 

@@ -60,8 +60,17 @@ constexpr size_t onepass_lds_bytes(int sp) {
 // descriptor over the batches, paged caches through per-lane page lookups,
 // kLayoutPagedLanes / kLayoutPagedBlockLanes); otherwise one batch per wave
 // with its length read once for the whole wave.
-template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false>
-__global__ __launch_bounds__(kBlockThreads) void onepass_decode_kernel(SplitArgs a) {
+// WPE: waves per SIMD the compiler schedules for (amdgpu_waves_per_eu; 1
+// gives the same code as no hint).  2 for one batch per wave of eight query
+// heads per KV head on pages of 16 rows or more with rows of up to four
+// 16-row blocks, where the default schedule measured slower (same 250
+// VGPRs; µs, 1 / 2: B=16384 S=24 Hq/Hkv 64/8 432 / 349, B=5461 S=24 153 /
+// 127, B=2730 S=48 145 / 119; but B=1024 S=128 115 / 134).  Elsewhere 2
+// measured equal (one-row pages, packed) or made the compiler spill
+// (several batches per wave).
+template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1>
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
+    SplitArgs a) {
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
   constexpr int HPW = P::HPW;
