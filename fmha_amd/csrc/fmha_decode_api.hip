@@ -559,17 +559,19 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv
   // 268/251/314/387; B=16 S=8192 16/16: 206/193/195/255; matrix cores,
   // B=64 S=4096 64/4: 245/219/-/274).
   if (layout == fmha_decode::kLayoutPaged && c > 256) c = 256;
-  // Paged caches with fewer KV heads than a wave holds, on the VALU passes:
-  // a P.V wave's 2^shift lane groups take chunks of one row, so rows get at
-  // least 2^shift chunks where chunks of 64 rows or more allow it (µs,
-  // 16-row pages, chunks as before / now: B=2048 S=512 Hq/Hkv 4/1 192 / 121,
-  // B=1024 S=1024 140 / 115, B=2048 S=512 8/2 254 / 216, D=64 2/1 80 / 65;
-  // one-row pages B=2048 S=512 4/1 141 / 118, D=64 2/1 88 / 64).  On packed
-  // caches, which took the same plan, the results were mixed (-7% to +8%).
-  if (fmha_decode::is_paged_layout(layout) && !split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d)) {
+  // Fewer KV heads than a wave holds, on the VALU passes: a P.V wave's
+  // 2^shift lane groups take chunks of one row, so rows get at least 2^shift
+  // chunks where chunks of 64 rows or more allow it: on paged caches for any
+  // shift (µs, 16-row pages, chunks as before / now: B=2048 S=512 Hq/Hkv
+  // 4/1 192 / 121, B=1024 S=1024 140 / 115, B=2048 S=512 8/2 254 / 216, D=64
+  // 2/1 80 / 65; one-row pages B=2048 S=512 4/1 141 / 118, D=64 2/1 88 /
+  // 64), on packed and strided ones from four lane groups up (packed B=2048
+  // S=512 4/1 123 / 115, D=64 2/1 66 / 62; with two, 8/2, 195 / 210).
+  if (!split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d)) {
     int shift = 0;
     while ((hkv << (shift + 1)) <= heads_per_wave && heads_per_wave % (hkv << (shift + 1)) == 0) ++shift;
-    while (shift > 0 && c > 64 && ((int64_t)c << shift) > max_rows) c /= 2;
+    if (shift >= (fmha_decode::is_paged_layout(layout) ? 1 : 2))
+      while (c > 64 && ((int64_t)c << shift) > max_rows) c /= 2;
   }
   // FMHA_DECODE_SPLIT_CHUNK=<64|...|2048> overrides C (for sweeps; the
   // workspace size follows, and a launch checks its workspace against it).
