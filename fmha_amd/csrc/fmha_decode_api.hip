@@ -318,14 +318,23 @@ bool gqa_kernel_forced(const char* kind) {
   return e && std::strcmp(e, kind) == 0;
 }
 
-bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d) {
+// One-row-page caches with fewer KV heads than a wave holds (per-lane page
+// lookups) and rows of at most 48 (max_rows) also put launch groups of 4 on
+// the matrix cores at D >= 128, where the VALU single pass with several
+// batches per wave, each lane looking up its own row, ran slower (µs, one-row
+// pages, Hq/Hkv 4/1: B=21845 S=48 D=128 205 against 145, B=43690 S=24 235 /
+// 224, D=256 B=21845 S=24 231 / 158; at D=64 the matrix cores lose, B=87381
+// S=24 250 / 413, and so does G=1, 197 / 217).
+bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d, int max_rows) {
   if (gqa_kernel_forced("valu")) return false;
   if (gqa_kernel_forced("mfma")) return true;
   if (kv_groups > 1) return true;
-  if (g_launch < 8) return false;
-  if (layout != fmha_decode::kLayoutPaged) return true;
   const int hpw = kWaveSize / (d / 8);
-  return 2 * hkv <= hpw && hpw % (2 * hkv) == 0;
+  const bool lanes = 2 * hkv <= hpw && hpw % (2 * hkv) == 0;
+  if (g_launch < 8)
+    return g_launch >= 4 && layout == fmha_decode::kLayoutPaged && lanes && d >= 128 && max_rows <= 48;
+  if (layout != fmha_decode::kLayoutPaged) return true;
+  return lanes;
 }
 
 bool use_mfma_kernel(int g) {
@@ -542,7 +551,7 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv
   p.units = upb * batch;
   int64_t per_chunk = p.units;  // P.V waves per chunk of every batch
   int64_t target = split_target_waves(hq, hkv, d);
-  if (split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d)) {
+  if (split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d, max_rows)) {
     const int hkv_mem = hkv / kv_groups;
     const int g_mem = hq / hkv_mem;
     const int tw = d == 256 ? 1 : 2;
@@ -567,7 +576,7 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv
   // 2/1 80 / 65; one-row pages B=2048 S=512 4/1 141 / 118, D=64 2/1 88 /
   // 64), on packed and strided ones from four lane groups up (packed B=2048
   // S=512 4/1 123 / 115, D=64 2/1 66 / 62; with two, 8/2, 195 / 210).
-  if (!split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d)) {
+  if (!split_on_matrix_cores(hq / hkv, kv_groups, layout, hkv, d, max_rows)) {
     int shift = 0;
     while ((hkv << (shift + 1)) <= heads_per_wave && heads_per_wave % (hkv << (shift + 1)) == 0) ++shift;
     if (shift >= (fmha_decode::is_paged_layout(layout) ? 1 : 2))
@@ -907,7 +916,8 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
                      : launch_split_layout<fmha_decode::kLayoutPagedBlock>(a, head_dim, g, s, onepass_only);
     }
   };
-  if (split_on_matrix_cores(a.num_heads_q / a.num_heads_kv, a.kv_groups, layout, a.num_heads_kv, head_dim)) {
+  if (split_on_matrix_cores(a.num_heads_q / a.num_heads_kv, a.kv_groups, layout, a.num_heads_kv, head_dim,
+                            a.max_rows)) {
     // Groups of 5-8 on rows that the VALU single pass holds (enough waves,
     // a row's scores in LDS, every lane group busy) take it on rows of at
     // most 128 at D = 128 and 256 and any it holds at D = 64 (with several
@@ -920,7 +930,10 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
     // 87 vs 67, D=256 B=8192 S=64 135 vs 119).  Longer rows favour the
     // split: D=128 S=160 224 vs 237, D=256 S=256 222 vs 252, 8/1 S=48 124
     // vs 148.
-    if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma")) {
+    // (One-row pages with per-lane lookups at D >= 128: the split, 8/1
+    // B=43690 S=24 278 against 230 µs.)
+    if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma") &&
+        !(layout == fmha_decode::kLayoutPaged && lanes && head_dim >= 128)) {
       err = valu(true);
       if (err != kOnepassNotTaken) {
         if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
