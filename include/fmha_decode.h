@@ -241,7 +241,11 @@ int fmha_decode_fwd_paged(void* stream,
  * split-KV passes; G = 5-8 and G > 8 on split-KV passes on the matrix cores
  * (all query heads of a KV head per wave; K and V read once), except G = 5-8
  * on pages of fewer than 16 rows with at least half a wave of KV heads,
- * which takes the VALU passes.  The workspace size includes the copies (two
+ * which takes the VALU passes.  Many short rows (>= 512 waves, a row's
+ * scores within a wave's LDS) take a single-pass kernel instead, at G <= 8
+ * on the rows where it measured faster, and G = 3-4 on pages of fewer than
+ * 16 rows with few KV heads, rows of at most 48 and head_dim >= 128 the
+ * matrix-core passes.  The workspace size includes the copies (two
  * of [batch, Hkv * padded group, head_dim], ahead of the split-KV data) and
  * covers whichever passes the layout takes.  FMHA_DECODE_GQA_KERNEL=valu
  * keeps every G on the VALU kernels (G > 8 as ceil(G / 8) groups of 8 query
@@ -313,9 +317,10 @@ int fmha_decode_fwd_splitkv_strided(void* stream,
  * and pages it does not map are never read.  Workspace as for
  * fmha_decode_fwd_splitkv_strided (when that bound is <= 16 the call runs
  * fmha_decode_fwd_paged's kernel, and the workspace only holds a padded
- * query group).  Any group size: G <= 8 on the VALU passes (3 and 5-7 on
- * padded query groups), G > 8 on the matrix-core split passes; with that
- * bound <= 16, G > 8 also takes the split passes and needs the workspace.
+ * query group).  Any group size, on the passes fmha_decode_fwd_splitkv
+ * describes for each G and layout (3 and 5-7 on padded query groups); with
+ * that bound <= 16, G > 8 also takes the split passes and needs the
+ * workspace.
  * No counterpart in the reference.
  */
 int fmha_decode_fwd_splitkv_paged(void* stream,
