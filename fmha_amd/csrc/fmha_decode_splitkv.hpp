@@ -270,12 +270,17 @@ struct LongRows {
     static_assert(NR <= 16, "a sub-block fits a 16-row page");
     if constexpr (LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided) {
       // Rows past this lane's end are moved out of range (a strided range
-      // can also cover other heads' padding rows).
+      // can also cover other heads' padding rows).  Offsets from one
+      // per-lane base plus a wave-uniform step: a per-row multiply of a
+      // per-lane row kept 16-32 offsets live (several batches per wave,
+      // G = 4: 256 VGPRs and 19 AGPRs against 215; the VALU P.V pass at
+      // G = 1: 257 against 169).
+      const int rowb = rel0 + lane_rows;
+      const uint32_t off0 = lane_off + (uint32_t)rowb * row_bytes;
+      const int lim = lane_n - rowb;
 #pragma unroll
-      for (int j = 0; j < NR; ++j) {
-        const int row = rel0 + j + lane_rows;
-        out[j] = buffer_load16_nt(rsrc, lane_off + (row < lane_n ? (uint32_t)row * row_bytes : kRowOutOfRange));
-      }
+      for (int j = 0; j < NR; ++j)
+        out[j] = buffer_load16_nt(rsrc, j < lim ? off0 + (uint32_t)j * row_bytes : kRowOutOfRange);
     } else if constexpr (LAYOUT == kLayoutPagedBlock) {
       const int valid = n - rel0 < 0 ? 0 : (n - rel0 > NR ? NR : n - rel0);
       const __amdgpu_buffer_rsrc_t pr = page_rsrc(lo + (valid > 0 ? rel0 : 0), valid);
