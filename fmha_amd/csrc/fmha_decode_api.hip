@@ -921,7 +921,7 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
     // Groups of 5-8 on rows that the VALU single pass holds (enough waves,
     // a row's scores in LDS, every lane group busy) take it on rows of at
     // most 128 at D = 128 and 256 and any it holds at D = 64 (with several
-    // batches per wave: 32 at D = 128, 64 at D = 64, 128 at D = 256): one
+    // batches per wave: 96 at D = 128, 64 at D = 64, 128 at D = 256): one
     // launch against four (µs, packed,
     // D = 128 unless given, matrix-core split vs single pass: B=16384 S=24
     // Hq/Hkv 64/8 486 vs 332, B=4096 S=64 64/8 230 vs 204, B=2048 S=128

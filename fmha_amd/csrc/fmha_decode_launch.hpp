@@ -323,14 +323,13 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
     // onepass_only: waves with no idle lane groups, on rows up to where the
-    // single pass measured faster than the matrix-core split.
-    // Strided caches with several batches per wave measured slower on it
-    // except at D = 64 on rows of one or two blocks (BHSD, µs, single pass
-    // against split: B=43690 S=24 8/1 D=128 206 / 162, D=256 B=21845 211 /
-    // 185; D=64 B=87381 S=24 211 / 295, B=43690 S=48 184 / 176).
-    const int only_nblk =
-        shift > 0 ? (LAYOUT == fmha_decode::kLayoutStrided ? (D == 64 ? 2 : 0) : D == 64 ? 4 : D == 128 ? 2 : 8)
-                  : (D == 64 ? a.nblk : 8);
+    // single pass measured faster than the matrix-core split: four 16-row
+    // blocks at D = 64, six at D = 128 (with several batches per wave) and
+    // eight otherwise (µs, Hq/Hkv 8/1, single pass against split: packed
+    // D=128 B=16384 S=64 105 / 121, B=10922 S=96 110 / 123, B=8192 S=128 140
+    // / 117; D=64 B=21845 S=96 150 / 138; BHSD D=256 B=21845 S=24 137 / 184,
+    // D=128 B=43690 S=24 142 / 161, D=64 B=43690 S=48 150 / 176).
+    const int only_nblk = shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : 8);
     if (onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);

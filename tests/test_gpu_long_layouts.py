@@ -209,10 +209,12 @@ def test_strided_long_sub_units(D, Hq, Hkv):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"bhsd sub-units D={D} Hq={Hq} Hkv={Hkv}")
 
 
-@pytest.mark.parametrize("D,Hq,Hkv,B,cap", [(64, 8, 1, 4100, 32), (128, 4, 1, 2049, 80), (64, 8, 2, 2100, 80)])
+@pytest.mark.parametrize("D,Hq,Hkv,B,cap", [(64, 8, 1, 4100, 64), (128, 8, 1, 2049, 96), (128, 4, 1, 2049, 80),
+                                             (64, 8, 2, 2100, 80)])
 def test_strided_single_pass_batches_per_wave(D, Hq, Hkv, B, cap):
     """Single pass, several batches per wave through one strided descriptor,
-    BHSD with NaN padding (G = 8 takes it at D = 64 on rows of up to 32)."""
+    BHSD with NaN padding (G = 8 takes it on rows of up to 64 at D = 64 and
+    96 at D = 128)."""
     import fmha_amd
     import torch
     rng = np.random.default_rng(D + B)

@@ -127,7 +127,7 @@ def test_bad_and_empty_lengths():
 # when batch * ceil(Hkv / (64 / (D/8))) >= 512 and the wave's scores and
 # weights (HPW * G * (6 rows + 8) bytes, rows rounded up to 32) fit 40 KiB of LDS;
 # at G = 8 (packed layout) only on rows of at most 128 at D = 128 and 256
-# and, with several batches per wave, 32 at D = 128 and 64 at D = 64 (else
+# and, with several batches per wave, 96 at D = 128 and 64 at D = 64 (else
 # the matrix-core split).
 def _onepass_taken(B, Hq, Hkv, D, max_len):
     """Waves = batch groups (2^shift batches each when Hkv is below the
@@ -136,7 +136,7 @@ def _onepass_taken(B, Hq, Hkv, D, max_len):
     r = _sub_units(Hkv, D)
     waves = (B + r - 1) // r * ((Hkv + hpw // r - 1) // (hpw // r))
     sp = (max_len + 31) // 32 * 32
-    limit = {64: 64, 128: 32, 256: 128}[D] if r > 1 else (128 if D > 64 else max_len)
+    limit = {64: 64, 128: 96, 256: 128}[D] if r > 1 else (128 if D > 64 else max_len)
     if Hq // Hkv == 8 and max_len > limit:
         return False
     return waves >= 512 and hpw * (Hq // Hkv) * (6 * sp + 8) <= 40 * 1024
@@ -161,7 +161,7 @@ def test_onepass_all_shapes(D, B, G):
 
 
 @pytest.mark.parametrize("D,Hkv,B,max_len", [(64, 16, 1024, 96), (64, 1, 4100, 64), (128, 8, 1100, 128),
-                                             (128, 2, 2050, 32), (256, 8, 600, 128), (256, 1, 1030, 128)])
+                                             (128, 2, 2050, 96), (256, 8, 600, 128), (256, 1, 1030, 128)])
 def test_onepass_group_of_eight(D, Hkv, B, max_len):
     """G = 8 on the single pass at the longest rows it takes there for each
     head dim (one batch per wave, and several: Hkv = 1, 2), with the 16-row
