@@ -371,12 +371,14 @@ def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
 
 
 
-@pytest.mark.parametrize("page_size", [1, 4])
-@pytest.mark.parametrize("D,max_len", [(64, 64), (128, 96), (256, 128)])
+@pytest.mark.parametrize("page_size", [1, 4, 16])
+@pytest.mark.parametrize("D,max_len", [(64, 64), (128, 96), (256, 128), (128, 48)])
 def test_paged_single_pass_group_of_eight(page_size, D, max_len):
-    """Pages under 16 rows, eight query heads per KV head on the single pass
-    (one batch per wave, per-row page lookups), at the longest rows it takes
-    there for each head dim, with empty rows and 16-row edges."""
+    """Eight query heads per KV head on the single pass (one batch per wave)
+    over paged caches: pages under 16 rows (per-row page lookups) at the
+    longest rows it takes there for each head dim, 16-row pages with rows of
+    up to four blocks (the kernel scheduled for two waves per SIMD) and
+    longer; empty rows and 16-row edges."""
     import fmha_amd
     import torch
     B, Hq, Hkv = 600, 64, 8
