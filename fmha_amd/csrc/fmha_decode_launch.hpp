@@ -309,10 +309,15 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
   // S=96 4/1 D=64 145 / 56, 1/1 151 / 69; B=6144 S=128 4/1 D=128 155 / 78;
   // one-row pages B=16384 S=48 4/1 D=64 147 / 79, B=8192 S=96 1/1 149 / 87).
   // Groups of 8 and D = 256 keep it to one or two blocks (B=6144 S=128 8/1
-  // D=128: 16-row pages 101 split / 113, one-row pages 102 / 176); longer
+  // D=128: 16-row pages 101 split / 113, one-row pages 102 / 176; B=21845
+  // S=48 D=128 145 / 154), except groups of 8 at D = 64 on 16-row pages, up
+  // to four blocks (B=43690 S=48 8/1 215 / 180, B=32768 S=64 184 / 169); longer
   // rows take the split passes at D = 64 and 128 and the one-batch single
   // pass at D = 256 (B=4096 S=64 4/1: 57 against 66 per-lane).
-  const bool lanes_onepass = LANES && a.nblk <= (G <= 4 && D < 256 ? 8 : 2);
+  const bool lanes_onepass =
+      LANES && a.nblk <= (G <= 4 && D < 256                                          ? 8
+                          : LAYOUT == fmha_decode::kLayoutPagedBlockLanes && D == 64 ? 4
+                                                                                     : 2);
   if (!LANES || D == 256 || lanes_onepass) {
     SplitArgs ao = a;
     ao.sub_shift = LANES && !lanes_onepass ? 0 : shift;

@@ -349,12 +349,13 @@ def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
 @pytest.mark.parametrize("page_size", [1, 4, 16, 32])
 @pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2100), (128, 16, 2, 1100), (256, 4, 1, 1100), (64, 8, 1, 4200),
                                         (128, 40, 8, 700)])
-@pytest.mark.parametrize("max_len", [17, 32])
+@pytest.mark.parametrize("max_len", [17, 32, 64])
 def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
-    """Rows of one or two 16-row blocks over paged caches with fewer KV heads
-    than a wave holds and >= 512 waves: the single pass with each lane group
-    looking up its own batch's pages (several batches per wave); the last
-    shape fills a wave and runs one batch per wave."""
+    """Rows of one to four 16-row blocks over paged caches with fewer KV
+    heads than a wave holds and >= 512 waves: the single pass with each lane
+    group looking up its own batch's pages (several batches per wave) where
+    the library takes it, the split passes elsewhere; the last shape fills a
+    wave and runs one batch per wave."""
     import fmha_amd
     import torch
     rng = np.random.default_rng(page_size * 11 + D + Hq + Hkv + B + max_len)
