@@ -5,6 +5,7 @@ the C ABI is include/fmha_decode.h; this package is its host-side interface.
 """
 from .decode import (MAX_SEQLEN_KV, NOALLOC_SCRATCH_BYTES, FmhaDecodeError, fmha_decode, fmha_decode_paged,
                      fmha_decode_splitkv, fmha_decode_strided, launch_fmha_decode, launch_fmha_decode_exact,
+                     launch_fmha_decode_fast, launch_fmha_decode_uniform_fast,
                      launch_fmha_decode_fp32_weights, launch_fmha_decode_paged,
                      launch_fmha_decode_splitkv, launch_fmha_decode_splitkv_paged, launch_fmha_decode_splitkv_strided,
                      launch_fmha_decode_strided, launch_fmha_decode_uniform, splitkv_workspace_size)
@@ -27,6 +28,8 @@ __all__ = [
     "launch_fmha_decode",
     "launch_fmha_decode_fp32_weights",
     "launch_fmha_decode_exact",
+    "launch_fmha_decode_fast",
+    "launch_fmha_decode_uniform_fast",
     "launch_fmha_decode_uniform",
     "LIB_PATH",
     "EXPORTED",

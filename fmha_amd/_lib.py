@@ -15,9 +15,11 @@ LIB_PATH = os.environ.get("FMHA_DECODE_LIB") or os.path.join(_HERE, "libfmha_dec
 # Every symbol include/fmha_decode.h declares.
 EXPORTED = (
     "fmha_decode_fwd",
+    "fmha_decode_fwd_fast",
     "fmha_decode_fwd_fp32_weights",
     "fmha_decode_fwd_exact",
     "fmha_decode_fwd_uniform",
+    "fmha_decode_fwd_uniform_fast",
     "fmha_decode_fwd_strided",
     "fmha_decode_fwd_paged",
     "fmha_decode_splitkv_workspace_size",
@@ -45,12 +47,16 @@ def load():
     vp, i32, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
     lib.fmha_decode_fwd.restype = ctypes.c_int
     lib.fmha_decode_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_fwd_fast.restype = ctypes.c_int
+    lib.fmha_decode_fwd_fast.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_fp32_weights.restype = ctypes.c_int
     lib.fmha_decode_fwd_fp32_weights.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_exact.restype = ctypes.c_int
     lib.fmha_decode_fwd_exact.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32]
     lib.fmha_decode_fwd_uniform.restype = ctypes.c_int
     lib.fmha_decode_fwd_uniform.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
+    lib.fmha_decode_fwd_uniform_fast.restype = ctypes.c_int
+    lib.fmha_decode_fwd_uniform_fast.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32]
     i64 = ctypes.c_int64
     lib.fmha_decode_fwd_strided.restype = ctypes.c_int
     lib.fmha_decode_fwd_strided.argtypes = [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, i32, i32,

@@ -147,6 +147,30 @@ int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths,
   return w < floor_w ? floor_w : (int)w;
 }
 
+// Waves per CU for the exact-arithmetic kernels (rows16 and g_real as for
+// waves_per_cu_for).  Their waves compute longer than the tree-order ones
+// (sequential score sums staged through LDS), so fewer of their waves have
+// requests in flight at a time and the CU needs more of them: 144 KiB of
+// unit bytes per CU with known lengths, 200 KiB with lengths on the device
+// (whose waves also wait for the lengths first); at least 4 waves, 6 for
+// groups of 4 or more, no cap from 16.  Sweep at B=30720 (us, best cap /
+// this model's / the tree-order kernel): known lengths Hq/Hkv 16/16 S=16
+// D=128 613.7 (4) / 613.7 (4) / 610.2, 32/16 S=16 665.0 (4) / 665.0 (4) /
+// 645.6, 32/32 S=16 D=256 2466.9 (4) / 2466.9 (4) / 2481.2, 16/16 S=5
+// D=256 440.0 (16) / 442.1 (12) / 416.9; device lengths 16/16 S=16 616.9
+// (4) / 626.1 (6; 5 here) / 614.6, 32/16 S=16 650.7 (6) / 650.7 (6) /
+// 645.7, 32/32 S=16 D=256 2504.1 (6) / 2504.1 (6) / 2505.3, the
+// reference's Poisson(4) lengths 16/16 D=128 191.8 (16) / 191.8 (16) /
+// 196.2, 32/32 D=256 837.8 (16) / 837.8 (16) / 823.3.
+int waves_per_cu_exact(int rows16, int g, int g_real, bool device_lengths) {
+  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
+  const int64_t budget = (device_lengths ? 200LL : 144LL) * 1024;
+  const int64_t w = 16 * budget / unit_bytes16;
+  if (w >= 16) return kMaxWavesPerCU;
+  const int floor_w = g >= 4 ? 6 : 4;
+  return w < floor_w ? floor_w : (int)w;
+}
+
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
 int bucket_for(int s) {
   int b = 1;
@@ -189,8 +213,9 @@ int check_common(const void* Q, const void* K, const void* V, void* O, int32_t b
 // Fills the layout-independent fields, picks the wave cap and launches.
 // rows16: 16 x the KV rows per batch used to size the per-CU wave cap (the
 // uniform length, or an estimate when lengths live on the device, which
-// device_lengths says); numerics selects the fp32-weight or the
-// exact-arithmetic kernels (packed layout only; exact: G = 1).
+// device_lengths says); numerics selects the tree-order bf16-weight kernels
+// (kBf16Weights), the fp32-weight ones or the exact-arithmetic ones (packed
+// layout only, G <= 8).
 enum class Numerics { kBf16Weights, kFp32Weights, kExact };
 
 int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, int sb, int rows16,
@@ -211,8 +236,8 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
                   a.group);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
-  if (exact && (layout != fmha_decode::kLayoutPacked || g != 1))
-    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "the exact kernels read the packed layout with G = 1");
+  if (exact && layout != fmha_decode::kLayoutPacked)
+    return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "the exact kernels read the packed layout");
   // Fewer KV heads than a wave holds: R batches per wave, every lane busy
   // (paged: per-lane page lookups and addresses).  Strided only when R
   // batches' spans fit one descriptor.
@@ -224,7 +249,8 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
                           (int64_t)(a.num_heads_kv - 1) * a.head_stride + dq) * 2;
     multi = span < (int64_t(1) << 30);
   }
-  int w = waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
+  int w = exact ? waves_per_cu_exact(rows16, g, a.group, device_lengths)
+               : waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
   // Waves that serve several batches (each lane group its own length and
   // rows) want at least 8 per CU at D <= 128 (B=30720 with lengths on the
   // device, µs at the byte model's cap / 8 waves: Hq/Hkv 8/1 S=16 79.0 /
@@ -245,11 +271,19 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
       a.units_per_batch = batch;
       a.total_units = (uint32_t)(((int64_t)batch + (1 << shift) - 1) >> shift);
     }
+#define FMHA_DECODE_EXACT_G(DD)                                    \
+  switch (g) {                                                     \
+    case 1: err = launch_exact<DD, 1>(a, multi, sb, w, s); break;  \
+    case 2: err = launch_exact<DD, 2>(a, multi, sb, w, s); break;  \
+    case 4: err = launch_exact<DD, 4>(a, multi, sb, w, s); break;  \
+    default: err = launch_exact<DD, 8>(a, multi, sb, w, s); break; \
+  }
     switch (dq) {
-      case 64: err = launch_exact<64>(a, multi, sb, w, s); break;
-      case 128: err = launch_exact<128>(a, multi, sb, w, s); break;
-      default: err = launch_exact<256>(a, multi, sb, w, s); break;
+      case 64: FMHA_DECODE_EXACT_G(64) break;
+      case 128: FMHA_DECODE_EXACT_G(128) break;
+      default: FMHA_DECODE_EXACT_G(256) break;
     }
+#undef FMHA_DECODE_EXACT_G
     if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
     return FMHA_DECODE_SUCCESS;
   }
@@ -611,60 +645,35 @@ SplitPlan plan_split(int64_t batch, int hq, int hkv, int max_rows, int d, int kv
 
 }  // namespace
 
-extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
-                               const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
-                               int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
-                               float softmax_scale) {
-  g_detail[0] = '\0';
-  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
-  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
-  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
-  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
-    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
-  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
-  a.lens = cu_seqlens_kv;
-  a.row_stride = num_heads_kv * head_dim_q;
-  a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv))
-    return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
-  a.rows_feedback = feedback_word(stream);
-  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
-                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true);
-}
+namespace {
 
-extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const void* K, const void* V, void* O,
-                                            const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
-                                            int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
-                                            int32_t head_dim_kv, float softmax_scale) {
-  g_detail[0] = '\0';
-  int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
-                        softmax_scale, false);
-  if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
-  if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
-  if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
-    return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
-  DecodeArgs a = base_args(Q, K, V, O, num_heads_q, num_heads_kv, softmax_scale);
-  a.lens = cu_seqlens_kv;
-  a.row_stride = num_heads_kv * head_dim_q;
-  a.head_stride = head_dim_q;
-  a.rows_feedback = feedback_word(stream);
-  return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
-                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, Numerics::kFp32Weights);
-}
+// Numerics of the default entry points (fmha_decode_fwd, _uniform, and
+// fmha_decode_fwd_splitkv up to 16 rows) for G query heads per KV head: the
+// reference loop's arithmetic up to 2, the group sizes of the reference's
+// own configurations and of BASELINE, where it costs at most 1% at B=30720
+// but for short rows at D = 256 (S=5: 440 against 417 us; the measurements
+// at waves_per_cu_exact); the tree-order kernels above, where the exact
+// ones measured 2-45% slower (Hq/Hkv 64/16 S=16 +4.5% with known lengths,
+// 64/16 Poisson(4) +20%, 80/16 and 128/16 S=16 +14-16%, 8/1 S=16 +16%,
+// D=64 40/8 +45%).
+Numerics default_numerics(int g) { return g <= 2 ? Numerics::kExact : Numerics::kBf16Weights; }
 
-extern "C" int fmha_decode_fwd_exact(void* stream, const void* Q, const void* K, const void* V, void* O,
-                                     const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
-                                     int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
-                                     float softmax_scale) {
+// The packed cu_seqlens entry points.  kExact: the reference loop's
+// arithmetic for G <= 8; G > 8 has no exact kernel and is rejected
+// (fmha_decode_fwd_exact).  kBf16Weights: the tree-order kernels, the VALU
+// kernel for G <= 8 and the matrix-core kernel above (or for every G under
+// FMHA_DECODE_GQA_KERNEL=mfma).
+int fwd_cu(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu_seqlens_kv,
+           int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+           int32_t head_dim_kv, float softmax_scale, Numerics numerics, bool exact_only) {
   g_detail[0] = '\0';
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
-  if (num_heads_q != num_heads_kv)
+  const int g = num_heads_q / num_heads_kv;
+  if (exact_only && valu_kernel_group(g) == 0)
     return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
-                  "the exact path computes one query head per KV head (num_heads_q == num_heads_kv; got %d and %d)",
-                  num_heads_q, num_heads_kv);
+                  "the exact path takes at most 8 query heads per KV head (got %d)", g);
   if (!cu_seqlens_kv) return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be non-null");
   if ((reinterpret_cast<uintptr_t>(cu_seqlens_kv) & 3u) != 0)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "cu_seqlens_kv must be 4-byte aligned");
@@ -672,15 +681,17 @@ extern "C" int fmha_decode_fwd_exact(void* stream, const void* Q, const void* K,
   a.lens = cu_seqlens_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
+  const bool mfma = numerics == Numerics::kBf16Weights && use_mfma_kernel(g);
+  if (mfma) return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, kVarlenRowsHint);
   a.rows_feedback = feedback_word(stream);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, 0,
-                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, Numerics::kExact);
+                feedback_rows16(a.rows_feedback, FMHA_DECODE_MAX_SEQLEN_KV), true, numerics);
 }
 
-extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,
-                                       int32_t seqlen_kv, int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
-                                       int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
-                                       float softmax_scale) {
+// The uniform entry points, numerics as fwd_cu.
+int fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O, int32_t seqlen_kv,
+                int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                int32_t head_dim_kv, float softmax_scale, Numerics numerics) {
   g_detail[0] = '\0';
   if (seqlen_kv < 0 || seqlen_kv > FMHA_DECODE_MAX_SEQLEN_KV)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_kv must lie in [0, %d] (got %d)",
@@ -692,10 +703,63 @@ extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* 
   a.seqlen_uniform = seqlen_kv;
   a.row_stride = num_heads_kv * head_dim_q;
   a.head_stride = head_dim_q;
-  if (use_mfma_kernel(num_heads_q / num_heads_kv))
+  const int g = num_heads_q / num_heads_kv;
+  if (numerics != Numerics::kExact && use_mfma_kernel(g))
     return launch_mfma(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, seqlen_kv);
   return launch(stream, fmha_decode::kLayoutPacked, a, batch, head_dim_q, bucket_for(seqlen_kv), 16 * seqlen_kv,
-                false);
+                false, numerics);
+}
+
+}  // namespace
+
+extern "C" int fmha_decode_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
+                               const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                               int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                               float softmax_scale) {
+  const int g = num_heads_kv > 0 ? num_heads_q / num_heads_kv : 0;
+  return fwd_cu(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                head_dim_kv, softmax_scale, default_numerics(g), false);
+}
+
+extern "C" int fmha_decode_fwd_fast(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                    const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                                    int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                    float softmax_scale) {
+  return fwd_cu(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                head_dim_kv, softmax_scale, Numerics::kBf16Weights, false);
+}
+
+extern "C" int fmha_decode_fwd_fp32_weights(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                            const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                                            int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                                            int32_t head_dim_kv, float softmax_scale) {
+  return fwd_cu(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                head_dim_kv, softmax_scale, Numerics::kFp32Weights, false);
+}
+
+extern "C" int fmha_decode_fwd_exact(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                     const int32_t* cu_seqlens_kv, int32_t batch, int32_t num_heads_q,
+                                     int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                     float softmax_scale) {
+  return fwd_cu(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                head_dim_kv, softmax_scale, Numerics::kExact, true);
+}
+
+extern "C" int fmha_decode_fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                       int32_t seqlen_kv, int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                       int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                       float softmax_scale) {
+  const int g = num_heads_kv > 0 ? num_heads_q / num_heads_kv : 0;
+  return fwd_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                     head_dim_kv, softmax_scale, default_numerics(g));
+}
+
+extern "C" int fmha_decode_fwd_uniform_fast(void* stream, const void* Q, const void* K, const void* V, void* O,
+                                            int32_t seqlen_kv, int32_t batch, int32_t num_heads_q,
+                                            int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
+                                            int32_t head_dim_kv, float softmax_scale) {
+  return fwd_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q,
+                     head_dim_kv, softmax_scale, Numerics::kBf16Weights);
 }
 
 extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* K, const void* V, void* O,
@@ -1044,7 +1108,8 @@ int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, vo
     d.row_stride = num_heads_kv * head_dim_q;
     d.head_stride = head_dim_q;
     d.max_rows = max_seqlen_kv;
-    if (use_mfma_kernel(num_heads_q / num_heads_kv))
+    const Numerics numerics = default_numerics(num_heads_q / num_heads_kv);
+    if (numerics != Numerics::kExact && use_mfma_kernel(num_heads_q / num_heads_kv))
       return launch_mfma(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, rows_hint);
     SplitArgs unused;
     rc = split_prepare(fmha_decode::kLayoutPacked, Q, K, V, O, max_seqlen_kv, batch, num_heads_q, num_heads_kv, 1,
@@ -1052,7 +1117,7 @@ int splitkv_packed(void* stream, const void* Q, const void* K, const void* V, vo
     if (rc != FMHA_DECODE_SUCCESS) return rc;
     d.rows_feedback = feedback_word(stream, may_allocate);
     return launch(stream, fmha_decode::kLayoutPacked, d, batch, head_dim_q, 0,
-                  feedback_rows16(d.rows_feedback, max_seqlen_kv), true);
+                  feedback_rows16(d.rows_feedback, max_seqlen_kv), true, numerics);
   }
   return with_group_padding(
       stream, Q, O, batch, num_heads_q, num_heads_kv, head_dim_q, workspace, workspace_bytes,

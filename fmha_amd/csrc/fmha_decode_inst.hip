@@ -6,7 +6,7 @@
 // padding); every other part instantiates launchers, and with them kernels,
 // that no other part does.
 //
-// FMHA_DECODE_PARTS 54
+// FMHA_DECODE_PARTS 63
 #ifndef FMHA_DECODE_PART
 #error "compile with -DFMHA_DECODE_PART=<part>"
 #endif
@@ -182,11 +182,29 @@ template hipError_t launch_split_group_d<256, kLayoutPaged>(const SplitArgs&, hi
 #elif FMHA_DECODE_PART == 50
 template hipError_t launch_split_group_d<256, kLayoutPagedBlock>(const SplitArgs&, hipStream_t);
 #elif FMHA_DECODE_PART == 51
-template hipError_t launch_exact<64>(const DecodeArgs&, bool, int, int, hipStream_t);
+template hipError_t launch_exact<64, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
 #elif FMHA_DECODE_PART == 52
-template hipError_t launch_exact<128>(const DecodeArgs&, bool, int, int, hipStream_t);
+template hipError_t launch_exact<64, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
 #elif FMHA_DECODE_PART == 53
-template hipError_t launch_exact<256>(const DecodeArgs&, bool, int, int, hipStream_t);
+template hipError_t launch_exact<64, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 54
+template hipError_t launch_exact<64, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 55
+template hipError_t launch_exact<128, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 56
+template hipError_t launch_exact<128, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 57
+template hipError_t launch_exact<128, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 58
+template hipError_t launch_exact<128, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 59
+template hipError_t launch_exact<256, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 60
+template hipError_t launch_exact<256, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 61
+template hipError_t launch_exact<256, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+#elif FMHA_DECODE_PART == 62
+template hipError_t launch_exact<256, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
 #else
 #error "FMHA_DECODE_PART out of range"
 #endif

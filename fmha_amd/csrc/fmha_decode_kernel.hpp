@@ -544,45 +544,141 @@ __device__ __forceinline__ void decode_core(const u32x4 (&qv)[G], const u32x4 (&
 // is not: it differed from the loop on a few outputs per million at logit
 // spreads of 2-4.)
 //
-// Data movement: the K rows a wave loaded as 16-byte chunks per lane go
-// through LDS so that one lane holds a whole row, [head][row][dims] with a
-// 16-byte pad per row (NSTAGE = 2 stages of D / 2 dims halve that LDS: K row
-// j is then loaded as the chunk exact_k_chunk(r, j), so that every lane
-// writes half its rows in each stage and holds only the other half while
-// the first stage's dims are summed); the query vectors go to LDS as
-// float32, one word per dim.  Lanes take the (head, query head, row) scores
-// in turn, SMAX consecutive lanes per head and query head, so the masked
-// max is an exchange within those lanes and the sum of exponentials a
-// sequential read of SMAX values from LDS.  P.V: one fma per output element
-// and row, rows in order.
+// Data movement.  A score is a chain of D dependent additions, so the wave's
+// G * SMAX scores per KV head are spread over the lanes as register blocks:
+// a lane accumulates GB query heads x JB rows of one head (GB * JB = the
+// wave's scores / 64 when there are more than 64), each chain in dim order,
+// so every K value it reads and widens serves GB chains and every Q value
+// JB.  The operands reach the lanes through LDS as loaded (bf16), or
+// widened to float32 by all lanes while they are staged when a wave has at
+// most 16 scores (then most lanes have no chain, and the chains do no
+// widening; with more scores float32 staging measured slower, its LDS
+// traffic doubled: 697 against 617 us at B=30720 H=16 S=16 D=128), NSTAGE
+// stages of D / NSTAGE dims each, which keeps the staging small enough for
+// the waves per CU the stream needs:
+//   * K: lane r of a head owns 16-byte chunk r of each row as loaded, so for
+//     the staging its register slot j is loaded with row
+//     NSTAGE * (j / NSTAGE) + (j + r / CH) % NSTAGE, chunk
+//     CH * (j % NSTAGE) + r % CH (CH = chunks per stage): slot j belongs to
+//     stage j % NSTAGE in every lane, every lane writes SMAX / NSTAGE rows in
+//     each stage, and the slots of a stage are dead once it is written;
+//   * Q: lane r writes its chunk of each query head in stage r / CH;
+//   * LDS rows are padded by 16 bytes and heads by the closed form below, so
+//     the block reads of each 16-lane group fall in distinct bank groups.
+// Softmax: SMAX consecutive lanes per (head, query head) take the max by a
+// lane exchange and the sum of exponentials as a sequential read of SMAX
+// values from LDS.  P.V: one fma per output element and row, rows in order.
 // ---------------------------------------------------------------------------
-
-// 16-byte chunk of K row j that lane r of a head loads for the exact path's
-// NSTAGE-stage staging: r itself for one stage; for two, r or its partner in
-// the other half of the row, alternating with j.
-template <int D, int NSTAGE>
-__device__ __forceinline__ int exact_k_chunk(int r, int j) {
-  static_assert(NSTAGE == 1 || NSTAGE == 2, "one or two stages");
-  return NSTAGE == 1 ? r : (r + (D / 16) * (j & 1)) % (D / 8);
-}
 
 template <int D, int G, int SMAX, int NSTAGE>
 struct ExactLayout {
   static constexpr int LPH = D / 8;
   static constexpr int HPW = kWaveSize / LPH;
-  static constexpr int CH = LPH / NSTAGE;       // 16-byte chunks per row and stage
-  static constexpr int KRS = CH * 16 + 16;      // LDS bytes per staged K row
-  static constexpr int QRS = D * 4 + 16;        // LDS bytes per query vector (a word per dim)
-  static constexpr int K_BYTES = HPW * SMAX * KRS;
-  static constexpr int Q_BYTES = HPW * G * QRS;
-  static constexpr int E_BYTES = HPW * G * SMAX * 4;
+  static constexpr int CH = LPH / NSTAGE;       // 16-byte bf16 chunks per row and stage
+  static constexpr int N = HPW * G * SMAX;      // scores of the wave
+  // At most a quarter wave of scores: the operands are staged widened to
+  // float32 (WIDE), by every lane, so that the few lanes with a chain do no
+  // widening in it; else as loaded (bf16), widened in the chains.  (Half a
+  // wave, widened, measured no faster and took 202 VGPRs against 151 at
+  // D = 256 with 16 rows.)
+  static constexpr bool WIDE = N <= kWaveSize / 4;
+  static constexpr int RB = CH * (WIDE ? 32 : 16) + 16;  // LDS bytes per staged row (K row or query)
+  static constexpr int BL = N > kWaveSize ? N / kWaveSize : 1;  // scores per lane
+  static constexpr int gb_for() {
+    int gb = 1;
+    while (gb * 2 <= G && gb * 2 * gb * 2 <= BL) gb *= 2;
+    return BL / gb > SMAX ? BL / SMAX : gb;
+  }
+  static constexpr int GB = gb_for();           // query heads per block
+  static constexpr int JB = BL / GB;            // rows per block
+  static constexpr int GBN = G / GB;            // blocks across the query heads
+  static constexpr int JBN = SMAX / JB;         // blocks across the rows
+  static constexpr int NB = N / BL;             // blocks (<= 64, one per lane)
+  // Head stride of the K rows in 16-byte units = JBN mod 16: the JBN rows of
+  // consecutive heads that one 16-lane read touches start in distinct bank
+  // groups (the row stride, RB / 16 units, is odd).
+  static constexpr int KH = SMAX * RB + 16 * ((JBN - SMAX * (RB / 16) % 16 + 16) % 16);
+  static constexpr int QH = G * RB;
+  static constexpr int K_BYTES = HPW * KH;
+  static constexpr int Q_BYTES = HPW * QH;
+  static constexpr int E_BYTES = N * 4;
   static constexpr int BYTES = K_BYTES + Q_BYTES + E_BYTES;
+  static_assert(LPH % NSTAGE == 0 && (SMAX % NSTAGE == 0 || SMAX == 1) && CH % 2 == 0,
+                "stages must split the chunks and rows, an even number of chunks each");
+  static_assert(GB * JB == BL && G % GB == 0 && SMAX % JB == 0 && NB <= kWaveSize, "score blocks");
 };
 
+// Staging budget per wave: the fewest stages (1, 2 or 4; at most the
+// bucket's rows, an even number of chunks each) whose LDS stays within it.
+// 12 KiB for one or two query heads per KV head, which leaves room for the
+// 12-16 waves per CU that short and varying rows want (B=30720 with the
+// reference's Poisson lengths: 198 / 194 us at 12 / 16 waves against 232 at
+// 8), 24 KiB for wider groups, whose caps are 4-6 waves.
+template <int D, int G, int SMAX>
+__device__ __forceinline__ constexpr int exact_stages() {
+  constexpr int budget = G <= 2 ? 12 * 1024 : 24 * 1024;
+  constexpr int lph = D / 8;
+  if constexpr (SMAX <= 1) {
+    return 1;
+  } else if constexpr (ExactLayout<D, G, SMAX, 1>::BYTES <= budget) {
+    return 1;
+  } else if constexpr (SMAX < 4 || lph < 8 || ExactLayout<D, G, SMAX, 2>::BYTES <= budget) {
+    return 2;
+  } else {
+    return 4;
+  }
+}
+
+// K register slot j of lane r (r < D/8): the row it is loaded with, and the
+// 16-byte chunk of that row, for NSTAGE stages.  With one stage these are j
+// and r, the plain load.
+template <int D, int NSTAGE>
+__device__ __forceinline__ int exact_k_row(int r, int j) {
+  constexpr int CH = D / 8 / NSTAGE;
+  return NSTAGE * (j / NSTAGE) + (j % NSTAGE + r / CH) % NSTAGE;
+}
+
+template <int D, int NSTAGE>
+__device__ __forceinline__ int exact_k_chunk(int r, int j) {
+  constexpr int CH = D / 8 / NSTAGE;
+  return CH * (j % NSTAGE) + r % CH;
+}
+
+// One loaded 16-byte chunk (8 bf16) into the staging: as it is, or widened
+// to 8 float32 (WIDE).
+template <bool WIDE>
+__device__ __forceinline__ void stage_chunk(unsigned char* dst, const u32x4 x) {
+  if constexpr (WIDE) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{x[0] << 16, x[0] & 0xffff0000u, x[1] << 16, x[1] & 0xffff0000u};
+    *reinterpret_cast<u32x4*>(dst + 16) = u32x4{x[2] << 16, x[2] & 0xffff0000u, x[3] << 16, x[3] & 0xffff0000u};
+  } else {
+    *reinterpret_cast<u32x4*>(dst) = x;
+  }
+}
+
+// The 8 dims of staged chunk c of a row as float32.
+template <bool WIDE>
+__device__ __forceinline__ void staged_dims(const unsigned char* row, int c, float (&f)[8]) {
+  if constexpr (WIDE) {
+    const float4 a = *reinterpret_cast<const float4*>(row + c * 32);
+    const float4 b = *reinterpret_cast<const float4*>(row + c * 32 + 16);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(row + c * 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = x[e];
+      f[2 * e] = __builtin_bit_cast(float, w << 16);
+      f[2 * e + 1] = __builtin_bit_cast(float, w & 0xffff0000u);
+    }
+  }
+}
+
 // lds: LDS of the weights (VP bf16 slots per KV head, as decode_core), then
-// ExactLayout::BYTES of staging.  GROUP_S: the lane groups serve different
-// batches, so a score lane takes the length of the head it scores from that
-// head's lanes.
+// ExactLayout::BYTES of staging.  kr: slot j as exact_k_row/exact_k_chunk
+// say.  GROUP_S: the lane groups serve different batches, so a score lane
+// takes the length of the head it scores from that head's lanes.
 template <int D, int G, int SMAX, int NSTAGE, bool GROUP_S>
 __device__ __forceinline__ void decode_core_exact(const u32x4 (&qv)[G], const u32x4 (&kr)[SMAX],
                                                   const u32x4 (&vr)[SMAX], int S, float scale, int lane,
@@ -592,124 +688,128 @@ __device__ __forceinline__ void decode_core_exact(const u32x4 (&qv)[G], const u3
 #pragma clang fp contract(off)
   using L = ExactLayout<D, G, SMAX, NSTAGE>;
   constexpr int LPH = L::LPH;
+  constexpr int CH = L::CH;
+  constexpr int RB = L::RB;
   constexpr int VP = G * kMaxSeq;
-  constexpr int N = L::HPW * G * SMAX;          // scores of the wave
+  constexpr int N = L::N;
   constexpr int NSLOT = (N + kWaveSize - 1) / kWaveSize;
+  // Softmax slots unrolled when a lane has at most two of them; rolled
+  // above, which keeps one score's registers live instead of NSLOT's.
+  constexpr int SLOT_UNROLL = NSLOT <= 2 ? NSLOT : 1;
+  constexpr int CH_UNROLL = CH < 4 ? CH : 4;
   constexpr int RS = ilog2(SMAX);               // row steps of the max exchange
   unsigned char* ks = reinterpret_cast<unsigned char*>(lds_p + L::HPW * VP);
   unsigned char* qz = ks + L::K_BYTES;
   float* es = reinterpret_cast<float*>(qz + L::Q_BYTES);
   const int r = lane % LPH;
   const int hkl = lane / LPH;
+  const int u = r / CH;                         // the stage of this lane's own chunk
 
-  // ---- the query as float32 words, one per dim ----
+  // ---- this lane's block: head bh, query heads bg + i GBN, rows bj + t JBN ----
+  const int bj = lane % L::JBN;
+  const int bg = (lane / L::JBN) % L::GBN;
+  const int bh = lane / (L::JBN * L::GBN);
+  const bool has_block = lane < L::NB;
+  float sacc[L::GB][L::JB];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    unsigned char* dst = qz + (hkl * G + g) * L::QRS + r * 32;
-    const u32x4 lo = {qv[g][0] << 16, qv[g][0] & 0xffff0000u, qv[g][1] << 16, qv[g][1] & 0xffff0000u};
-    const u32x4 hi = {qv[g][2] << 16, qv[g][2] & 0xffff0000u, qv[g][3] << 16, qv[g][3] & 0xffff0000u};
-    *reinterpret_cast<u32x4*>(dst) = lo;
-    *reinterpret_cast<u32x4*>(dst + 16) = hi;
-  }
-
-  // ---- this lane's scores: slot s is score sigma = lane + 64 s ----
-  int sj[NSLOT], sh[NSLOT], sg[NSLOT];
-  float sacc[NSLOT];
+  for (int i = 0; i < L::GB; ++i)
 #pragma unroll
-  for (int sl = 0; sl < NSLOT; ++sl) {
-    const int sigma = lane + kWaveSize * sl;
-    const int c = sigma / SMAX;                 // (head, query head) pair
-    sj[sl] = sigma % SMAX;
-    sg[sl] = c % G;
-    sh[sl] = (c / G) % L::HPW;                  // in range for slots past N (unused)
-    sacc[sl] = 0.0f;
-  }
+    for (int t = 0; t < L::JB; ++t) sacc[i][t] = 0.0f;
 
-  // Two stages: the lane's chunk of row j belongs to stage (r / CH + j) % 2,
-  // so in stage 0 it writes rows j = 2i + u (u = r / CH) and keeps rows
-  // 2i + 1 - u for stage 1.
-  constexpr int NH = NSTAGE == 2 ? SMAX / 2 : 1;
-  u32x4 rest[NH];
-  const int u = NSTAGE == 2 ? r / L::CH : 0;
 #pragma unroll
   for (int st = 0; st < NSTAGE; ++st) {
-    if (st > 0) {  // every lane is done with the previous stage's rows
+    if (st > 0) {  // every lane is done reading the previous stage
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if constexpr (NSTAGE == 1) {
+    // ---- stage st: K slots st, st + NSTAGE, ... and this lane's Q chunks ----
+    // ---- (when they belong here), widened to float32                     ----
+    constexpr int CB = L::WIDE ? 32 : 16;       // staged bytes per chunk
 #pragma unroll
-      for (int j = 0; j < SMAX; ++j) *reinterpret_cast<u32x4*>(ks + (hkl * SMAX + j) * L::KRS + r * 16) = kr[j];
-    } else {
-      static_assert(NSTAGE != 2 || SMAX % 2 == 0, "two stages need an even bucket");
+    for (int j = st; j < SMAX; j += NSTAGE)
+      stage_chunk<L::WIDE>(ks + hkl * L::KH + exact_k_row<D, NSTAGE>(r, j) * RB + (r % CH) * CB, kr[j]);
+    if (u == st) {
 #pragma unroll
-      for (int i = 0; i < NH; ++i) {
-        const int j = 2 * i + (st == 0 ? u : 1 - u);
-        u32x4 val;
-        if (st == 0) {
-          val = u ? kr[2 * i + 1] : kr[2 * i];
-          rest[i] = u ? kr[2 * i] : kr[2 * i + 1];
-          // selected here, so that kr is dead once stage 0 is written
-          asm volatile("" : "+v"(rest[i]));
-        } else {
-          val = rest[i];
-        }
-        *reinterpret_cast<u32x4*>(ks + (hkl * SMAX + j) * L::KRS + (r % L::CH) * 16) = val;
-      }
+      for (int g = 0; g < G; ++g) stage_chunk<L::WIDE>(qz + hkl * L::QH + g * RB + (r % CH) * CB, qv[g]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- this stage's dims of the lane's block, in dim order ----
+    if (has_block) {
+      const unsigned char* kb = ks + bh * L::KH + bj * RB;
+      const unsigned char* qb = qz + bh * L::QH + bg * RB;
+      // (unrolled by at most 4: unrolled in full, the compiler hoists every
+      // read of the loop and spills at D = 256)
+#pragma unroll CH_UNROLL
+      for (int c = 0; c < CH; ++c) {
+        // 8 dims of the block's query heads and rows, widened once each
+        float qf[L::GB][8], kf[L::JB][8];
 #pragma unroll
-    for (int sl = 0; sl < NSLOT; ++sl) {
-      if (lane + kWaveSize * sl >= N) continue;
-      const unsigned char* krow = ks + (sh[sl] * SMAX + sj[sl]) * L::KRS;
-      const unsigned char* qrow = qz + (sh[sl] * G + sg[sl]) * L::QRS + st * L::CH * 32;
-      float a = sacc[sl];
+        for (int i = 0; i < L::GB; ++i) staged_dims<L::WIDE>(qb + i * L::GBN * RB, c, qf[i]);
 #pragma unroll
-      for (int cc = 0; cc < L::CH; ++cc) {
-        const u32x4 k = *reinterpret_cast<const u32x4*>(krow + cc * 16);
-        const u32x4 q0 = *reinterpret_cast<const u32x4*>(qrow + cc * 32);
-        const u32x4 q1 = *reinterpret_cast<const u32x4*>(qrow + cc * 32 + 16);
-        const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+        for (int t = 0; t < L::JB; ++t) staged_dims<L::WIDE>(kb + t * L::JBN * RB, c, kf[t]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t kp = k[i];
-          a = __builtin_fmaf(__builtin_bit_cast(float, qw[2 * i]), __builtin_bit_cast(float, kp << 16), a);
-          a = __builtin_fmaf(__builtin_bit_cast(float, qw[2 * i + 1]), __builtin_bit_cast(float, kp & 0xffff0000u), a);
-        }
+        for (int i = 0; i < L::GB; ++i)
+#pragma unroll
+          for (int t = 0; t < L::JB; ++t) {
+            float a = sacc[i][t];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a = __builtin_fmaf(qf[i][e], kf[t][e], a);
+            sacc[i][t] = a;
+          }
       }
-      sacc[sl] = a;
     }
   }
-
-  // ---- softmax: max over the pair's SMAX lanes, exponentials, ----
-  // ---- their sum in row order through LDS, the bf16 weights    ----
-  float se[NSLOT];
-  bool sv[NSLOT];
+  // ---- the scores, [head][query head][row] ----
+  if (has_block) {
 #pragma unroll
-  for (int sl = 0; sl < NSLOT; ++sl) {
-    const int Sh = GROUP_S ? __shfl(S, sh[sl] * LPH, kWaveSize) : S;
-    sv[sl] = lane + kWaveSize * sl < N && sj[sl] < Sh;
-    const float t = sacc[sl] * scale;
-    float m = sv[sl] ? t : -__builtin_inff();
-    m = GroupReduce<SMAX, 0, RS, true>::run(m);
-    se[sl] = sv[sl] ? (float)exp((double)(t - m)) : 0.0f;
-    if (lane + kWaveSize * sl < N) es[lane + kWaveSize * sl] = se[sl];
+    for (int i = 0; i < L::GB; ++i)
+#pragma unroll
+      for (int t = 0; t < L::JB; ++t) es[(bh * G + bg + i * L::GBN) * SMAX + bj + t * L::JBN] = sacc[i][t];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
+
+  // ---- softmax: score sigma = lane + 64 sl; max over the pair's SMAX ----
+  // ---- lanes (every lane takes part in the exchange), the exponential ----
+  // ---- back into es[sigma]                                           ----
+#pragma unroll SLOT_UNROLL
   for (int sl = 0; sl < NSLOT; ++sl) {
-    if (lane + kWaveSize * sl >= N) continue;
-    const float* row = es + ((lane + kWaveSize * sl) / SMAX) * SMAX;
-    float sum = 0.0f;
+    const int sigma = lane + kWaveSize * sl;
+    const bool in = sigma < N;
+    const int c = sigma / SMAX;
+    const int h = in ? c / G : 0;
+    const int Sh = GROUP_S ? __shfl(S, h * LPH, kWaveSize) : S;
+    const bool valid = in && sigma % SMAX < Sh;
+    const float t = (in ? es[sigma] : 0.0f) * scale;
+    float m = valid ? t : -__builtin_inff();
+    m = GroupReduce<SMAX, 0, RS, true>::run(m);
+    const float e = valid ? (float)exp((double)(t - m)) : 0.0f;
+    if (in) es[sigma] = e;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // ---- the sum in row order, the quotient, the bf16 weight ----
+  // (an invalid row's exponential is +0: with at least one valid row the
+  // sum is >= 1 and its weight +0; with none the sum is 0 and so is every
+  // weight)
+#pragma unroll SLOT_UNROLL
+  for (int sl = 0; sl < NSLOT; ++sl) {
+    const int sigma = lane + kWaveSize * sl;
+    if (sigma < N) {
+      const int c = sigma / SMAX;
+      const float* row = es + c * SMAX;
+      float sum = 0.0f;
 #pragma unroll
-    for (int jj = 0; jj < SMAX; ++jj) sum += row[jj];
-    const float p = sv[sl] ? se[sl] / sum : 0.0f;
-    lds_p[sh[sl] * VP + sg[sl] * kMaxSeq + sj[sl]] = __builtin_bit_cast(uint16_t, (__bf16)p);
+      for (int jj = 0; jj < SMAX; ++jj) sum += row[jj];
+      const float e = row[sigma % SMAX];
+      const float p = sum > 0.0f ? e / sum : 0.0f;
+      lds_p[(c / G) * VP + (c % G) * kMaxSeq + sigma % SMAX] = __builtin_bit_cast(uint16_t, (__bf16)p);
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -722,10 +822,12 @@ __device__ __forceinline__ void decode_core_exact(const u32x4 (&qv)[G], const u3
   for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+    uint32_t w2[(SMAX + 1) / 2];
+#pragma unroll
+    for (int jp = 0; jp < (SMAX + 1) / 2; ++jp) w2[jp] = reinterpret_cast<const uint32_t*>(wrow + g * kMaxSeq)[jp];
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) {
-      const uint32_t w = wrow[g * kMaxSeq + j];
-      const float wf = __builtin_bit_cast(float, w << 16);
+      const float wf = __builtin_bit_cast(float, j % 2 == 0 ? w2[j / 2] << 16 : w2[j / 2] & 0xffff0000u);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t vp = vr[j][i];
@@ -741,18 +843,12 @@ __device__ __forceinline__ void decode_core_exact(const u32x4 (&qv)[G], const u3
   }
 }
 
-// Stages of the exact path's K staging.  Kernels that choose the bucket per
-// wave (VARLEN) size their LDS for the longest bucket; there bucket 16
-// stages in two halves, which keeps that size near bucket 8's (11.7 KiB per
-// wave at D = 128 against 19.9 KiB in one stage).
-__device__ __forceinline__ constexpr int exact_stages(int smax, bool varlen) { return varlen && smax >= 16 ? 2 : 1; }
-
-// Whether a bucket takes the exact path: kernels instantiated for it (one
-// query head per KV head, bf16 weights) and more than one row (one row has
-// weight 1 and output fp16(V) on either path).
+// Whether a bucket takes the exact path: kernels instantiated for it (bf16
+// weights, any of the VALU kernel's group sizes) and more than one row (one
+// row has weight 1 and output fp16(V) on either path).
 template <int G, int SMAX, bool PF32, bool EXACT>
 __device__ __forceinline__ constexpr bool exact_taken() {
-  static_assert(!EXACT || (G == 1 && !PF32), "the exact path computes one query head per KV head, bf16 weights");
+  static_assert(!EXACT || !PF32, "the exact path rounds the weights to bf16");
   return EXACT && SMAX > 1;
 }
 
@@ -763,7 +859,7 @@ __device__ __forceinline__ constexpr int exact_extra_bytes() {
   if constexpr (!exact_taken<G, SMAX_TOP, PF32, EXACT>()) {
     return 0;
   } else {
-    int m = ExactLayout<D, G, SMAX_TOP, exact_stages(SMAX_TOP, VARLEN)>::BYTES;
+    int m = ExactLayout<D, G, SMAX_TOP, exact_stages<D, G, SMAX_TOP>()>::BYTES;
     if constexpr (VARLEN && SMAX_TOP > 2) {
       const int n = exact_extra_bytes<D, G, SMAX_TOP / 2, PF32, VARLEN, EXACT>();
       m = n > m ? n : m;
@@ -772,11 +868,18 @@ __device__ __forceinline__ constexpr int exact_extra_bytes() {
   }
 }
 
-// Byte offset of the K chunk lane r loads for row j, relative to chunk r.
-template <int D, int G, int SMAX, bool PF32, bool VARLEN, bool EXACT>
+// The row K slot j of lane r is loaded with (j itself outside the exact path).
+template <int D, int G, int SMAX, bool PF32, bool EXACT>
+__device__ __forceinline__ int exact_k_row_of(int r, int j) {
+  if constexpr (exact_taken<G, SMAX, PF32, EXACT>()) return exact_k_row<D, exact_stages<D, G, SMAX>()>(r, j);
+  return j;
+}
+
+// Byte offset of the K chunk slot j of lane r loads, relative to chunk r.
+template <int D, int G, int SMAX, bool PF32, bool EXACT>
 __device__ __forceinline__ uint32_t exact_k_delta(int r, int j) {
   if constexpr (exact_taken<G, SMAX, PF32, EXACT>())
-    return (uint32_t)((exact_k_chunk<D, exact_stages(SMAX, VARLEN)>(r, j) - r) * 16);
+    return (uint32_t)((exact_k_chunk<D, exact_stages<D, G, SMAX>()>(r, j) - r) * 16);
   return 0u;
 }
 
@@ -786,7 +889,7 @@ __device__ __forceinline__ void decode_core_any(const u32x4 (&qv)[G], const u32x
                                                 const u32x4 (&vr)[SMAX], int S, float scale, int lane,
                                                 uint16_t* lds_p, float (&acc)[G][8], int active) {
   if constexpr (exact_taken<G, SMAX, PF32, EXACT>()) {
-    decode_core_exact<D, G, SMAX, exact_stages(SMAX, VARLEN), GROUP_S>(qv, kr, vr, S, scale, lane, lds_p, acc);
+    decode_core_exact<D, G, SMAX, exact_stages<D, G, SMAX>(), GROUP_S>(qv, kr, vr, S, scale, lane, lds_p, acc);
   } else {
     decode_core<D, G, SMAX, PF32, VARLEN>(qv, kr, vr, S, scale, lane, lds_p, acc, active);
   }
@@ -833,9 +936,16 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
   u32x4 vr[SMAX];
   if constexpr (LAYOUT != kLayoutPaged) {
 #pragma unroll
-    for (int j = 0; j < SMAX; ++j)
+    for (int j = 0; j < SMAX; ++j) {
+      // The exact path loads K slot j with another row and chunk (the same
+      // row and chunk r elsewhere).
+      const int jr = exact_k_row_of<D, G, SMAX, PF32, EXACT>(r, j);
+      const uint32_t roff = jr == j ? row_off[j]
+                            : (LAYOUT == kLayoutStrided && jr >= S) ? kRowOutOfRange
+                                                                    : (uint32_t)jr * kv.row_bytes;
       kr[j] = buffer_load16<kPolicyStream>(
-          k_rsrc, kv_off + row_off[j] + (head_ok ? exact_k_delta<D, G, SMAX, PF32, VARLEN, EXACT>(r, j) : 0u));
+          k_rsrc, kv_off + roff + (head_ok ? exact_k_delta<D, G, SMAX, PF32, EXACT>(r, j) : 0u));
+    }
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
   } else {
@@ -853,11 +963,10 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
       row_elem[j] = el < 0 ? 0u : (uint64_t)el;
       row_rec[j] = el < 0 ? 0u : kv.row_extent;
     }
+    static_assert(!exact_taken<G, SMAX, PF32, EXACT>(), "the exact path reads the packed and strided layouts");
 #pragma unroll
     for (int j = 0; j < SMAX; ++j)
-      kr[j] = buffer_load16<kPolicyStream>(
-          make_rsrc(kv.k + row_elem[j], row_rec[j]),
-          kv_off + (head_ok ? exact_k_delta<D, G, SMAX, PF32, VARLEN, EXACT>(r, j) : 0u));
+      kr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.k + row_elem[j], row_rec[j]), kv_off);
 #pragma unroll
     for (int j = 0; j < SMAX; ++j)
       vr[j] = buffer_load16<kPolicyStream>(make_rsrc(kv.v + row_elem[j], row_rec[j]), kv_off);
@@ -1035,9 +1144,13 @@ __device__ __forceinline__ void decode_multi_unit(const DecodeArgs& a, uint32_t 
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
 #pragma unroll
-  for (int j = 0; j < SMAX; ++j)
+  for (int j = 0; j < SMAX; ++j) {
+    // The exact path loads K slot j with another row and chunk.
+    const int jr = exact_k_row_of<D, G, SMAX, PF32, EXACT>(r, j);
+    const uint32_t roff = jr == j ? row_off[j] : (jr < S ? (uint32_t)jr * row_bytes : kRowOutOfRange);
     kr[j] = buffer_load16<kPolicyStream>(
-        k_rsrc, kv_off + row_off[j] + (lane_ok ? exact_k_delta<D, G, SMAX, PF32, true, EXACT>(r, j) : 0u));
+        k_rsrc, kv_off + roff + (lane_ok ? exact_k_delta<D, G, SMAX, PF32, EXACT>(r, j) : 0u));
+  }
 #pragma unroll
   for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
   __builtin_amdgcn_sched_barrier(0);

@@ -157,12 +157,21 @@ hipError_t launch_multi(const DecodeArgs& a, int d, int g, int w, hipStream_t st
 #undef FMHA_DECODE_MULTI_G
 }
 
-// The exact-arithmetic kernels: packed layout, one query head per KV head;
-// multi: R batches per wave (fewer KV heads than a wave holds).
-template <int D>
+// The exact-arithmetic kernels: packed layout, G query heads per KV head
+// (1, 2, 4, 8; 3 and 5-7 run on the 4- and 8-head kernels as padded
+// groups); multi: R batches per wave (fewer KV heads than a wave holds).
+// Known lengths (sb > 0, the uniform entry point) take them for G <= 2
+// only, the groups whose default numerics they are; above, only
+// fmha_decode_fwd_exact reaches them, with lengths on the device.
+template <int D, int G>
 hipError_t launch_exact(const DecodeArgs& a, bool multi, int sb, int w, hipStream_t stream) {
-  return multi ? launch_multi_one<D, 1, kLayoutPacked, false, true>(a, w, stream)
-               : launch_bucket<D, 1, kLayoutPacked, false, true>(a, sb, w, stream);
+  if (multi) return launch_multi_one<D, G, kLayoutPacked, false, true>(a, w, stream);
+  if constexpr (G <= 2) {
+    return launch_bucket<D, G, kLayoutPacked, false, true>(a, sb, w, stream);
+  } else {
+    (void)sb;
+    return launch_one<D, G, kLayoutPacked, 0, false, true>(a, w, stream);
+  }
 }
 
 template <int D, int NS, int LAYOUT>
@@ -473,9 +482,18 @@ extern template hipError_t launch_group<256, kLayoutPacked, false>(const DecodeA
 extern template hipError_t launch_group<256, kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_group<256, kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_group<256, kLayoutPaged, false>(const DecodeArgs&, int, int, int, hipStream_t);
-extern template hipError_t launch_exact<64>(const DecodeArgs&, bool, int, int, hipStream_t);
-extern template hipError_t launch_exact<128>(const DecodeArgs&, bool, int, int, hipStream_t);
-extern template hipError_t launch_exact<256>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<64, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<64, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<64, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<64, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<128, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<128, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<128, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<128, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<256, 1>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<256, 2>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<256, 4>(const DecodeArgs&, bool, int, int, hipStream_t);
+extern template hipError_t launch_exact<256, 8>(const DecodeArgs&, bool, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutPacked, false>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutPacked, true>(const DecodeArgs&, int, int, int, hipStream_t);
 extern template hipError_t launch_multi<kLayoutStrided, false>(const DecodeArgs&, int, int, int, hipStream_t);

@@ -43,11 +43,24 @@ def launch_fmha_decode(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, nu
     """Variable-length decode attention on raw device pointers (ints).
 
     stream is a hipStream_t as an int (0 = null stream).  Mirrors
-    launch_fmha_mfma_4x4x4 (fmha_mfma_4x4x4_kernel.hpp:370-376).
+    launch_fmha_mfma_4x4x4 (fmha_mfma_4x4x4_kernel.hpp:370-376).  Up to 2
+    query heads per KV head the outputs are the reference CPU loop's
+    (fmha_host.cpp:179-244) bit for bit; above, tree-order sums (within the
+    comparison gate).
     """
     rc = _lib.load().fmha_decode_fwd(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q,
                                      num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                                      float(softmax_scale))
+    _raise_if(rc)
+
+
+def launch_fmha_decode_fast(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv,
+                            seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
+    """launch_fmha_decode with tree-order sums and the device expf: the same
+    semantics within the comparison gate, not the CPU loop's bits."""
+    rc = _lib.load().fmha_decode_fwd_fast(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q,
+                                          num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                          float(softmax_scale))
     _raise_if(rc)
 
 
@@ -64,8 +77,9 @@ def launch_fmha_decode_fp32_weights(stream, Q, K, V, O, cu_seqlens_kv, batch, nu
 def launch_fmha_decode_exact(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q, num_heads_kv,
                              seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
     """launch_fmha_decode with the reference CPU loop's arithmetic step for
-    step (fmha_host.cpp:179-244): its outputs bit for bit wherever that
-    loop's expf returns the nearest float; num_heads_q == num_heads_kv."""
+    step (fmha_host.cpp:179-244) for every call: its outputs bit for bit
+    wherever that loop's expf returns the nearest float; more than 8 query
+    heads per KV head are rejected."""
     rc = _lib.load().fmha_decode_fwd_exact(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads_q,
                                            num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                                            float(softmax_scale))
@@ -74,10 +88,20 @@ def launch_fmha_decode_exact(stream, Q, K, V, O, cu_seqlens_kv, batch, num_heads
 
 def launch_fmha_decode_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv,
                                seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
-    """Uniform-length decode attention (K/V as [batch, seqlen_kv, Hkv, D])."""
+    """Uniform-length decode attention (K/V as [batch, seqlen_kv, Hkv, D]);
+    numerics as launch_fmha_decode."""
     rc = _lib.load().fmha_decode_fwd_uniform(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q,
                                              num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                                              float(softmax_scale))
+    _raise_if(rc)
+
+
+def launch_fmha_decode_uniform_fast(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q, num_heads_kv,
+                                    seqlen_q, head_dim_q, head_dim_kv, softmax_scale):
+    """launch_fmha_decode_uniform with the numerics of launch_fmha_decode_fast."""
+    rc = _lib.load().fmha_decode_fwd_uniform_fast(stream, Q, K, V, O, seqlen_kv, batch, num_heads_q,
+                                                  num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
+                                                  float(softmax_scale))
     _raise_if(rc)
 
 
@@ -303,7 +327,7 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
 
 
 def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None, out=None, fp32_weights=False,
-                exact=False):
+                exact=False, fast=False):
     """Decode attention on torch tensors; returns O (fp16, shaped like q).
 
     q: [B, Hq, 1, D] or [B, Hq, D], bfloat16, contiguous, on a GPU.
@@ -312,11 +336,17 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
     cu_seqlens_kv: int32 [B+1] on the same device, or None.
     softmax_scale: defaults to 1/sqrt(D), as the reference passes
       (fmha_host.cpp:371).
+    Numerics (at most one flag): by default the reference CPU loop's
+      arithmetic step for step up to 2 query heads per KV head (its outputs
+      bit for bit wherever its expf returns the nearest float) and tree-order
+      sums above;
+    exact: the loop's arithmetic for every call (with cu_seqlens_kv up to 8
+      query heads per KV head, with uniform lengths up to 2; others are
+      rejected);
+    fast: tree-order sums and the device expf (fmha_decode_fwd_fast,
+      fmha_decode_fwd_uniform_fast);
     fp32_weights: keep the softmax weights in fp32 (fmha_vectorized_fma's
       semantics) instead of rounding them to bf16; needs cu_seqlens_kv.
-    exact: the reference CPU loop's arithmetic step for step (its outputs
-      bit for bit wherever its expf returns the nearest float); needs
-      cu_seqlens_kv and Hq == Hkv.
     """
     import torch
 
@@ -340,6 +370,8 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
     Hkv = k.shape[-2]
     if k.shape[-1] != D:
         raise ValueError("k/v head_dim must equal q head_dim")
+    if int(bool(fp32_weights)) + int(bool(exact)) + int(bool(fast)) > 1:
+        raise ValueError("fp32_weights, exact and fast are different numerics; pick one")
     _check_device(q, k=k, v=v)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
@@ -357,21 +389,26 @@ def fmha_decode(q, k, v, cu_seqlens_kv=None, seqlen_kv=None, softmax_scale=None,
             raise ValueError("cu_seqlens_kv must be a contiguous tensor on q's device")
         if k.dim() != 3:
             raise ValueError("packed k/v must be [rows, Hkv, D]")
-        if fp32_weights and exact:
-            raise ValueError("fp32_weights and exact are different numerics; pick one")
         launch = (launch_fmha_decode_fp32_weights if fp32_weights else
-                  launch_fmha_decode_exact if exact else launch_fmha_decode)
+                  launch_fmha_decode_exact if exact else
+                  launch_fmha_decode_fast if fast else launch_fmha_decode)
         launch(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                cu_seqlens_kv.data_ptr(), B, Hq, Hkv, 1, D, D, softmax_scale)
     else:
-        if fp32_weights or exact:
-            raise ValueError("fp32_weights and exact need the packed layout with cu_seqlens_kv")
+        if fp32_weights:
+            raise ValueError("fp32_weights needs the packed layout with cu_seqlens_kv")
+        if exact and Hq // Hkv > 2:
+            # fmha_decode_fwd_uniform takes the exact numerics up to 2 query
+            # heads per KV head; fmha_decode_fwd_exact (cu_seqlens_kv) up to 8
+            raise ValueError("exact with uniform lengths takes at most 2 query heads per KV head (got %d); "
+                             "pass cu_seqlens_kv for up to 8" % (Hq // Hkv))
         if seqlen_kv is None:
             if k.dim() != 4 or k.shape[0] != B:
                 raise ValueError("uniform k/v must be [B, S, Hkv, D] when seqlen_kv is not given")
             seqlen_kv = k.shape[1]
         if k.numel() != B * seqlen_kv * Hkv * D:
             raise ValueError("k/v size does not match batch * seqlen_kv * Hkv * D")
-        launch_fmha_decode_uniform(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                   seqlen_kv, B, Hq, Hkv, 1, D, D, softmax_scale)
+        launch = launch_fmha_decode_uniform_fast if fast else launch_fmha_decode_uniform
+        launch(stream, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+               seqlen_kv, B, Hq, Hkv, 1, D, D, softmax_scale)
     return out

@@ -10,6 +10,15 @@
  *     P_j = bf16( exp(s_j*scale - max) / sum_i exp(s_i*scale - max) )
  *     O[b,h,d] = fp16( sum_j P_j * V[cu[b]+j, hk, d] )
  *
+ * Numerics.  With at most 2 query heads per KV head (Hq / Hkv <= 2: the
+ * reference's own configurations and BASELINE's), fmha_decode_fwd and
+ * fmha_decode_fwd_uniform compute this with the arithmetic of the reference
+ * CPU loop (fmha_host.cpp:179-244) step for step (see fmha_decode_fwd_exact):
+ * their outputs are that loop's, bit for bit.  With larger groups they sum
+ * in tree order with the device expf (see fmha_decode_fwd_fast): the same
+ * semantics within the comparison gate, not the same bits;
+ * fmha_decode_fwd_exact gives the loop's bits for groups of up to 8.
+ *
  * Layouts (element counts, row-major, no padding):
  *   Q  [batch, num_heads_q, 1, head_dim]    bf16   (BHSD with S = 1)
  *   O  [batch, num_heads_q, 1, head_dim]    fp16
@@ -23,8 +32,8 @@
  * the null stream) and may be issued from any number of host threads.  They
  * allocate no device memory.  The one piece of library state: the entry
  * points that read lengths from a device cu_seqlens_kv array
- * (fmha_decode_fwd, fmha_decode_fwd_fp32_weights, fmha_decode_fwd_exact
- * and fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
+ * (fmha_decode_fwd, its _fast, _fp32_weights and _exact forms, and
+ * fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
  * per device (64 bytes, allocated by the first such call that is not being
  * captured into a graph, never freed) in which each call's first wave leaves
  * the call's mean length; the next call sizes its launch (waves per CU) from
@@ -70,20 +79,19 @@ extern "C" {
  *   batch           >= 0 (0 launches nothing)
  *   num_heads_q     > 0, a multiple of num_heads_kv
  *   num_heads_kv    > 0; any group size G = num_heads_q / num_heads_kv.
- *                   G <= 8 runs the VALU kernel (G = 3 on its 4-head and
- *                   5-7 on its 8-head instantiation, the extra heads
- *                   reading and writing nothing); G > 8 runs the
- *                   matrix-core kernel (it needs num_heads_kv * head_dim
- *                   below 2^24, else FMHA_DECODE_ERROR_NOT_SUPPORTED).  The
- *                   same numerics within the comparison gate, not the same
- *                   bits.  The environment variable
- *                   FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel
- *                   for every G.  This entry point,
- *                   fmha_decode_fwd_uniform and fmha_decode_fwd_strided take
- *                   any G, and so do the split-KV entries (through a
- *                   padded query group beyond 16 rows);
- *                   fmha_decode_fwd_paged and fmha_decode_fwd_fp32_weights
- *                   G <= 8 (else FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   G <= 2 runs the exact-arithmetic VALU kernel (the
+ *                   reference loop's bits), G = 3-8 the tree-order VALU
+ *                   kernel (G = 3 on its 4-head and 5-7 on its 8-head
+ *                   instantiation, the extra heads reading and writing
+ *                   nothing), G > 8 the matrix-core kernel (it needs
+ *                   num_heads_kv * head_dim below 2^24, else
+ *                   FMHA_DECODE_ERROR_NOT_SUPPORTED).  This entry point,
+ *                   fmha_decode_fwd_uniform, their _fast forms and
+ *                   fmha_decode_fwd_strided take any G, and so do the
+ *                   split-KV entries (through a padded query group beyond
+ *                   16 rows); fmha_decode_fwd_exact, fmha_decode_fwd_paged
+ *                   and fmha_decode_fwd_fp32_weights G <= 8 (else
+ *                   FMHA_DECODE_ERROR_NOT_SUPPORTED).
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q
@@ -100,6 +108,29 @@ int fmha_decode_fwd(void* stream,
                     int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                     int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                     float softmax_scale);
+
+/*
+ * fmha_decode_fwd with tree-order numerics for every group size: each score
+ * summed over its dims as a tree of packed bf16 dot products, the device
+ * expf, the weights rounded to bf16 as in the loop, P.V as packed dot
+ * products and the last multiply-add rounded straight to fp16.  A few
+ * outputs in ten thousand differ from the reference loop in the last bits
+ * (every one within the comparison gate).  At most 1% faster than
+ * fmha_decode_fwd with one or two query heads per KV head, 5-6% with short
+ * rows at head_dim 256; the same kernels above.  G <= 8 runs the tree-order
+ * VALU kernel, G > 8 the matrix-core kernel; the environment variable
+ * FMHA_DECODE_GQA_KERNEL=mfma runs the matrix-core kernel for every G here
+ * and for G > 2 in fmha_decode_fwd (for comparisons).  Same arguments,
+ * layouts, checks and errors as fmha_decode_fwd.  No counterpart in the
+ * reference, whose CPU loop and wired-in kernel have these semantics with
+ * their own orders of summation.
+ */
+int fmha_decode_fwd_fast(void* stream,
+                         const void* Q, const void* K, const void* V, void* O,
+                         const int32_t* cu_seqlens_kv,
+                         int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                         int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                         float softmax_scale);
 
 /*
  * fmha_decode_fwd with the softmax weights kept in fp32: P_j is the fp32
@@ -121,25 +152,25 @@ int fmha_decode_fwd_fp32_weights(void* stream,
                                  float softmax_scale);
 
 /*
- * fmha_decode_fwd computed with the arithmetic of the reference CPU loop
- * (fmha_host.cpp:179-244) step for step, for the inputs that loop is written
- * for (num_heads_q == num_heads_kv, lengths up to 16): each score a float32
- * sum over d = 0, 1, ..., D-1 in order (every product exact, every addition
- * rounded), then * softmax_scale; the max; each exponential the float
- * nearest exp(s_j*scale - max) (evaluated in double and rounded once); their
- * float32 sum in row order; the IEEE quotient rounded to bf16; O a float32
- * sum over rows in order, rounded to fp16.  The outputs equal that loop's
- * bit for bit wherever its expf returns the nearest float (glibc 2.35's
- * expf misses it on about 0.07% of arguments, and an output can differ only
- * where such a miss also flips a bf16 weight: none in ten million random
- * heads).  fmha_decode_fwd sums in a tree order, uses the device expf and
- * rounds its last multiply-add straight to fp16, so there a few outputs in
- * ten thousand differ from the loop in the last bit.  Same arguments,
- * layouts, checks and errors as fmha_decode_fwd, and num_heads_q !=
- * num_heads_kv gives FMHA_DECODE_ERROR_NOT_SUPPORTED.  0.99-1.05x the time
- * of fmha_decode_fwd on the BASELINE and reference configurations.  No
- * counterpart in the reference, which has no GPU kernel with these results;
- * for callers that need the CPU loop's outputs.
+ * fmha_decode_fwd with the arithmetic of the reference CPU loop
+ * (fmha_host.cpp:179-244) step for step for every call, with the
+ * grouped-query head mapping (query head h reads KV head h / G; the loop
+ * itself indexes K/V with h, fmha_host.cpp:190-192, which agrees for
+ * G = 1): each score a float32 sum over d = 0, 1, ..., D-1 in order (every
+ * product exact, every addition rounded), then * softmax_scale; the max;
+ * each exponential the float nearest exp(s_j*scale - max) (evaluated in
+ * double and rounded once); their float32 sum in row order; the IEEE
+ * quotient rounded to bf16; O a float32 sum over rows in order, rounded to
+ * fp16.  The outputs equal that loop's bit for bit wherever its expf
+ * returns the nearest float (glibc 2.35's expf misses it on about 0.07% of
+ * arguments, and an output can differ only where such a miss also flips a
+ * bf16 weight: none in ten million random heads).  These are the numerics
+ * fmha_decode_fwd takes for G <= 2; this entry point gives them for
+ * G <= 8 too (1-45% slower than the tree-order kernels there) and rejects
+ * G > 8 (FMHA_DECODE_ERROR_NOT_SUPPORTED).  Same arguments, layouts, checks
+ * and errors as fmha_decode_fwd otherwise.  No counterpart in the
+ * reference, which has no GPU kernel with these results; for callers that
+ * need the CPU loop's outputs whatever the group size.
  */
 int fmha_decode_fwd_exact(void* stream,
                           const void* Q, const void* K, const void* V, void* O,
@@ -155,7 +186,8 @@ int fmha_decode_fwd_exact(void* stream,
  * launch contract's seqlen_kv parameter; the reference derives every length
  * from cu_seqlens_kv instead (fmha_mfma_4x4x4_kernel.hpp:94-96).
  * seqlen_kv must lie in [0, 16]; with seqlen_kv == 0 no row is read, every
- * output is 0 and K and V may be NULL.  Other arguments as fmha_decode_fwd.
+ * output is 0 and K and V may be NULL.  Other arguments and numerics as
+ * fmha_decode_fwd (the reference loop's bits for G <= 2).
  */
 int fmha_decode_fwd_uniform(void* stream,
                             const void* Q, const void* K, const void* V, void* O,
@@ -163,6 +195,15 @@ int fmha_decode_fwd_uniform(void* stream,
                             int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                             int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                             float softmax_scale);
+
+/* fmha_decode_fwd_uniform with the numerics of fmha_decode_fwd_fast.  No
+ * counterpart in the reference. */
+int fmha_decode_fwd_uniform_fast(void* stream,
+                                 const void* Q, const void* K, const void* V, void* O,
+                                 int32_t seqlen_kv,
+                                 int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
+                                 int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
+                                 float softmax_scale);
 
 /*
  * Decode attention over K/V addressed by strides, for caches that are not
@@ -223,8 +264,8 @@ int fmha_decode_fwd_paged(void* stream,
  * CPU loop (fmha_host.cpp:209-226) extended past its 16-row arrays; the
  * reference itself stops at 16 (fmha_mfma_4x4x4_kernel.hpp:179, README.md:233).
  *
- * The library picks the kernels: the kernel of fmha_decode_fwd when
- * max_seqlen_kv <= 16; one single-pass launch when there are at least 512
+ * The library picks the kernels: the kernel and numerics of fmha_decode_fwd
+ * when max_seqlen_kv <= 16; one single-pass launch when there are at least 512
  * (batch, KV-head group) waves and a row's scores fit the wave's LDS; else
  * four split-KV launches (scores, statistics, P.V per chunk, combine).
  *

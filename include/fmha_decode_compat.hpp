@@ -16,10 +16,12 @@
 //     any head_dim other than 128 or fails later at the caller's next
 //     HIP_CHECK (which throws std::runtime_error, fmha_host.cpp:26-35).
 //
-// Compiled with FMHA_DECODE_COMPAT_EXACT defined, the launches go to
-// fmha_decode_fwd_exact instead: the reference CPU loop's arithmetic step
-// for step, so its own check (fmha_host.cpp:158-284) sees its own bits
-// (num_heads_q == num_heads_kv, the case that loop is written for).
+// fmha_decode_fwd computes the reference CPU loop's arithmetic step for step
+// (fmha_host.cpp:179-244) for num_heads_q / num_heads_kv <= 2, so with the
+// reference's head counts its own check (fmha_host.cpp:158-284) sees its
+// own bits.  Compiled with FMHA_DECODE_COMPAT_EXACT defined, the launches go
+// to fmha_decode_fwd_exact instead, which does so for groups of up to 8
+// query heads per KV head and rejects larger ones.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -71,8 +71,10 @@ def to_dev(bits, device="cuda"):
     return t.view(torch.bfloat16)
 
 
-def run_gpu(q, k, v, cu, Hq, Hkv, D, scale=None, uniform_s=None, device="cuda"):
-    """Launch the HIP kernel through the C ABI; returns O as fp16 bits."""
+def run_gpu(q, k, v, cu, Hq, Hkv, D, scale=None, uniform_s=None, device="cuda", fast=False, exact=False):
+    """Launch the HIP kernel through the C ABI (fmha_decode_fwd, or
+    fmha_decode_fwd_uniform with uniform_s; their _fast forms with fast;
+    fmha_decode_fwd_exact with exact); returns O as fp16 bits."""
     import torch
     import fmha_amd
     scale = default_scale(D) if scale is None else scale
@@ -80,10 +82,10 @@ def run_gpu(q, k, v, cu, Hq, Hkv, D, scale=None, uniform_s=None, device="cuda"):
     qd, kd, vd = to_dev(q, device), to_dev(k, device), to_dev(v, device)
     if uniform_s is None:
         cud = torch.from_numpy(np.ascontiguousarray(cu)).to(device)
-        o = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, softmax_scale=scale)
+        o = fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, softmax_scale=scale, fast=fast, exact=exact)
     else:
         o = fmha_amd.fmha_decode(qd, kd.view(B, uniform_s, Hkv, D), vd.view(B, uniform_s, Hkv, D),
-                                 seqlen_kv=uniform_s, softmax_scale=scale)
+                                 seqlen_kv=uniform_s, softmax_scale=scale, fast=fast)
     torch.cuda.synchronize()
     return o.view(torch.int16).cpu().numpy().view(np.uint16)
 
@@ -94,6 +96,32 @@ def check(o, q, k, v, cu, Hq, Hkv, D, scale=None):
     r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, scale, p_mode=0, with_slack=True)
     st = oracle.compare(o.reshape(r.shape), r, slack, ATOL, RTOL)
     return st
+
+
+def assert_exact(o, q, k, v, cu, Hq, Hkv, D, ctx="", scale=None):
+    """o (fp16 bits) equals the oracle's restated reference loop with
+    nearest-float exponentials (oracle.decode(p_mode=2)) bit for bit: the
+    numerics of the default entry points up to 2 query heads per KV head,
+    and of fmha_decode_fwd_exact."""
+    scale = default_scale(D) if scale is None else scale
+    r, _ = oracle.decode(q, k, v, cu, Hq, Hkv, D, scale, p_mode=2)
+    diff = int(np.count_nonzero(np.asarray(o).reshape(r.shape) != r))
+    assert diff == 0, f"{ctx}: {diff} of {r.size} outputs differ from the restated loop (p_mode=2)"
+
+
+def check_entry_points(q, k, v, cu, Hq, Hkv, D, uniform_s=None, ctx=""):
+    """Both numerics on the same inputs: the default entry point (bit for
+    bit against the restated loop up to 2 query heads per KV head, through
+    the gate above that) and the _fast one (through the gate).  Returns the
+    default entry point's output bits."""
+    o = run_gpu(q, k, v, cu, Hq, Hkv, D, uniform_s=uniform_s)
+    if Hq // Hkv <= 2:
+        assert_exact(o, q, k, v, cu, Hq, Hkv, D, ctx + " (default)")
+    else:
+        assert_pass(check(o, q, k, v, cu, Hq, Hkv, D), ctx + " (default)")
+    of = run_gpu(q, k, v, cu, Hq, Hkv, D, uniform_s=uniform_s, fast=True)
+    assert_pass(check(of, q, k, v, cu, Hq, Hkv, D), ctx + " (fast)")
+    return o
 
 
 def assert_pass(st, ctx=""):

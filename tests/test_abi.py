@@ -32,8 +32,8 @@ def lib():
 
 def test_exports_every_declared_function(lib):
     names = header_functions()
-    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fp32_weights", "fmha_decode_fwd_exact",
-                          "fmha_decode_fwd_uniform",
+    assert set(names) == {"fmha_decode_fwd", "fmha_decode_fwd_fast", "fmha_decode_fwd_fp32_weights",
+                          "fmha_decode_fwd_exact", "fmha_decode_fwd_uniform", "fmha_decode_fwd_uniform_fast",
                           "fmha_decode_fwd_strided",
                           "fmha_decode_fwd_paged", "fmha_decode_splitkv_workspace_size",
                           "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_noalloc",
@@ -61,6 +61,14 @@ def fwd(lib, **kw):
                                a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
 
 
+def fwd_fast(lib, **kw):
+    a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
+             scale=0.088)
+    a.update(kw)
+    return lib.fmha_decode_fwd_fast(a["stream"], a["q"], a["k"], a["v"], a["o"], a["cu"], a["batch"], a["hq"],
+                                    a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+
+
 def fwd32(lib, **kw):
     a = dict(stream=None, q=Q, k=K, v=V, o=O, cu=CU, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
              scale=0.088)
@@ -77,12 +85,13 @@ def fwd_exact(lib, **kw):
                                      a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
 
 
-def uni(lib, **kw):
+def uni(lib, fast=False, **kw):
     a = dict(stream=None, q=Q, k=K, v=V, o=O, s=16, batch=4, hq=16, hkv=16, sq=1, dq=128, dkv=128,
              scale=0.088)
     a.update(kw)
-    return lib.fmha_decode_fwd_uniform(a["stream"], a["q"], a["k"], a["v"], a["o"], a["s"], a["batch"],
-                                       a["hq"], a["hkv"], a["sq"], a["dq"], a["dkv"], a["scale"])
+    f = lib.fmha_decode_fwd_uniform_fast if fast else lib.fmha_decode_fwd_uniform
+    return f(a["stream"], a["q"], a["k"], a["v"], a["o"], a["s"], a["batch"], a["hq"], a["hkv"], a["sq"], a["dq"],
+             a["dkv"], a["scale"])
 
 
 @pytest.mark.parametrize("kw,code,needle", [
@@ -111,6 +120,8 @@ def uni(lib, **kw):
 def test_varlen_rejects(lib, kw, code, needle):
     assert fwd(lib, **kw) == code
     assert needle in lib.fmha_decode_last_error_detail().decode()
+    assert fwd_fast(lib, **kw) == code
+    assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
 @pytest.mark.parametrize("kw,code,needle", [
@@ -121,8 +132,9 @@ def test_varlen_rejects(lib, kw, code, needle):
     (dict(v=None), BAD, "non-null"),
 ])
 def test_uniform_rejects(lib, kw, code, needle):
-    assert uni(lib, **kw) == code
-    assert needle in lib.fmha_decode_last_error_detail().decode()
+    for fast in (False, True):
+        assert uni(lib, fast=fast, **kw) == code
+        assert needle in lib.fmha_decode_last_error_detail().decode()
 
 
 @pytest.mark.parametrize("hq,hkv", [(32, 2), (96, 8), (18, 1)])
@@ -314,8 +326,8 @@ def test_fp32_weights_rejects(lib, kw, code, needle):
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(batch=-1), BAD, "batch"),
-    (dict(hq=32, hkv=16), NOTSUP, "one query head per KV head"),
-    (dict(hq=16, hkv=1), NOTSUP, "one query head per KV head"),
+    (dict(hq=96, hkv=8), NOTSUP, "at most 8 query heads per KV head"),
+    (dict(hq=16, hkv=1), NOTSUP, "at most 8 query heads per KV head"),
     (dict(hq=16, hkv=5), BAD, "multiple"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(dq=96, dkv=96), BAD, "64, 128 or 256"),
@@ -333,9 +345,11 @@ def test_exact_rejects(lib, kw, code, needle):
 def test_batch_zero_is_a_noop(lib):
     # Nothing is launched and no pointer is needed for an empty batch.
     assert fwd(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
+    assert fwd_fast(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert fwd32(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert fwd_exact(lib, batch=0, q=None, k=None, v=None, o=None, cu=None) == 0
     assert uni(lib, batch=0, q=None, k=None, v=None, o=None) == 0
+    assert uni(lib, fast=True, batch=0, q=None, k=None, v=None, o=None) == 0
     assert strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None) == 0
     assert paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None) == 0
     assert splitkv(lib, batch=0, q=None, k=None, v=None, o=None, cu=None, ws=None) == 0
@@ -416,7 +430,10 @@ def test_header_is_plain_c():
            '      void* ws) {\n'
            '  int rc = fmha_decode_fwd(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
            '  rc |= fmha_decode_fwd_fp32_weights(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_fast(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_exact(s, q, k, v, o, cu, 1, 16, 16, 1, 128, 128, 0.088f);\n'
            '  rc |= fmha_decode_fwd_uniform(s, q, k, v, o, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'
+           '  rc |= fmha_decode_fwd_uniform_fast(s, q, k, v, o, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'
            '  rc |= fmha_decode_fwd_strided(s, q, k, v, o, cu, 16, 32768, 2048, 128, 1, 16, 16, 1, 128, 128,\n'
            '                                0.088f);\n'
            '  rc |= fmha_decode_fwd_paged(s, q, k, v, o, cu, 4, cu, 16, 1, 16, 16, 1, 128, 128, 0.088f);\n'

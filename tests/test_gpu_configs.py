@@ -4,11 +4,16 @@ At B=30720 the whole oracle run is too slow for a test, so each config is
 checked through size-independent properties plus the oracle on a seeded
 sample of batches:
   * every output is finite;
-  * the cu_seqlens path and the uniform path give identical bits;
-  * a seeded sample of batches (plus the first and last) passes the gate
-    against the oracle (the gate is documented in tests/common.py);
-  * the same sample lies within the bf16-weight bound of float64 truth,
-    with no tie slack (tests/common.py: f64_bound);
+  * the default entry points (fmha_decode_fwd_uniform, and fmha_decode_fwd
+    with a cu_seqlens array) give identical bits;
+  * on a seeded sample of batches (plus the first and last) they equal the
+    oracle's restated reference loop (fmha_host.cpp:179-244, grouped-query
+    head mapping, nearest-float exponentials: oracle.decode(p_mode=2)) bit
+    for bit, with no gate and no slack;
+  * the tree-order entry point (fmha_decode_fwd_uniform_fast) passes the
+    gate against the oracle on the same sample (the gate is documented in
+    tests/common.py), and both lie within the bf16-weight bound of float64
+    truth, with no tie slack (tests/common.py: f64_bound);
   * config 1 (S=1): the whole output equals fp16(V) bit for bit.
 """
 import numpy as np
@@ -47,11 +52,13 @@ def test_baseline_config(cfg):
     cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32, device=dev)
     o_c = fmha_amd.fmha_decode(q, k.view(B * S, Hkv, D), v.view(B * S, Hkv, D), cu_seqlens_kv=cu,
                                softmax_scale=scale)
+    o_f = fmha_amd.fmha_decode(q, k, v, seqlen_kv=S, softmax_scale=scale, fast=True)
     torch.cuda.synchronize()
-    assert bool(torch.isfinite(o_u).all())
+    assert bool(torch.isfinite(o_u).all()) and bool(torch.isfinite(o_f).all())
     assert torch.equal(o_u.view(torch.int16), o_c.view(torch.int16))
     if S == 1:
         assert torch.equal(o_u.view(B, Hq, D), v.view(B, Hkv, D).to(torch.float16))
+        assert torch.equal(o_f.view(B, Hq, D), v.view(B, Hkv, D).to(torch.float16))
     rng = np.random.default_rng(cfg)
     sample = np.unique(np.concatenate([[0, B - 1], rng.choice(B, size=192, replace=False)]))
     idx = torch.from_numpy(sample).to(dev)
@@ -59,12 +66,19 @@ def test_baseline_config(cfg):
     ks = _bits(k[idx].reshape(-1, Hkv, D))
     vs = _bits(v[idx].reshape(-1, Hkv, D))
     os_ = _bits(o_u.view(B, Hq, D)[idx])
+    of_ = _bits(o_f.view(B, Hq, D)[idx])
     cus = cu_from_seqlens(np.full(len(sample), S, np.int32))
+    r2, _ = oracle.decode(qs, ks, vs, cus, Hq, Hkv, D, scale, p_mode=2)
+    diff = int(np.count_nonzero(os_.reshape(r2.shape) != r2))
+    print(f"config {cfg}: sampled {len(sample)} batches, default entry points: {diff} of {r2.size} outputs "
+          f"differ from the restated loop", flush=True)
+    assert diff == 0, f"config {cfg}: {diff} outputs differ from oracle p_mode=2"
     r, slack = oracle.decode(qs, ks, vs, cus, Hq, Hkv, D, scale, with_slack=True)
-    st = oracle.compare(os_, r, slack)
-    print(f"config {cfg}: sampled {len(sample)} batches: {st}", flush=True)
-    assert_pass(st, f"config {cfg}")
+    st = oracle.compare(of_, r, slack)
+    print(f"config {cfg}: sampled {len(sample)} batches, fast entry point: {st}", flush=True)
+    assert_pass(st, f"config {cfg} (fast)")
     t, bound = f64_bound(qs, ks, vs, cus, Hq, Hkv, D, scale)
-    sf = f64_check(os_, t, bound)
-    print(f"config {cfg}: sampled batches against float64, no slack: {sf}", flush=True)
-    assert sf["f64_violations"] == 0, f"config {cfg}: outside the bf16-weight bound of float64: {sf}"
+    for name, o in (("default", os_), ("fast", of_)):
+        sf = f64_check(o, t, bound)
+        print(f"config {cfg}: {name} entry point against float64, no slack: {sf}", flush=True)
+        assert sf["f64_violations"] == 0, f"config {cfg} ({name}): outside the bf16-weight bound of float64: {sf}"

@@ -156,11 +156,12 @@ def test_graph_matrix_core_kernel_replays_match_eager(monkeypatch, kernel):
     outs = [torch.empty(48, 20, 128, dtype=torch.float16, device="cuda") for _ in range(3)]
     outs.append(torch.empty(40, 32, 64, dtype=torch.float16, device="cuda"))
 
+    # the tree-order entry points, whose kernel FMHA_DECODE_GQA_KERNEL selects
     def calls():
-        fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, out=outs[0])
-        fmha_amd.fmha_decode(qd, kb, vb, out=outs[1])
+        fmha_amd.fmha_decode(qd, kd, vd, cu_seqlens_kv=cud, out=outs[0], fast=True)
+        fmha_amd.fmha_decode(qd, kb, vb, out=outs[1], fast=True)
         fmha_amd.fmha_decode_strided(qd, kb, vb, out=outs[2])
-        fmha_amd.fmha_decode(qmd, kmd, vmd, cu_seqlens_kv=cumd, out=outs[3])
+        fmha_amd.fmha_decode(qmd, kmd, vmd, cu_seqlens_kv=cumd, out=outs[3], fast=True)
 
     calls()
     torch.cuda.synchronize()

@@ -19,8 +19,15 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import (assert_pass, check, cu_from_seqlens, default_scale, make_inputs,
-                          run_gpu)
+import functools
+
+from tests import common
+from tests.common import assert_pass, check, cu_from_seqlens, default_scale, make_inputs
+
+# FMHA_DECODE_GQA_KERNEL selects the kernel of the tree-order entry points
+# (fmha_decode_fwd_fast, fmha_decode_fwd_uniform_fast, fmha_decode_fwd_strided);
+# every call here goes through them.
+run_gpu = functools.partial(common.run_gpu, fast=True)
 
 pytestmark = pytest.mark.gpu
 

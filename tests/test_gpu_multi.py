@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import assert_pass, check, cu_from_seqlens, default_scale, make_inputs, run_gpu, to_dev
+from tests.common import (assert_pass, check, check_entry_points, cu_from_seqlens, default_scale, make_inputs,
+                          run_gpu, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -38,8 +39,7 @@ def test_varlen(D, Hkv, G):
     seqlens[1] = 0
     seqlens[2] = 16
     q, k, v, cu = make_inputs(B, Hkv * G, Hkv, D, seqlens, seed=2000 + D + Hkv + G)
-    o = run_gpu(q, k, v, cu, Hkv * G, Hkv, D)
-    assert_pass(check(o, q, k, v, cu, Hkv * G, Hkv, D), f"multi varlen D={D} Hkv={Hkv} G={G}")
+    check_entry_points(q, k, v, cu, Hkv * G, Hkv, D, ctx=f"multi varlen D={D} Hkv={Hkv} G={G}")
 
 
 @pytest.mark.parametrize("D,Hkv", SMALL_HKV)
@@ -48,8 +48,7 @@ def test_uniform(D, Hkv, S):
     B, G = 37, 4
     seqlens = np.full(B, S, np.int32)
     q, k, v, cu = make_inputs(B, Hkv * G, Hkv, D, seqlens, seed=2100 + D + S)
-    o = run_gpu(q, k, v, cu, Hkv * G, Hkv, D, uniform_s=S)
-    assert_pass(check(o, q, k, v, cu, Hkv * G, Hkv, D), f"multi uniform D={D} Hkv={Hkv} S={S}")
+    check_entry_points(q, k, v, cu, Hkv * G, Hkv, D, uniform_s=S, ctx=f"multi uniform D={D} Hkv={Hkv} S={S}")
 
 
 @pytest.mark.parametrize("D,Hkv", [(64, 1), (128, 2), (256, 1)])

@@ -11,18 +11,19 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import (assert_pass, check, cu_from_seqlens, default_scale, make_inputs,
-                          run_gpu)
+from tests.common import (assert_exact, assert_pass, check, check_entry_points, cu_from_seqlens, default_scale,
+                          make_inputs, run_gpu)
 
 pytestmark = pytest.mark.gpu
 
 
 def _case(B, Hq, Hkv, D, seqlens, seed, std=1.0, uniform=False):
+    """Default entry point bit for bit against the restated loop, _fast entry
+    point through the gate (tests/common.py: check_entry_points)."""
     q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed, std)
-    o = run_gpu(q, k, v, cu, Hq, Hkv, D, uniform_s=(int(seqlens[0]) if uniform else None))
-    st = check(o, q, k, v, cu, Hq, Hkv, D)
-    assert_pass(st, f"B={B} Hq={Hq} Hkv={Hkv} D={D} seed={seed}")
-    return o, (q, k, v, cu), st
+    o = check_entry_points(q, k, v, cu, Hq, Hkv, D, uniform_s=(int(seqlens[0]) if uniform else None),
+                           ctx=f"B={B} Hq={Hq} Hkv={Hkv} D={D} seed={seed}")
+    return o, (q, k, v, cu)
 
 
 def test_reference_smoke_config():
@@ -95,15 +96,24 @@ def test_poisoned_neighbours():
     assert np.array_equal(o[1], o_alone.reshape(H, D))
 
 
-def test_gqa_equals_mha_on_repeated_kv():
-    """Grouped heads give the MHA result on head-repeated K/V (within the gate;
-    the kernel reduces in a different order for the two group sizes)."""
-    B, Hq, Hkv, D = 24, 32, 16, 128
+@pytest.mark.parametrize("G", [2, 3, 4, 8])
+def test_gqa_equals_mha_on_repeated_kv(G):
+    """Grouped heads give the MHA result on head-repeated K/V: bit for bit
+    through fmha_decode_fwd_exact (its arithmetic does not depend on the
+    group size; for G = 2 also through the default entry point, which takes
+    those numerics there), within the gate through the _fast one (which
+    reduces in a different order for the two group sizes)."""
+    B, Hkv, D = 24, 16 if G <= 4 else 8, 128
+    Hq = G * Hkv
     seqlens = oracle.generate_seqlens(B, 16)
-    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=700)
-    o_gqa = run_gpu(q, k, v, cu, Hq, Hkv, D)
-    kr, vr = np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1)
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=700 + G)
+    kr, vr = np.repeat(k, G, axis=1), np.repeat(v, G, axis=1)
     o_mha = run_gpu(q, kr, vr, cu, Hq, Hq, D)
+    assert np.array_equal(run_gpu(q, k, v, cu, Hq, Hkv, D, exact=True), o_mha)
+    if G <= 2:
+        assert np.array_equal(run_gpu(q, k, v, cu, Hq, Hkv, D), o_mha)
+    o_gqa = run_gpu(q, k, v, cu, Hq, Hkv, D, fast=True)
+    o_mha = run_gpu(q, kr, vr, cu, Hq, Hq, D, fast=True)
     r, slack = oracle.decode(q, kr, vr, cu, Hq, Hq, D, default_scale(D), with_slack=True)
     assert_pass(oracle.compare(o_gqa, o_mha, slack), "gqa vs mha")
     assert_pass(oracle.compare(o_gqa, r, slack), "gqa vs oracle")
@@ -129,4 +139,6 @@ def test_custom_scale():
     q, k, v, cu = make_inputs(16, 8, 8, 128, seqlens, seed=900)
     for scale in (0.0, 0.03125, 0.5):
         o = run_gpu(q, k, v, cu, 8, 8, 128, scale=scale)
-        assert_pass(check(o, q, k, v, cu, 8, 8, 128, scale=scale), f"scale={scale}")
+        assert_exact(o, q, k, v, cu, 8, 8, 128, f"scale={scale}", scale=scale)
+        o = run_gpu(q, k, v, cu, 8, 8, 128, scale=scale, fast=True)
+        assert_pass(check(o, q, k, v, cu, 8, 8, 128, scale=scale), f"scale={scale} (fast)")
