@@ -8,7 +8,7 @@ from .decode import (MAX_SEQLEN_KV, NOALLOC_SCRATCH_BYTES, FmhaDecodeError, fmha
                      launch_fmha_decode_fast, launch_fmha_decode_uniform_fast,
                      launch_fmha_decode_fp32_weights, launch_fmha_decode_paged,
                      launch_fmha_decode_splitkv, launch_fmha_decode_splitkv_paged, launch_fmha_decode_splitkv_strided,
-                     launch_fmha_decode_strided, launch_fmha_decode_uniform, splitkv_workspace_size)
+                     launch_fmha_decode_strided, launch_fmha_decode_uniform, last_plan, splitkv_workspace_size)
 from ._lib import LIB_PATH, EXPORTED
 
 __all__ = [
@@ -31,6 +31,7 @@ __all__ = [
     "launch_fmha_decode_fast",
     "launch_fmha_decode_uniform_fast",
     "launch_fmha_decode_uniform",
+    "last_plan",
     "LIB_PATH",
     "EXPORTED",
 ]

@@ -29,6 +29,7 @@ EXPORTED = (
     "fmha_decode_fwd_splitkv_paged",
     "fmha_decode_error_string",
     "fmha_decode_last_error_detail",
+    "fmha_decode_last_plan",
     "fmha_decode_version",
 )
 
@@ -80,6 +81,8 @@ def load():
     lib.fmha_decode_error_string.argtypes = [ctypes.c_int]
     lib.fmha_decode_last_error_detail.restype = ctypes.c_char_p
     lib.fmha_decode_last_error_detail.argtypes = []
+    lib.fmha_decode_last_plan.restype = ctypes.c_char_p
+    lib.fmha_decode_last_plan.argtypes = []
     lib.fmha_decode_version.restype = ctypes.c_int
     lib.fmha_decode_version.argtypes = []
     _lib = lib

@@ -20,6 +20,28 @@
 #include "fmha_decode.h"
 #include "fmha_decode_launch.hpp"
 
+namespace fmha_decode {
+namespace host {
+namespace {
+// The launches of this thread's most recent entry-point call.
+thread_local char g_plan[1024] = "";
+}  // namespace
+
+void plan_note(const char* fmt, ...) {
+  size_t n = std::strlen(g_plan);
+  if (n > 0 && n + 2 < sizeof(g_plan)) {
+    std::memcpy(g_plan + n, "; ", 3);
+    n += 2;
+  }
+  if (n + 1 >= sizeof(g_plan)) return;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_plan + n, sizeof(g_plan) - n, fmt, ap);
+  va_end(ap);
+}
+}  // namespace host
+}  // namespace fmha_decode
+
 namespace {
 
 // Launchers and their instantiations: fmha_decode_launch.hpp,
@@ -27,6 +49,12 @@ namespace {
 using namespace fmha_decode::host;
 
 thread_local char g_detail[256] = "";
+
+// Start of an entry-point call: no rejection detail, no launch yet.
+void begin_call() {
+  g_detail[0] = '\0';
+  fmha_decode::host::g_plan[0] = '\0';
+}
 
 int reject(int code, const char* fmt, ...) {
   va_list ap;
@@ -666,7 +694,7 @@ Numerics default_numerics(int g) { return g <= 2 ? Numerics::kExact : Numerics::
 int fwd_cu(void* stream, const void* Q, const void* K, const void* V, void* O, const int32_t* cu_seqlens_kv,
            int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
            int32_t head_dim_kv, float softmax_scale, Numerics numerics, bool exact_only) {
-  g_detail[0] = '\0';
+  begin_call();
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
@@ -692,7 +720,7 @@ int fwd_cu(void* stream, const void* Q, const void* K, const void* V, void* O, c
 int fwd_uniform(void* stream, const void* Q, const void* K, const void* V, void* O, int32_t seqlen_kv,
                 int32_t batch, int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
                 int32_t head_dim_kv, float softmax_scale, Numerics numerics) {
-  g_detail[0] = '\0';
+  begin_call();
   if (seqlen_kv < 0 || seqlen_kv > FMHA_DECODE_MAX_SEQLEN_KV)
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE, "seqlen_kv must lie in [0, %d] (got %d)",
                   FMHA_DECODE_MAX_SEQLEN_KV, seqlen_kv);
@@ -767,7 +795,7 @@ extern "C" int fmha_decode_fwd_strided(void* stream, const void* Q, const void* 
                                        int64_t kv_row_stride, int64_t kv_head_stride, int32_t batch,
                                        int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
                                        int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
-  g_detail[0] = '\0';
+  begin_call();
   if (seqlen_kv < 0 || (!seqlens_kv && seqlen_kv > FMHA_DECODE_MAX_SEQLEN_KV))
     return reject(FMHA_DECODE_ERROR_INVALID_VALUE,
                   "seqlen_kv must be >= 0, and <= %d when seqlens_kv is null (got %d)", FMHA_DECODE_MAX_SEQLEN_KV,
@@ -862,7 +890,7 @@ extern "C" int fmha_decode_fwd_paged(void* stream, const void* Q, const void* K_
                                      const int32_t* seqlens_kv, int32_t page_size, int32_t batch,
                                      int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
                                      int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
-  g_detail[0] = '\0';
+  begin_call();
   int rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
                         num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
@@ -1176,7 +1204,7 @@ extern "C" int fmha_decode_fwd_splitkv(void* stream, const void* Q, const void* 
                                        int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
                                        int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale,
                                        void* workspace, size_t workspace_bytes) {
-  g_detail[0] = '\0';
+  begin_call();
   return splitkv_packed(stream, Q, K, V, O, cu_seqlens_kv, max_seqlen_kv, batch, num_heads_q, num_heads_kv,
                         seqlen_q, head_dim_q, head_dim_kv, softmax_scale, workspace, workspace_bytes, true);
 }
@@ -1185,7 +1213,7 @@ extern "C" int fmha_decode_fwd_splitkv_noalloc(void* stream, const void* Q, cons
                                                const int32_t* cu_seqlens_kv, int32_t max_seqlen_kv, int32_t batch,
                                                int32_t num_heads_q, int32_t num_heads_kv, int32_t seqlen_q,
                                                int32_t head_dim_q, int32_t head_dim_kv, float softmax_scale) {
-  g_detail[0] = '\0';
+  begin_call();
   int rc = check_common(Q, K, V, O, batch, num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv,
                         softmax_scale, false);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
@@ -1213,7 +1241,7 @@ extern "C" int fmha_decode_fwd_splitkv_strided(void* stream, const void* Q, cons
                                                int32_t num_heads_kv, int32_t seqlen_q, int32_t head_dim_q,
                                                int32_t head_dim_kv, float softmax_scale, void* workspace,
                                                size_t workspace_bytes) {
-  g_detail[0] = '\0';
+  begin_call();
   int rc = split_check_workspace_args(max_seqlen_kv);
   if (rc != FMHA_DECODE_SUCCESS) return rc;
   if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV)
@@ -1256,7 +1284,7 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
                                              int32_t batch, int32_t num_heads_q, int32_t num_heads_kv,
                                              int32_t seqlen_q, int32_t head_dim_q, int32_t head_dim_kv,
                                              float softmax_scale, void* workspace, size_t workspace_bytes) {
-  g_detail[0] = '\0';
+  begin_call();
   int rc = split_check_workspace_args(max_seqlen_kv);
   if (rc != FMHA_DECODE_SUCCESS) return rc;
   rc = paged_checks(Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size, batch,
@@ -1299,5 +1327,7 @@ extern "C" const char* fmha_decode_error_string(int code) {
 }
 
 extern "C" const char* fmha_decode_last_error_detail(void) { return g_detail; }
+
+extern "C" const char* fmha_decode_last_plan(void) { return fmha_decode::host::g_plan; }
 
 extern "C" int fmha_decode_version(void) { return 100; }

@@ -65,6 +65,7 @@ void launch_split_combine(const SplitArgs& a, int d, hipStream_t stream) {
 
 hipError_t launch_pad_query_group(const uint16_t* q, uint16_t* qp, uint64_t streams, int G, int GP, int D,
                                   hipStream_t stream) {
+  plan_note("pad_query_group(G=%d to %d)", G, GP);
   const uint64_t chunks = streams * (uint64_t)GP * (uint64_t)(D / 8);
   hipLaunchKernelGGL(pad_query_group_kernel, dim3((uint32_t)((chunks + kPadThreads - 1) / kPadThreads)),
                      dim3(kPadThreads), 0, stream, q, qp, streams, G, 0, G, GP, D);

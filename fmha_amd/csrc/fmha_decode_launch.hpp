@@ -29,6 +29,23 @@ using fmha_decode::kBlockThreads;
 using fmha_decode::kWaveSize;
 using fmha_decode::kWavesPerBlock;
 
+// Appends one launch of the current entry-point call to the calling
+// thread's plan text (fmha_decode_last_plan): printf-style, launches
+// separated by "; ".  Defined in fmha_decode_api.hip.
+void plan_note(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Names of the K/V layouts in plan text.
+inline const char* layout_name(int layout) {
+  switch (layout) {
+    case fmha_decode::kLayoutPacked: return "packed";
+    case fmha_decode::kLayoutStrided: return "strided";
+    case fmha_decode::kLayoutPaged: return "paged";
+    case fmha_decode::kLayoutPagedLanes: return "paged_lanes";
+    case fmha_decode::kLayoutPagedBlock: return "paged16";
+    default: return "paged16_lanes";
+  }
+}
+
 // Concurrency cap.  Each wave issues all of its loads at once, and MI355X
 // streams fastest with a bounded amount of them in flight per CU: measured
 // sweeps put the best at about 80 KiB for units of 10-36 KiB (3 waves of the
@@ -88,6 +105,9 @@ size_t lds_reserve_kernel(int waves) {
 template <int D, int G, int LAYOUT, int SB, bool PF32, bool EXACT = false>
 hipError_t launch_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
   constexpr auto kernel = fmha_decode::fmha_decode_fwd_kernel<D, G, LAYOUT, SB, PF32, EXACT>;
+  plan_note("short(numerics=%s D=%d G=%d layout=%s bucket=%s%d waves_per_cu=%d)",
+            EXACT ? "exact" : PF32 ? "fp32_weights" : "fast", D, G, layout_name(LAYOUT), SB == 0 ? "per_wave<=" : "",
+            SB == 0 ? 16 : SB, waves_per_cu);
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
@@ -135,6 +155,9 @@ hipError_t launch_dim(const DecodeArgs& a, int d, int g, int sb, int w, hipStrea
 template <int D, int G, int LAYOUT, bool PF32, bool EXACT = false>
 hipError_t launch_multi_one(const DecodeArgs& a, int waves_per_cu, hipStream_t stream) {
   constexpr auto kernel = fmha_decode::fmha_decode_multi_kernel<D, G, LAYOUT, PF32, EXACT>;
+  plan_note("short_multi(numerics=%s D=%d G=%d layout=%s batches_per_wave=%d waves_per_cu=%d)",
+            EXACT ? "exact" : PF32 ? "fp32_weights" : "fast", D, G, layout_name(LAYOUT), 1 << a.sub_shift,
+            waves_per_cu);
   const uint32_t blocks = (a.total_units + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, a);
   return hipGetLastError();
@@ -177,6 +200,8 @@ hipError_t launch_exact(const DecodeArgs& a, bool multi, int sb, int w, hipStrea
 template <int D, int NS, int LAYOUT>
 hipError_t launch_mfma_one(const fmha_decode::GroupArgs& g, int waves_per_cu, hipStream_t stream) {
   constexpr auto kernel = fmha_decode::fmha_decode_group_kernel<D, 0, NS, LAYOUT>;
+  plan_note("short_matrix_core(D=%d G=%d layout=%s streams_per_tile=%d waves_per_cu=%d)", D, (int)g.group,
+            layout_name(LAYOUT), NS, waves_per_cu);
   hipLaunchKernelGGL(kernel, dim3(g.waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(waves_per_cu), stream, g);
   return hipGetLastError();
 }
@@ -264,6 +289,8 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   const int waves = LAYOUT == fmha_decode::kLayoutPaged && G <= 2 ? kOnepassWavesPerCUPagedRows
                     : !MULTI && G <= 2 && a.nblk <= 3     ? kOnepassWavesPerCUNarrow
                                                           : kOnepassWavesPerCU;
+  plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=%d blocks=%d waves_per_cu=%d)", D, G, layout_name(LAYOUT),
+            1 << a.sub_shift, a.nblk, waves);
   // 16-row pages, eight query heads per KV head, rows of up to four blocks:
   // the kernel scheduled for two waves per SIMD.
   if constexpr (!MULTI && G == 8 && LAYOUT == fmha_decode::kLayoutPagedBlock)
@@ -378,6 +405,8 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
   const uint32_t upb = (uint32_t)as.units_per_batch;
   const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + (1 << shift) - 1) >> shift) * upb;
   const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)((a.nchunks + (1 << shift) - 1) >> shift) * upb;
+  plan_note("split(D=%d G=%d layout=%s sub_units=%d blocks=%d chunk_rows=%d chunks=%d passes=%d)", D, G,
+            layout_name(LAYOUT), 1 << shift, a.nblk, a.chunk_rows, a.nchunks, a.nchunks == 1 ? 3 : 4);
   {
     constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
@@ -438,6 +467,8 @@ hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
   if (score_waves > INT32_MAX || pv_waves > INT32_MAX ||
       (uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX)
     return hipErrorInvalidValue;
+  plan_note("split_matrix_core(D=%d G=%d layout=%s blocks=%d chunk_rows=%d chunks=%d passes=%d)", D, (int)g,
+            layout_name(LAYOUT), a.nblk, a.chunk_rows, a.nchunks, a.nchunks == 1 ? 3 : 4);
   {
     constexpr auto kernel = fmha_decode::splitkv_scores_group_kernel<D, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),

@@ -5,9 +5,9 @@
 // Serving engines pad block tables with negative entries (-1).  A kernel that
 // turns such an entry into an address reads far outside the cache, so every
 // paged loader in this library forms a row's address only through
-// paged_row_elem, which refuses a negative entry, and treats a batch whose
-// rows use one as invalid: its outputs are NaN, and the unmapped rows are
-// never read.  Entries at or above the cache's page count are outside what
+// paged_row_elem, which refuses a negative entry, or its 32-bit-factor form
+// paged_row_u32, and treats a batch whose rows use one as invalid: its
+// outputs are NaN, and the unmapped rows are never read.  Entries at or above the cache's page count are outside what
 // the library can check (the C ABI does not carry the page count).
 //
 // Plain integer arithmetic, compiled for the device by the kernels and for
@@ -31,6 +31,26 @@ FMHA_DECODE_HD int64_t paged_row_elem(int32_t entry, uint32_t row, uint32_t page
   if (entry < 0) return -1;
   const uint64_t slot = (uint64_t)(row & ((1u << page_shift) - 1u));
   return (int64_t)((uint64_t)entry * page_stride + slot * row_elems);
+}
+
+// paged_row_elem in unsigned 32-bit factors, for loaders that keep the
+// arithmetic on scalar or 32-bit registers (the signed 64-bit form cost the
+// single pass about 90 VGPRs): the page (0 for a negative entry) and slot of
+// row `row`, and whether the entry is unmapped.  When it is not,
+// page * page_stride + slot * row_elems is paged_row_elem's offset; when it
+// is, the caller must read nothing for the row.
+struct PagedRowU32 {
+  uint32_t page;
+  uint32_t slot;
+  bool unmapped;
+};
+
+FMHA_DECODE_HD PagedRowU32 paged_row_u32(int32_t entry, uint32_t row, uint32_t page_shift) {
+  PagedRowU32 p;
+  p.unmapped = entry < 0;
+  p.page = p.unmapped ? 0u : (uint32_t)entry;
+  p.slot = row & ((1u << page_shift) - 1u);
+  return p;
 }
 
 // Block-table entries rows [0, S) of a batch use: ceil(S / page_size).

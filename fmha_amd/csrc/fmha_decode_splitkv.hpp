@@ -254,15 +254,13 @@ struct LongRows {
   // empty range too, nothing is read, and `bad` is set when rows > 0.
   __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(int row, int rows) {
     const int32_t entry = load_uniform_i32(pages, (uint32_t)row >> page_shift);
-    // paged_row_elem's arithmetic in unsigned 32-bit factors (a negative
-    // entry as page 0 with an empty range), which keeps it on the scalar
-    // unit: the signed 64-bit form cost the single pass about 90 VGPRs.
-    const bool neg = entry < 0;
-    const uint32_t page = neg ? 0u : (uint32_t)entry;
-    const uint32_t slot = (uint32_t)row & ((1u << page_shift) - 1u);
-    bad |= __builtin_amdgcn_readfirstlane(rows > 0 && neg ? 1 : 0);
-    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(neg ? 0 : rows * (int)row_bytes);
-    return make_rsrc(uniform_ptr(base + (uint64_t)page * page_stride + (uint64_t)slot * (row_bytes >> 1)), range);
+    // The scalar unit's form of the guard (a negative entry as page 0 with
+    // an empty range).
+    const PagedRowU32 pr = paged_row_u32(entry, (uint32_t)row, page_shift);
+    bad |= __builtin_amdgcn_readfirstlane(rows > 0 && pr.unmapped ? 1 : 0);
+    const uint32_t range = (uint32_t)__builtin_amdgcn_readfirstlane(pr.unmapped ? 0 : rows * (int)row_bytes);
+    return make_rsrc(uniform_ptr(base + (uint64_t)pr.page * page_stride + (uint64_t)pr.slot * (row_bytes >> 1)),
+                     range);
   }
 
   template <int NR>
@@ -370,32 +368,27 @@ struct PagedLaneRows {
     const int row0 = rel0 + lane_rows;
     u32x4 v[NR];
     bool unmapped[NR];
-    // paged_row_elem's guard in unsigned factors (a negative entry as page 0,
-    // never read): the signed 64-bit form cost registers.
-    const uint32_t slot_mask = (1u << page_shift) - 1u;
+    // The guard in unsigned factors (paged_row_u32: a negative entry as
+    // page 0, never read): the signed 64-bit form cost registers.
     if constexpr (BLOCK) {
       const bool any = row0 < lane_n;
-      const uint32_t abs0 = (uint32_t)(lo + row0);
-      const bool neg = e[0] < 0;
-      const uint64_t el =
-          (uint64_t)(neg ? 0u : (uint32_t)e[0]) * page_stride + (uint64_t)(abs0 & slot_mask) * row_elems;
+      const PagedRowU32 pr = paged_row_u32(e[0], (uint32_t)(lo + row0), page_shift);
+      const uint64_t el = (uint64_t)pr.page * page_stride + (uint64_t)pr.slot * row_elems;
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        const bool ok = !neg && row0 + j < lane_n;
+        const bool ok = !pr.unmapped && row0 + j < lane_n;
         v[j] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(ok ? base + el + (uint64_t)j * row_elems : safe));
-        unmapped[j] = any && neg;
+        unmapped[j] = any && pr.unmapped;
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         const bool ok = row0 + j < lane_n;
-        const uint32_t abs = (uint32_t)(lo + row0 + j);
-        const bool neg = e[j] < 0;
-        const uint64_t el =
-            (uint64_t)(neg ? 0u : (uint32_t)e[j]) * page_stride + (uint64_t)(abs & slot_mask) * row_elems;
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ok && !neg ? base + el : safe));
-        unmapped[j] = ok && neg;
+        const PagedRowU32 pr = paged_row_u32(e[j], (uint32_t)(lo + row0 + j), page_shift);
+        const uint64_t el = (uint64_t)pr.page * page_stride + (uint64_t)pr.slot * row_elems;
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ok && !pr.unmapped ? base + el : safe));
+        unmapped[j] = ok && pr.unmapped;
       }
     }
 #pragma unroll

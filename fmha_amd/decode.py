@@ -31,6 +31,14 @@ class FmhaDecodeError(RuntimeError):
         self.detail = detail
 
 
+def last_plan():
+    """The kernels the most recent call on this thread launched, as the
+    library describes them (fmha_decode_last_plan): a list of strings such
+    as "split(D=128 G=4 layout=packed sub_units=1 blocks=64 ...)"."""
+    text = _lib.load().fmha_decode_last_plan().decode()
+    return [p for p in text.split("; ") if p]
+
+
 def _raise_if(rc):
     if rc != 0:
         lib = _lib.load()

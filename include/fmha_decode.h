@@ -29,8 +29,10 @@
  *
  * All pointers are device pointers owned by the caller.  Calls are
  * asynchronous on the given stream (a hipStream_t passed as void*, NULL for
- * the null stream) and may be issued from any number of host threads.  They
- * allocate no device memory.  The one piece of library state: the entry
+ * the null stream) and may be issued from any number of host threads, with
+ * one exception: fmha_decode_fwd_splitkv_noalloc uses one workspace array per
+ * GPU, so its calls on one GPU must be ordered (one stream, or synchronised)
+ * or they corrupt each other's results.  They allocate no device memory.  The one piece of library state: the entry
  * points that read lengths from a device cu_seqlens_kv array
  * (fmha_decode_fwd, its _fast, _fp32_weights and _exact forms, and
  * fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
@@ -378,6 +380,17 @@ const char* fmha_decode_error_string(int code);
 /* Text describing why the most recent call on this host thread was rejected
  * ("" after a successful call). */
 const char* fmha_decode_last_error_detail(void);
+
+/* The kernels the most recent call on this host thread launched, in order,
+ * separated by "; " ("" after a rejected or empty call): each a kernel
+ * kind with the choices the library made for it, e.g.
+ *   "short(numerics=exact D=128 G=1 layout=packed bucket=16 waves_per_cu=4)"
+ *   "split(D=128 G=4 layout=packed sub_units=1 blocks=64 chunk_rows=256
+ *    chunks=4 passes=4)".
+ * Kinds: short, short_multi (several batches per wave), short_matrix_core,
+ * onepass, split, split_matrix_core, pad_query_group.  For tests and
+ * diagnostics; no counterpart in the reference. */
+const char* fmha_decode_last_plan(void);
 
 /* Library version, encoded as major*10000 + minor*100 + patch. */
 int fmha_decode_version(void);

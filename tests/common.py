@@ -90,6 +90,35 @@ def run_gpu(q, k, v, cu, Hq, Hkv, D, scale=None, uniform_s=None, device="cuda", 
     return o.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def last_plan():
+    """The launches of the most recent library call on this thread, as the
+    library reports them (fmha_decode_last_plan): [(kind, {key: int or
+    str})], e.g. ("onepass", {"D": 128, "G": 8, "layout": "paged16_lanes",
+    ...})."""
+    import fmha_amd
+    out = []
+    for entry in fmha_amd.last_plan():
+        kind, _, rest = entry.partition("(")
+        fields = {}
+        for kv in rest.rstrip(")").split():
+            key, _, val = kv.partition("=")
+            fields[key] = int(val) if val.lstrip("-").isdigit() else val
+        out.append((kind, fields))
+    return out
+
+
+def plan_kinds():
+    """The kernel kinds of the most recent call, in launch order."""
+    return [k for k, _ in last_plan()]
+
+
+def plan_launch(kind):
+    """The fields of the one launch of this kind in the most recent call."""
+    found = [f for k, f in last_plan() if k == kind]
+    assert len(found) == 1, f"expected one {kind} launch, plan: {last_plan()}"
+    return found[0]
+
+
 def check(o, q, k, v, cu, Hq, Hkv, D, scale=None):
     """Compare GPU output bits with the oracle; returns the stats dict."""
     scale = default_scale(D) if scale is None else scale

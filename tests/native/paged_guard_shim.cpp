@@ -14,4 +14,12 @@ int64_t guard_row_elem(int32_t entry, uint32_t row, uint32_t page_shift, uint64_
 
 int guard_entries_used(int S, uint32_t page_shift) { return fmha_decode::paged_entries_used(S, page_shift); }
 
+// paged_row_u32's offset as the loaders form it (page * page_stride + slot *
+// row_elems), or -1 for an unmapped entry.
+int64_t guard_row_u32(int32_t entry, uint32_t row, uint32_t page_shift, uint64_t page_stride, uint64_t row_elems) {
+  const fmha_decode::PagedRowU32 p = fmha_decode::paged_row_u32(entry, row, page_shift);
+  if (p.unmapped) return -1;
+  return (int64_t)((uint64_t)p.page * page_stride + (uint64_t)p.slot * row_elems);
+}
+
 }  // extern "C"

@@ -39,7 +39,7 @@ def test_exports_every_declared_function(lib):
                           "fmha_decode_fwd_splitkv", "fmha_decode_fwd_splitkv_noalloc",
                           "fmha_decode_fwd_splitkv_strided",
                           "fmha_decode_fwd_splitkv_paged", "fmha_decode_error_string",
-                          "fmha_decode_last_error_detail", "fmha_decode_version"}
+                          "fmha_decode_last_error_detail", "fmha_decode_last_plan", "fmha_decode_version"}
     from fmha_amd import _lib
     assert set(names) == set(_lib.EXPORTED)
     for n in names:
@@ -356,6 +356,12 @@ def test_batch_zero_is_a_noop(lib):
     assert splitkv_strided(lib, batch=0, q=None, k=None, v=None, o=None, lens=None, ws=None) == 0
     assert splitkv_paged(lib, batch=0, q=None, k=None, v=None, o=None, bt=None, lens=None, ws=None) == 0
     assert lib.fmha_decode_last_error_detail() == b""
+    assert lib.fmha_decode_last_plan() == b""
+
+
+def test_rejected_call_has_no_plan(lib):
+    assert fwd(lib, sq=2) == BAD
+    assert lib.fmha_decode_last_plan() == b""
 
 
 def test_python_wrapper_raises(lib):
@@ -445,6 +451,7 @@ def test_header_is_plain_c():
            '                                      0.088f, ws, n);\n'
            '  const char* t = fmha_decode_error_string(rc);\n'
            '  const char* d = fmha_decode_last_error_detail();\n'
+           '  d = fmha_decode_last_plan();\n'
            '  return rc + fmha_decode_version() + (t == d);\n}\n')
     with tempfile.TemporaryDirectory() as d:
         p = os.path.join(d, "t.c")

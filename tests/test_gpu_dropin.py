@@ -3,7 +3,9 @@ this library (oracle/_ref/fmha_dropin, built by oracle/Makefile from
 /root/reference/fmha_host.cpp and oracle/dropin_main.cpp): the reference's
 benchmark loop and its own CPU validation (fmha_host.cpp:434-445) run on this
 library's kernel and must report success.  Its configs 0..3
-(fmha_host.cpp:511-516) are MHA, where its CPU loop's indexing is valid."""
+(fmha_host.cpp:511-516: B=10 and 30720, H=16 and 32, D=128 and 256, its
+Poisson(4) lengths) are MHA, where its CPU loop's indexing is valid; config 3
+(B=30720, H=32, D=128) is the largest the CLI takes (fmha_host.cpp:485)."""
 import os
 import re
 import subprocess
@@ -20,7 +22,7 @@ pytestmark = [pytest.mark.gpu,
                                  reason="oracle/_ref/fmha_dropin not built (reference not mounted at build time)")]
 
 
-@pytest.mark.parametrize("config", [0, 1, 2])
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
 def test_reference_host_validates_this_kernel(config):
     r = subprocess.run([BIN, str(config)], capture_output=True, text=True, timeout=240)
     out = r.stdout

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import assert_pass, cu_from_seqlens, default_scale
+from tests.common import assert_pass, cu_from_seqlens, default_scale, last_plan
 
 pytestmark = pytest.mark.gpu
 
@@ -239,25 +239,33 @@ def test_tensors_on_another_device_are_rejected_before_launch():
     torch.cuda.synchronize()
 
 
-# (max_seqlen_kv or None for the short kernel, page_size, D, Hq, Hkv, B): the
+# (max_seqlen_kv or None for the short kernel, page_size, D, Hq, Hkv, B,
+# (kind, layout) of the call's last launch as the library reports it): the
 # short kernel one batch per wave (16 KV heads) and several batches per wave
 # (1 and 2 KV heads); beyond 16 rows the single pass (>= 512 waves), the
 # split passes over one page per wave (page size 16) and per-lane pages
 # (few KV heads, page sizes 4 and 16), and the matrix-core split passes
-# (G = 16, 12).
+# (G = 16, 12, and groups of 4-8 on pages under 16 rows at D >= 128).
 NEG_CASES = [
-    (None, 4, 128, 16, 16, 23), (None, 1, 128, 8, 1, 37), (None, 16, 128, 16, 2, 37), (None, 8, 256, 4, 1, 19),
-    (40, 16, 128, 8, 4, 600), (70, 16, 128, 16, 16, 9), (70, 4, 128, 16, 2, 9), (70, 16, 128, 8, 2, 9),
-    (70, 4, 64, 16, 1, 9),
-    (100, 16, 128, 24, 2, 7), (100, 4, 256, 24, 2, 7),
-    # one or two 16-row blocks with few KV heads and >= 512 waves: the single
-    # pass with per-lane page lookups
-    (32, 16, 128, 8, 1, 2100), (24, 4, 128, 16, 2, 1100), (32, 1, 64, 8, 1, 4200), (32, 8, 256, 4, 1, 1100),
+    (None, 4, 128, 16, 16, 23, ("short", "paged")), (None, 1, 128, 8, 1, 37, ("short_multi", "paged")),
+    (None, 16, 128, 16, 2, 37, ("short_multi", "paged")), (None, 8, 256, 4, 1, 19, ("short_multi", "paged")),
+    (40, 16, 128, 8, 4, 600, ("onepass", "paged16")), (70, 16, 128, 16, 16, 9, ("split", "paged16")),
+    (70, 4, 128, 16, 2, 9, ("split_matrix_core", "paged")), (70, 16, 128, 8, 2, 9, ("split", "paged16_lanes")),
+    (70, 4, 64, 16, 1, 9, ("split_matrix_core", "paged")),
+    (100, 16, 128, 24, 2, 7, ("split_matrix_core", "paged16")), (100, 4, 256, 24, 2, 7, ("split_matrix_core", "paged")),
+    (24, 4, 128, 16, 2, 1100, ("split_matrix_core", "paged")), (32, 8, 256, 4, 1, 1100, ("split_matrix_core", "paged")),
+    # >= 512 waves with few KV heads: the single pass with per-lane page
+    # lookups, several batches per wave: groups of 8 on rows of two blocks
+    # (16-row pages at D = 128, one-row pages at D = 64) and of four (16-row
+    # pages at D = 64), groups of up to 4 on rows of three to eight blocks
+    (32, 16, 128, 8, 1, 2100, ("onepass", "paged16_lanes")), (32, 1, 64, 8, 1, 4200, ("onepass", "paged_lanes")),
+    (64, 16, 64, 8, 1, 4200, ("onepass", "paged16_lanes")), (48, 16, 128, 4, 1, 2100, ("onepass", "paged16_lanes")),
+    (128, 1, 64, 2, 1, 4200, ("onepass", "paged_lanes")), (128, 4, 128, 8, 2, 1100, ("onepass", "paged_lanes")),
 ]
 
 
-@pytest.mark.parametrize("max_s,page_size,D,Hq,Hkv,B", NEG_CASES)
-def test_paged_negative_entries_give_nan(max_s, page_size, D, Hq, Hkv, B):
+@pytest.mark.parametrize("max_s,page_size,D,Hq,Hkv,B,route", NEG_CASES)
+def test_paged_negative_entries_give_nan(max_s, page_size, D, Hq, Hkv, B, route):
     """A negative block-table entry (serving engines pad with -1) for a row a
     batch has: that batch's outputs are NaN and its unmapped pages are never
     read; every other batch keeps its exact bits.  -1 entries past a
@@ -292,6 +300,8 @@ def test_paged_negative_entries_give_nan(max_s, page_size, D, Hq, Hkv, B):
         return o
 
     o = run(bt)
+    kind, fields = last_plan()[-1]
+    assert (kind, fields["layout"]) == route, last_plan()
     assert bool(torch.isfinite(o.float()).all())
     poisoned = sorted(set(rng.choice(B, size=max(1, B // 4), replace=False).tolist()) | {0})
     bad = bt.copy()

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import assert_pass, cu_from_seqlens, default_scale, make_inputs, to_dev
+from tests.common import assert_pass, cu_from_seqlens, default_scale, last_plan, make_inputs, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -346,6 +346,40 @@ def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged ps={page_size} D={D} {Hq}/{Hkv} B={B}")
 
 
+def _route():
+    """(kind, layout) of the last launch of the most recent call."""
+    kind, fields = last_plan()[-1]
+    return kind, fields["layout"]
+
+
+# The route each paged single-pass case takes, by (D, Hq, Hkv, max_len):
+# (pages under 16 rows, 16-row pages and larger).  "onepass" with a *_lanes
+# layout is the single pass with per-lane page lookups (several batches per
+# wave); pages under 16 rows with groups of 4-8 at D >= 128 take the
+# matrix-core split on short rows (the planner's rule in split_on_matrix_cores
+# and launch_split_dg, fmha_decode_api.hip / fmha_decode_launch.hpp).
+_MC = ("split_matrix_core", "paged")
+_MC16 = ("split_matrix_core", "paged16")
+_LANES = ("onepass", "paged_lanes")
+_LANES16 = ("onepass", "paged16_lanes")
+PAGED_FEW_ROUTES = {
+    (128, 8, 1, 17): (_MC, _LANES16), (128, 8, 1, 32): (_MC, _LANES16), (128, 8, 1, 64): (_MC, _MC16),
+    (128, 16, 2, 17): (_MC, _LANES16), (128, 16, 2, 32): (_MC, _LANES16), (128, 16, 2, 64): (_MC, _MC16),
+    (256, 4, 1, 17): (_MC, _LANES16), (256, 4, 1, 32): (_MC, _LANES16),
+    (256, 4, 1, 64): (("onepass", "paged"), ("onepass", "paged16")),
+    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_MC, _LANES16),
+    (128, 40, 8, 17): (("onepass", "paged"), ("onepass", "paged16")),
+    (128, 40, 8, 32): (("onepass", "paged"), ("onepass", "paged16")),
+    (128, 40, 8, 64): (("onepass", "paged"), ("onepass", "paged16")),
+}
+PAGED_LONGER_ROUTES = {
+    (128, 4, 1, 48): (_MC, _LANES16), (128, 4, 1, 128): (_LANES, _LANES16),
+    (64, 2, 1, 48): (_LANES, _LANES16), (64, 2, 1, 128): (_LANES, _LANES16),
+    (128, 8, 2, 48): (_MC, _LANES16), (128, 8, 2, 128): (_LANES, _LANES16),
+    (64, 1, 1, 48): (_LANES, _LANES16), (64, 1, 1, 128): (_LANES, _LANES16),
+}
+
+
 @pytest.mark.parametrize("page_size", [1, 4, 16, 32])
 @pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2100), (128, 16, 2, 1100), (256, 4, 1, 1100), (64, 8, 1, 4200),
                                         (128, 40, 8, 700)])
@@ -353,9 +387,9 @@ def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
 def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
     """Rows of one to four 16-row blocks over paged caches with fewer KV
     heads than a wave holds and >= 512 waves: the single pass with each lane
-    group looking up its own batch's pages (several batches per wave) where
-    the library takes it, the split passes elsewhere; the last shape fills a
-    wave and runs one batch per wave."""
+    group looking up its own batch's pages (several batches per wave), or
+    the matrix-core split, as PAGED_FEW_ROUTES pins each case; the last
+    shape fills a wave and runs one batch per wave."""
     import fmha_amd
     import torch
     rng = np.random.default_rng(page_size * 11 + D + Hq + Hkv + B + max_len)
@@ -368,6 +402,7 @@ def test_paged_single_pass_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
     o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
+    assert _route() == PAGED_FEW_ROUTES[(D, Hq, Hkv, max_len)][page_size >= 16], last_plan()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass ps={page_size} D={D} {Hq}/{Hkv} B={B}")
 
 
@@ -392,6 +427,7 @@ def test_paged_single_pass_group_of_eight(page_size, D, max_len):
     o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
+    assert _route() == ("onepass", "paged16" if page_size >= 16 else "paged"), last_plan()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged single pass G=8 ps={page_size} D={D}")
 
 
@@ -415,5 +451,6 @@ def test_paged_single_pass_few_kv_heads_longer_rows(page_size, D, Hq, Hkv, B, ma
     o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
+    assert _route() == PAGED_LONGER_ROUTES[(D, Hq, Hkv, max_len)][page_size >= 16], last_plan()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len,
            f"paged single pass longer rows ps={page_size} D={D} {Hq}/{Hkv} B={B} max={max_len}")

@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import assert_pass, cu_from_seqlens, default_scale, make_inputs, to_dev
+from tests.common import assert_pass, cu_from_seqlens, default_scale, last_plan, make_inputs, to_dev
+from tests.common import plan_kinds as _kinds, plan_launch as _launch
 
 pytestmark = pytest.mark.gpu
 
@@ -19,27 +20,16 @@ def _run(q, k, v, cu, Hq, Hkv, D, max_len):
     return o.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def _plan(B, Hq, Hkv, max_len, D):
-    """(chunks, blocks) of the split-KV plan (plan_split in
-    fmha_decode_api.hip): P.V chunks of C rows, C the largest of 512, 256,
-    ..., 64 that still gives the target number of waves, 16-row blocks."""
-    hpw = 64 // (D // 8)
-    units = B * ((Hkv + hpw - 1) // hpw)
-    target = 512 * (2 if Hq // Hkv >= 8 else 1) * hpw // min(Hkv, hpw)
-    c = 512
-    while c > 64 and units * ((max_len + c - 1) // c) < target:
-        c //= 2
-    c = min(c, max(16, (max_len + 15) // 16 * 16))
-    return (max_len + c - 1) // c, (max_len + 15) // 16
-
-
 def _case(B, Hq, Hkv, D, seqlens, max_len, seed, std=1.0):
+    """Oracle parity of one call; returns the call's plan (last_plan)."""
     q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed, std)
     o = _run(q, k, v, cu, Hq, Hkv, D, max_len)
+    plan = last_plan()
     r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True, max_seqlen=max_len)
     st = oracle.compare(o.reshape(r.shape), r, slack)
-    print(f"B={B} Hq={Hq} Hkv={Hkv} D={D} max={max_len}: {st}", flush=True)
+    print(f"B={B} Hq={Hq} Hkv={Hkv} D={D} max={max_len}: {st} plan={plan}", flush=True)
     assert_pass(st, f"splitkv B={B} D={D} max={max_len}")
+    return plan
 
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 16), (64, 32, 4), (256, 16, 8), (128, 8, 1), (128, 32, 8),
@@ -63,17 +53,17 @@ def test_block_boundaries(D, Hq, Hkv):
 
 def test_mid_chunk_count():
     """16 < chunks <= 256 (the 256-thread combine) with four query heads per KV head."""
-    assert 16 < _plan(4, 32, 8, 8192, 128)[0] <= 256
     rng = np.random.default_rng(12)
     seqlens = rng.integers(6000, 8193, size=4).astype(np.int32)
     seqlens[0] = 8192
     _case(4, 32, 8, 128, seqlens, 8192, seed=12, std=0.5)
+    assert 16 < _launch("split")["chunks"] <= 256
 
 
 def test_mid_block_count():
     """512 < blocks <= 2048 (the 256-thread statistics) on one long row."""
-    assert 512 < _plan(1, 32, 8, 20000, 128)[1] <= 2048
     _case(1, 32, 8, 128, np.array([20000], np.int32), 20000, seed=13, std=0.5)
+    assert 512 < _launch("split")["blocks"] <= 2048
 
 
 @pytest.mark.parametrize("max_len", [16, 5])
@@ -82,6 +72,7 @@ def test_short_lengths_match_short_path(max_len):
     it): oracle parity, and NaN for a batch longer than max_seqlen_kv."""
     seqlens = np.minimum(oracle.generate_seqlens(300, 16), max_len).astype(np.int32)
     _case(300, 16, 16, 128, seqlens, max_len, seed=5)
+    assert _launch("short")["numerics"] == "exact"
     if max_len < 16:
         bad = seqlens.copy()
         bad[7] = max_len + 1
@@ -92,17 +83,18 @@ def test_short_lengths_match_short_path(max_len):
 
 def test_many_batches_direct_path():
     """max length fits one chunk: the PV kernel writes O directly."""
-    assert _plan(200, 8, 8, 40, 128)[0] == 1
     seqlens = np.random.default_rng(3).integers(0, 41, size=200).astype(np.int32)
     _case(200, 8, 8, 128, seqlens, 40, seed=6)
+    split = _launch("split")
+    assert split["chunks"] == 1 and split["passes"] == 3
 
 
 def test_one_long_sequence():
     """More than 256 chunks (the 1024-thread combine), more than 2048 blocks
     (the 1024-thread statistics)."""
-    chunks, blocks = _plan(1, 32, 8, 40000, 128)
-    assert chunks > 256 and blocks > 2048
     _case(1, 32, 8, 128, np.array([40000], np.int32), 40000, seed=7, std=0.5)
+    split = _launch("split")
+    assert split["chunks"] > 256 and split["blocks"] > 2048
 
 
 def test_wide_logits():
@@ -124,40 +116,32 @@ def test_bad_and_empty_lengths():
 
 
 # Single-pass path (onepass_decode_kernel): taken by fmha_decode_fwd_splitkv
-# when batch * ceil(Hkv / (64 / (D/8))) >= 512 and the wave's scores and
-# weights (HPW * G * (6 rows + 8) bytes, rows rounded up to 32) fit 40 KiB of LDS;
-# at G = 8 (packed layout) only on rows of at most 128 at D = 128 and 256
-# and, with several batches per wave, 96 at D = 128 and 64 at D = 64 (else
-# the matrix-core split).
-def _onepass_taken(B, Hq, Hkv, D, max_len):
-    """Waves = batch groups (2^shift batches each when Hkv is below the
-    heads a wave holds, see _sub_units) times KV-head groups."""
-    hpw = 64 // (D // 8)
-    r = _sub_units(Hkv, D)
-    waves = (B + r - 1) // r * ((Hkv + hpw // r - 1) // (hpw // r))
-    sp = (max_len + 31) // 32 * 32
-    limit = {64: 64, 128: 96, 256: 128}[D] if r > 1 else (128 if D > 64 else max_len)
-    if Hq // Hkv == 8 and max_len > limit:
-        return False
-    return waves >= 512 and hpw * (Hq // Hkv) * (6 * sp + 8) <= 40 * 1024
+# for many rows of a few 16-row blocks (the planner's rules in
+# fmha_decode_launch.hpp: launch_split_dg); the tests below assert the plan
+# the library reports for each call.
 
 
-def test_split_path_still_covered():
-    """The split-KV cases above keep below the single-pass threshold."""
-    assert not _onepass_taken(6, 16, 16, 128, 2048) and not _onepass_taken(16, 32, 8, 128, 8192)
-    assert not _onepass_taken(1, 32, 8, 128, 40000) and not _onepass_taken(4, 16, 16, 256, 600)
-    assert not _onepass_taken(10, 16, 2, 64, 64) and not _onepass_taken(10, 32, 8, 128, 64)
-    assert not _onepass_taken(200, 8, 8, 128, 40)
+@pytest.mark.parametrize("D,Hq,Hkv,max_len,kind", [(128, 16, 16, 2048, "split"), (128, 32, 8, 8192, "split"),
+                                                   (256, 16, 16, 600, "split"), (64, 16, 2, 64, "split_matrix_core"),
+                                                   (128, 32, 8, 64, "split")])
+def test_split_path_still_covered(D, Hq, Hkv, max_len, kind):
+    """Few batches: the split-KV launches (VALU, or matrix cores for groups
+    of 8), not the single pass."""
+    B = 10
+    seqlens = np.random.default_rng(D + max_len).integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[0] = max_len
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=D + max_len + Hq)
+    assert _kinds() == [kind]
 
 
 @pytest.mark.parametrize("D,B", [(64, 1024), (128, 512), (256, 256)])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 def test_onepass_all_shapes(D, B, G):
     Hkv, max_len = 16, 96
-    assert _onepass_taken(B, Hkv * G, Hkv, D, max_len)
     seqlens = np.random.default_rng(D + G).integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hkv * G, Hkv, D, seqlens, max_len, seed=900 + D + G)
+    assert _kinds() == ["onepass"]
 
 
 @pytest.mark.parametrize("D,Hkv,B,max_len", [(64, 16, 1024, 96), (64, 1, 4100, 64), (128, 8, 1100, 128),
@@ -167,12 +151,16 @@ def test_onepass_group_of_eight(D, Hkv, B, max_len):
     head dim (one batch per wave, and several: Hkv = 1, 2), with the 16-row
     edges, empty rows and a last wave partly empty."""
     Hq = 8 * Hkv
-    assert _onepass_taken(B, Hq, Hkv, D, max_len) and not _onepass_taken(B, Hq, Hkv, D, max_len + 1)
     rng = np.random.default_rng(D * 3 + Hkv + B)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[:7] = np.minimum([max_len, 0, 1, 15, 16, 17, 31], max_len)
     seqlens[-1] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=2000 + D + Hkv)
+    assert _kinds() == ["onepass"]
+    # one row more and the same lengths leave the single pass
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=2000 + D + Hkv)
+    _run(q, k, v, cu, Hq, Hkv, D, max_len + 1)
+    assert "onepass" not in _kinds()
 
 
 def test_onepass_edge_lengths():
@@ -181,11 +169,11 @@ def test_onepass_edge_lengths():
     pass; an invalid length gives NaN for its batch only."""
     import torch
     B, Hq, Hkv, D, max_len = 2048, 32, 8, 128, 256
-    assert _onepass_taken(B, Hq, Hkv, D, max_len)
     edge = np.array([0, 1, 2, 3, 15, 16, 17, 31, 32, 33, 47, 48, 49, 255, 256], np.int32)
     seqlens = np.random.default_rng(31).integers(1, 64, size=B).astype(np.int32)
     seqlens[: len(edge)] = edge
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=931)
+    assert _kinds() == ["onepass"]
     bad = seqlens.copy()
     bad[5] = max_len + 1
     q, k, v, cu = make_inputs(B, Hq, Hkv, D, bad, seed=932)
@@ -204,18 +192,26 @@ def _sub_units(Hkv, D):
     return r
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 1), (64, 16, 2), (64, 32, 4), (128, 8, 1), (128, 16, 2),
-                                     (256, 8, 1), (128, 4, 2)])
+@pytest.mark.parametrize("D,Hq,Hkv,force_valu", [(64, 4, 1, False), (64, 8, 2, False), (64, 16, 4, False),
+                                                (128, 4, 1, False), (128, 8, 2, False), (256, 4, 1, False),
+                                                (128, 4, 2, False), (64, 8, 1, True), (64, 32, 4, True),
+                                                (128, 16, 2, True), (256, 8, 1, True)])
 @pytest.mark.parametrize("max_len", [300, 2050])
-def test_sub_units(D, Hq, Hkv, max_len):
-    """Lane groups serving different blocks and chunks: block and chunk
-    counts that are not multiples of the groups per wave, empty and short
-    rows next to long ones."""
+def test_sub_units(monkeypatch, D, Hq, Hkv, force_valu, max_len):
+    """Lane groups of the VALU split passes serving different blocks and
+    chunks: block and chunk counts that are not multiples of the groups per
+    wave, empty and short rows next to long ones.  Groups of up to 4 take
+    these passes by default; groups of 8 take the matrix-core split unless
+    FMHA_DECODE_GQA_KERNEL=valu keeps them here."""
+    if force_valu:
+        monkeypatch.setenv("FMHA_DECODE_GQA_KERNEL", "valu")
+    else:
+        monkeypatch.delenv("FMHA_DECODE_GQA_KERNEL", raising=False)
     assert _sub_units(Hkv, D) > 1
     B = 5
-    assert not _onepass_taken(B, Hq, Hkv, D, max_len)
     seqlens = np.array([max_len, 1, 0, max_len - 17, 33], np.int32)
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=1300 + D + Hkv + max_len)
+    assert _launch("split")["sub_units"] == _sub_units(Hkv, D)
 
 
 @pytest.mark.parametrize("D,Hq,Hkv,B,max_len", [(128, 8, 1, 2047, 32), (128, 4, 1, 2047, 96), (64, 8, 2, 2050, 96),
@@ -223,11 +219,12 @@ def test_sub_units(D, Hq, Hkv, max_len):
 def test_onepass_batches_per_wave(D, Hq, Hkv, B, max_len):
     """Single pass with several batches per wave (fewer KV heads than a wave
     holds): mixed lengths in one wave, empty rows, a last wave partly empty."""
-    assert _sub_units(Hkv, D) > 1 and _onepass_taken(B, Hq, Hkv, D, max_len)
+    assert _sub_units(Hkv, D) > 1
     rng = np.random.default_rng(D + Hkv + B)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[:6] = np.minimum([max_len, 0, 1, 17, 33, 95], max_len)
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=1500 + D + Hkv)
+    assert _launch("onepass")["batches_per_wave"] == _sub_units(Hkv, D)
 
 
 def test_onepass_batches_per_wave_invalid_length():
@@ -235,7 +232,6 @@ def test_onepass_batches_per_wave_invalid_length():
     its wave stay exact."""
     import torch
     B, Hq, Hkv, D, max_len = 2048, 8, 1, 128, 32
-    assert _onepass_taken(B, Hq, Hkv, D, max_len)
     rng = np.random.default_rng(77)
     seqlens = rng.integers(1, max_len + 1, size=B).astype(np.int32)
     bad = 5
@@ -246,6 +242,7 @@ def test_onepass_batches_per_wave_invalid_length():
     k2 = np.concatenate([k[:cu[bad + 1]], np.zeros((max_len + 3 - seqlens[bad], Hkv, D), np.uint16), k[cu[bad + 1]:]])
     v2 = np.concatenate([v[:cu[bad + 1]], np.zeros((max_len + 3 - seqlens[bad], Hkv, D), np.uint16), v[cu[bad + 1]:]])
     bits = _run(q, k2, v2, cu_bad, Hq, Hkv, D, max_len).reshape(B, Hq, D)
+    assert _launch("onepass")["batches_per_wave"] > 1
     f = oracle.f16_to_f32(bits)
     assert np.all(np.isnan(f[bad]))
     keep = np.array([b for b in range(B) if b != bad])
@@ -267,6 +264,7 @@ def test_padded_query_group(D, Hq, Hkv, B, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq)
+    assert _kinds()[0] == "pad_query_group"
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(24, 8), (48, 4), (32, 1)])
@@ -277,6 +275,7 @@ def test_any_group_short_rows_through_split_entry(Hq, Hkv):
     rng = np.random.default_rng(Hq)
     seqlens = rng.integers(0, 11, size=33).astype(np.int32)
     _case(33, Hq, Hkv, 128, seqlens, 10, seed=Hq + 7)
+    assert _kinds() == (["short_matrix_core"] if Hq // Hkv > 8 else ["short"])
     q, k, v, cu = make_inputs(3, Hq, Hkv, 128, np.array([4, 12, 9], np.int32), seed=Hq + 8)
     o = _run(q, k, v, cu, Hq, Hkv, 128, 10).reshape(3, Hq, 128)
     assert np.all(np.isnan(oracle.f16_to_f32(o[1])))      # 12 > max_seqlen_kv
@@ -307,6 +306,8 @@ def test_group_slices_beyond_eight(long_group_kernel, D, Hq, Hkv, B, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 1)
+    kinds = _kinds()
+    assert ("split_matrix_core" in kinds) == (long_group_kernel == "mfma"), kinds
 
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 16, 1), (128, 24, 1), (64, 32, 2), (256, 16, 1), (128, 48, 2)])
@@ -322,6 +323,8 @@ def test_grouped_launch_kv_heads(long_group_kernel, D, Hq, Hkv, B, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 2)
+    kinds = _kinds()
+    assert ("split_matrix_core" in kinds) == (long_group_kernel == "mfma") and "pad_query_group" not in kinds, kinds
 
 
 @pytest.mark.parametrize("B,max_len", [(4, 300), (700, 40)])
@@ -363,6 +366,7 @@ def test_matrix_core_split_many_tiles(D, Hq, Hkv, B, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 3)
+    assert "split_matrix_core" in _kinds()
 
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(128, 8, 8), (128, 32, 8), (64, 8, 2), (256, 12, 4), (128, 20, 4)])
@@ -376,3 +380,4 @@ def test_matrix_core_split_small_groups(monkeypatch, D, Hq, Hkv, B, max_len):
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[0] = max_len
     _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + max_len + Hq + 4)
+    assert "split_matrix_core" in _kinds()

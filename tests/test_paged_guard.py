@@ -1,5 +1,6 @@
-"""CPU checks of the paged-cache guards (fmha_amd/csrc/fmha_decode_paged.hpp)
-that every paged loader of the library forms its row addresses through.
+"""CPU checks of the paged-cache guards (fmha_amd/csrc/fmha_decode_paged.hpp:
+paged_row_elem and its 32-bit-factor form paged_row_u32) that every paged
+loader of the library forms its row addresses through.
 
 Serving engines pad block tables with negative entries; a kernel that turned
 one into an address would read far outside the cache and fault the GPU.
@@ -32,6 +33,8 @@ def guards(tmp_path_factory):
     lib.guard_row_elem.argtypes = [ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64]
     lib.guard_entries_used.restype = ctypes.c_int
     lib.guard_entries_used.argtypes = [ctypes.c_int, ctypes.c_uint32]
+    lib.guard_row_u32.restype = ctypes.c_int64
+    lib.guard_row_u32.argtypes = [ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64]
     return lib
 
 
@@ -40,6 +43,24 @@ def test_negative_entries_are_refused(guards):
         for row in (0, 1, 15, 16, 2 ** 20):
             for shift in (0, 4, 6, 20):
                 assert guards.guard_row_elem(entry, row, shift, 16 * 4096, 4096) == -1
+
+
+def test_unsigned_form_equals_the_signed_one(guards):
+    """paged_row_u32 (the 32-bit-factor form the long-row loaders use) gives
+    paged_row_elem's offset for every mapped entry and refuses every
+    negative one: entries from -2^31 to 2^31-1, rows up to 2^24, page sizes
+    1 to 2^20, the caches' page strides and row sizes."""
+    rng = np.random.default_rng(5)
+    entries = np.concatenate([[-(2 ** 31), -2, -1, 0, 1, 2 ** 31 - 1], rng.integers(-(2 ** 31), 2 ** 31, 2000)])
+    for shift in (0, 1, 4, 6, 10, 20):
+        for hkv, d in ((1, 64), (8, 128), (32, 256)):
+            row_elems = hkv * d
+            page_stride = (1 << shift) * row_elems
+            for entry in entries[:: 7 if shift else 1]:
+                for row in (0, 1, 15, 16, int(rng.integers(0, 2 ** 24))):
+                    a = guards.guard_row_elem(int(entry), row, shift, page_stride, row_elems)
+                    b = guards.guard_row_u32(int(entry), row, shift, page_stride, row_elems)
+                    assert a == b, (int(entry), row, shift, a, b)
 
 
 def test_entries_used_is_ceil_of_length_over_page(guards):
