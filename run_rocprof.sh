@@ -4,10 +4,15 @@
 #   ./run_rocprof.sh [OUTDIR] [WORKLOAD]
 #     OUTDIR    default gpurun_out/rocprof
 #     WORKLOAD  bench (default: bench.py's headline workload, BASELINE C2),
-#               bN (BASELINE config N, 1..5), bNv (the same through the
+#               bN (BASELINE config N, 1..5), b1rot (C1 over 8 input sets in
+#               turn: 504 MB, beyond the 256 MB MALL), bNv (the same through the
 #               cu_seqlens entry point fmha_decode_fwd), rN (the reference's
 #               config N, 0..4, Poisson lengths through fmha_decode_fwd) or gN
-#               (tests/fmha_host.py's GQA suite, config N, 1..8)
+#               (tests/fmha_host.py's GQA suite, config N, 1..8), or
+#               s:B:Hq:Hkv:S:D[:LAYOUT] (one shape through
+#               tests/profiling/splitkv_bench.py: lengths beyond 16 through
+#               the split-KV entry points, LAYOUT packed, bhsd or pagedN;
+#               summarised per kernel, with the workspace bytes apart)
 #     KERNEL    (environment) regular expression of the kernel summarised,
 #               default fmha_decode:: (every kernel of the library)
 #
@@ -34,6 +39,11 @@ case "$WL" in
           TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
   r[0-4]) CMD=(python3 "$ROOT/tests/fmha_host.py" "${WL#r}" --suite reference --validate none)
           TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
+  b1rot) CMD=(python3 "$ROOT/tests/fmha_host.py" 1 --suite baseline --validate none --rotate 8)
+          TRACE_ARGS=(--iters 64 --warmup 8); PMC_ARGS=(--iters 16 --warmup 8) ;;
+  s:*) IFS=: read -r _ SB SHQ SHKV SS SD SLAYOUT <<< "$WL"
+       CMD=(python3 "$ROOT/tests/profiling/splitkv_bench.py" --shapes "$SB:$SHQ:$SHKV:$SS:$SD" --layout "${SLAYOUT:-packed}")
+       TRACE_ARGS=(--iters 50 --warmup 5); PMC_ARGS=(--iters 3 --warmup 1) ;;
   *) echo "unknown workload $WL"; exit 2 ;;
 esac
 BYTES=$(python3 - "$ROOT" "$WL" <<'PY'
@@ -43,6 +53,10 @@ wl = sys.argv[2]
 from tests.fmha_host import SUITES, algorithmic_bytes
 if wl == "bench":
     B, Hq, Hkv, S, D, _ = SUITES["baseline"][2]
+elif wl == "b1rot":
+    B, Hq, Hkv, S, D, _ = SUITES["baseline"][1]
+elif wl.startswith("s:"):
+    B, Hq, Hkv, S, D = (int(x) for x in wl.split(":")[1:6])
 else:
     suite = {"b": "baseline", "r": "reference", "g": "gqa"}[wl[0]]
     B, Hq, Hkv, S, D, _ = SUITES[suite][int(wl[1:].rstrip("v"))]
@@ -70,5 +84,7 @@ pass_ cache 120 --pmc TCC_HIT_sum TCC_MISS_sum SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT
 pass_ calib_fetch 120 --pmc FETCH_SIZE --output-format csv -d "$OUT/calib_fetch" -o run -- python3 "$ROOT/tests/profiling/calib_copy.py"
 pass_ calib_write 120 --pmc WRITE_SIZE --output-format csv -d "$OUT/calib_write" -o run -- python3 "$ROOT/tests/profiling/calib_copy.py"
 KRE=${KERNEL:-fmha_decode::}
+EXTRA=()
+case "$WL" in s:*) EXTRA=(--per-kernel --bench-log "$OUT/trace.log") ;; esac
 python3 "$ROOT/tests/profiling/summarize.py" "$OUT" --bytes "$BYTES" --kernel "$KRE" --label "workload $WL" \
-  --command "./run_rocprof.sh gpurun_out/rocprof_$WL $WL"
+  --command "./run_rocprof.sh gpurun_out/rocprof_${WL//:/_} $WL" "${EXTRA[@]}"

@@ -7,9 +7,11 @@ library at least --warmup times and for at least 0.1 s (tests/common.py:
 gpu_warmup), then times --iters calls with a HIP event pair per
 call on the launch stream and prints one JSON line: median µs per call and
 algorithmic TB/s (Q + K + V + O as the reference counts them,
-fmha_host.cpp:428-430, with Hkv heads for K/V; workspace traffic not
-counted).  Run it under `rocprofv3 --kernel-trace --stats` for the per-kernel
-split.
+fmha_host.cpp:428-430, with Hkv heads for K/V), the plan the library reports
+for the call (fmha_decode_last_plan) and the bytes that plan moves through
+the workspace (workspace_traffic_bytes, counted apart).  Run it under
+`rocprofv3 --kernel-trace --stats` for the per-kernel split
+(run_rocprof.sh's s:... workloads).
 
     python3 tests/profiling/splitkv_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...]
         [--layout packed|bhsd|pagedN]
@@ -36,6 +38,27 @@ from tests.common import gpu_warmup  # noqa: E402
 SHAPES = [(64, 32, 8, 4096, 128), (8, 32, 8, 32768, 128), (256, 64, 8, 1024, 128), (1, 32, 8, 131072, 128),
           (2048, 32, 8, 128, 128), (4096, 32, 8, 64, 128), (16384, 32, 8, 24, 128), (8192, 16, 16, 64, 128),
           (512, 32, 8, 128, 128), (256, 32, 8, 256, 128), (128, 32, 8, 256, 128), (30720, 16, 16, 16, 128)]
+
+
+def workspace_traffic(plan, B, hq, hkv, D):
+    """Bytes the split-KV passes move through the workspace per call, from the
+    plan the library reports: the scores T (written by the scores pass, read
+    by P.V), the per-block max and sum (written, read by the statistics
+    pass), the per-head max and sum (written, read by P.V) and, with more
+    than one chunk per row, the fp32 partial outputs (written by P.V, read by
+    the combine).  0 for the single pass and the short kernels."""
+    total = 0
+    for entry in plan:
+        kind, _, rest = entry.partition("(")
+        if kind not in ("split", "split_matrix_core"):
+            continue
+        f = dict(kv.split("=") for kv in rest.rstrip(")").split())
+        heads = B * max(hq, hkv * int(f["G"]))
+        nblk, chunks = int(f["blocks"]), int(f["chunks"])
+        total += 2 * heads * nblk * 16 * 4 + 2 * 2 * heads * nblk * 4 + 2 * heads * 2 * 4
+        if chunks > 1:
+            total += 2 * heads * chunks * D * 4
+    return total
 
 
 def main():
@@ -102,9 +125,11 @@ def main():
         per = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
         med = per[len(per) // 2]
         nbytes = 2 * B * hq * D * 2 + 4 * B * S * hkv * D
+        plan = fmha_amd.last_plan()
         print(json.dumps({"layout": a.layout, "B": B, "Hq": hq, "Hkv": hkv, "S": S, "D": D,
                           "us_per_call_median": round(med, 1),
-                          "tb_s": round(nbytes / med / 1e6, 3), "workspace_bytes": ws.numel()}), flush=True)
+                          "tb_s": round(nbytes / med / 1e6, 3), "workspace_bytes": ws.numel(), "plan": plan,
+                          "workspace_traffic_bytes": workspace_traffic(plan, B, hq, hkv, D)}), flush=True)
         del q, o, ws, call
         torch.cuda.empty_cache()
 

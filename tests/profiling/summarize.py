@@ -56,6 +56,92 @@ def trace_stats(d, kernel_re):
     return durs
 
 
+def _short(name):
+    """A kernel's name without the return type and namespace."""
+    return re.sub(r"^void\s+", "", name).replace("fmha_decode::", "")
+
+
+def _bench_json(path):
+    """The JSON line the profiled program printed (splitkv_bench.py), if any."""
+    if not path or not os.path.exists(path):
+        return None
+    for line in open(path, errors="replace"):
+        line = line.strip()
+        if line.startswith("{") and "us_per_call_median" in line:
+            try:
+                return json.loads(line)
+            except ValueError:
+                pass
+    return None
+
+
+def per_kernel(a):
+    """Per-pass table of a call made of several kernels (split-KV): each
+    kernel's average duration, HBM bytes per dispatch (FETCH_SIZE and
+    WRITE_SIZE, copy-calibrated) and VALU/MFMA busy; the call's total against
+    the algorithmic bytes (Q + K + V + O) and the workspace bytes the plan
+    moves."""
+    names = sorted({r["Kernel_Name"] for r in _rows(os.path.join(a.dir, "trace", "**", "*kernel_trace.csv"))
+                    if re.search(a.kernel, r["Kernel_Name"])})
+    cf = counters(os.path.join(a.dir, "calib_fetch"), r"copy|elementwise|Copy")
+    cw = counters(os.path.join(a.dir, "calib_write"), r"copy|elementwise|Copy")
+    gib_kib = float(1 << 20)
+    f_scale = statistics.median(cf["FETCH_SIZE"]) / gib_kib if cf.get("FETCH_SIZE") else None
+    w_scale = statistics.median(cw["WRITE_SIZE"]) / gib_kib if cw.get("WRITE_SIZE") else None
+    bench = _bench_json(a.bench_log)
+    ws = bench.get("workspace_traffic_bytes", 0) if bench else 0
+    rows, tot_us, tot_bytes = [], 0.0, 0.0
+    for n in names:
+        kre = "^" + re.escape(n) + "$"
+        durs = trace_stats(os.path.join(a.dir, "trace"), kre)
+        avg = statistics.mean(durs) if durs else float("nan")
+        kf = counters(os.path.join(a.dir, "fetch"), kre).get("FETCH_SIZE")
+        kw = counters(os.path.join(a.dir, "write"), kre).get("WRITE_SIZE")
+        fetch = statistics.median(kf) / f_scale * 1024 if kf and f_scale else float("nan")
+        write = statistics.median(kw) / w_scale * 1024 if kw and w_scale else float("nan")
+        busy = {k: statistics.median(v) for k, v in counters(os.path.join(a.dir, "busy"), kre).items()}
+        cyc = busy.get("GRBM_GUI_ACTIVE", 0) / XCD_NUM
+        valu = 100 * 4 * busy["SQ_ACTIVE_INST_VALU"] / (SIMD_NUM * cyc) if cyc and "SQ_ACTIVE_INST_VALU" in busy else None
+        mfma = (100 * busy["SQ_VALU_MFMA_BUSY_CYCLES"] / (SIMD_NUM * cyc)
+                if cyc and "SQ_VALU_MFMA_BUSY_CYCLES" in busy else None)
+        tot_us += avg
+        tot_bytes += fetch + write
+        rows.append({"kernel": _short(n), "calls": len(durs), "avg_us": avg, "fetch_bytes": fetch,
+                     "write_bytes": write, "hbm_gbs": (fetch + write) / (avg * 1e-6) / 1e9 if durs else None,
+                     "valu_busy_pct": valu, "mfma_busy_pct": mfma, "waves": busy.get("SQ_WAVES")})
+    out = {"label": a.label, "per_kernel": rows, "algorithmic_bytes_per_call": a.bytes,
+           "workspace_bytes_per_call": ws, "kernel_us_per_call": tot_us, "hbm_bytes_per_call": tot_bytes,
+           "traffic_over_algorithmic": tot_bytes / a.bytes,
+           "traffic_over_algorithmic_plus_workspace": tot_bytes / (a.bytes + ws),
+           "achieved_gbs": a.bytes / (tot_us * 1e-6) / 1e9, "bench": bench}
+    lines = [f"# {a.label}", "", "Command:", "", "    " + a.command, ""]
+    if bench:
+        lines += [f"Plan (fmha_decode_last_plan): {'; '.join(bench.get('plan', []))}", "",
+                  f"Timed call (HIP events, median of the program's own loop): "
+                  f"{bench['us_per_call_median']} µs, {bench['tb_s']} TB/s algorithmic", ""]
+    lines += ["| kernel | dispatches | avg µs | FETCH bytes | WRITE bytes | HBM GB/s | VALUBusy % | MfmaUtil % |",
+              "|---|---|---|---|---|---|---|---|"]
+    fmt = lambda x, f: "-" if x is None or x != x else format(x, f)
+    for r in rows:
+        lines.append(f"| `{r['kernel']}` | {r['calls']} | {fmt(r['avg_us'], '.1f')} | {fmt(r['fetch_bytes'], '.4g')} | "
+                     f"{fmt(r['write_bytes'], '.4g')} | {fmt(r['hbm_gbs'], '.0f')} | {fmt(r['valu_busy_pct'], '.1f')} | "
+                     f"{fmt(r['mfma_busy_pct'], '.2f')} |")
+    lines += ["", f"Per call: kernel time {tot_us:.1f} µs (sum of the passes' averages); algorithmic bytes "
+                  f"{a.bytes:.4g} (Q + K + V + O, fmha_host.cpp:428-430) -> {out['achieved_gbs']:.0f} GB/s, "
+                  f"{out['achieved_gbs'] / 80:.1f}% of 8 TB/s; workspace bytes by the plan {ws:.4g}; measured HBM "
+                  f"bytes {tot_bytes:.4g} = {out['traffic_over_algorithmic']:.4f} x algorithmic, "
+                  f"{out['traffic_over_algorithmic_plus_workspace']:.4f} x (algorithmic + workspace).", "",
+              "FETCH_SIZE and WRITE_SIZE (KiB per dispatch, one counter per run) are scaled by what they read for "
+              "a 1 GiB device-to-device copy (tests/profiling/calib_copy.py); VALUBusy = 4 SQ_ACTIVE_INST_VALU / "
+              f"({SIMD_NUM} SIMDs x GRBM_GUI_ACTIVE / {XCD_NUM}), MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / "
+              f"({SIMD_NUM} x the same cycles), medians over dispatches.", ""]
+    with open(os.path.join(a.dir, "summary.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(os.path.join(a.dir, "traffic.json"), "w") as f:
+        json.dump(out, f, indent=1)
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("dir")
@@ -63,7 +149,12 @@ def main():
     ap.add_argument("--bytes", type=float, required=True, help="algorithmic bytes per launch")
     ap.add_argument("--label", default="")
     ap.add_argument("--command", default="")
+    ap.add_argument("--per-kernel", action="store_true", help="one row per kernel (multi-pass calls)")
+    ap.add_argument("--bench-log", default="", help="the profiled program's output (its JSON line)")
     a = ap.parse_args()
+    if a.per_kernel:
+        per_kernel(a)
+        return
 
     durs = trace_stats(os.path.join(a.dir, "trace"), a.kernel)
     names = set()
