@@ -2,7 +2,7 @@
 // in fmha_decode_launch.hpp, one slice per compilation: fmha_amd/_build.py
 // compiles this file once for each FMHA_DECODE_PART in [0, FMHA_DECODE_PARTS)
 // and links the objects with fmha_decode_api.hip.  Part 0 holds the kernels
-// every long-row path shares (split-KV statistics and combine, query-group
+// every long-row path shares (the split-KV statistics and combine passes, query-group
 // padding); every other part instantiates launchers, and with them kernels,
 // that no other part does.
 //
@@ -21,9 +21,10 @@ namespace host {
 
 #if FMHA_DECODE_PART == 0
 
-// Pass 2 of split-KV: the global max and sum per (batch, query head).  One
-// lane per head for rows of at most 16 blocks, else one workgroup per head
-// sized to the row's block count (8 blocks per thread and round).
+// The statistics pass of split-KV: the global max and sum per (batch, query
+// head).  One lane per head for rows of at most 16 blocks, else one
+// workgroup per head sized to the row's block count (8 blocks per thread
+// and round).
 void launch_split_stats(const SplitArgs& a, hipStream_t stream) {
   const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;
   if (a.nblk <= 16)
@@ -36,9 +37,9 @@ void launch_split_stats(const SplitArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(fmha_decode::splitkv_stats_kernel<1024>, dim3(heads), dim3(1024), 0, stream, a);
 }
 
-// Pass 4 of split-KV (more than one chunk per row): partial outputs summed
-// in chunk order, one lane per 8 dims for few chunks, else a workgroup per
-// (head, 32 dims).
+// The combine pass of split-KV (more than one chunk per row): partial
+// outputs summed in chunk order, one lane per 8 dims for few chunks, else a
+// workgroup per (head, 32 dims).
 template <int D>
 void launch_split_combine_d(const SplitArgs& a, hipStream_t stream) {
   const uint32_t heads = (uint32_t)a.batch * (uint32_t)a.num_heads_q;

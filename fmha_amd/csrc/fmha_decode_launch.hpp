@@ -13,6 +13,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <cstdlib>
 
 #include "fmha_decode_group.hpp"
 #include "fmha_decode_kernel.hpp"
@@ -302,11 +303,18 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
 
 // Launchers of the kernels every long-row path shares, defined once in the
 // part that owns them (fmha_decode_inst.hip, FMHA_DECODE_PART 0).
-// Pass 2 of split-KV: the global max and sum per (batch, query head).
+// The statistics pass of split-KV (rows of more than kPvStatBlocks blocks):
+// the global max and sum per (batch, query head).
 void launch_split_stats(const SplitArgs& a, hipStream_t stream);
-// Pass 4 of split-KV (more than one chunk per row): the partial outputs
-// summed in chunk order.
+// The combine pass of split-KV (more than one chunk per row): the partial
+// outputs summed in chunk order.
 void launch_split_combine(const SplitArgs& a, int d, hipStream_t stream);
+
+// Rows of up to this many 16-row blocks: every split-KV P.V wave reduces its
+// heads' block statistics itself (no statistics pass; µs with the pass /
+// without: B=256 S=1024 Hq/Hkv 64/8 222 / 218, B=128 S=256 32/8 41 / 37).
+constexpr int kPvStatBlocks = 64;
+
 // Q rows copied to, and O rows back from, a query group padded to GP rows
 // per (batch, KV head) stream (fmha_decode_group.hpp).
 hipError_t launch_pad_query_group(const uint16_t* q, uint16_t* qp, uint64_t streams, int G, int GP, int D,
@@ -392,39 +400,44 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
   }
   if (onepass_only) return kOnepassNotTaken;
-  // The combine grid has one workgroup per (batch, query head, 32 dims).
-  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
   // P.V sub-block rows (register budget: pages under 16 rows address every
   // row on its own, a descriptor or a 64-bit address per row; 16 rows there
   // leave one wave per SIMD).
   constexpr int NR = G >= 8 || LAYOUT == fmha_decode::kLayoutPaged || LAYOUT == fmha_decode::kLayoutPagedLanes ? 8 : 16;
-  // One block per scores wave otherwise (two measured 1-3% slower).
   SplitArgs as = a;
   as.sub_shift = shift;
   as.units_per_batch = (a.num_heads_kv + (HPW >> shift) - 1) / (HPW >> shift);
-  const uint32_t upb = (uint32_t)as.units_per_batch;
-  const uint32_t score_waves = (uint32_t)a.batch * (uint32_t)((a.nblk + (1 << shift) - 1) >> shift) * upb;
-  const uint32_t pv_waves = (uint32_t)a.batch * (uint32_t)((a.nchunks + (1 << shift) - 1) >> shift) * upb;
+  const int64_t upb = as.units_per_batch;
+  as.stat_pass = a.nblk > kPvStatBlocks;
+  const int64_t score_waves = (int64_t)a.batch * ((a.nblk + (1 << shift) - 1) >> shift) * upb;
+  const int64_t nwc = (a.nchunks + (1 << shift) - 1) >> shift;  // P.V waves per unit
+  const int64_t pv_waves = (int64_t)a.batch * nwc * upb;
+  if (score_waves > INT32_MAX || pv_waves > INT32_MAX) return hipErrorInvalidValue;
+  // The combine grid has one workgroup per (batch, query head, 32 dims).
+  if ((uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX) return hipErrorInvalidValue;
+  const int passes = 2 + as.stat_pass + (a.nchunks > 1);
   plan_note("split(D=%d G=%d layout=%s sub_units=%d blocks=%d chunk_rows=%d chunks=%d passes=%d)", D, G,
-            layout_name(LAYOUT), 1 << shift, a.nblk, a.chunk_rows, a.nchunks, a.nchunks == 1 ? 3 : 4);
+            layout_name(LAYOUT), 1 << shift, a.nblk, a.chunk_rows, a.nchunks, passes);
   {
     constexpr auto kernel = fmha_decode::splitkv_scores_kernel<D, G, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3(score_waves), dim3(kBlockThreads),
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),
                        lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, as);
   }
-  launch_split_stats(a, stream);
+  if (as.stat_pass) launch_split_stats(as, stream);
   if (a.nchunks == 1) {
     // One chunk per batch: the P.V wave writes O itself, one chunk per wave.
     constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, true, LAYOUT>;
+    SplitArgs ad = a;
+    ad.stat_pass = as.stat_pass;
     const uint32_t waves = (uint32_t)a.batch * (uint32_t)a.units_per_batch;
     hipLaunchKernelGGL(kernel, dim3(waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
-                       stream, a);
+                       stream, ad);
     return hipGetLastError();
   }
   {
     constexpr auto kernel = fmha_decode::splitkv_pv_kernel<D, G, NR, false, LAYOUT>;
-    hipLaunchKernelGGL(kernel, dim3(pv_waves), dim3(kBlockThreads), lds_reserve_kernel<kernel>(kSplitPvWavesPerCU),
-                       stream, as);
+    hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, as);
   }
   launch_split_combine(a, D, stream);
   return hipGetLastError();
@@ -451,7 +464,8 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
 
 // Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
 // are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
-// size.  Scores, stats, P.V (O directly with one chunk per row), combine.
+// size.  Scores, the statistics pass for rows of more than kPvStatBlocks
+// blocks, P.V (O directly with one chunk per row), combine.
 // P.V waves take TW tiles of 16 query heads, their accumulators TW * D/16 *
 // 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
 template <int D, int LAYOUT>
@@ -467,24 +481,26 @@ hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
   if (score_waves > INT32_MAX || pv_waves > INT32_MAX ||
       (uint64_t)a.batch * (uint64_t)a.num_heads_q * (D / 32) > UINT32_MAX)
     return hipErrorInvalidValue;
+  SplitArgs am = a;
+  am.stat_pass = a.nblk > kPvStatBlocks;
   plan_note("split_matrix_core(D=%d G=%d layout=%s blocks=%d chunk_rows=%d chunks=%d passes=%d)", D, (int)g,
-            layout_name(LAYOUT), a.nblk, a.chunk_rows, a.nchunks, a.nchunks == 1 ? 3 : 4);
+            layout_name(LAYOUT), a.nblk, a.chunk_rows, a.nchunks, 2 + am.stat_pass + (a.nchunks > 1));
   {
     constexpr auto kernel = fmha_decode::splitkv_scores_group_kernel<D, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3((uint32_t)score_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, a);
+                       lds_reserve_kernel<kernel>(kSplitScoresWavesPerCU), stream, am);
   }
-  launch_split_stats(a, stream);
+  if (am.stat_pass) launch_split_stats(am, stream);
   if (a.nchunks == 1) {
     constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, true, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, am);
     return hipGetLastError();
   }
   {
     constexpr auto kernel = fmha_decode::splitkv_pv_group_kernel<D, TW, false, LAYOUT>;
     hipLaunchKernelGGL(kernel, dim3((uint32_t)pv_waves), dim3(kBlockThreads),
-                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, a);
+                       lds_reserve_kernel<kernel>(kSplitPvWavesPerCU), stream, am);
   }
   launch_split_combine(a, D, stream);
   return hipGetLastError();

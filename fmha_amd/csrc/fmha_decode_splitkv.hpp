@@ -5,17 +5,19 @@
 // scores, max-subtracted softmax, weights rounded to bf16 *after*
 // normalisation (as the reference's CPU loop does, fmha_host.cpp:209-226),
 // fp32 P.V, one fp16 rounding.  Because the bf16 rounding needs the global
-// max and sum before any weight is formed, the work runs in four launches
-// over a caller-provided workspace:
+// max and sum before any weight is formed, the work runs in two to four
+// launches over a caller-provided workspace:
 //
 //   1. scores:  one wave per (batch, block of 16 rows, KV-head group): the
 //               block's Q and K rows are requested at once (as in the short
 //               kernel), dot products, transposing butterfly (shared with
 //               the short kernel); scaled scores t_j -> T, and per query head
 //               the block's max m_b and sum l_b of exp(t_j - m_b).
-//   2. stats:   one workgroup per (batch, query head): m = max_b m_b,
-//               L = sum_b l_b * exp(m_b - m), loads batched, reduction order
-//               fixed (deterministic).
+//   2. stats:   rows of more than kPvStatBlocks blocks only: one workgroup
+//               per (batch, query head): m = max_b m_b, L = sum_b l_b *
+//               exp(m_b - m), loads batched, reduction order fixed
+//               (deterministic).  Shorter rows skip it: each P.V wave
+//               reduces its heads' block statistics itself (row_stats).
 //   3. pv:      one wave per (batch, chunk of C rows, KV-head group), walking
 //               the chunk in sub-blocks of NR rows with two register sets:
 //               the next sub-block's V rows and scores are in flight while
@@ -24,7 +26,15 @@
 //               then packed dot2 accumulation; the chunk's fp32 partial
 //               output -> Opart, or fp16 O directly when every batch fits one
 //               chunk.
-//   4. combine: O = fp16(sum_c Opart), chunks added in order.
+//   4. combine: more than one chunk per row only: O = fp16(sum_c Opart),
+//               chunks added in order.
+//
+// The combine stays a launch of its own: folding it into pass 3 (the last
+// P.V wave of a row, found with an atomic counter, summing the partials)
+// needs an agent-scope release fence in every P.V wave, an L2 writeback
+// that measured about 350 ns of serialised L2 time per wave (B=256 S=1024
+// Hq/Hkv 64/8 with 4 chunks per row: 584 against 250 µs; B=1 S=131072
+// 32/8, 256 chunks: 137 against 106 µs).
 //
 // K and V are each read once; T adds 4 bytes per row and query head (written
 // by 1, read by 3), the block statistics 8 bytes per 16 rows and query head,
@@ -80,6 +90,9 @@ struct SplitArgs {
   // the kernels' G runs as kv_groups groups of G on one launch, launch head
   // hk reading memory head hk / kv_groups of num_heads_kv / kv_groups.
   int32_t kv_groups;
+  // 1: the statistics pass ran and ml holds each head's global max and sum;
+  // 0: every P.V wave reduces its heads' block statistics (m, l) itself.
+  int32_t stat_pass;
 };
 
 // KV heads of the cache in memory, and the one launch head hk reads.
@@ -590,8 +603,9 @@ __device__ __forceinline__ float block_reduce(float x, float* red) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. stats: per (batch, query head), the global max and sum of exponentials
-// over the row's 16-row blocks.
+// 2. stats (rows of more than kPvStatBlocks blocks): per (batch, query
+// head), the global max and sum of exponentials over the row's 16-row
+// blocks.
 // ---------------------------------------------------------------------------
 // Rows of at most 16 blocks: one lane per head, all loads in flight.
 #ifdef FMHA_DECODE_SHARED_KERNELS  // one translation unit emits it (not a template)
@@ -664,6 +678,77 @@ __global__ __launch_bounds__(THREADS) void splitkv_stats_kernel(SplitArgs a) {
   if (t == 0) {
     a.ml[2 * i] = gm;
     a.ml[2 * i + 1] = gl;
+  }
+}
+
+// The global max and sum of exp(t - max) of NS query heads (hqi[i]; ok[i]
+// false: none, 0 and 1 returned) of a row of S rows, for the P.V passes:
+// a.ml when the statistics pass ran, else the scores pass's block
+// statistics reduced here.  The NL lanes whose lane index differs only in the bits of
+// STRIDE * (NL - 1) share each head; lane k of them (k = (lane / STRIDE) %
+// NL) takes blocks k, k + NL, ... (the max, then the sum of l * exp(m -
+// max)), U of them in flight per head, then butterflies over the NL lanes in
+// a fixed order.
+template <int NL, int STRIDE, int NS>
+__device__ __forceinline__ void row_stats(const SplitArgs& a, const uint64_t (&hqi)[NS], const bool (&ok)[NS], int S,
+                                          int lane, float (&gm)[NS], float (&gl)[NS]) {
+  if (a.stat_pass) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      gm[i] = ok[i] ? a.ml[2 * hqi[i]] : 0.0f;
+      gl[i] = ok[i] ? a.ml[2 * hqi[i] + 1] : 1.0f;
+    }
+    return;
+  }
+  constexpr int U = 4;
+  const int k = (lane / STRIDE) % NL;
+  const int n = (S + kSplitBlockRows - 1) / kSplitBlockRows;
+  float mx[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) mx[i] = -__builtin_inff();
+  for (int s0 = k; s0 < n; s0 += NL * U) {
+    float x[NS][U];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int s = s0 + u * NL;
+        x[i][u] = ok[i] && s < n ? a.m[hqi[i] * a.nblk + s] : -__builtin_inff();
+      }
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx[i] = fmaxf(mx[i], x[i][u]);
+  }
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+#pragma unroll
+    for (int d = STRIDE; d < STRIDE * NL; d <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], d, kWaveSize));
+  float sm[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) sm[i] = 0.0f;
+  for (int s0 = k; s0 < n; s0 += NL * U) {
+    float x[NS][U], y[NS][U];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int s = s0 + u * NL;
+        const bool in = ok[i] && s < n;
+        x[i][u] = in ? a.m[hqi[i] * a.nblk + s] : 0.0f;
+        y[i][u] = in ? a.l[hqi[i] * a.nblk + s] : 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int u = 0; u < U; ++u) sm[i] += ok[i] && s0 + u * NL < n ? y[i][u] * expf(x[i][u] - mx[i]) : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+#pragma unroll
+    for (int d = STRIDE; d < STRIDE * NL; d <<= 1) sm[i] += __shfl_xor(sm[i], d, kWaveSize);
+    gm[i] = ok[i] ? mx[i] : 0.0f;
+    gl[i] = ok[i] ? sm[i] : 1.0f;
   }
 }
 
@@ -780,6 +865,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
   uint32_t t_off[PL];
   bool slot_ok[PL];
   int slot_rows[PL];
+  uint64_t hqi[PL];
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int f = lane + kWaveSize * i;
@@ -790,13 +876,13 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_kernel(SplitArgs a) 
     const int row0f = (int)((wc << a.sub_shift) + (uint32_t)su.unit(hklf)) * a.chunk_rows;
     slot_rows[i] = min(S - row0f, a.chunk_rows);
     slot_ok[i] = f < P::SLOTS && hkf < a.num_heads_kv && slot_rows[i] > 0;
-    const uint64_t hqi = (uint64_t)b * hq + hkf * G + gf;
-    gm[i] = slot_ok[i] ? a.ml[2 * hqi] : 0.0f;
-    gsum[i] = slot_ok[i] ? a.ml[2 * hqi + 1] : 1.0f;
+    hqi[i] = (uint64_t)b * hq + hkf * G + gf;
     t_off[i] = slot_ok[i] ? (uint32_t)((row0f / kSplitBlockRows) * hq * kSplitBlockRows +
                                        (hkf * G + gf) * kSplitBlockRows + jf) * 4u
                           : kLaneOutOfRange;
   }
+  // The NR lanes of a slot's (head, query) share its statistics.
+  row_stats<NR, 1, PL>(a, hqi, slot_ok, S, lane, gm, gsum);
 
   float acc[G][8];
 #pragma unroll

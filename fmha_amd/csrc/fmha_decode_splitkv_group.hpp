@@ -247,16 +247,18 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
   vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), row0, row0 + rows, (int)hk, true, r, s * NR, rows);
   const __amdgpu_buffer_rsrc_t t_rsrc =
       make_rsrc(a.t + t_block_base(a, b, 0), (uint32_t)a.nblk * (uint32_t)hq * NR * 4u);
-  // The row's global max and sum for this lane's query column of each tile.
+  // The row's global max and sum for this lane's query column of each tile
+  // (the four lanes q = 0..3 of a column share it).
   float gm[TW], gl[TW];
+  uint64_t hqi[TW];
+  bool hok[TW];
 #pragma unroll
   for (int i = 0; i < TW; ++i) {
     const int g = (tile0 + i) * 16 + n;
-    const bool ok = i < ntl && g < G;
-    const uint64_t hqi = (uint64_t)b * hq + (uint64_t)hk * G + (ok ? g : 0);
-    gm[i] = ok ? a.ml[2 * hqi] : 0.0f;
-    gl[i] = ok ? a.ml[2 * hqi + 1] : 1.0f;
+    hok[i] = i < ntl && g < G;
+    hqi[i] = (uint64_t)b * hq + (uint64_t)hk * G + (hok[i] ? g : 0);
   }
+  row_stats<4, 16, TW>(a, hqi, hok, S, lane, gm, gl);
   f32x4_v acc[TW][DPC];
 #pragma unroll
   for (int i = 0; i < TW; ++i)

@@ -52,7 +52,8 @@ def test_block_boundaries(D, Hq, Hkv):
 
 
 def test_mid_chunk_count():
-    """16 < chunks <= 256 (the 256-thread combine) with four query heads per KV head."""
+    """16 < chunks <= 256 with four query heads per KV head: rows of more
+    P.V waves than one combine group (16), summed in two levels."""
     rng = np.random.default_rng(12)
     seqlens = rng.integers(6000, 8193, size=4).astype(np.int32)
     seqlens[0] = 8192
@@ -61,9 +62,36 @@ def test_mid_chunk_count():
 
 
 def test_mid_block_count():
-    """512 < blocks <= 2048 (the 256-thread statistics) on one long row."""
+    """512 < blocks <= 2048 on one long row: the 256-thread statistics pass."""
     _case(1, 32, 8, 128, np.array([20000], np.int32), 20000, seed=13, std=0.5)
-    assert 512 < _launch("split")["blocks"] <= 2048
+    split = _launch("split")
+    assert 512 < split["blocks"] <= 2048 and split["passes"] == 4
+
+
+# (B, Hq, Hkv, D, max_len, kind, passes): rows of up to 64 blocks, whose P.V
+# waves reduce the block statistics themselves (no statistics pass), and one
+# block more; one chunk per row (O from the P.V pass) or several (combine).
+STAT_CASES = [
+    (6, 32, 8, 128, 1024, "split", 3),
+    (6, 32, 8, 128, 1040, "split", 4),
+    (256, 32, 8, 128, 1024, "split", 2),
+    (256, 32, 8, 128, 1040, "split", 4),
+    (8, 8, 2, 64, 1000, "split", 3),               # lane groups on several chunks
+    (8, 64, 4, 128, 1024, "split_matrix_core", 3),
+    (8, 64, 4, 128, 1040, "split_matrix_core", 4),
+    (512, 64, 4, 256, 700, "split_matrix_core", 2),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,max_len,kind,passes", STAT_CASES)
+def test_block_statistics_in_pv(B, Hq, Hkv, D, max_len, kind, passes):
+    """The P.V waves' own reduction of the block statistics, at and past its
+    64-block limit, with ragged lengths (0, 1, one block, the maximum)."""
+    rng = np.random.default_rng(B + max_len + Hq)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:4] = [max_len, 0, 1, 16]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B * 7 + D + Hq, std=0.5)
+    assert _launch(kind)["passes"] == passes
 
 
 @pytest.mark.parametrize("max_len", [16, 5])
@@ -86,7 +114,7 @@ def test_many_batches_direct_path():
     seqlens = np.random.default_rng(3).integers(0, 41, size=200).astype(np.int32)
     _case(200, 8, 8, 128, seqlens, 40, seed=6)
     split = _launch("split")
-    assert split["chunks"] == 1 and split["passes"] == 3
+    assert split["chunks"] == 1 and split["passes"] == 2
 
 
 def test_one_long_sequence():
@@ -94,7 +122,7 @@ def test_one_long_sequence():
     (the 1024-thread statistics)."""
     _case(1, 32, 8, 128, np.array([40000], np.int32), 40000, seed=7, std=0.5)
     split = _launch("split")
-    assert split["chunks"] > 256 and split["blocks"] > 2048
+    assert split["chunks"] > 256 and split["blocks"] > 2048 and split["passes"] == 4
 
 
 def test_wide_logits():
