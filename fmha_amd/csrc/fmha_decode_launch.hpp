@@ -276,6 +276,35 @@ bool onepass_fits(const SplitArgs& a) {
          fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk)) <= kOnepassMaxLdsPerWave;
 }
 
+// The single pass with two waves per unit (a workgroup sharing one row)
+// for rows with fewer than kOnepassMinUnits units: from 192 units with one
+// or two query heads per KV head and from 384 with four (eight take the
+// matrix cores), if a unit's LDS stays within kOnepassMaxLdsPerGroup.  Two
+// waves against the split passes (µs, D = 128 unless given, packed): B=64
+// S=256 Hq/Hkv 16/16 25.6 / 30.8, B=120 S=128 16/16 26.0 / 28.7, B=200
+// S=256 8/8 38.2 / 42.7, B=100 S=512 16/16 70.4 / 76.7, B=200 S=96 32/8
+// 25.6 / 31.5, D=64 B=64 S=256 32/32 28.1 / 30.9, D=256 B=60 S=160 16/8
+// 17.9 / 23.0 (240 units); fewer units lose (B=128 S=256 32/8, 256 units:
+// 38.9 / 37.0; B=64 S=256 32/8 36.7 / 25.1; B=32 S=1024 16/16 59.2 /
+// 51.4), and four or eight waves per row measured slower than two wherever
+// two applied.  Packed caches, and strided ones up to 16 blocks (BHSD:
+// B=64 S=256 16/16 30.8 / 32.2, B=200 S=96 32/8 25.7 / 31.3, but B=100
+// S=512 16/16 85.1 / 79.2); paged ones keep the split passes (within 1%
+// either way).  FMHA_DECODE_ONEPASS_WAVES=1 turns it off (for sweeps).
+constexpr size_t kOnepassMaxLdsPerGroup = 64 * 1024;
+constexpr int kOnepassGroupNW = 2;
+
+template <int D, int G, int LAYOUT>
+bool onepass_group_fits(const SplitArgs& a) {
+  if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_WAVES"))
+    if (std::atoi(e) == 1) return false;
+  const int64_t units = onepass_waves(a);
+  return G <= 4 && units < kOnepassMinUnits && units >= (G <= 2 ? 192 : 384) && a.nblk >= 2 * kOnepassGroupNW &&
+         (LAYOUT == fmha_decode::kLayoutPacked || a.nblk <= 16) &&
+         fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk, kOnepassGroupNW),
+                                              kOnepassGroupNW) <= kOnepassMaxLdsPerGroup;
+}
+
 template <auto KERNEL>
 hipError_t launch_onepass_kernel(const SplitArgs& a, size_t need, int waves, hipStream_t stream) {
   const size_t cap = lds_reserve_kernel<KERNEL>(waves);
@@ -298,6 +327,17 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
     if (a.nblk <= 4)
       return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI, 2>>(a, need, waves, stream);
   return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI>>(a, need, waves, stream);
+}
+
+// The single pass with kOnepassGroupNW waves per unit, one batch per unit.
+template <int D, int G, int LAYOUT>
+hipError_t launch_onepass_group(const SplitArgs& a, hipStream_t stream) {
+  constexpr int NW = kOnepassGroupNW;
+  const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk, NW), NW);
+  plan_note("onepass_group(D=%d G=%d layout=%s waves_per_row=%d blocks=%d)", D, G, layout_name(LAYOUT), NW, a.nblk);
+  hipLaunchKernelGGL((fmha_decode::onepass_decode_kernel<D, G, LAYOUT, false, 1, NW>), dim3((uint32_t)onepass_waves(a)),
+                     dim3(kBlockThreads * NW), need, stream, a);
+  return hipGetLastError();
 }
 
 
@@ -400,6 +440,12 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
   }
   if (onepass_only) return kOnepassNotTaken;
+  if constexpr (G <= 4 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)) {
+    // Too few units for one wave each: two waves per unit.
+    SplitArgs ag = a;
+    ag.sub_shift = 0;
+    if (onepass_group_fits<D, G, LAYOUT>(ag)) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
+  }
   // P.V sub-block rows (register budget: pages under 16 rows address every
   // row on its own, a descriptor or a 64-bit address per row; 16 rows there
   // leave one wave per SIMD).

@@ -40,19 +40,25 @@ struct OnepassShape {
   static constexpr int NRV = G >= 8 ? 8 : 16;  // V rows per sub-block (register budget)
 };
 
-// LDS row stride for a row bound of nblk 16-row blocks: an even number of
-// blocks, so the loops' paired sub-blocks always have room.
-constexpr int onepass_lds_rows(int nblk) { return (nblk + 1) / 2 * 2 * kSplitBlockRows; }
+// 16-row blocks each of NW waves sharing a row takes (an even number, so
+// the loops' paired sub-blocks always have room), for a row bound of nblk.
+constexpr int onepass_wave_blocks(int nblk, int nw) { return ((nblk + nw - 1) / nw + 1) / 2 * 2; }
+
+// LDS row stride for a row bound of nblk 16-row blocks split over NW waves.
+constexpr int onepass_lds_rows(int nblk, int nw = 1) { return nw * onepass_wave_blocks(nblk, nw) * kSplitBlockRows; }
 
 // LDS strides for sp rows: fp32 scores (floats) and bf16 weights (halves),
 // both an odd number of dwords.
 constexpr int onepass_score_stride(int sp) { return sp + 1; }
 constexpr int onepass_weight_stride(int sp) { return sp + 2; }
 
-// LDS bytes one wave needs for sp rows.
+// LDS bytes of one unit with sp rows: the scores and weights of the row,
+// and with NW > 1 waves the P.V partial sums of waves 1..NW-1 (16-byte
+// aligned after the weights).
 template <int D, int G>
-constexpr size_t onepass_lds_bytes(int sp) {
-  return (size_t)OnepassShape<D, G>::HPW * G * (onepass_score_stride(sp) * 4 + onepass_weight_stride(sp) * 2);
+constexpr size_t onepass_lds_bytes(int sp, int nw = 1) {
+  const size_t rows = (size_t)OnepassShape<D, G>::HPW * G * (onepass_score_stride(sp) * 4 + onepass_weight_stride(sp) * 2);
+  return nw == 1 ? rows : (rows + 15) / 16 * 16 + (size_t)(nw - 1) * kWaveSize * G * 8 * 4;
 }
 
 // MULTI: several batches per wave (fewer KV heads than a wave holds,
@@ -68,9 +74,17 @@ constexpr size_t onepass_lds_bytes(int sp) {
 // 127, B=2730 S=48 145 / 119; but B=1024 S=128 115 / 134).  Elsewhere 2
 // measured equal (one-row pages, packed) or made the compiler spill
 // (several batches per wave).
-template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1>
-__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
+// NW: waves per unit (a workgroup of NW waves, one batch): wave w
+// scores and multiplies rows [w * R, w * R + R) of the row (R =
+// onepass_wave_blocks * 16), the scores of all of them shared through LDS
+// for the softmax (each wave reduces the whole row, in the order one wave
+// would, and forms the weights of its own rows); waves 1..NW-1 hand their
+// P.V sums to wave 0 through LDS, which adds them in wave order.  For rows
+// with too few (batch, KV-head group) units to fill the GPU one wave each.
+template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1, int NW = 1>
+__global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
     SplitArgs a) {
+  static_assert(NW == 1 || !MULTI, "waves sharing a row serve one batch");
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
   constexpr int HPW = P::HPW;
@@ -86,6 +100,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
   extern __shared__ __attribute__((aligned(16))) float onepass_lds[];
 
   const int lane = threadIdx.x & (kWaveSize - 1);
+  const int wv = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWaveSize));
   const int hkl = lane / LPH;
   const int r = lane % LPH;
   const int hq = a.num_heads_q;
@@ -109,6 +124,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
     smax = S;
     if (S <= 0 || S > a.max_rows) {
       // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+      if (wv != 0) return;
       const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b * hq * D, (uint32_t)hq * D * 2);
       const uint32_t qo_off = head_ok ? (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
       const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : nan4;
@@ -164,7 +180,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + (uint64_t)b0 * hq * D, q_bytes);
   const uint32_t qo_off =
       head_ok ? (uint32_t)sub * (uint32_t)hq * D * 2u + (uint32_t)(hk * G * D + r * 8) * 2u : kLaneOutOfRange;
-  const int sp = onepass_lds_rows(a.nblk);
+  const int sp = onepass_lds_rows(a.nblk, NW);
   const int sps = onepass_score_stride(sp);   // floats
   const int spw = onepass_weight_stride(sp);  // halves (even: the P.V reads pairs)
   float* sc = onepass_lds + (size_t)hkl * G * sps;                                          // [G][sps] fp32
@@ -193,7 +209,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
   // ---- 1. scores of every row -> LDS ----
   const int blkl = r >> (NS - L);
   const bool writer = (r & ((1 << (NS - L)) - 1)) == 0;
-  const int nsub = ((smax + NR - 1) / NR + 1) / 2 * 2;  // even
+  // This wave's rows [lo, lo + span): the whole row with NW = 1.
+  const int wrows = onepass_wave_blocks(a.nblk, NW) * NR;
+  const int lo = wv * wrows;
+  const int span = NW == 1 ? smax : (smax - lo < 0 ? 0 : (smax - lo < wrows ? smax - lo : wrows));
+  const int sk0 = lo / NR;                              // first sub-block
+  const int nsub = ((span + NR - 1) / NR + 1) / 2 * 2;  // even
   auto load_k = [&](u32x4 (&kr)[NR], int s) { krows.template load<NR>(kr, s * NR); };
   auto score = [&](const u32x4 (&kr)[NR], int s) {
 #pragma unroll
@@ -219,11 +240,11 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
     // The scheduling barriers keep the compiler from interleaving a refill
     // with the scoring of the other set, which would make it wait for both.
     u32x4 ka[NR], kb[NR];
-    load_k(ka, 0);
+    load_k(ka, sk0);
     __builtin_amdgcn_sched_barrier(0);
-    load_k(kb, 1);
+    load_k(kb, sk0 + 1);
     __builtin_amdgcn_sched_barrier(0);
-    for (int s = 0; s < nsub; s += 2) {
+    for (int s = sk0; s < sk0 + nsub; s += 2) {
       score(ka, s);
       __builtin_amdgcn_sched_barrier(0);
       load_k(ka, s + 2);
@@ -239,13 +260,24 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
   using VBuf = u32x4[NRV];
   VBuf va, vb;
   auto load_v = [&](u32x4 (&vr)[NRV], int s) { vrows.template load<NRV>(vr, s * NRV); };
-  load_v(va, 0);
+  const int sv0 = lo / NRV;  // this wave's first V sub-block
+  load_v(va, sv0);
   __builtin_amdgcn_sched_barrier(0);
-  load_v(vb, 1);
+  load_v(vb, sv0 + 1);
   __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // An unmapped page among rows [0, S) (seen by the K phase, which reads
+  // them all): the batch is invalid (per lane group with MULTI, whose lane
+  // groups serve different batches).
+  bool poisoned;
+  if constexpr (NW == 1) {
+    poisoned = krows.bad != 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    // Every wave's scores are in LDS; any wave's unmapped page poisons the row.
+    poisoned = __syncthreads_or(krows.bad != 0) != 0;
+  }
 
   // ---- 2. softmax per (KV head, query head): lane r takes query head
   // r % G and rows r / G, r / G + LPG, ... ----
@@ -258,17 +290,28 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
 #pragma unroll
     for (int msk = G; msk < LPH; msk <<= 1) m = fmaxf(m, __shfl_xor(m, msk, kWaveSize));
     float l = 0.0f;
-    for (int j = j0; j < S; j += LPG) {
-      const float e = expf(t[j] - m);
-      t[j] = e;
-      l += e;
-    }
-#pragma unroll
-    for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
     uint16_t* p = pw + g * spw;
-    const int pad = (smax + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
-    for (int j = j0; j < pad; j += LPG)
-      p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? t[j] / l : 0.0f)) : (uint16_t)0;
+    if constexpr (NW == 1) {
+      for (int j = j0; j < S; j += LPG) {
+        const float e = expf(t[j] - m);
+        t[j] = e;
+        l += e;
+      }
+#pragma unroll
+      for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
+      const int pad = (smax + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows the V phase reads weights for
+      for (int j = j0; j < pad; j += LPG)
+        p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? t[j] / l : 0.0f)) : (uint16_t)0;
+    } else {
+      // The scores are shared: the exponentials are formed again for this
+      // wave's own rows rather than stored (the same values, the same sum).
+      for (int j = j0; j < S; j += LPG) l += expf(t[j] - m);
+#pragma unroll
+      for (int msk = G; msk < LPH; msk <<= 1) l += __shfl_xor(l, msk, kWaveSize);
+      const int pad = lo + (span + 2 * NRV - 1) / (2 * NRV) * (2 * NRV);  // rows this wave's V phase reads
+      for (int j = lo + j0; j < pad; j += LPG)
+        p[j] = j < S ? __builtin_bit_cast(uint16_t, (__bf16)(l > 0.0f ? expf(t[j] - m) / l : 0.0f)) : (uint16_t)0;
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -280,7 +323,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
-  const int nsv = ((smax + NRV - 1) / NRV + 1) / 2 * 2;  // even
+  const int nsv = ((span + NRV - 1) / NRV + 1) / 2 * 2;  // even
   auto pv = [&](const u32x4 (&vr)[NRV], int s) {
     uint32_t pp[G][NRV / 2];
 #pragma unroll
@@ -291,7 +334,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
     }
     accumulate_pv<G, NRV>(vr, pp, acc);
   };
-  for (int s = 0; s < nsv; s += 2) {
+  for (int s = sv0; s < sv0 + nsv; s += 2) {
     pv(va, s);
     __builtin_amdgcn_sched_barrier(0);
     load_v(va, s + 2);
@@ -301,10 +344,34 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(W
     load_v(vb, s + 3);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // An unmapped page among rows [0, S) (seen by the K phase, which reads
-  // them all): the batch is invalid (per lane group with MULTI, whose lane
-  // groups serve different batches).
-  const bool poisoned = krows.bad != 0;
+  if constexpr (NW > 1) {
+    // Waves 1..NW-1 hand their sums to wave 0 (LDS after the weights),
+    // which adds them in wave order.
+    float* red = reinterpret_cast<float*>(
+        reinterpret_cast<char*>(onepass_lds) +
+        ((size_t)HPW * G * (sps * 4 + spw * 2) + 15) / 16 * 16);
+    if (wv > 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int d = 0; d < 8; d += 4)
+          *reinterpret_cast<float4*>(red + (((size_t)(wv - 1) * G + g) * kWaveSize + lane) * 8 + d) =
+              float4{acc[g][d], acc[g][d + 1], acc[g][d + 2], acc[g][d + 3]};
+    }
+    __syncthreads();
+    if (wv > 0) return;
+    for (int w = 1; w < NW; ++w)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int d = 0; d < 8; d += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(red + (((size_t)(w - 1) * G + g) * kWaveSize + lane) * 8 + d);
+          acc[g][d] += x.x;
+          acc[g][d + 1] += x.y;
+          acc[g][d + 2] += x.z;
+          acc[g][d + 3] += x.w;
+        }
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if constexpr (MULTI)

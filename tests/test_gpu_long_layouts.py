@@ -71,6 +71,26 @@ def test_strided_long(layout, B, cap, D, Hq, Hkv):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} B={B} cap={cap} D={D} Hq={Hq} Hkv={Hkv} ({path})")
 
 
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+@pytest.mark.parametrize("D,Hq,Hkv,B,cap", [(128, 16, 16, 64, 256), (128, 32, 8, 200, 96), (256, 16, 8, 60, 160)])
+def test_strided_onepass_group(layout, D, Hq, Hkv, B, cap):
+    """Strided caches with too few units for one wave each: the single pass
+    with two waves per row (plan onepass_group), NaN padding past each
+    length never read."""
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(B + cap + D + 1)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[:4] = [cap, 0, 1, 33]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=B * 5 + D)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, layout), layout)
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, layout), layout)
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    assert [k for k, _ in last_plan()] == ["onepass_group"], last_plan()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} group B={B} cap={cap} D={D} Hq={Hq} Hkv={Hkv}")
+
+
 def test_strided_uniform_long_bhsd():
     """No lengths array: every batch has all cap rows."""
     import fmha_amd

@@ -125,6 +125,43 @@ def test_one_long_sequence():
     assert split["chunks"] > 256 and split["blocks"] > 2048 and split["passes"] == 4
 
 
+# (B, Hq, Hkv, D, max_len): fewer (batch, KV-head group) units than the
+# one-wave single pass needs, but enough for two waves per row, rows that fit
+# a workgroup's LDS.
+GROUP_CASES = [
+    (64, 16, 16, 128, 256),
+    (200, 32, 8, 128, 96),
+    (100, 16, 16, 128, 512),
+    (64, 32, 32, 64, 256),
+    (60, 16, 8, 256, 160),
+    (96, 8, 8, 128, 64),     # two blocks per wave
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,max_len", GROUP_CASES)
+def test_onepass_group(B, Hq, Hkv, D, max_len):
+    """The single pass with two waves per row: ragged lengths (0, 1, one
+    block, the maximum, one past a wave's rows) and an invalid one (NaN)."""
+    rng = np.random.default_rng(B + max_len + D)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:5] = [max_len, 0, 1, 16, min(max_len, 33)]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + D + 5, std=0.5)
+    assert _launch("onepass_group")["waves_per_row"] == 2
+    bad = seqlens.copy()
+    bad[3] = max_len + 1
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, bad, seed=B + 3)
+    o = oracle.f16_to_f32(_run(q, k, v, cu, Hq, Hkv, D, max_len).reshape(B, Hq, D))
+    assert np.all(np.isnan(o[3])) and np.all(np.isfinite(np.delete(o, 3, axis=0)))
+
+
+def test_onepass_group_off(monkeypatch):
+    """FMHA_DECODE_ONEPASS_WAVES=1: the same rows through the split passes."""
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_WAVES", "1")
+    seqlens = np.random.default_rng(1).integers(0, 257, size=64).astype(np.int32)
+    _case(64, 16, 16, 128, seqlens, 256, seed=41, std=0.5)
+    assert _kinds() == ["split"]
+
+
 def test_wide_logits():
     seqlens = np.array([513, 1, 0, 257], np.int32)
     _case(4, 16, 16, 256, seqlens, 600, seed=8, std=2.0)
@@ -150,7 +187,7 @@ def test_bad_and_empty_lengths():
 
 
 @pytest.mark.parametrize("D,Hq,Hkv,max_len,kind", [(128, 16, 16, 2048, "split"), (128, 32, 8, 8192, "split"),
-                                                   (256, 16, 16, 600, "split"), (64, 16, 2, 64, "split_matrix_core"),
+                                                   (256, 16, 16, 6000, "split"), (64, 16, 2, 64, "split_matrix_core"),
                                                    (128, 32, 8, 64, "split")])
 def test_split_path_still_covered(D, Hq, Hkv, max_len, kind):
     """Few batches: the split-KV launches (VALU, or matrix cores for groups
