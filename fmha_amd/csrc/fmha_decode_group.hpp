@@ -24,8 +24,10 @@
 //     of 4 columns for G <= 4, NS = 2 of 8 for G <= 8, one stream per tile
 //     above (query heads [16c, 16c + 16) of tile c); columns at or past G
 //     are padding that is never stored.  A wave handles HPW / NS tiles;
-//     larger groups take ceil(G / 16) waves per stream group, placed on one
-//     XCD so that their K/V re-reads hit its L2.  The query rows of a wave's
+//     larger groups take ceil(G / 16) waves per stream group, each loading
+//     the K/V of only the streams its tiles use (a stream whose tiles two
+//     waves share is read by both, on one XCD, so that the second read hits
+//     its L2).  The query rows of a wave's
 //     tiles are one contiguous range of Q; each lane loads its column's query
 //     words straight into the B operand (8 dims per MFMA step), so Q takes
 //     no LDS.
@@ -405,7 +407,15 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
     end = (sok && !bad && S > 0) ? (uint32_t)((lane_elem + (int64_t)(S - 1) * a.row_stride + D) * 2) : 0u;
   }
   if (!sok || bad) S = 0;
-  const uint32_t kv_off = (sok && !bad) ? (uint32_t)(lane_elem * 2) + (uint32_t)r * 16u : kLaneOutOfRange;
+  // With one stream per tile and several tiles per stream (G > 16), a
+  // chunk's tiles use only some of the group's streams: the other lanes load
+  // nothing (those streams' K/V belong to another chunk's tiles).
+  const int tps = a.tiles_per_stream;
+  const int tau0 = chunk * TW;
+  const int tau1 = min(tau0 + TW, ((nstreams + NS - 1) / NS) * tps) - 1;
+  const bool used = s >= (tau0 / tps) * NS && s < (tau1 / tps) * NS + NS;
+  const uint32_t kv_off =
+      (sok && !bad && used) ? (uint32_t)(lane_elem * 2) + (uint32_t)r * 16u : kLaneOutOfRange;
   // Descriptor range: the end of the last row any lane reads; bucket: the
   // longest length of the wave; invalid streams as a bit per stream.
   int smax = S;
