@@ -141,6 +141,14 @@ int valu_kernel_group(int g) {
 // 298/260/243/242/252: within 2-8% of each best).
 constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
 constexpr int kInflightBytesPerCUWideGroups = 200 * 1024;
+// The paged 1- and 2-head kernels (one batch per wave) look their pages up
+// before any K/V request and want about half as many waves again: 216 KiB
+// puts the swept shapes within 1% of their best caps (B=30720 D=128, µs
+// for 4/5/6/8/12/16 waves; 16-row pages Hq/Hkv 16/16 S=16
+// 678/653/645/665/682/680, S=8 417/391/379/376/379/379, 32/16 S=4
+// 335/282/250/227/224/227; one-row pages S=16 771/721/693/703/715/721, S=8
+// 470/426/403/382/377/378, 32/16 S=4 358/302/268/234/226/225).
+constexpr int kInflightBytesPerCUPaged = 216 * 1024;
 
 // bucket_per_wave: the kernel picks a bucket per wave (lengths on the
 // device, or several batches per wave), whose 4-head form scores two query
@@ -279,6 +287,10 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   }
   int w = exact ? waves_per_cu_exact(rows16, g, a.group, device_lengths)
                : waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
+  if (layout == fmha_decode::kLayoutPaged && !multi && g <= 2) {
+    const int64_t wp = 16LL * kInflightBytesPerCUPaged / (1024LL * (2LL * rows16 + 32LL * a.group));
+    w = wp >= 16 ? kMaxWavesPerCU : (wp < 3 ? 3 : (int)wp);
+  }
   // Waves that serve several batches (each lane group its own length and
   // rows) want at least 8 per CU at D <= 128 (B=30720 with lengths on the
   // device, µs at the byte model's cap / 8 waves: Hq/Hkv 8/1 S=16 79.0 /
@@ -507,7 +519,8 @@ DecodeArgs base_args(const void* Q, const void* K, const void* V, void* O, int32
 // in [2, 16], averages 4.3 rows, and its best cap is the 4-row one.
 constexpr int kVarlenRowsHint = 4;
 
-// Mean-length feedback for the packed cu_seqlens entry points.  The best
+// Mean-length feedback for the packed cu_seqlens and the paged entry
+// points.  The best
 // wave cap depends on the rows per batch (4-row batches: 8 waves per CU;
 // 16-row batches: 3, 7% faster than under the 4-row cap at B=30720 H=16
 // D=128), which the host cannot read without a synchronisation.  So the
@@ -518,7 +531,13 @@ constexpr int kVarlenRowsHint = 4;
 // by one row per step, so the previous call's mean is a close estimate; a
 // stale or foreign value changes speed, never results.  The word is
 // allocated on the first call that is not being captured into a graph (a
-// capture does not report), never freed, and read without a lock.
+// capture does not report), never freed, and read without a lock.  The
+// paged short kernels report likewise into a second word of the same
+// allocation (kPagedFeedbackWord), the mean of a sample of their lengths
+// (the first 4096): with 16-row pages their best cap follows the rows as
+// the packed kernels' does (B=30720 S=16 Hq/Hkv 16/16, µs at 5 waves per
+// CU / the 4-row cap of 14: 644 / 684).
+constexpr int kPagedFeedbackWord = 8;
 constexpr int kMaxFeedbackDevices = 64;
 std::atomic<int32_t*> g_feedback[kMaxFeedbackDevices];
 std::atomic<bool> g_feedback_failed[kMaxFeedbackDevices];
@@ -544,7 +563,7 @@ int32_t* feedback_word(void* stream, bool may_allocate = true) {
     g_feedback_failed[dev].store(true, std::memory_order_relaxed);
     return nullptr;
   }
-  *static_cast<volatile int32_t*>(host) = 0;
+  for (int i = 0; i < 16; ++i) static_cast<volatile int32_t*>(host)[i] = 0;
   word = static_cast<int32_t*>(mapped);
   g_feedback[dev].store(word, std::memory_order_release);
   return word;
@@ -879,8 +898,11 @@ int paged_short(void* stream, const void* Q, const void* K_cache, const void* V_
   a.head_stride = head_dim_q;
   a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
   a.max_rows = max_rows;
-  return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0,
-                16 * (max_rows < kVarlenRowsHint ? max_rows : kVarlenRowsHint), true);
+  // The paged calls' own feedback word (32 bytes past the packed calls').
+  int32_t* word = feedback_word(stream);
+  a.rows_feedback = word ? word + kPagedFeedbackWord : nullptr;
+  return launch(stream, fmha_decode::kLayoutPaged, a, batch, head_dim_q, 0, feedback_rows16(a.rows_feedback, max_rows),
+                true);
 }
 
 }  // namespace

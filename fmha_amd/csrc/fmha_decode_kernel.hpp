@@ -107,10 +107,11 @@ struct DecodeArgs {
   // 5-7 the G = 8 one, the query heads at or past `group` of each KV head
   // loading and storing nothing (out-of-range offsets).
   int32_t group;
-  // Packed layout with cu offsets only, else null: a word of host-visible
-  // memory where the call's first wave leaves 16 x the mean length,
-  // 16 * (cu[batch] - cu[0]) / batch, for the host to size the next call's
-  // wave cap (the host cannot read the lengths of this one).
+  // Packed layout with cu offsets and paged layout, else null: a word of
+  // host-visible memory where the call's first wave leaves 16 x the mean
+  // length (packed: 16 * (cu[batch] - cu[0]) / batch; paged: of the first
+  // 4096 lengths at most), for the host to size the next call's wave cap
+  // (the host cannot read the lengths of this one).
   int32_t* rows_feedback;
 };
 
@@ -122,6 +123,25 @@ __device__ __forceinline__ void report_mean_rows(const DecodeArgs& a, uint32_t u
     const int64_t mean16 = rows * 16 / (int64_t)batch;
     *a.rows_feedback = (int32_t)(mean16 < 0 ? 0 : (mean16 > 0x7fffffff ? 0x7fffffff : mean16));
   }
+}
+
+// The first wave of a paged call reports 16 x the mean of the first (at
+// most 4096) lengths of lens, each clamped to [0, max_rows], to the host: a
+// sample, 64 loads per lane at most, a butterfly sum, one vector store.
+// Every lane of the wave calls it (unit is the wave's).
+__device__ __forceinline__ void report_mean_rows_sample(const DecodeArgs& a, uint32_t unit, uint32_t batch,
+                                                        int lane) {
+  if (a.rows_feedback == nullptr || unit != 0 || batch == 0) return;
+  const int n = batch < 4096u ? (int)batch : 4096;
+  int sum = 0;
+#pragma unroll 16
+  for (int i = lane; i < n; i += kWaveSize) {
+    const int len = a.lens[i];
+    sum += len < 0 ? 0 : (len > a.max_rows ? a.max_rows : len);
+  }
+#pragma unroll
+  for (int m = 1; m < kWaveSize; m <<= 1) sum += __shfl_xor(sum, m, kWaveSize);
+  if (lane == 0) *a.rows_feedback = (int32_t)((int64_t)sum * 16 / n);
 }
 
 // Byte offset of query head g of the lane's KV head from qo_off (the head's
@@ -148,6 +168,10 @@ struct KVSpan {
   uint32_t page_shift;
   uint64_t page_stride;
   uint32_t row_extent;
+  // kLayoutPaged: pages[0], requested together with the length (every
+  // block-table row has an entry 0), so that a batch in one page waits for
+  // one round trip of scalar loads, not two.
+  int32_t entry0;
 };
 
 __device__ __forceinline__ constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
@@ -165,12 +189,14 @@ __device__ __forceinline__ int32_t load_uniform_i32(const int32_t* p, uint64_t i
 }
 
 // True when rows [0, S) of a batch (S <= 16) use a negative block-table
-// entry: such a batch is invalid (NaN outputs, no row read).
-__device__ __forceinline__ bool paged_rows_unmapped(const int32_t* pages, int S, uint32_t page_shift) {
+// entry: such a batch is invalid (NaN outputs, no row read).  entry0 is
+// pages[0].
+__device__ __forceinline__ bool paged_rows_unmapped(const int32_t* pages, int32_t entry0, int S,
+                                                    uint32_t page_shift) {
   const int n = paged_entries_used(S, page_shift);
-  int32_t sign = 0;
+  int32_t sign = n > 0 ? entry0 : 0;
 #pragma unroll
-  for (int i = 0; i < kMaxSeq; ++i) sign |= i < n ? load_uniform_i32(pages, (uint32_t)i) : 0;
+  for (int i = 1; i < kMaxSeq; ++i) sign |= i < n ? load_uniform_i32(pages, (uint32_t)i) : 0;
   return sign < 0;
 }
 
@@ -948,6 +974,22 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, uint32_t b, con
     }
 #pragma unroll
     for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + row_off[j]);
+  } else if (kv.page_shift >= 4) {
+    static_assert(!exact_taken<G, SMAX, PF32, EXACT>(), "the exact path reads the packed and strided layouts");
+    // Pages of 16 rows or more: rows [0, S) (S <= 16) are slots 0..S-1 of
+    // the batch's first page, one after another, so one entry and one
+    // descriptor per batch cover them (empty for an unmapped entry or S =
+    // 0; rows past S fall outside it and read 0 without access).
+    const int32_t entry = S > 0 ? kv.entry0 : -1;
+    const int64_t el = paged_row_elem(entry, 0u, kv.page_shift, kv.page_stride, kv.row_bytes >> 1);
+    const uint64_t base = el < 0 ? 0u : (uint64_t)el;
+    const uint32_t rec = el < 0 || S <= 0 ? 0u : (uint32_t)(S - 1) * kv.row_bytes + kv.row_extent;
+    const __amdgpu_buffer_rsrc_t kp = make_rsrc(kv.k + base, rec);
+    const __amdgpu_buffer_rsrc_t vp = make_rsrc(kv.v + base, rec);
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) kr[j] = buffer_load16<kPolicyStream>(kp, kv_off + row_off[j]);
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) vr[j] = buffer_load16<kPolicyStream>(vp, kv_off + row_off[j]);
   } else {
     // Row j sits in page pages[j >> page_shift] at slot j & (page_size-1):
     // one descriptor per row, spanning that row's heads, empty past S and
@@ -1018,9 +1060,10 @@ __device__ __forceinline__ bool batch_span(const DecodeArgs& a, uint32_t b, KVSp
     S = UNIFORM ? a.seqlen_uniform : a.lens[b];
     elem0 = (uint64_t)b * (uint64_t)a.batch_stride;
   } else {
+    kv.pages = a.block_table + (uint64_t)b * a.bt_stride;
+    kv.entry0 = load_uniform_i32(kv.pages, 0);
     S = a.lens[b];
     elem0 = 0;
-    kv.pages = a.block_table + (uint64_t)b * a.bt_stride;
     kv.page_shift = (uint32_t)a.seqlen_uniform;  // log2(page_size) for this layout
     kv.page_stride = (uint64_t)a.batch_stride;
     kv.row_extent = ((uint32_t)(a.num_heads_kv - 1) * (uint32_t)a.head_stride + D) * 2u;
@@ -1070,13 +1113,15 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_fwd_kernel(DecodeAr
   uint16_t* lds_wave = lds_p + wave * (HPW * VP * WB + XW);
 
   if constexpr (SB == 0 && LAYOUT == kLayoutPacked) report_mean_rows(a, unit, a.total_units / upb, lane);
+  if constexpr (LAYOUT == kLayoutPaged) report_mean_rows_sample(a, unit, a.total_units / upb, lane);
   KVSpan kv;
   const bool length_ok = batch_span<D, LAYOUT, SB != 0>(a, b, kv);
   // A uniform length was validated on the host; only table lengths can be
   // bad, and on a paged cache a negative block-table entry for a row the
   // batch has.
   bool valid = length_ok;
-  if constexpr (LAYOUT == kLayoutPaged) valid = valid && !paged_rows_unmapped(kv.pages, kv.S, kv.page_shift);
+  if constexpr (LAYOUT == kLayoutPaged)
+    valid = valid && !paged_rows_unmapped(kv.pages, kv.entry0, kv.S, kv.page_shift);
   if (SB == 0 && !valid) {
     decode_bad_length<D, G>(a, b, hk, head_ok, lane);
     return;
@@ -1273,6 +1318,8 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_multi_kernel(Decode
   const uint32_t batch = (uint32_t)a.units_per_batch;
   if constexpr (LAYOUT == kLayoutPacked) {
     if (a.lens) report_mean_rows(a, unit, batch, lane);
+  } else if constexpr (LAYOUT == kLayoutPaged) {
+    report_mean_rows_sample(a, unit, batch, lane);
   }
   const uint32_t b0 = unit << a.sub_shift;
   const uint32_t nb = batch - b0 < (1u << a.sub_shift) ? batch - b0 : (1u << a.sub_shift);

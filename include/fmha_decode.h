@@ -32,13 +32,15 @@
  * the null stream) and may be issued from any number of host threads, with
  * one exception: fmha_decode_fwd_splitkv_noalloc uses one workspace array per
  * GPU, so its calls on one GPU must be ordered (one stream, or synchronised)
- * or they corrupt each other's results.  They allocate no device memory.  The one piece of library state: the entry
- * points that read lengths from a device cu_seqlens_kv array
- * (fmha_decode_fwd, its _fast, _fp32_weights and _exact forms, and
- * fmha_decode_fwd_splitkv up to 16 rows) keep one word of pinned host memory
- * per device (64 bytes, allocated by the first such call that is not being
- * captured into a graph, never freed) in which each call's first wave leaves
- * the call's mean length; the next call sizes its launch (waves per CU) from
+ * or they corrupt each other's results.  They allocate no device memory.
+ * The one piece of library state: the entry points that read lengths from a
+ * device array (fmha_decode_fwd, its _fast, _fp32_weights and _exact forms,
+ * fmha_decode_fwd_splitkv up to 16 rows, and the paged entry points up to 16
+ * rows) keep pinned host memory per device (64 bytes, allocated by the
+ * first such call that is not being captured into a graph, never freed) in
+ * which each call's first wave leaves the call's mean length (paged: of a
+ * sample of up to 4096 lengths), one word for the cu_seqlens calls and one
+ * for the paged ones; the next call sizes its launch (waves per CU) from
  * it.  Results never depend on it.
  *
  * Return value: 0 (hipSuccess) or a hipError_t value.  Arguments are checked
