@@ -27,9 +27,10 @@ Suites:
              D in {128, 256}; all with Poisson lengths in [2, 16]
   gqa        full-size group sizes outside {1, 2, 4, 8} (the reference has
              no GQA): G = 3, 5, 7, 12, MQA G = 32, G = 5 with Poisson
-             lengths, D = 256 with std 2, D = 64; the library's kernel
-             choice runs 1, 4, 5, 8 on the matrix-core kernel and 2, 3, 6, 7
-             on the VALU kernel's padded 4- and 8-head instantiations
+             lengths, G = 6 at D = 256 with std 2, G = 5 at D = 64; the
+             library's kernel choice runs 4 and 5 (G > 8) on the
+             matrix-core kernel and 1, 2, 3, 6, 7, 8 on the VALU kernel's
+             padded 4- and 8-head instantiations
 """
 import argparse
 import json
