@@ -12,7 +12,7 @@
 // kernel's time over it is the share its arithmetic and reductions cost.
 //
 //   stream_ceiling B Hq Hkv S D [--sets N] [--iters N] [--no-write] [--waves W]
-//   (S in {1, 4, 5, 16}; D = 128 with G in {1, 2, 5, 32}, or D = 256 with G = 1)
+//   (S in {1, 4, 5, 16}; D = 128 with G in {1, 2, 5, 8, 32}, or D = 256 with G = 1)
 //
 // Prints one JSON line: median µs per call over --iters calls (HIP events per
 // call, after 5 warm-up calls), algorithmic TB/s with the same byte count as
@@ -180,6 +180,7 @@ bool dispatch(int B, int hq, int hkv, int S, int D, int sets, int iters, int wav
   if (D == 128 && g == 1) return by_len<128, 1, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 2) return by_len<128, 2, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 5) return by_len<128, 5, WRITE>(B, hq, hkv, S, sets, iters, waves);
+  if (D == 128 && g == 8) return by_len<128, 8, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 32) return by_len<128, 32, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 256 && g == 1) return by_len<256, 1, WRITE>(B, hq, hkv, S, sets, iters, waves);
   return false;
@@ -208,7 +209,7 @@ int main(int argc, char** argv) {
   const bool ok = write ? dispatch<true>(B, hq, hkv, S, D, sets, iters, waves)
                         : dispatch<false>(B, hq, hkv, S, D, sets, iters, waves);
   if (!ok) {
-    std::fprintf(stderr, "shape not built into this aid (S in {1,4,5,16}; D=128 with G in {1,2,5,32}, or D=256 with G=1)\n");
+    std::fprintf(stderr, "shape not built into this aid (S in {1,4,5,16}; D=128 with G in {1,2,5,8,32}, or D=256 with G=1)\n");
     return 2;
   }
   return 0;
