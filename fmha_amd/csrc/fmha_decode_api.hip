@@ -188,8 +188,9 @@ int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths,
 // (sequential score sums staged through LDS), so fewer of their waves have
 // requests in flight at a time and the CU needs more of them: 144 KiB of
 // unit bytes per CU with known lengths, 200 KiB with lengths on the device
-// (whose waves also wait for the lengths first); at least 4 waves, 6 for
-// groups of 4 or more, no cap from 16.  Sweep at B=30720 (us, best cap /
+// (whose waves also wait for the lengths first); at least 4 waves, 5 for
+// groups of 2 (C4 with known lengths, µs at 4 / 5 / 6 / 8 waves: 665.8 /
+// 652.7 / 667.1 / 691.4) and 6 for groups of 4 or more, no cap from 16.  Sweep at B=30720 (us, best cap /
 // this model's / the tree-order kernel): known lengths Hq/Hkv 16/16 S=16
 // D=128 613.7 (4) / 613.7 (4) / 610.2, 32/16 S=16 665.0 (4) / 665.0 (4) /
 // 645.6, 32/32 S=16 D=256 2466.9 (4) / 2466.9 (4) / 2481.2, 16/16 S=5
@@ -203,7 +204,7 @@ int waves_per_cu_exact(int rows16, int g, int g_real, bool device_lengths) {
   const int64_t budget = (device_lengths ? 200LL : 144LL) * 1024;
   const int64_t w = 16 * budget / unit_bytes16;
   if (w >= 16) return kMaxWavesPerCU;
-  const int floor_w = g >= 4 ? 6 : 4;
+  const int floor_w = g >= 4 ? 6 : 3 + g;
   return w < floor_w ? floor_w : (int)w;
 }
 
