@@ -508,6 +508,80 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
   }
 }
 
+// The matrix-core single pass (onepass_mfma_kernel): NW waves per (batch,
+// KV head), for groups of at most 16 query heads per KV head (after
+// padding) on packed and strided caches, rows of at least 8 blocks and at
+// least 512 units.  Against the matrix-core split passes (µs, packed, B x
+// Hq/Hkv x S; NW = 1 / 2 / 4 / split):
+//   D = 128: 1024 x 64/8 x 160: 127.9 / 156.1 / 166.7 / 145.9; x 256:
+//   199.7 / 191.6 / 205.9 / 220.4; 512 x 64/8 x 512: 200.8 / 189.3 / 258.0
+//   / 220.0; 256 x 64/8 x 1024: 255.5 / 202.4 / 217.2 / 219.1; x 1536:
+//   468.9 / 484.6 / 299.2 / 360.7; 128 x 64/8 x 2048: 588.9 / 320.3 / 195.8
+//   / 223.1; 512 x 16/1 x 600: 52.9 / 36.9 / 43.8 / 66.1; 512 x 128/8 x 512
+//   (G = 16): 250.8 / 216.6 / 259.9 / 252.2; 64 x 96/8 x 300 (G = 12): 36.7
+//   / 30.4 / 38.2 / 46.9;
+//   D = 256: 256 x 32/4 x 500: 85.3 / 102.5 / 104.6 / 100.6;
+//   D = 64: 600 x 8/1 x 1200: 145.5 / 81.3 / 81.7 / 68.4 (kept on split).
+// So at D = 128 one wave per row up to 12 blocks, two while a workgroup's
+// LDS stays within 80 KiB (two workgroups per CU), four while it stays
+// within 144 KiB; at D = 256 one wave within 80 KiB.
+// FMHA_DECODE_ONEPASS_MFMA=0 turns it off and =1, 2, 4 forces the waves
+// per row wherever the LDS fits (for sweeps).
+constexpr int64_t kOnepassMfmaMinUnits = 512;
+constexpr int kOnepassMfmaMinBlocks = 8;
+
+// Waves per row of the matrix-core single pass for a, or 0 where it does
+// not apply.
+template <int D, int LAYOUT>
+int onepass_mfma_waves(const SplitArgs& a) {
+  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
+    return 0;
+  } else {
+    const int g = a.num_heads_q / a.num_heads_kv;
+    const int64_t units = (int64_t)a.batch * a.num_heads_kv;
+    if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
+    auto lds = [&](int nw) { return fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw); };
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_MFMA")) {
+      const int v = std::atoi(e);
+      if (v == 0) return 0;
+      if (v == 1 || v == 2 || v == 4) return lds(v) <= 160 * 1024 ? v : 0;
+    }
+    if (a.nblk < kOnepassMfmaMinBlocks) return 0;
+    if constexpr (D == 128) {
+      if (a.nblk <= 12) return lds(1) <= 80 * 1024 ? 1 : 0;
+      if (lds(2) <= 80 * 1024) return 2;
+      return lds(4) <= 144 * 1024 ? 4 : 0;
+    } else if constexpr (D == 256) {
+      return lds(1) <= 80 * 1024 ? 1 : 0;
+    } else {
+      return 0;
+    }
+  }
+}
+
+template <int D, int LAYOUT>
+hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
+  const int g = a.num_heads_q / a.num_heads_kv;
+  const size_t need = fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw);
+  plan_note("onepass_matrix_core(D=%d G=%d layout=%s waves_per_row=%d blocks=%d)", D, g, layout_name(LAYOUT), nw,
+            a.nblk);
+  const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));
+  switch (nw) {
+    case 1:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 1, LAYOUT>), grid, dim3(kBlockThreads), need, stream, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 4, LAYOUT>), grid, dim3(kBlockThreads * 4), need, stream,
+                         a);
+      break;
+    default:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 2, LAYOUT>), grid, dim3(kBlockThreads * 2), need, stream,
+                         a);
+      break;
+  }
+  return hipGetLastError();
+}
+
 // Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
 // are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
 // size.  Scores, the statistics pass for rows of more than kPvStatBlocks
@@ -516,6 +590,8 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
 // 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
 template <int D, int LAYOUT>
 hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
+  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+    if (const int nw = onepass_mfma_waves<D, LAYOUT>(a)) return launch_onepass_mfma<D, LAYOUT>(a, nw, stream);
   constexpr int HPW = kWaveSize / (D / 8);
   constexpr int TW = D == 256 ? 1 : 2;
   const int64_t g = a.num_heads_q / a.num_heads_kv;

@@ -366,4 +366,239 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Single pass on the matrix cores: one (batch, KV head) per workgroup of NW
+// waves, all of its query heads in one 16-column tile (G <= 16), K and V
+// read once and nothing else in memory.
+// ---------------------------------------------------------------------------
+// Rows a wave takes (a multiple of the HPW 16-row blocks one round stages),
+// for a row bound of nblk 16-row blocks split over NW waves.
+template <int D>
+constexpr int onepass_mfma_wave_rows(int nblk, int nw) {
+  constexpr int RR = GroupShape<D>::HPW * kSplitBlockRows;
+  return ((nblk * kSplitBlockRows + nw * RR - 1) / (nw * RR)) * RR;
+}
+// LDS bytes of one workgroup: the row's fp32 scores ([G][rows + 4], the
+// stride off the bank period), the waves' (max, sum) per query column, and
+// per wave the K rows / V transpose staging of the matrix-core passes.
+template <int D>
+constexpr size_t onepass_mfma_lds_bytes(int g, int nblk, int nw) {
+  return (size_t)g * (nw * onepass_mfma_wave_rows<D>(nblk, nw) + 4) * 4 + (size_t)nw * 16 * 2 * 4 +
+         (size_t)nw * GroupShape<D>::KV_LDS;
+}
+
+// Wave w scores rows [w R, w R + R) of the row (R = onepass_mfma_wave_rows)
+// a round of HPW 16-row blocks at a time, as the split scores pass does (K
+// rows staged in LDS, S^T = K_blk . Q^T on v_mfma_f32_16x16x32_bf16), into
+// the workgroup's LDS, keeping per query column a running max and sum of
+// exponentials; the next round's K rows are in flight during a round's
+// products.  The waves exchange their (max, sum) per column and combine
+// them in wave order; each wave then walks V over its rows as the split
+// P.V pass does (V^T staged in LDS with v_perm, bf16(exp(t - max) / sum)
+// weights as the A operand of v_mfma_f32_16x16x16_bf16), and waves 1..NW-1
+// hand their sums to wave 0 through their own staging, which adds them in
+// wave order and writes fp16 O.  Packed and strided layouts.
+template <int D, int NW, int LAYOUT>
+__global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  constexpr int NR = kSplitBlockRows;
+  constexpr int DPC = Sh::DPC;
+  constexpr int RR = HPW * NR;  // rows per round
+  extern __shared__ __attribute__((aligned(16))) char onepass_mfma_lds[];
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWaveSize));
+  const uint32_t hkv = (uint32_t)a.num_heads_kv;
+  const uint32_t b = blockIdx.x / hkv;
+  const uint32_t hk = blockIdx.x - b * hkv;
+  if (b >= (uint32_t)a.batch) return;
+  const int hq = a.num_heads_q;
+  const int G = hq / (int)hkv;  // <= 16
+  const int S = split_len_l<LAYOUT>(a, b);
+  const int q = lane >> 4;   // MFMA lane group
+  const int n = lane & 15;   // MFMA row / column: this lane's query column
+  const int s = lane / LPH;  // load lane group: block s of each round
+  const int r = lane % LPH;
+  const bool gok = n < G;
+  const __amdgpu_buffer_rsrc_t o_rsrc =
+      make_rsrc(a.o + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  if (S <= 0 || S > a.max_rows) {
+    // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+    if (wv != 0) return;
+    const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+    for (int k = lane; k < G * (D / 8); k += kWaveSize)
+      buffer_store16(o_rsrc, (uint32_t)((k / (D / 8)) * D + (k % (D / 8)) * 8) * 2u, fill);
+    return;
+  }
+  const int wrows = onepass_mfma_wave_rows<D>(a.nblk, NW);
+  const int sps = NW * wrows + 4;  // floats per query column
+  float* sc = reinterpret_cast<float*>(onepass_mfma_lds);
+  float* pst = sc + (size_t)G * sps;  // [NW][16][2]
+  char* stage = reinterpret_cast<char*>(pst + NW * 16 * 2) + (size_t)wv * Sh::KV_LDS;
+  const int lo = wv * wrows;  // this wave's first row
+  const int span = S - lo < 0 ? 0 : (S - lo < wrows ? S - lo : wrows);
+  const int rounds = (span + RR - 1) / RR;
+
+  // ---- K: scores of rows [lo, lo + span) -> sc, running (max, sum) ----
+  GroupRows<D, LAYOUT> kv;
+  kv.init(a, a.k, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
+  const __amdgpu_buffer_rsrc_t q_rsrc =
+      make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  bf16x8_v qb[Sh::QLD];
+#pragma unroll
+  for (int cc = 0; cc < Sh::QLD; ++cc)
+    qb[cc] = __builtin_bit_cast(
+        bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, gok ? (uint32_t)(n * D + (4 * cc + q) * 8) * 2u : kLaneOutOfRange));
+  u32x4 kr[NR];
+  kv.template load<NR>(kr, lo);
+  float rm = -__builtin_inff(), rl = 0.0f;  // this lane's rows of column n
+  for (int k = 0; k < rounds; ++k) {
+    const int j0 = lo + k * RR;
+    wave_lds_sync();  // the previous round's reads of the staging are done
+#pragma unroll
+    for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(stage + j * Sh::KS + s * D * 2 + r * 16) = kr[j];
+    wave_lds_sync();
+    __builtin_amdgcn_sched_barrier(0);
+    // The next round's rows are in flight during this round's products
+    // (past the wave's rows: rows read 0 without access, or another wave's
+    // rows, never used).
+    if (k + 1 < rounds) kv.template load<NR>(kr, j0 + RR);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < HPW; ++p) {
+      const int jb = j0 + p * NR;
+      if (jb >= lo + span) break;
+      f32x4_v c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cc = 0; cc < Sh::QLD; ++cc) {
+        const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(stage + n * Sh::KS + p * D * 2 + (4 * cc + q) * 16);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[cc], c4, 0, 0, 0);
+      }
+      float x[4];
+      float bm = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = c4[e] * a.scale;
+        bm = jb + 4 * q + e < S ? fmaxf(bm, x[e]) : bm;
+      }
+      if (gok)
+        *reinterpret_cast<float4*>(sc + (size_t)n * sps + jb + 4 * q) = float4{x[0], x[1], x[2], x[3]};
+      const float mn = fmaxf(rm, bm);
+      float bs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bs += jb + 4 * q + e < S ? expf(x[e] - mn) : 0.0f;
+      rl = rl * (rm == mn ? 1.0f : expf(rm - mn)) + bs;
+      rm = mn;
+    }
+  }
+  // The wave's (max, sum) per column: over its four lane groups, then
+  // through LDS over the waves, in wave order.
+  {
+    const float cm = column_reduce<true>(rm);
+    const float cl = column_reduce<false>(rl * (rm == cm ? 1.0f : expf(rm - cm)));
+    if (q == 0) {
+      pst[(wv * 16 + n) * 2] = cm;
+      pst[(wv * 16 + n) * 2 + 1] = cl;
+    }
+  }
+  // V rows of the wave's first round, in flight across the exchange.
+  GroupRows<D, LAYOUT> vrows;
+  vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
+  u32x4 vr[NR];
+  vrows.template load<NR>(vr, lo);
+  __syncthreads();
+  float gm = -__builtin_inff();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) gm = fmaxf(gm, pst[(w * 16 + n) * 2]);
+  float gl = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float m = pst[(w * 16 + n) * 2];
+    gl += m == -__builtin_inff() ? 0.0f : pst[(w * 16 + n) * 2 + 1] * (m == gm ? 1.0f : expf(m - gm));
+  }
+
+  // ---- V: rows [lo, lo + span), weights from sc ----
+  f32x4_v acc[DPC];
+#pragma unroll
+  for (int dt = 0; dt < DPC; ++dt) acc[dt] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = 0; k < rounds; ++k) {
+    const int j0 = lo + k * RR;
+    wave_lds_sync();  // the previous round's reads of the staging are done
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 wv4;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const int j = 8 * half + 2 * pp;
+          wv4[pp] = __builtin_amdgcn_perm((uint32_t)vr[j + 1][e / 2], (uint32_t)vr[j][e / 2],
+                                          (e & 1) ? kPermHi : kPermLo);
+        }
+        *reinterpret_cast<u32x4*>(stage + s * Sh::VSTREAM + r * Sh::VB + e * (NR * 2) + half * 16) = wv4;
+      }
+    }
+    wave_lds_sync();
+    if (k + 1 < rounds) vrows.template load<NR>(vr, j0 + RR);
+#pragma unroll
+    for (int p = 0; p < HPW; ++p) {
+      const int jb = j0 + p * NR;
+      if (jb >= lo + span) break;
+      const char* vs = stage + p * Sh::VSTREAM;
+      bf16x4_v vb[DPC];
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const int dim = n * DPC + dt;
+        vb[dt] = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (NR * 2) + q * 8);
+      }
+      const float4 t4 = gok ? *reinterpret_cast<const float4*>(sc + (size_t)n * sps + jb + 4 * q)
+                            : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float tt[4] = {t4.x, t4.y, t4.z, t4.w};
+      bf16x4_v pa;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool valid = gok && jb + 4 * q + e < S;
+        pa[e] = (__bf16)(valid ? expf(tt[e] - gm) / gl : 0.0f);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[dt], acc[dt], 0, 0, 0);
+    }
+  }
+
+  // ---- waves 1..NW-1 -> wave 0 (each through its own staging) ----
+  if constexpr (NW > 1) {
+    wave_lds_sync();
+    if (wv > 0) {
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt)
+        *reinterpret_cast<f32x4_v*>(stage + ((size_t)dt * kWaveSize + lane) * 16) = acc[dt];
+    }
+    __syncthreads();
+    if (wv > 0) return;
+    for (int w = 1; w < NW; ++w) {
+      const char* ws = reinterpret_cast<char*>(pst + NW * 16 * 2) + (size_t)w * Sh::KV_LDS;
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const f32x4_v x = *reinterpret_cast<const f32x4_v*>(ws + ((size_t)dt * kWaveSize + lane) * 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[dt][e] += x[e];
+      }
+    }
+  }
+  // Lane (q, n) holds query rows 4q..4q+3, dims [n DPC, n DPC + DPC).
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int g = 4 * q + e;
+    float v[DPC];
+#pragma unroll
+    for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[dt][e];
+    store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
+  }
+}
+
 }  // namespace fmha_decode

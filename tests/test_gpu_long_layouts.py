@@ -91,6 +91,25 @@ def test_strided_onepass_group(layout, D, Hq, Hkv, B, cap):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} group B={B} cap={cap} D={D} Hq={Hq} Hkv={Hkv}")
 
 
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+def test_strided_onepass_matrix_core(layout):
+    """Strided caches, 8 query heads per KV head, 512 (batch, KV head)
+    units: the matrix-core single pass (plan onepass_matrix_core)."""
+    import fmha_amd
+    import torch
+    B, Hq, Hkv, D, cap = 128, 32, 4, 128, 400
+    rng = np.random.default_rng(77)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[:4] = [cap, 0, 1, 65]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=78)
+    kc = _strided_view(_strided_cache(kp, seqlens, cap, Hkv, D, layout), layout)
+    vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, layout), layout)
+    o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    torch.cuda.synchronize()
+    assert [k for k, _ in last_plan()] == ["onepass_matrix_core"], last_plan()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} matrix-core single pass")
+
+
 def test_strided_uniform_long_bhsd():
     """No lengths array: every batch has all cap rows."""
     import fmha_amd

@@ -84,9 +84,11 @@ STAT_CASES = [
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,max_len,kind,passes", STAT_CASES)
-def test_block_statistics_in_pv(B, Hq, Hkv, D, max_len, kind, passes):
+def test_block_statistics_in_pv(monkeypatch, B, Hq, Hkv, D, max_len, kind, passes):
     """The P.V waves' own reduction of the block statistics, at and past its
-    64-block limit, with ragged lengths (0, 1, one block, the maximum)."""
+    64-block limit, with ragged lengths (0, 1, one block, the maximum); the
+    matrix-core single pass off (FMHA_DECODE_ONEPASS_MFMA=0)."""
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", "0")
     rng = np.random.default_rng(B + max_len + Hq)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[:4] = [max_len, 0, 1, 16]
@@ -160,6 +162,55 @@ def test_onepass_group_off(monkeypatch):
     seqlens = np.random.default_rng(1).integers(0, 257, size=64).astype(np.int32)
     _case(64, 16, 16, 128, seqlens, 256, seed=41, std=0.5)
     assert _kinds() == ["split"]
+
+
+# (B, Hq, Hkv, D, max_len, waves, force): the matrix-core single pass (8 to
+# 16 query heads per KV head after padding, at least 512 (batch, KV head)
+# units, a row's scores within a workgroup's LDS) with the waves per row the
+# planner picks (one up to 12 blocks and at D = 256, two, four on long rows)
+# or that FMHA_DECODE_ONEPASS_MFMA forces (D = 64 stays on the split passes
+# by default).
+MFMA_ONEPASS_CASES = [
+    (256, 64, 8, 128, 1024, 2, None),   # G = 8
+    (512, 16, 1, 128, 600, 2, None),    # G = 16, one KV head
+    (128, 40, 8, 128, 700, 2, None),    # G = 5 on a group padded to 8
+    (64, 96, 8, 128, 300, 2, None),     # G = 12 on a group padded to 16
+    (600, 16, 2, 128, 150, 1, None),    # 10 blocks: one wave
+    (512, 8, 1, 128, 1600, 4, None),    # 100 blocks: four waves
+    (256, 32, 4, 256, 500, 1, None),    # D = 256
+    (600, 8, 1, 64, 1200, 2, "2"),      # D = 64, forced
+    (300, 16, 2, 128, 200, 4, "4"),     # four waves on a short row
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,max_len,waves,force", MFMA_ONEPASS_CASES)
+def test_onepass_matrix_core(monkeypatch, B, Hq, Hkv, D, max_len, waves, force):
+    """Groups of 8-16 query heads on the matrix-core single pass (1, 2 or 4
+    waves per (batch, KV head)): ragged lengths (0, 1, one block, a round's
+    rows and one past them, the maximum) and an invalid one (NaN)."""
+    if force:
+        monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", force)
+    else:
+        monkeypatch.delenv("FMHA_DECODE_ONEPASS_MFMA", raising=False)
+    rng = np.random.default_rng(B + max_len + D + Hq)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:6] = [max_len, 0, 1, 16, min(max_len, 64), min(max_len, 65)]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + D + Hq, std=0.5)
+    assert _launch("onepass_matrix_core")["waves_per_row"] == waves
+    bad = seqlens.copy()
+    bad[3] = max_len + 1
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, bad, seed=B + 9)
+    o = oracle.f16_to_f32(_run(q, k, v, cu, Hq, Hkv, D, max_len).reshape(B, Hq, D))
+    assert np.all(np.isnan(o[3])) and np.all(np.isfinite(np.delete(o, 3, axis=0)))
+
+
+def test_onepass_matrix_core_off(monkeypatch):
+    """FMHA_DECODE_ONEPASS_MFMA=0: the same rows through the matrix-core
+    split passes."""
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", "0")
+    seqlens = np.random.default_rng(2).integers(0, 1025, size=256).astype(np.int32)
+    _case(256, 64, 8, 128, seqlens, 1024, seed=42, std=0.5)
+    assert _kinds() == ["split_matrix_core"]
 
 
 def test_wide_logits():
