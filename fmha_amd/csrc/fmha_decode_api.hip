@@ -384,7 +384,10 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
 // D=256 B=16 64/8 115 vs 108, 40/8 236 vs 227; BHSD 64/8 B=8 260 vs 211;
 // 16-row pages 250 vs 233; one-row pages 64/8 B=64 273 vs 381 (the VALU
 // passes' per-row descriptors against per-lane addresses), 8/1 92 vs 66.
-// At G = 4 the VALU passes stay faster (B=64 S=4096 32/8 189 vs 206).
+// At G = 4 the VALU split passes stay faster (B=64 S=4096 32/8 189 vs 206);
+// groups of at most 4 on rows the one-wave single pass does not hold take
+// the register single pass on the matrix cores from the VALU launcher
+// (launch_split_dg) where it applies.
 // FMHA_DECODE_GQA_KERNEL=valu keeps every G on the VALU passes (G > 8 on
 // ceil(G / 8) launch KV heads of 8 query heads), =mfma puts every G on the
 // matrix cores.
@@ -1035,9 +1038,9 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
                             a.max_rows)) {
     // Groups of 5-8 on rows that the VALU single pass holds (enough waves,
     // a row's scores in LDS, every lane group busy) take it on rows of at
-    // most 128 at D = 128 and 256 and any it holds at D = 64 (with several
-    // batches per wave: 96 at D = 128, 64 at D = 64, 128 at D = 256): one
-    // launch against four (µs, packed,
+    // most 64 at D = 128, 128 at D = 256 and any it holds at D = 64 (with
+    // several batches per wave: 96 at D = 128, 64 at D = 64, 128 at D =
+    // 256; launch_split_dg's onepass_only): one launch against four (µs, packed,
     // D = 128 unless given, matrix-core split vs single pass: B=16384 S=24
     // Hq/Hkv 64/8 486 vs 332, B=4096 S=64 64/8 230 vs 204, B=2048 S=128
     // 225 vs 221, D=256 B=1024 S=128 48/8 246 vs 207, D=64 B=12288 S=32

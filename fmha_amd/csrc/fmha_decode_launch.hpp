@@ -366,6 +366,145 @@ hipError_t launch_unpad_output_group(const uint16_t* op, uint16_t* o, uint64_t s
 // does not apply (nothing launched).
 constexpr hipError_t kOnepassNotTaken = hipErrorNotReady;
 
+// The matrix-core single pass with the row's scores in LDS
+// (onepass_mfma_kernel): NW waves per (batch, KV head), for groups of at
+// most 16 query heads per KV head (after padding) on packed and strided
+// caches, rows of at least 8 blocks and at least 512 units, where the
+// register single pass below does not apply (D = 256; D = 128 rows beyond
+// its 2048).  Against the matrix-core split passes (µs, packed, B x Hq/Hkv
+// x S; NW = 1 / 2 / 4 / split):
+//   D = 128: 1024 x 64/8 x 160: 127.9 / 156.1 / 166.7 / 145.9; x 256:
+//   199.7 / 191.6 / 205.9 / 220.4; 512 x 64/8 x 512: 200.8 / 189.3 / 258.0
+//   / 220.0; 256 x 64/8 x 1024: 255.5 / 202.4 / 217.2 / 219.1; x 1536:
+//   468.9 / 484.6 / 299.2 / 360.7; 128 x 64/8 x 2048: 588.9 / 320.3 / 195.8
+//   / 223.1; 512 x 16/1 x 600: 52.9 / 36.9 / 43.8 / 66.1; 512 x 128/8 x 512
+//   (G = 16): 250.8 / 216.6 / 259.9 / 252.2; 64 x 96/8 x 300 (G = 12): 36.7
+//   / 30.4 / 38.2 / 46.9;
+//   D = 256: 256 x 32/4 x 500: 85.3 / 102.5 / 104.6 / 100.6 (the register
+//   single pass: 93.2 with 16 tiles per wave, 96.4 with 8);
+//   D = 64: 600 x 8/1 x 1200: 145.5 / 81.3 / 81.7 / 68.4.
+// So at D = 128 one wave per row up to 12 blocks, two while a workgroup's
+// LDS stays within 80 KiB (two workgroups per CU), four while it stays
+// within 144 KiB; at D = 256 one wave within 80 KiB.
+// FMHA_DECODE_ONEPASS_MFMA=0 turns it off and =1, 2, 4 forces the waves
+// per row wherever the LDS fits (for sweeps).
+constexpr int64_t kOnepassMfmaMinUnits = 512;
+constexpr int kOnepassMfmaMinBlocks = 8;
+
+// Waves per row of the matrix-core single pass for a, or 0 where it does
+// not apply.
+template <int D, int LAYOUT>
+int onepass_mfma_waves(const SplitArgs& a) {
+  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
+    return 0;
+  } else {
+    const int g = a.num_heads_q / a.num_heads_kv;
+    const int64_t units = (int64_t)a.batch * a.num_heads_kv;
+    if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
+    auto lds = [&](int nw) { return fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw); };
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_MFMA")) {
+      const int v = std::atoi(e);
+      if (v == 0) return 0;
+      if (v == 1 || v == 2 || v == 4) return lds(v) <= 160 * 1024 ? v : 0;
+    }
+    if (a.nblk < kOnepassMfmaMinBlocks) return 0;
+    if constexpr (D == 128) {
+      if (a.nblk <= 12) return lds(1) <= 80 * 1024 ? 1 : 0;
+      if (lds(2) <= 80 * 1024) return 2;
+      return lds(4) <= 144 * 1024 ? 4 : 0;
+    } else if constexpr (D == 256) {
+      return lds(1) <= 80 * 1024 ? 1 : 0;
+    } else {
+      return 0;
+    }
+  }
+}
+
+template <int D, int LAYOUT>
+hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
+  const int g = a.num_heads_q / a.num_heads_kv;
+  const size_t need = fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw);
+  plan_note("onepass_matrix_core(D=%d G=%d layout=%s waves_per_row=%d blocks=%d)", D, g, layout_name(LAYOUT), nw,
+            a.nblk);
+  const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));
+  switch (nw) {
+    case 1:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 1, LAYOUT>), grid, dim3(kBlockThreads), need, stream, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 4, LAYOUT>), grid, dim3(kBlockThreads * 4), need, stream,
+                         a);
+      break;
+    default:
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 2, LAYOUT>), grid, dim3(kBlockThreads * 2), need, stream,
+                         a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+// The matrix-core single pass with the row's scores in registers
+// (onepass_mfma_reg_kernel): workgroups of ceil(nblk / TPW) <= 8 waves, TPW
+// 16-row tiles per wave (8 up to 32 blocks, else 16), for groups of at most
+// 16 query heads per KV head (after padding), at least
+// kOnepassMfmaMinUnits (batch, KV head) units and kOnepassRegMinBlocks
+// blocks on packed and strided caches, D = 64 and 128.  Against the LDS single pass at its best waves per row
+// (µs, packed, D = 128, B x Hq/Hkv x S): 256 x 64/8 x 1024 173.7 / 202.6,
+// 512 x 64/8 x 512 179.2 / 189.7, 1024 x 64/8 x 256 188.9 / 190.7, 128 x
+// 64/8 x 2048 174.5 / 194.7, 256 x 64/8 x 1536 261.9 / 297.8, 512 x 16/1 x
+// 600 31.5 / 36.6, 512 x 128/8 x 512 188.1 / 216.5, 64 x 96/8 x 300 26.0 /
+// 30.4, 1024 x 64/8 x 160 123.9 / 127.7, 4096 x 8/1 x 256 91.1 / 99.1 (x
+// 128: 97.6 / 95.4); against the split passes at D = 64: 2048 x 64/8 x 256
+// 206.4 / 274.3, 1024 x 32/4 x 512 106.3 / 142.0, 4096 x 32/4 x 128 101.8 /
+// 147.6, 600 x 8/1 x 1200 65.1 / 68.4.  Eight tiles per wave against 16
+// (same shapes): 179.0 / 173.7, 179.2 / 183.3, 188.9 / 186.9, 34.1 / 31.5,
+// 188.1 / 190.3, 26.0 / 32.4, 123.9 / 125.4.  D = 256 keeps the LDS single
+// pass.  FMHA_DECODE_ONEPASS_REG=0 turns it off, =8 or 16 forces the tiles
+// per wave (D = 256 included, for sweeps).
+constexpr int kOnepassRegMaxWaves = 8;
+// Rows of fewer blocks keep the split passes (three blocks: µs, 8/8
+// B=200 S=40, 14.1 against 13.1).
+constexpr int kOnepassRegMinBlocks = 4;
+
+// Tiles per wave of the register single pass for a, or 0 where it does not
+// apply.
+template <int D, int LAYOUT>
+int onepass_reg_tiles(const SplitArgs& a) {
+  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
+    return 0;
+  } else {
+    const int g = a.num_heads_q / a.num_heads_kv;
+    const int64_t units = (int64_t)a.batch * a.num_heads_kv;
+    if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
+    int tpw = a.nblk <= 32 ? 8 : 16;
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG"))
+      tpw = std::atoi(e);
+    else if (D == 256 || a.nblk < kOnepassRegMinBlocks)
+      return 0;
+    if (tpw != 8 && tpw != 16) return 0;
+    const int nw = (a.nblk + tpw - 1) / tpw;
+    return nw <= kOnepassRegMaxWaves && fmha_decode::onepass_reg_lds_bytes<D>(nw) <= 160 * 1024 ? tpw : 0;
+  }
+}
+
+template <int D, int LAYOUT>
+hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
+  const int g = a.num_heads_q / a.num_heads_kv;
+  const int nw = (a.nblk + tpw - 1) / tpw;
+  const size_t need = fmha_decode::onepass_reg_lds_bytes<D>(nw);
+  plan_note("onepass_matrix_core_regs(D=%d G=%d layout=%s waves_per_row=%d tiles_per_wave=%d blocks=%d)", D, g,
+            layout_name(LAYOUT), nw, tpw, a.nblk);
+  const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));
+  const dim3 block((uint32_t)(kBlockThreads * nw));
+  if (tpw == 8)
+    hipLaunchKernelGGL((fmha_decode::onepass_mfma_reg_kernel<D, 8, kOnepassRegMaxWaves, LAYOUT>), grid, block, need,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((fmha_decode::onepass_mfma_reg_kernel<D, 16, kOnepassRegMaxWaves, LAYOUT>), grid, block, need,
+                       stream, a);
+  return hipGetLastError();
+}
+
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
 // onepass_only: launch the single pass if it applies with every lane group
 // busy, on rows of at most eight 16-row blocks at D = 128 and 256 (with
@@ -412,13 +551,19 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
     ao.units_per_batch = (a.num_heads_kv + (HPW >> ao.sub_shift) - 1) / (HPW >> ao.sub_shift);
     // onepass_only: waves with no idle lane groups, on rows up to where the
-    // single pass measured faster than the matrix-core split: four 16-row
-    // blocks at D = 64, six at D = 128 (with several batches per wave) and
-    // eight otherwise (µs, Hq/Hkv 8/1, single pass against split: packed
-    // D=128 B=16384 S=64 105 / 121, B=10922 S=96 110 / 123, B=8192 S=128 140
-    // / 117; D=64 B=21845 S=96 150 / 138; BHSD D=256 B=21845 S=24 137 / 184,
-    // D=128 B=43690 S=24 142 / 161, D=64 B=43690 S=48 150 / 176).
-    const int only_nblk = shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : 8);
+    // single pass measured faster than the matrix-core passes: four 16-row
+    // blocks at D = 64, six at D = 128 (with several batches per wave, and
+    // with one on packed and strided caches, where the register single pass
+    // takes longer rows) and eight otherwise (µs, single pass against the
+    // matrix cores: Hq/Hkv 8/1 packed D=128 B=16384 S=64 105 / 121 split,
+    // B=10922 S=96 110 / 123, B=8192 S=128 140 / 117; D=64 B=21845 S=96 150
+    // / 138; BHSD D=256 B=21845 S=24 137 / 184, D=128 B=43690 S=24 142 /
+    // 161, D=64 B=43690 S=48 150 / 176; 64/8 D=128 against the register
+    // single pass B=4096 S=64 205 / 211, B=2730 S=96 205 / 202, B=2048 S=128
+    // 221 / 199).
+    constexpr bool kRegRows = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided);
+    const int only_nblk =
+        shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : kRegRows ? 6 : 8);
     if (onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
@@ -441,10 +586,28 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
   }
   if (onepass_only) return kOnepassNotTaken;
   if constexpr (G <= 4 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)) {
-    // Too few units for one wave each: two waves per unit.
+    // Rows the one-wave single pass does not hold, of at least 4 blocks,
+    // with enough (batch, KV head) units: the matrix-core single pass, its
+    // query tile mostly padding; one query head per KV head keeps the
+    // two-wave single pass where that applies (µs, packed, D = 128, against
+    // the split passes or the two-wave single pass: B=128 S=256 32/8 25.7 /
+    // 37.1, B=256 S=512 89.2 / 99.3, B=128 S=1024 88.9 / 101.9, B=64 S=2048
+    // 89.2 / 103.7, 16/4 B=128 S=256 17.0 / 25.8, B=256 S=64 12.7 / 17.1,
+    // 8/2 B=512 S=128 16.5 / 25.0, 32/8 B=200 S=96 19.2 / 25.7, 32/16 B=64
+    // S=256 25.0 / 28.9, B=64 S=2048 170.6 / 177.7, 16/16 B=64 S=2048 170.3
+    // / 175.7; G = 1 with the two-wave pass: 8/8 B=200 S=256 42.3 / 37.9,
+    // 16/16 B=100 S=512 76.5 / 69.7, 8/8 B=96 S=64 12.1 / 10.1; three blocks:
+    // 8/8 B=200 S=40 14.1 / 13.1 split; where the one-wave pass holds the
+    // row it stays ahead: 32/8 B=512 S=256 93.7 / 90.5, 16/16 B=128 S=1024
+    // 173.1 / 163.8).
     SplitArgs ag = a;
     ag.sub_shift = 0;
-    if (onepass_group_fits<D, G, LAYOUT>(ag)) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
+    const bool group_fits = onepass_group_fits<D, G, LAYOUT>(ag);
+    if (G == 1 && group_fits) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
+    if constexpr (D == 128)
+      if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
+    // Too few units for one wave each: two waves per unit.
+    if (group_fits) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
   }
   // P.V sub-block rows (register budget: pages under 16 rows address every
   // row on its own, a descriptor or a 64-bit address per row; 16 rows there
@@ -508,80 +671,6 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
   }
 }
 
-// The matrix-core single pass (onepass_mfma_kernel): NW waves per (batch,
-// KV head), for groups of at most 16 query heads per KV head (after
-// padding) on packed and strided caches, rows of at least 8 blocks and at
-// least 512 units.  Against the matrix-core split passes (µs, packed, B x
-// Hq/Hkv x S; NW = 1 / 2 / 4 / split):
-//   D = 128: 1024 x 64/8 x 160: 127.9 / 156.1 / 166.7 / 145.9; x 256:
-//   199.7 / 191.6 / 205.9 / 220.4; 512 x 64/8 x 512: 200.8 / 189.3 / 258.0
-//   / 220.0; 256 x 64/8 x 1024: 255.5 / 202.4 / 217.2 / 219.1; x 1536:
-//   468.9 / 484.6 / 299.2 / 360.7; 128 x 64/8 x 2048: 588.9 / 320.3 / 195.8
-//   / 223.1; 512 x 16/1 x 600: 52.9 / 36.9 / 43.8 / 66.1; 512 x 128/8 x 512
-//   (G = 16): 250.8 / 216.6 / 259.9 / 252.2; 64 x 96/8 x 300 (G = 12): 36.7
-//   / 30.4 / 38.2 / 46.9;
-//   D = 256: 256 x 32/4 x 500: 85.3 / 102.5 / 104.6 / 100.6;
-//   D = 64: 600 x 8/1 x 1200: 145.5 / 81.3 / 81.7 / 68.4 (kept on split).
-// So at D = 128 one wave per row up to 12 blocks, two while a workgroup's
-// LDS stays within 80 KiB (two workgroups per CU), four while it stays
-// within 144 KiB; at D = 256 one wave within 80 KiB.
-// FMHA_DECODE_ONEPASS_MFMA=0 turns it off and =1, 2, 4 forces the waves
-// per row wherever the LDS fits (for sweeps).
-constexpr int64_t kOnepassMfmaMinUnits = 512;
-constexpr int kOnepassMfmaMinBlocks = 8;
-
-// Waves per row of the matrix-core single pass for a, or 0 where it does
-// not apply.
-template <int D, int LAYOUT>
-int onepass_mfma_waves(const SplitArgs& a) {
-  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
-    return 0;
-  } else {
-    const int g = a.num_heads_q / a.num_heads_kv;
-    const int64_t units = (int64_t)a.batch * a.num_heads_kv;
-    if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
-    auto lds = [&](int nw) { return fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw); };
-    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_MFMA")) {
-      const int v = std::atoi(e);
-      if (v == 0) return 0;
-      if (v == 1 || v == 2 || v == 4) return lds(v) <= 160 * 1024 ? v : 0;
-    }
-    if (a.nblk < kOnepassMfmaMinBlocks) return 0;
-    if constexpr (D == 128) {
-      if (a.nblk <= 12) return lds(1) <= 80 * 1024 ? 1 : 0;
-      if (lds(2) <= 80 * 1024) return 2;
-      return lds(4) <= 144 * 1024 ? 4 : 0;
-    } else if constexpr (D == 256) {
-      return lds(1) <= 80 * 1024 ? 1 : 0;
-    } else {
-      return 0;
-    }
-  }
-}
-
-template <int D, int LAYOUT>
-hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
-  const int g = a.num_heads_q / a.num_heads_kv;
-  const size_t need = fmha_decode::onepass_mfma_lds_bytes<D>(g, a.nblk, nw);
-  plan_note("onepass_matrix_core(D=%d G=%d layout=%s waves_per_row=%d blocks=%d)", D, g, layout_name(LAYOUT), nw,
-            a.nblk);
-  const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));
-  switch (nw) {
-    case 1:
-      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 1, LAYOUT>), grid, dim3(kBlockThreads), need, stream, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 4, LAYOUT>), grid, dim3(kBlockThreads * 4), need, stream,
-                         a);
-      break;
-    default:
-      hipLaunchKernelGGL((fmha_decode::onepass_mfma_kernel<D, 2, LAYOUT>), grid, dim3(kBlockThreads * 2), need, stream,
-                         a);
-      break;
-  }
-  return hipGetLastError();
-}
-
 // Split-KV on the matrix cores (fmha_decode_splitkv_group.hpp): a's KV heads
 // are the cache's (kv_groups = 1) and G = num_heads_q / num_heads_kv any
 // size.  Scores, the statistics pass for rows of more than kPvStatBlocks
@@ -590,8 +679,10 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
 template <int D, int LAYOUT>
 hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
-  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided) {
+    if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
     if (const int nw = onepass_mfma_waves<D, LAYOUT>(a)) return launch_onepass_mfma<D, LAYOUT>(a, nw, stream);
+  }
   constexpr int HPW = kWaveSize / (D / 8);
   constexpr int TW = D == 256 ? 1 : 2;
   const int64_t g = a.num_heads_q / a.num_heads_kv;

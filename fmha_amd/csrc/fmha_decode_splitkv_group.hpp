@@ -601,4 +601,247 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Single pass on the matrix cores, the row's scores in registers.
+// ---------------------------------------------------------------------------
+// The v_mfma_f32_16x16x32_bf16 scores of a 16-row tile leave lane (q, n)
+// (q = lane / 16, n = lane % 16) holding rows 4q..4q+3 of query column n:
+// exactly its A operand of v_mfma_f32_16x16x16_bf16 in the P.V product
+// (query row n, reduction index 4q + e).  So a wave that keeps its tiles'
+// scores in registers needs no LDS for them, and registers, not LDS, bound
+// the waves per CU.  Wave w of a workgroup of NW takes rows [w R, w R + R),
+// R = 16 TPW, of one (batch, KV head):
+//   * K rows straight from memory in the A operand's layout (lane (q, n):
+//     row n of the tile, 16-byte chunks 4c + q, c < D / 32; Q's B operand
+//     takes the same chunks), PF tiles in flight, one 16x16x32 MFMA chain
+//     per tile;
+//   * its (max, sum of exp(t - max)) per query column over its rows, those
+//     of the workgroup's waves exchanged through LDS and combined in wave
+//     order;
+//   * V rows 4q..4q+3 of each tile at dims [n D/16, n D/16 + D/16) straight
+//     from memory (each load a whole row across the 16 lanes of a lane
+//     group), transposed in registers with v_perm into the B operand;
+//     weights bf16(exp(t - max) / sum) with the row's global max and sum;
+//   * waves 1..NW-1 hand their fp32 sums to wave 0 through LDS, which adds
+//     them in wave order and writes fp16 O.
+// Rows past the wave's range are never read (out-of-range offsets read 0).
+// Packed and strided layouts.
+template <int D>
+constexpr int onepass_reg_pf() {
+  return D == 256 ? 2 : 4;  // tiles in flight per wave
+}
+// LDS of a workgroup of nw waves: the (max, sum) exchange, then each wave's
+// K staging (16 rows of HPW tiles), whose space the fp32 sums of waves
+// 1..nw-1 reuse once every wave is past the exchange.
+template <int D>
+constexpr size_t onepass_reg_stage_offset(int nw) {
+  return (size_t)nw * 16 * 2 * 4;
+}
+template <int D>
+constexpr size_t onepass_reg_lds_bytes(int nw) {
+  const size_t stage = (size_t)nw * GroupShape<D>::KS * kSplitBlockRows;
+  const size_t red = (size_t)(nw - 1) * (D / 16) * kWaveSize * 16;
+  return onepass_reg_stage_offset<D>(nw) + (stage > red ? stage : red);
+}
+
+template <int D, int TPW, int NWMAX, int LAYOUT>
+__global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel(SplitArgs a) {
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  constexpr int QLD = D / 32;  // 16-byte K chunks per lane per tile
+  constexpr int DPC = D / 16;  // output dims per lane (one P.V MFMA each)
+  constexpr int VW = DPC / 2;  // dwords of a lane's V run per row
+  constexpr int PF = onepass_reg_pf<D>();
+  constexpr int NR = kSplitBlockRows;
+  constexpr int R = TPW * NR;
+  using Sh = GroupShape<D>;
+  constexpr int LPH = Sh::LPH;
+  constexpr int HPW = Sh::HPW;
+  static_assert(TPW % HPW == 0, "whole rounds");
+  extern __shared__ __attribute__((aligned(16))) char onepass_reg_lds[];
+  const int lane = threadIdx.x & (kWaveSize - 1);
+  const int nw = (int)(blockDim.x / kWaveSize);
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWaveSize));
+  const uint32_t hkv = (uint32_t)a.num_heads_kv;
+  const uint32_t b = blockIdx.x / hkv;
+  const uint32_t hk = blockIdx.x - b * hkv;
+  if (b >= (uint32_t)a.batch) return;
+  const int hq = a.num_heads_q;
+  const int G = hq / (int)hkv;  // <= 16
+  const int S = split_len_l<LAYOUT>(a, b);
+  const int q = lane >> 4;
+  const int n = lane & 15;
+  const bool gok = n < G;
+  const __amdgpu_buffer_rsrc_t o_rsrc =
+      make_rsrc(a.o + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  if (S <= 0 || S > a.max_rows) {
+    // Empty rows give 0 (the reference loop's result), invalid ones NaN.
+    if (wv != 0) return;
+    const u32x4 fill = S == 0 ? u32x4{0u, 0u, 0u, 0u} : u32x4{0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u};
+    for (int k = lane; k < G * (D / 8); k += kWaveSize)
+      buffer_store16(o_rsrc, (uint32_t)((k / (D / 8)) * D + (k % (D / 8)) * 8) * 2u, fill);
+    return;
+  }
+  const int lo = wv * R;
+  const int span = S - lo < 0 ? 0 : (S - lo < R ? S - lo : R);
+  const int nt = (span + NR - 1) / NR;
+
+  // ---- K: scores of the wave's tiles, kept in x ----
+  // A round of HPW tiles: lane group s loads tile s's 16 rows whole (16
+  // bytes per lane, chunk r), stores them to the wave's staging, and the
+  // MFMA A operands (row n, chunks 4c + q) are read back from there; the
+  // next round's rows are in flight during a round's products.  Tiles past
+  // the wave's rows read 0 without memory access and are masked; the loops
+  // carry no branch, one branch skips them for a wave without rows.
+  const __amdgpu_buffer_rsrc_t q_rsrc =
+      make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
+  bf16x8_v qb[QLD];
+#pragma unroll
+  for (int c = 0; c < QLD; ++c)
+    qb[c] = __builtin_bit_cast(
+        bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, gok ? (uint32_t)(n * D + (4 * c + q) * 8) * 2u : kLaneOutOfRange));
+  const int s = lane / LPH;
+  const int r = lane % LPH;
+  char* stage = onepass_reg_lds + onepass_reg_stage_offset<D>(nw) + (size_t)wv * Sh::KS * NR;
+  LongRows<D, LAYOUT> kr;
+  kr.init(a, a.k, b, split_row_base<LAYOUT>(a, b), lo, lo + span, (int)hk, true, r, s * NR);
+  f32x4_v x[TPW];
+  float m = -__builtin_inff();
+  if (nt > 0) {
+    u32x4 kb[NR];
+    kr.template load<NR>(kb, 0);
+#pragma unroll
+    for (int k = 0; k < TPW / HPW; ++k) {
+      wave_lds_sync();  // the previous round's reads of the staging are done
+#pragma unroll
+      for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(stage + j * Sh::KS + s * D * 2 + r * 16) = kb[j];
+      wave_lds_sync();
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 1 < TPW / HPW) kr.template load<NR>(kb, (k + 1) * HPW * NR);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int p = 0; p < HPW; ++p) {
+        const int t = k * HPW + p;
+        f32x4_v c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < QLD; ++c) {
+          const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(stage + n * Sh::KS + p * D * 2 + (4 * c + q) * 16);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[c], c4, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[t][e] = c4[e] * a.scale;
+          m = t * NR + 4 * q + e < span ? fmaxf(m, x[t][e]) : m;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) x[t] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // The wave's (max, sum) per column, over its four lane groups.
+  const float cm = column_reduce<true>(m);
+  float l = 0.0f;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) l += t * NR + 4 * q + e < span ? expf(x[t][e] - cm) : 0.0f;
+  }
+  const float cl = column_reduce<false>(l);
+  float* pst = reinterpret_cast<float*>(onepass_reg_lds);  // [nw][16][2]
+  if (q == 0) {
+    pst[(wv * 16 + n) * 2] = cm;
+    pst[(wv * 16 + n) * 2 + 1] = cl;
+  }
+  // V rows of the wave's first tiles, in flight across the exchange.
+  LongRows<D, LAYOUT> vrw;
+  vrw.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, 0);
+  uint32_t vr[PF][4][VW];
+  auto v_load = [&](int p, int t) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = t * NR + 4 * q + e;
+      const uint32_t off = row < span ? vrw.lane_off + (uint32_t)(lo + row) * vrw.row_bytes + (uint32_t)(n * DPC * 2)
+                                      : kRowOutOfRange;
+      if constexpr (VW == 2) {
+        const u32x2 w2 = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrw.rsrc, (int)off, 0, kPolicyStream));
+        vr[p][e][0] = w2[0];
+        vr[p][e][1] = w2[1];
+      } else {
+#pragma unroll
+        for (int h = 0; h < VW / 4; ++h) {
+          const u32x4 w4 = buffer_load16_nt(vrw.rsrc, off + (uint32_t)h * 16u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vr[p][e][4 * h + i] = w4[i];
+        }
+      }
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < PF; ++p) v_load(p, p);
+  __syncthreads();
+  float gm = -__builtin_inff();
+  for (int w = 0; w < nw; ++w) gm = fmaxf(gm, pst[(w * 16 + n) * 2]);
+  float gl = 0.0f;
+  for (int w = 0; w < nw; ++w) {
+    const float mw = pst[(w * 16 + n) * 2];
+    gl += mw == -__builtin_inff() ? 0.0f : pst[(w * 16 + n) * 2 + 1] * (mw == gm ? 1.0f : expf(mw - gm));
+  }
+
+  // ---- V: weights from x ----
+  f32x4_v acc[DPC];
+#pragma unroll
+  for (int dt = 0; dt < DPC; ++dt) acc[dt] = f32x4_v{0.0f, 0.0f, 0.0f, 0.0f};
+  if (nt > 0) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      bf16x4_v pa;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool valid = gok && t * NR + 4 * q + e < span;
+        pa[e] = (__bf16)(valid ? expf(x[t][e] - gm) / gl : 0.0f);
+      }
+      const int p = t % PF;
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const uint32_t sel = (dt & 1) ? kPermHi : kPermLo;
+        const u32x2 w2 = {__builtin_amdgcn_perm(vr[p][1][dt / 2], vr[p][0][dt / 2], sel),
+                          __builtin_amdgcn_perm(vr[p][3][dt / 2], vr[p][2][dt / 2], sel)};
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(bf16x4_v, w2), acc[dt], 0, 0, 0);
+      }
+      if (t + PF < TPW) v_load(p, t + PF);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- waves 1..nw-1 -> wave 0 ----
+  if (nw > 1) {
+    f32x4_v* red = reinterpret_cast<f32x4_v*>(onepass_reg_lds + onepass_reg_stage_offset<D>(nw));
+    if (wv > 0) {
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) red[((size_t)(wv - 1) * DPC + dt) * kWaveSize + lane] = acc[dt];
+    }
+    __syncthreads();
+    if (wv > 0) return;
+    for (int w = 1; w < nw; ++w) {
+#pragma unroll
+      for (int dt = 0; dt < DPC; ++dt) {
+        const f32x4_v y = red[((size_t)(w - 1) * DPC + dt) * kWaveSize + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[dt][e] += y[e];
+      }
+    }
+  }
+  // Lane (q, n) holds query rows 4q..4q+3, dims [n DPC, n DPC + DPC).
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int g = 4 * q + e;
+    float v[DPC];
+#pragma unroll
+    for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[dt][e];
+    store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
+  }
+}
+
 }  // namespace fmha_decode

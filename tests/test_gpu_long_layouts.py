@@ -73,12 +73,14 @@ def test_strided_long(layout, B, cap, D, Hq, Hkv):
 
 @pytest.mark.parametrize("layout", ["bhsd", "bshd"])
 @pytest.mark.parametrize("D,Hq,Hkv,B,cap", [(128, 16, 16, 64, 256), (128, 32, 8, 200, 96), (256, 16, 8, 60, 160)])
-def test_strided_onepass_group(layout, D, Hq, Hkv, B, cap):
+def test_strided_onepass_group(monkeypatch, layout, D, Hq, Hkv, B, cap):
     """Strided caches with too few units for one wave each: the single pass
-    with two waves per row (plan onepass_group), NaN padding past each
-    length never read."""
+    with two waves per row (plan onepass_group; the register single pass,
+    which takes groups of 2 and 4 at D = 128 first, off), NaN padding past
+    each length never read."""
     import fmha_amd
     import torch
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
     rng = np.random.default_rng(B + cap + D + 1)
     seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
     seqlens[:4] = [cap, 0, 1, 33]
@@ -92,12 +94,14 @@ def test_strided_onepass_group(layout, D, Hq, Hkv, B, cap):
 
 
 @pytest.mark.parametrize("layout", ["bhsd", "bshd"])
-def test_strided_onepass_matrix_core(layout):
+@pytest.mark.parametrize("D,kind", [(128, "onepass_matrix_core_regs"), (256, "onepass_matrix_core")])
+def test_strided_onepass_matrix_core(layout, D, kind):
     """Strided caches, 8 query heads per KV head, 512 (batch, KV head)
-    units: the matrix-core single pass (plan onepass_matrix_core)."""
+    units: the matrix-core single pass, the scores in registers at D = 128
+    and in LDS at D = 256."""
     import fmha_amd
     import torch
-    B, Hq, Hkv, D, cap = 128, 32, 4, 128, 400
+    B, Hq, Hkv, cap = 128, 32, 4, 400
     rng = np.random.default_rng(77)
     seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
     seqlens[:4] = [cap, 0, 1, 65]
@@ -106,8 +110,8 @@ def test_strided_onepass_matrix_core(layout):
     vc = _strided_view(_strided_cache(vp, seqlens, cap, Hkv, D, layout), layout)
     o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
     torch.cuda.synchronize()
-    assert [k for k, _ in last_plan()] == ["onepass_matrix_core"], last_plan()
-    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} matrix-core single pass")
+    assert [k for k, _ in last_plan()] == [kind], last_plan()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"{layout} {kind}")
 
 
 def test_strided_uniform_long_bhsd():

@@ -87,8 +87,10 @@ STAT_CASES = [
 def test_block_statistics_in_pv(monkeypatch, B, Hq, Hkv, D, max_len, kind, passes):
     """The P.V waves' own reduction of the block statistics, at and past its
     64-block limit, with ragged lengths (0, 1, one block, the maximum); the
-    matrix-core single pass off (FMHA_DECODE_ONEPASS_MFMA=0)."""
+    matrix-core single passes off (FMHA_DECODE_ONEPASS_MFMA=0,
+    FMHA_DECODE_ONEPASS_REG=0)."""
     monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", "0")
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
     rng = np.random.default_rng(B + max_len + Hq)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[:4] = [max_len, 0, 1, 16]
@@ -141,9 +143,12 @@ GROUP_CASES = [
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,max_len", GROUP_CASES)
-def test_onepass_group(B, Hq, Hkv, D, max_len):
+def test_onepass_group(monkeypatch, B, Hq, Hkv, D, max_len):
     """The single pass with two waves per row: ragged lengths (0, 1, one
-    block, the maximum, one past a wave's rows) and an invalid one (NaN)."""
+    block, the maximum, one past a wave's rows) and an invalid one (NaN);
+    the register single pass off (it takes groups of 2 and 4 at D = 128
+    first)."""
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
     rng = np.random.default_rng(B + max_len + D)
     seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
     seqlens[:5] = [max_len, 0, 1, 16, min(max_len, 33)]
@@ -157,19 +162,22 @@ def test_onepass_group(B, Hq, Hkv, D, max_len):
 
 
 def test_onepass_group_off(monkeypatch):
-    """FMHA_DECODE_ONEPASS_WAVES=1: the same rows through the split passes."""
+    """FMHA_DECODE_ONEPASS_WAVES=1 (and the register single pass off): the
+    same rows through the split passes."""
     monkeypatch.setenv("FMHA_DECODE_ONEPASS_WAVES", "1")
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
     seqlens = np.random.default_rng(1).integers(0, 257, size=64).astype(np.int32)
     _case(64, 16, 16, 128, seqlens, 256, seed=41, std=0.5)
     assert _kinds() == ["split"]
 
 
-# (B, Hq, Hkv, D, max_len, waves, force): the matrix-core single pass (8 to
-# 16 query heads per KV head after padding, at least 512 (batch, KV head)
-# units, a row's scores within a workgroup's LDS) with the waves per row the
-# planner picks (one up to 12 blocks and at D = 256, two, four on long rows)
-# or that FMHA_DECODE_ONEPASS_MFMA forces (D = 64 stays on the split passes
-# by default).
+# (B, Hq, Hkv, D, max_len, waves, force): the matrix-core single pass with
+# the scores in LDS (8 to 16 query heads per KV head after padding, at least
+# 512 (batch, KV head) units, a row's scores within a workgroup's LDS) with
+# the waves per row the planner picks (one up to 12 blocks and at D = 256,
+# two, four on long rows) or that FMHA_DECODE_ONEPASS_MFMA forces; the
+# register single pass off (FMHA_DECODE_ONEPASS_REG=0) except at D = 256,
+# which it leaves to this kernel.
 MFMA_ONEPASS_CASES = [
     (256, 64, 8, 128, 1024, 2, None),   # G = 8
     (512, 16, 1, 128, 600, 2, None),    # G = 16, one KV head
@@ -183,20 +191,8 @@ MFMA_ONEPASS_CASES = [
 ]
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,max_len,waves,force", MFMA_ONEPASS_CASES)
-def test_onepass_matrix_core(monkeypatch, B, Hq, Hkv, D, max_len, waves, force):
-    """Groups of 8-16 query heads on the matrix-core single pass (1, 2 or 4
-    waves per (batch, KV head)): ragged lengths (0, 1, one block, a round's
-    rows and one past them, the maximum) and an invalid one (NaN)."""
-    if force:
-        monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", force)
-    else:
-        monkeypatch.delenv("FMHA_DECODE_ONEPASS_MFMA", raising=False)
-    rng = np.random.default_rng(B + max_len + D + Hq)
-    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
-    seqlens[:6] = [max_len, 0, 1, 16, min(max_len, 64), min(max_len, 65)]
-    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + D + Hq, std=0.5)
-    assert _launch("onepass_matrix_core")["waves_per_row"] == waves
+def _nan_row_check(B, Hq, Hkv, D, seqlens, max_len):
+    """A length above max_seqlen_kv: NaN for that batch only."""
     bad = seqlens.copy()
     bad[3] = max_len + 1
     q, k, v, cu = make_inputs(B, Hq, Hkv, D, bad, seed=B + 9)
@@ -204,13 +200,82 @@ def test_onepass_matrix_core(monkeypatch, B, Hq, Hkv, D, max_len, waves, force):
     assert np.all(np.isnan(o[3])) and np.all(np.isfinite(np.delete(o, 3, axis=0)))
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,D,max_len,waves,force", MFMA_ONEPASS_CASES)
+def test_onepass_matrix_core(monkeypatch, B, Hq, Hkv, D, max_len, waves, force):
+    """Groups of 8-16 query heads on the matrix-core single pass with the
+    scores in LDS (1, 2 or 4 waves per (batch, KV head)): ragged lengths (0,
+    1, one block, a round's rows and one past them, the maximum) and an
+    invalid one (NaN)."""
+    if force:
+        monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", force)
+    else:
+        monkeypatch.delenv("FMHA_DECODE_ONEPASS_MFMA", raising=False)
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
+    rng = np.random.default_rng(B + max_len + D + Hq)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:6] = [max_len, 0, 1, 16, min(max_len, 64), min(max_len, 65)]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + D + Hq, std=0.5)
+    assert _launch("onepass_matrix_core")["waves_per_row"] == waves
+    _nan_row_check(B, Hq, Hkv, D, seqlens, max_len)
+
+
 def test_onepass_matrix_core_off(monkeypatch):
-    """FMHA_DECODE_ONEPASS_MFMA=0: the same rows through the matrix-core
-    split passes."""
+    """FMHA_DECODE_ONEPASS_MFMA=0 and FMHA_DECODE_ONEPASS_REG=0: the same
+    rows through the matrix-core split passes."""
     monkeypatch.setenv("FMHA_DECODE_ONEPASS_MFMA", "0")
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
     seqlens = np.random.default_rng(2).integers(0, 1025, size=256).astype(np.int32)
     _case(256, 64, 8, 128, seqlens, 1024, seed=42, std=0.5)
     assert _kinds() == ["split_matrix_core"]
+
+
+# (B, Hq, Hkv, D, max_len, waves, tiles, force): the matrix-core single pass
+# with the scores in registers (at least 512 (batch, KV head) units and 4
+# blocks, ceil(blocks / tiles) <= 8 waves per row), groups of 8-16 through
+# the matrix-core launcher and of 2 and 4 through the VALU one where the
+# one-wave single pass does not hold the row: 8 tiles per wave up to 32
+# blocks, else 16, or what FMHA_DECODE_ONEPASS_REG forces.
+REG_ONEPASS_CASES = [
+    (256, 64, 8, 128, 1024, 4, 16, None),   # G = 8
+    (512, 16, 1, 128, 600, 3, 16, None),    # G = 16, one KV head
+    (128, 40, 8, 128, 700, 3, 16, None),    # G = 5 on a group padded to 8
+    (64, 96, 8, 128, 300, 3, 8, None),      # G = 12 on a group padded to 16
+    (600, 16, 2, 128, 150, 2, 8, None),     # 10 blocks
+    (70, 128, 8, 128, 2000, 8, 16, None),   # eight waves, G = 16
+    (128, 32, 8, 128, 256, 2, 8, None),     # G = 4 (the VALU launcher)
+    (512, 8, 2, 128, 128, 1, 8, None),      # G = 4, one wave
+    (64, 32, 16, 128, 256, 2, 8, None),     # G = 2
+    (600, 8, 1, 64, 1200, 5, 16, None),     # D = 64
+    (1024, 32, 4, 64, 128, 1, 8, None),     # D = 64, one wave
+    (256, 32, 4, 256, 500, 2, 16, "16"),    # D = 256, forced
+    (300, 16, 2, 128, 200, 1, 16, "16"),    # 16 tiles on a short row, forced
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,max_len,waves,tiles,force", REG_ONEPASS_CASES)
+def test_onepass_registers(monkeypatch, B, Hq, Hkv, D, max_len, waves, tiles, force):
+    """The matrix-core single pass with each wave's scores in registers:
+    ragged lengths (0, 1, one block, four blocks and one row past them, the
+    maximum), waves with no rows, and an invalid length (NaN)."""
+    if force:
+        monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", force)
+    else:
+        monkeypatch.delenv("FMHA_DECODE_ONEPASS_REG", raising=False)
+    rng = np.random.default_rng(B + max_len + D + Hq + 1)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:6] = [max_len, 0, 1, 16, min(max_len, 64), min(max_len, 65)]
+    _case(B, Hq, Hkv, D, seqlens, max_len, seed=B + D + Hq + 1, std=0.5)
+    launch = _launch("onepass_matrix_core_regs")
+    assert launch["waves_per_row"] == waves and launch["tiles_per_wave"] == tiles, launch
+    _nan_row_check(B, Hq, Hkv, D, seqlens, max_len)
+
+
+def test_onepass_registers_off(monkeypatch):
+    """FMHA_DECODE_ONEPASS_REG=0: a group of 4 on the split passes."""
+    monkeypatch.setenv("FMHA_DECODE_ONEPASS_REG", "0")
+    seqlens = np.random.default_rng(3).integers(0, 257, size=128).astype(np.int32)
+    _case(128, 32, 8, 128, seqlens, 256, seed=43, std=0.5)
+    assert _kinds() == ["split"]
 
 
 def test_wide_logits():
@@ -260,7 +325,7 @@ def test_onepass_all_shapes(D, B, G):
     assert _kinds() == ["onepass"]
 
 
-@pytest.mark.parametrize("D,Hkv,B,max_len", [(64, 16, 1024, 96), (64, 1, 4100, 64), (128, 8, 1100, 128),
+@pytest.mark.parametrize("D,Hkv,B,max_len", [(64, 16, 1024, 96), (64, 1, 4100, 64), (128, 8, 1100, 96),
                                              (128, 2, 2050, 96), (256, 8, 600, 128), (256, 1, 1030, 128)])
 def test_onepass_group_of_eight(D, Hkv, B, max_len):
     """G = 8 on the single pass at the longest rows it takes there for each
