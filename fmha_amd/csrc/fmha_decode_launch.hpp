@@ -465,6 +465,9 @@ constexpr int kOnepassRegMaxWaves = 8;
 // Rows of fewer blocks keep the split passes (three blocks: µs, 8/8
 // B=200 S=40, 14.1 against 13.1).
 constexpr int kOnepassRegMinBlocks = 4;
+// Waves of the one-wave VALU single pass below which groups of at most 4
+// take the register single pass first (launch_split_dg).
+constexpr int64_t kOnepassRegBeforeWaves = 1024;
 
 // Tiles per wave of the register single pass for a, or 0 where it does not
 // apply.
@@ -564,7 +567,16 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     constexpr bool kRegRows = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided);
     const int only_nblk =
         shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : kRegRows ? 6 : 8);
-    if (onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
+    // Groups of at most 4, one batch per wave, with fewer than
+    // kOnepassRegBeforeWaves waves of the one-wave pass (too few to fill the
+    // CUs): the register single pass below instead where it applies (µs,
+    // 32/8 S=256, one-wave / register: B=256, 512 waves, 58.4 / 49.4;
+    // B=512, 1024 waves, 90.5 / 93.7).
+    bool reg_first = false;
+    if constexpr (kRegRows && G <= 4)
+      reg_first = !onepass_only && ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves &&
+                  onepass_reg_tiles<D, LAYOUT>(a) > 0;
+    if (!reg_first && onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
       constexpr int OL = LAYOUT == fmha_decode::kLayoutPagedLanes        ? fmha_decode::kLayoutPaged
@@ -595,15 +607,16 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     // 89.2 / 103.7, 16/4 B=128 S=256 17.0 / 25.8, B=256 S=64 12.7 / 17.1,
     // 8/2 B=512 S=128 16.5 / 25.0, 32/8 B=200 S=96 19.2 / 25.7, 32/16 B=64
     // S=256 25.0 / 28.9, B=64 S=2048 170.6 / 177.7, 16/16 B=64 S=2048 170.3
-    // / 175.7; G = 1 with the two-wave pass: 8/8 B=200 S=256 42.3 / 37.9,
-    // 16/16 B=100 S=512 76.5 / 69.7, 8/8 B=96 S=64 12.1 / 10.1; three blocks:
+    // / 175.7; G = 1 with the two-wave pass up to 64 blocks: 8/8 B=200
+    // S=256 42.3 / 37.9, 16/16 B=100 S=512 76.5 / 69.7, 8/8 B=96 S=64 12.1 /
+    // 10.1 (beyond: 16/16 B=64 S=2048 170.3 / 175.7); three blocks:
     // 8/8 B=200 S=40 14.1 / 13.1 split; where the one-wave pass holds the
     // row it stays ahead: 32/8 B=512 S=256 93.7 / 90.5, 16/16 B=128 S=1024
     // 173.1 / 163.8).
     SplitArgs ag = a;
     ag.sub_shift = 0;
     const bool group_fits = onepass_group_fits<D, G, LAYOUT>(ag);
-    if (G == 1 && group_fits) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
+    if (G == 1 && group_fits && a.nblk <= 64) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
     if constexpr (D == 128)
       if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
     // Too few units for one wave each: two waves per unit.

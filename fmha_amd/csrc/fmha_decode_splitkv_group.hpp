@@ -36,6 +36,13 @@
 // lane its own 64-bit addresses instead.  The query heads of a KV head may
 // be padded (Q and O copies with a multiple of 8 heads): the kernels take
 // G = num_heads_q / num_heads_kv as given.
+//
+// The file ends with two single passes on the same products (one launch,
+// nothing through the workspace) for query groups of at most 16 with
+// enough (batch, KV head) units: onepass_mfma_kernel, one workgroup per
+// unit keeping the row's scores in LDS, and onepass_mfma_reg_kernel, each
+// wave of the workgroup keeping its rows' scores in the registers the
+// scores MFMA leaves them in.
 #pragma once
 
 #include "fmha_decode_group.hpp"
@@ -609,24 +616,29 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
 // (q = lane / 16, n = lane % 16) holding rows 4q..4q+3 of query column n:
 // exactly its A operand of v_mfma_f32_16x16x16_bf16 in the P.V product
 // (query row n, reduction index 4q + e).  So a wave that keeps its tiles'
-// scores in registers needs no LDS for them, and registers, not LDS, bound
-// the waves per CU.  Wave w of a workgroup of NW takes rows [w R, w R + R),
-// R = 16 TPW, of one (batch, KV head):
-//   * K rows straight from memory in the A operand's layout (lane (q, n):
-//     row n of the tile, 16-byte chunks 4c + q, c < D / 32; Q's B operand
-//     takes the same chunks), PF tiles in flight, one 16x16x32 MFMA chain
-//     per tile;
+// scores in registers needs no LDS for them, and more waves fit a CU than
+// with the row's scores in LDS.  Wave w of a workgroup of NW takes rows
+// [w R, w R + R), R = 16 TPW, of one (batch, KV head):
+//   * K a round of HPW tiles at a time, whole rows per lane group (16 bytes
+//     a lane) into a 16-row staging in LDS, read back in the A operand's
+//     layout (row n, 16-byte chunks 4c + q; Q's B operand takes the same
+//     chunks), the next round's rows in flight during a round's products
+//     (loading the A layout straight from memory, 64 bytes of 16 rows per
+//     instruction, measured 5-15% slower);
 //   * its (max, sum of exp(t - max)) per query column over its rows, those
 //     of the workgroup's waves exchanged through LDS and combined in wave
 //     order;
 //   * V rows 4q..4q+3 of each tile at dims [n D/16, n D/16 + D/16) straight
 //     from memory (each load a whole row across the 16 lanes of a lane
-//     group), transposed in registers with v_perm into the B operand;
-//     weights bf16(exp(t - max) / sum) with the row's global max and sum;
-//   * waves 1..NW-1 hand their fp32 sums to wave 0 through LDS, which adds
-//     them in wave order and writes fp16 O.
+//     group), PF tiles in flight, transposed in registers with v_perm into
+//     the B operand; weights bf16(exp(t - max) / sum) with the row's global
+//     max and sum;
+//   * waves 1..NW-1 hand their fp32 sums to wave 0 through LDS (the K
+//     staging's space), which adds them in wave order and writes fp16 O.
 // Rows past the wave's range are never read (out-of-range offsets read 0).
-// Packed and strided layouts.
+// The tile loops are unrolled over TPW with no branch inside: the scores'
+// registers need static indices, and a branch per tile made the compiler
+// wait for every load in flight at each tile.  Packed and strided layouts.
 template <int D>
 constexpr int onepass_reg_pf() {
   return D == 256 ? 2 : 4;  // tiles in flight per wave
