@@ -88,124 +88,105 @@ int valu_kernel_group(int g) {
   return 0;
 }
 
-// Waves per CU for a unit that moves `rows16` / 16 K/V rows (a mean, in
-// sixteenths) and g_real query heads per KV head on the g-head kernel at
-// head dim dq: each row costs 1 KiB of K plus 1 KiB of V per wave, each
-// query head 1 KiB of Q in and 1 KiB of O out, and the cap is the in-flight
-// budget over that, or a measured table where no one budget fits.  Caps of
-// 16 or more are dropped (no cap); the floor is 3 waves, 4 for the 8-head
-// kernel.
-//
-// Known lengths: 80 KiB per CU for the 1- and 2-head kernels (3 waves of the
-// 34 KiB C2 unit, 7.13 TB/s against 6.63 uncapped; 6 of the 12 KiB C3 unit,
-// 6.60 against 6.05).
-//
-// The 4-head kernel with known lengths scores all its query heads in one
-// pass; its best cap falls with the row count faster than any budget does
-// (B=30720, µs for 3/4/5/6/7/8 waves; D=128 Hkv=16: G=4 S=1
-// 311/251/216/199/191/193, S=2 325/268/241/231/232/233, S=4
-// 378/320/302/315/322/321, S=6 466/401/392/400/404/409, S=8
-// 497/477/492/497/498/499, S=12 665/637/661/671/676/676, S=16
-// 781/810/825/838/850/856; G=3 S=3 353/285/247/228/226/236, S=12
-// 638/582/613/626/631/634, S=16 754/777/799/803/807/812; D=64 Hkv=8 and
-// D=256 Hkv=8 B=15360, which want more waves on short rows: G=3 D=256 S=4
-// 182/146/126/116/123/127, S=16 360/346/361/368/370/375; D=64 S=2 best
-// with no cap, S=16 184/175/184/185/187/188).
-//
-// The 8-head kernel scores two query heads per pass at D <= 128 and wants
-// 200 KiB at D = 128 (Hkv=16, µs for 3/4/5/6/8 waves: G=8 S=4
-// 813/639/547/492/464, S=8 956/763/665/618/658, S=16
-// 1137/973/985/1008/1013; G=5 S=8 848/670/574/521/531, S=16
-// 937/848/867/897/921: each within 2% of its best).  At D = 64 (Hkv=8) its
-// waves want more in flight on 16 rows (G=8: 258/225/216/229 µs for
-// 4/5/6/8 waves, G=7 247/216/206/218, G=5 211/191/199/205) and no cap on 4
-// (G=8 149/128/119/114 and 108 uncapped); at D = 256 (one pass, Hkv=8
-// B=15360) fewer on short rows (G=6 S=4 209/191/195/206 for 4/5/6/8, S=8
-// 276/268/292/294).
-//
-// Waves of the 1- and 2-head kernels whose lengths come from a device
-// array first wait for them (one dependent load before any K/V request),
-// so they carry requests for a shorter part of their life and want more of
-// them per CU: 144 KiB against the 80 KiB of known lengths.  Sweep through
-// fmha_decode_fwd (B=30720, µs for 4/6/8/10/12/16 waves): S=16 H=16 D=128
-// 614/634/654/660/667/665; S=16 H=32 D=256 2516/2544/2569/2593/2617/2621;
-// S=5 D=256 643/504/446/433/423/427; the reference's Poisson(4) lengths
-// (mean 4.3) H=16 D=128 291/233/206/198/191/191, H=16 D=256
-// 595/460/409/393/374/376, H=32 D=128 570/446/409/393/377/377, H=32 D=256
-// 1165/918/833/812/813/817.  The 4- and 8-head kernels that pick a bucket
-// per wave score two query heads per pass at D <= 128 and take the 200 KiB
-// budget there (µs for 4/5/6/7/8 waves: G=4 S=8 514/480/481/496/496, S=16
-// 862/790/806/831/843, Poisson 429/374/341/323/316; G=5 S=8
-// 568/517/503/534/546, Hq=40 Hkv=8 Poisson 253/217/198/185/181; G=8 S=8
-// 670/615/631/655/662, S=16 1006/935/987/1000/1007, Poisson
-// 298/260/243/242/252: within 2-8% of each best).
-constexpr int kInflightBytesPerCUDeviceLengths = 144 * 1024;
-constexpr int kInflightBytesPerCUWideGroups = 200 * 1024;
-// The paged 1- and 2-head kernels (one batch per wave) look their pages up
-// before any K/V request and want about half as many waves again: 216 KiB
-// puts the swept shapes within 1% of their best caps (B=30720 D=128, µs
-// for 4/5/6/8/12/16 waves; 16-row pages Hq/Hkv 16/16 S=16
-// 678/653/645/665/682/680, S=8 417/391/379/376/379/379, 32/16 S=4
-// 335/282/250/227/224/227; one-row pages S=16 771/721/693/703/715/721, S=8
-// 470/426/403/382/377/378, 32/16 S=4 358/302/268/234/226/225).
-constexpr int kInflightBytesPerCUPaged = 216 * 1024;
+// The in-flight budget model behind every short-kernel launch's waves per
+// CU.  A wave of the g-head kernel serving `rows` K/V rows (a mean) and G
+// query heads per KV head moves a unit of 2 rows + c G KiB (each row 1 KiB of
+// K and 1 KiB of V per wave at any head dim, each query head 1 KiB of Q in
+// and 1 KiB of O out, which c weighs: 2 counts them in full, 1 at half,
+// their loads being few and their stores leaving nothing to wait for);
+// MI355X streams fastest with a bounded amount in flight per CU, A + B rows
+// KiB, larger for longer rows, whose waves compute longer between requests.
+// The cap is floor((A + B rows) / (2 rows + c G)) waves, at least `floor`,
+// none from 16 on (every wave the registers allow).
+struct WaveBudget {
+  int a_kib;   // A
+  int b2_kib;  // 2 B (KiB per row, in halves)
+  int c;       // KiB per query head
+  int floor;
+};
 
-// bucket_per_wave: the kernel picks a bucket per wave (lengths on the
-// device, or several batches per wave), whose 4-head form scores two query
-// heads per pass.
-int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths, bool bucket_per_wave) {
-  const int s = (rows16 + 15) / 16;  // rows, rounded up
-  if (!bucket_per_wave && g == 4) {
-    static const int8_t kWaves128[17] = {8, 8, 7, 6, 5, 5, 5, 4, 4, 4, 4, 4, 4, 3, 3, 3, 3};
-    if (dq == 128) return kWaves128[s < 16 ? s : 16];
-    return s <= 2 ? kMaxWavesPerCU : (s <= 4 ? 6 : 4);
-  }
-  if (!bucket_per_wave && g == 8 && dq == 64) return s <= 4 ? kMaxWavesPerCU : (s <= 8 || g_real > 5 ? 6 : 5);
-  if (!bucket_per_wave && g == 8 && dq == 256 && s > 2 && s <= 8) return 5;
-  if (device_lengths && g == 8 && dq == 128) {
-    // The 8-head kernel with lengths on the device: a budget of (120 + 7.5
-    // rows) KiB, which puts every shape swept within 1% of its best cap
-    // (B=30720, Hkv = 4 / 8 / 16, G = 5 and 8, S = 4 / 8 / 16 and the
-    // reference's Poisson lengths; µs with 200 KiB against this: Hq/Hkv
-    // 32/4 S=16 252.2 / 212.3, 128/16 S=16 1006.0 / 922.4, 64/8 S=16 510.9 /
-    // 475.3, 128/16 S=4 492.5 / 460.4, 80/16 S=8 535.4 / 499.1).
-    const int64_t w = (3840LL + 15LL * rows16) / (4LL * rows16 + 64LL * g_real);
-    if (w >= 16) return kMaxWavesPerCU;
-    return w < 4 ? 4 : (int)w;
-  }
-  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
-  const int64_t budget = g >= 4           ? kInflightBytesPerCUWideGroups
-                         : device_lengths ? kInflightBytesPerCUDeviceLengths
-                                          : kInflightBytesPerCU;
-  const int64_t w = 16 * budget / unit_bytes16;
+int budget_waves(const WaveBudget& m, int rows16, int g_real) {
+  // Numerator and denominator in 1/32 KiB: rows16 = 16 rows.
+  const int64_t num = 32LL * m.a_kib + (int64_t)m.b2_kib * rows16;
+  const int64_t den = 4LL * rows16 + 32LL * m.c * g_real;
+  const int64_t w = num / den;
   if (w >= 16) return kMaxWavesPerCU;
-  const int floor_w = g >= 8 ? 4 : 3;
-  return w < floor_w ? floor_w : (int)w;
+  return w < m.floor ? m.floor : (int)w;
 }
+
+// Budgets of the tree-order kernels, by kernel (g query heads, head dim dq)
+// and how the wave learns its lengths: known on the host with one batch per
+// wave, or bucket_per_wave (lengths on the device, or several batches per
+// wave).  The fitted ones come from tests/profiling/cap_sweep.py at B=30720
+// (15360 at D = 256), Hkv = 16 at D = 128 and 8 otherwise, S = 1-16, G =
+// 3-8 (102 shapes, two sweeps averaged): the lowest mean time over the
+// swept shapes that keeps the cap of every benchmark configuration, mean
+// and worst time over the best cap 1.003 and 1.023 to 1.015 and 1.091 per
+// kernel, against 1.003-1.027 and 1.016-1.196 for the per-shape rules they
+// replace (profiles/fmha_decode_wave_caps.md).
+//   * 1 or 2 query heads, lengths known: 80 KiB flat (3 waves of the 34 KiB
+//     S=16 D=128 unit, 7.13 TB/s against 6.63 uncapped; 6 of the 12 KiB S=5
+//     D=256 unit, 6.60 against 6.05).
+//   * 1 or 2 with lengths on the device: 144 KiB flat (their waves first
+//     wait for the length, so they carry requests for a shorter part of
+//     their life; B=30720 S=5 D=256 µs for 4/6/8/10/12/16 waves
+//     643/504/446/433/423/427, Poisson(4) lengths H=16 D=128
+//     291/233/206/198/191/191).
+//   * 4-head kernel, lengths known: one pass over all four query heads, its
+//     best cap falling with the rows faster than a flat budget does: (40 +
+//     6 rows, c = 1) at D = 128, (90 + rows / 2, c = 1, at least 4 waves) at
+//     D = 64, (78 + 2 rows, c = 1, at least 4) at D = 256.
+//   * 8-head kernel, lengths known: 200 KiB flat at D = 128 (two query heads
+//     per pass), (212 + rows / 2, c = 1) at D = 64, (54 + 8 rows, c = 1) at
+//     D = 256.
+//   * 8-head kernel at D = 128 with lengths on the device: (120 + 7.5 rows)
+//     (B=30720, µs against 200 KiB flat: Hq/Hkv 32/4 S=16 212.3 / 252.2,
+//     128/16 S=16 922.4 / 1006.0, 64/8 S=16 475.3 / 510.9).
+//   * the 4- and 8-head kernels otherwise (a bucket per wave, scoring two
+//     query heads per pass at D <= 128): 200 KiB flat (G=4 S=16 Poisson µs
+//     for 4/5/6/7/8 waves 429/374/341/323/316; G=8 S=8 670/615/631/655/662).
+WaveBudget tree_order_budget(int g, int dq, bool device_lengths, bool bucket_per_wave) {
+  if (!bucket_per_wave && g == 4)
+    return dq == 64 ? WaveBudget{90, 1, 1, 4} : dq == 128 ? WaveBudget{40, 12, 1, 3} : WaveBudget{78, 4, 1, 4};
+  if (!bucket_per_wave && g == 8 && dq != 128)
+    return dq == 64 ? WaveBudget{212, 1, 1, 3} : WaveBudget{54, 16, 1, 3};
+  if (device_lengths && g == 8 && dq == 128) return WaveBudget{120, 15, 2, 4};
+  if (g >= 4) return WaveBudget{200, 0, 2, g >= 8 ? 4 : 3};
+  if (device_lengths) return WaveBudget{144, 0, 2, 3};
+  return WaveBudget{kInflightBytesPerCU / 1024, 0, 2, 3};
+}
+
+// Waves per CU of the tree-order kernels: rows16 = 16 x the K/V rows per
+// batch (a mean), g_real the call's query heads per KV head on the g-head
+// kernel.
+int waves_per_cu_for(int rows16, int g, int g_real, int dq, bool device_lengths, bool bucket_per_wave) {
+  return budget_waves(tree_order_budget(g, dq, device_lengths, bucket_per_wave), rows16, g_real);
+}
+
+// Pages under 16 rows and pages of 16 with one batch per wave, 1 or 2 query
+// heads: 216 KiB flat, the page lookups coming before any K/V request
+// (B=30720 D=128, µs for 4/5/6/8/12/16 waves: 16-row pages Hq/Hkv 16/16
+// S=16 678/653/645/665/682/680, 32/16 S=4 335/282/250/227/224/227; one-row
+// pages S=16 771/721/693/703/715/721, S=8 470/426/403/382/377/378).
+constexpr WaveBudget kPagedBudget{216, 0, 2, 3};
 
 // Waves per CU for the exact-arithmetic kernels (rows16 and g_real as for
 // waves_per_cu_for).  Their waves compute longer than the tree-order ones
 // (sequential score sums staged through LDS), so fewer of their waves have
-// requests in flight at a time and the CU needs more of them: 144 KiB of
-// unit bytes per CU with known lengths, 200 KiB with lengths on the device
-// (whose waves also wait for the lengths first); at least 4 waves, 5 for
-// groups of 2 (C4 with known lengths, µs at 4 / 5 / 6 / 8 waves: 665.8 /
-// 652.7 / 667.1 / 691.4) and 6 for groups of 4 or more, no cap from 16.  Sweep at B=30720 (us, best cap /
+// requests in flight at a time and the CU needs more of them: 144 KiB per
+// CU with known lengths, 200 KiB with lengths on the device (whose waves
+// also wait for the lengths first); at least 4 waves, 5 for groups of 2 (C4
+// with known lengths, µs at 4 / 5 / 6 / 8 waves: 665.8 / 652.7 / 667.1 /
+// 691.4) and 6 for groups of 4 or more.  Sweep at B=30720 (µs, best cap /
 // this model's / the tree-order kernel): known lengths Hq/Hkv 16/16 S=16
 // D=128 613.7 (4) / 613.7 (4) / 610.2, 32/16 S=16 665.0 (4) / 665.0 (4) /
 // 645.6, 32/32 S=16 D=256 2466.9 (4) / 2466.9 (4) / 2481.2, 16/16 S=5
 // D=256 440.0 (16) / 442.1 (12) / 416.9; device lengths 16/16 S=16 616.9
 // (4) / 626.1 (6; 5 here) / 614.6, 32/16 S=16 650.7 (6) / 650.7 (6) /
-// 645.7, 32/32 S=16 D=256 2504.1 (6) / 2504.1 (6) / 2505.3, the
-// reference's Poisson(4) lengths 16/16 D=128 191.8 (16) / 191.8 (16) /
-// 196.2, 32/32 D=256 837.8 (16) / 837.8 (16) / 823.3.
+// 645.7, 32/32 S=16 D=256 2504.1 (6) / 2504.1 (6) / 2505.3.
 int waves_per_cu_exact(int rows16, int g, int g_real, bool device_lengths) {
-  const int64_t unit_bytes16 = 1024LL * (2LL * rows16 + 32LL * g_real);  // 16 x bytes
-  const int64_t budget = (device_lengths ? 200LL : 144LL) * 1024;
-  const int64_t w = 16 * budget / unit_bytes16;
-  if (w >= 16) return kMaxWavesPerCU;
-  const int floor_w = g >= 4 ? 6 : 3 + g;
-  return w < floor_w ? floor_w : (int)w;
+  const WaveBudget m{device_lengths ? 200 : 144, 0, 2, g >= 4 ? 6 : 3 + g};
+  return budget_waves(m, rows16, g_real);
 }
 
 // Smallest power-of-two bucket >= s (s in [0, 16]); 0 selects bucket 1.
@@ -288,10 +269,7 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   }
   int w = exact ? waves_per_cu_exact(rows16, g, a.group, device_lengths)
                : waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
-  if (layout == fmha_decode::kLayoutPaged && !multi && g <= 2) {
-    const int64_t wp = 16LL * kInflightBytesPerCUPaged / (1024LL * (2LL * rows16 + 32LL * a.group));
-    w = wp >= 16 ? kMaxWavesPerCU : (wp < 3 ? 3 : (int)wp);
-  }
+  if (layout == fmha_decode::kLayoutPaged && !multi && g <= 2) w = budget_waves(kPagedBudget, rows16, a.group);
   // Waves that serve several batches (each lane group its own length and
   // rows) want at least 8 per CU at D <= 128 (B=30720 with lengths on the
   // device, µs at the byte model's cap / 8 waves: Hq/Hkv 8/1 S=16 79.0 /
