@@ -446,21 +446,26 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 
 // The matrix-core single pass with the row's scores in registers
 // (onepass_mfma_reg_kernel): workgroups of ceil(nblk / TPW) <= 8 waves, TPW
-// 16-row tiles per wave (8 up to 32 blocks, else 16), for groups of at most
-// 16 query heads per KV head (after padding), at least
+// 16-row tiles per wave (8 up to 32 blocks, 16 up to 128, 32 beyond at D <=
+// 128: rows of up to 4096 at D <= 128, 2048 at D = 256), for groups of at
+// most 16 query heads per KV head (after padding), at least
 // kOnepassMfmaMinUnits (batch, KV head) units and kOnepassRegMinBlocks
-// blocks on packed and strided caches, D = 64 and 128.  Against the LDS single pass at its best waves per row
-// (µs, packed, D = 128, B x Hq/Hkv x S): 256 x 64/8 x 1024 173.7 / 202.6,
-// 512 x 64/8 x 512 179.2 / 189.7, 1024 x 64/8 x 256 188.9 / 190.7, 128 x
-// 64/8 x 2048 174.5 / 194.7, 256 x 64/8 x 1536 261.9 / 297.8, 512 x 16/1 x
-// 600 31.5 / 36.6, 512 x 128/8 x 512 188.1 / 216.5, 64 x 96/8 x 300 26.0 /
-// 30.4, 1024 x 64/8 x 160 123.9 / 127.7, 4096 x 8/1 x 256 91.1 / 99.1 (x
+// blocks on packed and strided caches, D = 64 and 128.  Against the LDS
+// single pass at its best waves per row (µs, packed, D = 128, B x Hq/Hkv x
+// S): 256 x 64/8 x 1024 173.7 / 202.6, 512 x 64/8 x 512 179.2 / 189.7, 1024 x
+// 64/8 x 256 188.9 / 190.7, 128 x 64/8 x 2048 174.5 / 194.7, 256 x 64/8 x
+// 1536 261.9 / 297.8, 512 x 16/1 x 600 31.5 / 36.6, 512 x 128/8 x 512 188.1
+// / 216.5, 64 x 96/8 x 300 26.0 / 30.4, 1024 x 64/8 x 160 123.9 / 127.7,
+// 4096 x 8/1 x 256 91.1 / 99.1 (x
 // 128: 97.6 / 95.4); against the split passes at D = 64: 2048 x 64/8 x 256
 // 206.4 / 274.3, 1024 x 32/4 x 512 106.3 / 142.0, 4096 x 32/4 x 128 101.8 /
 // 147.6, 600 x 8/1 x 1200 65.1 / 68.4.  Eight tiles per wave against 16
 // (same shapes): 179.0 / 173.7, 179.2 / 183.3, 188.9 / 186.9, 34.1 / 31.5,
-// 188.1 / 190.3, 26.0 / 32.4, 123.9 / 125.4.  D = 256 keeps the LDS single
-// pass.  FMHA_DECODE_ONEPASS_REG=0 turns it off, =8 or 16 forces the tiles
+// 188.1 / 190.3, 26.0 / 32.4, 123.9 / 125.4.  32 tiles (256 VGPRs, 20 bytes
+// of scratch per lane, V two tiles ahead) against the split passes: 64 x
+// 32/8 x 4096 175.1 / 189.9, 128 x 64/8 x 4096 348.5 / 427.9, 128 x 32/8 x
+// 3000 268.5 / 280.0, 256 x 16/2 x 4096 181.5 / 218.9, D=64 512 x 16/1 x
+// 4000 104.3 / 174.3.  D = 256 keeps the LDS single pass.  FMHA_DECODE_ONEPASS_REG=0 turns it off, =8 or 16 forces the tiles
 // per wave (D = 256 included, for sweeps).
 constexpr int kOnepassRegMaxWaves = 8;
 // Rows of fewer blocks keep the split passes (three blocks: µs, 8/8
@@ -480,12 +485,12 @@ int onepass_reg_tiles(const SplitArgs& a) {
     const int g = a.num_heads_q / a.num_heads_kv;
     const int64_t units = (int64_t)a.batch * a.num_heads_kv;
     if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
-    int tpw = a.nblk <= 32 ? 8 : 16;
+    int tpw = a.nblk <= 32 ? 8 : a.nblk <= 128 ? 16 : 32;
     if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG"))
       tpw = std::atoi(e);
     else if (D == 256 || a.nblk < kOnepassRegMinBlocks)
       return 0;
-    if (tpw != 8 && tpw != 16) return 0;
+    if (tpw != 8 && tpw != 16 && !(tpw == 32 && D <= 128)) return 0;
     const int nw = (a.nblk + tpw - 1) / tpw;
     return nw <= kOnepassRegMaxWaves && fmha_decode::onepass_reg_lds_bytes<D>(nw) <= 160 * 1024 ? tpw : 0;
   }
@@ -500,12 +505,19 @@ hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
             layout_name(LAYOUT), nw, tpw, a.nblk);
   const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));
   const dim3 block((uint32_t)(kBlockThreads * nw));
-  if (tpw == 8)
+  if (tpw == 8) {
     hipLaunchKernelGGL((fmha_decode::onepass_mfma_reg_kernel<D, 8, kOnepassRegMaxWaves, LAYOUT>), grid, block, need,
                        stream, a);
-  else
+  } else if (tpw == 16) {
     hipLaunchKernelGGL((fmha_decode::onepass_mfma_reg_kernel<D, 16, kOnepassRegMaxWaves, LAYOUT>), grid, block, need,
                        stream, a);
+  } else {
+    if constexpr (D <= 128)
+      hipLaunchKernelGGL((fmha_decode::onepass_mfma_reg_kernel<D, 32, kOnepassRegMaxWaves, LAYOUT>), grid, block, need,
+                         stream, a);
+    else
+      return hipErrorInvalidValue;  // onepass_reg_tiles gives 32 only at D <= 128
+  }
   return hipGetLastError();
 }
 

@@ -639,9 +639,9 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
 // The tile loops are unrolled over TPW with no branch inside: the scores'
 // registers need static indices, and a branch per tile made the compiler
 // wait for every load in flight at each tile.  Packed and strided layouts.
-template <int D>
+template <int D, int TPW>
 constexpr int onepass_reg_pf() {
-  return D == 256 ? 2 : 4;  // tiles in flight per wave
+  return D == 256 || TPW >= 32 ? 2 : 4;  // V tiles in flight per wave
 }
 // LDS of a workgroup of nw waves: the (max, sum) exchange, then each wave's
 // K staging (16 rows of HPW tiles), whose space the fp32 sums of waves
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   constexpr int QLD = D / 32;  // 16-byte K chunks per lane per tile
   constexpr int DPC = D / 16;  // output dims per lane (one P.V MFMA each)
   constexpr int VW = DPC / 2;  // dwords of a lane's V run per row
-  constexpr int PF = onepass_reg_pf<D>();
+  constexpr int PF = onepass_reg_pf<D, TPW>();
   constexpr int NR = kSplitBlockRows;
   constexpr int R = TPW * NR;
   using Sh = GroupShape<D>;

@@ -234,7 +234,7 @@ def test_onepass_matrix_core_off(monkeypatch):
 # blocks, ceil(blocks / tiles) <= 8 waves per row), groups of 8-16 through
 # the matrix-core launcher and of 2 and 4 through the VALU one where the
 # one-wave single pass does not hold the row: 8 tiles per wave up to 32
-# blocks, else 16, or what FMHA_DECODE_ONEPASS_REG forces.
+# blocks, 16 up to 128, else 32, or what FMHA_DECODE_ONEPASS_REG forces.
 REG_ONEPASS_CASES = [
     (256, 64, 8, 128, 1024, 4, 16, None),   # G = 8
     (512, 16, 1, 128, 600, 3, 16, None),    # G = 16, one KV head
@@ -249,6 +249,9 @@ REG_ONEPASS_CASES = [
     (1024, 32, 4, 64, 128, 1, 8, None),     # D = 64, one wave
     (256, 32, 4, 256, 500, 2, 16, "16"),    # D = 256, forced
     (300, 16, 2, 128, 200, 1, 16, "16"),    # 16 tiles on a short row, forced
+    (64, 32, 8, 128, 4096, 8, 32, None),    # 32 tiles, G = 4, rows of 4096
+    (256, 16, 2, 128, 2100, 5, 32, None),   # 32 tiles, G = 8
+    (512, 16, 1, 64, 2500, 5, 32, None),    # 32 tiles, D = 64, G = 16
 ]
 
 
