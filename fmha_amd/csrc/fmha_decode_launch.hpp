@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "fmha_decode_caps.hpp"
 #include "fmha_decode_group.hpp"
 #include "fmha_decode_kernel.hpp"
 #include "fmha_decode_onepass.hpp"
@@ -47,16 +48,6 @@ inline const char* layout_name(int layout) {
   }
 }
 
-// Concurrency cap.  Each wave issues all of its loads at once, and MI355X
-// streams fastest with a bounded amount of them in flight per CU: 80 KiB for
-// the one- and two-head kernels with known lengths (3 waves of the S=16,
-// D=128 unit: 7.13 TB/s, against 6.63 TB/s uncapped; 6 waves of the S=5,
-// D=256 unit), the base of the in-flight budget model that sizes every
-// short-kernel launch (fmha_decode_api.hip: budget_waves).  Tiny units
-// (S=1) want every wave the registers allow.  The library reserves unused
-// LDS per workgroup so that only that many waves fit on a CU.
-constexpr int kInflightBytesPerCU = 80 * 1024;
-constexpr int kMaxWavesPerCU = 32;
 
 // Dynamic LDS bytes that leave room for exactly `waves` one-wave workgroups
 // on a CU with `lds_per_cu` bytes (0 when no cap is needed).

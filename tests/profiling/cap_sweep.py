@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Wave-cap sweep of the short kernels (lengths up to 16), for the in-flight
 budget model that picks each launch's waves per CU
-(fmha_amd/csrc/fmha_decode_api.hip: waves_per_cu_for, waves_per_cu_exact).
+(fmha_amd/csrc/fmha_decode_caps.hpp: budget_waves, tree_order_budget; fmha_decode_api.hip:
+waves_per_cu_for, waves_per_cu_exact).
 
 For each shape, times the call with FMHA_DECODE_WAVE_CAP set to every cap
 of --caps and once without it (the model's own cap, read back from

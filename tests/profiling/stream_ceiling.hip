@@ -25,6 +25,7 @@
 #include <cstring>
 #include <vector>
 
+#include "fmha_decode_caps.hpp"
 #include "fmha_decode_kernel.hpp"
 
 using namespace fmha_decode;
@@ -84,25 +85,15 @@ __global__ __launch_bounds__(64) void stream_kernel(const uint16_t* q, const uin
   }
 }
 
-// The library's cap for known lengths (fmha_decode_api.hip,
-// waves_per_cu_for): about 80 KiB of K/V/Q/O requests per CU for G <= 2, at
-// least 3 waves; a table by rows for the 4-head kernel (G = 3, 4); 200 KiB
-// and at least 4 waves for the 8-head kernel (G = 5-8) at D = 128, tables at
-// D = 64 and 256; no cap at 16 or more.  g: the real group size.
+// The library's cap for known lengths, one batch per wave: its in-flight
+// budget model (fmha_decode_caps.hpp) for the kernel of the call's group
+// (1, 2, 4 for G = 3-4, 8 for G = 5-8 and the VALU replay of larger
+// groups); 32: no cap.  g: the real group size.
 int waves_for(int rows, int g, int d) {
   const int gk = g <= 2 ? g : (g <= 4 ? 4 : 8);
-  if (gk == 4) {
-    static const int w128[17] = {8, 8, 7, 6, 5, 5, 5, 4, 4, 4, 4, 4, 4, 3, 3, 3, 3};
-    if (d == 128) return w128[rows < 16 ? rows : 16];
-    return rows <= 2 ? 32 : (rows <= 4 ? 6 : 4);
-  }
-  if (gk == 8 && d == 64) return rows <= 4 ? 32 : (rows <= 8 || g > 5 ? 6 : 5);
-  if (gk == 8 && d == 256 && rows > 2 && rows <= 8) return 5;
-  const int budget = (gk == 8 ? 200 : 80) * 1024;
-  int w = budget / (1024 * (2 * rows + 2 * g));
-  if (w >= 16) return 32;
-  const int floor_w = gk == 8 ? 4 : 3;
-  return w < floor_w ? floor_w : w;
+  using fmha_decode::host::budget_waves;
+  using fmha_decode::host::tree_order_budget;
+  return budget_waves(tree_order_budget(gk, d, false, false), 16 * rows, g);
 }
 
 size_t lds_reserve(int waves, size_t static_lds) {
