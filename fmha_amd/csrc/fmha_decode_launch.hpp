@@ -441,7 +441,10 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // 128: rows of up to 4096 at D <= 128, 2048 at D = 256), for groups of at
 // most 16 query heads per KV head (after padding), at least
 // kOnepassMfmaMinUnits (batch, KV head) units and kOnepassRegMinBlocks
-// blocks on packed and strided caches, D = 64 and 128.  Against the LDS
+// blocks on packed and strided caches and pages of at least 16 rows, D = 64
+// and 128 (16-row pages, µs against the split passes: B=256 S=1024 64/8
+// 178.6 / 228.4, B=128 S=2048 64/8 177.9 / 232.6, B=64 S=4096 32/8 177.7 /
+// 199.3, B=128 S=256 32/8 25.8 / 38.2).  Against the LDS
 // single pass at its best waves per row (µs, packed, D = 128, B x Hq/Hkv x
 // S): 256 x 64/8 x 1024 173.7 / 202.6, 512 x 64/8 x 512 179.2 / 189.7, 1024 x
 // 64/8 x 256 188.9 / 190.7, 128 x 64/8 x 2048 174.5 / 194.7, 256 x 64/8 x
@@ -470,7 +473,8 @@ constexpr int64_t kOnepassRegBeforeWaves = 1024;
 // apply.
 template <int D, int LAYOUT>
 int onepass_reg_tiles(const SplitArgs& a) {
-  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
+  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided &&
+                LAYOUT != fmha_decode::kLayoutPagedBlock) {
     return 0;
   } else {
     const int g = a.num_heads_q / a.num_heads_kv;
@@ -511,6 +515,11 @@ hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
   }
   return hipGetLastError();
 }
+
+// The register single pass's layout for a VALU launcher layout: 16-row
+// pages whichever way the VALU passes address them.
+template <int LAYOUT>
+constexpr int RegLayout = LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock : LAYOUT;
 
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
 // onepass_only: launch the single pass if it applies with every lane group
@@ -568,7 +577,9 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     // 161, D=64 B=43690 S=48 150 / 176; 64/8 D=128 against the register
     // single pass B=4096 S=64 205 / 211, B=2730 S=96 205 / 202, B=2048 S=128
     // 221 / 199).
-    constexpr bool kRegRows = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided);
+    constexpr bool kRegRows = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
+                                           LAYOUT == fmha_decode::kLayoutPagedBlock ||
+                                           LAYOUT == fmha_decode::kLayoutPagedBlockLanes);
     const int only_nblk =
         shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : kRegRows ? 6 : 8);
     // Groups of at most 4, one batch per wave, with fewer than
@@ -579,7 +590,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     bool reg_first = false;
     if constexpr (kRegRows && G <= 4)
       reg_first = !onepass_only && ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves &&
-                  onepass_reg_tiles<D, LAYOUT>(a) > 0;
+                  onepass_reg_tiles<D, RegLayout<LAYOUT>>(a) > 0;
     if (!reg_first && onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)
         if (ao.sub_shift > 0) return launch_onepass_dg<D, G, LAYOUT, true>(ao, stream);
@@ -601,6 +612,12 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
   }
   if (onepass_only) return kOnepassNotTaken;
+  if constexpr (G <= 4 && D == 128 &&
+                (LAYOUT == fmha_decode::kLayoutPagedBlock || LAYOUT == fmha_decode::kLayoutPagedBlockLanes)) {
+    // Pages of at least 16 rows: the register single pass, as below.
+    if (const int tpw = onepass_reg_tiles<D, fmha_decode::kLayoutPagedBlock>(a))
+      return launch_onepass_reg<D, fmha_decode::kLayoutPagedBlock>(a, tpw, stream);
+  }
   if constexpr (G <= 4 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)) {
     // Rows the one-wave single pass does not hold, of at least 4 blocks,
     // with enough (batch, KV head) units: the matrix-core single pass, its
@@ -696,10 +713,11 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
 // 4 VGPRs: 2 tiles (G <= 32 in one wave) at D = 64 and 128, one at D = 256.
 template <int D, int LAYOUT>
 hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
-  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided) {
+  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
+                LAYOUT == fmha_decode::kLayoutPagedBlock)
     if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
+  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
     if (const int nw = onepass_mfma_waves<D, LAYOUT>(a)) return launch_onepass_mfma<D, LAYOUT>(a, nw, stream);
-  }
   constexpr int HPW = kWaveSize / (D / 8);
   constexpr int TW = D == 256 ? 1 : 2;
   const int64_t g = a.num_heads_q / a.num_heads_kv;

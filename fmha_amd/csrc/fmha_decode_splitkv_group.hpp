@@ -638,7 +638,12 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
 // Rows past the wave's range are never read (out-of-range offsets read 0).
 // The tile loops are unrolled over TPW with no branch inside: the scores'
 // registers need static indices, and a branch per tile made the compiler
-// wait for every load in flight at each tile.  Packed and strided layouts.
+// wait for every load in flight at each tile.  Packed and strided layouts,
+// and pages of at least 16 rows (kLayoutPagedBlock), where a tile lies in
+// one page: K through per-lane page addresses (PagedLaneRows), V through a
+// descriptor per tile from the tile's block-table entry, which each wave
+// requests for all its tiles at the start; a negative entry among them
+// makes the (batch, KV head)'s outputs NaN, its rows never read.
 template <int D, int TPW>
 constexpr int onepass_reg_pf() {
   return D == 256 || TPW >= 32 ? 2 : 4;  // V tiles in flight per wave
@@ -659,7 +664,9 @@ constexpr size_t onepass_reg_lds_bytes(int nw) {
 
 template <int D, int TPW, int NWMAX, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel(SplitArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided || LAYOUT == kLayoutPagedBlock,
+                "packed, strided, or pages of at least 16 rows");
+  constexpr bool PAGED = LAYOUT == kLayoutPagedBlock;
   constexpr int QLD = D / 32;  // 16-byte K chunks per lane per tile
   constexpr int DPC = D / 16;  // output dims per lane (one P.V MFMA each)
   constexpr int VW = DPC / 2;  // dwords of a lane's V run per row
@@ -697,6 +704,20 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   const int lo = wv * R;
   const int span = S - lo < 0 ? 0 : (S - lo < R ? S - lo : R);
   const int nt = (span + NR - 1) / NR;
+  // Pages of at least 16 rows: a tile lies in one page.  Lane t < nt holds
+  // the block-table entry of the wave's tile t (entry 0, which a batch with
+  // rows always has, elsewhere), requested here, long before V needs it; K
+  // and V share the table, so a negative entry among them makes the
+  // (batch, KV head) invalid: its outputs are NaN and the unmapped rows are
+  // never read.
+  int32_t tile_entry = 0;
+  int unmapped = 0;
+  if constexpr (PAGED) {
+    const int32_t* pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+    const bool has = lane < nt;
+    tile_entry = pages[has ? (uint32_t)(lo + lane * NR) >> (uint32_t)a.page_shift : 0u];
+    unmapped = __builtin_amdgcn_ballot_w64(has && tile_entry < 0) != 0 ? 1 : 0;
+  }
 
   // ---- K: scores of the wave's tiles, kept in x ----
   // A round of HPW tiles: lane group s loads tile s's 16 rows whole (16
@@ -715,7 +736,7 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   const int s = lane / LPH;
   const int r = lane % LPH;
   char* stage = onepass_reg_lds + onepass_reg_stage_offset<D>(nw) + (size_t)wv * Sh::KS * NR;
-  LongRows<D, LAYOUT> kr;
+  typename std::conditional<PAGED, PagedLaneRows<D, true>, LongRows<D, LAYOUT>>::type kr;
   kr.init(a, a.k, b, split_row_base<LAYOUT>(a, b), lo, lo + span, (int)hk, true, r, s * NR);
   f32x4_v x[TPW];
   float m = -__builtin_inff();
@@ -766,24 +787,44 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
     pst[(wv * 16 + n) * 2 + 1] = cl;
   }
   // V rows of the wave's first tiles, in flight across the exchange.
-  LongRows<D, LAYOUT> vrw;
-  vrw.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, 0);
+  LongRows<D, PAGED ? kLayoutPacked : LAYOUT> vrw;
+  if constexpr (!PAGED) vrw.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, 0);
+  const uint32_t v_row_bytes = (uint32_t)kv_heads_mem(a) * D * 2u;       // paged: bytes per slot
+  const uint32_t v_head_off = (uint32_t)kv_head_mem(a, (int)hk) * D * 2u;  // paged: this KV head in a slot
   uint32_t vr[PF][4][VW];
   auto v_load = [&](int p, int t) {
+    // Paged: the tile's page through its entry (readlane: no table round
+    // trip here), a descriptor over the tile's rows in it (none when the
+    // entry is unmapped: nothing is read).
+    __amdgpu_buffer_rsrc_t v_rsrc;
+    if constexpr (PAGED) {
+      const int32_t e = __builtin_amdgcn_readlane(tile_entry, t);
+      const PagedRowU32 pr = paged_row_u32(e, (uint32_t)(lo + t * NR), (uint32_t)a.page_shift);
+      const int rows = pr.unmapped ? 0 : (span - t * NR < 0 ? 0 : (span - t * NR < NR ? span - t * NR : NR));
+      v_rsrc = make_rsrc(uniform_ptr(a.v + (uint64_t)pr.page * (uint64_t)a.batch_stride +
+                                     (uint64_t)pr.slot * (v_row_bytes >> 1)),
+                         (uint32_t)rows * v_row_bytes);
+    } else {
+      v_rsrc = vrw.rsrc;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = t * NR + 4 * q + e;
-      const uint32_t off = row < span ? vrw.lane_off + (uint32_t)(lo + row) * vrw.row_bytes + (uint32_t)(n * DPC * 2)
-                                      : kRowOutOfRange;
+      uint32_t off;
+      if constexpr (PAGED)  // from the tile's first row
+        off = row < span ? v_head_off + (uint32_t)(4 * q + e) * v_row_bytes + (uint32_t)(n * DPC * 2) : kRowOutOfRange;
+      else
+        off = row < span ? vrw.lane_off + (uint32_t)(lo + row) * vrw.row_bytes + (uint32_t)(n * DPC * 2)
+                         : kRowOutOfRange;
       if constexpr (VW == 2) {
         const u32x2 w2 = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrw.rsrc, (int)off, 0, kPolicyStream));
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(v_rsrc, (int)off, 0, kPolicyStream));
         vr[p][e][0] = w2[0];
         vr[p][e][1] = w2[1];
       } else {
 #pragma unroll
         for (int h = 0; h < VW / 4; ++h) {
-          const u32x4 w4 = buffer_load16_nt(vrw.rsrc, off + (uint32_t)h * 16u);
+          const u32x4 w4 = buffer_load16_nt(v_rsrc, off + (uint32_t)h * 16u);
 #pragma unroll
           for (int i = 0; i < 4; ++i) vr[p][e][4 * h + i] = w4[i];
         }
@@ -792,7 +833,7 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   };
 #pragma unroll
   for (int p = 0; p < PF; ++p) v_load(p, p);
-  __syncthreads();
+  const int poisoned = PAGED ? __syncthreads_or(unmapped) : (__syncthreads(), 0);
   float gm = -__builtin_inff();
   for (int w = 0; w < nw; ++w) gm = fmaxf(gm, pst[(w * 16 + n) * 2]);
   float gl = 0.0f;
@@ -845,13 +886,14 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
       }
     }
   }
-  // Lane (q, n) holds query rows 4q..4q+3, dims [n DPC, n DPC + DPC).
+  // Lane (q, n) holds query rows 4q..4q+3, dims [n DPC, n DPC + DPC);
+  // NaN for a (batch, KV head) that met an unmapped page.
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int g = 4 * q + e;
     float v[DPC];
 #pragma unroll
-    for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[dt][e];
+    for (int dt = 0; dt < DPC; ++dt) v[dt] = poisoned ? __builtin_nanf("") : acc[dt][e];
     store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
   }
 }
