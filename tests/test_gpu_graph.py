@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.common import assert_pass, default_scale, make_inputs, to_dev
+from tests.common import assert_pass, default_scale, last_plan, make_inputs, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -128,6 +128,67 @@ def test_graph_long_rows_replay_match_eager():
         for i, (o, e) in enumerate(zip(outs, eager)):
             assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
         fmha_amd.fmha_decode_splitkv(q2d, k2d, v2d, cu2d, 64)
+        torch.cuda.synchronize()
+
+
+def test_graph_register_single_pass_replays_match_eager():
+    """The matrix-core register single pass (no workspace, one launch) in a
+    graph: a packed call (G = 4, two waves per row) and the same rows over
+    16-row pages, each replay checked bit for bit against the eager result
+    and the eager result against the oracle."""
+    import torch
+    import fmha_amd
+    rng = np.random.default_rng(95)
+    B, Hq, Hkv, D, cap = 128, 32, 8, 128, 256
+    lens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    lens[:3] = [cap, 0, 17]
+    q, k, v, cu = make_inputs(B, Hq, Hkv, D, lens, seed=96)
+    qd, kd, vd, cud = to_dev(q), to_dev(k), to_dev(v), torch.from_numpy(cu).cuda()
+    npg = B * (cap // 16)
+    bt = torch.from_numpy(rng.permutation(npg).astype(np.int32).reshape(B, cap // 16)).cuda()
+    kc = torch.zeros(npg, 16, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    for b in range(B):
+        n, r0 = int(lens[b]), int(cu[b])
+        for j in range(0, n, 16):
+            m = min(16, n - j)
+            kc[int(bt[b, j // 16]), :m] = kd[r0 + j:r0 + j + m]
+            vc[int(bt[b, j // 16]), :m] = vd[r0 + j:r0 + j + m]
+    lensd = torch.from_numpy(lens).cuda()
+    outs = [torch.empty(B, Hq, D, dtype=torch.float16, device="cuda") for _ in range(2)]
+    kinds = []
+
+    def calls():
+        fmha_amd.fmha_decode_splitkv(qd, kd, vd, cud, cap, out=outs[0])
+        kinds.append(last_plan()[-1][0])
+        fmha_amd.fmha_decode_paged(qd, kc, vc, bt, lensd, out=outs[1], max_seqlen_kv=cap)
+        kinds.append(last_plan()[-1][0])
+
+    calls()
+    torch.cuda.synchronize()
+    assert kinds == ["onepass_matrix_core_regs"] * 2, kinds
+    eager = [o.clone() for o in outs]
+    assert torch.equal(eager[0].view(torch.int16), eager[1].view(torch.int16))
+    r, slack = oracle.decode(q, k, v, cu, Hq, Hkv, D, default_scale(D), with_slack=True, max_seqlen=cap)
+    assert_pass(oracle.compare(eager[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(r.shape), r, slack),
+                "register single pass")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        calls()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep}, call {i}"
+        fmha_amd.fmha_decode_splitkv(qd, kd, vd, cud, cap)
         torch.cuda.synchronize()
 
 
