@@ -523,3 +523,56 @@ def test_paged_single_pass_few_kv_heads_longer_rows(page_size, D, Hq, Hkv, B, ma
     assert _route() == PAGED_LONGER_ROUTES[(D, Hq, Hkv, max_len)][page_size >= 16], last_plan()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len,
            f"paged single pass longer rows ps={page_size} D={D} {Hq}/{Hkv} B={B} max={max_len}")
+
+
+def _random_register_cases(n=12, seed=2026):
+    """Seeded shapes inside the register single pass's domain: groups of
+    2-16 query heads per KV head (after padding), D = 64 or 128, at least
+    512 (batch, KV head) units, max_len from 4 blocks to 4096 rows, and the
+    layout: packed, BHSD, or pages of 16 or 32 rows."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        D = int(rng.choice([64, 128]))
+        G = int(rng.choice([2, 3, 4, 5, 6, 8, 12, 16]))
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        max_len = int(rng.integers(64, 4097))
+        units = int(rng.integers(512, 1400))
+        B = -(-units // Hkv)
+        layout = str(rng.choice(["packed", "bhsd", "paged16", "paged32"]))
+        # bound the oracle's work (rows x query heads x D)
+        if B * max_len * G * Hkv * D // 2 > 2.5e9:
+            continue
+        cases.append((D, G * Hkv, Hkv, B, max_len, layout))
+    return cases
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,B,max_len,layout", _random_register_cases())
+def test_register_single_pass_random_shapes(D, Hq, Hkv, B, max_len, layout):
+    """Seeded random shapes that the planner sends to the matrix-core register
+    single pass (where the VALU single pass does not hold the row first),
+    against the oracle, with ragged lengths (0, 1, one block and the maximum
+    among them); the plan is checked to be that pass for groups of 5 and
+    more, whose routes it always takes here."""
+    import fmha_amd
+    import torch
+    rng = np.random.default_rng(D + Hq * 7 + Hkv * 31 + B + max_len)
+    seqlens = rng.integers(0, max_len + 1, size=B).astype(np.int32)
+    seqlens[:4] = [max_len, 0, 1, 16]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=B + max_len + Hq)
+    print(f"register pass random: {layout} D={D} {Hq}/{Hkv} B={B} max={max_len}", flush=True)
+    if layout == "packed":
+        o = fmha_amd.fmha_decode_splitkv(to_dev(q), to_dev(kp), to_dev(vp), torch.from_numpy(cu).cuda(), max_len)
+    elif layout == "bhsd":
+        kc = _strided_view(_strided_cache(kp, seqlens, max_len, Hkv, D, "bhsd"), "bhsd")
+        vc = _strided_view(_strided_cache(vp, seqlens, max_len, Hkv, D, "bhsd"), "bhsd")
+        o = fmha_amd.fmha_decode_strided(to_dev(q), kc, vc, seqlens_kv=torch.from_numpy(seqlens).cuda())
+    else:
+        kc, vc, bt = _paged_cache(kp, vp, seqlens, int(layout[5:]), Hkv, D, rng)
+        o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                       torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
+    torch.cuda.synchronize()
+    kinds = [k for k, _ in last_plan()]
+    if Hq // Hkv >= 5:
+        assert kinds[-1] == "onepass_matrix_core_regs", last_plan()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"register pass random {layout} D={D} {Hq}/{Hkv} B={B}")
