@@ -516,6 +516,16 @@ hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Groups of at most 4 (on the VALU launcher) that the register single pass
+// takes where the VALU single pass does not hold the row: every such group
+// at D = 128, groups of 4 at D = 64, whose 16-column query tile then holds
+// 4 heads (µs, packed, register pass / split: 32/8 B=1024 S=512 216.5 /
+// 257.4, 16/4 B=256 S=1000 52.4 / 74.6); with one or two heads per tile the
+// VALU passes stay ahead there (16/8 B=512 S=600 130.8 / 115.7, 32/32
+// B=128 S=2048 424.7 / 341.8).
+template <int D, int G>
+constexpr bool kRegSmallGroups = G <= 4 && (D == 128 || (D == 64 && G == 4));
+
 // The register single pass's layout for a VALU launcher layout: 16-row
 // pages whichever way the VALU passes address them.
 template <int LAYOUT>
@@ -577,18 +587,20 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     // 161, D=64 B=43690 S=48 150 / 176; 64/8 D=128 against the register
     // single pass B=4096 S=64 205 / 211, B=2730 S=96 205 / 202, B=2048 S=128
     // 221 / 199).
-    constexpr bool kRegRows = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
-                                           LAYOUT == fmha_decode::kLayoutPagedBlock ||
-                                           LAYOUT == fmha_decode::kLayoutPagedBlockLanes);
+    constexpr bool kRegLonger = D == 128 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided);
     const int only_nblk =
-        shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : kRegRows ? 6 : 8);
+        shift > 0 ? (D == 64 ? 4 : D == 128 ? 6 : 8) : (D == 64 ? a.nblk : kRegLonger ? 6 : 8);
     // Groups of at most 4, one batch per wave, with fewer than
     // kOnepassRegBeforeWaves waves of the one-wave pass (too few to fill the
     // CUs): the register single pass below instead where it applies (µs,
     // 32/8 S=256, one-wave / register: B=256, 512 waves, 58.4 / 49.4;
     // B=512, 1024 waves, 90.5 / 93.7).
+    constexpr bool kRegRows =
+        kRegSmallGroups<D, G> && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
+                                  LAYOUT == fmha_decode::kLayoutPagedBlock ||
+                                  LAYOUT == fmha_decode::kLayoutPagedBlockLanes);
     bool reg_first = false;
-    if constexpr (kRegRows && G <= 4)
+    if constexpr (kRegRows)
       reg_first = !onepass_only && ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves &&
                   onepass_reg_tiles<D, RegLayout<LAYOUT>>(a) > 0;
     if (!reg_first && onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
@@ -612,7 +624,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
   }
   if (onepass_only) return kOnepassNotTaken;
-  if constexpr (G <= 4 && D == 128 &&
+  if constexpr (kRegSmallGroups<D, G> &&
                 (LAYOUT == fmha_decode::kLayoutPagedBlock || LAYOUT == fmha_decode::kLayoutPagedBlockLanes)) {
     // Pages of at least 16 rows: the register single pass, as below.
     if (const int tpw = onepass_reg_tiles<D, fmha_decode::kLayoutPagedBlock>(a))
@@ -638,7 +650,7 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     ag.sub_shift = 0;
     const bool group_fits = onepass_group_fits<D, G, LAYOUT>(ag);
     if (G == 1 && group_fits && a.nblk <= 64) return launch_onepass_group<D, G, LAYOUT>(ag, stream);
-    if constexpr (D == 128)
+    if constexpr (kRegSmallGroups<D, G>)
       if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
     // Too few units for one wave each: two waves per unit.
     if (group_fits) return launch_onepass_group<D, G, LAYOUT>(ag, stream);

@@ -252,6 +252,7 @@ REG_ONEPASS_CASES = [
     (64, 32, 8, 128, 4096, 8, 32, None),    # 32 tiles, G = 4, rows of 4096
     (256, 16, 2, 128, 2100, 5, 32, None),   # 32 tiles, G = 8
     (512, 16, 1, 64, 2500, 5, 32, None),    # 32 tiles, D = 64, G = 16
+    (256, 16, 4, 64, 1000, 4, 16, None),    # D = 64, G = 4 (the VALU launcher)
 ]
 
 
