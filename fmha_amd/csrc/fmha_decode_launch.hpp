@@ -441,8 +441,9 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // 128: rows of up to 4096 at D <= 128, 2048 at D = 256), for groups of at
 // most 16 query heads per KV head (after padding), at least
 // kOnepassMfmaMinUnits (batch, KV head) units and kOnepassRegMinBlocks
-// blocks on packed and strided caches and pages of at least 16 rows, D = 64
-// and 128 (16-row pages, µs against the split passes: B=256 S=1024 64/8
+// blocks (at D = 256 more than kOnepassReg256LdsBlocks) on packed and
+// strided caches and pages of at least 16 rows (16-row pages, µs against
+// the split passes: B=256 S=1024 64/8
 // 178.6 / 228.4, B=128 S=2048 64/8 177.9 / 232.6, B=64 S=4096 32/8 177.7 /
 // 199.3, B=128 S=256 32/8 25.8 / 38.2).  Against the LDS
 // single pass at its best waves per row (µs, packed, D = 128, B x Hq/Hkv x
@@ -459,12 +460,21 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // of scratch per lane, V two tiles ahead) against the split passes: 64 x
 // 32/8 x 4096 175.1 / 189.9, 128 x 64/8 x 4096 348.5 / 427.9, 128 x 32/8 x
 // 3000 268.5 / 280.0, 256 x 16/2 x 4096 181.5 / 218.9, D=64 512 x 16/1 x
-// 4000 104.3 / 174.3.  D = 256 keeps the LDS single pass.  FMHA_DECODE_ONEPASS_REG=0 turns it off, =8 or 16 forces the tiles
-// per wave (D = 256 included, for sweeps).
+// 4000 104.3 / 174.3.  FMHA_DECODE_ONEPASS_REG=0 turns it off, =8, 16 or
+// 32 forces the tiles per wave (32 at D <= 128; for sweeps).
 constexpr int kOnepassRegMaxWaves = 8;
 // Rows of fewer blocks keep the split passes (three blocks: µs, 8/8
 // B=200 S=40, 14.1 against 13.1).
 constexpr int kOnepassRegMinBlocks = 4;
+// At D = 256 the LDS single pass (one wave per row) keeps rows of up to
+// this many blocks and the register pass takes longer ones, 16 tiles per
+// wave (µs, Hq/Hkv 32/4, LDS / register: B=256 S=500 84.9 / 93.2, B=512
+// S=600 205.3 / 225.9; B=256 S=768 206.3 / 135.3, S=1024 272.1 / 176.5,
+// B=512 S=900 373.3 / 323.6, 64/8 B=256 S=1536 699.7 / 524.5; against the
+// matrix-core split passes B=128 S=2048 187.6 / 174.9, 64/8 B=64 S=2000
+// 194.7 / 173.4, 96/8 B=128 S=1024 223.4 / 193.8; 8 tiles per wave were
+// slower at every length swept).
+constexpr int kOnepassReg256LdsBlocks = 40;
 // Waves of the one-wave VALU single pass below which groups of at most 4
 // take the register single pass first (launch_split_dg).
 constexpr int64_t kOnepassRegBeforeWaves = 1024;
@@ -481,10 +491,14 @@ int onepass_reg_tiles(const SplitArgs& a) {
     const int64_t units = (int64_t)a.batch * a.num_heads_kv;
     if (g > 16 || units < kOnepassMfmaMinUnits || units > INT32_MAX) return 0;
     int tpw = a.nblk <= 32 ? 8 : a.nblk <= 128 ? 16 : 32;
-    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG"))
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG")) {
       tpw = std::atoi(e);
-    else if (D == 256 || a.nblk < kOnepassRegMinBlocks)
+    } else if (D == 256) {
+      if (a.nblk <= kOnepassReg256LdsBlocks) return 0;
+      tpw = 16;
+    } else if (a.nblk < kOnepassRegMinBlocks) {
       return 0;
+    }
     if (tpw != 8 && tpw != 16 && !(tpw == 32 && D <= 128)) return 0;
     const int nw = (a.nblk + tpw - 1) / tpw;
     return nw <= kOnepassRegMaxWaves && fmha_decode::onepass_reg_lds_bytes<D>(nw) <= 160 * 1024 ? tpw : 0;

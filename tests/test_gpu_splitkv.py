@@ -248,6 +248,7 @@ REG_ONEPASS_CASES = [
     (600, 8, 1, 64, 1200, 5, 16, None),     # D = 64
     (1024, 32, 4, 64, 128, 1, 8, None),     # D = 64, one wave
     (256, 32, 4, 256, 500, 2, 16, "16"),    # D = 256, forced
+    (256, 32, 4, 256, 1000, 4, 16, None),   # D = 256 beyond 40 blocks
     (300, 16, 2, 128, 200, 1, 16, "16"),    # 16 tiles on a short row, forced
     (64, 32, 8, 128, 4096, 8, 32, None),    # 32 tiles, G = 4, rows of 4096
     (256, 16, 2, 128, 2100, 5, 32, None),   # 32 tiles, G = 8
