@@ -362,9 +362,11 @@ constexpr hipError_t kOnepassNotTaken = hipErrorNotReady;
 // (onepass_mfma_kernel): NW waves per (batch, KV head), for groups of at
 // most 16 query heads per KV head (after padding) on packed and strided
 // caches, rows of at least 8 blocks and at least 512 units, where the
-// register single pass below does not apply (D = 256; D = 128 rows beyond
-// its 2048).  Against the matrix-core split passes (µs, packed, B x Hq/Hkv
-// x S; NW = 1 / 2 / 4 / split):
+// register single pass below does not apply: D = 256 rows of up to 40
+// blocks, one wave per row within 80 KiB of LDS.  At D = 128 and 64 the
+// register pass measured faster wherever this one fits, and takes those
+// rows.  Against the matrix-core split passes (µs, packed, B x Hq/Hkv x S;
+// NW = 1 / 2 / 4 / split):
 //   D = 128: 1024 x 64/8 x 160: 127.9 / 156.1 / 166.7 / 145.9; x 256:
 //   199.7 / 191.6 / 205.9 / 220.4; 512 x 64/8 x 512: 200.8 / 189.3 / 258.0
 //   / 220.0; 256 x 64/8 x 1024: 255.5 / 202.4 / 217.2 / 219.1; x 1536:
@@ -375,9 +377,7 @@ constexpr hipError_t kOnepassNotTaken = hipErrorNotReady;
 //   D = 256: 256 x 32/4 x 500: 85.3 / 102.5 / 104.6 / 100.6 (the register
 //   single pass: 93.2 with 16 tiles per wave, 96.4 with 8);
 //   D = 64: 600 x 8/1 x 1200: 145.5 / 81.3 / 81.7 / 68.4.
-// So at D = 128 one wave per row up to 12 blocks, two while a workgroup's
-// LDS stays within 80 KiB (two workgroups per CU), four while it stays
-// within 144 KiB; at D = 256 one wave within 80 KiB.
+// At D = 256 one wave per row within 80 KiB.
 // FMHA_DECODE_ONEPASS_MFMA=0 turns it off and =1, 2, 4 forces the waves
 // per row wherever the LDS fits (for sweeps).
 constexpr int64_t kOnepassMfmaMinUnits = 512;
@@ -400,14 +400,10 @@ int onepass_mfma_waves(const SplitArgs& a) {
       if (v == 1 || v == 2 || v == 4) return lds(v) <= 160 * 1024 ? v : 0;
     }
     if (a.nblk < kOnepassMfmaMinBlocks) return 0;
-    if constexpr (D == 128) {
-      if (a.nblk <= 12) return lds(1) <= 80 * 1024 ? 1 : 0;
-      if (lds(2) <= 80 * 1024) return 2;
-      return lds(4) <= 144 * 1024 ? 4 : 0;
-    } else if constexpr (D == 256) {
+    if constexpr (D == 256) {
       return lds(1) <= 80 * 1024 ? 1 : 0;
     } else {
-      return 0;
+      return 0;  // the register single pass takes these rows
     }
   }
 }

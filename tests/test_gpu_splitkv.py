@@ -173,20 +173,20 @@ def test_onepass_group_off(monkeypatch):
 
 # (B, Hq, Hkv, D, max_len, waves, force): the matrix-core single pass with
 # the scores in LDS (8 to 16 query heads per KV head after padding, at least
-# 512 (batch, KV head) units, a row's scores within a workgroup's LDS) with
-# the waves per row the planner picks (one up to 12 blocks and at D = 256,
-# two, four on long rows) or that FMHA_DECODE_ONEPASS_MFMA forces; the
-# register single pass off (FMHA_DECODE_ONEPASS_REG=0) except at D = 256,
-# which it leaves to this kernel.
+# 512 (batch, KV head) units, a row's scores within a workgroup's LDS): the
+# planner's one wave per row at D = 256 up to 40 blocks, and at D = 128 and
+# 64, where the register single pass takes every row this one fits, the
+# waves per row FMHA_DECODE_ONEPASS_MFMA forces; the register single pass
+# off (FMHA_DECODE_ONEPASS_REG=0).
 MFMA_ONEPASS_CASES = [
-    (256, 64, 8, 128, 1024, 2, None),   # G = 8
-    (512, 16, 1, 128, 600, 2, None),    # G = 16, one KV head
-    (128, 40, 8, 128, 700, 2, None),    # G = 5 on a group padded to 8
-    (64, 96, 8, 128, 300, 2, None),     # G = 12 on a group padded to 16
-    (600, 16, 2, 128, 150, 1, None),    # 10 blocks: one wave
-    (512, 8, 1, 128, 1600, 4, None),    # 100 blocks: four waves
-    (256, 32, 4, 256, 500, 1, None),    # D = 256
-    (600, 8, 1, 64, 1200, 2, "2"),      # D = 64, forced
+    (256, 64, 8, 128, 1024, 2, "2"),    # G = 8
+    (512, 16, 1, 128, 600, 2, "2"),     # G = 16, one KV head
+    (128, 40, 8, 128, 700, 2, "2"),     # G = 5 on a group padded to 8
+    (64, 96, 8, 128, 300, 2, "2"),      # G = 12 on a group padded to 16
+    (600, 16, 2, 128, 150, 1, "1"),     # 10 blocks, one wave
+    (512, 8, 1, 128, 1600, 4, "4"),     # 100 blocks, four waves
+    (256, 32, 4, 256, 500, 1, None),    # D = 256, the planner's
+    (600, 8, 1, 64, 1200, 2, "2"),      # D = 64
     (300, 16, 2, 128, 200, 4, "4"),     # four waves on a short row
 ]
 
