@@ -437,9 +437,10 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // 128: rows of up to 4096 at D <= 128, 2048 at D = 256), for groups of at
 // most 16 query heads per KV head (after padding), at least
 // kOnepassMfmaMinUnits (batch, KV head) units and kOnepassRegMinBlocks
-// blocks (at D = 256 more than kOnepassReg256LdsBlocks) on packed and
-// strided caches and pages of at least 16 rows (16-row pages, µs against
-// the split passes: B=256 S=1024 64/8
+// blocks (at D = 256 more than kOnepassReg256LdsBlocks) on packed,
+// strided and paged caches (one-row pages, µs against the split passes:
+// B=256 S=1024 64/8 189.3 / 241.6, B=128 S=256 32/8 27.4 / 45.5; 16-row
+// pages: B=256 S=1024 64/8
 // 178.6 / 228.4, B=128 S=2048 64/8 177.9 / 232.6, B=64 S=4096 32/8 177.7 /
 // 199.3, B=128 S=256 32/8 25.8 / 38.2).  Against the LDS
 // single pass at its best waves per row (µs, packed, D = 128, B x Hq/Hkv x
@@ -480,7 +481,7 @@ constexpr int64_t kOnepassRegBeforeWaves = 1024;
 template <int D, int LAYOUT>
 int onepass_reg_tiles(const SplitArgs& a) {
   if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided &&
-                LAYOUT != fmha_decode::kLayoutPagedBlock) {
+                LAYOUT != fmha_decode::kLayoutPagedBlock && LAYOUT != fmha_decode::kLayoutPaged) {
     return 0;
   } else {
     const int g = a.num_heads_q / a.num_heads_kv;
@@ -536,10 +537,16 @@ hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
 template <int D, int G>
 constexpr bool kRegSmallGroups = G <= 4 && (D == 128 || (D == 64 && G == 4));
 
-// The register single pass's layout for a VALU launcher layout: 16-row
-// pages whichever way the VALU passes address them.
+// The register single pass's layout for a VALU launcher layout: pages of
+// either size whichever way the VALU passes address them.
 template <int LAYOUT>
-constexpr int RegLayout = LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock : LAYOUT;
+constexpr int RegLayout = LAYOUT == fmha_decode::kLayoutPagedBlockLanes ? fmha_decode::kLayoutPagedBlock
+                          : LAYOUT == fmha_decode::kLayoutPagedLanes    ? fmha_decode::kLayoutPaged
+                                                                        : LAYOUT;
+template <int LAYOUT>
+constexpr bool kPagedLayout = LAYOUT == fmha_decode::kLayoutPaged || LAYOUT == fmha_decode::kLayoutPagedLanes ||
+                              LAYOUT == fmha_decode::kLayoutPagedBlock ||
+                              LAYOUT == fmha_decode::kLayoutPagedBlockLanes;
 
 // LAYOUT: how the K/V rows are addressed (fmha_decode::LongRows).
 // onepass_only: launch the single pass if it applies with every lane group
@@ -605,10 +612,8 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     // CUs): the register single pass below instead where it applies (µs,
     // 32/8 S=256, one-wave / register: B=256, 512 waves, 58.4 / 49.4;
     // B=512, 1024 waves, 90.5 / 93.7).
-    constexpr bool kRegRows =
-        kRegSmallGroups<D, G> && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
-                                  LAYOUT == fmha_decode::kLayoutPagedBlock ||
-                                  LAYOUT == fmha_decode::kLayoutPagedBlockLanes);
+    constexpr bool kRegRows = kRegSmallGroups<D, G> && (LAYOUT == fmha_decode::kLayoutPacked ||
+                                                        LAYOUT == fmha_decode::kLayoutStrided || kPagedLayout<LAYOUT>);
     bool reg_first = false;
     if constexpr (kRegRows)
       reg_first = !onepass_only && ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves &&
@@ -634,11 +639,12 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     }
   }
   if (onepass_only) return kOnepassNotTaken;
-  if constexpr (kRegSmallGroups<D, G> &&
-                (LAYOUT == fmha_decode::kLayoutPagedBlock || LAYOUT == fmha_decode::kLayoutPagedBlockLanes)) {
-    // Pages of at least 16 rows: the register single pass, as below.
-    if (const int tpw = onepass_reg_tiles<D, fmha_decode::kLayoutPagedBlock>(a))
-      return launch_onepass_reg<D, fmha_decode::kLayoutPagedBlock>(a, tpw, stream);
+  if constexpr ((kRegSmallGroups<D, G> || G == 8) && kPagedLayout<LAYOUT>) {
+    // Paged caches: the register single pass, as below for groups of at
+    // most 4, and for groups of 8 on the pages under 16 rows that the
+    // planner leaves to the VALU passes (half a wave of KV heads or more).
+    if (const int tpw = onepass_reg_tiles<D, RegLayout<LAYOUT>>(a))
+      return launch_onepass_reg<D, RegLayout<LAYOUT>>(a, tpw, stream);
   }
   if constexpr (G <= 4 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)) {
     // Rows the one-wave single pass does not hold, of at least 4 blocks,
@@ -736,7 +742,7 @@ hipError_t launch_split_layout(const SplitArgs& a, int d, int g, hipStream_t str
 template <int D, int LAYOUT>
 hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
   if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
-                LAYOUT == fmha_decode::kLayoutPagedBlock)
+                LAYOUT == fmha_decode::kLayoutPagedBlock || LAYOUT == fmha_decode::kLayoutPaged)
     if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
   if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
     if (const int nw = onepass_mfma_waves<D, LAYOUT>(a)) return launch_onepass_mfma<D, LAYOUT>(a, nw, stream);

@@ -639,11 +639,13 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
 // The tile loops are unrolled over TPW with no branch inside: the scores'
 // registers need static indices, and a branch per tile made the compiler
 // wait for every load in flight at each tile.  Packed and strided layouts,
-// and pages of at least 16 rows (kLayoutPagedBlock), where a tile lies in
-// one page: K through per-lane page addresses (PagedLaneRows), V through a
-// descriptor per tile from the tile's block-table entry, which each wave
-// requests for all its tiles at the start; a negative entry among them
-// makes the (batch, KV head)'s outputs NaN, its rows never read.
+// and paged ones: pages of at least 16 rows (kLayoutPagedBlock), where a
+// tile lies in one page, K through per-lane page addresses (PagedLaneRows),
+// V through a descriptor per tile from the tile's block-table entry, which
+// each wave requests for all its tiles at the start; smaller pages
+// (kLayoutPaged), every row through its own entry and a per-lane address,
+// the entries requested ahead of their rows.  A negative entry among a
+// (batch, KV head)'s rows makes its outputs NaN, its rows never read.
 template <int D, int TPW>
 constexpr int onepass_reg_pf() {
   return D == 256 || TPW >= 32 ? 2 : 4;  // V tiles in flight per wave
@@ -664,9 +666,11 @@ constexpr size_t onepass_reg_lds_bytes(int nw) {
 
 template <int D, int TPW, int NWMAX, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel(SplitArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided || LAYOUT == kLayoutPagedBlock,
-                "packed, strided, or pages of at least 16 rows");
-  constexpr bool PAGED = LAYOUT == kLayoutPagedBlock;
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided || LAYOUT == kLayoutPagedBlock ||
+                    LAYOUT == kLayoutPaged,
+                "packed, strided or paged");
+  constexpr bool PAGED = LAYOUT == kLayoutPagedBlock;  // pages of at least 16 rows
+  constexpr bool PAGED_ROWS = LAYOUT == kLayoutPaged;  // pages under 16 rows
   constexpr int QLD = D / 32;  // 16-byte K chunks per lane per tile
   constexpr int DPC = D / 16;  // output dims per lane (one P.V MFMA each)
   constexpr int VW = DPC / 2;  // dwords of a lane's V run per row
@@ -736,13 +740,24 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   const int s = lane / LPH;
   const int r = lane % LPH;
   char* stage = onepass_reg_lds + onepass_reg_stage_offset<D>(nw) + (size_t)wv * Sh::KS * NR;
-  typename std::conditional<PAGED, PagedLaneRows<D, true>, LongRows<D, LAYOUT>>::type kr;
+  typename std::conditional<PAGED || PAGED_ROWS, PagedLaneRows<D, PAGED>, LongRows<D, LAYOUT>>::type kr;
   kr.init(a, a.k, b, split_row_base<LAYOUT>(a, b), lo, lo + span, (int)hk, true, r, s * NR);
   f32x4_v x[TPW];
   float m = -__builtin_inff();
   if (nt > 0) {
     u32x4 kb[NR];
-    kr.template load<NR>(kb, 0);
+    // Pages under 16 rows: each row's block-table entry, requested a round
+    // ahead of its rows (entries and rows complete in request order, so
+    // the entries of round k + 2 go out after the rows of round k + 1,
+    // and waiting for them waits for nothing the round does not need).
+    int32_t ek[PAGED_ROWS ? NR : 1];
+    if constexpr (PAGED_ROWS) {
+      kr.template entries<NR>(ek, 0);
+      kr.template load_entries<NR>(kb, 0, ek);
+      if (TPW / HPW > 1) kr.template entries<NR>(ek, HPW * NR);
+    } else {
+      kr.template load<NR>(kb, 0);
+    }
 #pragma unroll
     for (int k = 0; k < TPW / HPW; ++k) {
       wave_lds_sync();  // the previous round's reads of the staging are done
@@ -750,7 +765,14 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
       for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(stage + j * Sh::KS + s * D * 2 + r * 16) = kb[j];
       wave_lds_sync();
       __builtin_amdgcn_sched_barrier(0);
-      if (k + 1 < TPW / HPW) kr.template load<NR>(kb, (k + 1) * HPW * NR);
+      if constexpr (PAGED_ROWS) {
+        if (k + 1 < TPW / HPW) {
+          kr.template load_entries<NR>(kb, (k + 1) * HPW * NR, ek);
+          if (k + 2 < TPW / HPW) kr.template entries<NR>(ek, (k + 2) * HPW * NR);
+        }
+      } else if (k + 1 < TPW / HPW) {
+        kr.template load<NR>(kb, (k + 1) * HPW * NR);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int p = 0; p < HPW; ++p) {
@@ -787,12 +809,55 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
     pst[(wv * 16 + n) * 2 + 1] = cl;
   }
   // V rows of the wave's first tiles, in flight across the exchange.
-  LongRows<D, PAGED ? kLayoutPacked : LAYOUT> vrw;
-  if constexpr (!PAGED) vrw.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, 0);
+  // A wave of pages under 16 rows has met an unmapped page among its rows
+  // if its K loads have (V reads the same rows through the same table).
+  if constexpr (PAGED_ROWS) unmapped = __builtin_amdgcn_ballot_w64(kr.bad != 0) != 0 ? 1 : 0;
+  LongRows<D, PAGED || PAGED_ROWS ? kLayoutPacked : LAYOUT> vrw;
+  if constexpr (!PAGED && !PAGED_ROWS) vrw.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, 0);
   const uint32_t v_row_bytes = (uint32_t)kv_heads_mem(a) * D * 2u;       // paged: bytes per slot
   const uint32_t v_head_off = (uint32_t)kv_head_mem(a, (int)hk) * D * 2u;  // paged: this KV head in a slot
   uint32_t vr[PF][4][VW];
+  // Pages under 16 rows: the entries of this lane's four rows of a tile,
+  // requested PF tiles ahead of the tile's rows (after the rows of the tile
+  // PF steps earlier, so waiting for them waits only for rows already due).
+  int32_t ev[PAGED_ROWS ? PF : 1][4];
+  const int32_t* v_pages = a.block_table + (uint64_t)b * (uint64_t)a.bt_stride;
+  auto v_entries = [&](int p, int t) {
+    if constexpr (PAGED_ROWS) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = t * NR + 4 * q + e;
+        ev[p][e] = v_pages[row < span ? (uint32_t)(lo + row) >> (uint32_t)a.page_shift : 0u];
+      }
+    }
+  };
   auto v_load = [&](int p, int t) {
+    if constexpr (PAGED_ROWS) {
+      // Per-lane addresses; a row past the wave's rows or in an unmapped
+      // page reads Q's first row (memory that exists) and becomes 0.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = t * NR + 4 * q + e;
+        const PagedRowU32 pr = paged_row_u32(ev[p][e], (uint32_t)(lo + row), (uint32_t)a.page_shift);
+        const bool ok = row < span && !pr.unmapped;
+        const uint16_t* src = ok ? a.v + (uint64_t)pr.page * (uint64_t)a.batch_stride +
+                                       (uint64_t)pr.slot * (v_row_bytes >> 1) + (v_head_off >> 1) + n * DPC
+                                 : a.q;
+        if constexpr (VW == 2) {
+          const u32x2 w2 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+          vr[p][e][0] = ok ? w2[0] : 0u;
+          vr[p][e][1] = ok ? w2[1] : 0u;
+        } else {
+#pragma unroll
+          for (int h = 0; h < VW / 4; ++h) {
+            const u32x4 w4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vr[p][e][4 * h + i] = ok ? w4[i] : 0u;
+          }
+        }
+      }
+      return;
+    }
     // Paged: the tile's page through its entry (readlane: no table round
     // trip here), a descriptor over the tile's rows in it (none when the
     // entry is unmapped: nothing is read).
@@ -831,9 +896,17 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
       }
     }
   };
+  if constexpr (PAGED_ROWS) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) v_entries(p, p);
+  }
 #pragma unroll
   for (int p = 0; p < PF; ++p) v_load(p, p);
-  const int poisoned = PAGED ? __syncthreads_or(unmapped) : (__syncthreads(), 0);
+  if constexpr (PAGED_ROWS) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) v_entries(p, p + PF);
+  }
+  const int poisoned = PAGED || PAGED_ROWS ? __syncthreads_or(unmapped) : (__syncthreads(), 0);
   float gm = -__builtin_inff();
   for (int w = 0; w < nw; ++w) gm = fmaxf(gm, pst[(w * 16 + n) * 2]);
   float gl = 0.0f;
@@ -863,7 +936,10 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
                           __builtin_amdgcn_perm(vr[p][3][dt / 2], vr[p][2][dt / 2], sel)};
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(bf16x4_v, w2), acc[dt], 0, 0, 0);
       }
-      if (t + PF < TPW) v_load(p, t + PF);
+      if (t + PF < TPW) {
+        v_load(p, t + PF);
+        if (t + 2 * PF < TPW) v_entries(p, t + 2 * PF);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }

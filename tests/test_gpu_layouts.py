@@ -261,11 +261,13 @@ NEG_CASES = [
     (32, 16, 128, 8, 1, 2100, ("onepass", "paged16_lanes")), (32, 1, 64, 8, 1, 4200, ("onepass", "paged_lanes")),
     (64, 16, 64, 8, 1, 4200, ("onepass", "paged16_lanes")), (48, 16, 128, 4, 1, 2100, ("onepass", "paged16_lanes")),
     (128, 1, 64, 2, 1, 4200, ("onepass", "paged_lanes")), (128, 4, 128, 8, 2, 1100, ("onepass", "paged_lanes")),
-    # rows of 4 blocks and more with >= 512 (batch, KV head) units on pages of
-    # 16 rows and more: the matrix-core register single pass (groups of 8 and
-    # 4, one and two waves per row)
+    # rows of 4 blocks and more with >= 512 (batch, KV head) units: the
+    # matrix-core register single pass (groups of 8 and 4, pages of 16 and
+    # 32 rows, then of 1 and 4)
     (600, 16, 128, 64, 8, 128, ("onepass_matrix_core_regs", "paged16")),
     (300, 32, 128, 32, 8, 128, ("onepass_matrix_core_regs", "paged16")),
+    (600, 1, 128, 64, 8, 128, ("onepass_matrix_core_regs", "paged")),
+    (300, 4, 128, 32, 8, 128, ("onepass_matrix_core_regs", "paged")),
 ]
 
 

@@ -389,13 +389,14 @@ def test_paged_long_few_kv_heads(page_size, D, Hq, Hkv, B, max_len):
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged ps={page_size} D={D} {Hq}/{Hkv} B={B}")
 
 
-@pytest.mark.parametrize("page_size", [16, 32, 64])
+@pytest.mark.parametrize("page_size", [1, 4, 8, 16, 32, 64])
 @pytest.mark.parametrize("Hq,Hkv,B,max_len", [(64, 8, 128, 1000), (32, 8, 100, 700), (128, 8, 70, 2000)])
 def test_paged_onepass_registers(page_size, Hq, Hkv, B, max_len):
-    """Pages of 16 rows and more, rows of 4 blocks and more with >= 512
-    (batch, KV head) units: the matrix-core register single pass (groups of
-    8, 4 and 16), each 16-row tile read through its page, NaN in every slot
-    no batch owns; ragged lengths, empty rows and 16-row edges."""
+    """Paged caches, rows of 4 blocks and more with >= 512 (batch, KV head)
+    units: the matrix-core register single pass (groups of 8, 4 and 16),
+    each 16-row tile read through its page (pages of 16 rows and more) or
+    each row through its own (smaller pages), NaN in every slot no batch
+    owns; ragged lengths, empty rows and 16-row edges."""
     import fmha_amd
     import torch
     D = 128
@@ -408,7 +409,7 @@ def test_paged_onepass_registers(page_size, Hq, Hkv, B, max_len):
     o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
                                    torch.from_numpy(seqlens).cuda(), max_seqlen_kv=max_len)
     torch.cuda.synchronize()
-    assert _route() == ("onepass_matrix_core_regs", "paged16"), last_plan()
+    assert _route() == ("onepass_matrix_core_regs", "paged16" if page_size >= 16 else "paged"), last_plan()
     _check(o, q, kp, vp, seqlens, Hq, Hkv, D, max_len, f"paged register pass ps={page_size} {Hq}/{Hkv} B={B}")
 
 
@@ -422,8 +423,8 @@ def _route():
 # (pages under 16 rows, 16-row pages and larger).  "onepass" with a *_lanes
 # layout is the single pass with per-lane page lookups (several batches per
 # wave); pages under 16 rows with groups of 4-8 at D >= 128 take the
-# matrix-core split on short rows, and 16-row pages with rows of four blocks
-# the matrix-core register single pass (the planner's rules in
+# matrix-core split on short rows, and rows of four blocks the matrix-core
+# register single pass (the planner's rules in
 # split_on_matrix_cores, launch_split_dg and onepass_reg_tiles,
 # fmha_decode_api.hip / fmha_decode_launch.hpp).
 _MC = ("split_matrix_core", "paged")
@@ -431,12 +432,13 @@ _MC16 = ("split_matrix_core", "paged16")
 _LANES = ("onepass", "paged_lanes")
 _LANES16 = ("onepass", "paged16_lanes")
 _REG16 = ("onepass_matrix_core_regs", "paged16")
+_REG = ("onepass_matrix_core_regs", "paged")
 PAGED_FEW_ROUTES = {
-    (128, 8, 1, 17): (_MC, _LANES16), (128, 8, 1, 32): (_MC, _LANES16), (128, 8, 1, 64): (_MC, _REG16),
-    (128, 16, 2, 17): (_MC, _LANES16), (128, 16, 2, 32): (_MC, _LANES16), (128, 16, 2, 64): (_MC, _REG16),
+    (128, 8, 1, 17): (_MC, _LANES16), (128, 8, 1, 32): (_MC, _LANES16), (128, 8, 1, 64): (_REG, _REG16),
+    (128, 16, 2, 17): (_MC, _LANES16), (128, 16, 2, 32): (_MC, _LANES16), (128, 16, 2, 64): (_REG, _REG16),
     (256, 4, 1, 17): (_MC, _LANES16), (256, 4, 1, 32): (_MC, _LANES16),
     (256, 4, 1, 64): (("onepass", "paged"), ("onepass", "paged16")),
-    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_MC, _LANES16),
+    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_REG, _LANES16),
     (128, 40, 8, 17): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 32): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 64): (("onepass", "paged"), ("onepass", "paged16")),
