@@ -728,8 +728,9 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   // bytes per lane, chunk r), stores them to the wave's staging, and the
   // MFMA A operands (row n, chunks 4c + q) are read back from there; the
   // next round's rows are in flight during a round's products.  Tiles past
-  // the wave's rows read 0 without memory access and are masked; the loops
-  // carry no branch, one branch skips them for a wave without rows.
+  // the wave's rows read 0 (without memory access; on pages under 16 rows
+  // from Q's first row) and are masked; the loops carry no branch, one
+  // branch skips them for a wave without rows.
   const __amdgpu_buffer_rsrc_t q_rsrc =
       make_rsrc(a.q + ((uint64_t)b * hq + (uint64_t)hk * G) * D, (uint32_t)G * D * 2u);
   bf16x8_v qb[QLD];
