@@ -230,8 +230,9 @@ def test_onepass_matrix_core_off(monkeypatch):
 
 
 # (B, Hq, Hkv, D, max_len, waves, tiles, force): the matrix-core single pass
-# with the scores in registers (at least 512 (batch, KV head) units and 4
-# blocks, ceil(blocks / tiles) <= 8 waves per row), groups of 8-16 through
+# with the scores in registers (at least 512 (batch, KV head) units, at D =
+# 128 128 for groups of 5 and more and 256 below, and 4 blocks,
+# ceil(blocks / tiles) <= 8 waves per row), groups of 8-16 through
 # the matrix-core launcher and of 2 and 4 through the VALU one where the
 # one-wave single pass does not hold the row: 8 tiles per wave up to 32
 # blocks, 16 up to 128, else 32, or what FMHA_DECODE_ONEPASS_REG forces.
@@ -254,6 +255,9 @@ REG_ONEPASS_CASES = [
     (256, 16, 2, 128, 2100, 5, 32, None),   # 32 tiles, G = 8
     (512, 16, 1, 64, 2500, 5, 32, None),    # 32 tiles, D = 64, G = 16
     (256, 16, 4, 64, 1000, 4, 16, None),    # D = 64, G = 4 (the VALU launcher)
+    (128, 16, 2, 128, 1024, 4, 16, None),   # 256 units, G = 8
+    (16, 64, 8, 128, 1024, 4, 16, None),    # 128 units, G = 8
+    (64, 16, 4, 128, 512, 4, 8, None),      # 256 units, G = 4
 ]
 
 
