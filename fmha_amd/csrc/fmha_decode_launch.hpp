@@ -436,8 +436,8 @@ hipError_t launch_onepass_mfma(const SplitArgs& a, int nw, hipStream_t stream) {
 // 16-row tiles per wave (8 up to 32 blocks, 16 up to 128, 32 beyond at D <=
 // 128: rows of up to 4096 at D <= 128, 2048 at D = 256), for groups of at
 // most 16 query heads per KV head (after padding), at least
-// kOnepassMfmaMinUnits (batch, KV head) units (fewer at D = 128:
-// kOnepassRegMinUnitsWide / Small) and kOnepassRegMinBlocks
+// 128-256 (batch, KV head) units (kOnepassRegMinUnitsWide / Small / 256)
+// and kOnepassRegMinBlocks
 // blocks (at D = 256 more than kOnepassReg256LdsBlocks) on packed,
 // strided and paged caches (one-row pages, µs against the split passes:
 // B=256 S=1024 64/8 189.3 / 241.6, B=128 S=256 32/8 27.4 / 45.5; 16-row
@@ -473,17 +473,21 @@ constexpr int kOnepassRegMinBlocks = 4;
 // 194.7 / 173.4, 96/8 B=128 S=1024 223.4 / 193.8; 8 tiles per wave were
 // slower at every length swept).
 constexpr int kOnepassReg256LdsBlocks = 40;
-// At D = 128 fewer (batch, KV head) units than kOnepassMfmaMinUnits still
-// fill the CUs with several waves per row: 128 units from groups of 5 (the
-// matrix-core split passes the alternative), 256 below (the VALU ones).
-// µs, packed, register pass / split passes: 16/2 B=128 S=1024 (256 units)
-// 29.8 / 47.9, 64/8 B=32 S=1024 28.6 / 47.1, B=48 S=2048 79.3 / 99.7, 32/8
-// B=32 S=4096 93.1 / 104.5, 16/4 B=64 S=512 16.9 / 26.7; 64/8 B=16 S=4096
-// (128 units) 66.0 / 72.1, S=1024 24.7 / 33.7; fewer lose, 64/8 B=8 S=4096
-// (64 units) 60.9 / 47.4, and so do groups of 4 at 128, 32/8 B=16 S=4096
-// 66.0 / 61.0.
+// Fewer (batch, KV head) units than kOnepassMfmaMinUnits still fill the
+// CUs with several waves per row: at D = 128 from 128 units for groups of 5
+// and more (the matrix-core split passes the alternative) and 256 below
+// (the VALU ones), at D = 64 from 128, at D = 256 from 192.  µs, packed,
+// register pass / split passes: D = 128 16/2 B=128 S=1024 (256 units) 29.8
+// / 47.9, 64/8 B=32 S=1024 28.6 / 47.1, B=48 S=2048 79.3 / 99.7, 32/8 B=32
+// S=4096 93.1 / 104.5, 16/4 B=64 S=512 16.9 / 26.7; 64/8 B=16 S=4096 (128
+// units) 66.0 / 72.1, S=1024 24.7 / 33.7; fewer lose, 64/8 B=8 S=4096 (64
+// units) 60.9 / 47.4, and so do groups of 4 at 128, 32/8 B=16 S=4096 66.0 /
+// 61.0.  D = 64: 64/8 B=32 S=2048 31.1 / 54.6, B=16 27.4 / 35.5, 16/4 B=32
+// S=2048 26.6 / 32.4.  D = 256: 64/8 B=32 S=1024 49.9 / 61.6, 32/4 B=48
+// S=1536 60.5 / 69.2, but 64/8 B=16 S=2048 (128 units) 68.0 / 63.4.
 constexpr int64_t kOnepassRegMinUnitsWide = 128;
 constexpr int64_t kOnepassRegMinUnitsSmall = 256;
+constexpr int64_t kOnepassRegMinUnits256 = 192;
 // Waves of the one-wave VALU single pass below which groups of at most 4
 // take the register single pass first (launch_split_dg).
 constexpr int64_t kOnepassRegBeforeWaves = 1024;
@@ -498,8 +502,9 @@ int onepass_reg_tiles(const SplitArgs& a) {
   } else {
     const int g = a.num_heads_q / a.num_heads_kv;
     const int64_t units = (int64_t)a.batch * a.num_heads_kv;
-    const int64_t min_units = D == 128 ? (g >= 5 ? kOnepassRegMinUnitsWide : kOnepassRegMinUnitsSmall)
-                                       : kOnepassMfmaMinUnits;
+    const int64_t min_units = D == 128  ? (g >= 5 ? kOnepassRegMinUnitsWide : kOnepassRegMinUnitsSmall)
+                              : D == 64 ? kOnepassRegMinUnitsWide
+                                        : kOnepassRegMinUnits256;
     if (g > 16 || units < min_units || units > INT32_MAX) return 0;
     int tpw = a.nblk <= 32 ? 8 : a.nblk <= 128 ? 16 : 32;
     if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG")) {

@@ -230,8 +230,8 @@ def test_onepass_matrix_core_off(monkeypatch):
 
 
 # (B, Hq, Hkv, D, max_len, waves, tiles, force): the matrix-core single pass
-# with the scores in registers (at least 512 (batch, KV head) units, at D =
-# 128 128 for groups of 5 and more and 256 below, and 4 blocks,
+# with the scores in registers (at least 128-256 (batch, KV head) units by
+# head dim and group, and 4 blocks,
 # ceil(blocks / tiles) <= 8 waves per row), groups of 8-16 through
 # the matrix-core launcher and of 2 and 4 through the VALU one where the
 # one-wave single pass does not hold the row: 8 tiles per wave up to 32
@@ -258,6 +258,8 @@ REG_ONEPASS_CASES = [
     (128, 16, 2, 128, 1024, 4, 16, None),   # 256 units, G = 8
     (16, 64, 8, 128, 1024, 4, 16, None),    # 128 units, G = 8
     (64, 16, 4, 128, 512, 4, 8, None),      # 256 units, G = 4
+    (16, 64, 8, 64, 2048, 8, 16, None),     # 128 units, D = 64
+    (32, 64, 8, 256, 1024, 4, 16, None),    # 256 units, D = 256
 ]
 
 
