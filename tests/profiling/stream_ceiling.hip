@@ -170,6 +170,8 @@ bool dispatch(int B, int hq, int hkv, int S, int D, int sets, int iters, int wav
   const int g = hq / hkv;
   if (D == 128 && g == 1) return by_len<128, 1, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 2) return by_len<128, 2, WRITE>(B, hq, hkv, S, sets, iters, waves);
+  if (D == 128 && g == 3) return by_len<128, 3, WRITE>(B, hq, hkv, S, sets, iters, waves);
+  if (D == 128 && g == 4) return by_len<128, 4, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 5) return by_len<128, 5, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 8) return by_len<128, 8, WRITE>(B, hq, hkv, S, sets, iters, waves);
   if (D == 128 && g == 32) return by_len<128, 32, WRITE>(B, hq, hkv, S, sets, iters, waves);
@@ -200,7 +202,7 @@ int main(int argc, char** argv) {
   const bool ok = write ? dispatch<true>(B, hq, hkv, S, D, sets, iters, waves)
                         : dispatch<false>(B, hq, hkv, S, D, sets, iters, waves);
   if (!ok) {
-    std::fprintf(stderr, "shape not built into this aid (S in {1,4,5,16}; D=128 with G in {1,2,5,8,32}, or D=256 with G=1)\n");
+    std::fprintf(stderr, "shape not built into this aid (S in {1,4,5,16}; D=128 with G in {1,2,3,4,5,8,32}, or D=256 with G=1)\n");
     return 2;
   }
   return 0;
