@@ -13,8 +13,13 @@ the workspace (workspace_traffic_bytes, counted apart).  Run it under
 `rocprofv3 --kernel-trace --stats` for the per-kernel split
 (run_rocprof.sh's s:... workloads).
 
-    python3 tests/profiling/splitkv_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,...]
+    python3 tests/profiling/splitkv_bench.py [--iters N] [--shapes B:Hq:Hkv:S:D,... | --preset layouts]
         [--layout packed|bhsd|pagedN]
+
+--preset layouts: 85 shapes for comparing layouts, B sized for about 512 MB
+of K and V: D = 128 with Hq/Hkv 8/8, 32/8, 64/8, 128/8, 4/1, 8/1, 16/2 and
+D = 64, 256 with 8/8, 32/8, 64/8, 4/1, 8/1, each at S = 24, 48, 128, 512,
+4096.
 
 --layout bhsd stores K/V as [B, Hkv, S, D] (fmha_decode_strided on the
 transposed view); pagedN as pages of N rows handed out in a random order
@@ -38,6 +43,18 @@ from tests.common import gpu_warmup  # noqa: E402
 SHAPES = [(64, 32, 8, 4096, 128), (8, 32, 8, 32768, 128), (256, 64, 8, 1024, 128), (1, 32, 8, 131072, 128),
           (2048, 32, 8, 128, 128), (4096, 32, 8, 64, 128), (16384, 32, 8, 24, 128), (8192, 16, 16, 64, 128),
           (512, 32, 8, 128, 128), (256, 32, 8, 256, 128), (128, 32, 8, 256, 128), (30720, 16, 16, 16, 128)]
+
+
+def layout_shapes():
+    """The shapes of --preset layouts."""
+    heads = [(128, h) for h in ((8, 8), (32, 8), (64, 8), (128, 8), (4, 1), (8, 1), (16, 2))]
+    heads += [(d, h) for d in (64, 256) for h in ((8, 8), (32, 8), (64, 8), (4, 1), (8, 1))]
+    shapes = []
+    for D, (hq, hkv) in heads:
+        for S in (24, 48, 128, 512, 4096):
+            B = max(1, round(512e6 / (S * hkv * D * 4)))
+            shapes.append((B, hq, hkv, S, D))
+    return shapes
 
 
 def workspace_traffic(plan, B, hq, hkv, D):
@@ -66,12 +83,16 @@ def main():
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--shapes", default="")
+    ap.add_argument("--preset", choices=["layouts"], default=None)
     ap.add_argument("--layout", default="packed")
     a = ap.parse_args()
     import torch
     import fmha_amd
 
-    shapes = [tuple(int(x) for x in s.split(":")) for s in a.shapes.split(",")] if a.shapes else SHAPES
+    if a.preset == "layouts":
+        shapes = layout_shapes()
+    else:
+        shapes = [tuple(int(x) for x in s.split(":")) for s in a.shapes.split(",")] if a.shapes else SHAPES
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
     for B, hq, hkv, S, D in shapes:
