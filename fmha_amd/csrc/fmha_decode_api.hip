@@ -306,21 +306,13 @@ bool gqa_kernel_forced(const char* kind) {
   return e && std::strcmp(e, kind) == 0;
 }
 
-// One-row-page caches with fewer KV heads than a wave holds (per-lane page
-// lookups) and rows of at most 48 (max_rows) also put launch groups of 4 on
-// the matrix cores at D >= 128, where the VALU single pass with several
-// batches per wave, each lane looking up its own row, ran slower (µs, one-row
-// pages, Hq/Hkv 4/1: B=21845 S=48 D=128 205 against 145, B=43690 S=24 235 /
-// 224, D=256 B=21845 S=24 231 / 158; at D=64 the matrix cores lose, B=87381
-// S=24 250 / 413, and so does G=1, 197 / 217).
 bool split_on_matrix_cores(int g_launch, int kv_groups, int layout, int hkv, int d, int max_rows) {
   if (gqa_kernel_forced("valu")) return false;
   if (gqa_kernel_forced("mfma")) return true;
   if (kv_groups > 1) return true;
   const int hpw = kWaveSize / (d / 8);
   const bool lanes = 2 * hkv <= hpw && hpw % (2 * hkv) == 0;
-  if (g_launch < 8)
-    return g_launch >= 4 && layout == fmha_decode::kLayoutPaged && lanes && d >= 128 && max_rows <= 48;
+  if (g_launch < 8) return false;
   if (layout != fmha_decode::kLayoutPaged) return true;
   return lanes;
 }
@@ -957,11 +949,8 @@ int split_launch(void* stream, int layout, const SplitArgs& a, int32_t head_dim)
     // 343 vs 165, B=4096 S=96 216 vs 201, MQA-like 8/1 D=64 B=16384 S=64
     // 87 vs 67, D=256 B=8192 S=64 135 vs 119).  Longer rows favour the
     // split: D=128 S=160 224 vs 237, D=256 S=256 222 vs 252, 8/1 S=48 124
-    // vs 148.
-    // (One-row pages with per-lane lookups at D >= 128: the split, 8/1
-    // B=43690 S=24 278 against 230 µs.)
-    if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma") &&
-        !(layout == fmha_decode::kLayoutPaged && lanes && head_dim >= 128)) {
+    // vs 148.  One-row pages with per-lane lookups: launch_split_dg's rule.
+    if (g == 8 && a.kv_groups == 1 && !gqa_kernel_forced("mfma")) {
       err = valu(true);
       if (err != kOnepassNotTaken) {
         if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));

@@ -585,24 +585,32 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     while ((a.num_heads_kv << (shift + 1)) <= HPW && HPW % (a.num_heads_kv << (shift + 1)) == 0) ++shift;
   // The single pass spans 2^shift batches with one descriptor: for the
   // strided layout only when their span stays below 1 GiB.  On paged caches
-  // (LANES) its lane groups look up their own batches' pages.  With up to 4
-  // query heads per KV head and D <= 128 that pays for rows of up to eight
-  // 16-row blocks,
-  // where the split passes, with one or two chunks per row, leave most lane
-  // groups idle (µs, Hq/Hkv, split against single pass: 16-row pages
-  // B=16384 S=48 4/1 D=64 191 / 49, D=128 202 / 91, 1/1 195 / 88; B=8192
-  // S=96 4/1 D=64 145 / 56, 1/1 151 / 69; B=6144 S=128 4/1 D=128 155 / 78;
-  // one-row pages B=16384 S=48 4/1 D=64 147 / 79, B=8192 S=96 1/1 149 / 87).
-  // Groups of 8 and D = 256 keep it to one or two blocks (B=6144 S=128 8/1
-  // D=128: 16-row pages 101 split / 113, one-row pages 102 / 176; B=21845
-  // S=48 D=128 145 / 154), except groups of 8 at D = 64 on 16-row pages, up
-  // to four blocks (B=43690 S=48 8/1 215 / 180, B=32768 S=64 184 / 169); longer
-  // rows take the split passes at D = 64 and 128 and the one-batch single
-  // pass at D = 256 (B=4096 S=64 4/1: 57 against 66 per-lane).
-  const bool lanes_onepass =
-      LANES && a.nblk <= (G <= 4 && D < 256                                          ? 8
-                          : LAYOUT == fmha_decode::kLayoutPagedBlockLanes && D == 64 ? 4
-                                                                                     : 2);
+  // (LANES) its lane groups look up their own batches' pages.
+  // 16-row pages and larger: with up to 4 query heads per KV head and D <=
+  // 128 that pays for rows of up to eight 16-row blocks, where the split
+  // passes, with one or two chunks per row, leave most lane groups idle (µs,
+  // Hq/Hkv, split against single pass: B=16384 S=48 4/1 D=64 191 / 49, D=128
+  // 202 / 91, 1/1 195 / 88; B=8192 S=96 4/1 D=64 145 / 56, 1/1 151 / 69;
+  // B=6144 S=128 4/1 D=128 155 / 78).  Groups of 8 and D = 256 keep it to
+  // one or two blocks (B=6144 S=128 8/1 D=128 101 split / 113), except
+  // groups of 8 at D = 64, up to four blocks (B=43690 S=48 8/1 215 / 180,
+  // B=32768 S=64 184 / 169); longer rows take the split passes at D = 64
+  // and 128 and the one-batch single pass at D = 256.
+  // Pages under 16 rows (a lookup per row, made two sub-blocks ahead): rows
+  // of up to eight blocks, four for groups of 8 at D <= 128 and six for
+  // groups of 4 at D = 64, beyond which the register single pass is faster
+  // (one-row pages, µs, single pass against the matrix-core passes,
+  // B sized for 512 MB of K and V: 4/1 D=64 S=24 117 / 446, S=96 111 / 140,
+  // S=128 140 / 119; D=128 S=24 110 / 237, S=128 87 / 93; D=256 S=24 110 /
+  // 160, S=128 86 / 111; 8/1 D=64 S=24 136 / 453, S=64 150 / 183, S=96 201
+  // / 141; D=128 S=24 134 / 242, S=64 118 / 134, S=96 129 / 108; D=256
+  // S=24 132 / 188, S=128 107 / 119).
+  const int lanes_blocks = LAYOUT == fmha_decode::kLayoutPagedLanes
+                               ? (G == 8 && D <= 128 ? 4 : G == 4 && D == 64 ? 6 : 8)
+                           : G <= 4 && D < 256 ? 8
+                           : D == 64           ? 4
+                                               : 2;
+  const bool lanes_onepass = LANES && a.nblk <= lanes_blocks;
   if (!LANES || D == 256 || lanes_onepass) {
     SplitArgs ao = a;
     ao.sub_shift = LANES && !lanes_onepass ? 0 : shift;

@@ -8,7 +8,9 @@
 // the short kernel, in three phases:
 //
 //   1. K: 16-row sub-blocks with two register sets (two sub-blocks in flight,
-//      a set refilled as soon as it is scored); dot products and the
+//      a set refilled as soon as it is scored; 8-row ones, with each row's
+//      block-table entry requested two sub-blocks ahead, when every lane
+//      looks up its own rows' pages under 16 rows); dot products and the
 //      transposing butterfly of the short kernel; scaled scores -> LDS.  The
 //      first two V sub-blocks are requested at the end of this phase.
 //   2. softmax in the wave: per (KV head, query head) the max and the sum of
@@ -88,9 +90,16 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
   constexpr int HPW = P::HPW;
-  constexpr int NRV = P::NRV;
+  // Per-lane page lookups (several batches per wave on a paged cache).
+  constexpr bool LANES = LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes;
+  // One lookup and one 64-bit address per row (pages under 16 rows): 8-row
+  // sub-blocks for K and for V (4-row ones for V with eight query heads per
+  // KV head), which leave room for two waves per SIMD (16-row ones took 416
+  // registers at G = 4, 8-row V sub-blocks 300 at G = 8).
+  constexpr bool ROW_PAGES = LAYOUT == kLayoutPagedLanes;
+  constexpr int NRV = ROW_PAGES ? (G >= 8 ? 4 : 8) : P::NRV;
   constexpr int NS = ilog2(LPH);
-  constexpr int NR = kSplitBlockRows;
+  constexpr int NR = ROW_PAGES ? 8 : kSplitBlockRows;
   constexpr int GH = G > 4 ? 4 : G;  // query heads scored per pass (partial sums per lane <= 64)
   constexpr int VS = GH * NR;
   constexpr int L = NS < ilog2(VS) ? NS : ilog2(VS);
@@ -187,7 +196,6 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   uint16_t* pw = reinterpret_cast<uint16_t*>(onepass_lds + (size_t)HPW * G * sps) + (size_t)hkl * G * spw;  // [G][spw]
 
   // Rows [0, S) of each lane group's batch: later rows read 0 without access.
-  constexpr bool LANES = LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes;
   static_assert(!LANES || MULTI, "per-lane page lookups serve several batches per wave");
   SplitRows<D, LAYOUT> krows, vrows;
   if constexpr (!MULTI || LANES) {
@@ -216,6 +224,21 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   const int sk0 = lo / NR;                              // first sub-block
   const int nsub = ((span + NR - 1) / NR + 1) / 2 * 2;  // even
   auto load_k = [&](u32x4 (&kr)[NR], int s) { krows.template load<NR>(kr, s * NR); };
+  // One lookup per row: each sub-block's block-table entries are requested
+  // two sub-blocks ahead, between the row requests of the two register
+  // sets.  Vector loads complete in order, so entries requested with their
+  // own rows would make every refill wait for the rows before it (one
+  // sub-block in flight, and a table round trip each).  (16-row pages keep
+  // the plain loop: one lookup per sub-block, and the early entries'
+  // registers took the kernel to one wave per SIMD from four query heads.)
+  constexpr int NE = ROW_PAGES ? NR : 1;
+  constexpr int NEV = ROW_PAGES ? NRV : 1;
+  auto entries_k = [&](int32_t (&e)[NE], int s) {
+    if constexpr (ROW_PAGES) krows.template entries<NR>(e, s * NR);
+  };
+  auto fill_k = [&](u32x4 (&kr)[NR], int s, const int32_t (&e)[NE]) {
+    if constexpr (ROW_PAGES) krows.template load_entries<NR>(kr, s * NR, e);
+  };
   auto score = [&](const u32x4 (&kr)[NR], int s) {
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GH) {
@@ -234,25 +257,66 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
       }
     }
   };
+  const int sv0 = lo / NRV;    // this wave's first V sub-block
+  int32_t eva[NEV], evb[NEV];  // one lookup per row: the next V entries
   {
     // Two sub-blocks in flight: a register set is refilled as soon as it has
     // been scored (past the row's end the refills read 0 without access).
     // The scheduling barriers keep the compiler from interleaving a refill
     // with the scoring of the other set, which would make it wait for both.
     u32x4 ka[NR], kb[NR];
-    load_k(ka, sk0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_k(kb, sk0 + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    for (int s = sk0; s < sk0 + nsub; s += 2) {
-      score(ka, s);
+    if constexpr (ROW_PAGES) {
+      // In flight at the top of each pass: rows s, entries s + 2, rows s + 1
+      // (the last pass refills nothing: rows past every lane's end would
+      // still be read, from Q's first row).
+      int32_t ea[NE], eb[NE];
+      entries_k(ea, sk0);
+      entries_k(eb, sk0 + 1);
       __builtin_amdgcn_sched_barrier(0);
-      load_k(ka, s + 2);
+      fill_k(ka, sk0, ea);
+      __builtin_amdgcn_sched_barrier(0);
+      entries_k(ea, sk0 + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      fill_k(kb, sk0 + 1, eb);
+      __builtin_amdgcn_sched_barrier(0);
+      int s = sk0;
+      for (; s + 2 < sk0 + nsub; s += 2) {
+        score(ka, s);
+        __builtin_amdgcn_sched_barrier(0);
+        entries_k(eb, s + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        fill_k(ka, s + 2, ea);
+        __builtin_amdgcn_sched_barrier(0);
+        score(kb, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        entries_k(ea, s + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        fill_k(kb, s + 3, eb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // The first V entries, behind the last K rows.
+      vrows.template entries<NRV>(eva, sv0 * NRV);
+      vrows.template entries<NRV>(evb, (sv0 + 1) * NRV);
+      __builtin_amdgcn_sched_barrier(0);
+      score(ka, s);
       __builtin_amdgcn_sched_barrier(0);
       score(kb, s + 1);
       __builtin_amdgcn_sched_barrier(0);
-      load_k(kb, s + 3);
+    } else {
+      load_k(ka, sk0);
       __builtin_amdgcn_sched_barrier(0);
+      load_k(kb, sk0 + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      for (int s = sk0; s < sk0 + nsub; s += 2) {
+        score(ka, s);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(ka, s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        score(kb, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(kb, s + 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   // The first two V sub-blocks are requested before the softmax, which they
@@ -260,11 +324,19 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   using VBuf = u32x4[NRV];
   VBuf va, vb;
   auto load_v = [&](u32x4 (&vr)[NRV], int s) { vrows.template load<NRV>(vr, s * NRV); };
-  const int sv0 = lo / NRV;  // this wave's first V sub-block
-  load_v(va, sv0);
-  __builtin_amdgcn_sched_barrier(0);
-  load_v(vb, sv0 + 1);
-  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ROW_PAGES) {
+    vrows.template load_entries<NRV>(va, sv0 * NRV, eva);
+    __builtin_amdgcn_sched_barrier(0);
+    vrows.template entries<NRV>(eva, (sv0 + 2) * NRV);
+    __builtin_amdgcn_sched_barrier(0);
+    vrows.template load_entries<NRV>(vb, (sv0 + 1) * NRV, evb);
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    load_v(va, sv0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(vb, sv0 + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // An unmapped page among rows [0, S) (seen by the K phase, which reads
   // them all): the batch is invalid (per lane group with MULTI, whose lane
   // groups serve different batches).
@@ -334,15 +406,37 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
     }
     accumulate_pv<G, NRV>(vr, pp, acc);
   };
-  for (int s = sv0; s < sv0 + nsv; s += 2) {
+  if constexpr (ROW_PAGES) {
+    // As the K phase: rows s, entries s + 2, rows s + 1 in flight.
+    int s = sv0;
+    for (; s + 2 < sv0 + nsv; s += 2) {
+      pv(va, s);
+      __builtin_amdgcn_sched_barrier(0);
+      vrows.template entries<NRV>(evb, (s + 3) * NRV);
+      __builtin_amdgcn_sched_barrier(0);
+      vrows.template load_entries<NRV>(va, (s + 2) * NRV, eva);
+      __builtin_amdgcn_sched_barrier(0);
+      pv(vb, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      vrows.template entries<NRV>(eva, (s + 4) * NRV);
+      __builtin_amdgcn_sched_barrier(0);
+      vrows.template load_entries<NRV>(vb, (s + 3) * NRV, evb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     pv(va, s);
     __builtin_amdgcn_sched_barrier(0);
-    load_v(va, s + 2);
-    __builtin_amdgcn_sched_barrier(0);
     pv(vb, s + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    load_v(vb, s + 3);
-    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    for (int s = sv0; s < sv0 + nsv; s += 2) {
+      pv(va, s);
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(va, s + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      pv(vb, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(vb, s + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   if constexpr (NW > 1) {
     // Waves 1..NW-1 hand their sums to wave 0 (LDS after the weights),

@@ -244,8 +244,9 @@ def test_tensors_on_another_device_are_rejected_before_launch():
 # short kernel one batch per wave (16 KV heads) and several batches per wave
 # (1 and 2 KV heads); beyond 16 rows the single pass (>= 512 waves), the
 # split passes over one page per wave (page size 16) and per-lane pages
-# (few KV heads, page sizes 4 and 16), and the matrix-core split passes
-# (G = 16, 12, and groups of 4-8 on pages under 16 rows at D >= 128).
+# (few KV heads, page sizes 4 and 16), the matrix-core split passes (G =
+# 16, 12, and groups of 8 with too few waves for the single pass on pages
+# under 16 rows), and the per-lane single pass on short rows at D >= 128.
 NEG_CASES = [
     (None, 4, 128, 16, 16, 23, ("short", "paged")), (None, 1, 128, 8, 1, 37, ("short_multi", "paged")),
     (None, 16, 128, 16, 2, 37, ("short_multi", "paged")), (None, 8, 256, 4, 1, 19, ("short_multi", "paged")),
@@ -253,7 +254,7 @@ NEG_CASES = [
     (70, 4, 128, 16, 2, 9, ("split_matrix_core", "paged")), (70, 16, 128, 8, 2, 9, ("split", "paged16_lanes")),
     (70, 4, 64, 16, 1, 9, ("split_matrix_core", "paged")),
     (100, 16, 128, 24, 2, 7, ("split_matrix_core", "paged16")), (100, 4, 256, 24, 2, 7, ("split_matrix_core", "paged")),
-    (24, 4, 128, 16, 2, 1100, ("split_matrix_core", "paged")), (32, 8, 256, 4, 1, 1100, ("split_matrix_core", "paged")),
+    (24, 4, 128, 16, 2, 1100, ("onepass", "paged_lanes")), (32, 8, 256, 4, 1, 1100, ("onepass", "paged_lanes")),
     # >= 512 waves with few KV heads: the single pass with per-lane page
     # lookups, several batches per wave: groups of 8 on rows of two blocks
     # (16-row pages at D = 128, one-row pages at D = 64) and of four (16-row

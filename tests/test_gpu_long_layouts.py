@@ -422,31 +422,28 @@ def _route():
 # The route each paged single-pass case takes, by (D, Hq, Hkv, max_len):
 # (pages under 16 rows, 16-row pages and larger).  "onepass" with a *_lanes
 # layout is the single pass with per-lane page lookups (several batches per
-# wave); pages under 16 rows with groups of 4-8 at D >= 128 take the
-# matrix-core split on short rows, and rows of four blocks the matrix-core
-# register single pass (the planner's rules in
-# split_on_matrix_cores, launch_split_dg and onepass_reg_tiles,
-# fmha_decode_api.hip / fmha_decode_launch.hpp).
-_MC = ("split_matrix_core", "paged")
-_MC16 = ("split_matrix_core", "paged16")
+# wave); rows of four blocks take the matrix-core register single pass
+# where that is faster (the planner's rules in split_on_matrix_cores,
+# launch_split_dg and onepass_reg_tiles, fmha_decode_api.hip /
+# fmha_decode_launch.hpp).
 _LANES = ("onepass", "paged_lanes")
 _LANES16 = ("onepass", "paged16_lanes")
 _REG16 = ("onepass_matrix_core_regs", "paged16")
 _REG = ("onepass_matrix_core_regs", "paged")
 PAGED_FEW_ROUTES = {
-    (128, 8, 1, 17): (_MC, _LANES16), (128, 8, 1, 32): (_MC, _LANES16), (128, 8, 1, 64): (_REG, _REG16),
-    (128, 16, 2, 17): (_MC, _LANES16), (128, 16, 2, 32): (_MC, _LANES16), (128, 16, 2, 64): (_REG, _REG16),
-    (256, 4, 1, 17): (_MC, _LANES16), (256, 4, 1, 32): (_MC, _LANES16),
-    (256, 4, 1, 64): (("onepass", "paged"), ("onepass", "paged16")),
-    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_REG, _LANES16),
+    (128, 8, 1, 17): (_LANES, _LANES16), (128, 8, 1, 32): (_LANES, _LANES16), (128, 8, 1, 64): (_LANES, _REG16),
+    (128, 16, 2, 17): (_LANES, _LANES16), (128, 16, 2, 32): (_LANES, _LANES16), (128, 16, 2, 64): (_LANES, _REG16),
+    (256, 4, 1, 17): (_LANES, _LANES16), (256, 4, 1, 32): (_LANES, _LANES16),
+    (256, 4, 1, 64): (_LANES, ("onepass", "paged16")),
+    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_LANES, _LANES16),
     (128, 40, 8, 17): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 32): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 64): (("onepass", "paged"), ("onepass", "paged16")),
 }
 PAGED_LONGER_ROUTES = {
-    (128, 4, 1, 48): (_MC, _LANES16), (128, 4, 1, 128): (_LANES, _LANES16),
+    (128, 4, 1, 48): (_LANES, _LANES16), (128, 4, 1, 128): (_LANES, _LANES16),
     (64, 2, 1, 48): (_LANES, _LANES16), (64, 2, 1, 128): (_LANES, _LANES16),
-    (128, 8, 2, 48): (_MC, _LANES16), (128, 8, 2, 128): (_LANES, _LANES16),
+    (128, 8, 2, 48): (_LANES, _LANES16), (128, 8, 2, 128): (_LANES, _LANES16),
     (64, 1, 1, 48): (_LANES, _LANES16), (64, 1, 1, 128): (_LANES, _LANES16),
 }
 
