@@ -255,6 +255,9 @@ constexpr int kOnepassWavesPerCUNarrow = 4;
 // B=16384 S=24 16/16 895 / 597, S=48 1391 / 1065; 16-row pages measured
 // 2-6% slower at 12 and keep the caps above).
 constexpr int kOnepassWavesPerCUPagedRows = 12;
+// Waves per CU the LDS must hold for the 8-row sub-blocks of the one-batch
+// paged single pass on rows of more than four blocks (launch_onepass_dg).
+constexpr int kOnepassRows8MinWaves = 12;
 
 // Waves of the single pass: ceil(batch / 2^sub_shift) batch groups times
 // the KV-head groups of one.
@@ -308,9 +311,30 @@ hipError_t launch_onepass_kernel(const SplitArgs& a, size_t need, int waves, hip
 template <int D, int G, int LAYOUT, bool MULTI>
 hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   const size_t need = fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk));
-  const int waves = LAYOUT == fmha_decode::kLayoutPaged && G <= 2 ? kOnepassWavesPerCUPagedRows
-                    : !MULTI && G <= 2 && a.nblk <= 3     ? kOnepassWavesPerCUNarrow
-                                                          : kOnepassWavesPerCU;
+  int waves = LAYOUT == fmha_decode::kLayoutPaged && G <= 2 ? kOnepassWavesPerCUPagedRows
+              : !MULTI && G <= 2 && a.nblk <= 3     ? kOnepassWavesPerCUNarrow
+                                                    : kOnepassWavesPerCU;
+  // FMHA_DECODE_ONEPASS_WAVES_PER_CU=n: n waves per CU instead (sweeps).
+  if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU"))
+    if (std::atoi(e) > 0) waves = std::atoi(e);
+  if constexpr (LAYOUT == fmha_decode::kLayoutPaged && !MULTI) {
+    // Pages under 16 rows, one batch per wave: 8-row sub-blocks and more
+    // waves per CU on rows of up to four blocks, and on longer ones where
+    // the LDS holds kOnepassRows8MinWaves waves (µs, one-row pages, 16-row
+    // sub-blocks at 8 or 12 waves / 8-row ones, B sized for 512 MB of K and
+    // V: Hq/Hkv 32/8 D=128 S=24 130 / 105, S=96 102 / 90; 64/8 S=24 156 /
+    // 120, S=48 139 / 116; 8/8 S=24 104 / 97; D=64 32/8 S=24 131 / 107,
+    // 64/8 S=48 156 / 137; D=256 64/8 S=96 118 / 98; where the LDS holds
+    // 8 waves the 16-row ones stay ahead: D=64 32/8 S=96 111 / 118, D=128
+    // 64/8 S=96 124 / 136).
+    if (a.nblk <= 4 || need * kOnepassRows8MinWaves <= (size_t)lds_per_cu()) {
+      if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = a.nblk <= 6 ? 16 : 12;
+      plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=1 blocks=%d waves_per_cu=%d rows=8)", D, G,
+                layout_name(LAYOUT), a.nblk, waves);
+      return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, false, 1, 1, true>>(a, need, waves,
+                                                                                                      stream);
+    }
+  }
   plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=%d blocks=%d waves_per_cu=%d)", D, G, layout_name(LAYOUT),
             1 << a.sub_shift, a.nblk, waves);
   // 16-row pages, eight query heads per KV head, rows of up to four blocks:

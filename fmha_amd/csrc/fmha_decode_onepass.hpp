@@ -83,10 +83,14 @@ constexpr size_t onepass_lds_bytes(int sp, int nw = 1) {
 // would, and forms the weights of its own rows); waves 1..NW-1 hand their
 // P.V sums to wave 0 through LDS, which adds them in wave order.  For rows
 // with too few (batch, KV-head group) units to fill the GPU one wave each.
-template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1, int NW = 1>
+// ROWS8: 8-row sub-blocks on pages under 16 rows with one batch per wave
+// (kLayoutPaged): half the registers of 16-row ones (123 against 208 VGPRs
+// at G = 4), for more waves per CU where the LDS leaves room for them.
+template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1, int NW = 1, bool ROWS8 = false>
 __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
     SplitArgs a) {
   static_assert(NW == 1 || !MULTI, "waves sharing a row serve one batch");
+  static_assert(!ROWS8 || (LAYOUT == kLayoutPaged && !MULTI), "8-row sub-blocks: one batch per wave, per-row pages");
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
   constexpr int HPW = P::HPW;
@@ -97,9 +101,9 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   // KV head), which leave room for two waves per SIMD (16-row ones took 416
   // registers at G = 4, 8-row V sub-blocks 300 at G = 8).
   constexpr bool ROW_PAGES = LAYOUT == kLayoutPagedLanes;
-  constexpr int NRV = ROW_PAGES ? (G >= 8 ? 4 : 8) : P::NRV;
+  constexpr int NRV = ROW_PAGES || ROWS8 ? (G >= 8 ? 4 : 8) : P::NRV;
   constexpr int NS = ilog2(LPH);
-  constexpr int NR = ROW_PAGES ? 8 : kSplitBlockRows;
+  constexpr int NR = ROW_PAGES || ROWS8 ? 8 : kSplitBlockRows;
   constexpr int GH = G > 4 ? 4 : G;  // query heads scored per pass (partial sums per lane <= 64)
   constexpr int VS = GH * NR;
   constexpr int L = NS < ilog2(VS) ? NS : ilog2(VS);
