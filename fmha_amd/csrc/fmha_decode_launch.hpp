@@ -78,6 +78,23 @@ inline int lds_per_cu() {
   return bytes;
 }
 
+// Compute units of the current device, queried once per device.
+inline int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cacheable = dev >= 0 && dev < kMaxDevices;
+  if (cacheable) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (cacheable) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 // Static LDS of a kernel, queried once (a property of the code object).
 template <auto KERNEL>
 size_t static_lds() {
@@ -314,6 +331,18 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   int waves = LAYOUT == fmha_decode::kLayoutPaged && G <= 2 ? kOnepassWavesPerCUPagedRows
               : !MULTI && G <= 2 && a.nblk <= 3     ? kOnepassWavesPerCUNarrow
                                                     : kOnepassWavesPerCU;
+  if constexpr (LAYOUT == fmha_decode::kLayoutPagedBlockLanes) {
+    // 16-row pages with per-lane lookups (three waves per SIMD fit): 8 or
+    // 12 waves per CU, whichever leaves the last round of waves fuller --
+    // each wave is one pass of about equal length, so a launch runs in
+    // rounds (µs, 8 / 12 waves per CU: 4/1 D=128 S=96, 2605 waves, 113 /
+    // 87; S=64, 3907 waves, 95 / 99; S=24, 10417 waves, 112 / 108; 8/1
+    // D=256 S=96 150 / 107; 2/1 D=64 S=64 87 / 90).  Ties take 12.
+    const int64_t w = onepass_waves(a);
+    const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    auto slots = [&](int64_t c) { return (w + c * cus - 1) / (c * cus) * c; };
+    waves = slots(12) <= slots(8) ? 12 : 8;
+  }
   // FMHA_DECODE_ONEPASS_WAVES_PER_CU=n: n waves per CU instead (sweeps).
   if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU"))
     if (std::atoi(e) > 0) waves = std::atoi(e);
@@ -610,30 +639,25 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
   // The single pass spans 2^shift batches with one descriptor: for the
   // strided layout only when their span stays below 1 GiB.  On paged caches
   // (LANES) its lane groups look up their own batches' pages.
-  // 16-row pages and larger: with up to 4 query heads per KV head and D <=
-  // 128 that pays for rows of up to eight 16-row blocks, where the split
-  // passes, with one or two chunks per row, leave most lane groups idle (µs,
-  // Hq/Hkv, split against single pass: B=16384 S=48 4/1 D=64 191 / 49, D=128
-  // 202 / 91, 1/1 195 / 88; B=8192 S=96 4/1 D=64 145 / 56, 1/1 151 / 69;
-  // B=6144 S=128 4/1 D=128 155 / 78).  Groups of 8 and D = 256 keep it to
-  // one or two blocks (B=6144 S=128 8/1 D=128 101 split / 113), except
-  // groups of 8 at D = 64, up to four blocks (B=43690 S=48 8/1 215 / 180,
-  // B=32768 S=64 184 / 169); longer rows take the split passes at D = 64
-  // and 128 and the one-batch single pass at D = 256.
-  // Pages under 16 rows (a lookup per row, made two sub-blocks ahead): rows
-  // of up to eight blocks, four for groups of 8 at D <= 128 and six for
-  // groups of 4 at D = 64, beyond which the register single pass is faster
-  // (one-row pages, µs, single pass against the matrix-core passes,
-  // B sized for 512 MB of K and V: 4/1 D=64 S=24 117 / 446, S=96 111 / 140,
-  // S=128 140 / 119; D=128 S=24 110 / 237, S=128 87 / 93; D=256 S=24 110 /
-  // 160, S=128 86 / 111; 8/1 D=64 S=24 136 / 453, S=64 150 / 183, S=96 201
-  // / 141; D=128 S=24 134 / 242, S=64 118 / 134, S=96 129 / 108; D=256
-  // S=24 132 / 188, S=128 107 / 119).
-  const int lanes_blocks = LAYOUT == fmha_decode::kLayoutPagedLanes
-                               ? (G == 8 && D <= 128 ? 4 : G == 4 && D == 64 ? 6 : 8)
-                           : G <= 4 && D < 256 ? 8
-                           : D == 64           ? 4
-                                               : 2;
+  // Against the split passes, which leave most lane groups idle with one
+  // or two chunks per row, that pays for rows of a few 16-row blocks (µs,
+  // 16-row pages, split / single pass: B=16384 S=48 4/1 D=64 191 / 49, D=128
+  // 202 / 91, 1/1 195 / 88; B=8192 S=96 4/1 D=64 145 / 56).  With the
+  // lookups made two sub-blocks ahead (one per row on pages under 16 rows,
+  // one per sub-block on larger ones): rows of up to eight blocks, four for
+  // groups of 8 at D <= 128 (three on 16-row pages) and six for groups of 4
+  // at D = 64, beyond which the register single pass is faster (µs, single
+  // pass against the matrix-core passes, B sized for 512 MB of K and V;
+  // one-row pages: 4/1 D=64 S=24 117 / 446, S=96 111 / 140, S=128 140 /
+  // 119; D=128 S=24 110 / 237, S=128 87 / 93; D=256 S=24 110 / 160, S=128
+  // 86 / 111; 8/1 D=64 S=24 136 / 453, S=64 150 / 183, S=96 201 / 141;
+  // D=128 S=24 134 / 242, S=64 118 / 134, S=96 129 / 108; D=256 S=24 132 /
+  // 188, S=128 107 / 119; 16-row pages: 8/1 D=128 S=48 121 / 146, S=64
+  // 131 / 114; D=64 S=48 158 / 230, S=64 164 / 154; D=256 S=96 107 / 124;
+  // 4/1 D=256 S=128 83 / 108, where the one-batch single pass took 91).
+  const int lanes_blocks = G == 8 && D <= 128 ? (LAYOUT == fmha_decode::kLayoutPagedLanes ? 4 : 3)
+                           : G == 4 && D == 64   ? 6
+                                                 : 8;
   const bool lanes_onepass = LANES && a.nblk <= lanes_blocks;
   if (!LANES || D == 256 || lanes_onepass) {
     SplitArgs ao = a;

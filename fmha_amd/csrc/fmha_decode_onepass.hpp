@@ -8,9 +8,9 @@
 // the short kernel, in three phases:
 //
 //   1. K: 16-row sub-blocks with two register sets (two sub-blocks in flight,
-//      a set refilled as soon as it is scored; 8-row ones, with each row's
-//      block-table entry requested two sub-blocks ahead, when every lane
-//      looks up its own rows' pages under 16 rows); dot products and the
+//      a set refilled as soon as it is scored; 8-row ones, with their
+//      block-table entries requested two sub-blocks ahead, when every lane
+//      looks up its own rows' pages); dot products and the
 //      transposing butterfly of the short kernel; scaled scores -> LDS.  The
 //      first two V sub-blocks are requested at the end of this phase.
 //   2. softmax in the wave: per (KV head, query head) the max and the sum of
@@ -96,14 +96,14 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   constexpr int HPW = P::HPW;
   // Per-lane page lookups (several batches per wave on a paged cache).
   constexpr bool LANES = LAYOUT == kLayoutPagedLanes || LAYOUT == kLayoutPagedBlockLanes;
-  // One lookup and one 64-bit address per row (pages under 16 rows): 8-row
-  // sub-blocks for K and for V (4-row ones for V with eight query heads per
-  // KV head), which leave room for two waves per SIMD (16-row ones took 416
-  // registers at G = 4, 8-row V sub-blocks 300 at G = 8).
-  constexpr bool ROW_PAGES = LAYOUT == kLayoutPagedLanes;
-  constexpr int NRV = ROW_PAGES || ROWS8 ? (G >= 8 ? 4 : 8) : P::NRV;
+  // Per-lane lookups: 8-row sub-blocks for K and for V (4-row ones for V
+  // with eight query heads per KV head), which leave room for two waves per
+  // SIMD with a lookup and a 64-bit address per row on pages under 16 rows
+  // (16-row sub-blocks took 416 registers at G = 4, 8-row V sub-blocks 300
+  // at G = 8) and for three on larger pages.
+  constexpr int NRV = LANES || ROWS8 ? (G >= 8 ? 4 : 8) : P::NRV;
   constexpr int NS = ilog2(LPH);
-  constexpr int NR = ROW_PAGES || ROWS8 ? 8 : kSplitBlockRows;
+  constexpr int NR = LANES || ROWS8 ? 8 : kSplitBlockRows;
   constexpr int GH = G > 4 ? 4 : G;  // query heads scored per pass (partial sums per lane <= 64)
   constexpr int VS = GH * NR;
   constexpr int L = NS < ilog2(VS) ? NS : ilog2(VS);
@@ -228,20 +228,19 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   const int sk0 = lo / NR;                              // first sub-block
   const int nsub = ((span + NR - 1) / NR + 1) / 2 * 2;  // even
   auto load_k = [&](u32x4 (&kr)[NR], int s) { krows.template load<NR>(kr, s * NR); };
-  // One lookup per row: each sub-block's block-table entries are requested
-  // two sub-blocks ahead, between the row requests of the two register
-  // sets.  Vector loads complete in order, so entries requested with their
-  // own rows would make every refill wait for the rows before it (one
-  // sub-block in flight, and a table round trip each).  (16-row pages keep
-  // the plain loop: one lookup per sub-block, and the early entries'
-  // registers took the kernel to one wave per SIMD from four query heads.)
-  constexpr int NE = ROW_PAGES ? NR : 1;
-  constexpr int NEV = ROW_PAGES ? NRV : 1;
+  // Per-lane lookups: each sub-block's block-table entries (one per row on
+  // pages under 16 rows, else one) are requested two sub-blocks ahead,
+  // between the row requests of the two register sets.  Vector loads
+  // complete in order, so entries requested with their own rows would make
+  // every refill wait for the rows before it (one sub-block in flight, and
+  // a table round trip each).
+  constexpr int NE = LANES ? PagedLaneRows<D, LAYOUT == kLayoutPagedBlockLanes>::template kEntries<NR> : 1;
+  constexpr int NEV = LANES ? PagedLaneRows<D, LAYOUT == kLayoutPagedBlockLanes>::template kEntries<NRV> : 1;
   auto entries_k = [&](int32_t (&e)[NE], int s) {
-    if constexpr (ROW_PAGES) krows.template entries<NR>(e, s * NR);
+    if constexpr (LANES) krows.template entries<NR>(e, s * NR);
   };
   auto fill_k = [&](u32x4 (&kr)[NR], int s, const int32_t (&e)[NE]) {
-    if constexpr (ROW_PAGES) krows.template load_entries<NR>(kr, s * NR, e);
+    if constexpr (LANES) krows.template load_entries<NR>(kr, s * NR, e);
   };
   auto score = [&](const u32x4 (&kr)[NR], int s) {
 #pragma unroll
@@ -262,14 +261,14 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
     }
   };
   const int sv0 = lo / NRV;    // this wave's first V sub-block
-  int32_t eva[NEV], evb[NEV];  // one lookup per row: the next V entries
+  int32_t eva[NEV], evb[NEV];  // per-lane lookups: the next V entries
   {
     // Two sub-blocks in flight: a register set is refilled as soon as it has
     // been scored (past the row's end the refills read 0 without access).
     // The scheduling barriers keep the compiler from interleaving a refill
     // with the scoring of the other set, which would make it wait for both.
     u32x4 ka[NR], kb[NR];
-    if constexpr (ROW_PAGES) {
+    if constexpr (LANES) {
       // In flight at the top of each pass: rows s, entries s + 2, rows s + 1
       // (the last pass refills nothing: rows past every lane's end would
       // still be read, from Q's first row).
@@ -328,7 +327,7 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
   using VBuf = u32x4[NRV];
   VBuf va, vb;
   auto load_v = [&](u32x4 (&vr)[NRV], int s) { vrows.template load<NRV>(vr, s * NRV); };
-  if constexpr (ROW_PAGES) {
+  if constexpr (LANES) {
     vrows.template load_entries<NRV>(va, sv0 * NRV, eva);
     __builtin_amdgcn_sched_barrier(0);
     vrows.template entries<NRV>(eva, (sv0 + 2) * NRV);
@@ -410,7 +409,7 @@ __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per
     }
     accumulate_pv<G, NRV>(vr, pp, acc);
   };
-  if constexpr (ROW_PAGES) {
+  if constexpr (LANES) {
     // As the K phase: rows s, entries s + 2, rows s + 1 in flight.
     int s = sv0;
     for (; s + 2 < sv0 + nsv; s += 2) {

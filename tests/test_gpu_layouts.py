@@ -257,10 +257,10 @@ NEG_CASES = [
     (24, 4, 128, 16, 2, 1100, ("onepass", "paged_lanes")), (32, 8, 256, 4, 1, 1100, ("onepass", "paged_lanes")),
     # >= 512 waves with few KV heads: the single pass with per-lane page
     # lookups, several batches per wave: groups of 8 on rows of two blocks
-    # (16-row pages at D = 128, one-row pages at D = 64) and of four (16-row
+    # (16-row pages at D = 128, one-row pages at D = 64) and of three (16-row
     # pages at D = 64), groups of up to 4 on rows of three to eight blocks
     (32, 16, 128, 8, 1, 2100, ("onepass", "paged16_lanes")), (32, 1, 64, 8, 1, 4200, ("onepass", "paged_lanes")),
-    (64, 16, 64, 8, 1, 4200, ("onepass", "paged16_lanes")), (48, 16, 128, 4, 1, 2100, ("onepass", "paged16_lanes")),
+    (48, 16, 64, 8, 1, 4200, ("onepass", "paged16_lanes")), (48, 16, 128, 4, 1, 2100, ("onepass", "paged16_lanes")),
     (128, 1, 64, 2, 1, 4200, ("onepass", "paged_lanes")), (128, 4, 128, 8, 2, 1100, ("onepass", "paged_lanes")),
     # rows of 4 blocks and more with >= 512 (batch, KV head) units: the
     # matrix-core register single pass (groups of 8 and 4, pages of 16 and

@@ -434,8 +434,8 @@ PAGED_FEW_ROUTES = {
     (128, 8, 1, 17): (_LANES, _LANES16), (128, 8, 1, 32): (_LANES, _LANES16), (128, 8, 1, 64): (_LANES, _REG16),
     (128, 16, 2, 17): (_LANES, _LANES16), (128, 16, 2, 32): (_LANES, _LANES16), (128, 16, 2, 64): (_LANES, _REG16),
     (256, 4, 1, 17): (_LANES, _LANES16), (256, 4, 1, 32): (_LANES, _LANES16),
-    (256, 4, 1, 64): (_LANES, ("onepass", "paged16")),
-    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_LANES, _LANES16),
+    (256, 4, 1, 64): (_LANES, _LANES16),
+    (64, 8, 1, 17): (_LANES, _LANES16), (64, 8, 1, 32): (_LANES, _LANES16), (64, 8, 1, 64): (_LANES, _REG16),
     (128, 40, 8, 17): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 32): (("onepass", "paged"), ("onepass", "paged16")),
     (128, 40, 8, 64): (("onepass", "paged"), ("onepass", "paged16")),
