@@ -364,6 +364,25 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
                                                                                                       stream);
     }
   }
+  if constexpr ((LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided) && G >= 4) {
+    // One descriptor per wave, groups of 8, and of 4 on rows of up to two
+    // blocks: 8-row sub-blocks at 16 waves per CU (µs, packed, B sized for
+    // 512 MB of K and V, 16-row sub-blocks at 8 waves / 8-row ones: Hq/Hkv
+    // 16/2 D=128 S=24 123.5 / 110.4, S=48 117.1 / 107.1; 64/8 S=24 117.4 /
+    // 112.4; 8/1 D=64 S=24 123.0 / 117.3; 64/8 D=256 S=48 113.7 / 104.1,
+    // S=128 94.1 / 91.8; 4/1 D=64 S=24 103.6 / 97.6, D=128 100.3 / 97.1; but
+    // 32/8 D=64 S=48 98.8 / 100.1, S=128 114.5 / 116.8).
+    // FMHA_DECODE_ONEPASS_ROWS8=0 or 1 turns them off or on (sweeps).
+    bool rows8 = G == 8 || a.nblk <= 2;
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_ROWS8")) rows8 = std::atoi(e) != 0;
+    if (rows8) {
+      if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = 16;
+      plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=%d blocks=%d waves_per_cu=%d rows=8)", D, G,
+                layout_name(LAYOUT), 1 << a.sub_shift, a.nblk, waves);
+      return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI, 1, 1, true>>(a, need, waves,
+                                                                                                      stream);
+    }
+  }
   plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=%d blocks=%d waves_per_cu=%d)", D, G, layout_name(LAYOUT),
             1 << a.sub_shift, a.nblk, waves);
   // 16-row pages, eight query heads per KV head, rows of up to four blocks:

@@ -83,14 +83,16 @@ constexpr size_t onepass_lds_bytes(int sp, int nw = 1) {
 // would, and forms the weights of its own rows); waves 1..NW-1 hand their
 // P.V sums to wave 0 through LDS, which adds them in wave order.  For rows
 // with too few (batch, KV-head group) units to fill the GPU one wave each.
-// ROWS8: 8-row sub-blocks on pages under 16 rows with one batch per wave
-// (kLayoutPaged): half the registers of 16-row ones (123 against 208 VGPRs
-// at G = 4), for more waves per CU where the LDS leaves room for them.
+// ROWS8: 8-row sub-blocks, half the registers of 16-row ones (123 against
+// 208 VGPRs at G = 4 on pages under 16 rows with one batch per wave, 145
+// against 242 at G = 8 packed), for more waves per CU where the LDS leaves
+// room for them.
 template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE = 1, int NW = 1, bool ROWS8 = false>
 __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
     SplitArgs a) {
   static_assert(NW == 1 || !MULTI, "waves sharing a row serve one batch");
-  static_assert(!ROWS8 || (LAYOUT == kLayoutPaged && !MULTI), "8-row sub-blocks: one batch per wave, per-row pages");
+  static_assert(!ROWS8 || (LAYOUT == kLayoutPaged && !MULTI) || LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided,
+                "8-row sub-blocks: per-row pages one batch per wave, or one descriptor");
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
   constexpr int HPW = P::HPW;
