@@ -310,8 +310,14 @@ template <int D, int G, int LAYOUT>
 bool onepass_group_fits(const SplitArgs& a) {
   if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_WAVES"))
     if (std::atoi(e) == 1) return false;
+  // One batch per unit: with fewer KV heads than a wave's lane groups the
+  // rest would idle (µs, packed, D = 256, two-wave single pass / split
+  // passes with the lane groups on other blocks: B=488 S=1024 4/1 152.0 /
+  // 99-102, B=244 S=2048 2/1 116.3 / 96-104).
+  constexpr int HPW = kWaveSize / (D / 8);
   const int64_t units = onepass_waves(a);
-  return G <= 4 && units < kOnepassMinUnits && units >= (G <= 2 ? 192 : 384) && a.nblk >= 2 * kOnepassGroupNW &&
+  return G <= 4 && a.num_heads_kv >= HPW && units < kOnepassMinUnits && units >= (G <= 2 ? 192 : 384) &&
+         a.nblk >= 2 * kOnepassGroupNW &&
          (LAYOUT == fmha_decode::kLayoutPacked || a.nblk <= 16) &&
          fmha_decode::onepass_lds_bytes<D, G>(fmha_decode::onepass_lds_rows(a.nblk, kOnepassGroupNW),
                                               kOnepassGroupNW) <= kOnepassMaxLdsPerGroup;
