@@ -354,16 +354,20 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
     if (std::atoi(e) > 0) waves = std::atoi(e);
   if constexpr (LAYOUT == fmha_decode::kLayoutPaged && !MULTI) {
     // Pages under 16 rows, one batch per wave: 8-row sub-blocks and more
-    // waves per CU on rows of up to four blocks, and on longer ones where
-    // the LDS holds kOnepassRows8MinWaves waves (µs, one-row pages, 16-row
-    // sub-blocks at 8 or 12 waves / 8-row ones, B sized for 512 MB of K and
-    // V: Hq/Hkv 32/8 D=128 S=24 130 / 105, S=96 102 / 90; 64/8 S=24 156 /
-    // 120, S=48 139 / 116; 8/8 S=24 104 / 97; D=64 32/8 S=24 131 / 107,
-    // 64/8 S=48 156 / 137; D=256 64/8 S=96 118 / 98; where the LDS holds
-    // 8 waves the 16-row ones stay ahead: D=64 32/8 S=96 111 / 118, D=128
-    // 64/8 S=96 124 / 136).
-    if (a.nblk <= 4 || need * kOnepassRows8MinWaves <= (size_t)lds_per_cu()) {
-      if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = a.nblk <= 6 ? 16 : 12;
+    // waves per CU on rows of up to four blocks, and on rows of five or six
+    // where the LDS holds kOnepassRows8MinWaves waves (µs, one-row pages,
+    // 16-row sub-blocks at 8 or 12 waves / 8-row ones, B sized for 512 MB
+    // of K and V unless given: Hq/Hkv 32/8 D=128 S=24 130 / 105, S=96 102 /
+    // 90, B=2048 S=96 145 / 140; 64/8 S=24 156 / 120, S=48 139 / 116; 8/8
+    // S=24 104 / 97; D=64 32/8 S=24 131 / 107, 64/8 S=48 156 / 137; D=256
+    // 64/8 S=96 118 / 98; where the LDS holds 8 waves the 16-row ones stay
+    // ahead: D=64 32/8 S=96 111 / 118, D=128 64/8 S=96 124 / 136; and on
+    // rows of eight blocks with more waves than one round at 8 per CU:
+    // B=2048 S=128 32/8 185 / 201, B=4096 366 / 388).
+    bool rows8 = a.nblk <= 4 || (a.nblk <= 6 && need * kOnepassRows8MinWaves <= (size_t)lds_per_cu());
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_ROWS8")) rows8 = std::atoi(e) != 0;
+    if (rows8) {
+      if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = 16;
       plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=1 blocks=%d waves_per_cu=%d rows=8)", D, G,
                 layout_name(LAYOUT), a.nblk, waves);
       return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, false, 1, 1, true>>(a, need, waves,
@@ -371,15 +375,17 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
     }
   }
   if constexpr ((LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided) && G >= 4) {
-    // One descriptor per wave, groups of 8, and of 4 on rows of up to two
-    // blocks: 8-row sub-blocks at 16 waves per CU (µs, packed, B sized for
-    // 512 MB of K and V, 16-row sub-blocks at 8 waves / 8-row ones: Hq/Hkv
-    // 16/2 D=128 S=24 123.5 / 110.4, S=48 117.1 / 107.1; 64/8 S=24 117.4 /
-    // 112.4; 8/1 D=64 S=24 123.0 / 117.3; 64/8 D=256 S=48 113.7 / 104.1,
-    // S=128 94.1 / 91.8; 4/1 D=64 S=24 103.6 / 97.6, D=128 100.3 / 97.1; but
-    // 32/8 D=64 S=48 98.8 / 100.1, S=128 114.5 / 116.8).
+    // One descriptor per wave, groups of 8 on rows of up to four blocks
+    // (any at D = 256), groups of 4 on rows of up to two: 8-row sub-blocks
+    // at 16 waves per CU (µs, packed, B sized for 512 MB of K and V unless
+    // given, 16-row sub-blocks at 8 waves / 8-row ones: Hq/Hkv 16/2 D=128
+    // S=24 123.5 / 110.4, S=48 117.1 / 107.1; 64/8 S=24 117.4 / 112.4; 8/1
+    // D=64 S=24 123.0 / 117.3; 64/8 D=256 S=48 113.7 / 104.1, S=128 94.1 /
+    // 91.8, B=2048 S=128 380.2 / 371.8; 4/1 D=64 S=24 103.6 / 97.6, D=128
+    // 100.3 / 97.1; but 32/8 D=64 S=48 98.8 / 100.1, S=128 114.5 / 116.8;
+    // 64/8 D=128 B=4096 S=96 298.5 / 320.1).
     // FMHA_DECODE_ONEPASS_ROWS8=0 or 1 turns them off or on (sweeps).
-    bool rows8 = G == 8 || a.nblk <= 2;
+    bool rows8 = G == 8 ? (D == 256 || a.nblk <= 4) : a.nblk <= 2;
     if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_ROWS8")) rows8 = std::atoi(e) != 0;
     if (rows8) {
       if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = 16;
