@@ -686,11 +686,24 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
   // 188, S=128 107 / 119; 16-row pages: 8/1 D=128 S=48 121 / 146, S=64
   // 131 / 114; D=64 S=48 158 / 230, S=64 164 / 154; D=256 S=96 107 / 124;
   // 4/1 D=256 S=128 83 / 108, where the one-batch single pass took 91).
-  const int lanes_blocks = G == 8 && D <= 128 ? (LAYOUT == fmha_decode::kLayoutPagedLanes ? 4 : 3)
-                           : G == 4 && D == 64   ? 6
-                                                 : 8;
+  // Pages under 16 rows at D >= 128 with up to 4 query heads per KV head:
+  // longer rows too, ten blocks at D = 128 and any the single pass holds at
+  // D = 256 (the per-lane split passes beyond it), where the other choices
+  // are the register single pass and the one-batch single pass, half of
+  // whose lane groups idle (µs, one-row pages, other / per-lane: D=128
+  // B=8192 S=160 1/1 152 / 105, 4/1 155 / 112, but S=256 184 / 248; D=256
+  // B=4096 S=384 4/1 329 / 257, 1/1 312 / 244; B=977 S=512 4/1 162 / 117
+  // on the split passes).  16-row pages keep the one-batch single pass at
+  // D = 256 (B=6144 S=256 4/1 266 / 330).
+  // FMHA_DECODE_LANES_BLOCKS=n: n blocks instead (sweeps).
+  int lanes_blocks = LAYOUT == fmha_decode::kLayoutPagedLanes
+                         ? (G == 8 ? (D <= 128 ? 4 : 8) : D == 64 ? (G == 4 ? 6 : 8) : D == 128 ? 10 : 1 << 20)
+                     : G == 8 && D <= 128 ? 3
+                     : G == 4 && D == 64  ? 6
+                                          : 8;
+  if (const char* e = std::getenv("FMHA_DECODE_LANES_BLOCKS")) lanes_blocks = std::atoi(e);
   const bool lanes_onepass = LANES && a.nblk <= lanes_blocks;
-  if (!LANES || D == 256 || lanes_onepass) {
+  if (!LANES || (D == 256 && LAYOUT != fmha_decode::kLayoutPagedLanes) || lanes_onepass) {
     SplitArgs ao = a;
     ao.sub_shift = LANES && !lanes_onepass ? 0 : shift;
     if (LAYOUT == fmha_decode::kLayoutStrided && shift > 0) {
