@@ -471,7 +471,12 @@ constexpr int kOnepassMfmaMinBlocks = 8;
 // not apply.
 template <int D, int LAYOUT>
 int onepass_mfma_waves(const SplitArgs& a) {
-  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided) {
+  // Pages of 16 rows or more too (µs, D = 256, G = 8, the split passes /
+  // this pass: B=122 S=512 64/8 111.5 / 105.0, B=977 S=512 8/1 112.4 /
+  // 104.7); pages under 16 rows, a lookup per row, keep the split passes
+  // (B=160 S=640 64/8 200.5 / 314.5, B=977 S=512 8/1 116.5 / 124.9).
+  if constexpr (LAYOUT != fmha_decode::kLayoutPacked && LAYOUT != fmha_decode::kLayoutStrided &&
+                LAYOUT != fmha_decode::kLayoutPagedBlock) {
     return 0;
   } else {
     const int g = a.num_heads_q / a.num_heads_kv;
@@ -863,7 +868,8 @@ hipError_t launch_split_group_d(const SplitArgs& a, hipStream_t stream) {
   if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
                 LAYOUT == fmha_decode::kLayoutPagedBlock || LAYOUT == fmha_decode::kLayoutPaged)
     if (const int tpw = onepass_reg_tiles<D, LAYOUT>(a)) return launch_onepass_reg<D, LAYOUT>(a, tpw, stream);
-  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided)
+  if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided ||
+                LAYOUT == fmha_decode::kLayoutPagedBlock)
     if (const int nw = onepass_mfma_waves<D, LAYOUT>(a)) return launch_onepass_mfma<D, LAYOUT>(a, nw, stream);
   constexpr int HPW = kWaveSize / (D / 8);
   constexpr int TW = D == 256 ? 1 : 2;

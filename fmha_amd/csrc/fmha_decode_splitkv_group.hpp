@@ -408,7 +408,12 @@ constexpr size_t onepass_mfma_lds_bytes(int g, int nblk, int nw) {
 // wave order and writes fp16 O.  Packed and strided layouts.
 template <int D, int NW, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided || LAYOUT == kLayoutPagedBlock,
+                "packed, strided or pages of at least 16 rows");
+  // Paged caches: every lane addresses its own rows (GroupRows), a row in
+  // an unmapped page (a negative entry) is read as Q's first row and sets
+  // the lane's flag; the (batch, KV head)'s outputs are then NaN.
+  constexpr bool PAGED = is_paged_layout(LAYOUT);
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -516,7 +521,13 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
   vrows.init(a, a.v, b, split_row_base<LAYOUT>(a, b), 0, S, (int)hk, true, r, s * NR);
   u32x4 vr[NR];
   vrows.template load<NR>(vr, lo);
-  __syncthreads();
+  // Paged: K met an unmapped page among the rows of some wave (V reads the
+  // same rows through the same table).
+  int poisoned = 0;
+  if constexpr (PAGED)
+    poisoned = __syncthreads_or(kv.bad != 0);
+  else
+    __syncthreads();
   float gm = -__builtin_inff();
 #pragma unroll
   for (int w = 0; w < NW; ++w) gm = fmaxf(gm, pst[(w * 16 + n) * 2]);
@@ -603,7 +614,7 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
     const int g = 4 * q + e;
     float v[DPC];
 #pragma unroll
-    for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[dt][e];
+    for (int dt = 0; dt < DPC; ++dt) v[dt] = poisoned ? __builtin_nanf("") : acc[dt][e];
     store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
   }
 }

@@ -269,6 +269,9 @@ NEG_CASES = [
     (300, 32, 128, 32, 8, 128, ("onepass_matrix_core_regs", "paged16")),
     (600, 1, 128, 64, 8, 128, ("onepass_matrix_core_regs", "paged")),
     (300, 4, 128, 32, 8, 128, ("onepass_matrix_core_regs", "paged")),
+    # D = 256, rows of at most 40 blocks: the matrix-core single pass with
+    # the scores in LDS (16-row pages)
+    (300, 16, 256, 64, 8, 80, ("onepass_matrix_core", "paged16")),
 ]
 
 

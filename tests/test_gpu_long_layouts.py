@@ -448,6 +448,29 @@ PAGED_LONGER_ROUTES = {
 }
 
 
+@pytest.mark.parametrize("page_size", [16, 32, 64])
+@pytest.mark.parametrize("Hq,Hkv,B,cap", [(64, 8, 80, 400), (32, 4, 130, 300)])
+def test_paged_onepass_matrix_core(page_size, Hq, Hkv, B, cap):
+    """Pages of 16 rows or more at D = 256, groups of 8, at least 512
+    (batch, KV head) units and rows of at most 40 blocks: the matrix-core
+    single pass with the row's scores in LDS, every lane addressing its own
+    rows; empty rows and 16-row edges."""
+    import fmha_amd
+    import torch
+    D = 256
+    rng = np.random.default_rng(page_size * 5 + Hq + B)
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[:5] = [cap, 0, 1, 16, 129]
+    q, kp, vp, cu = make_inputs(B, Hq, Hkv, D, seqlens, seed=page_size + Hq + B + 5)
+    kc, vc, bt = _paged_cache(kp, vp, seqlens, page_size, Hkv, D, rng)
+    print(f"paged matrix-core single pass: ps={page_size} {Hq}/{Hkv} B={B} cap={cap}", flush=True)
+    o = fmha_amd.fmha_decode_paged(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(bt).cuda(),
+                                   torch.from_numpy(seqlens).cuda(), max_seqlen_kv=cap)
+    torch.cuda.synchronize()
+    assert _route() == ("onepass_matrix_core", "paged16"), last_plan()
+    _check(o, q, kp, vp, seqlens, Hq, Hkv, D, cap, f"paged matrix-core single pass ps={page_size} {Hq}/{Hkv}")
+
+
 @pytest.mark.parametrize("page_size", [1, 4, 16, 32])
 @pytest.mark.parametrize("D,Hq,Hkv,B", [(128, 8, 1, 2100), (128, 16, 2, 1100), (256, 4, 1, 1100), (64, 8, 1, 4200),
                                         (128, 40, 8, 700)])
