@@ -374,6 +374,24 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
                                                                                                       stream);
     }
   }
+  if constexpr (LAYOUT == fmha_decode::kLayoutPagedBlock && !MULTI && G >= 4) {
+    // Pages of 16 rows or more, one batch per wave: 8-row sub-blocks at 16
+    // waves per CU for groups of 8 (rows of up to three blocks at D = 64,
+    // six at D = 128, any at D = 256) and of 4 at D = 128 on rows of up to
+    // three (µs, B sized for 512 MB of K and V, 16-row sub-blocks / 8-row:
+    // 64/8 D=256 S=24 132.5 / 113.6, S=128 110.3 / 87.0; D=128 S=24 121.5 /
+    // 113.9, S=96 126.0 / 119.5, but S=128 112.9 / 142.6; D=64 S=96 142.9 /
+    // 150.7; 32/8 D=128 S=48 99.6 / 94.3).
+    bool rows8 = G == 8 ? (D == 256 || a.nblk <= (D == 128 ? 6 : 3)) : D == 128 && a.nblk <= 3;
+    if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_ROWS8")) rows8 = std::atoi(e) != 0;
+    if (rows8) {
+      if (!std::getenv("FMHA_DECODE_ONEPASS_WAVES_PER_CU")) waves = 16;
+      plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=1 blocks=%d waves_per_cu=%d rows=8)", D, G,
+                layout_name(LAYOUT), a.nblk, waves);
+      return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, false, 1, 1, true>>(a, need, waves,
+                                                                                                      stream);
+    }
+  }
   if constexpr ((LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided) && G >= 4) {
     // One descriptor per wave, groups of 8 on rows of up to four blocks
     // (any at D = 256), groups of 4 on rows of up to two: 8-row sub-blocks

@@ -91,7 +91,8 @@ template <int D, int G, int LAYOUT = kLayoutPacked, bool MULTI = false, int WPE 
 __global__ __launch_bounds__(kBlockThreads * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void onepass_decode_kernel(
     SplitArgs a) {
   static_assert(NW == 1 || !MULTI, "waves sharing a row serve one batch");
-  static_assert(!ROWS8 || (LAYOUT == kLayoutPaged && !MULTI) || LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided,
+  static_assert(!ROWS8 || ((LAYOUT == kLayoutPaged || LAYOUT == kLayoutPagedBlock) && !MULTI) ||
+                    LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided,
                 "8-row sub-blocks: per-row pages one batch per wave, or one descriptor");
   using P = OnepassShape<D, G>;
   constexpr int LPH = P::LPH;
