@@ -614,6 +614,13 @@ int onepass_reg_tiles(const SplitArgs& a) {
                                         : kOnepassRegMinUnits256;
     if (g > 16 || units < min_units || units > INT32_MAX) return 0;
     int tpw = a.nblk <= 32 ? 8 : a.nblk <= 128 ? 16 : 32;
+    // Paged caches at D = 64: 8 tiles per wave up to 64 blocks, 32 beyond
+    // (16 took the per-row-page kernel to 171 VGPRs, two waves per SIMD; µs,
+    // 8 / 16 / 32 tiles: one-row pages B=244 S=1024 32/8 113.3 / 131.6 /
+    // 130.0, B=976 S=2048 8/1 - / 138.7 / 122.9; 16-row pages B=976 S=2048
+    // 8/1 - / 114.7 / 104.7, B=128 S=2048 32/8 - / 118.8 / 109.7).
+    if (D == 64 && (LAYOUT == fmha_decode::kLayoutPaged || LAYOUT == fmha_decode::kLayoutPagedBlock))
+      tpw = a.nblk <= 64 ? 8 : 32;
     if (const char* e = std::getenv("FMHA_DECODE_ONEPASS_REG")) {
       tpw = std::atoi(e);
     } else if (D == 256) {
@@ -624,7 +631,7 @@ int onepass_reg_tiles(const SplitArgs& a) {
     }
     if (tpw != 8 && tpw != 16 && !(tpw == 32 && D <= 128)) return 0;
     const int nw = (a.nblk + tpw - 1) / tpw;
-    return nw <= kOnepassRegMaxWaves && fmha_decode::onepass_reg_lds_bytes<D>(nw) <= 160 * 1024 ? tpw : 0;
+    return nw <= kOnepassRegMaxWaves && fmha_decode::onepass_reg_lds_bytes<D>(nw, tpw, LAYOUT) <= 160 * 1024 ? tpw : 0;
   }
 }
 
@@ -632,7 +639,7 @@ template <int D, int LAYOUT>
 hipError_t launch_onepass_reg(const SplitArgs& a, int tpw, hipStream_t stream) {
   const int g = a.num_heads_q / a.num_heads_kv;
   const int nw = (a.nblk + tpw - 1) / tpw;
-  const size_t need = fmha_decode::onepass_reg_lds_bytes<D>(nw);
+  const size_t need = fmha_decode::onepass_reg_lds_bytes<D>(nw, tpw, LAYOUT);
   plan_note("onepass_matrix_core_regs(D=%d G=%d layout=%s waves_per_row=%d tiles_per_wave=%d blocks=%d)", D, g,
             layout_name(LAYOUT), nw, tpw, a.nblk);
   const dim3 grid((uint32_t)((int64_t)a.batch * a.num_heads_kv));

@@ -661,16 +661,28 @@ template <int D, int TPW>
 constexpr int onepass_reg_pf() {
   return D == 256 || TPW >= 32 ? 2 : 4;  // V tiles in flight per wave
 }
+// Tiles per K staging round: a wave's lane groups (HPW) at D >= 128; at
+// D = 64 with up to 16 tiles per wave (three or more waves per SIMD by
+// registers), and on pages under 16 rows, half of them, two lane groups
+// loading 8 rows each of one tile, which halves the staging (more waves
+// per CU).
+constexpr int onepass_reg_round_tiles(int d, int tpw, int layout) {
+  return d == 64 && (tpw <= 16 || layout == kLayoutPaged) ? kWaveSize / (d / 8) / 2 : kWaveSize / (d / 8);
+}
+// LDS bytes per staged row: the round's tiles' D dims, plus padding.
+constexpr int onepass_reg_stage_row(int d, int tpw, int layout) {
+  return onepass_reg_round_tiles(d, tpw, layout) * d * 2 + 16;
+}
 // LDS of a workgroup of nw waves: the (max, sum) exchange, then each wave's
-// K staging (16 rows of HPW tiles), whose space the fp32 sums of waves
-// 1..nw-1 reuse once every wave is past the exchange.
+// K staging (16 rows of a round's tiles), whose space the fp32 sums of
+// waves 1..nw-1 reuse once every wave is past the exchange.
 template <int D>
 constexpr size_t onepass_reg_stage_offset(int nw) {
   return (size_t)nw * 16 * 2 * 4;
 }
 template <int D>
-constexpr size_t onepass_reg_lds_bytes(int nw) {
-  const size_t stage = (size_t)nw * GroupShape<D>::KS * kSplitBlockRows;
+constexpr size_t onepass_reg_lds_bytes(int nw, int tpw, int layout) {
+  const size_t stage = (size_t)nw * onepass_reg_stage_row(D, tpw, layout) * kSplitBlockRows;
   const size_t red = (size_t)(nw - 1) * (D / 16) * kWaveSize * 16;
   return onepass_reg_stage_offset<D>(nw) + (stage > red ? stage : red);
 }
@@ -691,7 +703,10 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
-  static_assert(TPW % HPW == 0, "whole rounds");
+  constexpr int RT = onepass_reg_round_tiles(D, TPW, LAYOUT);  // tiles per staging round
+  constexpr int KR = NR * RT / HPW;                            // rows a lane group loads per round
+  constexpr int KSR = onepass_reg_stage_row(D, TPW, LAYOUT);   // staging bytes per row
+  static_assert(TPW % RT == 0, "whole rounds");
   extern __shared__ __attribute__((aligned(16))) char onepass_reg_lds[];
   const int lane = threadIdx.x & (kWaveSize - 1);
   const int nw = (int)(blockDim.x / kWaveSize);
@@ -735,8 +750,9 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
   }
 
   // ---- K: scores of the wave's tiles, kept in x ----
-  // A round of HPW tiles: lane group s loads tile s's 16 rows whole (16
-  // bytes per lane, chunk r), stores them to the wave's staging, and the
+  // A round of RT tiles: lane group s loads KR rows of tile s % RT (16
+  // bytes per lane, chunk r; the whole tile with RT = HPW, its rows 8 (s /
+  // RT) on with RT = HPW / 2), stores them to the wave's staging, and the
   // MFMA A operands (row n, chunks 4c + q) are read back from there; the
   // next round's rows are in flight during a round's products.  Tiles past
   // the wave's rows read 0 (without memory access; on pages under 16 rows
@@ -751,48 +767,50 @@ __global__ __launch_bounds__(kBlockThreads * NWMAX) void onepass_mfma_reg_kernel
         bf16x8_v, buffer_load16<kPolicyDefault>(q_rsrc, gok ? (uint32_t)(n * D + (4 * c + q) * 8) * 2u : kLaneOutOfRange));
   const int s = lane / LPH;
   const int r = lane % LPH;
-  char* stage = onepass_reg_lds + onepass_reg_stage_offset<D>(nw) + (size_t)wv * Sh::KS * NR;
+  const int ps = s % RT;        // this lane group's tile of a round
+  const int ph = (s / RT) * KR;  // and its first row in it
+  char* stage = onepass_reg_lds + onepass_reg_stage_offset<D>(nw) + (size_t)wv * KSR * NR;
   typename std::conditional<PAGED || PAGED_ROWS, PagedLaneRows<D, PAGED>, LongRows<D, LAYOUT>>::type kr;
-  kr.init(a, a.k, b, split_row_base<LAYOUT>(a, b), lo, lo + span, (int)hk, true, r, s * NR);
+  kr.init(a, a.k, b, split_row_base<LAYOUT>(a, b), lo, lo + span, (int)hk, true, r, ps * NR + ph);
   f32x4_v x[TPW];
   float m = -__builtin_inff();
   if (nt > 0) {
-    u32x4 kb[NR];
+    u32x4 kb[KR];
     // Pages under 16 rows: each row's block-table entry, requested a round
     // ahead of its rows (entries and rows complete in request order, so
     // the entries of round k + 2 go out after the rows of round k + 1,
     // and waiting for them waits for nothing the round does not need).
-    int32_t ek[PAGED_ROWS ? NR : 1];
+    int32_t ek[PAGED_ROWS ? KR : 1];
     if constexpr (PAGED_ROWS) {
-      kr.template entries<NR>(ek, 0);
-      kr.template load_entries<NR>(kb, 0, ek);
-      if (TPW / HPW > 1) kr.template entries<NR>(ek, HPW * NR);
+      kr.template entries<KR>(ek, 0);
+      kr.template load_entries<KR>(kb, 0, ek);
+      if (TPW / RT > 1) kr.template entries<KR>(ek, RT * NR);
     } else {
-      kr.template load<NR>(kb, 0);
+      kr.template load<KR>(kb, 0);
     }
 #pragma unroll
-    for (int k = 0; k < TPW / HPW; ++k) {
+    for (int k = 0; k < TPW / RT; ++k) {
       wave_lds_sync();  // the previous round's reads of the staging are done
 #pragma unroll
-      for (int j = 0; j < NR; ++j) *reinterpret_cast<u32x4*>(stage + j * Sh::KS + s * D * 2 + r * 16) = kb[j];
+      for (int j = 0; j < KR; ++j) *reinterpret_cast<u32x4*>(stage + (ph + j) * KSR + ps * D * 2 + r * 16) = kb[j];
       wave_lds_sync();
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (PAGED_ROWS) {
-        if (k + 1 < TPW / HPW) {
-          kr.template load_entries<NR>(kb, (k + 1) * HPW * NR, ek);
-          if (k + 2 < TPW / HPW) kr.template entries<NR>(ek, (k + 2) * HPW * NR);
+        if (k + 1 < TPW / RT) {
+          kr.template load_entries<KR>(kb, (k + 1) * RT * NR, ek);
+          if (k + 2 < TPW / RT) kr.template entries<KR>(ek, (k + 2) * RT * NR);
         }
-      } else if (k + 1 < TPW / HPW) {
-        kr.template load<NR>(kb, (k + 1) * HPW * NR);
+      } else if (k + 1 < TPW / RT) {
+        kr.template load<KR>(kb, (k + 1) * RT * NR);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int p = 0; p < HPW; ++p) {
-        const int t = k * HPW + p;
+      for (int p = 0; p < RT; ++p) {
+        const int t = k * RT + p;
         f32x4_v c4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < QLD; ++c) {
-          const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(stage + n * Sh::KS + p * D * 2 + (4 * c + q) * 16);
+          const bf16x8_v ka = *reinterpret_cast<const bf16x8_v*>(stage + n * KSR + p * D * 2 + (4 * c + q) * 16);
           c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[c], c4, 0, 0, 0);
         }
 #pragma unroll
