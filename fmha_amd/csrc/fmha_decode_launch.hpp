@@ -764,8 +764,18 @@ hipError_t launch_split_dg(const SplitArgs& a, hipStream_t stream, bool onepass_
     constexpr bool kRegRows = kRegSmallGroups<D, G> && (LAYOUT == fmha_decode::kLayoutPacked ||
                                                         LAYOUT == fmha_decode::kLayoutStrided || kPagedLayout<LAYOUT>);
     bool reg_first = false;
+    // Groups of 4 at D = 64 on rows of more than four blocks with several
+    // batches per wave on packed and strided caches: the register pass too
+    // (µs, packed, single pass / register pass: 4/1 B=15625 S=128 116.4 /
+    // 87.2, B=12500 S=160 133.8 / 97.6, B=20833 S=96 101.6 / 89.7, 8/2
+    // B=15625 S=128 188.1 / 175.0; BHSD 4/1 S=160 148.3 / 90.2; but 4/1
+    // B=31250 S=64 92.9 / 110.9).
+    constexpr bool kRegMulti64 =
+        D == 64 && G == 4 && (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided);
     if constexpr (kRegRows)
-      reg_first = !onepass_only && ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves &&
+      reg_first = !onepass_only &&
+                  ((ao.sub_shift == 0 && onepass_waves(ao) < kOnepassRegBeforeWaves) ||
+                   (kRegMulti64 && ao.sub_shift > 0 && a.nblk > 4)) &&
                   onepass_reg_tiles<D, RegLayout<LAYOUT>>(a) > 0;
     if (!reg_first && onepass_fits<D, G>(ao) && (!onepass_only || (ao.sub_shift == shift && a.nblk <= only_nblk))) {
       if constexpr (LAYOUT == fmha_decode::kLayoutPacked || LAYOUT == fmha_decode::kLayoutStrided || LANES)

@@ -260,6 +260,7 @@ REG_ONEPASS_CASES = [
     (64, 16, 4, 128, 512, 4, 8, None),      # 256 units, G = 4
     (16, 64, 8, 64, 2048, 8, 16, None),     # 128 units, D = 64
     (32, 64, 8, 256, 1024, 4, 16, None),    # 256 units, D = 256
+    (4200, 4, 1, 64, 160, 2, 8, None),      # D = 64, G = 4, one KV head (the VALU launcher's several batches per wave)
 ]
 
 
@@ -406,7 +407,7 @@ def test_sub_units(monkeypatch, D, Hq, Hkv, force_valu, max_len):
     assert _launch("split")["sub_units"] == _sub_units(Hkv, D)
 
 
-@pytest.mark.parametrize("D,Hq,Hkv,B,max_len", [(128, 8, 1, 2047, 32), (128, 4, 1, 2047, 96), (64, 8, 2, 2050, 96),
+@pytest.mark.parametrize("D,Hq,Hkv,B,max_len", [(128, 8, 1, 2047, 32), (128, 4, 1, 2047, 96), (64, 8, 2, 2050, 64),
                                                  (256, 8, 1, 1030, 32), (256, 4, 1, 1030, 96), (128, 8, 2, 1100, 96)])
 def test_onepass_batches_per_wave(D, Hq, Hkv, B, max_len):
     """Single pass with several batches per wave (fewer KV heads than a wave
