@@ -415,8 +415,9 @@ hipError_t launch_onepass_dg(const SplitArgs& a, hipStream_t stream) {
   }
   plan_note("onepass(D=%d G=%d layout=%s batches_per_wave=%d blocks=%d waves_per_cu=%d)", D, G, layout_name(LAYOUT),
             1 << a.sub_shift, a.nblk, waves);
-  // 16-row pages, eight query heads per KV head, rows of up to four blocks:
-  // the kernel scheduled for two waves per SIMD.
+  // 16-row pages, eight query heads per KV head, rows of up to four blocks
+  // that keep 16-row sub-blocks (D = 64, four blocks; or the 8-row form
+  // turned off): the kernel scheduled for two waves per SIMD.
   if constexpr (!MULTI && G == 8 && LAYOUT == fmha_decode::kLayoutPagedBlock)
     if (a.nblk <= 4)
       return launch_onepass_kernel<fmha_decode::onepass_decode_kernel<D, G, LAYOUT, MULTI, 2>>(a, need, waves, stream);
