@@ -201,7 +201,26 @@ int launch(void* stream, int layout, DecodeArgs a, int32_t batch, int32_t dq, in
   }
   int w = exact ? waves_per_cu_exact(rows16, g, a.group, device_lengths)
                : waves_per_cu_for(rows16, g, a.group, dq, device_lengths, device_lengths || multi || sb == 0);
-  if (layout == fmha_decode::kLayoutPaged && !multi && g <= 2) w = budget_waves(kPagedBudget, rows16, a.group);
+  if (layout == fmha_decode::kLayoutPaged && !multi) {
+    if (g <= 2) {
+      w = budget_waves(kPagedBudget, rows16, a.group);
+    } else {
+      // Three or more query heads per KV head: the page lookups come first
+      // here too, and the byte model's cap (5 at 16 rows) leaves the CU
+      // short of requests: at least 8 waves for groups of 3-4 at D <= 128,
+      // 6 otherwise (B=30720 D=128, µs at the model's cap / this floor:
+      // one-row pages 32/8 S=16 472.9 / 402.1, S=12 385.5 / 353.8, 24/8 S=16
+      // 443.6 / 395.2, 64/8 S=12 490.4 / 441.7, S=16 550.1 / 521.4; 16-row
+      // pages 32/8 S=16 436.5 / 404.1, 64/8 S=12 461.8 / 420.9, S=16 499.1 /
+      // 505.0; D=64 32/8 S=16 245.6 / 211.3; D=256 B=15360 32/8 S=16 407.0
+      // / 399.9 at 6, 408.9 at 8); rows of a whole 16-row page keep the
+      // model's cap above four query heads (64/8 S=16 499.1 at 5 / 517.7 at
+      // 6).
+      const bool page_rows = a.seqlen_uniform >= 4 && rows16 >= 16 * 16;  // paged: log2(page size)
+      const int floor = dq <= 128 && a.group <= 4 ? 8 : page_rows ? 0 : 6;
+      if (w < floor) w = floor;
+    }
+  }
   // Waves that serve several batches (each lane group its own length and
   // rows) want at least 8 per CU at D <= 128 (B=30720 with lengths on the
   // device, µs at the byte model's cap / 8 waves: Hq/Hkv 8/1 S=16 79.0 /
