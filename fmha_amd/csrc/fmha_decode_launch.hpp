@@ -627,7 +627,13 @@ int onepass_reg_tiles(const SplitArgs& a) {
     } else if (D == 256) {
       if (a.nblk <= kOnepassReg256LdsBlocks) return 0;
       tpw = 16;
-    } else if (a.nblk < kOnepassRegMinBlocks) {
+    } else if (a.nblk < (g > 8 && D <= 128 && LAYOUT != fmha_decode::kLayoutPaged ? 2 : kOnepassRegMinBlocks)) {
+      // Groups above 8 (a 16-column tile full or nearly so) from two blocks,
+      // against the matrix-core split passes (µs, D = 128, Hq/Hkv 128/8,
+      // split / register pass: packed B=3000 S=40 150.9 / 127.2, B=2604
+      // S=48 144.3 / 120.9, B=4096 S=32 172.0 / 159.6, B=5208 S=24 198.0 /
+      // 196.5; 16-row pages S=40 168.3 / 151.8, S=24 242.1 / 230.8; one-row
+      // pages, a lookup per row, keep the split passes: S=24 252.6 / 289.0).
       return 0;
     }
     if (tpw != 8 && tpw != 16 && !(tpw == 32 && D <= 128)) return 0;
