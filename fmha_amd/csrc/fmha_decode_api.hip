@@ -364,6 +364,14 @@ int launch_mfma(void* stream, int layout, const DecodeArgs& a, int32_t batch, in
     const int64_t row_bytes = hkv * dq * 2;
     if (row_bytes * FMHA_DECODE_MAX_SEQLEN_KV * batches >= (int64_t(1) << 30))
       return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
+  } else if (layout == fmha_decode::kLayoutPagedLanes) {
+    // 64-bit addresses per lane: no descriptor to bound.
+  } else if (layout == fmha_decode::kLayoutPaged) {
+    // One batch's rows within its first page (paged_mfma_layout).
+    const int64_t rows = a.max_rows > 0 ? a.max_rows : 1;
+    const int64_t span = ((rows - 1) * a.row_stride + (hkv - 1) * a.head_stride + dq) * 2;
+    if (span >= (int64_t(1) << 30))
+      return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED, "num_heads_kv * head_dim too large (%lld)", (long long)(hkv * dq));
   } else {
     const int64_t rows = a.max_rows > 0 ? a.max_rows : 1;
     const int64_t span = ((batches - 1) * a.batch_stride + (rows - 1) * a.row_stride + (hkv - 1) * a.head_stride + dq) * 2;
@@ -398,6 +406,8 @@ int launch_mfma(void* stream, int layout, const DecodeArgs& a, int32_t batch, in
   ga.chunks = (int32_t)tps;
   ga.waves = (uint32_t)waves;
   ga.scale = a.scale;
+  ga.block_table = a.block_table;
+  ga.bt_stride = a.bt_stride;
   // Waves per CU, from sweeps (B=30720, S=16, µs for 4/5/6/8 waves; the
   // kernel's 17 KiB of LDS and 172-215 VGPRs allow 8): the best cap follows
   // the tiles a wave computes more than its bytes.  D=128: 4 (G=3
@@ -420,6 +430,10 @@ int launch_mfma(void* stream, int layout, const DecodeArgs& a, int32_t batch, in
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t err = layout == fmha_decode::kLayoutPacked
                              ? launch_mfma_layout<fmha_decode::kLayoutPacked>(ga, dq, ns, w, s)
+                         : layout == fmha_decode::kLayoutPaged
+                             ? launch_mfma_layout<fmha_decode::kLayoutPaged>(ga, dq, ns, w, s)
+                         : layout == fmha_decode::kLayoutPagedLanes
+                             ? launch_mfma_layout<fmha_decode::kLayoutPagedLanes>(ga, dq, ns, w, s)
                              : launch_mfma_layout<fmha_decode::kLayoutStrided>(ga, dq, ns, w, s);
   if (err != hipSuccess) return reject((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return FMHA_DECODE_SUCCESS;
@@ -808,6 +822,17 @@ int32_t paged_capacity(int32_t block_table_stride, int32_t page_size, int32_t ma
   return cap < max_rows ? (int32_t)cap : max_rows;
 }
 
+// Groups above 8 on a paged cache run on the matrix-core short kernel when
+// every length the call accepts (cap) lies within a batch's first page: one
+// descriptor per wave based at that page where the wave's streams share a
+// batch (num_heads_kv a multiple of the streams a wave holds), else an
+// address per lane.  The kernel's layout, or -1 when rows may span pages.
+int paged_mfma_layout(int32_t page_size, int32_t cap, int32_t num_heads_kv, int32_t head_dim) {
+  if (cap > page_size) return -1;
+  const int hpw = kWaveSize / (head_dim / 8);
+  return num_heads_kv % hpw == 0 ? fmha_decode::kLayoutPaged : fmha_decode::kLayoutPagedLanes;
+}
+
 // The short kernel over a paged cache; lengths above max_rows (<= 16) give NaN.
 int paged_short(void* stream, const void* Q, const void* K_cache, const void* V_cache, void* O,
                 const int32_t* block_table, int32_t block_table_stride, const int32_t* seqlens_kv, int32_t page_size,
@@ -815,6 +840,22 @@ int paged_short(void* stream, const void* Q, const void* K_cache, const void* V_
                 float softmax_scale) {
   max_rows = paged_capacity(block_table_stride, page_size, max_rows);
   DecodeArgs a = base_args(Q, K_cache, V_cache, O, num_heads_q, num_heads_kv, softmax_scale);
+  if (valu_kernel_group(num_heads_q / num_heads_kv) == 0) {
+    const int layout = paged_mfma_layout(page_size, max_rows, num_heads_kv, head_dim_q);
+    if (layout < 0)
+      return reject(FMHA_DECODE_ERROR_NOT_SUPPORTED,
+                    "num_heads_q / num_heads_kv above 8 (got %d) needs lengths up to %d within one page (page_size "
+                    "%d) here",
+                    num_heads_q / num_heads_kv, max_rows, page_size);
+    a.lens = seqlens_kv;
+    a.block_table = block_table;
+    a.bt_stride = block_table_stride;
+    a.row_stride = num_heads_kv * head_dim_q;
+    a.head_stride = head_dim_q;
+    a.batch_stride = (int64_t)page_size * num_heads_kv * head_dim_q;
+    a.max_rows = max_rows;
+    return launch_mfma(stream, layout, a, batch, head_dim_q, max_rows < kVarlenRowsHint ? max_rows : kVarlenRowsHint);
+  }
   a.lens = seqlens_kv;
   a.block_table = block_table;
   a.bt_stride = block_table_stride;
@@ -1235,10 +1276,15 @@ extern "C" int fmha_decode_fwd_splitkv_paged(void* stream, const void* Q, const 
                     num_heads_q, num_heads_kv, seqlen_q, head_dim_q, head_dim_kv, softmax_scale);
   if (rc != FMHA_DECODE_SUCCESS || batch == 0) return rc;
   max_seqlen_kv = paged_capacity(block_table_stride, page_size, max_seqlen_kv);
-  // Short rows with G <= 8 take the VALU paged kernel directly; with G > 8
-  // they go through the split kernels below like longer rows (one 16-row
-  // block, one chunk).
-  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV && valu_kernel_group(num_heads_q / num_heads_kv) != 0)
+  // Short rows take the short kernels directly: the VALU paged kernel for G
+  // <= 8, the matrix-core one above where rows lie within a batch's first
+  // page (paged_mfma_layout); otherwise they go through the split kernels
+  // below like longer rows (one 16-row block, one chunk).  µs, B=7812 Hq/Hkv
+  // 128/8 S=16 D=128 on 16-row pages: split 331.0, matrix-core short kernel
+  // 147.4 (packed 149.5).
+  if (max_seqlen_kv <= FMHA_DECODE_MAX_SEQLEN_KV &&
+      (valu_kernel_group(num_heads_q / num_heads_kv) != 0 ||
+       paged_mfma_layout(page_size, max_seqlen_kv, num_heads_kv, head_dim_q) >= 0))
     return paged_short(stream, Q, K_cache, V_cache, O, block_table, block_table_stride, seqlens_kv, page_size,
                        max_seqlen_kv, batch, num_heads_q, num_heads_kv, head_dim_q, softmax_scale);
   // A sub-block's range covers at most 16 rows of one page.

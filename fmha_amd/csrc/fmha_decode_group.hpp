@@ -60,13 +60,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct GroupArgs {
   const uint16_t* q;       // [streams * G, D] bf16 bits (= [batch, Hq, D])
-  const uint16_t* k;       // bf16 bits, packed or strided (LAYOUT)
+  const uint16_t* k;       // bf16 bits, packed, strided or paged (LAYOUT)
   const uint16_t* v;
   uint16_t* o;             // [batch, Hq, D] fp16 bits
   const int32_t* lens;     // packed: [batch + 1] row offsets; strided: [batch] lengths; or null
   int32_t seqlen_uniform;  // rows per batch when lens is null
   int32_t max_rows;        // longest valid length (16; strided: the rows each batch has, capped at 16)
-  int64_t batch_stride;    // strided: elements between batches
+  int64_t batch_stride;    // strided: elements between batches; paged: between pages
   int32_t row_stride;      // elements between rows (packed: Hkv * D)
   int32_t head_stride;     // elements between KV heads (packed: D)
   int32_t num_heads_kv;
@@ -77,6 +77,8 @@ struct GroupArgs {
   int32_t chunks;          // waves per stream group: ceil(HPW * tiles_per_stream / HPW) = tiles_per_stream
   uint32_t waves;          // grid size (>= stream_groups * chunks)
   float scale;
+  const int32_t* block_table;  // paged: [batch, bt_stride] page indices
+  int32_t bt_stride;
 };
 
 template <int D>
@@ -126,10 +128,14 @@ constexpr uint32_t kPermHi = 0x07060302u;
 // [16c, 16c + 16) of stream tau / TPS, c = tau % TPS (TPS = ceil(G / 16)).
 // Columns whose query head is at or past G are padding, never stored.  The
 // rows of a wave's tiles are one contiguous range [R0, R0 + nrows) of Q.
-template <int D, int SMAX, int NS>
+// LANES: kbase and vbase are this lane's own addresses (its stream's row 0
+// plus its 16-byte chunk) and load_rows its rows to read (0 for a lane that
+// reads nothing); kv_off and records are then unused.
+template <int D, int SMAX, int NS, bool LANES>
 __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int chunk, int lane, int S,
                                            uint32_t kv_off, const uint16_t* kbase, const uint16_t* vbase,
-                                           uint32_t row_bytes, uint32_t records, uint64_t bad_mask, char* lds) {
+                                           uint32_t row_bytes, uint32_t records, uint64_t bad_mask, char* lds,
+                                           int load_rows) {
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -158,8 +164,6 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   const uint64_t qrow0 = (uint64_t)sigma0 * G + R0;
   const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(a.q + qrow0 * D, (uint32_t)nrows * D * 2u);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o + qrow0 * D, (uint32_t)nrows * D * 2u);
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
 
   // ---- issue every load: the query words straight into the B operand of
   //      the score MFMA (lane (q, n): 8 dims of column n's query row per
@@ -180,12 +184,30 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
   }
   u32x4 kr[SMAX];
   u32x4 vr[SMAX];
+  if constexpr (LANES) {
+    // Rows j < load_rows, row_stride elements apart; zeros beyond, as the
+    // descriptor form's out-of-range rows.
+    const uint32_t row_elems = (uint32_t)a.row_stride;
 #pragma unroll
-  for (int j = 0; j < SMAX; ++j)
-    kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+    for (int j = 0; j < SMAX; ++j) {
+      kr[j] = u32x4{0u, 0u, 0u, 0u};
+      if (j < load_rows) kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + j * row_elems));
+    }
 #pragma unroll
-  for (int j = 0; j < SMAX; ++j)
-    vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+    for (int j = 0; j < SMAX; ++j) {
+      vr[j] = u32x4{0u, 0u, 0u, 0u};
+      if (j < load_rows) vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + j * row_elems));
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, records);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, records);
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j)
+      kr[j] = buffer_load16<kPolicyStream>(k_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j)
+      vr[j] = buffer_load16<kPolicyStream>(v_rsrc, kv_off + (j < S ? (uint32_t)j * row_bytes : kRowOutOfRange));
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- K rows to LDS ----
@@ -343,9 +365,21 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
 // kLayoutStrided (element (b, j, h, d) at b*batch_stride + j*row_stride +
 // h*head_stride + d, lengths lens[b]); one descriptor spans the wave's
 // streams from its first batch (the host bounds that span below 1 GiB).
+// kLayoutPaged: row j of batch b in slot j of page block_table[b *
+// bt_stride] (pages batch_stride elements apart), lengths lens[b]; launched
+// only where a wave's streams share one batch (Hkv a multiple of HPW) and
+// no length the wave accepts (max_rows) reaches past that first page, so
+// the descriptor is based at the page.  A negative entry, or a wave whose
+// streams would span batches, makes the batch invalid (NaN output) and
+// nothing of it is read.  kLayoutPagedLanes: the same rows through a 64-bit
+// address per lane, for waves whose streams span batches (Hkv below HPW or
+// not a multiple of it), each lane looking up its own batch's page.
 template <int D, int SB, int NS, int LAYOUT>
 __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupArgs a) {
-  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided, "one descriptor per wave");
+  static_assert(LAYOUT == kLayoutPacked || LAYOUT == kLayoutStrided || LAYOUT == kLayoutPaged ||
+                    LAYOUT == kLayoutPagedLanes,
+                "one descriptor per wave, or one address per lane");
+  constexpr bool LANES = LAYOUT == kLayoutPagedLanes;
   using Sh = GroupShape<D>;
   constexpr int LPH = Sh::LPH;
   constexpr int HPW = Sh::HPW;
@@ -399,6 +433,20 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
     base_elem = (uint64_t)row_first * a.row_stride;
     lane_elem = rel * a.row_stride + (int64_t)h * a.head_stride;
     end = (sok && !bad && S > 0) ? (uint32_t)((rel + S) * (int64_t)row_bytes) : 0u;
+  } else if constexpr (LAYOUT == kLayoutPaged) {
+    S = a.lens[bq];
+    const int32_t entry = __builtin_amdgcn_readfirstlane(a.block_table[(int64_t)b_first * a.bt_stride]);
+    bad = sok && (S < 0 || S > a.max_rows || (S > 0 && entry < 0) || bq != b_first);
+    base_elem = entry < 0 ? 0u : (uint64_t)(uint32_t)entry * (uint64_t)a.batch_stride;
+    lane_elem = (int64_t)h * a.head_stride;
+    end = (sok && !bad && S > 0) ? (uint32_t)((lane_elem + (int64_t)(S - 1) * a.row_stride + D) * 2) : 0u;
+  } else if constexpr (LANES) {
+    S = sok ? a.lens[bq] : 0;
+    const int32_t entry = a.block_table[(int64_t)bq * a.bt_stride];
+    bad = sok && (S < 0 || S > a.max_rows || (S > 0 && entry < 0));
+    base_elem = 0;
+    lane_elem = (sok && !bad && S > 0) ? (int64_t)entry * a.batch_stride + (int64_t)h * a.head_stride : 0;
+    end = 0u;
   } else {
     S = a.lens ? a.lens[bq] : a.seqlen_uniform;
     bad = sok && (S < 0 || S > a.max_rows);
@@ -415,7 +463,8 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const int tau1 = min(tau0 + TW, ((nstreams + NS - 1) / NS) * tps) - 1;
   const bool used = s >= (tau0 / tps) * NS && s < (tau1 / tps) * NS + NS;
   const uint32_t kv_off =
-      (sok && !bad && used) ? (uint32_t)(lane_elem * 2) + (uint32_t)r * 16u : kLaneOutOfRange;
+      (sok && !bad && used && !LANES) ? (uint32_t)(lane_elem * 2) + (uint32_t)r * 16u : kLaneOutOfRange;
+  const int load_rows = (sok && !bad && used) ? S : 0;
   // Descriptor range: the end of the last row any lane reads; bucket: the
   // longest length of the wave; invalid streams as a bit per stream.
   int smax = S;
@@ -427,11 +476,11 @@ __global__ __launch_bounds__(kBlockThreads) void fmha_decode_group_kernel(GroupA
   const uint32_t records = (uint32_t)__builtin_amdgcn_readfirstlane((int)end);
   smax = __builtin_amdgcn_readfirstlane(smax);
   const uint64_t bad_mask = __ballot(bad && r == 0);
-  const uint16_t* kbase = a.k + base_elem;
-  const uint16_t* vbase = a.v + base_elem;
+  const uint16_t* kbase = LANES ? a.k + lane_elem + r * 8 : a.k + base_elem;
+  const uint16_t* vbase = LANES ? a.v + lane_elem + r * 8 : a.v + base_elem;
 
 #define FMHA_GROUP_UNIT(SM) \
-  group_unit<D, SM, NS>(a, sg, chunk, lane, S, kv_off, kbase, vbase, row_bytes, records, bad_mask, lds)
+  group_unit<D, SM, NS, LANES>(a, sg, chunk, lane, S, kv_off, kbase, vbase, row_bytes, records, bad_mask, lds, load_rows)
   if constexpr (SB != 0) {
     FMHA_GROUP_UNIT(SB);
   } else {

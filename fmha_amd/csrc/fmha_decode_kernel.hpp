@@ -79,6 +79,20 @@ constexpr uint32_t kNaNBf16x2 = 0x7fc07fc0u;
 constexpr int kLayoutPacked = 0;
 constexpr int kLayoutStrided = 1;
 constexpr int kLayoutPaged = 2;
+// Pages of at least 16 rows, for the long-row kernels: a sub-block of up to
+// 16 rows (aligned to its size) lies in one page, so it needs one block-table
+// lookup and one descriptor.  kLayoutPaged then means pages of 1-8 rows (one
+// lookup per row).  The host picks between the two, so that no pipelined loop
+// carries a branch (the compiler would wait for every request at its head).
+constexpr int kLayoutPagedBlock = 3;
+// The same two paged layouts read through per-lane addresses
+// (PagedLaneRows; in the matrix-core short kernel, a 64-bit address per
+// lane), so that the lane groups of a wave can read rows of different pages:
+// sub-units (SplitArgs::sub_shift) with fewer KV heads than a wave holds.
+constexpr int kLayoutPagedLanes = 4;
+constexpr int kLayoutPagedBlockLanes = 5;
+
+constexpr bool is_paged_layout(int layout) { return layout >= kLayoutPaged && layout <= kLayoutPagedBlockLanes; }
 
 struct DecodeArgs {
   const uint16_t* q;        // [batch, Hq, D] bf16 bits

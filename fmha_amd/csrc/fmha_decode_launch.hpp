@@ -229,10 +229,21 @@ hipError_t launch_mfma_d(const fmha_decode::GroupArgs& g, int ns, int w, hipStre
 
 template <int LAYOUT>
 hipError_t launch_mfma_layout(const fmha_decode::GroupArgs& g, int dq, int ns, int w, hipStream_t stream) {
-  switch (dq) {
-    case 64: return launch_mfma_d<64, LAYOUT>(g, ns, w, stream);
-    case 128: return launch_mfma_d<128, LAYOUT>(g, ns, w, stream);
-    default: return launch_mfma_d<256, LAYOUT>(g, ns, w, stream);
+  if constexpr (LAYOUT == fmha_decode::kLayoutPaged || LAYOUT == fmha_decode::kLayoutPagedLanes) {
+    // Paged caches reach the matrix-core kernel for groups above 8 only:
+    // one stream per 16-column tile.
+    if (ns != 1) return hipErrorInvalidValue;
+    switch (dq) {
+      case 64: return launch_mfma_one<64, 1, LAYOUT>(g, w, stream);
+      case 128: return launch_mfma_one<128, 1, LAYOUT>(g, w, stream);
+      default: return launch_mfma_one<256, 1, LAYOUT>(g, w, stream);
+    }
+  } else {
+    switch (dq) {
+      case 64: return launch_mfma_d<64, LAYOUT>(g, ns, w, stream);
+      case 128: return launch_mfma_d<128, LAYOUT>(g, ns, w, stream);
+      default: return launch_mfma_d<256, LAYOUT>(g, ns, w, stream);
+    }
   }
 }
 

@@ -135,20 +135,6 @@ __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voffset, 0, kPolicyDefault));
 }
 
-// Pages of at least 16 rows, for the long-row kernels: a sub-block of up to
-// 16 rows (aligned to its size) lies in one page, so it needs one block-table
-// lookup and one descriptor.  kLayoutPaged then means pages of 1-8 rows (one
-// lookup per row).  The host picks between the two, so that no pipelined loop
-// carries a branch (the compiler would wait for every request at its head).
-constexpr int kLayoutPagedBlock = 3;
-// The same two paged layouts read through per-lane addresses
-// (PagedLaneRows), so that the lane groups of a wave can read rows of
-// different pages: sub-units (SplitArgs::sub_shift) with fewer KV heads than
-// a wave holds.
-constexpr int kLayoutPagedLanes = 4;
-constexpr int kLayoutPagedBlockLanes = 5;
-
-constexpr bool is_paged_layout(int layout) { return layout >= kLayoutPaged && layout <= kLayoutPagedBlockLanes; }
 
 // A pointer the whole wave holds, moved to scalar registers: a buffer
 // descriptor built from a value the compiler keeps in vector registers

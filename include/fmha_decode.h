@@ -93,9 +93,10 @@ extern "C" {
  *                   fmha_decode_fwd_uniform, their _fast forms and
  *                   fmha_decode_fwd_strided take any G, and so do the
  *                   split-KV entries (through a padded query group beyond
- *                   16 rows); fmha_decode_fwd_exact, fmha_decode_fwd_paged
- *                   and fmha_decode_fwd_fp32_weights G <= 8 (else
- *                   FMHA_DECODE_ERROR_NOT_SUPPORTED).
+ *                   16 rows); fmha_decode_fwd_exact and
+ *                   fmha_decode_fwd_fp32_weights G <= 8 (else
+ *                   FMHA_DECODE_ERROR_NOT_SUPPORTED); fmha_decode_fwd_paged
+ *                   G > 8 where rows lie in a batch's first page.
  *   seqlen_q        must be 1 (decode)
  *   head_dim_q      64, 128 or 256
  *   head_dim_kv     must equal head_dim_q
@@ -247,10 +248,12 @@ int fmha_decode_fwd_strided(void* stream,
  *                       block_table_stride * page_size)]; a length outside
  *                       that range gets NaN outputs
  *   page_size           a power of two in [1, 2^20]
- * Other arguments as fmha_decode_fwd, with group sizes up to 8 only (the
- * VALU kernel; fmha_decode_fwd_splitkv_paged takes any).  The reference has
- * no paged layout; this entry point is the KV-cache format of serving
- * engines.
+ * Other arguments as fmha_decode_fwd.  Group sizes up to 8 run on the VALU
+ * kernel; above 8 on the matrix-core kernel when every length the call
+ * accepts (min(16, block_table_stride * page_size)) lies within page_size,
+ * else FMHA_DECODE_ERROR_NOT_SUPPORTED (fmha_decode_fwd_splitkv_paged takes
+ * those on its split passes).  The reference has no paged layout; this entry
+ * point is the KV-cache format of serving engines.
  */
 int fmha_decode_fwd_paged(void* stream,
                           const void* Q, const void* K_cache, const void* V_cache, void* O,
@@ -279,8 +282,8 @@ int fmha_decode_fwd_paged(void* stream,
  * share a workspace must be ordered (same stream or synchronised).
  *
  * Group sizes G = num_heads_q / num_heads_kv: any.  With max_seqlen_kv <= 16
- * as fmha_decode_fwd (the paged entry: G <= 8 as fmha_decode_fwd_paged, G > 8
- * as beyond 16).  Beyond 16, G = 3 and 5-7 run on copies of Q and O padded
+ * as fmha_decode_fwd (the paged entry: as fmha_decode_fwd_paged, and G > 8
+ * with rows that may reach a second page as beyond 16).  Beyond 16, G = 3 and 5-7 run on copies of Q and O padded
  * to 4 or 8 query heads per KV head, and G > 8 on copies padded to a
  * multiple of 8 (copies only when G is not one).  G <= 4 runs on the VALU
  * split-KV passes; G = 5-8 and G > 8 on split-KV passes on the matrix cores
@@ -364,8 +367,8 @@ int fmha_decode_fwd_splitkv_strided(void* stream,
  * fmha_decode_fwd_paged's kernel, and the workspace only holds a padded
  * query group).  Any group size, on the passes fmha_decode_fwd_splitkv
  * describes for each G and layout (3 and 5-7 on padded query groups); with
- * that bound <= 16, G > 8 also takes the split passes and needs the
- * workspace.
+ * that bound <= 16, G > 8 takes the split passes, and needs the workspace,
+ * only where the bound exceeds page_size.
  * No counterpart in the reference.
  */
 int fmha_decode_fwd_splitkv_paged(void* stream,

@@ -192,8 +192,9 @@ def test_strided_rejects(lib, kw, code, needle):
     (dict(bts=0), BAD, "block_table_stride"),
     (dict(sq=2), BAD, "seqlen_q"),
     (dict(v=None), BAD, "non-null"),
-    # no workspace: the VALU kernel only, group sizes up to 8
-    (dict(hq=192, hkv=16), NOTSUP, "at most 8"),
+    # no workspace: group sizes above 8 only where every length up to 16
+    # lies in a batch's first page
+    (dict(hq=192, hkv=16, ps=8), NOTSUP, "within one page"),
 ])
 def test_paged_rejects(lib, kw, code, needle):
     assert paged(lib, **kw) == code

@@ -206,6 +206,97 @@ def test_paged_few_kv_heads_batches_per_wave(page_size, D, Hq, Hkv):
     assert torch.equal(o2[keep].view(torch.int16), o[keep].view(torch.int16))
 
 
+@pytest.mark.parametrize("entry", ["short", "splitkv"])
+@pytest.mark.parametrize("page_size,cap", [(16, 16), (64, 16), (8, 8)])
+@pytest.mark.parametrize("D,Hq,Hkv,layout", [(128, 64, 4, "paged"), (64, 96, 8, "paged"), (256, 48, 2, "paged"),
+                                              (128, 160, 4, "paged"), (128, 32, 1, "paged_lanes"),
+                                              (128, 36, 2, "paged_lanes"), (64, 72, 6, "paged_lanes"),
+                                              (256, 27, 1, "paged_lanes")])
+def test_paged_groups_above_eight(entry, page_size, cap, D, Hq, Hkv, layout):
+    """Short rows with more than 8 query heads per KV head on a paged cache,
+    G = 16, 12, 24, 40, 32, 18, 12 and 27 (one to three 16-column query
+    tiles per stream): the matrix-core short kernel with its descriptor based
+    at each batch's page where a wave's streams share a batch, else with an
+    address per lane, through the workspace-less entry (max_seqlen_kv None)
+    and the split entry (max_seqlen_kv = cap).  NaN in every slot no batch
+    owns, -1 in unused entries, empty batches; then a length beyond the
+    capacity and an unmapped page give NaN for their batches only."""
+    import torch
+    import fmha_amd
+    if entry == "short" and cap < 16:
+        pytest.skip("the workspace-less entry accepts lengths up to 16: cap 8 needs an 8-row table bound")
+    print(f"paged groups above 8: {entry} ps={page_size} cap={cap} D={D} Hq={Hq} Hkv={Hkv}", flush=True)
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(page_size + D + Hq)
+    rng = np.random.default_rng(page_size * 3 + D + Hq + Hkv)
+    B = 45
+    seqlens = rng.integers(0, cap + 1, size=B).astype(np.int32)
+    seqlens[0], seqlens[7] = cap, 0
+    num_pages = B + 5
+    perm = rng.permutation(num_pages)
+    bt = np.full((B, 2), -1, np.int32)
+    for b in range(B):
+        if seqlens[b] > 0:
+            bt[b, 0] = perm[b]
+    kc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full((num_pages, page_size, Hkv, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    q = _bf16(gen, (B, Hq, 1, D), dev)
+    rows_k, rows_v = [], []
+    for b in range(B):
+        for j in range(seqlens[b]):
+            kr, vr = _bf16(gen, (Hkv, D), dev), _bf16(gen, (Hkv, D), dev)
+            kc[bt[b, 0], j], vc[bt[b, 0], j] = kr, vr
+            rows_k.append(_bits(kr))
+            rows_v.append(_bits(vr))
+    max_s = None if entry == "short" else cap
+
+    def run(table, lens):
+        o = fmha_amd.fmha_decode_paged(q, kc, vc, torch.from_numpy(table).to(dev), torch.from_numpy(lens).to(dev),
+                                       max_seqlen_kv=max_s)
+        torch.cuda.synchronize()
+        return o
+
+    o = run(bt, seqlens)
+    kind, fields = last_plan()[-1]
+    assert (kind, fields["layout"]) == ("short_matrix_core", layout), last_plan()
+    _check(o, q, np.stack(rows_k), np.stack(rows_v), seqlens, Hq, Hkv, D,
+           f"paged G={Hq // Hkv} {entry} ps={page_size} D={D}")
+    bad_lens, bad_bt = seqlens.copy(), bt.copy()
+    bad_lens[3] = cap + 1
+    bad_bt[0, 0] = -1
+    o2 = run(bad_bt, bad_lens)
+    assert torch.isnan(o2[[0, 3]].float()).all()
+    keep = [b for b in range(B) if b not in (0, 3)]
+    assert torch.equal(o2[keep].view(torch.int16), o[keep].view(torch.int16))
+
+
+def test_paged_groups_above_eight_rows_beyond_a_page():
+    """Groups above 8 whose rows may reach past a batch's first page: the
+    split entry runs them on the split passes (exact against the oracle);
+    the workspace-less entry rejects them."""
+    import torch
+    import fmha_amd
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    for page_size, Hq, Hkv in [(8, 32, 2), (4, 64, 4)]:
+        D, B, cap = 128, 9, 16
+        seqlens = np.array([16, 3, 0, 9, 16, 1, 12, 5, 7], np.int32)
+        pages = (cap + page_size - 1) // page_size
+        bt = np.arange(B * pages, dtype=np.int32).reshape(B, pages)
+        kc = _bf16(gen, (B * pages, page_size, Hkv, D), dev)
+        vc = _bf16(gen, (B * pages, page_size, Hkv, D), dev)
+        q = _bf16(gen, (B, Hq, 1, D), dev)
+        rows_k = [_bits(kc[bt[b, j // page_size], j % page_size]) for b in range(B) for j in range(seqlens[b])]
+        rows_v = [_bits(vc[bt[b, j // page_size], j % page_size]) for b in range(B) for j in range(seqlens[b])]
+        bt_dev, lens = torch.from_numpy(bt).to(dev), torch.from_numpy(seqlens).to(dev)
+        o = fmha_amd.fmha_decode_paged(q, kc, vc, bt_dev, lens, max_seqlen_kv=cap)
+        torch.cuda.synchronize()
+        assert last_plan()[-1][0] == "split_matrix_core", last_plan()
+        _check(o, q, np.stack(rows_k), np.stack(rows_v), seqlens, Hq, Hkv, D, f"paged G>8 split ps={page_size}")
+        with pytest.raises(RuntimeError, match="above 8"):
+            fmha_amd.fmha_decode_paged(q, kc, vc, bt_dev, lens)
+
+
 def test_tensors_on_another_device_are_rejected_before_launch():
     """out, k, v, caches, block tables and lengths must be on q's device: a
     host tensor's pointer handed to the kernel would fault, so every wrapper
@@ -246,9 +337,13 @@ def test_tensors_on_another_device_are_rejected_before_launch():
 # split passes over one page per wave (page size 16) and per-lane pages
 # (few KV heads, page sizes 4 and 16), the matrix-core split passes (G =
 # 16, 12, and groups of 8 with too few waves for the single pass on pages
-# under 16 rows), and the per-lane single pass on short rows at D >= 128.
+# under 16 rows), the per-lane single pass on short rows at D >= 128, and
+# the matrix-core short kernel for groups above 8 (G = 16 and 12, both
+# entries; G = 32 on one KV head, an address per lane).
 NEG_CASES = [
     (None, 4, 128, 16, 16, 23, ("short", "paged")), (None, 1, 128, 8, 1, 37, ("short_multi", "paged")),
+    (None, 16, 128, 64, 4, 40, ("short_matrix_core", "paged")), (16, 32, 64, 96, 8, 30, ("short_matrix_core", "paged")),
+    (None, 16, 128, 32, 1, 41, ("short_matrix_core", "paged_lanes")),
     (None, 16, 128, 16, 2, 37, ("short_multi", "paged")), (None, 8, 256, 4, 1, 19, ("short_multi", "paged")),
     (40, 16, 128, 8, 4, 600, ("onepass", "paged16")), (70, 16, 128, 16, 16, 9, ("split", "paged16")),
     (70, 4, 128, 16, 2, 9, ("split_matrix_core", "paged")), (70, 16, 128, 8, 2, 9, ("split", "paged16_lanes")),
