@@ -206,8 +206,10 @@ def test_paged_few_kv_heads_batches_per_wave(page_size, D, Hq, Hkv):
     assert torch.equal(o2[keep].view(torch.int16), o[keep].view(torch.int16))
 
 
-@pytest.mark.parametrize("entry", ["short", "splitkv"])
-@pytest.mark.parametrize("page_size,cap", [(16, 16), (64, 16), (8, 8)])
+# (entry, page size, lengths up to): the workspace-less entry accepts up to
+# 16 rows, so its pages are of 16 rows or more.
+@pytest.mark.parametrize("entry,page_size,cap", [("short", 16, 16), ("short", 64, 16), ("splitkv", 16, 16),
+                                                 ("splitkv", 64, 16), ("splitkv", 8, 8)])
 @pytest.mark.parametrize("D,Hq,Hkv,layout", [(128, 64, 4, "paged"), (64, 96, 8, "paged"), (256, 48, 2, "paged"),
                                               (128, 160, 4, "paged"), (128, 32, 1, "paged_lanes"),
                                               (128, 36, 2, "paged_lanes"), (64, 72, 6, "paged_lanes"),
@@ -223,8 +225,6 @@ def test_paged_groups_above_eight(entry, page_size, cap, D, Hq, Hkv, layout):
     capacity and an unmapped page give NaN for their batches only."""
     import torch
     import fmha_amd
-    if entry == "short" and cap < 16:
-        pytest.skip("the workspace-less entry accepts lengths up to 16: cap 8 needs an 8-row table bound")
     print(f"paged groups above 8: {entry} ps={page_size} cap={cap} D={D} Hq={Hq} Hkv={Hkv}", flush=True)
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(page_size + D + Hq)
