@@ -45,7 +45,8 @@
 //     ([stream][8-dim block][dim][16 rows], 16 bytes of padding per block),
 //     over the K rows, which are dead by then; per tile and stream P.V is
 //     D/16 MFMAs, each output row keeping its own stream's; column n covers
-//     dims [n*D/16, (n+1)*D/16) so each lane stores whole 8/16/32-byte runs.
+//     dims [n*D/16, (n+1)*D/16) (D <= 128; at D = 256 two runs of 8,
+//     out_dim) so each lane stores whole 8/16-byte runs.
 //   * 48 MFMAs per wave for G <= 16 at every D.
 #pragma once
 
@@ -118,6 +119,17 @@ __device__ __forceinline__ float column_reduce(float x) {
 // v_perm selector: low halves / high halves of two dwords (lo, hi) -> one dword.
 constexpr uint32_t kPermLo = 0x05040100u;
 constexpr uint32_t kPermHi = 0x07060302u;
+
+// Output dim of P.V column n's dt-th value (dt < DPC = D / 16): n * DPC +
+// dt up to 8 dims per column; above (D = 256), column n takes dims [128h +
+// 8n, 128h + 8n + 8) for h = dt / 8, so each store instruction of a row
+// (one per h) covers 256 contiguous bytes over the row's 16 lanes rather
+// than every other 16 bytes of 512 (half-written lines doubled the HBM
+// write bytes), and the V^T reads land on distinct banks.
+template <int DPC>
+__device__ __forceinline__ int out_dim(int n, int dt) {
+  return DPC <= 8 ? n * DPC + dt : (dt / 8) * 128 + n * 8 + dt % 8;
+}
 
 // One wave: HPW consecutive streams of stream group sg (wave-local stream
 // p = 0..HPW-1), KV bucket SMAX, query tiles [chunk*TW, chunk*TW + TW) of the
@@ -316,7 +328,7 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
       const char* vs = v_lds + min(pt + k, HPW - 1) * Sh::VSTREAM;
 #pragma unroll
       for (int dt = 0; dt < DPC; ++dt) {
-        const int dim = n * DPC + dt;
+        const int dim = out_dim<DPC>(n, dt);
         const bf16x4_v vb =
             *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (kMaxSeq * 2) + q * 8);
         const f32x4_v c4 =
@@ -336,7 +348,7 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
       const int p = pt + (4 * q + e) / CPS;
       const int g = c16 + (4 * q + e) % CPS;
       const uint32_t off =
-          (g < G && p < nstreams) ? (uint32_t)((p * G + g - R0) * D + n * DPC) * 2u : kLaneOutOfRange;
+          (g < G && p < nstreams) ? (uint32_t)((p * G + g - R0) * D + out_dim<DPC>(n, 0)) * 2u : kLaneOutOfRange;
 #pragma unroll
       for (int h8 = 0; h8 < (DPC + 7) / 8; ++h8) {
         constexpr int W = DPC < 8 ? DPC : 8;  // dims per store
@@ -345,7 +357,7 @@ __device__ __forceinline__ void group_unit(const GroupArgs& a, uint32_t sg, int 
         for (int k8 = 0; k8 < 8; ++k8) vals[k8] = k8 < W ? acc[h8 * 8 + (k8 < W ? k8 : 0)][e] : 0.0f;
         const u32x4 pk = pack_f16x8(vals);
         if constexpr (W == 8) {
-          buffer_store16(o_rsrc, off + h8 * 16, pk);
+          buffer_store16(o_rsrc, off + h8 * 256, pk);  // out_dim(n, 8 * h8) = out_dim(n, 0) + 128 * h8
         } else {
           __builtin_amdgcn_raw_buffer_store_b64(u32x2{pk[0], pk[1]}, o_rsrc, (int)off, 0, kPolicyStreamStore);
         }
