@@ -300,8 +300,10 @@ def fmha_decode_paged(q, k_cache, v_cache, block_table, seqlens_kv, softmax_scal
     max_pages * page_size give NaN.  With max_seqlen_kv given the call goes
     through fmha_decode_fwd_splitkv_paged with workspace (a uint8 device
     tensor of splitkv_workspace_size(B, Hq, Hkv, max_seqlen_kv, D) bytes,
-    allocated here when None; for max_seqlen_kv <= 16 it only holds the
-    padded query group of a group size above 8)."""
+    allocated here when None; for max_seqlen_kv <= 16 it is used only by a
+    group size above 8 whose rows may reach past a batch's first page).
+    Without max_seqlen_kv, a group size above 8 needs pages of at least
+    min(16, max_pages * page_size) rows (FmhaDecodeError otherwise)."""
     import torch
     B, Hq, D = _q_shape(q)
     out = _check_q_out(q, out)
