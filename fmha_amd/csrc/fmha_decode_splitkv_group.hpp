@@ -196,6 +196,21 @@ __device__ __forceinline__ void store_f16_run(__amdgpu_buffer_rsrc_t o_rsrc, uin
   }
 }
 
+// fp16 output of P.V column n's DPC dims of one query row (dims out_dim(n,
+// 0..DPC-1)) whose first element is at byte offset row_off: one contiguous
+// run over the row's 16 lanes per store instruction.
+template <int DPC>
+__device__ __forceinline__ void store_f16_cols(__amdgpu_buffer_rsrc_t o_rsrc, uint32_t row_off, int n,
+                                               const float* v) {
+  if constexpr (DPC <= 8) {
+    store_f16_run<DPC>(o_rsrc, row_off + (uint32_t)out_dim<DPC>(n, 0) * 2u, v);
+  } else {
+#pragma unroll
+    for (int h8 = 0; h8 < DPC / 8; ++h8)
+      store_f16_run<8>(o_rsrc, row_off + (uint32_t)out_dim<DPC>(n, 8 * h8) * 2u, v + 8 * h8);
+  }
+}
+
 // Grid: units = batch * nchunks * Hkv (unit (b * nchunks + c) * Hkv + hk),
 // each in TC = ceil(tiles / TW) tile chunks; ceil(units / 8) * 8 * TC
 // one-wave workgroups, workgroup w serving unit ((w / 8) / TC) * 8 + w % 8
@@ -321,7 +336,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
       bf16x4_v vb[DPC];
 #pragma unroll
       for (int dt = 0; dt < DPC; ++dt) {
-        const int dim = n * DPC + dt;
+        const int dim = out_dim<DPC>(n, dt);
         vb[dt] = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (NR * 2) + q * 8);
       }
 #pragma unroll
@@ -342,7 +357,7 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
     }
   }
 
-  // Lane (q, n) holds query rows 4q..4q+3 of each tile, dims [n DPC, n DPC + DPC).
+  // Lane (q, n) holds query rows 4q..4q+3 of each tile, dims out_dim(n, 0..DPC-1).
 #pragma unroll
   for (int i = 0; i < TW; ++i) {
     if (i >= ntl) break;
@@ -353,19 +368,20 @@ __global__ __launch_bounds__(kBlockThreads) void splitkv_pv_group_kernel(SplitAr
 #pragma unroll
       for (int dt = 0; dt < DPC; ++dt) v[dt] = acc[i][dt][e];
       if constexpr (DIRECT) {
-        store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
+        store_f16_cols<DPC>(o_rsrc, g < G ? (uint32_t)(g * D) * 2u : kLaneOutOfRange, n, v);
       } else {
         // Partial outputs [Hq][nchunks][D] of this batch (default policy:
         // the combine pass reads them right after).
         const uint32_t part_bytes = nchunks * D * 4u;
         const __amdgpu_buffer_rsrc_t p_rsrc =
             make_rsrc(a.opart + ((uint64_t)b * hq + (uint64_t)hk * G) * nchunks * D, (uint32_t)G * part_bytes);
-        const uint32_t off = g < G ? (uint32_t)g * part_bytes + (c * D + n * DPC) * 4u : kLaneOutOfRange;
+        const uint32_t off = g < G ? (uint32_t)g * part_bytes + (uint32_t)(c * D) * 4u : kLaneOutOfRange;
 #pragma unroll
         for (int h4 = 0; h4 < DPC / 4; ++h4) {
           const u32x4 x4 = {__builtin_bit_cast(uint32_t, v[4 * h4]), __builtin_bit_cast(uint32_t, v[4 * h4 + 1]),
                             __builtin_bit_cast(uint32_t, v[4 * h4 + 2]), __builtin_bit_cast(uint32_t, v[4 * h4 + 3])};
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x4), p_rsrc, (int)(off + h4 * 16), 0,
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_gcc, x4), p_rsrc,
+                                                 (int)(off + (uint32_t)out_dim<DPC>(n, 4 * h4) * 4u), 0,
                                                  kPolicyDefault);
         }
       }
@@ -570,7 +586,7 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
       bf16x4_v vb[DPC];
 #pragma unroll
       for (int dt = 0; dt < DPC; ++dt) {
-        const int dim = n * DPC + dt;
+        const int dim = out_dim<DPC>(n, dt);
         vb[dt] = *reinterpret_cast<const bf16x4_v*>(vs + (dim / 8) * Sh::VB + (dim % 8) * (NR * 2) + q * 8);
       }
       const float4 t4 = gok ? *reinterpret_cast<const float4*>(sc + (size_t)n * sps + jb + 4 * q)
@@ -608,14 +624,14 @@ __global__ __launch_bounds__(kBlockThreads * NW) void onepass_mfma_kernel(SplitA
       }
     }
   }
-  // Lane (q, n) holds query rows 4q..4q+3, dims [n DPC, n DPC + DPC).
+  // Lane (q, n) holds query rows 4q..4q+3, dims out_dim(n, 0..DPC-1).
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int g = 4 * q + e;
     float v[DPC];
 #pragma unroll
     for (int dt = 0; dt < DPC; ++dt) v[dt] = poisoned ? __builtin_nanf("") : acc[dt][e];
-    store_f16_run<DPC>(o_rsrc, g < G ? (uint32_t)(g * D + n * DPC) * 2u : kLaneOutOfRange, v);
+    store_f16_cols<DPC>(o_rsrc, g < G ? (uint32_t)(g * D) * 2u : kLaneOutOfRange, n, v);
   }
 }
 
